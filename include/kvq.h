@@ -1,0 +1,142 @@
+/*
+ * libkvq — C ABI of the MI355X (gfx950) packed-KV decode hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers (hipMalloc / torch CUDA tensors) unless stated otherwise.
+ *   - Sizes are int64 element counts; strides are in elements of the pointed-to type.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Launches are asynchronous:
+ *     nothing here synchronises the device, allocates device memory or keeps state between
+ *     calls, so every call is HIP-graph capturable.
+ *   - Return value: KVQ_OK (0) on success; KVQ_EINVAL when an argument is rejected before
+ *     any launch; KVQ_EHIP when the HIP runtime reported an error.  kvq_last_error() returns
+ *     the message of the last failure on the calling thread.
+ *   - fp16 metadata (KIVI zero points `lo` and scales) is passed as raw uint16 bit patterns.
+ *
+ * The reference (TahirSher/KV-Project) is Python; its "FFI" for this path is the set of
+ * Python functions each entry point replaces, cited per declaration as FILE:LINE.
+ */
+#ifndef KVQ_H_
+#define KVQ_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVQ_OK 0
+#define KVQ_EINVAL 1
+#define KVQ_EHIP 2
+
+/* element type codes */
+#define KVQ_F32 0
+#define KVQ_F16 1
+#define KVQ_BF16 2
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* kvq_last_error(void);
+
+/* ABI version of the library (bumped on any signature change). */
+int kvq_abi_version(void);
+
+/* ------------------------------------------------------------------------------------------
+ * A1  KIVI group quantisation (+ fused MSB-first packing).
+ * Replaces kivi_quant (STRATA_KV.py:826-856) and, for the packed output, pack_codes applied to
+ * its codes (STRATA_KV.py:2728-2732, as payload_bytes uses it, 2752-2755).
+ *
+ * x: (B, H, T, d) of x_dtype with element strides (sb, sh, st); channels contiguous.
+ * Rows [0, n_sink) are not quantised.  n = T - n_sink rows are.
+ * along_tokens != 0 (keys): per channel over groups of `group` tokens; n_g = ceil(n / group);
+ *     lo, scale: (B, H, n_g, d) fp16, (b,h) stride meta_bh elements.
+ * along_tokens == 0 (values): per token over groups of `group` channels (d when d % group);
+ *     lo, scale: (B, H, n, d / width) fp16, (b,h) stride meta_bh elements.
+ * codes  (optional, may be NULL): (B, H, n, d) uint8, (b,h) stride codes_bh bytes.
+ * packed (optional): MSB-first packed codes of each (b,h) row block, rows of d*bits/8 bytes,
+ *     (b,h) stride packed_bh bytes.  Requires bits in {2, 4, 8}.
+ * xhat   (optional): (B, H, T, d) float32 contiguous = sinks exact + codes*scale+lo.
+ * Bit-exact with the reference: fp16 round-to-nearest-even of lo and scale, IEEE fp32 division,
+ * round-half-even codes, clamp to [0, 2^bits - 1], scale clamped at 2^-24.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_kivi_quant(const void* x, int x_dtype, int64_t B, int64_t H, int64_t T, int64_t d,
+                   int64_t sb, int64_t sh, int64_t st, int bits, int group, int along_tokens,
+                   int n_sink, uint8_t* codes, int64_t codes_bh, uint8_t* packed,
+                   int64_t packed_bh, uint16_t* lo, uint16_t* scale, int64_t meta_bh,
+                   float* xhat, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * A3  Bit packing.  kvq_pack_codes replaces pack_codes (STRATA_KV.py:2728-2732): `count`
+ * uint8 codes (< 2^bits) -> ceil(count*bits/8) bytes, first code in the most significant bits,
+ * last byte zero padded.  kvq_unpack_codes is its inverse.  bits in {1, 2, 4, 8}.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_pack_codes(const uint8_t* codes, int64_t count, int bits, uint8_t* out, void* stream);
+int kvq_unpack_codes(const uint8_t* packed, int64_t count, int bits, uint8_t* out, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * A3  KIVI value-code decode layout (no reference counterpart: the reference never reads
+ * packed KIVI bytes at decode; its stored format is pack_codes, STRATA_KV.py:2752-2755).
+ * Value codes are kept in 32-token tiles laid out for the decode kernel's matrix-core operand
+ * (each 32-bit word holds 8 tokens of one channel); per-token fp16 (scale, lo) pairs of every
+ * channel group are kept per tile in the same token order.  These two calls convert between
+ * pack_codes rows and the tile layout, both directions, bit-exact.
+ *   rows:  (BH, n, d/2) bytes, (b,h) stride rows_bh; tiles: (BH, cap_t/32, 16*d) bytes,
+ *   (b,h) stride cap_t*d/2.  Rows past n in the last tile are written as code 0.
+ *   meta:  lo/scale (BH, n, ngv) fp16 -> vmeta (BH, cap_t/32, ngv, 32, 2) fp16.
+ * Only 4-bit codes and d % 64 == 0 are supported.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_v_tile(const uint8_t* rows, int64_t BH, int64_t n, int64_t rows_bh, int64_t d,
+               int64_t cap_t, uint8_t* tiles, void* stream);
+int kvq_v_untile(const uint8_t* tiles, int64_t BH, int64_t n, int64_t d, int64_t cap_t,
+                 uint8_t* rows, int64_t rows_bh, void* stream);
+int kvq_vmeta_tile(const uint16_t* lo, const uint16_t* scale, int64_t BH, int64_t n, int64_t ngv,
+                   int64_t meta_bh, int64_t cap_t, uint16_t* vmeta, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * A4  Split-K flash decoding over a packed 4-bit KIVI cache plus exact rows.
+ * Replaces LayerState.attend -> chunked_attention over KIVI token entries
+ * (STRATA_KV.py:716-719, 641-675, entries from 801-823) for a decode step.
+ *
+ * q: (B, Hq, Tq, d) of q_dtype, element strides (q_sb, q_sh, q_st), channels contiguous.
+ *    KV head h serves query heads h*rep .. h*rep+rep-1 (STRATA_KV.py:527-529); the rows of
+ *    KV head h are (query head, t) pairs, R = rep*Tq <= 8.
+ * Packed cache of capacity cap_t tokens per (b,h), n_q tokens valid:
+ *    kc    (B*Hkv, cap_t, d/2)  uint8, pack_codes rows (STRATA_KV.py:2728-2732)
+ *    k_lo, k_sc (B*Hkv, cap_t/group_k, d) fp16
+ *    vc    (B*Hkv, cap_t/32, 16*d) uint8 value tiles (kvq_v_tile)
+ *    vmeta (B*Hkv, cap_t/32, d/group_v, 32, 2) fp16 (kvq_vmeta_tile)
+ * Exact rows: k_exact, v_exact (B*Hkv, cap_e, d) of exact_dtype, rows [0, n_exact) used.
+ *    exact_pos (cap_e,) int64 and q_pos (Tq,) int64 (device, both may be NULL = every exact
+ *    row visible): exact row i is visible to query t iff exact_pos[i] <= q_pos[t].
+ *    Every packed row is visible to every query.
+ * out: (B, Tq, Hq, d) of out_dtype, contiguous (the reference's output layout).
+ * workspace: float32 scratch of kvq_kivi_decode_workspace(...) floats (split partials).
+ * split_tokens: packed tokens per workgroup (multiple of 128; 0 = automatic).
+ * phases: 3 = both kernels; 1 = only the split kernel (partials into the workspace); 2 = only
+ *    the merge (reads the partials a phases=1 call left, same arguments).
+ * Requires d == 128, 4-bit codes, group_k % 32 == 0, group_v in {32, 64, 128}.
+ * ---------------------------------------------------------------------------------------- */
+int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
+                                  int64_t n_q, int64_t n_exact, int group_k,
+                                  int64_t split_tokens);
+int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                    int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling,
+                    const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_sc,
+                    const uint8_t* vc, const uint16_t* vmeta, int64_t cap_t, int64_t n_q,
+                    int group_k, int group_v, const void* k_exact, const void* v_exact,
+                    int exact_dtype, int64_t cap_e, int64_t n_exact, const int64_t* exact_pos,
+                    const int64_t* q_pos, void* out, int out_dtype, float* workspace,
+                    int64_t workspace_floats, int64_t split_tokens, int phases,
+                    void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Self-test of the matrix-core operand layout the decode kernel is written against
+ * (v_mfma_f32_16x16x32_f16 on gfx950): writes, for A = I-pattern inputs, the 16x16 product
+ * as each lane sees it, followed by the lane each lane reads under row_shr:4 and row_ror:4.
+ * a, b: 64*8 fp16 each (lane-major); out: 64*4 + 64 + 64 floats.  No reference counterpart
+ * (layout check only).
+ * ---------------------------------------------------------------------------------------- */
+int kvq_selftest_mfma_layout(const uint16_t* a, const uint16_t* b, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KVQ_H_ */

@@ -1,0 +1,80 @@
+// Shared helpers of libkvq: error reporting, dtype codes, fp16 / bf16 conversion.
+// Every entry point returns 0 (KVQ_OK) or a nonzero status and records a message that
+// kvq_last_error() returns; nothing here allocates device memory or synchronises.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/kvq.h"
+
+namespace kvq {
+
+void set_error(const char* fmt, ...);
+
+#define KVQ_REQUIRE(cond, ...)                 \
+  do {                                         \
+    if (!(cond)) {                             \
+      ::kvq::set_error(__VA_ARGS__);           \
+      return KVQ_EINVAL;                       \
+    }                                          \
+  } while (0)
+
+#define KVQ_LAUNCH_CHECK(what)                                               \
+  do {                                                                       \
+    hipError_t e_ = hipGetLastError();                                       \
+    if (e_ != hipSuccess) {                                                  \
+      ::kvq::set_error("%s: %s", what, hipGetErrorString(e_));               \
+      return KVQ_EHIP;                                                       \
+    }                                                                        \
+  } while (0)
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+
+// fp32 -> fp16, round to nearest even (hardware conversion under the default rounding mode).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+template <int DT>
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i) {
+  if constexpr (DT == KVQ_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == KVQ_F16) return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void store_from_f32(void* p, int64_t i, float v) {
+  if constexpr (DT == KVQ_F32) static_cast<float*>(p)[i] = v;
+  else if constexpr (DT == KVQ_F16) static_cast<uint16_t*>(p)[i] = f32_to_f16(v);
+  else static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+
+inline bool valid_dtype(int dt) { return dt == KVQ_F32 || dt == KVQ_F16 || dt == KVQ_BF16; }
+
+}  // namespace kvq
+
+// Dispatch a runtime dtype code to a compile-time template parameter named DT_.
+#define KVQ_DISPATCH_DTYPE(dt, ...)                          \
+  switch (dt) {                                              \
+    case KVQ_F32: { constexpr int DT_ = KVQ_F32; __VA_ARGS__; break; }   \
+    case KVQ_F16: { constexpr int DT_ = KVQ_F16; __VA_ARGS__; break; }   \
+    case KVQ_BF16: { constexpr int DT_ = KVQ_BF16; __VA_ARGS__; break; } \
+    default: ::kvq::set_error("unknown dtype code %d", (int)(dt)); return KVQ_EINVAL; \
+  }

@@ -1,0 +1,14 @@
+"""kvq — MI355X-native (gfx950) packed-KV decode hot path of TahirSher/KV-Project.
+
+Host-side mirror of the reference's Python entry points for this path, calling hand-written HIP
+kernels in ``libkvq.so`` through the C ABI of ``include/kvq.h``.  No CPU fallback exists: every
+op requires GPU tensors and raises ``KVQError`` when the library is missing.
+"""
+from ._lib import KVQError, load as load_library
+from .kivi import kivi_quant, kivi_quant_stored, pack_codes, unpack_codes, v_tile, v_untile, vmeta_tile
+from .decode import PackedKIVICache, kivi_decode, workspace_floats
+
+__all__ = [
+    "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes",
+    "v_tile", "v_untile", "vmeta_tile", "PackedKIVICache", "kivi_decode", "workspace_floats",
+]

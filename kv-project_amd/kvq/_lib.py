@@ -1,0 +1,86 @@
+"""ctypes binding of libkvq.so (the C ABI declared in include/kvq.h).
+
+The library is loaded lazily and only from this package directory.  There is no fallback:
+every product entry point raises ``KVQError`` when the library is missing or a call fails, so a
+silent CPU path can never stand in for the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
+
+KVQ_F32, KVQ_F16, KVQ_BF16 = 0, 1, 2
+DTYPE_CODE = {torch.float32: KVQ_F32, torch.float16: KVQ_F16, torch.bfloat16: KVQ_BF16}
+
+i64, i32, f32, vp = C.c_int64, C.c_int, C.c_float, C.c_void_p
+
+# name -> (restype, argtypes); mirrors include/kvq.h
+SIGNATURES = {
+    "kvq_last_error": (C.c_char_p, []),
+    "kvq_abi_version": (i32, []),
+    "kvq_kivi_quant": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, i64, i32, i32, i32, i32,
+                             vp, i64, vp, i64, vp, vp, i64, vp, vp]),
+    "kvq_pack_codes": (i32, [vp, i64, i32, vp, vp]),
+    "kvq_unpack_codes": (i32, [vp, i64, i32, vp, vp]),
+    "kvq_v_tile": (i32, [vp, i64, i64, i64, i64, i64, vp, vp]),
+    "kvq_v_untile": (i32, [vp, i64, i64, i64, i64, vp, i64, vp]),
+    "kvq_vmeta_tile": (i32, [vp, vp, i64, i64, i64, i64, i64, vp, vp]),
+    "kvq_kivi_decode_workspace": (i64, [i64, i64, i64, i64, i64, i64, i64, i32, i64]),
+    "kvq_kivi_decode": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32,
+                              vp, vp, vp, vp, vp, i64, i64, i32, i32, vp, vp, i32, i64, i64,
+                              vp, vp, vp, i32, vp, i64, i64, i32, vp]),
+    "kvq_selftest_mfma_layout": (i32, [vp, vp, vp, vp]),
+}
+
+
+class KVQError(RuntimeError):
+    """A libkvq call was rejected or failed, or the library is not available."""
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Load libkvq.so (once) and attach the ctypes signatures."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise KVQError(f"{LIB_PATH} is not built: run `python kv-project_amd/kvq/build.py` "
+                               "(or __graft_entry__.build()) first")
+            lib = C.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype, fn.argtypes = res, args
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> int:
+    """Call an int-status entry point; raise KVQError with the library's message on failure."""
+    rc = getattr(load(), name)(*args)
+    if rc != 0:
+        msg = load().kvq_last_error().decode(errors="replace")
+        raise KVQError(f"{name} failed ({rc}): {msg}")
+    return rc
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_gpu(*tensors: torch.Tensor) -> None:
+    """The product path runs only on the GPU: CPU tensors are rejected, never computed on."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise KVQError("kvq kernels take GPU tensors only (got a CPU tensor); there is no CPU path")

@@ -1,0 +1,140 @@
+"""Packed KIVI cache on the GPU and its split-K flash-decoding call.
+
+``PackedKIVICache`` holds one layer's cache in the decode layout of libkvq: 4-bit key codes in
+pack_codes rows (STRATA_KV.py:2728-2732), per-channel fp16 key lo/scale per group of
+``group_k`` tokens, 4-bit value codes in 32-token tiles, per-token fp16 value (scale, lo) per
+channel group, and the exact rows (the residual window, model dtype).  ``kivi_decode`` is one
+decode step of attention over it; it replaces chunked_attention over KIVI token entries
+(STRATA_KV.py:641-675 via LayerState.attend 716-719) for a single step.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .kivi import kivi_quant_stored, v_tile, vmeta_tile
+
+
+def _round_up(x: int, m: int) -> int:
+    return -(-x // m) * m
+
+
+@dataclass
+class PackedKIVICache:
+    kc: torch.Tensor            # (B, Hkv, cap_t, d/2) uint8
+    k_lo: torch.Tensor          # (B, Hkv, cap_t/group_k, d) fp16
+    k_sc: torch.Tensor
+    vc: torch.Tensor            # (B, Hkv, cap_t/32, 16*d) uint8
+    vmeta: torch.Tensor         # (B, Hkv, cap_t/32, d/group_v, 32, 2) fp16 (scale, lo)
+    n_q: int
+    group_k: int
+    group_v: int
+    k_exact: torch.Tensor       # (B, Hkv, cap_e, d) model dtype
+    v_exact: torch.Tensor
+    n_exact: int
+    exact_pos: Optional[torch.Tensor] = None    # (cap_e,) int64, positions of the exact rows
+    bits: int = 4
+
+    @property
+    def cap_t(self) -> int:
+        return self.kc.shape[2]
+
+    @property
+    def cap_e(self) -> int:
+        return self.k_exact.shape[2]
+
+    @classmethod
+    @torch.no_grad()
+    def from_context(cls, K: torch.Tensor, V: torch.Tensor, *, window: int, group_k: int,
+                     group_v: int, bits: int = 4, extra_tokens: int = 0, extra_exact: int = 0,
+                     dtype: Optional[torch.dtype] = None) -> "PackedKIVICache":
+        """Compress a context cache K, V (B, Hkv, T, d) the way KIVIMethod leaves it at a horizon
+        (STRATA_KV.py:801-823, no sinks): rows [0, T - window) are read from their codes, the last
+        ``window`` rows stay exact.  Key groups are formed over all T rows (a group that straddles
+        the window boundary takes its min/max over all of its rows, as kivi_quant over the whole
+        tensor does).  ``extra_tokens`` / ``extra_exact`` reserve capacity for appends."""
+        _lib.require_gpu(K, V)
+        if bits != 4:
+            raise ValueError("the decode kernel reads 4-bit codes")
+        B, H, T, d = K.shape
+        if window > T or window < 0:
+            raise ValueError("window must be in [0, T]")
+        n_q = T - window
+        dtype = dtype or K.dtype
+        dev = K.device
+        cap_t = max(_round_up(max(n_q + extra_tokens, 1), math.lcm(group_k, 32)), math.lcm(group_k, 32))
+        kq = kivi_quant_stored(K, bits, group_k, True, 0)
+        vq = kivi_quant_stored(V, bits, group_v, False, 0)
+        kc = torch.zeros((B, H, cap_t, d // 2), dtype=torch.uint8, device=dev)
+        kc[:, :, :n_q] = kq["packed"][:, :, :n_q]
+        n_gq = -(-n_q // group_k)
+        k_lo = torch.zeros((B, H, cap_t // group_k, d), dtype=torch.float16, device=dev)
+        k_sc = torch.zeros_like(k_lo)
+        k_lo[:, :, :n_gq] = kq["lo"][:, :, :n_gq]
+        k_sc[:, :, :n_gq] = kq["scale"][:, :, :n_gq]
+        vc = v_tile(vq["packed"][:, :, :n_q].contiguous(), cap_t)
+        vmeta = vmeta_tile(vq["lo"][:, :, :n_q].contiguous(), vq["scale"][:, :, :n_q].contiguous(), cap_t)
+        cap_e = max(window + extra_exact, 1)
+        k_ex = torch.zeros((B, H, cap_e, d), dtype=dtype, device=dev)
+        v_ex = torch.zeros_like(k_ex)
+        k_ex[:, :, :window] = K[:, :, n_q:].to(dtype)
+        v_ex[:, :, :window] = V[:, :, n_q:].to(dtype)
+        return cls(kc, k_lo, k_sc, vc, vmeta, n_q, group_k, group_v, k_ex, v_ex, window)
+
+    def payload_bytes(self) -> int:
+        """Bytes a decode step reads: codes and metadata of the n_q packed rows + exact rows."""
+        B, H = self.kc.shape[:2]
+        d = self.kc.shape[3] * 2
+        n_g = -(-self.n_q // self.group_k)
+        codes = 2 * B * H * self.n_q * d // 2
+        kmeta = B * H * n_g * d * 4
+        vmeta = B * H * self.n_q * (d // self.group_v) * 4
+        exact = 2 * B * H * self.n_exact * d * self.k_exact.element_size()
+        return codes + kmeta + vmeta + exact
+
+
+def workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_q: int, n_exact: int,
+                     group_k: int, split_tokens: int = 0) -> int:
+    n = _lib.load().kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, d, n_q, n_exact, group_k, split_tokens)
+    if n < 0:
+        raise _lib.KVQError("kvq_kivi_decode_workspace rejected the shape")
+    return n
+
+
+@torch.no_grad()
+def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
+                q_pos: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                workspace: Optional[torch.Tensor] = None, split_tokens: int = 0,
+                phases: int = 3) -> torch.Tensor:
+    """Attention of q (B, Hq, Tq, d) over the packed cache; returns (B, Tq, Hq, d) in q's dtype.
+
+    With ``q_pos`` (Tq,) int64 and ``cache.exact_pos`` set, exact row i is visible to query t iff
+    exact_pos[i] <= q_pos[t] (the causal rule of chunked_attention among appended rows); every
+    packed row is visible.  ``phases`` 1/2 run only the split / merge kernel (timing)."""
+    _lib.require_gpu(q)
+    B, Hq, Tq, d = q.shape
+    Hkv = cache.kc.shape[1]
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if cache.k_exact.dtype != q.dtype:
+        raise TypeError("q and the exact rows must share a dtype")
+    if out is None:
+        out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
+    need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, split_tokens)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty((need,), dtype=torch.float32, device=q.device)
+    ep = cache.exact_pos if q_pos is not None else None
+    qp = q_pos if ep is not None else None
+    dt = _lib.DTYPE_CODE[q.dtype]
+    _lib.call("kvq_kivi_decode", q.data_ptr(), dt, q.stride(0), q.stride(1), q.stride(2),
+              B, Hq, Hkv, Tq, d, float(scaling),
+              cache.kc.data_ptr(), cache.k_lo.data_ptr(), cache.k_sc.data_ptr(), cache.vc.data_ptr(),
+              cache.vmeta.data_ptr(), cache.cap_t, cache.n_q, cache.group_k, cache.group_v,
+              cache.k_exact.data_ptr(), cache.v_exact.data_ptr(), dt, cache.cap_e, cache.n_exact,
+              _lib.ptr(ep), _lib.ptr(qp), out.data_ptr(), dt, workspace.data_ptr(), workspace.numel(),
+              split_tokens, phases, _lib.stream_of(q))
+    return out

@@ -1,0 +1,44 @@
+"""The C-ABI library loads on a CPU-only machine and exports every symbol include/kvq.h declares,
+with the ctypes signatures the Python side binds (no compute call: that needs a GPU)."""
+import re
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "kvq.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kvq_[a-z0-9_]+)\s*\(", text)))
+
+
+def _ensure_built():
+    from kvq import _lib
+    if not _lib.LIB_PATH.exists():
+        import kvq.build as b
+        b.build()
+    return _lib
+
+
+def test_library_exports_every_declared_symbol():
+    _lib = _ensure_built()
+    lib = _lib.load()
+    names = _declared()
+    assert names, "no declarations parsed"
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/kvq.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert lib.kvq_abi_version() == 1
+    assert lib.kvq_last_error() == b""
+
+
+def test_argument_validation_without_gpu():
+    # rejected before any launch: no device needed
+    _lib = _ensure_built()
+    lib = _lib.load()
+    rc = lib.kvq_pack_codes(None, 10, 3, None, None)
+    assert rc == 1 and b"bits" in lib.kvq_last_error()
+    rc = lib.kvq_kivi_decode(None, 0, 0, 0, 0, 1, 8, 8, 1, 64, 0.1, None, None, None, None, None, 64, 0, 32, 32,
+                             None, None, 0, 1, 1, None, None, None, 0, None, 0, 0, 3, None)
+    assert rc == 1 and b"head_dim" in lib.kvq_last_error()
+    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 0) > 0
