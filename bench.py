@@ -5,9 +5,11 @@ One step = one decode step of attention for one Llama-3-8B-shaped layer: batch 1
 heads, 8 KV heads, head_dim 128, 32768 cached tokens (32640 4-bit packed + 128 exact bf16
 rows), over the packed KIVI cache already resident in HBM.  Prints ONE JSON line.
 
-Timing: W untimed warm-up steps, then K steps between HIP events on the launch stream (with a
-device synchronisation on both sides).  The dominant kernel (the split-K decode kernel) is
-timed the same way on its own (phase 1 only) for the roofline figure.  The CPU baseline is the
+Timing: the step is captured once in a HIP graph (the reference's _time_callable protocol,
+STRATA_KV.py:3424-3447); W untimed warm-up replays, then K replays between HIP events on the
+launch stream (device synchronisation on both sides).  The eager (uncaptured) step time is
+reported too.  The dominant kernel (the split-K decode kernel) is timed the same way on its own
+(phase 1 only) for the roofline figure.  The CPU baseline is the
 oracle's restatement of the reference decode (dequantise + chunked_attention in float32) on a
 bounded sample of (batch, KV head) pairs of the same cache, scaled to the whole layer.
 """
@@ -102,24 +104,42 @@ def main() -> int:
                                              group_v=shape.group_v)
     scaling = shape.d ** -0.5
     out = torch.empty((shape.B, 1, shape.Hq, shape.d), dtype=shape.dtype, device="cuda")
-    ws = torch.empty((kvq.workspace_floats(shape.B, shape.Hq, shape.Hkv, 1, shape.d, cache.n_q, cache.n_exact,
+    ws = torch.zeros((kvq.workspace_floats(shape.B, shape.Hq, shape.Hkv, 1, shape.d, cache.n_q, cache.n_exact,
                                            shape.group_k, args.split_tokens),), dtype=torch.float32,
                      device="cuda")
 
     def step():
         kvq.kivi_decode(q, scaling, cache, out=out, workspace=ws, split_tokens=args.split_tokens)
 
+
     def split_only():
         kvq.kivi_decode(q, scaling, cache, out=out, workspace=ws, split_tokens=args.split_tokens, phases=1)
+
+    def graph_of(fn):
+        """Capture fn once in a HIP graph (as the reference's _time_callable, STRATA_KV.py:3424-3447)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            fn()
+        return gr
 
     log("timing")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    ms_per_step = _events_ms(step, args.steps)
+    eager_ms = _events_ms(step, args.steps)
+    g_step, g_split = graph_of(step), graph_of(split_only)
     for _ in range(args.warmup):
-        split_only()
-    split_ms = _events_ms(split_only, args.steps)
+        g_step.replay()
+    ms_per_step = _events_ms(g_step.replay, args.steps)
+    for _ in range(args.warmup):
+        g_split.replay()
+    split_ms = _events_ms(g_split.replay, args.steps)
 
     io_bytes = q.numel() * q.element_size() + out.numel() * out.element_size()
     bytes_alg = cache.payload_bytes() + io_bytes
@@ -141,6 +161,8 @@ def main() -> int:
                    "group_k": shape.group_k, "group_v": shape.group_v, "bits": shape.bits,
                    "split_tokens": args.split_tokens},
         "us_per_layer": round(ms_per_step * 1e3, 3),
+        "timer": "HIP graph replay, HIP events over the timed steps",
+        "eager_us_per_layer": round(eager_ms * 1e3, 3),
         "bytes_alg": bytes_alg,
         "packed_code_GBs": round(2 * shape.B * shape.Hkv * cache.n_q * shape.d // 2 / (ms_per_step * 1e-3) / 1e9, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -108,10 +108,11 @@ int kvq_vmeta_tile(const uint16_t* lo, const uint16_t* scale, int64_t BH, int64_
  *    row visible): exact row i is visible to query t iff exact_pos[i] <= q_pos[t].
  *    Every packed row is visible to every query.
  * out: (B, Tq, Hq, d) of out_dtype, contiguous (the reference's output layout).
- * workspace: float32 scratch of kvq_kivi_decode_workspace(...) floats (split partials).
+ * workspace: float32 scratch of kvq_kivi_decode_workspace(...) floats (split partials).  Calls
+ *    sharing one workspace must not overlap in time (same stream, or ordered streams).
  * split_tokens: packed tokens per workgroup (multiple of 128; 0 = automatic).
- * phases: 3 = both kernels; 1 = only the split kernel (partials into the workspace); 2 = only
- *    the merge (reads the partials a phases=1 call left, same arguments).
+ * phases: 3 = split kernel then merge kernel; 1 = only the split kernel (partials into the
+ *    workspace); 2 = only the merge kernel over the partials a phases=1 call left (same args).
  * Requires d == 128, 4-bit codes, group_k % 32 == 0, group_v in {32, 64, 128}.
  * ---------------------------------------------------------------------------------------- */
 int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
@@ -126,6 +127,24 @@ int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int6
                     const int64_t* q_pos, void* out, int out_dtype, float* workspace,
                     int64_t workspace_floats, int64_t split_tokens, int phases,
                     void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * A2  Fused quantise + pack append of one token per sequence (streaming KIVI window).
+ * No per-step quantiser exists in the reference (its decode-time appends stay exact,
+ * STRATA_KV.py:707-714); this restates KIVIMethod's window rule (806-822) for a streaming cache:
+ * a token is read exact while among the last W positions, then from its kivi_quant codes.
+ * k_new, v_new: (B, Hkv, 1, d) of dtype with element strides (k_sb, k_sh) / (v_sb, v_sh).
+ * k_ring, v_ring: (B*Hkv, W, d) of dtype, position p in slot p % W.  Packed cache as for
+ * kvq_kivi_decode (capacity cap_t tokens).  For pos >= W, token pos-W is quantised (value row;
+ * and, when (pos-W) % group_k == 0, key group (pos-W)/group_k from the ring) before the new row
+ * is written into slot pos % W.  After the call the decode reads n_q = max(0, pos+1-W) packed
+ * tokens and min(pos+1, W) ring rows.  Requires d == 128, 4-bit, W >= group_k, group_k % 32 == 0.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_kivi_append(const void* k_new, const void* v_new, int dtype, int64_t k_sb, int64_t k_sh,
+                    int64_t v_sb, int64_t v_sh, int64_t B, int64_t Hkv, int64_t d, int64_t pos,
+                    void* k_ring, void* v_ring, int64_t W, uint8_t* kc, uint16_t* k_lo,
+                    uint16_t* k_sc, uint8_t* vc, uint16_t* vmeta, int64_t cap_t, int group_k,
+                    int group_v, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * Self-test of the matrix-core operand layout the decode kernel is written against

@@ -76,6 +76,7 @@ struct DecodeParams {
   float* ws_l;
   float* ws_o;
   int n_exact_wg, n_split, split_tokens, S1;
+  int BH;
   void* out;
 };
 
@@ -258,135 +259,145 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   }
   const half8 ones = as_half8(u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
 
-  for (int gs = t0; gs < t1; gs += G) {
-    // ---- per key group: B operand of the scaled query and the logit correction ----
-    const int gi = gs / G;
-    const uint16_t* ksc = p.k_sc + kmeta_bh + static_cast<int64_t>(gi) * kD;
-    const uint16_t* klo = p.k_lo + kmeta_bh + static_cast<int64_t>(gi) * kD;
-    const float sc0 = f16_to_f32(ksc[c0]) * kinv, sc1 = f16_to_f32(ksc[c1]) * kinv;
-    const float lo0 = f16_to_f32(klo[c0]), lo1 = f16_to_f32(klo[c1]);
+  // ---- software pipeline: the loads of chunk cb+32 are in flight while chunk cb computes ----
+  struct Chunk {
+    u32x4 kw[2], vw[2];
+    u32x4 mw[NB][2];
+    uint32_t ks, kl;                               // key scale / lo pairs of (c0, c1), group start only
+  };
+  auto load_chunk = [&](int cb, Chunk& c) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float x0 = qa[r] * sc0, x1 = qb[r] * sc1;
-      const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
-      const _Float16 e0 = static_cast<_Float16>(x0 - static_cast<float>(h0));
-      const _Float16 e1 = static_cast<_Float16>(x1 - static_cast<float>(h1));
-      bq[(2 * r) * 64 + l] = pack_h2(h0, h1);
-      bq[(2 * r + 1) * 64 + l] = pack_h2(e0, e1);
-      // bias q.lo minus the 1024 offset carried by every A operand element
-      float P = qa[r] * lo0 + qb[r] * lo1 -
-                1024.0f * ((static_cast<float>(h0) + static_cast<float>(h1)) +
-                           (static_cast<float>(e0) + static_cast<float>(e1)));
-      P += dpp<kQuadSwap1>(P);
-      P += dpp<kQuadSwap2>(P);
-      if (ck == 0) {
-        const _Float16 ph = static_cast<_Float16>(P);
-        const _Float16 pl = static_cast<_Float16>(P - static_cast<float>(ph));
-        bv[r * 16 + g * 4 + ci] = pack_h2(ph, pl);
-      }
+    for (int tau = 0; tau < 2; ++tau)
+      c.kw[tau] = *reinterpret_cast<const u32x4*>(kc + static_cast<int64_t>(cb + 16 * tau + n) * (kD / 2) + 16 * g);
+    const uint8_t* vchunk = vc + static_cast<int64_t>(cb / 32) * (16 * kD);
+#pragma unroll
+    for (int qq = 0; qq < 2; ++qq) c.vw[qq] = *reinterpret_cast<const u32x4*>(vchunk + qq * 1024 + l * 16);
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      const int gc = bb * GPB + gcl;
+      const uint16_t* src = vm + (static_cast<int64_t>(cb / 32) * NGV + (gc < NGV ? gc : 0)) * 64 + g * 16;
+      c.mw[bb][0] = *reinterpret_cast<const u32x4*>(src);
+      c.mw[bb][1] = *reinterpret_cast<const u32x4*>(src + 8);
     }
-    wave_lds_fence();
-    half8 bqk[4];
-    {
+    if ((cb - t0) % G == 0) {
+      const int64_t mo = kmeta_bh + static_cast<int64_t>(cb / G) * kD;
+      c.ks = static_cast<uint32_t>(p.k_sc[mo + c0]) | (static_cast<uint32_t>(p.k_sc[mo + c1]) << 16);
+      c.kl = static_cast<uint32_t>(p.k_lo[mo + c0]) | (static_cast<uint32_t>(p.k_lo[mo + c1]) << 16);
+    }
+  };
+
+  half8 bqk[4];
+  half8 bvirt;
+  Chunk cur, nxt;
+  if (t0 < t1) load_chunk(t0, nxt);
+  for (int cb = t0; cb < t1; cb += 32) {
+    cur = nxt;
+    if (cb + 32 < t1) load_chunk(cb + 32, nxt);
+    if ((cb - t0) % G == 0) {
+      // ---- per key group: B operand of the scaled query and the logit correction ----
+      const float sc0 = h2f(cur.ks, 0) * kinv, sc1 = h2f(cur.ks, 1) * kinv;
+      const float lo0 = h2f(cur.kl, 0), lo1 = h2f(cur.kl, 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float x0 = qa[r] * sc0, x1 = qb[r] * sc1;
+        const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
+        const _Float16 e0 = static_cast<_Float16>(x0 - static_cast<float>(h0));
+        const _Float16 e1 = static_cast<_Float16>(x1 - static_cast<float>(h1));
+        bq[(2 * r) * 64 + l] = pack_h2(h0, h1);
+        bq[(2 * r + 1) * 64 + l] = pack_h2(e0, e1);
+        // bias q.lo minus the 1024 offset carried by every A operand element
+        float P = qa[r] * lo0 + qb[r] * lo1 -
+                  1024.0f * ((static_cast<float>(h0) + static_cast<float>(h1)) +
+                             (static_cast<float>(e0) + static_cast<float>(e1)));
+        P += dpp<kQuadSwap1>(P);
+        P += dpp<kQuadSwap2>(P);
+        if (ck == 0) {
+          const _Float16 ph = static_cast<_Float16>(P);
+          const _Float16 pl = static_cast<_Float16>(P - static_cast<float>(ph));
+          bv[r * 16 + g * 4 + ci] = pack_h2(ph, pl);
+        }
+      }
+      wave_lds_fence();
       const u32x4* src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl_qk) * 64 + g * 16);
 #pragma unroll
       for (int i = 0; i < 4; ++i) bqk[i] = as_half8(src[i]);
+      u32x4 bvr = *reinterpret_cast<const u32x4*>(bv + r_n * 16 + g * 4);
+      if (hl_qk) bvr = u32x4{0u, 0u, 0u, 0u};
+      bvirt = as_half8(bvr);
+      wave_lds_fence();
     }
-    u32x4 bvr = *reinterpret_cast<const u32x4*>(bv + r_n * 16 + g * 4);
-    if (hl_qk) bvr = u32x4{0u, 0u, 0u, 0u};
-    const half8 bvirt = as_half8(bvr);
-    wave_lds_fence();
-
-    for (int cb = gs; cb < min(gs + G, t1); cb += 32) {
-      // ---- loads of one chunk ----
-      u32x4 kw[2], vw[2];
+    // ---- logits ----
+    float s[8];
 #pragma unroll
-      for (int tau = 0; tau < 2; ++tau)
-        kw[tau] = *reinterpret_cast<const u32x4*>(kc + static_cast<int64_t>(cb + 16 * tau + n) * (kD / 2) + 16 * g);
-      const uint8_t* vchunk = vc + static_cast<int64_t>(cb / 32) * (16 * kD);
+    for (int tau = 0; tau < 2; ++tau) {
+      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int qq = 0; qq < 2; ++qq) vw[qq] = *reinterpret_cast<const u32x4*>(vchunk + qq * 1024 + l * 16);
-      u32x4 mw[NB][2];
+      for (int i = 0; i < 4; ++i) d = mfma(unpack4(cur.kw[tau][i]), bqk[i], d);
+      d = mfma(ones, bvirt, d);
 #pragma unroll
-      for (int bb = 0; bb < NB; ++bb) {
-        const int gc = bb * GPB + gcl;
-        const uint16_t* src = vm + (static_cast<int64_t>(cb / 32) * NGV + (gc < NGV ? gc : 0)) * 64 + g * 16;
-        mw[bb][0] = *reinterpret_cast<const u32x4*>(src);
-        mw[bb][1] = *reinterpret_cast<const u32x4*>(src + 8);
+      for (int i = 0; i < 4; ++i) {
+        const float full = d[i] + dpp<kRowRor + R>(d[i]);
+        const int tok = cb + 16 * tau + 4 * g + i;
+        s[4 * tau + i] = tok < t1 ? full : -INFINITY;
       }
-      // ---- logits ----
-      float s[8];
+    }
+    // ---- online softmax (base 2) ----
+    float cm = s[0];
 #pragma unroll
-      for (int tau = 0; tau < 2; ++tau) {
-        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 1; j < 8; ++j) cm = fmaxf(cm, s[j]);
+    cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
+    cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+    const float m_new = fmaxf(m_run, cm);
+    if (__any(m_new > m_run)) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) d = mfma(unpack4(kw[tau][i]), bqk[i], d);
-        d = mfma(ones, bvirt, d);
+      for (int k = 0; k < 8; ++k) acc[k] *= alpha;
+      l_run *= alpha;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float full = d[i] + dpp<kRowRor + R>(d[i]);
-          const int tok = cb + 16 * tau + 4 * g + i;
-          s[4 * tau + i] = tok < t1 ? full : -INFINITY;
+      for (int k = 0; k < NB; ++k) {
+        S[k] *= alpha;
+        Z[k] *= alpha;
+      }
+      m_run = m_new;
+    }
+    float pr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run);
+      l_run += pr[j];
+    }
+    // ---- PV operands: p * sv, hi/lo split; sums of the operands for the 1024 offset ----
+    half8 bp[NB];
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      const int gc = bb * GPB + gcl;
+      const bool gvalid = gc < NGV;
+      uint32_t words[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        _Float16 hv[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int j = 2 * jj + e;
+          const uint32_t mword = cur.mw[bb][j >> 2][j & 3];
+          const float sv = h2f(mword, 0), lv = h2f(mword, 1);
+          const float kv = ((j & 3) >= 2) ? 0.0625f : 1.0f;
+          const float x = gvalid ? pr[j] * sv * kv : 0.0f;
+          const _Float16 hx = static_cast<_Float16>(x);
+          const _Float16 val = hl_pv ? static_cast<_Float16>(x - static_cast<float>(hx)) : hx;
+          hv[e] = val;
+          S[bb] += static_cast<float>(val);
+          Z[bb] += gvalid ? pr[j] * lv : 0.0f;
         }
+        words[jj] = pack_h2(hv[0], hv[1]);
       }
-      // ---- online softmax (base 2) ----
-      float cm = s[0];
+      bp[bb] = as_half8(u32x4{words[0], words[1], words[2], words[3]});
+    }
+    // ---- PV ----
 #pragma unroll
-      for (int j = 1; j < 8; ++j) cm = fmaxf(cm, s[j]);
-      cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
-      cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
-      const float m_new = fmaxf(m_run, cm);
-      if (__any(m_new > m_run)) {
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) acc[k] *= alpha;
-        l_run *= alpha;
-#pragma unroll
-        for (int k = 0; k < NB; ++k) {
-          S[k] *= alpha;
-          Z[k] *= alpha;
-        }
-        m_run = m_new;
-      }
-      float pr[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run);
-        l_run += pr[j];
-      }
-      // ---- PV operands: p * sv, hi/lo split; sums of the operands for the 1024 offset ----
-      half8 bp[NB];
-#pragma unroll
-      for (int bb = 0; bb < NB; ++bb) {
-        const int gc = bb * GPB + gcl;
-        const bool gvalid = gc < NGV;
-        uint32_t words[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          _Float16 hv[2];
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int j = 2 * jj + e;
-            const uint32_t mword = mw[bb][j >> 2][j & 3];
-            const float sv = h2f(mword, 0), lv = h2f(mword, 1);
-            const float kv = ((j & 3) >= 2) ? 0.0625f : 1.0f;
-            const float x = gvalid ? pr[j] * sv * kv : 0.0f;
-            const _Float16 hx = static_cast<_Float16>(x);
-            const _Float16 val = hl_pv ? static_cast<_Float16>(x - static_cast<float>(hx)) : hx;
-            hv[e] = val;
-            S[bb] += static_cast<float>(val);
-            Z[bb] += gvalid ? pr[j] * lv : 0.0f;
-          }
-          words[jj] = pack_h2(hv[0], hv[1]);
-        }
-        bp[bb] = as_half8(u32x4{words[0], words[1], words[2], words[3]});
-      }
-      // ---- PV ----
-#pragma unroll
-      for (int blk = 0; blk < 8; ++blk) {
-        const int gcb = (16 * blk) / GV;
-        acc[blk] = mfma(unpack4(vw[blk >> 2][blk & 3]), bp[gcb / GPB], acc[blk]);
-      }
+    for (int blk = 0; blk < 8; ++blk) {
+      const int gcb = (16 * blk) / GV;
+      acc[blk] = mfma(unpack4(cur.vw[blk >> 2][blk & 3]), bp[gcb / GPB], acc[blk]);
     }
   }
 
@@ -442,20 +453,9 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   }
 }
 
-template <int R, int GV, int DT>
-__global__ __launch_bounds__(kThreads) void kivi_decode_split(DecodeParams p) {
-  extern __shared__ float smem[];
-  const int bh = blockIdx.y;
-  const int sidx = blockIdx.x;
-  if (sidx < p.n_exact_wg) exact_block<R, DT>(p, bh, sidx, smem);
-  else packed_block<R, GV, DT>(p, bh, sidx, smem);
-}
-
-// exact log-sum-exp merge of the S1 partials of every (b, h) and the output write
+// exact log-sum-exp merge of the S1 partials of (b, h) and the output write
 template <int R, int DT>
-__global__ __launch_bounds__(kThreads) void kivi_decode_merge(DecodeParams p) {
-  extern __shared__ float smem[];
-  const int bh = blockIdx.x;
+__device__ void merge_bh(const DecodeParams& p, int bh, float* smem) {
   const int b = bh / p.Hkv, h = bh % p.Hkv;
   float* wgt = smem;                             // [S1][R]
   float* tot = smem + p.S1 * R;                  // L[R]
@@ -484,21 +484,44 @@ __global__ __launch_bounds__(kThreads) void kivi_decode_merge(DecodeParams p) {
   }
 }
 
+// One block per (b, h, split).  Blocks are dispatched round-robin over the 8 XCDs by linear id,
+// so id -> (xcd = id % 8, k = id / 8) -> bh = xcd + 8*(k / S1), split = k % S1 keeps every
+// split of one (b, h) on one XCD (its query rows and key metadata are read through one L2).
 template <int R, int GV, int DT>
-int launch(DecodeParams& p, int B, int phases, hipStream_t stream) {
+__global__ __launch_bounds__(kThreads) void kivi_decode_split(DecodeParams p) {
+  extern __shared__ float smem[];
+  const int id = blockIdx.x;
+  const int k = id / 8;
+  const int bh = id % 8 + 8 * (k / p.S1);
+  const int sidx = k % p.S1;
+  if (bh >= p.BH) return;
+  if (sidx < p.n_exact_wg) exact_block<R, DT>(p, bh, sidx, smem);
+  else packed_block<R, GV, DT>(p, bh, sidx, smem);
+}
+
+template <int R, int DT>
+__global__ __launch_bounds__(kThreads) void kivi_decode_merge(DecodeParams p) {
+  extern __shared__ float smem[];
+  merge_bh<R, DT>(p, blockIdx.x, smem);
+}
+
+template <int R, int GV, int DT>
+int launch(DecodeParams& p, int phases, hipStream_t stream) {
   const size_t exact_smem = (R * kD + R * kExactRows + 2 * R) * sizeof(float);
   const size_t packed_smem = std::max<size_t>((R * kD) * sizeof(float) + kWaves * (2 * R * 64 + R * 16) * 4,
                                               (kWaves * R * kD + kWaves * 2 * R) * sizeof(float));
-  const size_t smem = std::max(exact_smem, packed_smem);
-  const dim3 grid(p.n_exact_wg + p.n_split, B * p.Hkv);
+  const size_t msmem = (static_cast<size_t>(p.S1) * R + R) * sizeof(float);
+  const size_t smem = std::max({exact_smem, packed_smem, msmem});
+  const int bh_pad = (p.BH + 7) / 8 * 8;
+  const dim3 grid(static_cast<unsigned>(p.S1) * bh_pad);
   if (phases & 1) {
     hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), grid, dim3(kThreads), smem, stream, p);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(split)");
   }
-  if (!(phases & 2)) return KVQ_OK;
-  const size_t msmem = (static_cast<size_t>(p.S1) * R + R) * sizeof(float);
-  hipLaunchKernelGGL((kivi_decode_merge<R, DT>), dim3(B * p.Hkv), dim3(kThreads), msmem, stream, p);
-  KVQ_LAUNCH_CHECK("kvq_kivi_decode(merge)");
+  if (phases & 2) {
+    hipLaunchKernelGGL((kivi_decode_merge<R, DT>), dim3(p.BH), dim3(kThreads), msmem, stream, p);
+    KVQ_LAUNCH_CHECK("kvq_kivi_decode(merge)");
+  }
   return KVQ_OK;
 }
 
@@ -576,6 +599,7 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   KVQ_REQUIRE(n_q < (1LL << 31) && B * Hkv < 65536, "kvq_kivi_decode: sizes out of range");
   const SplitPlan sp = plan_split(B, Hq, Hkv, Tq, n_q, n_exact, split_tokens, group_k);
   const int64_t need = B * Hkv * static_cast<int64_t>(sp.S1) * sp.R * (kD + 2);
+  KVQ_REQUIRE(static_cast<int64_t>(sp.S1) * R_real <= 16384, "kvq_kivi_decode: too many splits");
   KVQ_REQUIRE(workspace_floats >= need, "kvq_kivi_decode: workspace too small (%lld < %lld floats)",
               (long long)workspace_floats, (long long)need);
   DecodeParams p{};
@@ -591,14 +615,15 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   p.ws_o = workspace;
   p.ws_m = workspace + nrow * kD;
   p.ws_l = p.ws_m + nrow;
+  p.BH = static_cast<int>(B * Hkv);
   p.n_exact_wg = sp.n_exact_wg; p.n_split = sp.n_split; p.split_tokens = sp.split_tokens; p.S1 = sp.S1;
   p.out = out;
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define KVQ_GV(R_, DT_)                                                             \
   switch (group_v) {                                                                \
-    case 32: return launch<R_, 32, DT_>(p, (int)B, phases, s);                             \
-    case 64: return launch<R_, 64, DT_>(p, (int)B, phases, s);                             \
-    default: return launch<R_, 128, DT_>(p, (int)B, phases, s);                            \
+    case 32: return launch<R_, 32, DT_>(p, phases, s);                             \
+    case 64: return launch<R_, 64, DT_>(p, phases, s);                             \
+    default: return launch<R_, 128, DT_>(p, phases, s);                            \
   }
 #define KVQ_R(DT_)                                                                  \
   switch (sp.R) {                                                                   \

@@ -360,7 +360,7 @@ extern "C" int kvq_unpack_codes(const uint8_t* packed, int64_t count, int bits, 
 
 extern "C" int kvq_v_tile(const uint8_t* rows, int64_t BH, int64_t n, int64_t rows_bh, int64_t d,
                           int64_t cap_t, uint8_t* tiles, void* stream) {
-  KVQ_REQUIRE(rows && tiles, "kvq_v_tile: null pointer");
+  KVQ_REQUIRE((n == 0 || rows) && tiles, "kvq_v_tile: null pointer");
   KVQ_REQUIRE(d % 64 == 0 && d > 0 && cap_t % 32 == 0 && n >= 0 && n <= cap_t && BH >= 0,
               "kvq_v_tile: need d %% 64 == 0, cap_t %% 32 == 0, 0 <= n <= cap_t");
   if (BH == 0 || cap_t == 0) return KVQ_OK;
@@ -384,7 +384,7 @@ extern "C" int kvq_v_untile(const uint8_t* tiles, int64_t BH, int64_t n, int64_t
 
 extern "C" int kvq_vmeta_tile(const uint16_t* lo, const uint16_t* scale, int64_t BH, int64_t n,
                               int64_t ngv, int64_t meta_bh, int64_t cap_t, uint16_t* vmeta, void* stream) {
-  KVQ_REQUIRE(lo && scale && vmeta, "kvq_vmeta_tile: null pointer");
+  KVQ_REQUIRE((n == 0 || (lo && scale)) && vmeta, "kvq_vmeta_tile: null pointer");
   KVQ_REQUIRE(cap_t % 32 == 0 && n >= 0 && n <= cap_t && ngv > 0 && BH >= 0,
               "kvq_vmeta_tile: need cap_t %% 32 == 0, 0 <= n <= cap_t");
   if (BH == 0 || cap_t == 0) return KVQ_OK;

@@ -38,6 +38,8 @@ class PackedKIVICache:
     n_exact: int
     exact_pos: Optional[torch.Tensor] = None    # (cap_e,) int64, positions of the exact rows
     bits: int = 4
+    ring: bool = False          # exact rows form a ring: position p in slot p % cap_e
+    next_pos: int = 0           # ring mode: position of the next appended token
 
     @property
     def cap_t(self) -> int:
@@ -51,7 +53,7 @@ class PackedKIVICache:
     @torch.no_grad()
     def from_context(cls, K: torch.Tensor, V: torch.Tensor, *, window: int, group_k: int,
                      group_v: int, bits: int = 4, extra_tokens: int = 0, extra_exact: int = 0,
-                     dtype: Optional[torch.dtype] = None) -> "PackedKIVICache":
+                     dtype: Optional[torch.dtype] = None, ring: bool = False) -> "PackedKIVICache":
         """Compress a context cache K, V (B, Hkv, T, d) the way KIVIMethod leaves it at a horizon
         (STRATA_KV.py:801-823, no sinks): rows [0, T - window) are read from their codes, the last
         ``window`` rows stay exact.  Key groups are formed over all T rows (a group that straddles
@@ -70,20 +72,54 @@ class PackedKIVICache:
         kq = kivi_quant_stored(K, bits, group_k, True, 0)
         vq = kivi_quant_stored(V, bits, group_v, False, 0)
         kc = torch.zeros((B, H, cap_t, d // 2), dtype=torch.uint8, device=dev)
-        kc[:, :, :n_q] = kq["packed"][:, :, :n_q]
         n_gq = -(-n_q // group_k)
+        # a key group is quantised once, when its first token leaves the window: keep the codes of
+        # every row of the groups that have started (later rows of the last group are masked at
+        # decode until they leave the window themselves)
+        rows_k = min(n_gq * group_k, T, cap_t)
+        kc[:, :, :rows_k] = kq["packed"][:, :, :rows_k]
         k_lo = torch.zeros((B, H, cap_t // group_k, d), dtype=torch.float16, device=dev)
         k_sc = torch.zeros_like(k_lo)
         k_lo[:, :, :n_gq] = kq["lo"][:, :, :n_gq]
         k_sc[:, :, :n_gq] = kq["scale"][:, :, :n_gq]
         vc = v_tile(vq["packed"][:, :, :n_q].contiguous(), cap_t)
         vmeta = vmeta_tile(vq["lo"][:, :, :n_q].contiguous(), vq["scale"][:, :, :n_q].contiguous(), cap_t)
-        cap_e = max(window + extra_exact, 1)
+        cap_e = window if ring else max(window + extra_exact, 1)
+        if ring and (window < group_k or window == 0):
+            raise ValueError("the streaming window must hold at least one key group")
         k_ex = torch.zeros((B, H, cap_e, d), dtype=dtype, device=dev)
         v_ex = torch.zeros_like(k_ex)
-        k_ex[:, :, :window] = K[:, :, n_q:].to(dtype)
-        v_ex[:, :, :window] = V[:, :, n_q:].to(dtype)
-        return cls(kc, k_lo, k_sc, vc, vmeta, n_q, group_k, group_v, k_ex, v_ex, window)
+        slots = (torch.arange(n_q, T, device=dev) % cap_e) if ring else torch.arange(window, device=dev)
+        k_ex[:, :, slots] = K[:, :, n_q:].to(dtype)
+        v_ex[:, :, slots] = V[:, :, n_q:].to(dtype)
+        return cls(kc, k_lo, k_sc, vc, vmeta, n_q, group_k, group_v, k_ex, v_ex, window, ring=ring,
+                   next_pos=T)
+
+    @torch.no_grad()
+    def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Streaming append of one token per sequence, k, v (B, Hkv, 1, d): the token leaving the
+        window is quantised and packed in place (and its key group once it is complete), then the
+        new rows enter the ring (libkvq kvq_kivi_append).  Raises when the packed capacity is
+        exhausted, as LayerState.append does for its buffer (STRATA_KV.py:707-714)."""
+        if not self.ring:
+            raise ValueError("append() needs a ring-layout cache (from_context(..., ring=True))")
+        _lib.require_gpu(k, v)
+        if k.dtype != self.k_exact.dtype or v.dtype != self.k_exact.dtype:
+            raise TypeError("appended rows must have the cache's exact-row dtype")
+        B, H, t, d = k.shape
+        if t != 1:
+            raise ValueError("append() takes one token per sequence")
+        W, pos = self.cap_e, self.next_pos
+        if pos >= W and (pos - W) + self.group_k > self.cap_t:
+            raise RuntimeError("decode buffer exhausted")
+        _lib.call("kvq_kivi_append", k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[k.dtype], k.stride(0),
+                  k.stride(1), v.stride(0), v.stride(1), B, H, d, pos, self.k_exact.data_ptr(),
+                  self.v_exact.data_ptr(), W, self.kc.data_ptr(), self.k_lo.data_ptr(), self.k_sc.data_ptr(),
+                  self.vc.data_ptr(), self.vmeta.data_ptr(), self.cap_t, self.group_k, self.group_v,
+                  _lib.stream_of(k))
+        self.next_pos = pos + 1
+        self.n_q = max(0, self.next_pos - W)
+        self.n_exact = min(self.next_pos, W)
 
     def payload_bytes(self) -> int:
         """Bytes a decode step reads: codes and metadata of the n_q packed rows + exact rows."""
@@ -126,7 +162,7 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
         out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
     need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, split_tokens)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty((need,), dtype=torch.float32, device=q.device)
+        workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)   # counters start at zero
     ep = cache.exact_pos if q_pos is not None else None
     qp = q_pos if ep is not None else None
     dt = _lib.DTYPE_CODE[q.dtype]
