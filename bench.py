@@ -86,6 +86,8 @@ def main() -> int:
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (profiler counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path is single-GPU by design (multi-GPU sharding is "
@@ -95,6 +97,16 @@ def main() -> int:
     import kvq
     from kvq.synth import C2, decode_inputs
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        # a copy of known size: FETCH_SIZE / WRITE_SIZE per dispatch of this kernel against the
+        # 1 GiB it must read and write gives the counters' scale on this device
+        src = torch.ones((1 << 28,), dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": args.steps}), flush=True)
+        return 0
     shape = C2
     log = lambda m: print(f"[bench] {m}", file=sys.stderr, flush=True)
     log("generating C2 inputs on the GPU")

@@ -149,8 +149,9 @@ int kvq_kivi_append(const void* k_new, const void* v_new, int dtype, int64_t k_s
 /* ------------------------------------------------------------------------------------------
  * Self-test of the matrix-core operand layout the decode kernel is written against
  * (v_mfma_f32_16x16x32_f16 on gfx950): writes, for A = I-pattern inputs, the 16x16 product
- * as each lane sees it, followed by the lane each lane reads under row_shr:4 and row_ror:4.
- * a, b: 64*8 fp16 each (lane-major); out: 64*4 + 64 + 64 floats.  No reference counterpart
+ * as each lane sees it, followed by the lane each lane reads under row_shr:4 and row_ror:4 and
+ * the two results of v_permlane32_swap and v_permlane16_swap applied to the lane index.
+ * a, b: 64*8 fp16 each (lane-major); out: 64*4 + 6*64 floats.  No reference counterpart
  * (layout check only).
  * ---------------------------------------------------------------------------------------- */
 int kvq_selftest_mfma_layout(const uint16_t* a, const uint16_t* b, float* out, void* stream);

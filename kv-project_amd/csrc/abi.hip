@@ -42,6 +42,14 @@ __global__ void mfma_layout_probe(const uint16_t* __restrict__ a, const uint16_t
   const int ror = __builtin_amdgcn_update_dpp(-1, l, 0x124, 0xF, 0xF, false);
   out[256 + l] = static_cast<float>(shr);
   out[320 + l] = static_cast<float>(ror);
+  // gfx950 cross-row swaps: the lane each lane receives in the second result of
+  // v_permlane32_swap / v_permlane16_swap with both operands holding the lane index
+  const auto s32 = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(l), static_cast<unsigned>(l), false, false);
+  const auto s16 = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(l), static_cast<unsigned>(l), false, false);
+  out[384 + l] = static_cast<float>(s32[0]);
+  out[448 + l] = static_cast<float>(s32[1]);
+  out[512 + l] = static_cast<float>(s16[0]);
+  out[576 + l] = static_cast<float>(s16[1]);
 }
 
 }  // namespace

@@ -31,9 +31,9 @@
 //        p * sv (hi/lo split, one column pair per (row, channel group)); the token "slots"
 //        j = 0..7 of lane group g are exactly the tokens the QK output left in that lane
 //        (4g+i of tile 0, then of tile 1), so probabilities never leave their lane.
-//   Codes become fp16 operands with one and-or each: 0x6400|c is the fp16 value 1024+c, and
-//   the high nibble of a byte masked in place is 1024+16c (its operand column is pre-divided by
-//   16).  The constant 1024 is cancelled exactly with the sums of the B operands actually used.
+//   Codes become fp16 operands with one and each: a nibble masked in place is the fp16 subnormal
+//   c*2^-24 (low nibble) or 16c*2^-24 (high nibble, its operand column pre-divided by 16); the
+//   matrix core keeps subnormal inputs, so codes enter exactly and no offset has to be cancelled.
 #include <algorithm>
 
 #include "common.hpp"
@@ -44,6 +44,33 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Build-time structure of the split kernel's chunk pipeline (defaults are the tuned values):
+//   KVQ_PIPE_DEPTH  chunks held in registers (2: one in flight while one computes; 3: two)
+//   KVQ_BQ_LDS      1: re-read the query operand from LDS for every chunk instead of keeping it
+//                   in 20 VGPRs
+//   KVQ_WAVES       waves per SIMD the register allocation targets (0: per-variant default)
+#ifndef KVQ_PIPE_DEPTH
+#define KVQ_PIPE_DEPTH 2
+#endif
+#ifndef KVQ_BQ_LDS
+#define KVQ_BQ_LDS 0
+#endif
+#ifndef KVQ_WAVES
+#define KVQ_WAVES 0
+#endif
+//   KVQ_INTERLEAVE  1: wavefront w of a block takes key groups w, w+4, w+8, ... of the split (the
+//                   four wavefronts stream adjacent memory); 0: one contiguous quarter each
+#ifndef KVQ_INTERLEAVE
+#define KVQ_INTERLEAVE 0
+#endif
+//   KVQ_LOAD_AUX    cache-policy bits of the streaming code/metadata loads (gfx950: 1 = sc0,
+//                   2 = nt, 16 = sc1).  Default nt: every code byte is read once per launch, so
+//                   marking it non-temporal keeps it from displacing reused lines (measured ~4%
+//                   faster on the 16x32x32768 workload than the default policy)
+#ifndef KVQ_LOAD_AUX
+#define KVQ_LOAD_AUX 2
+#endif
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kD = 128;            // head_dim supported by the matrix-core path
@@ -82,19 +109,6 @@ struct DecodeParams {
 
 __device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
-// 8 nibbles -> 8 fp16 operands, slot order (nib0, nib4 | 16*nib1, 16*nib5 | nib2, nib6 |
-// 16*nib3, 16*nib7), each value offset by 1024.
-__device__ __forceinline__ half8 unpack4(uint32_t w) {
-  const uint32_t M = 0x64006400u;
-  const uint32_t w8 = w >> 8;
-  u32x4 r;
-  r[0] = (w & 0x000F000Fu) | M;
-  r[1] = (w & 0x00F000F0u) | M;
-  r[2] = (w8 & 0x000F000Fu) | M;
-  r[3] = (w8 & 0x00F000F0u) | M;
-  return as_half8(r);
-}
-
 __device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -107,6 +121,24 @@ constexpr int kRowShr = 0x110;     // row_shr:k  (lane i reads lane i-k of its r
 constexpr int kRowRor = 0x120;     // row_ror:k
 constexpr int kQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int kQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
+
+// max / sum with the xor-16 and xor-32 lane partners (gfx950 permlane swaps: VALU, no LDS trip)
+__device__ __forceinline__ float xmax16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xmax32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xsum16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xsum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
@@ -203,6 +235,17 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
 
 // ---------------------------------------------------------------------------------------------
 // packed split: 4 wavefronts, each streaming its quarter of the split in 32-token chunks
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // raw buffer: loads past `bytes` return zero instead of touching memory
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ half2v h2(uint32_t w) { return __builtin_bit_cast(half2v, w); }
+__device__ __forceinline__ uint32_t w2(half2v h) { return __builtin_bit_cast(uint32_t, h); }
+
 template <int R, int GV, int DT>
 __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* smem) {
   constexpr int VPB = 16 / R;                       // PV columns per row: (group, hi/lo) variants
@@ -216,7 +259,8 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   load_q_rows<R, DT>(p, b, h, qs);
   __syncthreads();
 
-  const int wave = threadIdx.x / 64;
+  // wave index made explicitly uniform: every token offset derived from it lives in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   const int l = threadIdx.x % 64;
   const int g = l >> 4, n = l & 15;
   const int r_n = n % R;
@@ -234,81 +278,126 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   const int ST = p.split_tokens;
   const int WT = ST / kWaves;
   const int s_begin = (sidx - p.n_exact_wg) * ST;
+  const int G = p.group_k;
+#if KVQ_INTERLEAVE
+  // chunk k of this wavefront starts at token s_begin + ((k / cpg) * 4 + wave) * G + (k % cpg) * 32
+  const int cpg = G / 32;
+  const int t1 = min(s_begin + ST, p.n_q);           // valid tokens of the whole split
+  const int t0 = s_begin + wave * G;
+  auto chunk_tok = [&](int k) { return s_begin + ((k / cpg) * kWaves + wave) * G + (k % cpg) * 32; };
+#else
   const int t0 = s_begin + wave * WT;
   const int t1 = min(t0 + WT, p.n_q);
-  const int G = p.group_k;
+#endif
 
-  const uint8_t* kc = p.kc + static_cast<int64_t>(bh) * p.cap_t * (kD / 2);
-  const uint8_t* vc = p.vc + static_cast<int64_t>(bh) * p.cap_t * (kD / 2);
-  const uint16_t* vm = p.vmeta + static_cast<int64_t>(bh) * (p.cap_t / 32) * NGV * 64;
-  const int64_t kmeta_bh = static_cast<int64_t>(bh) * (p.cap_t / G) * kD;
+  // buffer resources over this (b, h)'s slices; chunk advance goes in the scalar offset
+  const uint32_t code_bytes = static_cast<uint32_t>(p.cap_t) * (kD / 2);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.kc + static_cast<int64_t>(bh) * p.cap_t * (kD / 2), code_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vc + static_cast<int64_t>(bh) * p.cap_t * (kD / 2), code_bytes);
+  const uint32_t vm_bytes = static_cast<uint32_t>(p.cap_t / 32) * NGV * 128;
+  const __amdgpu_buffer_rsrc_t rm =
+      make_rsrc(p.vmeta + static_cast<int64_t>(bh) * (p.cap_t / 32) * NGV * 64, vm_bytes);
+  const uint32_t km_bytes = static_cast<uint32_t>(p.cap_t / G) * kD * 2;
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(p.k_sc + static_cast<int64_t>(bh) * (p.cap_t / G) * kD, km_bytes);
+  const __amdgpu_buffer_rsrc_t rkl = make_rsrc(p.k_lo + static_cast<int64_t>(bh) * (p.cap_t / G) * kD, km_bytes);
+  const int vo_k = n * (kD / 2) + 16 * g;           // token n of a 16-token tile, channels 32g..32g+31
+  const int vo_v = l * 16;
+  int vo_m[NB];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb) {
+    const int gc = bb * GPB + gcl;
+    vo_m[bb] = ((gc < NGV ? gc : 0) * 64 + g * 16) * 2;
+  }
+
+  // A nibble masked in place is an fp16 subnormal: c * 2^-24 (low nibble) or 16c * 2^-24 (high
+  // nibble), exact, so every code becomes a matrix-core operand with one and; all products carry
+  // the common factor 2^-24, removed once from the logits and once from the value sums.
+  auto unpack = [&](uint32_t w) -> half8 {
+    const uint32_t w8 = w >> 8;
+    u32x4 r;
+    r[0] = w & 0x000F000Fu;
+    r[1] = w & 0x00F000F0u;
+    r[2] = w8 & 0x000F000Fu;
+    r[3] = w8 & 0x00F000F0u;
+    return as_half8(r);
+  };
+  constexpr float kTwo24 = 16777216.0f;
+  constexpr float kLazy = 4.0f;
+
+  struct Chunk {
+    u32x4 kw[2], vw[2];
+    u32x4 mw[NB][2];
+  };
+  struct KMeta {
+    uint32_t ks0, ks1, kl0, kl1;                     // key scale / lo of channels (c0, c1)
+  };
+  auto load_kmeta = [&](int cb, KMeta& m) {
+    const int sok = __builtin_amdgcn_readfirstlane((cb / G) * kD * 2);
+    m.ks0 = __builtin_amdgcn_raw_buffer_load_b16(rks, c0 * 2, sok, 0);
+    m.ks1 = __builtin_amdgcn_raw_buffer_load_b16(rks, c1 * 2, sok, 0);
+    m.kl0 = __builtin_amdgcn_raw_buffer_load_b16(rkl, c0 * 2, sok, 0);
+    m.kl1 = __builtin_amdgcn_raw_buffer_load_b16(rkl, c1 * 2, sok, 0);
+  };
+  auto load_chunk = [&](int cb, Chunk& c) {
+    // scalar offsets: uniform by construction (readfirstlane keeps them out of waterfall loops)
+    const int so = __builtin_amdgcn_readfirstlane(cb * (kD / 2));   // key rows and value tiles alike
+    c.kw[0] = __builtin_amdgcn_raw_buffer_load_b128(rk, vo_k, so, KVQ_LOAD_AUX);
+    c.kw[1] = __builtin_amdgcn_raw_buffer_load_b128(rk, vo_k + 16 * (kD / 2), so, KVQ_LOAD_AUX);
+    c.vw[0] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo_v, so, KVQ_LOAD_AUX);
+    c.vw[1] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo_v + 1024, so, KVQ_LOAD_AUX);
+    const int som = __builtin_amdgcn_readfirstlane((cb / 32) * NGV * 128);
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      c.mw[bb][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, vo_m[bb], som, KVQ_LOAD_AUX);
+      c.mw[bb][1] = __builtin_amdgcn_raw_buffer_load_b128(rm, vo_m[bb] + 16, som, KVQ_LOAD_AUX);
+    }
+  };
 
   f32x4 acc[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.0f;
-  float S[NB], Z[NB];
+  // probability sums and zero-point sums, split by slot scale: slots 2,3,6,7 hold p/16
+  float m_run = -INFINITY, la = 0.0f, lb = 0.0f;
+  float Za[NB], Zb[NB];
 #pragma unroll
-  for (int k = 0; k < NB; ++k) S[k] = Z[k] = 0.0f;
-
-  float qa[R], qb[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    qa[r] = qs[r][c0];
-    qb[r] = qs[r][c1];
-  }
-  const half8 ones = as_half8(u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
-
-  // ---- software pipeline: the loads of chunk cb+32 are in flight while chunk cb computes ----
-  struct Chunk {
-    u32x4 kw[2], vw[2];
-    u32x4 mw[NB][2];
-    uint32_t ks, kl;                               // key scale / lo pairs of (c0, c1), group start only
-  };
-  auto load_chunk = [&](int cb, Chunk& c) {
-#pragma unroll
-    for (int tau = 0; tau < 2; ++tau)
-      c.kw[tau] = *reinterpret_cast<const u32x4*>(kc + static_cast<int64_t>(cb + 16 * tau + n) * (kD / 2) + 16 * g);
-    const uint8_t* vchunk = vc + static_cast<int64_t>(cb / 32) * (16 * kD);
-#pragma unroll
-    for (int qq = 0; qq < 2; ++qq) c.vw[qq] = *reinterpret_cast<const u32x4*>(vchunk + qq * 1024 + l * 16);
-#pragma unroll
-    for (int bb = 0; bb < NB; ++bb) {
-      const int gc = bb * GPB + gcl;
-      const uint16_t* src = vm + (static_cast<int64_t>(cb / 32) * NGV + (gc < NGV ? gc : 0)) * 64 + g * 16;
-      c.mw[bb][0] = *reinterpret_cast<const u32x4*>(src);
-      c.mw[bb][1] = *reinterpret_cast<const u32x4*>(src + 8);
-    }
-    if ((cb - t0) % G == 0) {
-      const int64_t mo = kmeta_bh + static_cast<int64_t>(cb / G) * kD;
-      c.ks = static_cast<uint32_t>(p.k_sc[mo + c0]) | (static_cast<uint32_t>(p.k_sc[mo + c1]) << 16);
-      c.kl = static_cast<uint32_t>(p.k_lo[mo + c0]) | (static_cast<uint32_t>(p.k_lo[mo + c1]) << 16);
-    }
-  };
-
-  half8 bqk[4];
+  for (int k = 0; k < NB; ++k) Za[k] = Zb[k] = 0.0f;
+  const half8 tiny = as_half8(u32x4{0x00010001u, 0x00010001u, 0x00010001u, 0x00010001u});   // 2^-24
+  const half2v hl_neg = hl_pv ? half2v{static_cast<_Float16>(-1.0f), static_cast<_Float16>(-1.0f)}
+                              : half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
+  const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl_qk) * 64 + g * 16);
+  const u32x4* bv_src = reinterpret_cast<const u32x4*>(bv + r_n * 16 + g * 4);
+#if !KVQ_BQ_LDS
+  half8 bqk[4];                                      // query operand of the current key group
   half8 bvirt;
-  Chunk cur, nxt;
-  if (t0 < t1) load_chunk(t0, nxt);
-  for (int cb = t0; cb < t1; cb += 32) {
-    cur = nxt;
-    if (cb + 32 < t1) load_chunk(cb + 32, nxt);
-    if ((cb - t0) % G == 0) {
+#endif
+
+  KMeta km;                                          // metadata of the next key group, in flight
+  if (t0 < t1) load_kmeta(t0, km);
+  auto step = [&](int cb, const Chunk& c) {
+    if (cb % G == 0) {
+      wave_lds_fence();                              // previous group's operand reads are done
       // ---- per key group: B operand of the scaled query and the logit correction ----
-      const float sc0 = h2f(cur.ks, 0) * kinv, sc1 = h2f(cur.ks, 1) * kinv;
-      const float lo0 = h2f(cur.kl, 0), lo1 = h2f(cur.kl, 1);
+      const _Float16 sc0 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(km.ks0));
+      const _Float16 sc1 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(km.ks1));
+      const _Float16 lo0 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(km.kl0));
+      const _Float16 lo1 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(km.kl1));
+#if KVQ_INTERLEAVE
+      if (cb + kWaves * G < t1) load_kmeta(cb + kWaves * G, km);   // this wavefront's next group
+#else
+      if (cb + G < t1) load_kmeta(cb + G, km);       // next group's metadata while this group runs
+#endif
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float x0 = qa[r] * sc0, x1 = qb[r] * sc1;
-        const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
-        const _Float16 e0 = static_cast<_Float16>(x0 - static_cast<float>(h0));
-        const _Float16 e1 = static_cast<_Float16>(x1 - static_cast<float>(h1));
+        const float qa = qs[r][c0], qb = qs[r][c1];
+        const float qak = qa * kinv, qbk = qb * kinv;
+        const _Float16 h0 = static_cast<_Float16>(qak * static_cast<float>(sc0));
+        const _Float16 h1 = static_cast<_Float16>(qbk * static_cast<float>(sc1));
+        const _Float16 e0 = static_cast<_Float16>(qak * static_cast<float>(sc0) - static_cast<float>(h0));
+        const _Float16 e1 = static_cast<_Float16>(qbk * static_cast<float>(sc1) - static_cast<float>(h1));
         bq[(2 * r) * 64 + l] = pack_h2(h0, h1);
         bq[(2 * r + 1) * 64 + l] = pack_h2(e0, e1);
-        // bias q.lo minus the 1024 offset carried by every A operand element
-        float P = qa[r] * lo0 + qb[r] * lo1 -
-                  1024.0f * ((static_cast<float>(h0) + static_cast<float>(h1)) +
-                             (static_cast<float>(e0) + static_cast<float>(e1)));
+        // logit bias q.lo of this key group (added through the virtual k-step)
+        float P = qa * static_cast<float>(lo0) + qb * static_cast<float>(lo1);
         P += dpp<kQuadSwap1>(P);
         P += dpp<kQuadSwap2>(P);
         if (ck == 0) {
@@ -318,78 +407,85 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
         }
       }
       wave_lds_fence();
-      const u32x4* src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl_qk) * 64 + g * 16);
+#if !KVQ_BQ_LDS
 #pragma unroll
-      for (int i = 0; i < 4; ++i) bqk[i] = as_half8(src[i]);
-      u32x4 bvr = *reinterpret_cast<const u32x4*>(bv + r_n * 16 + g * 4);
+      for (int i = 0; i < 4; ++i) bqk[i] = as_half8(bq_src[i]);
+      u32x4 bvr = *bv_src;
       if (hl_qk) bvr = u32x4{0u, 0u, 0u, 0u};
       bvirt = as_half8(bvr);
-      wave_lds_fence();
+#endif
     }
+#if KVQ_BQ_LDS
+    half8 bqk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bqk[i] = as_half8(bq_src[i]);
+    u32x4 bvr = *bv_src;
+    if (hl_qk) bvr = u32x4{0u, 0u, 0u, 0u};
+    const half8 bvirt = as_half8(bvr);
+#endif
     // ---- logits ----
     float s[8];
 #pragma unroll
     for (int tau = 0; tau < 2; ++tau) {
       f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) d = mfma(unpack4(cur.kw[tau][i]), bqk[i], d);
-      d = mfma(ones, bvirt, d);
+      for (int i = 0; i < 4; ++i) d = mfma(unpack(c.kw[tau][i]), bqk[i], d);
+      d = mfma(tiny, bvirt, d);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float full = d[i] + dpp<kRowRor + R>(d[i]);
-        const int tok = cb + 16 * tau + 4 * g + i;
-        s[4 * tau + i] = tok < t1 ? full : -INFINITY;
-      }
+      for (int i = 0; i < 4; ++i) s[4 * tau + i] = d[i] + dpp<kRowRor + R>(d[i]);   // 2^-24 * logit
     }
-    // ---- online softmax (base 2) ----
-    float cm = s[0];
+    if (cb + 32 > t1) {                              // last chunk of the range: mask past t1
 #pragma unroll
-    for (int j = 1; j < 8; ++j) cm = fmaxf(cm, s[j]);
-    cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
-    cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
-    const float m_new = fmaxf(m_run, cm);
-    if (__any(m_new > m_run)) {
+      for (int j = 0; j < 8; ++j)
+        if (cb + 16 * (j >> 2) + 4 * g + (j & 3) >= t1) s[j] = -INFINITY;
+    }
+    // ---- online softmax (base 2) with a lazy maximum: probabilities are taken against the running
+    // maximum m_run as long as no logit exceeds it by more than kLazy (p <= 2^kLazy = 16, so
+    // p * scale stays far inside fp16 range); only then is the exact chunk maximum reduced across
+    // lanes and everything rescaled.  The first chunk always takes this path (m_run = -inf).
+    float lm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    if (__any(lm * kTwo24 > m_run + kLazy)) {
+      const float cm = xmax32(xmax16(lm)) * kTwo24;
+      const float m_new = fmaxf(m_run, cm);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
       for (int k = 0; k < 8; ++k) acc[k] *= alpha;
-      l_run *= alpha;
 #pragma unroll
       for (int k = 0; k < NB; ++k) {
-        S[k] *= alpha;
-        Z[k] *= alpha;
+        Za[k] *= alpha;
+        Zb[k] *= alpha;
       }
+      la *= alpha;
+      lb *= alpha;
       m_run = m_new;
     }
+    // slots 2,3,6,7 (tile registers 2,3) carry p/16: their value codes are 16x (high nibbles)
+    const float m4 = m_run + 4.0f;
     float pr[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run);
-      l_run += pr[j];
-    }
-    // ---- PV operands: p * sv, hi/lo split; sums of the operands for the 1024 offset ----
+    for (int j = 0; j < 8; ++j) pr[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], kTwo24, -(((j & 3) >= 2) ? m4 : m_run)));
+    la += (pr[0] + pr[1]) + (pr[4] + pr[5]);
+    lb += (pr[2] + pr[3]) + (pr[6] + pr[7]);
+    // ---- PV operands p * sv (hi part, or lo part = p*sv - hi), zero-point sums ----
     half8 bp[NB];
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb) {
-      const int gc = bb * GPB + gcl;
-      const bool gvalid = gc < NGV;
       uint32_t words[4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        _Float16 hv[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int j = 2 * jj + e;
-          const uint32_t mword = cur.mw[bb][j >> 2][j & 3];
-          const float sv = h2f(mword, 0), lv = h2f(mword, 1);
-          const float kv = ((j & 3) >= 2) ? 0.0625f : 1.0f;
-          const float x = gvalid ? pr[j] * sv * kv : 0.0f;
-          const _Float16 hx = static_cast<_Float16>(x);
-          const _Float16 val = hl_pv ? static_cast<_Float16>(x - static_cast<float>(hx)) : hx;
-          hv[e] = val;
-          S[bb] += static_cast<float>(val);
-          Z[bb] += gvalid ? pr[j] * lv : 0.0f;
-        }
-        words[jj] = pack_h2(hv[0], hv[1]);
+        const int j0 = 2 * jj, j1 = 2 * jj + 1;
+        const half2v m0 = h2(c.mw[bb][j0 >> 2][j0 & 3]);          // (sv, lv) of slot j0
+        const half2v m1 = h2(c.mw[bb][j1 >> 2][j1 & 3]);
+        const float x0 = pr[j0] * static_cast<float>(m0[0]);
+        const float x1 = pr[j1] * static_cast<float>(m1[0]);
+        const half2v hi = half2v{static_cast<_Float16>(x0), static_cast<_Float16>(x1)};
+        const half2v cn = hi * hl_neg;                                  // 0 (hi lanes) or -hi (lo lanes)
+        const half2v val = half2v{static_cast<_Float16>(x0 + static_cast<float>(cn[0])),
+                                  static_cast<_Float16>(x1 + static_cast<float>(cn[1]))};
+        words[jj] = w2(val);
+        float& z = ((j0 & 3) >= 2) ? Zb[bb] : Za[bb];
+        z = __builtin_fmaf(pr[j0], static_cast<float>(m0[1]), z);
+        z = __builtin_fmaf(pr[j1], static_cast<float>(m1[1]), z);
       }
       bp[bb] = as_half8(u32x4{words[0], words[1], words[2], words[3]});
     }
@@ -397,21 +493,57 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
       const int gcb = (16 * blk) / GV;
-      acc[blk] = mfma(unpack4(cur.vw[blk >> 2][blk & 3]), bp[gcb / GPB], acc[blk]);
+      acc[blk] = mfma(unpack(c.vw[blk >> 2][blk & 3]), bp[gcb / GPB], acc[blk]);
     }
+  };
+
+#if KVQ_INTERLEAVE
+  // ---- software pipeline over this wavefront's chunks: two register buffers used in turn ----
+  Chunk ca, cb_;
+  if (chunk_tok(0) < t1) load_chunk(chunk_tok(0), ca);
+  for (int k = 0; chunk_tok(k) < t1; k += 2) {
+    const int ta = chunk_tok(k), tb = chunk_tok(k + 1), tc = chunk_tok(k + 2);
+    const bool has2 = tb < t1;
+    if (has2) load_chunk(tb, cb_);
+    step(ta, ca);
+    if (!has2) break;
+    if (tc < t1) load_chunk(tc, ca);
+    step(tb, cb_);
   }
+#elif KVQ_PIPE_DEPTH == 3
+  // ---- software pipeline over chunks: three register buffers, two chunks in flight ----
+  Chunk c0_, c1_, c2_;
+  if (t0 < t1) load_chunk(t0, c0_);
+  if (t0 + 32 < t1) load_chunk(t0 + 32, c1_);
+  for (int cb = t0; cb < t1; cb += 96) {
+    if (cb + 64 < t1) load_chunk(cb + 64, c2_);
+    step(cb, c0_);
+    if (cb + 32 >= t1) break;
+    if (cb + 96 < t1) load_chunk(cb + 96, c0_);
+    step(cb + 32, c1_);
+    if (cb + 64 >= t1) break;
+    if (cb + 128 < t1) load_chunk(cb + 128, c1_);
+    step(cb + 64, c2_);
+  }
+#else
+  // ---- software pipeline over chunks: two register buffers used in turn ----
+  Chunk ca, cb_;
+  if (t0 < t1) load_chunk(t0, ca);
+  for (int cb = t0; cb < t1; cb += 64) {
+    const bool has2 = cb + 32 < t1;
+    if (has2) load_chunk(cb + 32, cb_);
+    step(cb, ca);
+    if (!has2) break;
+    if (cb + 64 < t1) load_chunk(cb + 64, ca);
+    step(cb + 32, cb_);
+  }
+#endif
 
   // ---- wavefront epilogue: row sums over lane groups, hi+lo columns, offset and zero terms ----
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  const float l_run = xsum32(xsum16(la + 16.0f * lb));
+  float Z[NB];
 #pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    S[k] += __shfl_xor(S[k], 16, 64);
-    S[k] += __shfl_xor(S[k], 32, 64);
-    Z[k] += __shfl_xor(Z[k], 16, 64);
-    Z[k] += __shfl_xor(Z[k], 32, 64);
-    S[k] += dpp<kRowShr + R>(S[k]);            // lo column (v odd) gets its hi partner
-  }
+  for (int k = 0; k < NB; ++k) Z[k] = xsum32(xsum16(Za[k] + 16.0f * Zb[k]));
   __syncthreads();                               // q rows / operand scratch no longer needed
   float* red_o = smem;                           // [wave][R][kD]
   float* red_ml = smem + kWaves * R * kD;        // [wave][2][R]
@@ -419,11 +551,11 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   for (int blk = 0; blk < 8; ++blk) {
     const int gcb = (16 * blk) / GV;
     const bool mine = hl_pv == 1 && (gcb % GPB) == gcl;
-    const float Sb = S[gcb / GPB], Zb = Z[gcb / GPB];
+    const float Zv = Z[gcb / GPB];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float a = acc[blk][i] + dpp<kRowShr + R>(acc[blk][i]);
-      if (mine) red_o[(wave * R + r_n) * kD + 16 * blk + 4 * g + i] = a - 1024.0f * Sb + Zb;
+      const float a = acc[blk][i] + dpp<kRowShr + R>(acc[blk][i]);   // hi + lo columns
+      if (mine) red_o[(wave * R + r_n) * kD + 16 * blk + 4 * g + i] = __builtin_fmaf(a, kTwo24, Zv);
     }
   }
   if (g == 0 && n < R) {
@@ -487,8 +619,17 @@ __device__ void merge_bh(const DecodeParams& p, int bh, float* smem) {
 // One block per (b, h, split).  Blocks are dispatched round-robin over the 8 XCDs by linear id,
 // so id -> (xcd = id % 8, k = id / 8) -> bh = xcd + 8*(k / S1), split = k % S1 keeps every
 // split of one (b, h) on one XCD (its query rows and key metadata are read through one L2).
+// Waves per SIMD the register allocation targets: 3 where the loop fits 168 VGPRs without
+// spilling (one PV operand, <= 4 rows), 2 otherwise.
+template <int R, int GV>
+constexpr int split_waves() {
+  constexpr int NB = ((kD / GV) + (8 / R) - 1) / (8 / R);
+  return KVQ_WAVES > 0 ? KVQ_WAVES : ((NB == 1 && R <= 4) ? 3 : 2);
+}
+
 template <int R, int GV, int DT>
-__global__ __launch_bounds__(kThreads) void kivi_decode_split(DecodeParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(split_waves<R, GV>())))
+void kivi_decode_split(DecodeParams p) {
   extern __shared__ float smem[];
   const int id = blockIdx.x;
   const int k = id / 8;

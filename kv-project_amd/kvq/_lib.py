@@ -12,7 +12,10 @@ from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "libkvq.so"
+import os
+
+# the in-tree build; KVQ_LIBRARY may name another build of the same sources (A/B comparisons)
+LIB_PATH = Path(os.environ.get("KVQ_LIBRARY") or (Path(__file__).resolve().parent / "libkvq.so"))
 
 KVQ_F32, KVQ_F16, KVQ_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: KVQ_F32, torch.float16: KVQ_F16, torch.bfloat16: KVQ_BF16}

@@ -26,6 +26,9 @@ HIPCC_FLAGS = [
     # packed fp32 instructions are kept out of every kernel (see the known-issue list of the box)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result", f"-I{INCLUDE}",
+    # matrix-core accumulators in VGPRs: the decode loop's occasional softmax rescale then stays a
+    # plain multiply instead of accumulation-register copies on every iteration
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
@@ -36,9 +39,15 @@ def _hipcc() -> str:
     return h
 
 
-def _compile(src: Path, verbose: bool) -> Path:
-    obj = OBJ / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+# per-source extra flags: the decode kernels never see NaN logits from finite inputs, so max()
+# needs no NaN quieting (no canonicalising instruction before every v_max); infinities (masking)
+# keep their IEEE meaning
+EXTRA_FLAGS = {"decode.hip": ["-fno-honor-nans"]}
+
+
+def _compile(src: Path, verbose: bool, obj_dir: Path, extra=()) -> Path:
+    obj = obj_dir / (src.stem + ".o")
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -50,26 +59,32 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
-def build(jobs: int = 4, verbose: bool = False) -> Path:
-    """Compile and link; always rebuilds every source.  Returns the library path."""
-    OBJ.mkdir(exist_ok=True)
+def build(jobs: int = 4, verbose: bool = False, defines=(), out: Path | None = None) -> Path:
+    """Compile and link; always rebuilds every source.  Returns the library path.
+    ``defines`` (e.g. ["KVQ_PIPE_DEPTH=3"]) and ``out`` build a variant elsewhere."""
+    obj_dir = OBJ if not defines else OBJ.parent / ("_build_" + "_".join(d.replace("=", "") for d in defines))
+    obj_dir.mkdir(exist_ok=True)
+    extra = [f"-D{d}" for d in defines]
     srcs = sorted(CSRC.glob("*.hip"))
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda s: _compile(s, verbose, obj_dir, extra), srcs))
+    lib = Path(out) if out is not None else LIB
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=min(8, os.cpu_count() or 1))
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("-D", dest="defines", action="append", default=[])
+    ap.add_argument("-o", dest="out", default=None)
     a = ap.parse_args()
-    print(build(a.j, a.verbose))
+    print(build(a.j, a.verbose, a.defines, a.out))
