@@ -117,7 +117,7 @@ def main() -> int:
     scaling = shape.d ** -0.5
     out = torch.empty((shape.B, 1, shape.Hq, shape.d), dtype=shape.dtype, device="cuda")
     ws = torch.zeros((kvq.workspace_floats(shape.B, shape.Hq, shape.Hkv, 1, shape.d, cache.n_q, cache.n_exact,
-                                           shape.group_k, args.split_tokens),), dtype=torch.float32,
+                                           shape.group_k, shape.group_v, args.split_tokens),), dtype=torch.float32,
                      device="cuda")
 
     def step():
@@ -155,7 +155,8 @@ def main() -> int:
 
     io_bytes = q.numel() * q.element_size() + out.numel() * out.element_size()
     bytes_alg = cache.payload_bytes() + io_bytes
-    split_bytes = bytes_alg - out.numel() * out.element_size()     # the split kernel writes partials, not out
+    # the split kernel reads the packed rows, the exact rows and q; the output belongs to the merge
+    split_bytes = cache.payload_bytes() + q.numel() * q.element_size()
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
     achieved = split_bytes / (split_ms * 1e-3) / 1e9
     traffic = None

@@ -103,20 +103,24 @@ int kvq_vmeta_tile(const uint16_t* lo, const uint16_t* scale, int64_t BH, int64_
  *    k_lo, k_sc (B*Hkv, cap_t/group_k, d) fp16
  *    vc    (B*Hkv, cap_t/32, 16*d) uint8 value tiles (kvq_v_tile)
  *    vmeta (B*Hkv, cap_t/32, d/group_v, 32, 2) fp16 (kvq_vmeta_tile)
- * Exact rows: k_exact, v_exact (B*Hkv, cap_e, d) of exact_dtype, rows [0, n_exact) used.
+ * Exact rows: k_exact, v_exact (B*Hkv, cap_e, d) of exact_dtype, 16-byte aligned, rows
+ *    [0, n_exact) used.
  *    exact_pos (cap_e,) int64 and q_pos (Tq,) int64 (device, both may be NULL = every exact
  *    row visible): exact row i is visible to query t iff exact_pos[i] <= q_pos[t].
  *    Every packed row is visible to every query.
  * out: (B, Tq, Hq, d) of out_dtype, contiguous (the reference's output layout).
  * workspace: float32 scratch of kvq_kivi_decode_workspace(...) floats (split partials).  Calls
  *    sharing one workspace must not overlap in time (same stream, or ordered streams).
- * split_tokens: packed tokens per workgroup (multiple of 128; 0 = automatic).
- * phases: 3 = split kernel then merge kernel; 1 = only the split kernel (partials into the
- *    workspace); 2 = only the merge kernel over the partials a phases=1 call left (same args).
+ * split_tokens: target packed tokens per workgroup (the packed rows of each (b,h) are cut into
+ *    ceil(n_q / split_tokens) splits of equal 32-token chunk counts; 0 = automatic: the split
+ *    count whose launch fills whole rounds of resident workgroups).
+ * phases: 3 = split kernel then merge kernel; 1 = only the split kernel (partials of the packed
+ *    splits and the exact rows into the workspace); 2 = only the merge kernel (log-sum-exp merge
+ *    of the partials and the output write) after a phases=1 call (same args).
  * Requires d == 128, 4-bit codes, group_k % 32 == 0, group_v in {32, 64, 128}.
  * ---------------------------------------------------------------------------------------- */
 int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
-                                  int64_t n_q, int64_t n_exact, int group_k,
+                                  int64_t n_q, int64_t n_exact, int group_k, int group_v,
                                   int64_t split_tokens);
 int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
                     int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling,

@@ -45,36 +45,22 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Build-time structure of the split kernel's chunk pipeline (defaults are the tuned values):
-//   KVQ_PIPE_DEPTH  chunks held in registers (2: one in flight while one computes; 3: two)
-//   KVQ_BQ_LDS      1: re-read the query operand from LDS for every chunk instead of keeping it
-//                   in 20 VGPRs
+// Build-time switches of the split kernel (defaults are the tuned values):
 //   KVQ_WAVES       waves per SIMD the register allocation targets (0: per-variant default)
-#ifndef KVQ_PIPE_DEPTH
-#define KVQ_PIPE_DEPTH 2
-#endif
-#ifndef KVQ_BQ_LDS
-#define KVQ_BQ_LDS 0
-#endif
-#ifndef KVQ_WAVES
-#define KVQ_WAVES 0
-#endif
-//   KVQ_INTERLEAVE  1: wavefront w of a block takes key groups w, w+4, w+8, ... of the split (the
-//                   four wavefronts stream adjacent memory); 0: one contiguous quarter each
-#ifndef KVQ_INTERLEAVE
-#define KVQ_INTERLEAVE 0
-#endif
 //   KVQ_LOAD_AUX    cache-policy bits of the streaming code/metadata loads (gfx950: 1 = sc0,
 //                   2 = nt, 16 = sc1).  Default nt: every code byte is read once per launch, so
 //                   marking it non-temporal keeps it from displacing reused lines (measured ~4%
 //                   faster on the 16x32x32768 workload than the default policy)
+#ifndef KVQ_WAVES
+#define KVQ_WAVES 0
+#endif
 #ifndef KVQ_LOAD_AUX
 #define KVQ_LOAD_AUX 2
 #endif
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kD = 128;            // head_dim supported by the matrix-core path
-constexpr int kExactRows = 512;    // exact rows per exact-row block
+constexpr int kExactRows = 32;     // exact rows per exact-row block (16 per pass of 4 wavefronts)
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 
@@ -174,33 +160,89 @@ __device__ void load_q_rows(const DecodeParams& p, int b, int h, float (*qs)[kD]
 }
 
 // ---------------------------------------------------------------------------------------------
-// exact rows: plain fp32 attention over rows [e0, e1) of the residual buffer
+// exact rows: fp32 attention over rows [e0, e0 + kExactRows) of the residual buffer
+
+// 8 consecutive elements (16-byte aligned) as floats: one 16-byte load for 16-bit types, two for fp32
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t i, float (&x)[8]) {
+  if constexpr (DT == KVQ_F32) {
+    const float4* p4 = reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    const float4 a = p4[0], c = p4[1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t lo = static_cast<uint16_t>(ws[k] & 0xffffu), hi = static_cast<uint16_t>(ws[k] >> 16);
+      x[2 * k] = DT == KVQ_F16 ? f16_to_f32(lo) : bf16_to_f32(lo);
+      x[2 * k + 1] = DT == KVQ_F16 ? f16_to_f32(hi) : bf16_to_f32(hi);
+    }
+  }
+}
+
+// Partial (m, l, o) of exact-row block `sidx`.  A wavefront takes 4 rows at a time, 16 lanes per
+// row and 8 channels per lane (coalesced 16-byte loads); logits are reduced over the 16 lanes,
+// values are accumulated per lane and reduced over row slots and wavefronts at the end.
 template <int R, int DT>
 __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem) {
   const int b = bh / p.Hkv, h = bh % p.Hkv;
   float (*qs)[kD] = reinterpret_cast<float (*)[kD]>(smem);
   float* sl = smem + R * kD;                        // logits / probabilities [R][kExactRows]
   float* stat = sl + R * kExactRows;                // m[R], l[R]
+  float* red = stat + 2 * R;                        // [wave][R][kD] value sums
   load_q_rows<R, DT>(p, b, h, qs);
   __syncthreads();
   const int e0 = sidx * kExactRows;
   const int ne = min(kExactRows, p.n_exact - e0);
   const int64_t kbase = static_cast<int64_t>(bh) * p.cap_e * kD;
-  for (int idx = threadIdx.x; idx < p.R_real * ne; idx += kThreads) {
-    const int r = idx / ne, i = idx % ne;
-    const int e = e0 + i;
-    bool vis = true;
-    if (p.exact_pos != nullptr && p.q_pos != nullptr) vis = p.exact_pos[e] <= p.q_pos[r % p.Tq];
-    float acc = 0.0f;
-    if (vis) {
-      const int64_t ro = kbase + static_cast<int64_t>(e) * kD;
-#pragma unroll 8
-      for (int c = 0; c < kD; ++c) acc += qs[r][c] * load_as_f32<DT>(p.k_exact, ro + c);
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int j = lane >> 4, part = lane & 15;       // row slot of 4, 8-channel slice of 16
+  const bool masked = p.exact_pos != nullptr && p.q_pos != nullptr;
+  float qv[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) qv[r][k] = qs[r][8 * part + k];
+  // every key and value row slice of this lane is loaded before any is used, so all the block's
+  // loads are in flight together (kExactRows = 16 rows per pass x kPass passes)
+  constexpr int kStride = 4 * kWaves;
+  constexpr int kPass = kExactRows / kStride;
+  float kx[kPass][8], vx[kPass][8];
+#pragma unroll
+  for (int u = 0; u < kPass; ++u) {
+    const int i = 4 * wave + kStride * u + j;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) kx[u][k] = vx[u][k] = 0.0f;
+    if (i < ne) {
+      load8<DT>(p.k_exact, kbase + static_cast<int64_t>(e0 + i) * kD + 8 * part, kx[u]);
+      load8<DT>(p.v_exact, kbase + static_cast<int64_t>(e0 + i) * kD + 8 * part, vx[u]);
     }
-    sl[r * kExactRows + i] = vis ? acc : -INFINITY;
+  }
+#pragma unroll
+  for (int u = 0; u < kPass; ++u) {
+    const int i = 4 * wave + kStride * u + j;
+    float d[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float t = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) t = __builtin_fmaf(qv[r][k], kx[u][k], t);
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) t += __shfl_xor(t, o, 16);
+      d[r] = t;
+    }
+    if (part == 0 && i < ne) {
+      const int64_t ep = masked ? p.exact_pos[e0 + i] : 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const bool vis = !masked || ep <= p.q_pos[r % p.Tq];
+        sl[r * kExactRows + i] = r < p.R_real ? (vis ? d[r] : -INFINITY) : 0.0f;
+      }
+    }
   }
   __syncthreads();
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   for (int r = wave; r < p.R_real; r += kWaves) {
     float mx = -INFINITY;
     for (int i = lane; i < ne; i += 64) mx = fmaxf(mx, sl[r * kExactRows + i]);
@@ -219,12 +261,39 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
     }
   }
   __syncthreads();
+  float o[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[r][k] = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kPass; ++u) {
+    const int i = 4 * wave + kStride * u + j;
+    if (i < ne) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float pr = sl[r * kExactRows + i];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[r][k] = __builtin_fmaf(pr, vx[u][k], o[r][k]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float t = o[r][k];
+      t += __shfl_xor(t, 16, 64);
+      t += __shfl_xor(t, 32, 64);
+      if (j == 0) red[(wave * R + r) * kD + 8 * part + k] = t;
+    }
+  __syncthreads();
   const int64_t po = static_cast<int64_t>(bh) * p.S1 + sidx;
   for (int idx = threadIdx.x; idx < p.R_real * kD; idx += kThreads) {
     const int r = idx / kD, c = idx % kD;
     float acc = 0.0f;
-    for (int i = 0; i < ne; ++i)
-      acc += sl[r * kExactRows + i] * load_as_f32<DT>(p.v_exact, kbase + static_cast<int64_t>(e0 + i) * kD + c);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) acc += red[(w * R + r) * kD + c];
     p.ws_o[(po * R + r) * kD + c] = acc;
     if (c == 0) {
       p.ws_m[po * R + r] = stat[r];
@@ -275,20 +344,18 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   uint32_t* bq = bq_all + wave * 2 * R * 64;
   uint32_t* bv = bv_all + wave * R * 16;
 
-  const int ST = p.split_tokens;
-  const int WT = ST / kWaves;
-  const int s_begin = (sidx - p.n_exact_wg) * ST;
+  // wavefront w = sidx * 4 + wave of this (b, h) takes chunks [w * NC / NW, (w + 1) * NC / NW) of
+  // the NC 32-token chunks (balanced to one chunk; a range may start inside a key group)
   const int G = p.group_k;
-#if KVQ_INTERLEAVE
-  // chunk k of this wavefront starts at token s_begin + ((k / cpg) * 4 + wave) * G + (k % cpg) * 32
-  const int cpg = G / 32;
-  const int t1 = min(s_begin + ST, p.n_q);           // valid tokens of the whole split
-  const int t0 = s_begin + wave * G;
-  auto chunk_tok = [&](int k) { return s_begin + ((k / cpg) * kWaves + wave) * G + (k % cpg) * 32; };
-#else
-  const int t0 = s_begin + wave * WT;
-  const int t1 = min(t0 + WT, p.n_q);
-#endif
+  const int NC = (p.n_q + 31) / 32;
+  const int NW = p.n_split * kWaves;
+  const int w_all = sidx * kWaves + wave;
+  const int t0 = 32 * static_cast<int>(static_cast<int64_t>(w_all) * NC / NW);
+  const int t1 = min(32 * static_cast<int>(static_cast<int64_t>(w_all + 1) * NC / NW), p.n_q);
+  // start of this wavefront's last chunk: loads past it are clamped onto it (they then hit in
+  // cache), so every load of the pipeline is unconditional and the wait before each chunk's
+  // compute counts exactly the loads issued after that chunk's
+  const int t_last = t0 < t1 ? t0 + ((t1 - 1 - t0) & ~31) : t0;
 
   // buffer resources over this (b, h)'s slices; chunk advance goes in the scalar offset
   const uint32_t code_bytes = static_cast<uint32_t>(p.cap_t) * (kD / 2);
@@ -324,21 +391,15 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   constexpr float kTwo24 = 16777216.0f;
   constexpr float kLazy = 4.0f;
 
+  // one 32-token chunk of this wavefront: key rows, value tile, value metadata, and the key
+  // scale / zero of channels (c0, c1) of the chunk's key group (used when the chunk starts one)
   struct Chunk {
     u32x4 kw[2], vw[2];
     u32x4 mw[NB][2];
-  };
-  struct KMeta {
-    uint32_t ks0, ks1, kl0, kl1;                     // key scale / lo of channels (c0, c1)
-  };
-  auto load_kmeta = [&](int cb, KMeta& m) {
-    const int sok = __builtin_amdgcn_readfirstlane((cb / G) * kD * 2);
-    m.ks0 = __builtin_amdgcn_raw_buffer_load_b16(rks, c0 * 2, sok, 0);
-    m.ks1 = __builtin_amdgcn_raw_buffer_load_b16(rks, c1 * 2, sok, 0);
-    m.kl0 = __builtin_amdgcn_raw_buffer_load_b16(rkl, c0 * 2, sok, 0);
-    m.kl1 = __builtin_amdgcn_raw_buffer_load_b16(rkl, c1 * 2, sok, 0);
+    uint32_t ks0, ks1, kl0, kl1;
   };
   auto load_chunk = [&](int cb, Chunk& c) {
+    cb = min(cb, t_last);
     // scalar offsets: uniform by construction (readfirstlane keeps them out of waterfall loops)
     const int so = __builtin_amdgcn_readfirstlane(cb * (kD / 2));   // key rows and value tiles alike
     c.kw[0] = __builtin_amdgcn_raw_buffer_load_b128(rk, vo_k, so, KVQ_LOAD_AUX);
@@ -351,6 +412,11 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
       c.mw[bb][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, vo_m[bb], som, KVQ_LOAD_AUX);
       c.mw[bb][1] = __builtin_amdgcn_raw_buffer_load_b128(rm, vo_m[bb] + 16, som, KVQ_LOAD_AUX);
     }
+    const int sok = __builtin_amdgcn_readfirstlane((cb / G) * kD * 2);
+    c.ks0 = __builtin_amdgcn_raw_buffer_load_b16(rks, c0 * 2, sok, 0);
+    c.ks1 = __builtin_amdgcn_raw_buffer_load_b16(rks, c1 * 2, sok, 0);
+    c.kl0 = __builtin_amdgcn_raw_buffer_load_b16(rkl, c0 * 2, sok, 0);
+    c.kl1 = __builtin_amdgcn_raw_buffer_load_b16(rkl, c1 * 2, sok, 0);
   };
 
   f32x4 acc[8];
@@ -366,26 +432,17 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
                               : half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
   const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl_qk) * 64 + g * 16);
   const u32x4* bv_src = reinterpret_cast<const u32x4*>(bv + r_n * 16 + g * 4);
-#if !KVQ_BQ_LDS
   half8 bqk[4];                                      // query operand of the current key group
   half8 bvirt;
-#endif
 
-  KMeta km;                                          // metadata of the next key group, in flight
-  if (t0 < t1) load_kmeta(t0, km);
   auto step = [&](int cb, const Chunk& c) {
-    if (cb % G == 0) {
+    if (cb % G == 0 || cb == t0) {
       wave_lds_fence();                              // previous group's operand reads are done
       // ---- per key group: B operand of the scaled query and the logit correction ----
-      const _Float16 sc0 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(km.ks0));
-      const _Float16 sc1 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(km.ks1));
-      const _Float16 lo0 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(km.kl0));
-      const _Float16 lo1 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(km.kl1));
-#if KVQ_INTERLEAVE
-      if (cb + kWaves * G < t1) load_kmeta(cb + kWaves * G, km);   // this wavefront's next group
-#else
-      if (cb + G < t1) load_kmeta(cb + G, km);       // next group's metadata while this group runs
-#endif
+      const _Float16 sc0 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(c.ks0));
+      const _Float16 sc1 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(c.ks1));
+      const _Float16 lo0 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(c.kl0));
+      const _Float16 lo1 = __builtin_bit_cast(_Float16, static_cast<uint16_t>(c.kl1));
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const float qa = qs[r][c0], qb = qs[r][c1];
@@ -407,22 +464,12 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
         }
       }
       wave_lds_fence();
-#if !KVQ_BQ_LDS
 #pragma unroll
       for (int i = 0; i < 4; ++i) bqk[i] = as_half8(bq_src[i]);
       u32x4 bvr = *bv_src;
       if (hl_qk) bvr = u32x4{0u, 0u, 0u, 0u};
       bvirt = as_half8(bvr);
-#endif
     }
-#if KVQ_BQ_LDS
-    half8 bqk[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) bqk[i] = as_half8(bq_src[i]);
-    u32x4 bvr = *bv_src;
-    if (hl_qk) bvr = u32x4{0u, 0u, 0u, 0u};
-    const half8 bvirt = as_half8(bvr);
-#endif
     // ---- logits ----
     float s[8];
 #pragma unroll
@@ -476,12 +523,13 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
         const int j0 = 2 * jj, j1 = 2 * jj + 1;
         const half2v m0 = h2(c.mw[bb][j0 >> 2][j0 & 3]);          // (sv, lv) of slot j0
         const half2v m1 = h2(c.mw[bb][j1 >> 2][j1 & 3]);
-        const float x0 = pr[j0] * static_cast<float>(m0[0]);
-        const float x1 = pr[j1] * static_cast<float>(m1[0]);
-        const half2v hi = half2v{static_cast<_Float16>(x0), static_cast<_Float16>(x1)};
+        // hi = fp16(p * sv) rounded once from the exact product (a mixed-precision fma each);
+        // lo = fp16(p * sv - hi), again from the exact product
+        const half2v hi = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], static_cast<float>(m0[0]), 0.0f)),
+                                 static_cast<_Float16>(__builtin_fmaf(pr[j1], static_cast<float>(m1[0]), 0.0f))};
         const half2v cn = hi * hl_neg;                                  // 0 (hi lanes) or -hi (lo lanes)
-        const half2v val = half2v{static_cast<_Float16>(x0 + static_cast<float>(cn[0])),
-                                  static_cast<_Float16>(x1 + static_cast<float>(cn[1]))};
+        const half2v val = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], static_cast<float>(m0[0]), static_cast<float>(cn[0]))),
+                                  static_cast<_Float16>(__builtin_fmaf(pr[j1], static_cast<float>(m1[0]), static_cast<float>(cn[1])))};
         words[jj] = w2(val);
         float& z = ((j0 & 3) >= 2) ? Zb[bb] : Za[bb];
         z = __builtin_fmaf(pr[j0], static_cast<float>(m0[1]), z);
@@ -497,47 +545,20 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     }
   };
 
-#if KVQ_INTERLEAVE
-  // ---- software pipeline over this wavefront's chunks: two register buffers used in turn ----
-  Chunk ca, cb_;
-  if (chunk_tok(0) < t1) load_chunk(chunk_tok(0), ca);
-  for (int k = 0; chunk_tok(k) < t1; k += 2) {
-    const int ta = chunk_tok(k), tb = chunk_tok(k + 1), tc = chunk_tok(k + 2);
-    const bool has2 = tb < t1;
-    if (has2) load_chunk(tb, cb_);
-    step(ta, ca);
-    if (!has2) break;
-    if (tc < t1) load_chunk(tc, ca);
-    step(tb, cb_);
+  // ---- software pipeline over chunks: two register buffers used in turn; the load of the next
+  // chunk is always issued (clamped) before the current chunk is computed ----
+  if (t0 < t1) {
+    Chunk ca, cb_;
+    load_chunk(t0, ca);
+    for (int cb = t0;; cb += 64) {
+      load_chunk(cb + 32, cb_);
+      step(cb, ca);
+      if (cb + 32 >= t1) break;
+      load_chunk(cb + 64, ca);
+      step(cb + 32, cb_);
+      if (cb + 64 >= t1) break;
+    }
   }
-#elif KVQ_PIPE_DEPTH == 3
-  // ---- software pipeline over chunks: three register buffers, two chunks in flight ----
-  Chunk c0_, c1_, c2_;
-  if (t0 < t1) load_chunk(t0, c0_);
-  if (t0 + 32 < t1) load_chunk(t0 + 32, c1_);
-  for (int cb = t0; cb < t1; cb += 96) {
-    if (cb + 64 < t1) load_chunk(cb + 64, c2_);
-    step(cb, c0_);
-    if (cb + 32 >= t1) break;
-    if (cb + 96 < t1) load_chunk(cb + 96, c0_);
-    step(cb + 32, c1_);
-    if (cb + 64 >= t1) break;
-    if (cb + 128 < t1) load_chunk(cb + 128, c1_);
-    step(cb + 64, c2_);
-  }
-#else
-  // ---- software pipeline over chunks: two register buffers used in turn ----
-  Chunk ca, cb_;
-  if (t0 < t1) load_chunk(t0, ca);
-  for (int cb = t0; cb < t1; cb += 64) {
-    const bool has2 = cb + 32 < t1;
-    if (has2) load_chunk(cb + 32, cb_);
-    step(cb, ca);
-    if (!has2) break;
-    if (cb + 64 < t1) load_chunk(cb + 64, ca);
-    step(cb + 32, cb_);
-  }
-#endif
 
   // ---- wavefront epilogue: row sums over lane groups, hi+lo columns, offset and zero terms ----
   const float l_run = xsum32(xsum16(la + 16.0f * lb));
@@ -563,7 +584,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     red_ml[(wave * 2 + 1) * R + n] = l_run;
   }
   __syncthreads();
-  const int64_t po = static_cast<int64_t>(bh) * p.S1 + sidx;
+  const int64_t po = static_cast<int64_t>(bh) * p.S1 + p.n_exact_wg + sidx;
   for (int idx = threadIdx.x; idx < p.R_real * kD; idx += kThreads) {
     const int r = idx / kD, c = idx % kD;
     float M = -INFINITY;
@@ -631,13 +652,21 @@ template <int R, int GV, int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(split_waves<R, GV>())))
 void kivi_decode_split(DecodeParams p) {
   extern __shared__ float smem[];
+  const int bh_pad = (p.BH + 7) / 8 * 8;
+  const int n_packed = p.n_split * bh_pad;
   const int id = blockIdx.x;
-  const int k = id / 8;
-  const int bh = id % 8 + 8 * (k / p.S1);
-  const int sidx = k % p.S1;
-  if (bh >= p.BH) return;
-  if (sidx < p.n_exact_wg) exact_block<R, DT>(p, bh, sidx, smem);
-  else packed_block<R, GV, DT>(p, bh, sidx, smem);
+  if (id < n_packed) {
+    const int k = id / 8;
+    const int bh = id % 8 + 8 * (k / p.n_split);
+    if (bh < p.BH) packed_block<R, GV, DT>(p, bh, k % p.n_split, smem);
+  } else {
+    // exact-row blocks come last in dispatch order: they take the slots that packed blocks free
+    // at the end of their round
+    const int e_id = id - n_packed;
+    const int k = e_id / 8;
+    const int bh = e_id % 8 + 8 * (k / p.n_exact_wg);
+    if (bh < p.BH) exact_block<R, DT>(p, bh, k % p.n_exact_wg, smem);
+  }
 }
 
 template <int R, int DT>
@@ -648,15 +677,15 @@ __global__ __launch_bounds__(kThreads) void kivi_decode_merge(DecodeParams p) {
 
 template <int R, int GV, int DT>
 int launch(DecodeParams& p, int phases, hipStream_t stream) {
-  const size_t exact_smem = (R * kD + R * kExactRows + 2 * R) * sizeof(float);
+  const size_t exact_smem = (R * kD + R * kExactRows + 2 * R + kWaves * R * kD) * sizeof(float);
   const size_t packed_smem = std::max<size_t>((R * kD) * sizeof(float) + kWaves * (2 * R * 64 + R * 16) * 4,
                                               (kWaves * R * kD + kWaves * 2 * R) * sizeof(float));
   const size_t msmem = (static_cast<size_t>(p.S1) * R + R) * sizeof(float);
-  const size_t smem = std::max({exact_smem, packed_smem, msmem});
   const int bh_pad = (p.BH + 7) / 8 * 8;
   const dim3 grid(static_cast<unsigned>(p.S1) * bh_pad);
   if (phases & 1) {
-    hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), grid, dim3(kThreads), smem, stream, p);
+    hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), grid, dim3(kThreads), std::max(packed_smem, exact_smem),
+                       stream, p);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(split)");
   }
   if (phases & 2) {
@@ -676,22 +705,47 @@ struct SplitPlan {
   int n_exact_wg, n_split, split_tokens, S1, R;
 };
 
+constexpr int kCUs = 256;          // MI355X compute units
+constexpr int64_t kBlockCost = 1024;
+
 inline SplitPlan plan_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t n_q,
-                            int64_t n_exact, int64_t split_tokens, int group_k) {
+                            int64_t n_exact, int64_t split_tokens, int group_k, int group_v) {
   SplitPlan sp;
   sp.R = pow2_rows((Hq / Hkv) * Tq);
-  const int64_t unit = kWaves * std::max<int64_t>(group_k, 32);
-  int64_t st = split_tokens;
-  if (st <= 0) {
-    const int64_t target = 1024;                         // ~4 blocks per CU on 256 CUs
-    const int64_t per = (n_q * B * Hkv + target - 1) / target;
-    st = std::max<int64_t>(unit, (per + unit - 1) / unit * unit);
-  } else {
-    st = (st + unit - 1) / unit * unit;
+  // blocks resident per CU = waves per SIMD of the variant (one wavefront of each block per SIMD)
+  int resident_blocks = 2;
+  switch (sp.R) {
+    case 1: resident_blocks = group_v == 128 ? split_waves<1, 128>() : group_v == 64 ? split_waves<1, 64>() : split_waves<1, 32>(); break;
+    case 2: resident_blocks = group_v == 128 ? split_waves<2, 128>() : group_v == 64 ? split_waves<2, 64>() : split_waves<2, 32>(); break;
+    case 4: resident_blocks = group_v == 128 ? split_waves<4, 128>() : group_v == 64 ? split_waves<4, 64>() : split_waves<4, 32>(); break;
+    default: resident_blocks = group_v == 128 ? split_waves<8, 128>() : group_v == 64 ? split_waves<8, 64>() : split_waves<8, 32>(); break;
   }
-  sp.split_tokens = static_cast<int>(st);
-  sp.n_split = static_cast<int>((n_q + st - 1) / st);
+  const int64_t nc = (n_q + 31) / 32;                   // 32-token chunks per (b, h)
   sp.n_exact_wg = static_cast<int>((n_exact + kExactRows - 1) / kExactRows);
+  int64_t ns = 0;
+  if (nc > 0 && split_tokens > 0) {
+    ns = (n_q + split_tokens - 1) / split_tokens;
+  } else if (nc > 0) {
+    // Fewest rounds of resident blocks times (chunks of the longest wavefront + a fixed per-block
+    // cost of kBlockCost tokens: query load, operand set-up, partial write, one more merge
+    // input): blocks of one launch run in ceil(blocks / slots) rounds.  Ties go to fewer splits.
+    const int64_t bh = B * Hkv;
+    const int64_t slots = static_cast<int64_t>(kCUs) * resident_blocks;
+    int64_t best_cost = 0;
+    for (int64_t cand = 1; cand <= std::min<int64_t>((nc + kWaves - 1) / kWaves, 512); ++cand) {
+      const int64_t per_wave = (nc + cand * kWaves - 1) / (cand * kWaves);
+      const int64_t rounds = (bh * cand + slots - 1) / slots;
+      const int64_t cost = rounds * (32 * per_wave * kWaves + kBlockCost);
+      if (ns == 0 || cost < best_cost) {
+        ns = cand;
+        best_cost = cost;
+      }
+    }
+  }
+  // every wavefront gets at least one chunk
+  ns = std::min<int64_t>(ns, (nc + kWaves - 1) / kWaves);
+  sp.n_split = static_cast<int>(ns);
+  sp.split_tokens = ns > 0 ? static_cast<int>((n_q + ns - 1) / ns) : 0;
   sp.S1 = sp.n_exact_wg + sp.n_split;
   return sp;
 }
@@ -703,9 +757,10 @@ using namespace kvq;
 
 extern "C" int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq,
                                              int64_t d, int64_t n_q, int64_t n_exact,
-                                             int group_k, int64_t split_tokens) {
+                                             int group_k, int group_v, int64_t split_tokens) {
   if (d != kD || B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Tq <= 0 || group_k <= 0) return -1;
-  const SplitPlan sp = plan_split(B, Hq, Hkv, Tq, n_q, n_exact, split_tokens, group_k);
+  if (group_v != 32 && group_v != 64 && group_v != 128) return -1;
+  const SplitPlan sp = plan_split(B, Hq, Hkv, Tq, n_q, n_exact, split_tokens, group_k, group_v);
   return B * Hkv * static_cast<int64_t>(sp.S1) * sp.R * (kD + 2);
 }
 
@@ -730,15 +785,18 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   KVQ_REQUIRE(group_v == 32 || group_v == 64 || group_v == 128, "kvq_kivi_decode: group_v in {32,64,128}");
   KVQ_REQUIRE(cap_t % group_k == 0 && cap_t % 32 == 0 && n_q >= 0 && n_q <= cap_t,
               "kvq_kivi_decode: cap_t must be a multiple of group_k and 32, 0 <= n_q <= cap_t");
-  KVQ_REQUIRE(n_exact >= 0 && n_exact <= cap_e && n_exact <= 128 * kExactRows,
+  KVQ_REQUIRE(n_exact >= 0 && n_exact <= cap_e && n_exact <= 65536,
               "kvq_kivi_decode: bad n_exact");
   KVQ_REQUIRE(n_q + n_exact > 0, "kvq_kivi_decode: empty cache");
   KVQ_REQUIRE(n_q == 0 || (kc && k_lo && k_sc && vc && vmeta), "kvq_kivi_decode: null packed cache");
   KVQ_REQUIRE(n_exact == 0 || (k_exact && v_exact), "kvq_kivi_decode: null exact rows");
+  KVQ_REQUIRE(n_exact == 0 || (reinterpret_cast<uintptr_t>(k_exact) % 16 == 0 &&
+                               reinterpret_cast<uintptr_t>(v_exact) % 16 == 0),
+              "kvq_kivi_decode: exact rows must be 16-byte aligned");
   KVQ_REQUIRE(q && out && workspace, "kvq_kivi_decode: null q/out/workspace");
   KVQ_REQUIRE((exact_pos == nullptr) == (q_pos == nullptr), "kvq_kivi_decode: exact_pos and q_pos go together");
   KVQ_REQUIRE(n_q < (1LL << 31) && B * Hkv < 65536, "kvq_kivi_decode: sizes out of range");
-  const SplitPlan sp = plan_split(B, Hq, Hkv, Tq, n_q, n_exact, split_tokens, group_k);
+  const SplitPlan sp = plan_split(B, Hq, Hkv, Tq, n_q, n_exact, split_tokens, group_k, group_v);
   const int64_t need = B * Hkv * static_cast<int64_t>(sp.S1) * sp.R * (kD + 2);
   KVQ_REQUIRE(static_cast<int64_t>(sp.S1) * R_real <= 16384, "kvq_kivi_decode: too many splits");
   KVQ_REQUIRE(workspace_floats >= need, "kvq_kivi_decode: workspace too small (%lld < %lld floats)",

@@ -121,21 +121,31 @@ class PackedKIVICache:
         self.n_q = max(0, self.next_pos - W)
         self.n_exact = min(self.next_pos, W)
 
-    def payload_bytes(self) -> int:
-        """Bytes a decode step reads: codes and metadata of the n_q packed rows + exact rows."""
+    def packed_bytes(self) -> int:
+        """Bytes of the n_q packed rows a decode step reads: 4-bit codes + fp16 metadata."""
         B, H = self.kc.shape[:2]
         d = self.kc.shape[3] * 2
         n_g = -(-self.n_q // self.group_k)
         codes = 2 * B * H * self.n_q * d // 2
         kmeta = B * H * n_g * d * 4
         vmeta = B * H * self.n_q * (d // self.group_v) * 4
-        exact = 2 * B * H * self.n_exact * d * self.k_exact.element_size()
-        return codes + kmeta + vmeta + exact
+        return codes + kmeta + vmeta
+
+    def exact_bytes(self) -> int:
+        """Bytes of the n_exact exact key/value rows a decode step reads."""
+        B, H = self.kc.shape[:2]
+        d = self.kc.shape[3] * 2
+        return 2 * B * H * self.n_exact * d * self.k_exact.element_size()
+
+    def payload_bytes(self) -> int:
+        """Bytes a decode step reads: codes and metadata of the n_q packed rows + exact rows."""
+        return self.packed_bytes() + self.exact_bytes()
 
 
 def workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_q: int, n_exact: int,
-                     group_k: int, split_tokens: int = 0) -> int:
-    n = _lib.load().kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, d, n_q, n_exact, group_k, split_tokens)
+                     group_k: int, group_v: int, split_tokens: int = 0) -> int:
+    n = _lib.load().kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, d, n_q, n_exact, group_k, group_v,
+                                              split_tokens)
     if n < 0:
         raise _lib.KVQError("kvq_kivi_decode_workspace rejected the shape")
     return n
@@ -160,7 +170,8 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
         raise TypeError("q and the exact rows must share a dtype")
     if out is None:
         out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
-    need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, split_tokens)
+    need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, cache.group_v,
+                            split_tokens)
     if workspace is None or workspace.numel() < need:
         workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)   # counters start at zero
     ep = cache.exact_pos if q_pos is not None else None

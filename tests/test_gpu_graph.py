@@ -15,7 +15,7 @@ def test_graph_replays_match_eager():
     cache = kvq.PackedKIVICache.from_context(K, V, window=128, group_k=64, group_v=64)
     q = torch.randn((B, Hq, 1, d), generator=g, device="cuda").bfloat16()
     out = torch.empty((B, 1, Hq, d), dtype=torch.bfloat16, device="cuda")
-    ws = torch.zeros((kvq.workspace_floats(B, Hq, Hkv, 1, d, cache.n_q, cache.n_exact, 64),), device="cuda")
+    ws = torch.zeros((kvq.workspace_floats(B, Hq, Hkv, 1, d, cache.n_q, cache.n_exact, 64, 64),), device="cuda")
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
