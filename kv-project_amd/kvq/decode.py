@@ -173,7 +173,7 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
     need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, cache.group_v,
                             split_tokens)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)   # counters start at zero
+        workspace = torch.empty((need,), dtype=torch.float32, device=q.device)
     ep = cache.exact_pos if q_pos is not None else None
     qp = q_pos if ep is not None else None
     dt = _lib.DTYPE_CODE[q.dtype]
@@ -185,3 +185,39 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
               _lib.ptr(ep), _lib.ptr(qp), out.data_ptr(), dt, workspace.data_ptr(), workspace.numel(),
               split_tokens, phases, _lib.stream_of(q))
     return out
+
+
+def _unpack_rows(rows: torch.Tensor) -> torch.Tensor:
+    """pack_codes rows (..., d/2) uint8 -> codes (..., d) int: channel 2i in the high nibble."""
+    hi, lo = (rows >> 4).to(torch.int32), (rows & 15).to(torch.int32)
+    return torch.stack([hi, lo], -1).flatten(-2)
+
+
+def _dequant_keys(c: PackedKIVICache) -> torch.Tensor:
+    """Dequantised keys of the n_q packed rows, float32 (B, Hkv, n_q, d): code * scale + lo."""
+    codes = _unpack_rows(c.kc[:, :, :c.n_q]).float()
+    g = torch.arange(c.n_q, device=c.kc.device) // c.group_k
+    sc = c.k_sc[:, :, g].float()
+    lo = c.k_lo[:, :, g].float()
+    return codes * sc + lo
+
+
+# token of each of the 32 metadata slots of a value tile: slot 8g + j holds token
+# 16 * (j >> 2) + 4g + (j & 3)
+_SLOT_TOKEN = [16 * (j >> 2) + 4 * g + (j & 3) for g in range(4) for j in range(8)]
+
+
+def _dequant_values(c: PackedKIVICache) -> torch.Tensor:
+    """Dequantised values of the n_q packed rows, float32 (B, Hkv, n_q, d)."""
+    from .kivi import v_untile
+    B, H = c.kc.shape[:2]
+    d = c.kc.shape[3] * 2
+    codes = _unpack_rows(v_untile(c.vc, c.n_q)).float()                     # (B, H, n_q, d)
+    ngv = d // c.group_v
+    inv = torch.empty(32, dtype=torch.long)
+    inv[torch.tensor(_SLOT_TOKEN)] = torch.arange(32)
+    vm = c.vmeta[:, :, :, :, inv.to(c.vmeta.device)]                          # token order
+    vm = vm.permute(0, 1, 2, 4, 3, 5).reshape(B, H, -1, ngv, 2)[:, :, :c.n_q].float()
+    sc = vm[..., 0].repeat_interleave(c.group_v, -1)
+    lo = vm[..., 1].repeat_interleave(c.group_v, -1)
+    return codes * sc + lo
