@@ -114,9 +114,16 @@ int kvq_vmeta_tile(const uint16_t* lo, const uint16_t* scale, int64_t BH, int64_
  * split_tokens: target packed tokens per workgroup (the packed rows of each (b,h) are cut into
  *    ceil(n_q / split_tokens) splits of equal 32-token chunk counts; 0 = automatic: the split
  *    count whose launch fills whole rounds of resident workgroups).
- * phases: 3 = split kernel then merge kernel; 1 = only the split kernel (partials of the packed
- *    splits and the exact rows into the workspace); 2 = only the merge kernel (log-sum-exp merge
- *    of the partials and the output write) after a phases=1 call (same args).
+ * scores (optional, NULL = plain decode): (B*Hkv, scores_bh) float32, one row per (b, KV head)
+ *    over the n_q packed positions.  The score pass adds score_weight * (sum over the rows of the
+ *    KV head of each row's softmax probability of the packed token) to scores[bh][t]: the
+ *    decode-time form of SnapKV's scores (STRATA_KV.py:932-954: mean over the query heads of a
+ *    KV group and over queries, with score_weight = 1 / (rep * Tq * steps)).  The softmax runs over
+ *    packed and visible exact rows, as the decode's.
+ * phases (bit mask): 1 = split kernel (partials of the packed splits and the exact rows into the
+ *    workspace); 2 = merge kernel (log-sum-exp merge, output write, and each row's global max/sum
+ *    into the workspace); 4 = score pass (needs scores; reads the row statistics of a merge of
+ *    the same call or an earlier one with the same args).  3 = decode, 7 = decode + scores.
  * Requires d == 128, 4-bit codes, group_k % 32 == 0, group_v in {32, 64, 128}.
  * ---------------------------------------------------------------------------------------- */
 int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
@@ -129,8 +136,33 @@ int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int6
                     int group_k, int group_v, const void* k_exact, const void* v_exact,
                     int exact_dtype, int64_t cap_e, int64_t n_exact, const int64_t* exact_pos,
                     const int64_t* q_pos, void* out, int out_dtype, float* workspace,
-                    int64_t workspace_floats, int64_t split_tokens, int phases,
-                    void* stream);
+                    int64_t workspace_floats, float* scores, int64_t scores_bh, float score_weight,
+                    int64_t split_tokens, int phases, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * A7  Top-k retention of accumulated scores.  Replaces scores.topk(k).indices.sort() of the
+ * SnapKV / MTLP selection (STRATA_KV.py:975, 1022-1023): for each of BH rows of n float32
+ * scores (row stride scores_bh), writes the positions of the k largest in increasing order to
+ * idx (int32, row stride idx_bh).  Among scores equal to the k-th largest the lowest positions
+ * are kept (the reference's torch.topk leaves that order unspecified).  The caller keeps the
+ * recent window (the exact rows) by passing only the packed positions.  0 <= k <= n < 2^31.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_topk_retain(const float* scores, int64_t BH, int64_t n, int64_t scores_bh, int64_t k,
+                    int32_t* idx, int64_t idx_bh, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * A7  Retained-set rows for the gathered decode.  For each (b, h) and i < count, position
+ * t = idx[bh*idx_bh + i] of the packed cache (layout as kvq_kivi_decode) is dequantised the way
+ * kivi_quant's xhat is (code * scale + lo in fp32, STRATA_KV.py:855) and written, rounded to
+ * out_dtype, to k_out / v_out (B*Hkv, out_bh elements per (b,h), row i at i*d).  Positions must
+ * lie in [0, n_valid); others produce NaN rows.  The decode over the retained set is then
+ * kvq_kivi_decode with these rows (plus the recent window) as exact rows and n_q = 0.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_kivi_gather_dequant(const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_sc,
+                            const uint8_t* vc, const uint16_t* vmeta, int64_t cap_t, int64_t n_valid,
+                            int group_k, int group_v, int64_t BH, int64_t d, const int32_t* idx,
+                            int64_t count, int64_t idx_bh, void* k_out, void* v_out, int out_dtype,
+                            int64_t out_bh, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * A2  Fused quantise + pack append of one token per sequence (streaming KIVI window).

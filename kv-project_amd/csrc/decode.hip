@@ -87,6 +87,10 @@ struct DecodeParams {
   const int64_t* q_pos;
   float* ws_m;
   float* ws_l;
+  float* row_ml;                      // per (b, h, row): global max (log2 units) and sum of exp2
+  float* scores;                      // score pass: (BH, scores_bh) accumulated probabilities
+  int64_t scores_bh;
+  float score_weight;
   float* ws_o;
   int n_exact_wg, n_split, split_tokens, S1;
   int BH;
@@ -315,7 +319,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 __device__ __forceinline__ half2v h2(uint32_t w) { return __builtin_bit_cast(half2v, w); }
 __device__ __forceinline__ uint32_t w2(half2v h) { return __builtin_bit_cast(uint32_t, h); }
 
-template <int R, int GV, int DT>
+// SCORE = false: flash-decoding partials of this split.  SCORE = true: the score pass of the
+// eviction path -- the same logits, normalised by the row's global (max, sum) from the merge,
+// summed over the rows of the KV head and accumulated into the scores row (no value work).
+template <int R, int GV, int DT, bool SCORE>
 __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* smem) {
   constexpr int VPB = 16 / R;                       // PV columns per row: (group, hi/lo) variants
   constexpr int GPB = VPB / 2;                      // channel groups per PV B operand
@@ -340,7 +347,10 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   const int ci = (l >> 2) & 3, ck = l & 3;
   const int c0 = 32 * g + 8 * ci + kCos[2 * ck];
   const int c1 = 32 * g + 8 * ci + kCos[2 * ck + 1];
-  const float kinv = (ck & 1) ? 0.0625f : 1.0f;    // high-nibble slots carry 16*code
+  // key slots of high nibbles carry 16*code: their query operand is q*scale, the low-nibble
+  // slots' is 16*q*scale, so every product is 16 * code * q*scale * 2^-24 and the fp16 low part
+  // of the operand stays out of the subnormal range
+  const float kinv = (ck & 1) ? 1.0f : 16.0f;
   uint32_t* bq = bq_all + wave * 2 * R * 64;
   uint32_t* bv = bv_all + wave * R * 16;
 
@@ -377,8 +387,9 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   }
 
   // A nibble masked in place is an fp16 subnormal: c * 2^-24 (low nibble) or 16c * 2^-24 (high
-  // nibble), exact, so every code becomes a matrix-core operand with one and; all products carry
-  // the common factor 2^-24, removed once from the logits and once from the value sums.
+  // nibble), exact, so every code becomes a matrix-core operand with one and.  Key products carry
+  // the common factor 2^-20 (see kinv), removed once from the logits; value products carry 2^-24,
+  // removed once from the value sums.
   auto unpack = [&](uint32_t w) -> half8 {
     const uint32_t w8 = w >> 8;
     u32x4 r;
@@ -389,6 +400,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     return as_half8(r);
   };
   constexpr float kTwo24 = 16777216.0f;
+  constexpr float kTwo20 = 1048576.0f;              // logit = 2^20 * matrix-core sum
   constexpr float kLazy = 4.0f;
 
   // one 32-token chunk of this wavefront: key rows, value tile, value metadata, and the key
@@ -404,13 +416,15 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     const int so = __builtin_amdgcn_readfirstlane(cb * (kD / 2));   // key rows and value tiles alike
     c.kw[0] = __builtin_amdgcn_raw_buffer_load_b128(rk, vo_k, so, KVQ_LOAD_AUX);
     c.kw[1] = __builtin_amdgcn_raw_buffer_load_b128(rk, vo_k + 16 * (kD / 2), so, KVQ_LOAD_AUX);
-    c.vw[0] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo_v, so, KVQ_LOAD_AUX);
-    c.vw[1] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo_v + 1024, so, KVQ_LOAD_AUX);
-    const int som = __builtin_amdgcn_readfirstlane((cb / 32) * NGV * 128);
+    if constexpr (!SCORE) {
+      c.vw[0] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo_v, so, KVQ_LOAD_AUX);
+      c.vw[1] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo_v + 1024, so, KVQ_LOAD_AUX);
+      const int som = __builtin_amdgcn_readfirstlane((cb / 32) * NGV * 128);
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) {
-      c.mw[bb][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, vo_m[bb], som, KVQ_LOAD_AUX);
-      c.mw[bb][1] = __builtin_amdgcn_raw_buffer_load_b128(rm, vo_m[bb] + 16, som, KVQ_LOAD_AUX);
+      for (int bb = 0; bb < NB; ++bb) {
+        c.mw[bb][0] = __builtin_amdgcn_raw_buffer_load_b128(rm, vo_m[bb], som, KVQ_LOAD_AUX);
+        c.mw[bb][1] = __builtin_amdgcn_raw_buffer_load_b128(rm, vo_m[bb] + 16, som, KVQ_LOAD_AUX);
+      }
     }
     const int sok = __builtin_amdgcn_readfirstlane((cb / G) * kD * 2);
     c.ks0 = __builtin_amdgcn_raw_buffer_load_b16(rks, c0 * 2, sok, 0);
@@ -427,13 +441,22 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   float Za[NB], Zb[NB];
 #pragma unroll
   for (int k = 0; k < NB; ++k) Za[k] = Zb[k] = 0.0f;
-  const half8 tiny = as_half8(u32x4{0x00010001u, 0x00010001u, 0x00010001u, 0x00010001u});   // 2^-24
+  const half8 tiny = as_half8(u32x4{0x00100010u, 0x00100010u, 0x00100010u, 0x00100010u});   // 2^-20
   const half2v hl_neg = hl_pv ? half2v{static_cast<_Float16>(-1.0f), static_cast<_Float16>(-1.0f)}
                               : half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
   const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl_qk) * 64 + g * 16);
   const u32x4* bv_src = reinterpret_cast<const u32x4*>(bv + r_n * 16 + g * 4);
   half8 bqk[4];                                      // query operand of the current key group
   half8 bvirt;
+  // score pass: this lane's row statistics (padded rows contribute nothing)
+  float score_m = 0.0f, score_il = 0.0f;
+  float* score_row = nullptr;
+  if constexpr (SCORE) {
+    const int64_t ri = (static_cast<int64_t>(bh) * R + r_n) * 2;
+    score_m = r_n < p.R_real ? p.row_ml[ri] : 0.0f;
+    score_il = r_n < p.R_real ? 1.0f / p.row_ml[ri + 1] : 0.0f;
+    score_row = p.scores + static_cast<int64_t>(bh) * p.scores_bh;
+  }
 
   auto step = [&](int cb, const Chunk& c) {
     if (cb % G == 0 || cb == t0) {
@@ -479,20 +502,41 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
       for (int i = 0; i < 4; ++i) d = mfma(unpack(c.kw[tau][i]), bqk[i], d);
       d = mfma(tiny, bvirt, d);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[4 * tau + i] = d[i] + dpp<kRowRor + R>(d[i]);   // 2^-24 * logit
+      for (int i = 0; i < 4; ++i) s[4 * tau + i] = d[i] + dpp<kRowRor + R>(d[i]);   // 2^-20 * logit
     }
     if (cb + 32 > t1) {                              // last chunk of the range: mask past t1
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (cb + 16 * (j >> 2) + 4 * g + (j & 3) >= t1) s[j] = -INFINITY;
     }
+    if constexpr (SCORE) {
+      // probability of each (row, token) under the row's global softmax, summed over the rows
+      // of this KV head (lanes n = 0 .. R-1 hold rows 0 .. R-1 of one column variant)
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], kTwo20, -score_m)) * score_il;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if constexpr (R >= 2) x[j] += dpp<kQuadSwap1>(x[j]);
+        if constexpr (R >= 4) x[j] += dpp<kQuadSwap2>(x[j]);
+        if constexpr (R >= 8) x[j] += __shfl_xor(x[j], 4, 64);
+      }
+      if (n == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int tok = cb + 16 * (j >> 2) + 4 * g + (j & 3);
+          if (tok < t1) score_row[tok] = __builtin_fmaf(p.score_weight, x[j], score_row[tok]);
+        }
+      }
+      return;
+    }
     // ---- online softmax (base 2) with a lazy maximum: probabilities are taken against the running
     // maximum m_run as long as no logit exceeds it by more than kLazy (p <= 2^kLazy = 16, so
     // p * scale stays far inside fp16 range); only then is the exact chunk maximum reduced across
     // lanes and everything rescaled.  The first chunk always takes this path (m_run = -inf).
     float lm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-    if (__any(lm * kTwo24 > m_run + kLazy)) {
-      const float cm = xmax32(xmax16(lm)) * kTwo24;
+    if (__any(lm * kTwo20 > m_run + kLazy)) {
+      const float cm = xmax32(xmax16(lm)) * kTwo20;
       const float m_new = fmaxf(m_run, cm);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
@@ -510,7 +554,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     const float m4 = m_run + 4.0f;
     float pr[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) pr[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], kTwo24, -(((j & 3) >= 2) ? m4 : m_run)));
+    for (int j = 0; j < 8; ++j) pr[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], kTwo20, -(((j & 3) >= 2) ? m4 : m_run)));
     la += (pr[0] + pr[1]) + (pr[4] + pr[5]);
     lb += (pr[2] + pr[3]) + (pr[6] + pr[7]);
     // ---- PV operands p * sv (hi part, or lo part = p*sv - hi), zero-point sums ----
@@ -560,6 +604,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     }
   }
 
+  if constexpr (SCORE) return;
   // ---- wavefront epilogue: row sums over lane groups, hi+lo columns, offset and zero terms ----
   const float l_run = xsum32(xsum16(la + 16.0f * lb));
   float Z[NB];
@@ -625,6 +670,10 @@ __device__ void merge_bh(const DecodeParams& p, int bh, float* smem) {
       L += w * p.ws_l[(pb + s) * R + r];
     }
     tot[r] = L;
+    if (p.row_ml != nullptr && r < p.R_real) {
+      p.row_ml[(static_cast<int64_t>(bh) * R + r) * 2] = M;
+      p.row_ml[(static_cast<int64_t>(bh) * R + r) * 2 + 1] = L;
+    }
   }
   __syncthreads();
   for (int idx = threadIdx.x; idx < p.R_real * kD; idx += kThreads) {
@@ -658,7 +707,7 @@ void kivi_decode_split(DecodeParams p) {
   if (id < n_packed) {
     const int k = id / 8;
     const int bh = id % 8 + 8 * (k / p.n_split);
-    if (bh < p.BH) packed_block<R, GV, DT>(p, bh, k % p.n_split, smem);
+    if (bh < p.BH) packed_block<R, GV, DT, false>(p, bh, k % p.n_split, smem);
   } else {
     // exact-row blocks come last in dispatch order: they take the slots that packed blocks free
     // at the end of their round
@@ -667,6 +716,16 @@ void kivi_decode_split(DecodeParams p) {
     const int bh = e_id % 8 + 8 * (k / p.n_exact_wg);
     if (bh < p.BH) exact_block<R, DT>(p, bh, k % p.n_exact_wg, smem);
   }
+}
+
+// Score pass of the eviction path: packed blocks only, same split grid and mapping.
+template <int R, int GV, int DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(split_waves<R, GV>())))
+void kivi_score_split(DecodeParams p) {
+  extern __shared__ float smem[];
+  const int k = blockIdx.x / 8;
+  const int bh = blockIdx.x % 8 + 8 * (k / p.n_split);
+  if (bh < p.BH) packed_block<R, GV, DT, true>(p, bh, k % p.n_split, smem);
 }
 
 template <int R, int DT>
@@ -691,6 +750,11 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
   if (phases & 2) {
     hipLaunchKernelGGL((kivi_decode_merge<R, DT>), dim3(p.BH), dim3(kThreads), msmem, stream, p);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(merge)");
+  }
+  if ((phases & 4) && p.scores != nullptr && p.n_split > 0) {
+    hipLaunchKernelGGL((kivi_score_split<R, GV, DT>), dim3(static_cast<unsigned>(p.n_split) * bh_pad),
+                       dim3(kThreads), packed_smem, stream, p);
+    KVQ_LAUNCH_CHECK("kvq_kivi_decode(score)");
   }
   return KVQ_OK;
 }
@@ -761,7 +825,7 @@ extern "C" int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv,
   if (d != kD || B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Tq <= 0 || group_k <= 0) return -1;
   if (group_v != 32 && group_v != 64 && group_v != 128) return -1;
   const SplitPlan sp = plan_split(B, Hq, Hkv, Tq, n_q, n_exact, split_tokens, group_k, group_v);
-  return B * Hkv * static_cast<int64_t>(sp.S1) * sp.R * (kD + 2);
+  return B * Hkv * (static_cast<int64_t>(sp.S1) * sp.R * (kD + 2) + 2 * sp.R);
 }
 
 extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
@@ -772,9 +836,11 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
                                const void* k_exact, const void* v_exact, int exact_dtype,
                                int64_t cap_e, int64_t n_exact, const int64_t* exact_pos,
                                const int64_t* q_pos, void* out, int out_dtype, float* workspace,
-                               int64_t workspace_floats, int64_t split_tokens, int phases,
+                               int64_t workspace_floats, float* scores, int64_t scores_bh,
+                               float score_weight, int64_t split_tokens, int phases,
                                void* stream) {
-  KVQ_REQUIRE(phases >= 1 && phases <= 3, "kvq_kivi_decode: phases must be 1, 2 or 3");
+  KVQ_REQUIRE(phases >= 1 && phases <= 7, "kvq_kivi_decode: phases must be in 1..7");
+  KVQ_REQUIRE(scores == nullptr || scores_bh >= n_q, "kvq_kivi_decode: scores row stride < n_q");
   KVQ_REQUIRE(d == kD, "kvq_kivi_decode: head_dim must be 128 (got %lld)", (long long)d);
   KVQ_REQUIRE(valid_dtype(q_dtype) && q_dtype == exact_dtype && q_dtype == out_dtype,
               "kvq_kivi_decode: q, exact rows and output must share one dtype");
@@ -797,7 +863,7 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   KVQ_REQUIRE((exact_pos == nullptr) == (q_pos == nullptr), "kvq_kivi_decode: exact_pos and q_pos go together");
   KVQ_REQUIRE(n_q < (1LL << 31) && B * Hkv < 65536, "kvq_kivi_decode: sizes out of range");
   const SplitPlan sp = plan_split(B, Hq, Hkv, Tq, n_q, n_exact, split_tokens, group_k, group_v);
-  const int64_t need = B * Hkv * static_cast<int64_t>(sp.S1) * sp.R * (kD + 2);
+  const int64_t need = B * Hkv * (static_cast<int64_t>(sp.S1) * sp.R * (kD + 2) + 2 * sp.R);
   KVQ_REQUIRE(static_cast<int64_t>(sp.S1) * R_real <= 16384, "kvq_kivi_decode: too many splits");
   KVQ_REQUIRE(workspace_floats >= need, "kvq_kivi_decode: workspace too small (%lld < %lld floats)",
               (long long)workspace_floats, (long long)need);
@@ -814,6 +880,10 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   p.ws_o = workspace;
   p.ws_m = workspace + nrow * kD;
   p.ws_l = p.ws_m + nrow;
+  p.row_ml = p.ws_l + nrow;
+  p.scores = scores;
+  p.scores_bh = scores_bh;
+  p.score_weight = score_weight;
   p.BH = static_cast<int>(B * Hkv);
   p.n_exact_wg = sp.n_exact_wg; p.n_split = sp.n_split; p.split_tokens = sp.split_tokens; p.S1 = sp.S1;
   p.out = out;

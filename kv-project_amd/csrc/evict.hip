@@ -1,0 +1,192 @@
+// Eviction: top-k retention of accumulated scores, and the gather + dequantise of the retained
+// rows that the retained-set decode reads.
+//
+// Top-k (SnapKV-style retention, STRATA_KV.py:975 topk, 1022-1023 position order): one block of
+// 1024 threads per (b, h) row of scores.  A 4-pass radix select over order-preserving uint32 keys
+// of the fp32 scores (8 bits per pass, LDS histogram) finds the k-th largest key T and how many
+// keys equal to T are kept; a counting pass and a writing pass over contiguous per-thread ranges,
+// with block-wide prefix sums, emit the retained positions in increasing order.  Among keys equal
+// to T the lowest positions are kept (torch.topk leaves that order unspecified).  The scores row
+// is re-read every pass; after the first it is served from L2.
+#include "common.hpp"
+
+namespace kvq {
+namespace {
+
+constexpr int kTopkThreads = 1024;
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Exclusive prefix sum of v over the block (1024 threads); *total receives the sum.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_sums, uint32_t* total) {
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wave_sums[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    uint32_t w = lane < kTopkThreads / 64 ? wave_sums[lane] : 0u;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const uint32_t y = __shfl_up(w, o, 64);
+      if (lane >= o) w += y;
+    }
+    if (lane < kTopkThreads / 64) wave_sums[16 + lane] = w;       // inclusive wave prefix
+  }
+  __syncthreads();
+  const uint32_t before = (wave > 0 ? wave_sums[16 + wave - 1] : 0u) + x - v;
+  *total = wave_sums[16 + kTopkThreads / 64 - 1];
+  __syncthreads();                                                 // wave_sums reusable after return
+  return before;
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_retain_kernel(const float* __restrict__ scores,
+                                                                   int64_t n, int64_t scores_bh, int64_t k,
+                                                                   int32_t* __restrict__ idx, int64_t idx_bh) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wave_sums[32];
+  __shared__ uint32_t sh_prefix, sh_krem;
+  const int tid = threadIdx.x;
+  const float* s = scores + static_cast<int64_t>(blockIdx.x) * scores_bh;
+  int32_t* out = idx + static_cast<int64_t>(blockIdx.x) * idx_bh;
+  uint32_t prefix = 0, mask = 0, krem = static_cast<uint32_t>(k);
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    if (tid < 256) hist[tid] = 0;
+    __syncthreads();
+    for (int64_t i = tid; i < n; i += kTopkThreads) {
+      const uint32_t u = order_key(s[i]);
+      if ((u & mask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t acc = 0;
+      for (int b = 255; b >= 0; --b) {
+        if (acc + hist[b] >= krem) {
+          sh_prefix = prefix | (static_cast<uint32_t>(b) << shift);
+          sh_krem = krem - acc;
+          break;
+        }
+        acc += hist[b];
+      }
+    }
+    __syncthreads();
+    prefix = sh_prefix;
+    krem = sh_krem;
+    mask |= 0xFFu << shift;
+  }
+  // prefix = key of the k-th largest score; krem = how many keys equal to it are retained
+  const int64_t per = (n + kTopkThreads - 1) / kTopkThreads;
+  const int64_t lo = min<int64_t>(n, tid * per), hi = min<int64_t>(n, lo + per);
+  uint32_t c_gt = 0, c_eq = 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    const uint32_t u = order_key(s[i]);
+    c_gt += u > prefix;
+    c_eq += u == prefix;
+  }
+  uint32_t total;
+  const uint32_t eq_before = block_exclusive_scan(c_eq, wave_sums, &total);
+  const uint32_t take_eq = eq_before >= krem ? 0u : min(c_eq, krem - eq_before);
+  uint32_t off = block_exclusive_scan(c_gt + take_eq, wave_sums, &total);
+  uint32_t taken = 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    const uint32_t u = order_key(s[i]);
+    const bool eq = u == prefix;
+    if (u > prefix || (eq && taken < take_eq)) out[off++] = static_cast<int32_t>(i);
+    taken += eq;
+  }
+}
+
+// nibble (bit offset / 4) of the value-tile word that holds token slot j
+__device__ __constant__ int kNibbleOfSlotG[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+
+// Dequantised key and value rows of the retained positions: thread (row i, channel c) of
+// (b, h) reads position t = idx[i] from the packed cache (key codes in pack_codes rows, key
+// metadata of group t / group_k; value code from the 32-token tile, its (scale, lo) pair) and
+// writes code * scale + lo (fp32 multiply then add, as kivi_quant's xhat, STRATA_KV.py:855)
+// rounded to the output type.  An index outside [0, n_valid) writes NaN rows.
+template <int DT>
+__global__ __launch_bounds__(256) void gather_dequant_kernel(
+    const uint8_t* __restrict__ kc, const uint16_t* __restrict__ k_lo, const uint16_t* __restrict__ k_sc,
+    const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vmeta, int64_t cap_t, int64_t n_valid,
+    int group_k, int group_v, int d, const int32_t* __restrict__ idx, int64_t count, int64_t idx_bh,
+    void* __restrict__ k_out, void* __restrict__ v_out, int64_t out_bh, int64_t total) {
+  const int64_t flat = static_cast<int64_t>(blockIdx.x) * (256 / 128) + threadIdx.x / 128;
+  if (flat >= total) return;
+  const int c = threadIdx.x % 128;
+  const int64_t bh = flat / count, i = flat % count;
+  const int64_t t = idx[bh * idx_bh + i];
+  const int64_t o = bh * out_bh + i * d + c;
+  if (t < 0 || t >= n_valid) {
+    store_from_f32<DT>(k_out, o, __int_as_float(0x7fc00000));
+    store_from_f32<DT>(v_out, o, __int_as_float(0x7fc00000));
+    return;
+  }
+  const uint8_t kb = kc[(bh * cap_t + t) * (d / 2) + c / 2];
+  const int kcode = (c & 1) ? (kb & 15) : (kb >> 4);
+  const int64_t km = (bh * (cap_t / group_k) + t / group_k) * d + c;
+  const float kx = __fadd_rn(__fmul_rn(static_cast<float>(kcode), f16_to_f32(k_sc[km])), f16_to_f32(k_lo[km]));
+  const int64_t chunk = t / 32;
+  const int u = static_cast<int>(t % 32);
+  const int g = (u % 16) / 4, j = 4 * (u / 16) + (u % 4);
+  const int blk = c / 16;
+  const uint32_t* word = reinterpret_cast<const uint32_t*>(vc + bh * cap_t * (d / 2) + chunk * 16 * d) +
+                         (blk / 4) * 256 + (16 * g + c % 16) * 4 + (blk % 4);
+  const int vcode = static_cast<int>((*word >> (4 * kNibbleOfSlotG[j])) & 15u);
+  const int ngv = d / group_v;
+  const uint16_t* vm = vmeta + ((bh * (cap_t / 32) + chunk) * ngv + c / group_v) * 64 + (8 * g + j) * 2;
+  const float vx = __fadd_rn(__fmul_rn(static_cast<float>(vcode), f16_to_f32(vm[0])), f16_to_f32(vm[1]));
+  store_from_f32<DT>(k_out, o, kx);
+  store_from_f32<DT>(v_out, o, vx);
+}
+
+}  // namespace
+}  // namespace kvq
+
+using namespace kvq;
+
+extern "C" int kvq_kivi_gather_dequant(const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_sc,
+                                       const uint8_t* vc, const uint16_t* vmeta, int64_t cap_t, int64_t n_valid,
+                                       int group_k, int group_v, int64_t BH, int64_t d, const int32_t* idx,
+                                       int64_t count, int64_t idx_bh, void* k_out, void* v_out, int out_dtype,
+                                       int64_t out_bh, void* stream) {
+  KVQ_REQUIRE(valid_dtype(out_dtype), "kvq_kivi_gather_dequant: bad dtype");
+  KVQ_REQUIRE(d == 128, "kvq_kivi_gather_dequant: head_dim must be 128");
+  KVQ_REQUIRE(group_k > 0 && group_k % 32 == 0 && cap_t % group_k == 0 && cap_t % 32 == 0,
+              "kvq_kivi_gather_dequant: bad group_k / capacity");
+  KVQ_REQUIRE(group_v == 32 || group_v == 64 || group_v == 128, "kvq_kivi_gather_dequant: group_v in {32,64,128}");
+  KVQ_REQUIRE(0 <= n_valid && n_valid <= cap_t, "kvq_kivi_gather_dequant: bad n_valid");
+  KVQ_REQUIRE(BH >= 0 && count >= 0 && idx_bh >= count && out_bh >= count * d, "kvq_kivi_gather_dequant: bad sizes");
+  const int64_t total = BH * count;
+  if (total == 0) return KVQ_OK;
+  KVQ_REQUIRE(kc && k_lo && k_sc && vc && vmeta && idx && k_out && v_out, "kvq_kivi_gather_dequant: null pointer");
+  const int64_t blocks = (total + 1) / 2;
+  KVQ_REQUIRE(blocks < (1LL << 31), "kvq_kivi_gather_dequant: too many rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  KVQ_DISPATCH_DTYPE(out_dtype, hipLaunchKernelGGL((gather_dequant_kernel<DT_>), dim3(static_cast<unsigned>(blocks)),
+                                                  dim3(256), 0, s, kc, k_lo, k_sc, vc, vmeta, cap_t, n_valid,
+                                                  group_k, group_v, static_cast<int>(d), idx, count, idx_bh,
+                                                  k_out, v_out, out_bh, total));
+  KVQ_LAUNCH_CHECK("kvq_kivi_gather_dequant");
+  return KVQ_OK;
+}
+
+extern "C" int kvq_topk_retain(const float* scores, int64_t BH, int64_t n, int64_t scores_bh, int64_t k,
+                               int32_t* idx, int64_t idx_bh, void* stream) {
+  KVQ_REQUIRE(BH >= 0 && BH < (1LL << 31), "kvq_topk_retain: bad BH");
+  KVQ_REQUIRE(n >= 0 && n < (1LL << 31) && k >= 0 && k <= n, "kvq_topk_retain: need 0 <= k <= n < 2^31");
+  KVQ_REQUIRE(scores_bh >= n && idx_bh >= k, "kvq_topk_retain: row strides smaller than the rows");
+  if (BH == 0 || k == 0) return KVQ_OK;
+  KVQ_REQUIRE(scores && idx, "kvq_topk_retain: null pointer");
+  hipLaunchKernelGGL(topk_retain_kernel, dim3(static_cast<unsigned>(BH)), dim3(kTopkThreads), 0,
+                     static_cast<hipStream_t>(stream), scores, n, scores_bh, k, idx, idx_bh);
+  KVQ_LAUNCH_CHECK("kvq_topk_retain");
+  return KVQ_OK;
+}

@@ -8,9 +8,11 @@ from ._lib import KVQError, load as load_library
 from .kivi import kivi_quant, kivi_quant_stored, pack_codes, unpack_codes, v_tile, v_untile, vmeta_tile
 from .decode import PackedKIVICache, kivi_decode, workspace_floats
 from .state import DecodeCtl, KIVIState, Router, register, routed, router_attention
+from .evict import gather_dequant, retained_cache, topk_retain
 
 __all__ = [
     "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes",
     "v_tile", "v_untile", "vmeta_tile", "PackedKIVICache", "kivi_decode", "workspace_floats",
     "DecodeCtl", "KIVIState", "Router", "register", "routed", "router_attention",
+    "gather_dequant", "retained_cache", "topk_retain",
 ]

@@ -155,12 +155,17 @@ def workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_q: int, n_exa
 def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
                 q_pos: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                 workspace: Optional[torch.Tensor] = None, split_tokens: int = 0,
-                phases: int = 3) -> torch.Tensor:
+                phases: Optional[int] = None, scores: Optional[torch.Tensor] = None,
+                score_weight: float = 1.0) -> torch.Tensor:
     """Attention of q (B, Hq, Tq, d) over the packed cache; returns (B, Tq, Hq, d) in q's dtype.
 
     With ``q_pos`` (Tq,) int64 and ``cache.exact_pos`` set, exact row i is visible to query t iff
     exact_pos[i] <= q_pos[t] (the causal rule of chunked_attention among appended rows); every
-    packed row is visible.  ``phases`` 1/2 run only the split / merge kernel (timing)."""
+    packed row is visible.  ``phases`` 1/2 run only the split / merge kernel (timing).
+
+    ``scores`` (B, Hkv, >= n_q) float32 on the GPU: the step also adds ``score_weight`` times the
+    probability mass each packed token received from the query heads of its KV group (the
+    decode-time accumulation of the eviction path)."""
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.kc.shape[1]
@@ -174,6 +179,13 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
                             split_tokens)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty((need,), dtype=torch.float32, device=q.device)
+    if phases is None:
+        phases = 7 if scores is not None else 3
+    if scores is not None:
+        _lib.require_gpu(scores)
+        if scores.dtype != torch.float32 or scores.shape[:2] != (B, Hkv) or scores.stride(-1) != 1 \
+                or scores.stride(0) != Hkv * scores.stride(1) or scores.shape[2] < cache.n_q:
+            raise ValueError("scores must be float32 (B, Hkv, >= n_q) with contiguous rows")
     ep = cache.exact_pos if q_pos is not None else None
     qp = q_pos if ep is not None else None
     dt = _lib.DTYPE_CODE[q.dtype]
@@ -183,6 +195,7 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
               cache.vmeta.data_ptr(), cache.cap_t, cache.n_q, cache.group_k, cache.group_v,
               cache.k_exact.data_ptr(), cache.v_exact.data_ptr(), dt, cache.cap_e, cache.n_exact,
               _lib.ptr(ep), _lib.ptr(qp), out.data_ptr(), dt, workspace.data_ptr(), workspace.numel(),
+              _lib.ptr(scores), scores.stride(1) if scores is not None else 0, float(score_weight),
               split_tokens, phases, _lib.stream_of(q))
     return out
 

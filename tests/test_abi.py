@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/kvq.h but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert lib.kvq_abi_version() == 2
+    assert lib.kvq_abi_version() == 3
     assert lib.kvq_last_error() == b""
 
 
@@ -39,7 +39,7 @@ def test_argument_validation_without_gpu():
     rc = lib.kvq_pack_codes(None, 10, 3, None, None)
     assert rc == 1 and b"bits" in lib.kvq_last_error()
     rc = lib.kvq_kivi_decode(None, 0, 0, 0, 0, 1, 8, 8, 1, 64, 0.1, None, None, None, None, None, 64, 0, 32, 32,
-                             None, None, 0, 1, 1, None, None, None, 0, None, 0, 0, 3, None)
+                             None, None, 0, 1, 1, None, None, None, 0, None, 0, None, 0, 0.0, 0, 3, None)
     assert rc == 1 and b"head_dim" in lib.kvq_last_error()
     assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 0) > 0
 
@@ -47,15 +47,15 @@ def test_argument_validation_without_gpu():
 def test_split_plan_fills_one_round():
     """Automatic split (16x8 (b, h), 32640 packed + 128 exact tokens, 3 resident blocks per CU on
     256 CUs): 6 packed splits per (b, h) = 768 blocks, one round; the 128 exact rows are 4 blocks of
-    32 rows per (b, h), dispatched after the packed blocks.  The workspace holds S1 * rows * (d + 2) floats per
-    (b, h), S1 = exact partials + packed splits."""
+    32 rows per (b, h), dispatched after the packed blocks.  The workspace holds S1 * rows * (d + 2) + 2 * rows floats
+    per (b, h), S1 = exact partials + packed splits (partials, then each row's max and sum)."""
     from kvq import _lib
     lib = _lib.load()
     BH, R, d = 16 * 8, 4, 128
-    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 0) == BH * (4 + 6) * R * (d + 2)
+    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 0) == BH * ((4 + 6) * R * (d + 2) + 2 * R)
     # explicit split size: ceil(n_q / split_tokens) splits
-    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 3000) == BH * (4 + 11) * R * (d + 2)
+    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 3000) == BH * ((4 + 11) * R * (d + 2) + 2 * R)
     assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 48, 0) == -1
     # exact rows only / packed rows only
-    assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 0, 100, 32, 32, 0) == 8 * 4 * 1 * (d + 2)
-    assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 64, 0, 32, 32, 0) == 8 * 1 * 1 * (d + 2)
+    assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 0, 100, 32, 32, 0) == 8 * (4 * 1 * (d + 2) + 2)
+    assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 64, 0, 32, 32, 0) == 8 * (1 * 1 * (d + 2) + 2)

@@ -1,0 +1,126 @@
+"""Eviction path on the GPU against the CPU oracle (oracle/evict.py).
+
+* top-k retention: bit-exact retained positions (position order, lowest positions among ties at
+  the k-th score) on random, tied, constant and signed rows of ragged lengths;
+* decode-time score accumulation: probabilities of the packed tokens summed over the query
+  heads of each KV group, over several steps, for 1, 4 and 8 rows per KV head (rtol 2e-4);
+* gather + dequantise of retained rows: bit-exact against kivi_quant's xhat (fp32);
+* a reduced C4: keys with a 1% +3 shift, scores over 4 decode steps, top-k, decode over the
+  retained set plus the recent window.  Retained sets equal the oracle's except for positions
+  whose oracle score lies within 1e-4 (relative) of the k-th score; outputs within 2e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.kivi as ok
+from oracle.attention import chunked_attention
+from oracle.evict import accumulate_decode_scores, decode_step_probs, topk_retain
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (100, 7), (1023, 1023), (1024, 300), (5000, 2048), (65280, 2048)])
+def test_topk_retain_bit_exact(n, k):
+    import kvq
+    rng = np.random.default_rng(n + k)
+    rows = np.stack([
+        rng.random(n, dtype=np.float32) * 1e-3,                             # distinct
+        rng.integers(0, 5, n).astype(np.float32) * 0.25,                    # heavy ties
+        np.full(n, 3.0, np.float32),                                        # all equal
+        (rng.standard_normal(n) * 10).astype(np.float32),                   # signed
+    ])
+    got = kvq.topk_retain(torch.from_numpy(rows).cuda(), k).cpu().numpy()
+    want = topk_retain(rows, k)
+    np.testing.assert_array_equal(got, want)
+
+
+def _packed(B, Hkv, T, W, gk, gv, seed, dtype=torch.float32, shift_frac=0.0):
+    import kvq
+    g = torch.Generator().manual_seed(seed)
+    d = 128
+    K = torch.randn((B, Hkv, T, d), generator=g)
+    V = torch.randn((B, Hkv, T, d), generator=g)
+    if shift_frac:
+        n_shift = max(1, int(shift_frac * T))
+        for b in range(B):
+            for h in range(Hkv):
+                K[b, h, torch.randperm(T - W, generator=g)[:n_shift]] += 3.0
+    K, V = K.to(dtype), V.to(dtype)
+    cache = kvq.PackedKIVICache.from_context(K.cuda(), V.cuda(), window=W, group_k=gk, group_v=gv)
+    Kf, Vf = K.float().numpy(), V.float().numpy()
+    kq, vq = ok.kivi_quant(Kf, 4, gk, True, 0), ok.kivi_quant(Vf, 4, gv, False, 0)
+    n_q = T - W
+    kh = ok.kivi_dequant(kq["codes"], kq["lo"], kq["scale"], gk, True)[:, :, :n_q]
+    vh = ok.kivi_dequant(vq["codes"][:, :, :n_q], vq["lo"][:, :, :n_q], vq["scale"][:, :, :n_q], gv, False)
+    return cache, K, V, kh, vh, g
+
+
+@pytest.mark.parametrize("Hq,Hkv,Tq", [(8, 8, 1), (8, 2, 1), (8, 2, 2)])
+def test_decode_score_accumulation(Hq, Hkv, Tq):
+    import kvq
+    B, T, W, gk, gv, d, steps = 2, 1200, 64, 64, 64, 128, 3
+    cache, K, V, kh, vh, g = _packed(B, Hkv, T, W, gk, gv, seed=Hq + Hkv + Tq)
+    rep = Hq // Hkv
+    n_q = T - W
+    scores = torch.zeros((B, Hkv, n_q + 5), dtype=torch.float32, device="cuda")   # row stride > n_q
+    want = np.zeros((B, Hkv, n_q))
+    w = 1.0 / (rep * Tq * steps)
+    for _ in range(steps):
+        q = torch.randn((B, Hq, Tq, d), generator=g)
+        kvq.kivi_decode(q.cuda(), d ** -0.5, cache, scores=scores, score_weight=w)
+        p = decode_step_probs(q.numpy(), d ** -0.5, kh, K[:, :, n_q:].numpy())
+        want = accumulate_decode_scores(want, p, w)
+    got = scores[..., :n_q].cpu().numpy()
+    assert np.all(scores[..., n_q:].cpu().numpy() == 0.0)
+    np.testing.assert_allclose(got, want, rtol=2e-4, atol=1e-9)
+
+
+def test_gather_dequant_bit_exact():
+    import kvq
+    B, Hkv, T, W, gk, gv = 2, 2, 1000, 40, 64, 32
+    cache, K, V, kh, vh, g = _packed(B, Hkv, T, W, gk, gv, seed=7)
+    n_q = T - W
+    idx = torch.stack([torch.sort(torch.randperm(n_q, generator=g)[:77]).values for _ in range(B * Hkv)])
+    idx[0, -1] = n_q - 1                                                   # last row of the last tile
+    idx = idx.reshape(B, Hkv, 77).to(torch.int32)
+    ko, vo = kvq.gather_dequant(cache, idx.cuda(), torch.float32)
+    ii = idx.long().numpy()
+    want_k = np.take_along_axis(kh.astype(np.float32), ii[..., None], 2)
+    want_v = np.take_along_axis(vh.astype(np.float32), ii[..., None], 2)
+    np.testing.assert_array_equal(ko.cpu().numpy(), want_k)
+    np.testing.assert_array_equal(vo.cpu().numpy(), want_v)
+
+
+def test_c4_reduced_eviction_end_to_end():
+    import kvq
+    B, Hq, Hkv, T, W, gk, gv, d, steps, keep = 2, 16, 4, 8448, 256, 64, 64, 128, 4, 512
+    cache, K, V, kh, vh, g = _packed(B, Hkv, T, W, gk, gv, seed=21, shift_frac=0.01)
+    n_q = T - W
+    rep = Hq // Hkv
+    scores = torch.zeros((B, Hkv, n_q), dtype=torch.float32, device="cuda")
+    want = np.zeros((B, Hkv, n_q))
+    for _ in range(steps):
+        q = torch.randn((B, Hq, 1, d), generator=g)
+        kvq.kivi_decode(q.cuda(), d ** -0.5, cache, scores=scores, score_weight=1.0 / (rep * steps))
+        want = accumulate_decode_scores(want, decode_step_probs(q.numpy(), d ** -0.5, kh, K[:, :, n_q:].numpy()),
+                                        1.0 / (rep * steps))
+    idx = kvq.topk_retain(scores, keep)
+    got = idx.cpu().numpy()
+    ref = topk_retain(want, keep)
+    for b in range(B):
+        for h in range(Hkv):
+            kth = np.sort(want[b, h])[-keep]
+            near = set(np.nonzero(np.abs(want[b, h] - kth) <= 1e-4 * kth)[0].tolist())
+            diff = set(got[b, h].tolist()) ^ set(ref[b, h].tolist())
+            assert diff <= near, (b, h, sorted(diff - near)[:10])
+    # decode over the retained set + the recent window
+    rc = kvq.retained_cache(cache, idx)
+    q = torch.randn((B, Hq, 1, d), generator=g)
+    out = kvq.kivi_decode(q.cuda(), d ** -0.5, rc).cpu().numpy()
+    ii = got.astype(np.int64)
+    kk = np.concatenate([np.take_along_axis(kh, ii[..., None], 2), K[:, :, n_q:].numpy()], 2)
+    vv = np.concatenate([np.take_along_axis(vh, ii[..., None], 2), V[:, :, n_q:].numpy()], 2)
+    ref_out = chunked_attention(q.numpy(), d ** -0.5, np.array([T]), kk, vv, np.zeros(kk.shape[2], int),
+                                np.full(kk.shape[2], 1 << 40), None)
+    assert float(np.abs(out - ref_out).max()) <= 2e-3
