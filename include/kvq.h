@@ -165,6 +165,43 @@ int kvq_kivi_gather_dequant(const uint8_t* kc, const uint16_t* k_lo, const uint1
                             int64_t out_bh, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * A3  Planar packing.  kvq_pack_planar replaces pack_planar (STRATA_KV.py:1171-1182): `rows`
+ * rows of d uint8 codes (< 2^bits) -> rows of d*bits/8 bytes, byte i holding coordinate
+ * p*d/P + i in bits [p*bits, (p+1)*bits), P = 8/bits.  kvq_unpack_planar is unpack_planar
+ * (1185-1189).  bits in {2, 4, 8}.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_pack_planar(const uint8_t* codes, int64_t rows, int64_t d, int bits, uint8_t* out, void* stream);
+int kvq_unpack_planar(const uint8_t* packed, int64_t rows, int64_t d, int bits, uint8_t* codes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * A5  STRATA codec.  One side (keys or values) of a layer's coded tokens, as compress_layer does
+ * it (STRATA_KV.py:1546-1548) with rotation_matrix (1110-1128) and strata_quantize (1158-1168):
+ *   kvq_strata_center_rotate: x (BH, n, d) of x_dtype, (b,h) stride x_bh elements ->
+ *     mu (BH, d) fp16 = fp16(mean over the n tokens), y (BH, n, d) float32 = (x - mu) R^T with
+ *     R = H_d diag(signs) / sqrt(d) (signs: d float32 +-1 on the device).
+ *   kvq_strata_quantize: rows idx[bh][0..m) of y (all n rows in order when idx is NULL) ->
+ *     planar codes (BH, m, d*bits/8) and fp16 scales (BH, m): s = max(fp16(step * rms(y)), 2^-24),
+ *     code = clamp(round(y / s + (2^bits - 1) / 2)); step = uniform_step(bits) (1132-1155).
+ * The arithmetic order is fixed (float64 sums, fast Walsh-Hadamard transform with stages
+ * h = 1 .. d/2 then * float32(1/sqrt(d))), so results are reproducible bit for bit; they equal the
+ * reference's torch float32 results up to float32 rounding of mu, y and rms.  d == 128.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_strata_center_rotate(const void* x, int x_dtype, int64_t BH, int64_t n, int64_t d, int64_t x_bh,
+                             const float* signs, uint16_t* mu, float* y, void* stream);
+int kvq_strata_quantize(const float* y, int64_t BH, int64_t n, int64_t d, const int32_t* idx, int64_t m,
+                        int bits, float step, uint8_t* codes, uint16_t* scales, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * A6 layout (no reference counterpart: the reference's Triton kernel reads planar rows).  Value
+ * codes of a stratum in the STRATA decode kernel's tile layout: planar rows (BH, n, d*bits/8),
+ * (b,h) stride rows_bh bytes -> tiles (BH, cap_t/32, 512*bits bytes), and fp16 value scales vs
+ * (BH, n), stride vs_bh -> vsl (BH, cap_t/32, 32) in the kernel's token-slot order.  Positions
+ * >= n hold code 0 / scale 0.  cap_t % 32 == 0, d == 128.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_strata_v_tile(const uint8_t* rows, int64_t BH, int64_t n, int64_t rows_bh, int bits, int64_t cap_t,
+                      uint8_t* tiles, const uint16_t* vs, int64_t vs_bh, uint16_t* vsl, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * A2  Fused quantise + pack append of one token per sequence (streaming KIVI window).
  * No per-step quantiser exists in the reference (its decode-time appends stay exact,
  * STRATA_KV.py:707-714); this restates KIVIMethod's window rule (806-822) for a streaming cache:

@@ -37,13 +37,11 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "mfma_common.hpp"
 
 namespace kvq {
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Build-time switches of the split kernel (defaults are the tuned values):
 //   KVQ_WAVES       waves per SIMD the register allocation targets (0: per-variant default)
@@ -96,54 +94,6 @@ struct DecodeParams {
   int BH;
   void* out;
 };
-
-__device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
-
-__device__ __forceinline__ f32x4 mfma(half8 a, half8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
-}
-constexpr int kRowShr = 0x110;     // row_shr:k  (lane i reads lane i-k of its row of 16)
-constexpr int kRowRor = 0x120;     // row_ror:k
-constexpr int kQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
-constexpr int kQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
-
-// max / sum with the xor-16 and xor-32 lane partners (gfx950 permlane swaps: VALU, no LDS trip)
-__device__ __forceinline__ float xmax16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xmax32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xsum16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float xsum32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
-}
-
-__device__ __forceinline__ float h2f(uint32_t w, int hi) {
-  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hi ? (w >> 16) : (w & 0xffffu))));
-}
-
-__device__ __forceinline__ void wave_lds_fence() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Row r of KV head h is (query head h*rep + r/Tq, position t = r%Tq).
 __device__ __forceinline__ int64_t q_offset(const DecodeParams& p, int b, int h, int r) {
@@ -308,17 +258,6 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
 
 // ---------------------------------------------------------------------------------------------
 // packed split: 4 wavefronts, each streaming its quarter of the split in 32-token chunks
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  // raw buffer: loads past `bytes` return zero instead of touching memory
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                           static_cast<int>(bytes), 0x00020000);
-}
-
-__device__ __forceinline__ half2v h2(uint32_t w) { return __builtin_bit_cast(half2v, w); }
-__device__ __forceinline__ uint32_t w2(half2v h) { return __builtin_bit_cast(uint32_t, h); }
-
 // SCORE = false: flash-decoding partials of this split.  SCORE = true: the score pass of the
 // eviction path -- the same logits, normalised by the row's global (max, sum) from the merge,
 // summed over the rows of the KV head and accumulated into the scores row (no value work).

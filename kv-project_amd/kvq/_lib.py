@@ -40,6 +40,11 @@ SIGNATURES = {
     "kvq_topk_retain": (i32, [vp, i64, i64, i64, i64, vp, i64, vp]),
     "kvq_kivi_gather_dequant": (i32, [vp, vp, vp, vp, vp, i64, i64, i32, i32, i64, i64, vp, i64, i64, vp,
                                       vp, i32, i64, vp]),
+    "kvq_pack_planar": (i32, [vp, i64, i64, i32, vp, vp]),
+    "kvq_unpack_planar": (i32, [vp, i64, i64, i32, vp, vp]),
+    "kvq_strata_center_rotate": (i32, [vp, i32, i64, i64, i64, i64, vp, vp, vp, vp]),
+    "kvq_strata_quantize": (i32, [vp, i64, i64, i64, vp, i64, i32, f32, vp, vp, vp]),
+    "kvq_strata_v_tile": (i32, [vp, i64, i64, i64, i32, i64, vp, vp, i64, vp, vp]),
     "kvq_kivi_append": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp, vp, i64,
                               vp, vp, vp, vp, vp, i64, i32, i32, vp]),
     "kvq_selftest_mfma_layout": (i32, [vp, vp, vp, vp]),

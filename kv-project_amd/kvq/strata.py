@@ -1,0 +1,119 @@
+"""STRATA codec and planar packing on the GPU (STRATA_KV.py:1110-1189, 1546-1548).
+
+``rotation_signs`` and ``uniform_step`` restate the reference's host-side constants
+(rotation_matrix's seeded sign draw, 1119-1124 with _rng 306-307; the golden-section quantiser
+step, 1132-1155); everything per token runs in libkvq.
+"""
+from __future__ import annotations
+
+import math
+import zlib
+from functools import lru_cache
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+
+
+@lru_cache(maxsize=None)
+def _signs_np(d: int, key: str) -> np.ndarray:
+    g = np.random.default_rng([42, zlib.crc32(b"rotation"), zlib.crc32(key.encode())])
+    return g.choice([-1.0, 1.0], d)
+
+
+def rotation_signs(d: int, key: str = "strata", device="cuda") -> torch.Tensor:
+    """The +-1 vector s of rotation_matrix(d, key) = H_d diag(s) / sqrt(d) (float32 on the device)."""
+    if d & (d - 1):
+        raise ValueError("the Hadamard rotation needs a power-of-two head_dim")
+    return torch.tensor(_signs_np(d, key), dtype=torch.float32, device=device)
+
+
+@lru_cache(maxsize=None)
+def uniform_step(bits: int) -> float:
+    """Step (in RMS units) of the MSE-optimal mid-rise uniform quantiser of N(0, 1) with 2^bits
+    levels: the reference's golden-section search on a 360001-point grid (STRATA_KV.py:1132-1155)."""
+    x = np.linspace(-9.0, 9.0, 360001)
+    w = np.exp(-0.5 * x * x)
+    w /= w.sum()
+    half = (2 ** bits - 1) / 2.0
+
+    def mse(step):
+        c = np.clip(np.round(x / step + half), 0, 2 ** bits - 1)
+        return float((w * (x - (c - half) * step) ** 2).sum())
+    lo, hi = 1e-4, 4.0
+    g = (math.sqrt(5) - 1) / 2
+    for _ in range(200):
+        a, b = hi - g * (hi - lo), lo + g * (hi - lo)
+        lo, hi = (lo, b) if mse(a) < mse(b) else (a, hi)
+    return 0.5 * (lo + hi)
+
+
+@torch.no_grad()
+def pack_planar(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """(..., d) uint8 codes -> (..., d*bits/8) planar bytes (STRATA_KV.py:1171-1182)."""
+    _lib.require_gpu(codes)
+    d = codes.shape[-1]
+    c = codes.reshape(-1, d).contiguous()
+    out = torch.empty((c.shape[0], d * bits // 8), dtype=torch.uint8, device=codes.device)
+    _lib.call("kvq_pack_planar", c.data_ptr(), c.shape[0], d, bits, out.data_ptr(), _lib.stream_of(codes))
+    return out.reshape(*codes.shape[:-1], d * bits // 8)
+
+
+@torch.no_grad()
+def unpack_planar(packed: torch.Tensor, bits: int) -> torch.Tensor:
+    """Inverse of pack_planar (STRATA_KV.py:1185-1189), uint8 codes."""
+    _lib.require_gpu(packed)
+    d = packed.shape[-1] * 8 // bits
+    p = packed.reshape(-1, packed.shape[-1]).contiguous()
+    out = torch.empty((p.shape[0], d), dtype=torch.uint8, device=packed.device)
+    _lib.call("kvq_unpack_planar", p.data_ptr(), p.shape[0], d, bits, out.data_ptr(), _lib.stream_of(packed))
+    return out.reshape(*packed.shape[:-1], d)
+
+
+@torch.no_grad()
+def strata_center_rotate(x: torch.Tensor, signs: Optional[torch.Tensor] = None):
+    """x (B, Hkv, n, d) -> (mu (B, Hkv, d) fp16, y (B, Hkv, n, d) float32 = (x - mu) R^T)."""
+    _lib.require_gpu(x)
+    B, H, n, d = x.shape
+    signs = rotation_signs(d, device=x.device) if signs is None else signs
+    x = x.contiguous()
+    mu = torch.empty((B, H, d), dtype=torch.float16, device=x.device)
+    y = torch.empty((B, H, n, d), dtype=torch.float32, device=x.device)
+    _lib.call("kvq_strata_center_rotate", x.data_ptr(), _lib.DTYPE_CODE[x.dtype], B * H, n, d, n * d,
+              signs.data_ptr(), mu.data_ptr(), y.data_ptr(), _lib.stream_of(x))
+    return mu, y
+
+
+@torch.no_grad()
+def strata_quantize(y: torch.Tensor, bits: int, idx: Optional[torch.Tensor] = None):
+    """Rotated rows y (B, Hkv, n, d) float32 (rows idx (B, Hkv, m) int32 if given) -> (planar codes
+    (B, Hkv, m, d*bits/8) uint8, scales (B, Hkv, m) fp16), STRATA_KV.py:1158-1168."""
+    _lib.require_gpu(y)
+    B, H, n, d = y.shape
+    y = y.contiguous()
+    if idx is not None:
+        idx = idx.to(torch.int32).contiguous()
+        if idx.shape[:2] != (B, H) or bool(((idx < 0) | (idx >= n)).any()):
+            raise ValueError("idx must be (B, Hkv, m) positions in [0, n)")
+    m = n if idx is None else idx.shape[2]
+    codes = torch.empty((B, H, m, d * bits // 8), dtype=torch.uint8, device=y.device)
+    scales = torch.empty((B, H, m), dtype=torch.float16, device=y.device)
+    _lib.call("kvq_strata_quantize", y.data_ptr(), B * H, n, d, _lib.ptr(idx), m, bits, uniform_step(bits),
+              codes.data_ptr(), scales.data_ptr(), _lib.stream_of(y))
+    return codes, scales
+
+
+@torch.no_grad()
+def strata_v_tile(rows: torch.Tensor, vs: torch.Tensor, bits: int, cap_t: int):
+    """Planar value rows (B, Hkv, n, d*bits/8) and fp16 scales (B, Hkv, n) -> (tiles
+    (B, Hkv, cap_t/32, 512*bits) uint8, slot-ordered scales (B, Hkv, cap_t/32, 32) fp16)."""
+    _lib.require_gpu(rows, vs)
+    B, H, n, rb = rows.shape
+    rows, vs = rows.contiguous(), vs.contiguous()
+    tiles = torch.empty((B, H, cap_t // 32, 512 * bits), dtype=torch.uint8, device=rows.device)
+    vsl = torch.empty((B, H, cap_t // 32, 32), dtype=torch.float16, device=rows.device)
+    _lib.call("kvq_strata_v_tile", rows.data_ptr(), B * H, n, n * rb, bits, cap_t, tiles.data_ptr(), vs.data_ptr(),
+              n, vsl.data_ptr(), _lib.stream_of(rows))
+    return tiles, vsl

@@ -1,0 +1,100 @@
+"""STRATA codec, planar packing and value tiles on the GPU against the CPU oracle (bit-exact).
+
+* pack_planar / unpack_planar (STRATA_KV.py:1171-1189) for 2/4/8 bits;
+* centring + rotation (1546-1547): fp16 means and float32 rotated rows equal the oracle's bit for
+  bit (same fixed arithmetic order), for fp32 and bf16 inputs;
+* strata_quantize (1158-1168): planar codes and fp16 scales, all rows and a gathered subset;
+* the decode kernel's value tiles: every (token, channel) code read back through the documented
+  word layout equals the planar code; slot-ordered scales.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.strata as os_
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_planar_pack_unpack(bits):
+    import kvq
+    rng = np.random.default_rng(bits)
+    codes = rng.integers(0, 2 ** bits, (3, 37, 128)).astype(np.uint8)
+    packed = kvq.pack_planar(torch.from_numpy(codes).cuda(), bits).cpu().numpy()
+    np.testing.assert_array_equal(packed, os_.pack_planar(codes, bits))
+    back = kvq.unpack_planar(torch.from_numpy(packed).cuda(), bits).cpu().numpy()
+    np.testing.assert_array_equal(back, codes)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_center_rotate_and_quantize_bit_exact(dtype):
+    import kvq
+    g = torch.Generator().manual_seed(3)
+    B, H, n, d = 2, 3, 301, 128
+    x = (torch.randn((B, H, n, d), generator=g) * 3 + 0.7).to(dtype)
+    mu, y = kvq.strata_center_rotate(x.cuda())
+    s = os_.rotation_signs(d)
+    mu_o, y_o = os_.strata_center_rotate(x.float().numpy().reshape(B * H, n, d), s)
+    np.testing.assert_array_equal(mu.float().cpu().numpy().reshape(B * H, d), mu_o)
+    np.testing.assert_array_equal(y.cpu().numpy().reshape(B * H, n, d), y_o)
+    for bits in (2, 4, 8):
+        assert kvq.uniform_step(bits) == os_.uniform_step(bits)[0]
+        codes, sc = kvq.strata_quantize(y, bits)
+        c_o, s_o, _ = os_.strata_quantize(y_o, bits, os_.uniform_step(bits)[0])
+        np.testing.assert_array_equal(codes.cpu().numpy().reshape(B * H, n, -1), os_.pack_planar(c_o, bits))
+        np.testing.assert_array_equal(sc.float().cpu().numpy().reshape(B * H, n), s_o)
+        idx = torch.stack([torch.randperm(n, generator=g)[:50] for _ in range(B * H)]).reshape(B, H, 50)
+        cg, sg = kvq.strata_quantize(y, bits, idx.cuda())
+        ii = idx.numpy().reshape(B * H, 50)
+        want = os_.pack_planar(np.take_along_axis(c_o, ii[..., None], 1), bits)
+        np.testing.assert_array_equal(cg.cpu().numpy().reshape(B * H, 50, -1), want)
+        np.testing.assert_array_equal(sg.float().cpu().numpy().reshape(B * H, 50), np.take_along_axis(s_o, ii, 1))
+
+
+def _slot_token(g, j):
+    return 16 * (j >> 2) + 4 * g + (j & 3)
+
+
+def _tile_codes(tiles: np.ndarray, bits: int) -> np.ndarray:
+    """Read a chunk's tile words back to codes[token 0..31][channel 0..127] by the documented layout."""
+    words = tiles.view(np.uint32)
+    out = np.full((32, 128), -1, np.int64)
+    slot4, slot8 = [0, 2, 4, 6, 1, 3, 5, 7], [0, 2, 1, 3, 4, 6, 5, 7]
+    for w, word in enumerate(words.tolist()):
+        if bits == 4:
+            blk, l = (w // 256) * 4 + w % 4, (w % 256) // 4
+            for k in range(8):
+                out[_slot_token(l // 16, slot4[k]), 16 * blk + l % 16] = (word >> (4 * k)) & 15
+        elif bits == 8:
+            blk, l, half = (w // 256) * 2 + (w % 4) // 2, (w % 256) // 4, w % 2
+            for k in range(4):
+                out[_slot_token(l // 16, slot8[4 * half + k]), 16 * blk + l % 16] = (word >> (8 * k)) & 255
+        else:
+            l, bp = w // 4, w % 4
+            for k in range(16):
+                blk, slot = 2 * bp + ((k >> 2) & 1), 2 * (k & 3) + (k >> 3)
+                out[_slot_token(l // 16, slot), 16 * blk + l % 16] = (word >> (2 * k)) & 3
+    return out
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_value_tiles_layout(bits):
+    import kvq
+    rng = np.random.default_rng(10 + bits)
+    B, H, n, cap = 1, 2, 70, 96
+    codes = rng.integers(0, 2 ** bits, (B, H, n, 128)).astype(np.uint8)
+    vs = rng.random((B, H, n)).astype(np.float16)
+    rows = torch.from_numpy(os_.pack_planar(codes, bits)).cuda()
+    tiles, vsl = kvq.strata_v_tile(rows, torch.from_numpy(vs).cuda(), bits, cap)
+    tiles, vsl = tiles.cpu().numpy(), vsl.cpu().numpy()
+    full = np.zeros((B, H, cap, 128), np.int64)
+    full[:, :, :n] = codes
+    vfull = np.zeros((B, H, cap), np.float16)
+    vfull[:, :, :n] = vs
+    for h in range(H):
+        for c in range(cap // 32):
+            got = _tile_codes(tiles[0, h, c], bits)
+            np.testing.assert_array_equal(got, full[0, h, 32 * c:32 * c + 32])
+            want_s = [vfull[0, h, 32 * c + _slot_token(s // 8, s % 8)] for s in range(32)]
+            np.testing.assert_array_equal(vsl[0, h, c], np.array(want_s, np.float16))
