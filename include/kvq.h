@@ -202,6 +202,31 @@ int kvq_strata_v_tile(const uint8_t* rows, int64_t BH, int64_t n, int64_t rows_b
                       uint8_t* tiles, const uint16_t* vs, int64_t vs_bh, uint16_t* vsl, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * A6  STRATA decode.  Replaces StrataState.attend (STRATA_KV.py:1762-1795) with its strata read
+ * by strata_tier_kernel (1450-1469; tier_reference 1751-1760) for a decode step, batch B >= 1.
+ * q: (B, Hq, Tq, d) of q_dtype, strides as kvq_kivi_decode; R = rep*Tq <= 8; d == 128.
+ * signs (d) float32 +-1 and mu_k, mu_v (B*Hkv, d) fp16: the rotation and means of the coded tokens.
+ * Tier t (host arrays of n_tiers <= 16 entries): tier_bits[t] in {2,4,8}, tier_n[t] tokens, key
+ *   planar rows tier_kc[t] (B*Hkv, n, d*bits/8), key scales tier_ks[t] (B*Hkv, cap) fp16 (zero
+ *   past n), value tiles
+ *   tier_vt[t] and slot-ordered value scales tier_vsl[t] of capacity tier_cap[t] (kvq_strata_v_tile).
+ * Exact rows as kvq_kivi_decode (k_exact, v_exact (B*Hkv, cap_e, d) of q_dtype, exact_pos / q_pos).
+ * out: (B, Tq, Hq, d) of q_dtype.  workspace: kvq_strata_decode_workspace(...) floats.
+ * Logit of a coded token (base e in the reference, base 2 here with log2(e) folded in):
+ *   s_j = ks_j (q^ . c_j) - ks_j (2^b - 1)/2 sum(q^) + scaling q . mu_K,   q^ = scaling q R^T;
+ * output = [w_e o_exact + (sum_t w_t acc_t) R + (sum_t w_t l_t) mu_V] / (sum of all w l).
+ * ---------------------------------------------------------------------------------------- */
+int64_t kvq_strata_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t n_exact,
+                                    int n_tiers, const int64_t* tier_n);
+int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B, int64_t Hq,
+                      int64_t Hkv, int64_t Tq, int64_t d, float scaling, const float* signs, const uint16_t* mu_k,
+                      const uint16_t* mu_v, int n_tiers, const int* tier_bits, const int64_t* tier_n,
+                      const int64_t* tier_cap, const uint8_t* const* tier_kc, const uint16_t* const* tier_ks,
+                      const uint8_t* const* tier_vt, const uint16_t* const* tier_vsl, const void* k_exact,
+                      const void* v_exact, int64_t cap_e, int64_t n_exact, const int64_t* exact_pos,
+                      const int64_t* q_pos, void* out, float* workspace, int64_t workspace_floats, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * A2  Fused quantise + pack append of one token per sequence (streaming KIVI window).
  * No per-step quantiser exists in the reference (its decode-time appends stay exact,
  * STRATA_KV.py:707-714); this restates KIVIMethod's window rule (806-822) for a streaming cache:

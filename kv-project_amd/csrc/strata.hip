@@ -285,3 +285,601 @@ extern "C" int kvq_strata_v_tile(const uint8_t* rows, int64_t BH, int64_t n, int
   KVQ_LAUNCH_CHECK("kvq_strata_v_tile(scales)");
   return KVQ_OK;
 }
+
+// =============================================================================================
+// A6  STRATA tier decode: split-K flash-decoding partials of one stratum (STRATA_KV.py:1374-1469
+// computes the same with a Triton kernel over planar rows; tier_reference 1751-1760), merged with
+// the exact rows' partials and rotated back (StrataState.attend 1762-1795).
+//
+// Per (b, h, split): 4 wavefronts each stream an equal share of 32-token chunks.  Logit of token j
+// for row r (base 2): s = ks_j * (q^ . c_j - half * sum(q^)) + qb, q^ = scaling*log2(e) * q R^T.
+// The dot q^ . c_j runs on v_mfma_f32_16x16x32_f16 with the codes masked in place as fp16
+// subnormals (a code at bit offset o within a 16-bit half is c * 2^o * 2^-24, exact) against the
+// query operand q^ * Smax / 2^o split into fp16 hi / lo columns.  Values: p * vs as the B operand
+// of the same product over value tiles; the offset -half * sum(p * vs) is added to every channel.
+namespace kvq {
+namespace {
+
+constexpr int kSThreads = 256;
+constexpr int kSWaves = 4;
+
+struct StrataParams {
+  const void* q;
+  int64_t q_sb, q_sh, q_st;
+  int Hq, Hkv, Tq, rep, R_real, BH;
+  float qscale;                 // scaling * log2(e)
+  const float* signs;           // (d) +-1
+  const uint16_t* mu_k;         // (BH, d) fp16
+  const uint16_t* mu_v;
+  int64_t n_t, cap_t;           // tier tokens, tile capacity
+  const uint8_t* kc;            // (BH, n_t, d*bits/8) planar rows
+  const uint16_t* ks;           // (BH, cap_t) fp16, zero past n_t
+  const uint8_t* vt;            // (BH, cap_t/32, 512*bits) value tiles
+  const uint16_t* vsl;          // (BH, cap_t/32, 32) fp16 slot-ordered value scales
+  int n_split;
+  float* ws_o;                  // tier partials (BH * S_all partials)
+  float* ws_m;
+  float* ws_l;
+  int S_all, s_base;
+  const float* ex_o;            // exact-row partials (BH * S_ex partials)
+  const float* ex_m;
+  const float* ex_l;
+  int S_ex;
+  void* out;
+};
+
+__device__ __forceinline__ int64_t strata_q_offset(const StrataParams& p, int b, int h, int r) {
+  const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
+  return static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq) * p.q_sh + static_cast<int64_t>(t) * p.q_st;
+}
+
+// Key operand element e of k-step w for lane group g: the channel it multiplies and log2 of the
+// factor its code carries (its position within the 16-bit half).
+template <int BITS>
+__device__ __forceinline__ int key_channel(int g, int w, int e) {
+  if constexpr (BITS == 4) {
+    const int byte = 16 * g + 4 * w + ((e >> 2) & 1) + 2 * (e & 1);
+    return ((e >> 1) & 1) ? 64 + byte : byte;
+  } else if constexpr (BITS == 8) {
+    constexpr int kOff[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    return 32 * g + 8 * w + kOff[e];
+  } else {
+    return 32 * (e >> 1) + 8 * g + 4 * (w >> 1) + 2 * (e & 1) + (w & 1);
+  }
+}
+template <int BITS>
+__device__ __forceinline__ int code_shift(int e) {
+  if constexpr (BITS == 4) return ((e >> 1) & 1) ? 4 : 0;
+  else if constexpr (BITS == 8) return 0;
+  else return 2 * (e >> 1);
+}
+template <int BITS>
+constexpr int smax_shift() { return BITS == 4 ? 4 : (BITS == 8 ? 0 : 6); }
+
+__device__ __forceinline__ half8 unpack4(uint32_t w) {
+  const uint32_t w8 = w >> 8;
+  return as_half8(u32x4{w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u});
+}
+__device__ __forceinline__ half8 unpack8(uint32_t w0, uint32_t w1) {
+  return as_half8(u32x4{w0 & 0x00FF00FFu, (w0 >> 8) & 0x00FF00FFu, w1 & 0x00FF00FFu, (w1 >> 8) & 0x00FF00FFu});
+}
+__device__ __forceinline__ half8 unpack2(uint32_t x) {
+  return as_half8(u32x4{x & 0x00030003u, x & 0x000C000Cu, x & 0x00300030u, x & 0x00C000C0u});
+}
+
+template <int BITS>
+struct StrataChunk {
+  static constexpr int KW = BITS;               // key words per tile per lane (4*BITS bytes)
+  static constexpr int VW = 2 * BITS;           // value words per lane per chunk
+  uint32_t kw[2][KW];
+  uint32_t ksw[2][2];
+  uint32_t vw[VW];
+  u32x4 vsw;
+};
+
+template <int BITS, int R, int DT>
+__device__ void strata_block(const StrataParams& p, int bh, int sidx, float* smem) {
+  constexpr int NCLS = BITS == 2 ? 4 : (BITS == 4 ? 2 : 1);   // probability classes (code factors)
+  constexpr int RB = 16 * BITS;                 // bytes per planar row
+  const int b = bh / p.Hkv, h = bh % p.Hkv;
+  float (*qs)[kSD] = reinterpret_cast<float (*)[kSD]>(smem);  // rotated, scaled query rows
+  float* qsum = smem + R * kSD;
+  float* qbias = qsum + R;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const int l = threadIdx.x % 64;
+  const int g = l >> 4, n = l & 15;
+  const int r_n = n % R;
+  const int hl_qk = (n / R) & 1;
+  const int v_pv = n / R;
+  const int gcl = v_pv >> 1, hl_pv = v_pv & 1;
+
+  // ---- query rows: q^ = FWHT(q * s) / sqrt(d) * qscale, sum(q^), qb = qscale * q . mu_K ----
+  for (int r = wave; r < R; r += kSWaves) {
+    float v0 = 0.0f, v1 = 0.0f, mk = 0.0f;
+    if (r < p.R_real) {
+      const int64_t qo = strata_q_offset(p, b, h, r);
+      const float x0 = load_as_f32<DT>(p.q, qo + l), x1 = load_as_f32<DT>(p.q, qo + l + 64);
+      mk = x0 * f16_to_f32(p.mu_k[static_cast<int64_t>(bh) * kSD + l]) +
+           x1 * f16_to_f32(p.mu_k[static_cast<int64_t>(bh) * kSD + l + 64]);
+      v0 = x0 * p.signs[l];
+      v1 = x1 * p.signs[l + 64];
+      fwht128(v0, v1, l);
+      const float f = 0.08838834764831845f * p.qscale;
+      v0 *= f;
+      v1 *= f;
+    }
+    qs[r][l] = v0;
+    qs[r][l + 64] = v1;
+    float su = v0 + v1;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      su += __shfl_xor(su, o, 64);
+      mk += __shfl_xor(mk, o, 64);
+    }
+    if (l == 0) {
+      qsum[r] = su;
+      qbias[r] = mk * p.qscale;
+    }
+  }
+  __syncthreads();
+  // ---- query operand of the key product (fixed for the block) ----
+  half8 bqk[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = qs[r_n][key_channel<BITS>(g, w, e)] *
+                      static_cast<float>(1 << (smax_shift<BITS>() - code_shift<BITS>(e)));
+      const _Float16 hi = static_cast<_Float16>(x);
+      bqk[w][e] = hl_qk ? static_cast<_Float16>(x - static_cast<float>(hi)) : hi;
+    }
+  }
+  const float half = static_cast<float>((1 << BITS) - 1) * 0.5f;
+  const float hq = half * qsum[r_n];
+  const float qbr = qbias[r_n];
+  constexpr float kDotScale = static_cast<float>(1 << (24 - smax_shift<BITS>()));   // dot = D * this
+
+  // ---- this wavefront's chunk range (balanced over the split's 4 wavefronts and all splits) ----
+  const int NC = static_cast<int>((p.n_t + 31) / 32);
+  const int NW = p.n_split * kSWaves;
+  const int w_all = sidx * kSWaves + wave;
+  const int t0 = 32 * static_cast<int>(static_cast<int64_t>(w_all) * NC / NW);
+  const int t1 = min(32 * static_cast<int>(static_cast<int64_t>(w_all + 1) * NC / NW), static_cast<int>(p.n_t));
+  const int t_last = t0 < t1 ? t0 + ((t1 - 1 - t0) & ~31) : t0;
+
+  const __amdgpu_buffer_rsrc_t rk =
+      make_rsrc(p.kc + static_cast<int64_t>(bh) * p.n_t * RB, static_cast<uint32_t>(p.n_t * RB));
+  // key scales padded to the tile capacity: a 4-token load never straddles the end of the row
+  const __amdgpu_buffer_rsrc_t rks =
+      make_rsrc(p.ks + static_cast<int64_t>(bh) * p.cap_t, static_cast<uint32_t>(p.cap_t * 2));
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(p.vt + static_cast<int64_t>(bh) * (p.cap_t / 32) * 512 * BITS,
+                static_cast<uint32_t>((p.cap_t / 32) * 512 * BITS));
+  const __amdgpu_buffer_rsrc_t rvs =
+      make_rsrc(p.vsl + static_cast<int64_t>(bh) * p.cap_t, static_cast<uint32_t>(p.cap_t * 2));
+  const int vo_k = n * RB + g * 4 * BITS;
+
+  using Chunk = StrataChunk<BITS>;
+  auto load_chunk = [&](int cb, Chunk& c) {
+    cb = min(cb, t_last);
+    const int so = __builtin_amdgcn_readfirstlane(cb * RB);
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+      const int vo = vo_k + tau * 16 * RB;
+      if constexpr (BITS == 2) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rk, vo, so, 2);
+        c.kw[tau][0] = x[0];
+        c.kw[tau][1] = x[1];
+      } else {
+#pragma unroll
+        for (int i = 0; i < BITS / 4; ++i) {
+          const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, vo + 16 * i, so, 2);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) c.kw[tau][4 * i + k] = x[k];
+        }
+      }
+      const auto kx = __builtin_amdgcn_raw_buffer_load_b64(rks, (16 * tau + 4 * g) * 2,
+                                                           __builtin_amdgcn_readfirstlane(cb * 2), 0);
+      c.ksw[tau][0] = kx[0];
+      c.ksw[tau][1] = kx[1];
+    }
+    const int sv = __builtin_amdgcn_readfirstlane((cb / 32) * 512 * BITS);
+#pragma unroll
+    for (int i = 0; i < BITS / 2; ++i) {
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, l * 16 + 1024 * i, sv, 2);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) c.vw[4 * i + k] = x[k];
+    }
+    c.vsw = __builtin_amdgcn_raw_buffer_load_b128(rvs, g * 16, __builtin_amdgcn_readfirstlane((cb / 32) * 64), 0);
+  };
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;
+  float lc[NCLS], zc[NCLS];
+#pragma unroll
+  for (int k = 0; k < NCLS; ++k) lc[k] = zc[k] = 0.0f;
+  const half2v hl_neg = hl_pv ? half2v{static_cast<_Float16>(-1.0f), static_cast<_Float16>(-1.0f)}
+                              : half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
+  constexpr float kLazy = 4.0f;
+
+  auto cls = [](int j) -> int { return BITS == 2 ? (j >> 1) : (BITS == 4 ? (((j & 3) >= 2) ? 1 : 0) : 0); };
+  auto step = [&](int cb, const Chunk& c) {
+    float s[8];
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        half8 a;
+        if constexpr (BITS == 4) a = unpack4(c.kw[tau][w]);
+        else if constexpr (BITS == 8) a = unpack8(c.kw[tau][2 * w], c.kw[tau][2 * w + 1]);
+        else a = unpack2((w & 1) ? (c.kw[tau][w >> 1] >> 8) : c.kw[tau][w >> 1]);
+        d = mfma(a, bqk[w], d);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dot = d[i] + dpp<kRowRor + R>(d[i]);                          // hi + lo columns
+        const float ks = h2f(c.ksw[tau][i >> 1], i & 1);
+        s[4 * tau + i] = __builtin_fmaf(ks, __builtin_fmaf(dot, kDotScale, -hq), qbr);
+      }
+    }
+    if (cb + 32 > t1) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (cb + 16 * (j >> 2) + 4 * g + (j & 3) >= t1) s[j] = -INFINITY;
+    }
+    float lm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    if (__any(lm > m_run + kLazy)) {
+      const float m_new = fmaxf(m_run, xmax32(xmax16(lm)));
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] *= alpha;
+#pragma unroll
+      for (int k = 0; k < NCLS; ++k) {
+        lc[k] *= alpha;
+        zc[k] *= alpha;
+      }
+      m_run = m_new;
+    }
+    float pr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pr[j] = __builtin_amdgcn_exp2f(s[j] - (m_run + static_cast<float>(code_shift<BITS>(j))));
+    uint32_t words[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j0 = 2 * jj, j1 = 2 * jj + 1;
+      const float v0 = h2f(c.vsw[jj], 0), v1 = h2f(c.vsw[jj], 1);          // scales of slots j0, j1
+      const half2v hi = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], v0, 0.0f)),
+                               static_cast<_Float16>(__builtin_fmaf(pr[j1], v1, 0.0f))};
+      const half2v cn = hi * hl_neg;
+      const half2v val = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], v0, static_cast<float>(cn[0]))),
+                                static_cast<_Float16>(__builtin_fmaf(pr[j1], v1, static_cast<float>(cn[1])))};
+      words[jj] = w2(val);
+      lc[cls(j0)] += pr[j0];
+      lc[cls(j1)] += pr[j1];
+      zc[cls(j0)] = __builtin_fmaf(pr[j0], v0, zc[cls(j0)]);
+      zc[cls(j1)] = __builtin_fmaf(pr[j1], v1, zc[cls(j1)]);
+    }
+    const half8 bp = as_half8(u32x4{words[0], words[1], words[2], words[3]});
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      half8 a;
+      if constexpr (BITS == 4) a = unpack4(c.vw[blk]);
+      else if constexpr (BITS == 8) a = unpack8(c.vw[(blk >> 1) * 4 + (blk & 1) * 2], c.vw[(blk >> 1) * 4 + (blk & 1) * 2 + 1]);
+      else a = unpack2((blk & 1) ? (c.vw[blk >> 1] >> 8) : c.vw[blk >> 1]);
+      acc[blk] = mfma(a, bp, acc[blk]);
+    }
+  };
+
+  if (t0 < t1) {
+    Chunk ca, cb_;
+    load_chunk(t0, ca);
+    for (int cb = t0;; cb += 64) {
+      load_chunk(cb + 32, cb_);
+      step(cb, ca);
+      if (cb + 32 >= t1) break;
+      load_chunk(cb + 64, ca);
+      step(cb + 32, cb_);
+      if (cb + 64 >= t1) break;
+    }
+  }
+
+  // ---- wavefront epilogue ----
+  float lsum = 0.0f, zsum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NCLS; ++k) {
+    const float f = static_cast<float>(1 << (BITS == 2 ? 2 * k : 4 * k));
+    lsum = __builtin_fmaf(lc[k], f, lsum);
+    zsum = __builtin_fmaf(zc[k], f, zsum);
+  }
+  const float l_run = xsum32(xsum16(lsum));
+  const float Z = -half * xsum32(xsum16(zsum));
+  __syncthreads();
+  float* red_o = smem;                           // [wave][R][d]
+  float* red_ml = smem + kSWaves * R * kSD;      // [wave][2][R]
+  constexpr float kTwo24 = 16777216.0f;
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = acc[blk][i] + dpp<kRowShr + R>(acc[blk][i]);
+      if (hl_pv == 1 && gcl == 0) red_o[(wave * R + r_n) * kSD + 16 * blk + 4 * g + i] = __builtin_fmaf(a, kTwo24, Z);
+    }
+  }
+  if (g == 0 && n < R) {
+    red_ml[(wave * 2 + 0) * R + n] = m_run;
+    red_ml[(wave * 2 + 1) * R + n] = l_run;
+  }
+  __syncthreads();
+  const int64_t po = static_cast<int64_t>(bh) * p.S_all + p.s_base + sidx;
+  for (int idx = threadIdx.x; idx < p.R_real * kSD; idx += kSThreads) {
+    const int r = idx / kSD, c = idx % kSD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kSWaves; ++w) M = fmaxf(M, red_ml[(w * 2) * R + r]);
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSWaves; ++w) {
+      const float mw_ = red_ml[(w * 2) * R + r];
+      const float wgt = (mw_ == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw_ - M);
+      O += wgt * red_o[(w * R + r) * kSD + c];
+      L += wgt * red_ml[(w * 2 + 1) * R + r];
+    }
+    p.ws_o[(po * R + r) * kSD + c] = O;
+    if (c == 0) {
+      p.ws_m[po * R + r] = M;
+      p.ws_l[po * R + r] = L;
+    }
+  }
+}
+
+template <int BITS, int R, int DT>
+__global__ __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(BITS == 8 ? 2 : 3)))
+void strata_tier_split(StrataParams p) {
+  extern __shared__ float smem[];
+  const int k = blockIdx.x / 8;
+  const int bh = blockIdx.x % 8 + 8 * (k / p.n_split);
+  if (bh < p.BH) strata_block<BITS, R, DT>(p, bh, k % p.n_split, smem);
+}
+
+// Merge of one (b, h): exact-row partials (unrotated) and every tier partial (rotated basis):
+// o = [sum_e w o_e + (sum_t w o_t) R + (sum_t w l_t) mu_V] / sum_all w l   (STRATA_KV.py:1784-1792)
+template <int R, int DT>
+__global__ __launch_bounds__(kSThreads) void strata_merge(StrataParams p) {
+  extern __shared__ float smem[];
+  const int bh = blockIdx.x;
+  const int b = bh / p.Hkv, h = bh % p.Hkv;
+  float* oc = smem;                              // [R][d] coded sum, then rotated back
+  float* stat = smem + R * kSD;                  // M[R], L[R], Lc[R]
+  const int wave = threadIdx.x / 64, l = threadIdx.x % 64;
+  if (threadIdx.x < R) {
+    const int r = threadIdx.x;
+    float M = -INFINITY;
+    for (int s = 0; s < p.S_ex; ++s) M = fmaxf(M, p.ex_m[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r]);
+    for (int s = 0; s < p.S_all; ++s) M = fmaxf(M, p.ws_m[(static_cast<int64_t>(bh) * p.S_all + s) * R + r]);
+    float L = 0.0f, Lc = 0.0f;
+    for (int s = 0; s < p.S_ex; ++s) {
+      const float m = p.ex_m[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r];
+      if (m != -INFINITY) L += __builtin_amdgcn_exp2f(m - M) * p.ex_l[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r];
+    }
+    for (int s = 0; s < p.S_all; ++s) {
+      const float m = p.ws_m[(static_cast<int64_t>(bh) * p.S_all + s) * R + r];
+      if (m != -INFINITY) Lc += __builtin_amdgcn_exp2f(m - M) * p.ws_l[(static_cast<int64_t>(bh) * p.S_all + s) * R + r];
+    }
+    stat[r] = M;
+    stat[R + r] = L + Lc;
+    stat[2 * R + r] = Lc;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < R * kSD; idx += kSThreads) {
+    const int r = idx / kSD, c = idx % kSD;
+    float O = 0.0f;
+    const float M = stat[r];
+    for (int s = 0; s < p.S_all; ++s) {
+      const int64_t po = static_cast<int64_t>(bh) * p.S_all + s;
+      const float m = p.ws_m[po * R + r];
+      if (m != -INFINITY) O += __builtin_amdgcn_exp2f(m - M) * p.ws_o[(po * R + r) * kSD + c];
+    }
+    oc[r * kSD + c] = O;
+  }
+  __syncthreads();
+  for (int r = wave; r < R; r += kSWaves) {       // coded sum back to the channel basis: x R
+    float v0 = oc[r * kSD + l], v1 = oc[r * kSD + l + 64];
+    fwht128(v0, v1, l);
+    oc[r * kSD + l] = v0 * 0.08838834764831845f * p.signs[l];
+    oc[r * kSD + l + 64] = v1 * 0.08838834764831845f * p.signs[l + 64];
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < p.R_real * kSD; idx += kSThreads) {
+    const int r = idx / kSD, c = idx % kSD;
+    const float M = stat[r];
+    float O = oc[r * kSD + c] + stat[2 * R + r] * f16_to_f32(p.mu_v[static_cast<int64_t>(bh) * kSD + c]);
+    for (int s = 0; s < p.S_ex; ++s) {
+      const int64_t po = static_cast<int64_t>(bh) * p.S_ex + s;
+      const float m = p.ex_m[po * R + r];
+      if (m != -INFINITY) O += __builtin_amdgcn_exp2f(m - M) * p.ex_o[(po * R + r) * kSD + c];
+    }
+    const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
+    store_from_f32<DT>(p.out, ((static_cast<int64_t>(b) * p.Tq + t) * p.Hq + hq) * kSD + c, O / stat[R + r]);
+  }
+}
+
+inline int strata_pow2(int64_t r) {
+  int R = 1;
+  while (R < r) R <<= 1;
+  return R;
+}
+
+// splits of each tier: fill about one round of resident blocks across all tiers, in proportion to
+// each tier's tokens, at least one 32-token chunk per wavefront
+inline void strata_plan(int64_t BH, int n_tiers, const int64_t* tier_n, int* ns) {
+  int64_t total = 0;
+  for (int t = 0; t < n_tiers; ++t) total += tier_n[t];
+  const int64_t target = 768;
+  for (int t = 0; t < n_tiers; ++t) {
+    const int64_t nc = (tier_n[t] + 31) / 32;
+    int64_t s = total > 0 ? (target * tier_n[t] + total * BH - 1) / (total * BH) : 1;
+    s = std::max<int64_t>(1, std::min<int64_t>(s, (nc + kSWaves - 1) / kSWaves));
+    ns[t] = tier_n[t] > 0 ? static_cast<int>(s) : 0;
+  }
+}
+
+}  // namespace
+}  // namespace kvq
+
+extern "C" int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t n_q,
+                                             int64_t n_exact, int group_k, int group_v, int64_t split_tokens);
+extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B,
+                               int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling, const uint8_t* kc,
+                               const uint16_t* k_lo, const uint16_t* k_sc, const uint8_t* vc, const uint16_t* vmeta,
+                               int64_t cap_t, int64_t n_q, int group_k, int group_v, const void* k_exact,
+                               const void* v_exact, int exact_dtype, int64_t cap_e, int64_t n_exact,
+                               const int64_t* exact_pos, const int64_t* q_pos, void* out, int out_dtype,
+                               float* workspace, int64_t workspace_floats, float* scores, int64_t scores_bh,
+                               float score_weight, int64_t split_tokens, int phases, void* stream);
+
+namespace {
+int64_t strata_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t n_exact, int n_tiers,
+                        const int64_t* tier_n, int64_t* ex_floats, int* S_all) {
+  int ns[16];
+  kvq::strata_plan(B * Hkv, n_tiers, tier_n, ns);
+  int S = 0;
+  for (int t = 0; t < n_tiers; ++t) S += ns[t];
+  *S_all = S;
+  *ex_floats = n_exact > 0 ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
+  const int64_t R = kvq::strata_pow2((Hq / Hkv) * Tq);
+  return *ex_floats + B * Hkv * static_cast<int64_t>(S) * R * (128 + 2);
+}
+}  // namespace
+
+extern "C" int64_t kvq_strata_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
+                                               int64_t n_exact, int n_tiers, const int64_t* tier_n) {
+  if (d != 128 || B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Tq <= 0 || n_tiers < 0 || n_tiers > 16) return -1;
+  if (n_tiers > 0 && tier_n == nullptr) return -1;
+  int64_t ex;
+  int S;
+  return strata_ws_parts(B, Hq, Hkv, Tq, n_exact, n_tiers, tier_n, &ex, &S);
+}
+
+extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B,
+                                 int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling, const float* signs,
+                                 const uint16_t* mu_k, const uint16_t* mu_v, int n_tiers, const int* tier_bits,
+                                 const int64_t* tier_n, const int64_t* tier_cap, const uint8_t* const* tier_kc,
+                                 const uint16_t* const* tier_ks, const uint8_t* const* tier_vt,
+                                 const uint16_t* const* tier_vsl, const void* k_exact, const void* v_exact,
+                                 int64_t cap_e, int64_t n_exact, const int64_t* exact_pos, const int64_t* q_pos,
+                                 void* out, float* workspace, int64_t workspace_floats, void* stream) {
+  using namespace kvq;
+  KVQ_REQUIRE(d == 128, "kvq_strata_decode: head_dim must be 128");
+  KVQ_REQUIRE(valid_dtype(q_dtype), "kvq_strata_decode: bad dtype");
+  KVQ_REQUIRE(B > 0 && Hkv > 0 && Hq % Hkv == 0 && Tq > 0, "kvq_strata_decode: bad head counts");
+  const int64_t R_real = (Hq / Hkv) * Tq;
+  KVQ_REQUIRE(R_real <= 8, "kvq_strata_decode: rep*Tq must be <= 8");
+  KVQ_REQUIRE(n_tiers >= 0 && n_tiers <= 16, "kvq_strata_decode: at most 16 tiers");
+  KVQ_REQUIRE(n_tiers == 0 || (tier_bits && tier_n && tier_cap && tier_kc && tier_ks && tier_vt && tier_vsl),
+              "kvq_strata_decode: null tier arrays");
+  int64_t coded = 0;
+  for (int t = 0; t < n_tiers; ++t) {
+    KVQ_REQUIRE(tier_bits[t] == 2 || tier_bits[t] == 4 || tier_bits[t] == 8, "kvq_strata_decode: tier bits in {2,4,8}");
+    KVQ_REQUIRE(tier_n[t] >= 0 && tier_cap[t] % 32 == 0 && tier_n[t] <= tier_cap[t] && tier_n[t] < (1LL << 30),
+                "kvq_strata_decode: tier capacity must be a multiple of 32 holding n");
+    KVQ_REQUIRE(tier_n[t] == 0 || (tier_kc[t] && tier_ks[t] && tier_vt[t] && tier_vsl[t]), "kvq_strata_decode: null tier");
+    coded += tier_n[t];
+  }
+  KVQ_REQUIRE(coded == 0 || (signs && mu_k && mu_v), "kvq_strata_decode: null rotation / means");
+  KVQ_REQUIRE(coded + n_exact > 0, "kvq_strata_decode: empty cache");
+  KVQ_REQUIRE(q && out && workspace, "kvq_strata_decode: null q / out / workspace");
+  int64_t ex_floats;
+  int S_all;
+  const int64_t need = strata_ws_parts(B, Hq, Hkv, Tq, n_exact, n_tiers, tier_n, &ex_floats, &S_all);
+  KVQ_REQUIRE(workspace_floats >= need, "kvq_strata_decode: workspace too small (%lld < %lld floats)",
+              (long long)workspace_floats, (long long)need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int R = strata_pow2(R_real);
+  StrataParams p{};
+  p.q = q; p.q_sb = q_sb; p.q_sh = q_sh; p.q_st = q_st;
+  p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.Tq = (int)Tq; p.rep = (int)(Hq / Hkv); p.R_real = (int)R_real;
+  p.BH = (int)(B * Hkv);
+  p.qscale = scaling * 1.4426950408889634f;
+  p.signs = signs; p.mu_k = mu_k; p.mu_v = mu_v;
+  p.out = out;
+  // exact rows: partials of the KIVI exact-row blocks (no packed rows), into the first region
+  const int64_t S_ex = (n_exact + 31) / 32;
+  if (n_exact > 0) {
+    const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,
+                                   nullptr, nullptr, 0, 0, 32, 32, k_exact, v_exact, q_dtype, cap_e, n_exact, exact_pos,
+                                   q_pos, out, q_dtype, workspace, ex_floats, nullptr, 0, 0.0f, 0, 1, stream);
+    if (rc != KVQ_OK) return rc;
+    const int64_t nrow = B * Hkv * S_ex * R;
+    p.ex_o = workspace;
+    p.ex_m = workspace + nrow * 128;
+    p.ex_l = p.ex_m + nrow;
+    p.S_ex = (int)S_ex;
+  }
+  float* tw = workspace + ex_floats;
+  const int64_t trow = B * Hkv * static_cast<int64_t>(S_all) * R;
+  p.ws_o = tw;
+  p.ws_m = tw + trow * 128;
+  p.ws_l = p.ws_m + trow;
+  p.S_all = S_all;
+  int ns[16];
+  strata_plan(B * Hkv, n_tiers, tier_n, ns);
+  const int bh_pad = (p.BH + 7) / 8 * 8;
+  const size_t split_smem = std::max<size_t>((R * kSD + 2 * R) * sizeof(float),
+                                             (kSWaves * R * kSD + kSWaves * 2 * R) * sizeof(float));
+  int base = 0;
+  for (int t = 0; t < n_tiers; ++t) {
+    if (ns[t] == 0) continue;
+    p.n_t = tier_n[t]; p.cap_t = tier_cap[t];
+    p.kc = tier_kc[t]; p.ks = tier_ks[t]; p.vt = tier_vt[t]; p.vsl = tier_vsl[t];
+    p.n_split = ns[t];
+    p.s_base = base;
+    base += ns[t];
+    const dim3 grid(static_cast<unsigned>(ns[t]) * bh_pad);
+#define KVQ_STRATA_LAUNCH(BITS_, R_, DT_) \
+    hipLaunchKernelGGL((strata_tier_split<BITS_, R_, DT_>), grid, dim3(kSThreads), split_smem, s, p)
+#define KVQ_STRATA_R(BITS_, DT_)                                         \
+    switch (R) {                                                         \
+      case 1: KVQ_STRATA_LAUNCH(BITS_, 1, DT_); break;                   \
+      case 2: KVQ_STRATA_LAUNCH(BITS_, 2, DT_); break;                   \
+      case 4: KVQ_STRATA_LAUNCH(BITS_, 4, DT_); break;                   \
+      default: KVQ_STRATA_LAUNCH(BITS_, 8, DT_); break;                  \
+    }
+#define KVQ_STRATA_BITS(DT_)                                             \
+    switch (tier_bits[t]) {                                              \
+      case 2: KVQ_STRATA_R(2, DT_) break;                                \
+      case 4: KVQ_STRATA_R(4, DT_) break;                                \
+      default: KVQ_STRATA_R(8, DT_) break;                               \
+    }
+    switch (q_dtype) {
+      case KVQ_F32: KVQ_STRATA_BITS(KVQ_F32) break;
+      case KVQ_F16: KVQ_STRATA_BITS(KVQ_F16) break;
+      default: KVQ_STRATA_BITS(KVQ_BF16) break;
+    }
+#undef KVQ_STRATA_BITS
+#undef KVQ_STRATA_R
+#undef KVQ_STRATA_LAUNCH
+    KVQ_LAUNCH_CHECK("kvq_strata_decode(tier)");
+  }
+  const size_t msmem = (R * kSD + 3 * R) * sizeof(float);
+#define KVQ_STRATA_MERGE(R_, DT_) \
+  hipLaunchKernelGGL((strata_merge<R_, DT_>), dim3(p.BH), dim3(kSThreads), msmem, s, p)
+#define KVQ_STRATA_MR(DT_)                                               \
+  switch (R) {                                                           \
+    case 1: KVQ_STRATA_MERGE(1, DT_); break;                             \
+    case 2: KVQ_STRATA_MERGE(2, DT_); break;                             \
+    case 4: KVQ_STRATA_MERGE(4, DT_); break;                             \
+    default: KVQ_STRATA_MERGE(8, DT_); break;                            \
+  }
+  switch (q_dtype) {
+    case KVQ_F32: KVQ_STRATA_MR(KVQ_F32) break;
+    case KVQ_F16: KVQ_STRATA_MR(KVQ_F16) break;
+    default: KVQ_STRATA_MR(KVQ_BF16) break;
+  }
+#undef KVQ_STRATA_MR
+#undef KVQ_STRATA_MERGE
+  KVQ_LAUNCH_CHECK("kvq_strata_decode(merge)");
+  return KVQ_OK;
+}

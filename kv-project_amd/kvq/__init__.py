@@ -9,13 +9,14 @@ from .kivi import kivi_quant, kivi_quant_stored, pack_codes, unpack_codes, v_til
 from .decode import PackedKIVICache, kivi_decode, workspace_floats
 from .state import DecodeCtl, KIVIState, Router, register, routed, router_attention
 from .evict import gather_dequant, retained_cache, topk_retain
-from .strata import (pack_planar, rotation_signs, strata_center_rotate, strata_quantize, strata_v_tile,
-                     uniform_step, unpack_planar)
+from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strata_center_rotate, strata_decode,
+                     strata_quantize, strata_v_tile, strata_workspace_floats, uniform_step, unpack_planar)
 
 __all__ = [
     "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes",
     "v_tile", "v_untile", "vmeta_tile", "PackedKIVICache", "kivi_decode", "workspace_floats",
     "DecodeCtl", "KIVIState", "Router", "register", "routed", "router_attention",
     "gather_dequant", "retained_cache", "topk_retain", "pack_planar", "unpack_planar", "rotation_signs",
-    "uniform_step", "strata_center_rotate", "strata_quantize", "strata_v_tile",
+    "uniform_step", "strata_center_rotate", "strata_quantize", "strata_v_tile", "StrataCache", "StrataTier",
+    "strata_decode", "strata_workspace_floats",
 ]

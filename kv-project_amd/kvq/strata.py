@@ -117,3 +117,127 @@ def strata_v_tile(rows: torch.Tensor, vs: torch.Tensor, bits: int, cap_t: int):
     _lib.call("kvq_strata_v_tile", rows.data_ptr(), B * H, n, n * rb, bits, cap_t, tiles.data_ptr(), vs.data_ptr(),
               n, vsl.data_ptr(), _lib.stream_of(rows))
     return tiles, vsl
+
+
+from dataclasses import dataclass, field
+from typing import List, Sequence, Tuple
+
+
+@dataclass
+class StrataTier:
+    """One stratum of a STRATA cache on the GPU (the tier dict of STRATA_KV.py:1615-1623 plus the
+    decode kernel's value tiles): planar key rows (B, Hkv, n, d*bits/8), fp16 key scales
+    (B, Hkv, cap) zero past n, value tiles and slot-ordered value scales of capacity cap
+    (multiple of 32)."""
+    bits: int
+    n: int
+    kc: torch.Tensor
+    ks: torch.Tensor
+    vt: torch.Tensor
+    vsl: torch.Tensor
+    cap: int
+    vc: torch.Tensor = None          # planar value rows (kept for byte accounting / repacking)
+    vs: torch.Tensor = None
+
+
+@dataclass
+class StrataCache:
+    """STRATA-coded context of one layer (StrataState, STRATA_KV.py:1710-1760): per-head fp16 means,
+    the rotation signs, strata of 2/4/8-bit codes, and exact rows (window + appended tokens)."""
+    mu_k: torch.Tensor
+    mu_v: torch.Tensor
+    signs: torch.Tensor
+    tiers: List[StrataTier]
+    k_exact: torch.Tensor
+    v_exact: torch.Tensor
+    n_exact: int
+    exact_pos: Optional[torch.Tensor] = None
+
+    @classmethod
+    @torch.no_grad()
+    def from_context(cls, K: torch.Tensor, V: torch.Tensor, *, window: int,
+                     assign: Sequence[Tuple[int, torch.Tensor]], extra_exact: int = 0) -> "StrataCache":
+        """K, V (B, Hkv, T, d): rows [0, T - window) are coded, the last ``window`` stay exact.
+        ``assign`` = [(bits, idx (B, Hkv, m) positions in [0, T - window))]: the tokens of each
+        stratum (a token in no stratum is dropped, as the reference's level 0).  The means are
+        taken over all coded rows (STRATA_KV.py:1546)."""
+        _lib.require_gpu(K, V)
+        B, H, T, d = K.shape
+        nc = T - window
+        signs = rotation_signs(d, device=K.device)
+        mu_k, yk = strata_center_rotate(K[:, :, :nc], signs)
+        mu_v, yv = strata_center_rotate(V[:, :, :nc], signs)
+        tiers = []
+        for bits, idx in assign:
+            idx = idx.to(device=K.device, dtype=torch.int32)
+            m = idx.shape[2]
+            kc, ks = strata_quantize(yk, bits, idx)
+            vc, vs = strata_quantize(yv, bits, idx)
+            cap = max(32, -(-m // 32) * 32)
+            vt, vsl = strata_v_tile(vc, vs, bits, cap)
+            ksp = torch.zeros((B, H, cap), dtype=torch.float16, device=K.device)
+            ksp[:, :, :m] = ks
+            tiers.append(StrataTier(bits, m, kc, ksp, vt, vsl, cap, vc, vs))
+        cap_e = max(window + extra_exact, 1)
+        ke = torch.zeros((B, H, cap_e, d), dtype=K.dtype, device=K.device)
+        ve = torch.zeros_like(ke)
+        ke[:, :, :window] = K[:, :, nc:]
+        ve[:, :, :window] = V[:, :, nc:]
+        return cls(mu_k, mu_v, signs, tiers, ke, ve, window)
+
+    def coded_bytes(self) -> int:
+        """Bytes of the coded context a decode step reads: codes + fp16 scales of every stratum and
+        the fp16 means (context_bytes' coded part, STRATA_KV.py:1729-1735)."""
+        tot = self.mu_k.numel() * 2 + self.mu_v.numel() * 2
+        for t in self.tiers:
+            tot += 2 * t.kc.numel() + 2 * t.n * t.kc.shape[0] * t.kc.shape[1] * 2
+        return tot
+
+
+def strata_workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_exact: int, tier_n: Sequence[int]) -> int:
+    import ctypes
+    arr = (ctypes.c_int64 * max(1, len(tier_n)))(*tier_n)
+    n = _lib.load().kvq_strata_decode_workspace(B, Hq, Hkv, Tq, d, n_exact, len(tier_n), arr)
+    if n < 0:
+        raise _lib.KVQError("kvq_strata_decode_workspace rejected the shape")
+    return n
+
+
+@torch.no_grad()
+def strata_decode(q: torch.Tensor, scaling: float, cache: StrataCache, *, q_pos: Optional[torch.Tensor] = None,
+                  out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """StrataState.attend (STRATA_KV.py:1762-1795) for q (B, Hq, Tq, d) -> (B, Tq, Hq, d): the exact
+    rows (visible per q_pos / exact_pos when both are set) and every stratum, merged exactly, the
+    coded part rotated back once and the value mean added."""
+    import ctypes
+    _lib.require_gpu(q)
+    B, Hq, Tq, d = q.shape
+    Hkv = cache.k_exact.shape[1]
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if cache.k_exact.dtype != q.dtype:
+        raise TypeError("q and the exact rows must share a dtype")
+    tiers = [t for t in cache.tiers if t.n > 0]
+    nt = len(tiers)
+    need = strata_workspace_floats(B, Hq, Hkv, Tq, d, cache.n_exact, [t.n for t in tiers])
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty((need,), dtype=torch.float32, device=q.device)
+    if out is None:
+        out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
+    P = ctypes.c_void_p
+    bits = (ctypes.c_int * max(1, nt))(*[t.bits for t in tiers])
+    tn = (ctypes.c_int64 * max(1, nt))(*[t.n for t in tiers])
+    cap = (ctypes.c_int64 * max(1, nt))(*[t.cap for t in tiers])
+    kc = (P * max(1, nt))(*[t.kc.data_ptr() for t in tiers])
+    ks = (P * max(1, nt))(*[t.ks.data_ptr() for t in tiers])
+    vt = (P * max(1, nt))(*[t.vt.data_ptr() for t in tiers])
+    vsl = (P * max(1, nt))(*[t.vsl.data_ptr() for t in tiers])
+    ep = cache.exact_pos if q_pos is not None else None
+    qp = q_pos if ep is not None else None
+    dt = _lib.DTYPE_CODE[q.dtype]
+    _lib.call("kvq_strata_decode", q.data_ptr(), dt, q.stride(0), q.stride(1), q.stride(2), B, Hq, Hkv, Tq, d,
+              float(scaling), cache.signs.data_ptr(), cache.mu_k.data_ptr(), cache.mu_v.data_ptr(), nt, bits, tn,
+              cap, kc, ks, vt, vsl, cache.k_exact.data_ptr(), cache.v_exact.data_ptr(), cache.k_exact.shape[2],
+              cache.n_exact, _lib.ptr(ep), _lib.ptr(qp), out.data_ptr(), workspace.data_ptr(), workspace.numel(),
+              _lib.stream_of(q))
+    return out

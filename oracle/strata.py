@@ -167,11 +167,16 @@ def strata_attend(q: np.ndarray, scaling: float, k_exact: np.ndarray, v_exact: n
     rep = Hq // Hkv
     qg = q.reshape(Hkv, rep * Tq, d).astype(np.float64)
     R = R.astype(np.float64)
-    s_ex = np.einsum("hrd,hnd->hrn", qg, k_exact.astype(np.float64)) * scaling
-    m_e = s_ex.max(-1)
-    e_ex = np.exp(s_ex - m_e[..., None])
-    l_e = e_ex.sum(-1)
-    o = np.einsum("hrn,hnd->hrd", e_ex, v_exact.astype(np.float64))
+    if k_exact.shape[1]:
+        s_ex = np.einsum("hrd,hnd->hrn", qg, k_exact.astype(np.float64)) * scaling
+        m_e = s_ex.max(-1)
+        e_ex = np.exp(s_ex - m_e[..., None])
+        l_e = e_ex.sum(-1)
+        o = np.einsum("hrn,hnd->hrd", e_ex, v_exact.astype(np.float64))
+    else:                                   # no exact rows: an empty partial
+        m_e = np.full(qg.shape[:2], -np.inf)
+        l_e = np.zeros(qg.shape[:2])
+        o = np.zeros(qg.shape)
     if tiers:
         qr = (qg @ R.T) * scaling
         qb = np.einsum("hrd,hd->hr", qg, mu_k.astype(np.float64)) * scaling

@@ -98,3 +98,69 @@ def test_value_tiles_layout(bits):
             np.testing.assert_array_equal(got, full[0, h, 32 * c:32 * c + 32])
             want_s = [vfull[0, h, 32 * c + _slot_token(s // 8, s % 8)] for s in range(32)]
             np.testing.assert_array_equal(vsl[0, h, c], np.array(want_s, np.float16))
+
+
+def _assign(B, H, nc, fracs, g):
+    """Per (b, h): tokens ranked by a random importance; the top fracs[0] -> 8 bits, the next
+    fracs[1] -> 4 bits, the next fracs[2] -> 2 bits, the rest dropped (level 0)."""
+    imp = torch.rand((B, H, nc), generator=g)
+    order = imp.argsort(-1, descending=True).to(torch.int32)
+    out, a = [], 0
+    for bits, f in zip((8, 4, 2), fracs):
+        m = int(round(f * nc))
+        if m:
+            out.append((bits, order[..., a:a + m].contiguous()))
+        a += m
+    return out
+
+
+def _oracle_out(cache, q, K, V, window, scaling):
+    B = q.shape[0]
+    d = q.shape[-1]
+    R = os_.rotation_matrix(d)
+    outs = []
+    for b in range(B):
+        tiers = []
+        for t in cache.tiers:
+            ck = os_.unpack_planar(t.kc[b].cpu().numpy(), t.bits)
+            cv = os_.unpack_planar(t.vc[b].cpu().numpy(), t.bits)
+            tiers.append((t.bits, ck, t.ks[b, :, :t.n].float().cpu().numpy(), cv, t.vs[b].float().cpu().numpy()))
+        nc = K.shape[2] - window
+        outs.append(os_.strata_attend(q[b:b + 1].float().numpy(), scaling, K[b, :, nc:].float().numpy(),
+                                      V[b, :, nc:].float().numpy(), tiers, cache.mu_k[b].float().cpu().numpy(),
+                                      cache.mu_v[b].float().cpu().numpy(), R))
+    return np.concatenate(outs, 0)
+
+
+@pytest.mark.parametrize("dtype,Hq,Hkv,Tq", [(torch.float32, 8, 2, 1), (torch.bfloat16, 8, 2, 1),
+                                             (torch.float32, 8, 2, 2)])
+def test_strata_decode_mixed_tiers(dtype, Hq, Hkv, Tq):
+    import kvq
+    g = torch.Generator().manual_seed(5 + Tq)
+    B, T, W, d = 2, 700, 40, 128
+    K = (torch.randn((B, Hkv, T, d), generator=g) * 1.5 + 0.3).to(dtype)
+    V = torch.randn((B, Hkv, T, d), generator=g).to(dtype)
+    q = torch.randn((B, Hq, Tq, d), generator=g).to(dtype)
+    assign = _assign(B, Hkv, T - W, (0.1, 0.3, 0.5), g)
+    cache = kvq.StrataCache.from_context(K.cuda(), V.cuda(), window=W, assign=assign)
+    out = kvq.strata_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
+    ref = _oracle_out(cache, q, K, V, W, d ** -0.5)
+    err = float(np.abs(out - ref).max())
+    tol = 2e-3 if dtype == torch.float32 else 1e-2
+    assert err <= tol, err
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_strata_decode_single_width_no_exact_rows(bits):
+    import kvq
+    g = torch.Generator().manual_seed(40 + bits)
+    B, Hq, Hkv, T, d = 1, 4, 4, 1000, 128
+    K = torch.randn((B, Hkv, T, d), generator=g)
+    V = torch.randn((B, Hkv, T, d), generator=g)
+    q = torch.randn((B, Hq, 1, d), generator=g)
+    idx = torch.stack([torch.randperm(T, generator=g)[:777] for _ in range(Hkv)])[None].to(torch.int32)
+    cache = kvq.StrataCache.from_context(K.cuda(), V.cuda(), window=0, assign=[(bits, idx)])
+    cache.n_exact = 0
+    out = kvq.strata_decode(q.cuda(), d ** -0.5, cache).cpu().numpy()
+    ref = _oracle_out(cache, q, K, V, 0, d ** -0.5)
+    assert float(np.abs(out - ref).max()) <= 2e-3
