@@ -227,6 +227,36 @@ int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, in
                       const int64_t* q_pos, void* out, float* workspace, int64_t workspace_floats, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * A9  Blockwise token-axis DCT coding (no counterpart in the reference; the contract follows its
+ * conventions: absmax_quant, STRATA_KV.py:549-554, and offset-binary 4-bit storage,
+ * TILT_KV.py:2621-2625).  Per (b, h, 64-token block, channel): X_k = sum_n C[k][n] x_n for the
+ * 16 kept rows of the orthonormal DCT-II, summed over n = 0..63 in increasing n in float32
+ * without fused multiply-add; s = max(fp16(max|X| / 7), 2^-24); code = clamp(rint(X / s), -7, 7) + 7.
+ * x: (BH, T, d) of x_dtype, row stride d, head stride x_bh; T % 64 == 0, d == 128.
+ * ctab: (16, 64) float32 (float32 of the closed form).  Per block, 1024 code bytes and 128 fp16
+ * scales: for_values == 0 -> key layout (16 pack_codes rows of 64 bytes by coefficient; scales by
+ * channel); for_values == 1 -> value tile (word (gp*16 + n)*8 + blk holds coefficients
+ * 8gp .. 8gp+7 of channel 16*blk + n, coefficient 8gp + e at nibble {0,4,1,5,2,6,3,7}[e]; scales
+ * ordered [n][blk]).
+ * ---------------------------------------------------------------------------------------- */
+int kvq_dct_encode(const void* x, int x_dtype, int64_t BH, int64_t T, int64_t d, int64_t x_bh,
+                   const float* ctab, int for_values, uint8_t* codes, uint16_t* scales, void* stream);
+
+/* Decode over a DCT-coded context of T tokens (T % 64 == 0, kc/ks key blocks, vc/vs value blocks,
+ * each (B*Hkv, T/64, ...)) plus n_exact exact rows (as kvq_kivi_decode's exact rows, dtype =
+ * q_dtype): attention over the reconstructions x_n = sum_k C[k][n] s_k (code_k - 7), computed in
+ * the coefficient domain (logits C^T (K-codes q), values (V-codes) (C p)).  out (B, Tq, Hq, d) of
+ * q_dtype.  Workspace floats from kvq_dct_decode_workspace. */
+int64_t kvq_dct_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t T,
+                                 int64_t n_exact);
+int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B, int64_t Hq,
+                   int64_t Hkv, int64_t Tq, int64_t d, float scaling, const float* ctab, int64_t T,
+                   const uint8_t* kc, const uint16_t* ks, const uint8_t* vc, const uint16_t* vs,
+                   const void* k_exact, const void* v_exact, int64_t cap_e, int64_t n_exact,
+                   const int64_t* exact_pos, const int64_t* q_pos, void* out, float* workspace,
+                   int64_t workspace_floats, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * A2  Fused quantise + pack append of one token per sequence (streaming KIVI window).
  * No per-step quantiser exists in the reference (its decode-time appends stay exact,
  * STRATA_KV.py:707-714); this restates KIVIMethod's window rule (806-822) for a streaming cache:

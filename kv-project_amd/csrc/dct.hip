@@ -1,0 +1,645 @@
+// Blockwise token-axis DCT coding of K/V (A9) and the decode over it.
+//
+// The reference has no DCT; the contract follows its conventions: per (KV head,
+// channel, 64-token block) an orthonormal DCT-II along tokens, coefficients 0..15 kept, each
+// (block, channel) quantised with symmetric absmax at 4 bits (absmax_quant, STRATA_KV.py:549-554:
+// s = max(fp16(max|X| / 7), 2^-24), codes clamp(round(X / s), -7, 7)), stored offset-binary (+7) as
+// TILT_KV.py:2621-2625 does.
+//
+// Encoder arithmetic order (restated by the CPU oracle, so codes and scales agree bit for bit):
+// X_k = sum over n = 0..63 in increasing n of float32(C[k][n] * x_n), no fused multiply-add, C the
+// float32 table of the kept rows (passed in); s and codes in float32 with IEEE division.
+//
+// Stored per (b, h, block):
+//   key codes   16 rows (coefficients) x 64 bytes in pack_codes order (byte i = c[2i] << 4 | c[2i+1])
+//   key scales  128 fp16 (by channel)
+//   value codes 1 KiB decode tile: word (gp * 16 + n) * 8 + blk (gp = coefficient half 0/1, n = 0..15,
+//               blk = 0..7) holds the codes of coefficients 8gp .. 8gp+7 of channel 16*blk + n, code
+//               of coefficient 8gp + e at nibble kNib[e] = {0,4,1,5,2,6,3,7}[e]
+//   value scales 128 fp16 ordered [n][blk] (channel 16*blk + n)
+//
+// Decode (coefficient domain, four matrix-core stages per block and wavefront):
+//   u_k   = sum_c q_c s^K_c (code_kc - 7)             (q x key codes, the KIVI key-group machinery)
+//   s_n   = sum_k C[k][n] u_k                         (logits of the block's 64 tokens)
+//   w_k   = sum_n C[k][n] p_n                         (after the online softmax)
+//   out_c += s^V_c (sum_k w_k code_kc - 7 sum_k w_k)  (w transposed through LDS against value codes)
+#include "common.hpp"
+#include "mfma_common.hpp"
+
+namespace kvq {
+namespace {
+
+constexpr int kDB = 64;                   // tokens per block
+constexpr int kDK = 16;                   // kept coefficients
+constexpr int kDD = 128;                  // head_dim
+constexpr int kDThreads = 256;
+constexpr int kDWaves = 4;
+
+__device__ __forceinline__ float as_stored_h(float x) {
+  x = fminf(fmaxf(x, -65504.0f), 65504.0f);
+  return f16_to_f32(f32_to_f16(x));
+}
+
+__device__ __constant__ int kNibOfElem[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+
+// one thread per (b, h, block, channel)
+template <int DT>
+__global__ __launch_bounds__(256) void dct_encode_kernel(const void* __restrict__ x, int64_t T, int64_t x_bh,
+                                                         const float* __restrict__ ctab, int for_values,
+                                                         uint8_t* __restrict__ codes, uint16_t* __restrict__ scales,
+                                                         int64_t total) {
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int c = static_cast<int>(id % kDD);
+  const int64_t blk_all = id / kDD;                // (bh, block)
+  const int64_t nb = T / kDB;
+  const int64_t bh = blk_all / nb, blk = blk_all % nb;
+  const int64_t base = bh * x_bh + blk * kDB * kDD + c;
+  float X[kDK];
+#pragma unroll
+  for (int k = 0; k < kDK; ++k) X[k] = 0.0f;
+  for (int n = 0; n < kDB; ++n) {
+    const float xv = load_as_f32<DT>(x, base + static_cast<int64_t>(n) * kDD);
+#pragma unroll
+    for (int k = 0; k < kDK; ++k) X[k] = __fadd_rn(X[k], __fmul_rn(ctab[k * kDB + n], xv));
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kDK; ++k) amax = fmaxf(amax, fabsf(X[k]));
+  const float s = fmaxf(as_stored_h(__fdiv_rn(amax, 7.0f)), 5.9604644775390625e-08f);
+  int q[kDK];
+#pragma unroll
+  for (int k = 0; k < kDK; ++k) q[k] = static_cast<int>(fminf(fmaxf(rintf(__fdiv_rn(X[k], s)), -7.0f), 7.0f)) + 7;
+  uint8_t* out = codes + blk_all * 1024;
+  if (!for_values) {
+    scales[blk_all * kDD + c] = f32_to_f16(s);
+#pragma unroll
+    for (int k = 0; k < kDK; ++k) {
+      const int other = __shfl_down(q[k], 1, 64);
+      if ((c & 1) == 0) out[k * 64 + c / 2] = static_cast<uint8_t>((q[k] << 4) | other);
+    }
+  } else {
+    const int n = c % 16, b8 = c / 16;
+    scales[blk_all * kDD + n * 8 + b8] = f32_to_f16(s);
+    uint32_t* words = reinterpret_cast<uint32_t*>(out);
+#pragma unroll
+    for (int gp = 0; gp < 2; ++gp) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w |= static_cast<uint32_t>(q[8 * gp + e]) << (4 * kNibOfElem[e]);
+      words[(gp * 16 + n) * 8 + b8] = w;
+    }
+  }
+}
+
+// Channel of slot s within an 8-channel k-slice of a pack_codes row (as the KIVI key kernels).
+__device__ __constant__ int kCosD[8] = {1, 5, 0, 4, 3, 7, 2, 6};
+
+struct DctParams {
+  const void* q;
+  int64_t q_sb, q_sh, q_st;
+  int Hq, Hkv, Tq, rep, R_real, BH;
+  float qscale;
+  int64_t nb;                     // blocks per (b, h)
+  const uint8_t* kc;              // (BH, nb, 16, 64)
+  const uint16_t* ks;             // (BH, nb, 128)
+  const uint8_t* vc;              // (BH, nb, 1024)
+  const uint16_t* vs;             // (BH, nb, 128) [n][blk]
+  const float* ctab;              // (16, 64) float32
+  int n_split;
+  float* ws_o;
+  float* ws_m;
+  float* ws_l;
+  int S_all;
+  const float* ex_o;
+  const float* ex_m;
+  const float* ex_l;
+  int S_ex;
+  void* out;
+};
+
+__device__ __forceinline__ int64_t dct_q_offset(const DctParams& p, int b, int h, int r) {
+  const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
+  return static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq) * p.q_sh + static_cast<int64_t>(t) * p.q_st;
+}
+
+template <int R, int DT>
+__device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
+  const int b = bh / p.Hkv, h = bh % p.Hkv;
+  float (*qs)[kDD] = reinterpret_cast<float (*)[kDD]>(smem);                    // q * qscale
+  uint32_t* bq_all = reinterpret_cast<uint32_t*>(smem + R * kDD);               // [wave][2R][64]
+  uint32_t* bv_all = bq_all + kDWaves * 2 * R * 64;                            // [wave][R][16]
+  float* wsm_all = reinterpret_cast<float*>(bv_all + kDWaves * R * 16);         // [wave][R][16 + 2]
+  u32x4* cst = reinterpret_cast<u32x4*>(wsm_all + kDWaves * R * 18);            // [12][64] lane constants
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const int l = threadIdx.x % 64;
+  const int g = l >> 4, n = l & 15;
+  const int r_n = n % R;
+  const int hl = (n / R) & 1;
+  const int ci = (l >> 2) & 3, ck = l & 3;
+  const int c0 = 32 * g + 8 * ci + kCosD[2 * ck];
+  const int c1 = 32 * g + 8 * ci + kCosD[2 * ck + 1];
+  const float kinv = (ck & 1) ? 1.0f : 16.0f;
+  uint32_t* bq = bq_all + wave * 2 * R * 64;
+  uint32_t* bv = bv_all + wave * R * 16;
+  float* wsm = wsm_all + wave * R * 18;            // [R][16] w values, [R] sum w, [R] alpha
+
+  for (int idx = threadIdx.x; idx < R * kDD; idx += kDThreads) {
+    const int r = idx / kDD, c = idx % kDD;
+    qs[r][c] = r < p.R_real ? load_as_f32<DT>(p.q, dct_q_offset(p, b, h, r) + c) * p.qscale : 0.0f;
+  }
+  // lane constants (the same for every wavefront; wave 0 writes them): C^T tiles of the logit
+  // stage, hi / lo, 4 nonzero slots each; C slices of the coefficient stage, hi / lo per k-step
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint32_t hi[2], lo[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const float a = p.ctab[(4 * g + 2 * kk) * kDB + 16 * t + n];
+        const float bb = p.ctab[(4 * g + 2 * kk + 1) * kDB + 16 * t + n];
+        const _Float16 ah = static_cast<_Float16>(a), bh16 = static_cast<_Float16>(bb);
+        hi[kk] = pack_h2(ah, bh16);
+        lo[kk] = pack_h2(static_cast<_Float16>(a - static_cast<float>(ah)), static_cast<_Float16>(bb - static_cast<float>(bh16)));
+      }
+      cst[(2 * t) * 64 + l] = u32x4{hi[0], hi[1], 0u, 0u};
+      cst[(2 * t + 1) * 64 + l] = u32x4{lo[0], lo[1], 0u, 0u};
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        float v[2];
+        _Float16 vh[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int j = 2 * jj + u;
+          const int tok = 32 * ks + 16 * (j >> 2) + 4 * g + (j & 3);
+          v[u] = p.ctab[n * kDB + tok];                 // row n = coefficient (M index m = n)
+          vh[u] = static_cast<_Float16>(v[u]);
+        }
+        hi[jj] = pack_h2(vh[0], vh[1]);
+        lo[jj] = pack_h2(static_cast<_Float16>(v[0] - static_cast<float>(vh[0])),
+                         static_cast<_Float16>(v[1] - static_cast<float>(vh[1])));
+      }
+      cst[(8 + 2 * ks) * 64 + l] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+      cst[(8 + 2 * ks + 1) * 64 + l] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    }
+  }
+  __syncthreads();
+
+  const int NW = p.n_split * kDWaves;
+  const int w_all = sidx * kDWaves + wave;
+  const int b0 = static_cast<int>(static_cast<int64_t>(w_all) * p.nb / NW);
+  const int b1 = static_cast<int>(static_cast<int64_t>(w_all + 1) * p.nb / NW);
+
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.kc + static_cast<int64_t>(bh) * p.nb * 1024,
+                                              static_cast<uint32_t>(p.nb * 1024));
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(p.ks + static_cast<int64_t>(bh) * p.nb * kDD,
+                                               static_cast<uint32_t>(p.nb * kDD * 2));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vc + static_cast<int64_t>(bh) * p.nb * 1024,
+                                              static_cast<uint32_t>(p.nb * 1024));
+  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(p.vs + static_cast<int64_t>(bh) * p.nb * kDD,
+                                               static_cast<uint32_t>(p.nb * kDD * 2));
+  // value-code lanes: coefficient half g < 2 reads its 8 words; g >= 2 reads past the range (zero)
+  const int vo_v = g < 2 ? (g * 16 + n) * 32 : 0x40000000;
+
+  struct Blk {
+    u32x4 kw;
+    uint32_t ks0, ks1;
+    u32x4 vw[2];
+    u32x4 vsw;
+  };
+  auto load_blk = [&](int bi, Blk& c) {
+    bi = min(bi, b1 - 1);
+    const int so = __builtin_amdgcn_readfirstlane(bi * 1024);
+    c.kw = __builtin_amdgcn_raw_buffer_load_b128(rk, n * 64 + 16 * g, so, 2);
+    const int sk = __builtin_amdgcn_readfirstlane(bi * kDD * 2);
+    c.ks0 = __builtin_amdgcn_raw_buffer_load_b16(rks, c0 * 2, sk, 0);
+    c.ks1 = __builtin_amdgcn_raw_buffer_load_b16(rks, c1 * 2, sk, 0);
+    c.vw[0] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo_v, so, 2);
+    c.vw[1] = __builtin_amdgcn_raw_buffer_load_b128(rv, vo_v + 16, so, 2);
+    c.vsw = __builtin_amdgcn_raw_buffer_load_b128(rvs, n * 16, sk, 2);
+  };
+
+  auto unpack = [](uint32_t w) -> half8 {
+    const uint32_t w8 = w >> 8;
+    return as_half8(u32x4{w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u});
+  };
+  constexpr float kTwo20 = 1048576.0f;
+  constexpr float kTwo24 = 16777216.0f;
+  constexpr float kLazy = 4.0f;
+  constexpr float kPOff = 6.0f;   // probabilities carry 2^6 so their fp16 parts stay normal; m is stored minus it
+  const half8 tiny = as_half8(u32x4{0x00100010u, 0x00100010u, 0x00100010u, 0x00100010u});   // 2^-20
+  const half2v hl_neg = hl ? half2v{static_cast<_Float16>(-1.0f), static_cast<_Float16>(-1.0f)}
+                           : half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
+  const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl) * 64 + g * 16);
+  const u32x4* bv_src = reinterpret_cast<const u32x4*>(bv + r_n * 16 + g * 4);
+
+  float acc[8][2];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k][0] = acc[k][1] = 0.0f;
+  float m_run = -INFINITY, la = 0.0f;
+  // split of an fp32 value into the fp16 hi (variant 0) or lo (variant 1) part this lane feeds
+  auto part = [&](float x) -> _Float16 {
+    const _Float16 hi16 = static_cast<_Float16>(x);
+    return hl ? static_cast<_Float16>(x - static_cast<float>(hi16)) : hi16;
+  };
+
+  auto step = [&](const Blk& c) {
+    // ---- key group of this block: B operand q * sK (hi / lo), bias -7 q . sK ----
+    wave_lds_fence();
+    {
+      const float sc0 = h2f(c.ks0, 0), sc1 = h2f(c.ks1, 0);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float qa = qs[r][c0], qb = qs[r][c1];
+        const float qak = qa * kinv, qbk = qb * kinv;
+        const _Float16 h0 = static_cast<_Float16>(qak * sc0);
+        const _Float16 h1 = static_cast<_Float16>(qbk * sc1);
+        const _Float16 e0 = static_cast<_Float16>(qak * sc0 - static_cast<float>(h0));
+        const _Float16 e1 = static_cast<_Float16>(qbk * sc1 - static_cast<float>(h1));
+        bq[(2 * r) * 64 + l] = pack_h2(h0, h1);
+        bq[(2 * r + 1) * 64 + l] = pack_h2(e0, e1);
+        float P = -7.0f * (qa * sc0 + qb * sc1);
+        P += dpp<kQuadSwap1>(P);
+        P += dpp<kQuadSwap2>(P);
+        if (ck == 0) {
+          const _Float16 ph = static_cast<_Float16>(P);
+          const _Float16 pl = static_cast<_Float16>(P - static_cast<float>(ph));
+          bv[r * 16 + g * 4 + ci] = pack_h2(ph, pl);
+        }
+      }
+    }
+    wave_lds_fence();
+    half8 bqk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bqk[i] = as_half8(bq_src[i]);
+    u32x4 bvr = *bv_src;
+    if (hl) bvr = u32x4{0u, 0u, 0u, 0u};
+    // ---- u_k (coefficient k = 4g + i), log2 units ----
+    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d = mfma(unpack(c.kw[i]), bqk[i], d);
+    d = mfma(tiny, as_half8(bvr), d);
+    float u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = (d[i] + dpp<kRowRor + R>(d[i])) * kTwo20;
+    // ---- logits of the 64 tokens: s = C^T u (token 16t + 4g + i in register 4t + i) ----
+    const half8 b2 = as_half8(u32x4{pack_h2(part(u[0]), part(u[1])), pack_h2(part(u[2]), part(u[3])), 0u, 0u});
+    float s[16];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f32x4 e = mfma(as_half8(cst[(2 * t) * 64 + l]), b2, f32x4{0.f, 0.f, 0.f, 0.f});
+      e = mfma(as_half8(cst[(2 * t + 1) * 64 + l]), b2, e);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[4 * t + i] = e[i] + dpp<kRowRor + R>(e[i]);
+    }
+    // ---- online softmax, lazy maximum ----
+    float lm = s[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) lm = fmaxf(lm, s[j]);
+    if (__any(lm > m_run + kLazy)) {
+      const float m_new = fmaxf(m_run, xmax32(xmax16(lm)));
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      la *= alpha;
+      m_run = m_new;
+      if (g == 0 && n < R) wsm[R * 17 + n] = alpha;           // alpha of row n for the value lanes
+      wave_lds_fence();
+#pragma unroll
+      for (int jr = 0; jr < 2; ++jr) {
+        const int r = 2 * g + jr;
+        const float a = r < R ? wsm[R * 17 + r] : 1.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k][jr] *= a;
+      }
+    }
+    float pr[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run + kPOff);
+      la += pr[j];
+    }
+    // ---- w_k = sum_n C[k][n] p_n (coefficient 4g + i) ----
+    f32x4 dw = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      uint32_t words[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j0 = 2 * jj, j1 = 2 * jj + 1;
+        const float x0 = pr[4 * (2 * ks + (j0 >> 2)) + (j0 & 3)];
+        const float x1 = pr[4 * (2 * ks + (j1 >> 2)) + (j1 & 3)];
+        const half2v hi2 = half2v{static_cast<_Float16>(x0), static_cast<_Float16>(x1)};
+        const half2v cn = hi2 * hl_neg;
+        words[jj] = w2(half2v{static_cast<_Float16>(x0 + static_cast<float>(cn[0])),
+                              static_cast<_Float16>(x1 + static_cast<float>(cn[1]))});
+      }
+      const half8 b4 = as_half8(u32x4{words[0], words[1], words[2], words[3]});
+      dw = mfma(as_half8(cst[(8 + 2 * ks) * 64 + l]), b4, dw);
+      dw = mfma(as_half8(cst[(8 + 2 * ks + 1) * 64 + l]), b4, dw);
+    }
+    // ---- w to LDS (rows of the value stage), and sum_k w per row ----
+    float wsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float w = dw[i] + dpp<kRowRor + R>(dw[i]);
+      wsum += w;
+      if (n < R) wsm[n * 16 + 4 * g + i] = w;
+    }
+    wsum = xsum32(xsum16(wsum));
+    if (g == 0 && n < R) wsm[R * 16 + n] = wsum;
+    wave_lds_fence();
+    // A operand: row m = 2r + hl5 of w (hi / lo), coefficients 8g .. 8g+7 (g < 2), element e / 16
+    // for the high-nibble elements 2, 3, 6, 7
+    const int m_r = n >> 1, m_hl = n & 1;
+    uint32_t aw[4] = {0u, 0u, 0u, 0u};
+    if (g < 2 && m_r < R) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        float x[2];
+#pragma unroll
+        for (int u2 = 0; u2 < 2; ++u2) {
+          const int e = 2 * jj + u2;
+          x[u2] = wsm[m_r * 16 + 8 * g + e] * (((e >> 1) & 1) ? 0.0625f : 1.0f);
+        }
+        _Float16 hh[2];
+#pragma unroll
+        for (int u2 = 0; u2 < 2; ++u2) {
+          const _Float16 hi16 = static_cast<_Float16>(x[u2]);
+          hh[u2] = m_hl ? static_cast<_Float16>(x[u2] - static_cast<float>(hi16)) : hi16;
+        }
+        aw[jj] = pack_h2(hh[0], hh[1]);
+      }
+    }
+    const half8 a5 = as_half8(u32x4{aw[0], aw[1], aw[2], aw[3]});
+    const float W0 = 2 * g < R ? wsm[R * 16 + 2 * g] : 0.0f;
+    const float W1 = 2 * g + 1 < R ? wsm[R * 16 + 2 * g + 1] : 0.0f;
+    // ---- out rows 2g, 2g+1, channel 16*blk + n ----
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      const f32x4 d5 = mfma(a5, unpack(c.vw[blk >> 2][blk & 3]), f32x4{0.f, 0.f, 0.f, 0.f});
+      const float sv = h2f(c.vsw[blk >> 1], blk & 1);
+      acc[blk][0] = __builtin_fmaf(sv, __builtin_fmaf(d5[0] + d5[1], kTwo24, -7.0f * W0), acc[blk][0]);
+      acc[blk][1] = __builtin_fmaf(sv, __builtin_fmaf(d5[2] + d5[3], kTwo24, -7.0f * W1), acc[blk][1]);
+    }
+  };
+
+  if (b0 < b1) {
+    Blk ca, cb_;
+    load_blk(b0, ca);
+    for (int bi = b0;; bi += 2) {
+      load_blk(bi + 1, cb_);
+      step(ca);
+      if (bi + 1 >= b1) break;
+      load_blk(bi + 2, ca);
+      step(cb_);
+      if (bi + 2 >= b1) break;
+    }
+  }
+
+  // ---- epilogue: 4-wave merge of (m, l, o) into this split's partial ----
+  const float l_run = xsum32(xsum16(la));
+  __syncthreads();
+  float* red_o = smem;                            // [wave][R][d]
+  float* red_ml = smem + kDWaves * R * kDD;       // [wave][2][R]
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk) {
+#pragma unroll
+    for (int jr = 0; jr < 2; ++jr) {
+      const int r = 2 * g + jr;
+      if (r < R) red_o[(wave * R + r) * kDD + 16 * blk + n] = acc[blk][jr];
+    }
+  }
+  if (g == 0 && n < R) {
+    red_ml[(wave * 2 + 0) * R + n] = m_run - kPOff;
+    red_ml[(wave * 2 + 1) * R + n] = l_run;
+  }
+  __syncthreads();
+  const int64_t po = static_cast<int64_t>(bh) * p.S_all + sidx;
+  for (int idx = threadIdx.x; idx < p.R_real * kDD; idx += kDThreads) {
+    const int r = idx / kDD, c = idx % kDD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDWaves; ++w) M = fmaxf(M, red_ml[(w * 2) * R + r]);
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kDWaves; ++w) {
+      const float mw_ = red_ml[(w * 2) * R + r];
+      const float wgt = (mw_ == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw_ - M);
+      O += wgt * red_o[(w * R + r) * kDD + c];
+      L += wgt * red_ml[(w * 2 + 1) * R + r];
+    }
+    p.ws_o[(po * R + r) * kDD + c] = O;
+    if (c == 0) {
+      p.ws_m[po * R + r] = M;
+      p.ws_l[po * R + r] = L;
+    }
+  }
+}
+
+template <int R, int DT>
+__global__ __launch_bounds__(kDThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void dct_split(DctParams p) {
+  extern __shared__ float smem[];
+  const int k = blockIdx.x / 8;
+  const int bh = blockIdx.x % 8 + 8 * (k / p.n_split);
+  if (bh < p.BH) dct_block<R, DT>(p, bh, k % p.n_split, smem);
+}
+
+template <int R, int DT>
+__global__ __launch_bounds__(kDThreads) void dct_merge(DctParams p) {
+  extern __shared__ float smem[];
+  const int bh = blockIdx.x;
+  const int b = bh / p.Hkv, h = bh % p.Hkv;
+  float* stat = smem;                            // M[R], L[R]
+  if (threadIdx.x < R) {
+    const int r = threadIdx.x;
+    float M = -INFINITY, L = 0.0f;
+    for (int s = 0; s < p.S_ex; ++s) M = fmaxf(M, p.ex_m[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r]);
+    for (int s = 0; s < p.S_all; ++s) M = fmaxf(M, p.ws_m[(static_cast<int64_t>(bh) * p.S_all + s) * R + r]);
+    for (int s = 0; s < p.S_ex; ++s) {
+      const int64_t po = static_cast<int64_t>(bh) * p.S_ex + s;
+      if (p.ex_m[po * R + r] != -INFINITY) L += __builtin_amdgcn_exp2f(p.ex_m[po * R + r] - M) * p.ex_l[po * R + r];
+    }
+    for (int s = 0; s < p.S_all; ++s) {
+      const int64_t po = static_cast<int64_t>(bh) * p.S_all + s;
+      if (p.ws_m[po * R + r] != -INFINITY) L += __builtin_amdgcn_exp2f(p.ws_m[po * R + r] - M) * p.ws_l[po * R + r];
+    }
+    stat[r] = M;
+    stat[R + r] = L;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < p.R_real * kDD; idx += kDThreads) {
+    const int r = idx / kDD, c = idx % kDD;
+    const float M = stat[r];
+    float O = 0.0f;
+    for (int s = 0; s < p.S_ex; ++s) {
+      const int64_t po = static_cast<int64_t>(bh) * p.S_ex + s;
+      if (p.ex_m[po * R + r] != -INFINITY) O += __builtin_amdgcn_exp2f(p.ex_m[po * R + r] - M) * p.ex_o[(po * R + r) * kDD + c];
+    }
+    for (int s = 0; s < p.S_all; ++s) {
+      const int64_t po = static_cast<int64_t>(bh) * p.S_all + s;
+      if (p.ws_m[po * R + r] != -INFINITY) O += __builtin_amdgcn_exp2f(p.ws_m[po * R + r] - M) * p.ws_o[(po * R + r) * kDD + c];
+    }
+    const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
+    store_from_f32<DT>(p.out, ((static_cast<int64_t>(b) * p.Tq + t) * p.Hq + hq) * kDD + c, O / stat[R + r]);
+  }
+}
+
+inline int dct_pow2(int64_t r) {
+  int R = 1;
+  while (R < r) R <<= 1;
+  return R;
+}
+
+// splits per (b, h): about one round of 768 resident blocks, at least one block per wavefront
+inline int dct_splits(int64_t BH, int64_t nb) {
+  int64_t s = (768 + BH - 1) / BH;
+  s = std::max<int64_t>(1, std::min<int64_t>(s, (nb + kDWaves - 1) / kDWaves));
+  return static_cast<int>(s);
+}
+
+}  // namespace
+}  // namespace kvq
+
+using namespace kvq;
+
+extern "C" int kvq_dct_encode(const void* x, int x_dtype, int64_t BH, int64_t T, int64_t d, int64_t x_bh,
+                              const float* ctab, int for_values, uint8_t* codes, uint16_t* scales, void* stream) {
+  KVQ_REQUIRE(valid_dtype(x_dtype), "kvq_dct_encode: bad dtype");
+  KVQ_REQUIRE(d == kDD, "kvq_dct_encode: head_dim must be 128");
+  KVQ_REQUIRE(BH >= 0 && T >= 0 && T % kDB == 0 && x_bh >= T * d, "kvq_dct_encode: T must be a multiple of 64");
+  const int64_t total = BH * (T / kDB) * kDD;
+  if (total == 0) return KVQ_OK;
+  KVQ_REQUIRE(x && ctab && codes && scales, "kvq_dct_encode: null pointer");
+  KVQ_REQUIRE(total / 256 < (1LL << 31), "kvq_dct_encode: too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  KVQ_DISPATCH_DTYPE(x_dtype, hipLaunchKernelGGL((dct_encode_kernel<DT_>), dim3(static_cast<unsigned>((total + 255) / 256)),
+                                                dim3(256), 0, s, x, T, x_bh, ctab, for_values, codes, scales, total));
+  KVQ_LAUNCH_CHECK("kvq_dct_encode");
+  return KVQ_OK;
+}
+
+extern "C" int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t n_q,
+                                             int64_t n_exact, int group_k, int group_v, int64_t split_tokens);
+extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B,
+                               int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling, const uint8_t* kc,
+                               const uint16_t* k_lo, const uint16_t* k_sc, const uint8_t* vc, const uint16_t* vmeta,
+                               int64_t cap_t, int64_t n_q, int group_k, int group_v, const void* k_exact,
+                               const void* v_exact, int exact_dtype, int64_t cap_e, int64_t n_exact,
+                               const int64_t* exact_pos, const int64_t* q_pos, void* out, int out_dtype,
+                               float* workspace, int64_t workspace_floats, float* scores, int64_t scores_bh,
+                               float score_weight, int64_t split_tokens, int phases, void* stream);
+
+namespace {
+int64_t dct_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t T, int64_t n_exact, int64_t* ex_floats,
+                     int* S) {
+  *S = T > 0 ? kvq::dct_splits(B * Hkv, T / 64) : 0;
+  *ex_floats = n_exact > 0 ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
+  const int64_t R = kvq::dct_pow2((Hq / Hkv) * Tq);
+  return *ex_floats + B * Hkv * static_cast<int64_t>(*S) * R * (128 + 2);
+}
+}  // namespace
+
+extern "C" int64_t kvq_dct_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t T,
+                                            int64_t n_exact) {
+  if (d != 128 || B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Tq <= 0 || T < 0 || T % 64 != 0) return -1;
+  int64_t ex;
+  int S;
+  return dct_ws_parts(B, Hq, Hkv, Tq, T, n_exact, &ex, &S);
+}
+
+extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B,
+                              int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling, const float* ctab,
+                              int64_t T, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc, const uint16_t* vs,
+                              const void* k_exact, const void* v_exact, int64_t cap_e, int64_t n_exact,
+                              const int64_t* exact_pos, const int64_t* q_pos, void* out, float* workspace,
+                              int64_t workspace_floats, void* stream) {
+  KVQ_REQUIRE(d == kDD, "kvq_dct_decode: head_dim must be 128");
+  KVQ_REQUIRE(valid_dtype(q_dtype), "kvq_dct_decode: bad dtype");
+  KVQ_REQUIRE(B > 0 && Hkv > 0 && Hq % Hkv == 0 && Tq > 0, "kvq_dct_decode: bad head counts");
+  const int64_t R_real = (Hq / Hkv) * Tq;
+  KVQ_REQUIRE(R_real <= 8, "kvq_dct_decode: rep*Tq must be <= 8");
+  KVQ_REQUIRE(T >= 0 && T % kDB == 0, "kvq_dct_decode: T must be a multiple of 64");
+  KVQ_REQUIRE(T / kDB * 1024 < (1LL << 31), "kvq_dct_decode: more than 2^21 blocks per head");
+  KVQ_REQUIRE(T == 0 || (ctab && kc && ks && vc && vs), "kvq_dct_decode: null coded cache");
+  KVQ_REQUIRE(T + n_exact > 0, "kvq_dct_decode: empty cache");
+  KVQ_REQUIRE(q && out && workspace, "kvq_dct_decode: null q / out / workspace");
+  int64_t ex_floats;
+  int S;
+  const int64_t need = dct_ws_parts(B, Hq, Hkv, Tq, T, n_exact, &ex_floats, &S);
+  KVQ_REQUIRE(workspace_floats >= need, "kvq_dct_decode: workspace too small (%lld < %lld floats)",
+              (long long)workspace_floats, (long long)need);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int R = dct_pow2(R_real);
+  DctParams p{};
+  p.q = q; p.q_sb = q_sb; p.q_sh = q_sh; p.q_st = q_st;
+  p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.Tq = (int)Tq; p.rep = (int)(Hq / Hkv); p.R_real = (int)R_real;
+  p.BH = (int)(B * Hkv);
+  p.qscale = scaling * 1.4426950408889634f;
+  p.nb = T / kDB;
+  p.kc = kc; p.ks = ks; p.vc = vc; p.vs = vs; p.ctab = ctab;
+  p.out = out;
+  const int64_t S_ex = (n_exact + 31) / 32;
+  if (n_exact > 0) {
+    const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,
+                                   nullptr, nullptr, 0, 0, 32, 32, k_exact, v_exact, q_dtype, cap_e, n_exact, exact_pos,
+                                   q_pos, out, q_dtype, workspace, ex_floats, nullptr, 0, 0.0f, 0, 1, stream);
+    if (rc != KVQ_OK) return rc;
+    const int64_t nrow = B * Hkv * S_ex * R;
+    p.ex_o = workspace;
+    p.ex_m = workspace + nrow * 128;
+    p.ex_l = p.ex_m + nrow;
+    p.S_ex = (int)S_ex;
+  }
+  float* tw = workspace + ex_floats;
+  const int64_t trow = B * Hkv * static_cast<int64_t>(S) * R;
+  p.ws_o = tw;
+  p.ws_m = tw + trow * 128;
+  p.ws_l = p.ws_m + trow;
+  p.S_all = S;
+  p.n_split = S;
+  const int bh_pad = (p.BH + 7) / 8 * 8;
+  const size_t split_smem = std::max<size_t>(
+      (R * kDD + kDWaves * (2 * R * 64 + R * 16) + kDWaves * R * 18) * sizeof(float) + 12 * 64 * 16,
+      (kDWaves * R * kDD + kDWaves * 2 * R) * sizeof(float));
+  if (S > 0) {
+#define KVQ_DCT_SPLIT(R_, DT_) \
+    hipLaunchKernelGGL((dct_split<R_, DT_>), dim3(static_cast<unsigned>(S) * bh_pad), dim3(kDThreads), split_smem, s, p)
+#define KVQ_DCT_R(DT_)                                   \
+    switch (R) {                                         \
+      case 1: KVQ_DCT_SPLIT(1, DT_); break;              \
+      case 2: KVQ_DCT_SPLIT(2, DT_); break;              \
+      case 4: KVQ_DCT_SPLIT(4, DT_); break;              \
+      default: KVQ_DCT_SPLIT(8, DT_); break;             \
+    }
+    switch (q_dtype) {
+      case KVQ_F32: KVQ_DCT_R(KVQ_F32) break;
+      case KVQ_F16: KVQ_DCT_R(KVQ_F16) break;
+      default: KVQ_DCT_R(KVQ_BF16) break;
+    }
+#undef KVQ_DCT_R
+#undef KVQ_DCT_SPLIT
+    KVQ_LAUNCH_CHECK("kvq_dct_decode(split)");
+  }
+  const size_t msmem = 2 * R * sizeof(float);
+#define KVQ_DCT_MERGE(R_, DT_) hipLaunchKernelGGL((dct_merge<R_, DT_>), dim3(p.BH), dim3(kDThreads), msmem, s, p)
+#define KVQ_DCT_MR(DT_)                                  \
+  switch (R) {                                           \
+    case 1: KVQ_DCT_MERGE(1, DT_); break;                \
+    case 2: KVQ_DCT_MERGE(2, DT_); break;                \
+    case 4: KVQ_DCT_MERGE(4, DT_); break;                \
+    default: KVQ_DCT_MERGE(8, DT_); break;               \
+  }
+  switch (q_dtype) {
+    case KVQ_F32: KVQ_DCT_MR(KVQ_F32) break;
+    case KVQ_F16: KVQ_DCT_MR(KVQ_F16) break;
+    default: KVQ_DCT_MR(KVQ_BF16) break;
+  }
+#undef KVQ_DCT_MR
+#undef KVQ_DCT_MERGE
+  KVQ_LAUNCH_CHECK("kvq_dct_decode(merge)");
+  return KVQ_OK;
+}

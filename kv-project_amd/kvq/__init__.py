@@ -11,6 +11,7 @@ from .state import DecodeCtl, KIVIState, Router, register, routed, router_attent
 from .evict import gather_dequant, retained_cache, topk_retain
 from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strata_center_rotate, strata_decode,
                      strata_quantize, strata_v_tile, strata_workspace_floats, uniform_step, unpack_planar)
+from .dct import DctCache, dct_decode, dct_encode, dct_table, dct_workspace_floats
 
 __all__ = [
     "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes",
@@ -18,5 +19,6 @@ __all__ = [
     "DecodeCtl", "KIVIState", "Router", "register", "routed", "router_attention",
     "gather_dequant", "retained_cache", "topk_retain", "pack_planar", "unpack_planar", "rotation_signs",
     "uniform_step", "strata_center_rotate", "strata_quantize", "strata_v_tile", "StrataCache", "StrataTier",
-    "strata_decode", "strata_workspace_floats",
+    "strata_decode", "strata_workspace_floats", "DctCache", "dct_decode", "dct_encode", "dct_table",
+    "dct_workspace_floats",
 ]

@@ -1,0 +1,117 @@
+"""Blockwise DCT coder and decode on the GPU against the CPU oracle (oracle/dct.py).
+
+* dct_encode: key and value layouts read back to (coefficient, channel) codes and fp16 scales
+  equal the oracle's bit for bit (same fixed float32 arithmetic order), fp32 and bf16 inputs;
+* dct_decode: attention over the reconstructed rows plus exact rows, within 2e-3 (fp32) /
+  1e-2 (bf16) of the oracle's float64 result, for every GQA row count R = rep * Tq in 1..8,
+  with and without exact rows, and over a coded-only context.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.dct as od
+
+pytestmark = pytest.mark.gpu
+
+_NIB = [0, 4, 1, 5, 2, 6, 3, 7]
+
+
+def _keys_to_oracle(codes: np.ndarray) -> np.ndarray:
+    """(BH, nb, 1024) key layout -> (BH, nb, 16, 128) codes."""
+    rows = codes.reshape(codes.shape[0], codes.shape[1], 16, 64)
+    out = np.empty(rows.shape[:3] + (128,), np.uint8)
+    out[..., 0::2] = rows >> 4
+    out[..., 1::2] = rows & 15
+    return out
+
+
+def _values_to_oracle(codes: np.ndarray, scales: np.ndarray):
+    """(BH, nb, 1024) value tiles + (BH, nb, 128) [n][blk] scales -> (BH, nb, 16, 128), (BH, nb, 128)."""
+    words = codes.view(np.uint32).reshape(codes.shape[0], codes.shape[1], 2, 16, 8)   # gp, n, blk
+    out = np.empty((codes.shape[0], codes.shape[1], 16, 128), np.uint8)
+    for gp in range(2):
+        for e in range(8):
+            nib = (words[:, :, gp] >> (4 * _NIB[e])) & 15                               # (BH, nb, n, blk)
+            out[:, :, 8 * gp + e] = nib.transpose(0, 1, 3, 2).reshape(codes.shape[0], codes.shape[1], 128)
+    sc = scales.reshape(scales.shape[0], scales.shape[1], 16, 8).transpose(0, 1, 3, 2).reshape(scales.shape)
+    return out, sc
+
+
+def test_dct_table_matches_oracle():
+    import kvq
+    np.testing.assert_array_equal(kvq.dct_table().cpu().numpy(), od.dct_table())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_encode_bit_exact(dtype):
+    import kvq
+    g = torch.Generator().manual_seed(11)
+    B, H, T = 2, 3, 320
+    x = (torch.randn((B, H, T, 128), generator=g).cumsum(2) * 0.3 + 0.5).to(dtype)
+    x[0, 0, :64, 5] = 0                                                 # an all-zero (block, channel)
+    kc, ks = kvq.dct_encode(x.cuda())
+    vc, vs = kvq.dct_encode(x.cuda(), for_values=True)
+    c_o, s_o, _ = od.dct_encode(x.float().numpy().reshape(B * H, T, 128))
+    nb = T // 64
+    got_k = _keys_to_oracle(kc.cpu().numpy().reshape(B * H, nb, 1024))
+    np.testing.assert_array_equal(got_k, c_o)
+    np.testing.assert_array_equal(ks.float().cpu().numpy().reshape(B * H, nb, 128), s_o)
+    got_v, got_vs = _values_to_oracle(vc.cpu().numpy().reshape(B * H, nb, 1024),
+                                      vs.float().cpu().numpy().reshape(B * H, nb, 128))
+    np.testing.assert_array_equal(got_v, c_o)
+    np.testing.assert_array_equal(got_vs, s_o)
+    assert s_o[0, 0, 5] == np.float32(2.0 ** -24) and (c_o[0, 0, :, 5] == 7).all()
+
+
+def _oracle(cache, q, scaling):
+    B = q.shape[0]
+    nb = cache.T // 64
+    BH = cache.kc.shape[0] * cache.kc.shape[1]
+    kc = _keys_to_oracle(cache.kc.cpu().numpy().reshape(BH, nb, 1024))
+    ks = cache.ks.float().cpu().numpy().reshape(BH, nb, 128)
+    vc, vs = _values_to_oracle(cache.vc.cpu().numpy().reshape(BH, nb, 1024),
+                               cache.vs.float().cpu().numpy().reshape(BH, nb, 128))
+    ne = cache.n_exact
+    ke = cache.k_exact[:, :, :ne].float().cpu().numpy()
+    ve = cache.v_exact[:, :, :ne].float().cpu().numpy()
+    return od.dct_decode(q.float().numpy(), scaling, kc, ks, vc, vs, ke, ve)
+
+
+@pytest.mark.parametrize("dtype,Hq,Hkv,Tq,T,W", [
+    (torch.float32, 4, 4, 1, 1000, 40),     # R = 1, coded tail spills into the exact rows
+    (torch.float32, 8, 4, 1, 640, 64),      # R = 2
+    (torch.float32, 8, 2, 1, 2048, 0),      # R = 4, coded only
+    (torch.float32, 8, 2, 2, 777, 9),       # R = 8
+    (torch.bfloat16, 8, 2, 1, 1500, 30),
+    (torch.float32, 8, 1, 1, 130, 2),       # R = 8 over two blocks
+])
+def test_decode_matches_oracle(dtype, Hq, Hkv, Tq, T, W):
+    import kvq
+    g = torch.Generator().manual_seed(T + Hq)
+    B, d = 2, 128
+    K = (torch.randn((B, Hkv, T, d), generator=g).cumsum(2) * 0.2 + 0.4).to(dtype)
+    V = torch.randn((B, Hkv, T, d), generator=g).to(dtype)
+    q = torch.randn((B, Hq, Tq, d), generator=g).to(dtype)
+    cache = kvq.DctCache.from_context(K.cuda(), V.cuda(), window=W)
+    assert cache.T == (T - W) // 64 * 64 and cache.n_exact == T - cache.T
+    out = kvq.dct_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
+    ref = _oracle(cache, q, d ** -0.5)
+    err = float(np.abs(out - ref).max())
+    tol = 2e-3 if dtype == torch.float32 else 1e-2
+    assert err <= tol, err
+
+
+def test_decode_peaked_logits():
+    """Large logits (one block dominates): the online maximum and lazy rescale path."""
+    import kvq
+    g = torch.Generator().manual_seed(3)
+    B, Hq, Hkv, T, d = 1, 8, 2, 4096, 128
+    K = torch.randn((B, Hkv, T, d), generator=g) * 0.3
+    K[:, :, 2000:2064] += 4.0
+    V = torch.randn((B, Hkv, T, d), generator=g)
+    q = torch.ones((B, Hq, 1, d)) * 0.5
+    cache = kvq.DctCache.from_context(K.cuda(), V.cuda(), window=0)
+    out = kvq.dct_decode(q.cuda(), d ** -0.5, cache).cpu().numpy()
+    ref = _oracle(cache, q, d ** -0.5)
+    assert float(np.abs(out - ref).max()) <= 2e-3
