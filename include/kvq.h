@@ -227,6 +227,33 @@ int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, in
                       const int64_t* q_pos, void* out, float* workspace, int64_t workspace_floats, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * C3  Mixed-width KIVI blocks.  Every 64-token block of a (b, h) has its own width b in
+ * {2, 4, 8}; inside it the codes and fp16 metadata are kivi_quant's (STRATA_KV.py:826-856) at
+ * that width with group 32.  The reference keeps one dense tensor per width and launches once per
+ * width (StrataState.attend, STRATA_KV.py:1782-1783); here one flat buffer holds, per (b, h) from
+ * 2 KiB unit bh_base[bh], the 8-bit blocks, then the 4-bit, then the 2-bit blocks (token order
+ * within a width), a block of width b taking b + 1 units:
+ *   0              key rows, planar (pack_planar, STRATA_KV.py:1171-1182), 64 x 16b bytes
+ *   1024 b         value tiles of the two 32-token chunks (the STRATA tier tile layout), 512 b each
+ *   2048 b         key scales sc[2][128] fp16, key zeros lo[2][128] fp16
+ *   2048 b + 1024  value (scale | zero << 16) words per chunk [group 4][lane group 4][slot 8]
+ * Offset table: blk_bits (BH, nb) and blk_off (BH, nb) int32 units from bh_base[bh].
+ * kvq_mixed_encode: k, v (BH, nb*64, 128) of dtype, head stride x_bh; one workgroup per block.
+ * kvq_mixed_decode: seg (BH, 4) int64 = (bh_base, n8, n4, n2); every block visible; exact rows
+ * as kvq_kivi_decode's (dtype = q_dtype).  out (B, Tq, Hq, 128) of q_dtype.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_mixed_encode(const void* k, const void* v, int dtype, int64_t BH, int64_t nb, int64_t d, int64_t x_bh,
+                     const uint8_t* blk_bits, const int32_t* blk_off, const int64_t* bh_base, uint8_t* buf,
+                     void* stream);
+int64_t kvq_mixed_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t nb,
+                                   int64_t n_exact);
+int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B, int64_t Hq,
+                     int64_t Hkv, int64_t Tq, int64_t d, float scaling, const uint8_t* buf, const int64_t* seg,
+                     int64_t nb, const void* k_exact, const void* v_exact, int64_t cap_e, int64_t n_exact,
+                     const int64_t* exact_pos, const int64_t* q_pos, void* out, float* workspace,
+                     int64_t workspace_floats, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * A9  Blockwise token-axis DCT coding (no counterpart in the reference; the contract follows its
  * conventions: absmax_quant, STRATA_KV.py:549-554, and offset-binary 4-bit storage,
  * TILT_KV.py:2621-2625).  Per (b, h, 64-token block, channel): X_k = sum_n C[k][n] x_n for the

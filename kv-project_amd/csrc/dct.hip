@@ -25,6 +25,7 @@
 //   out_c += s^V_c (sum_k w_k code_kc - 7 sum_k w_k)  (w transposed through LDS against value codes)
 #include "common.hpp"
 #include "mfma_common.hpp"
+#include "partials.hpp"
 
 namespace kvq {
 namespace {
@@ -449,43 +450,9 @@ void dct_split(DctParams p) {
 }
 
 template <int R, int DT>
-__global__ __launch_bounds__(kDThreads) void dct_merge(DctParams p) {
+__global__ __launch_bounds__(kDThreads) void dct_merge(MergeArgs a) {
   extern __shared__ float smem[];
-  const int bh = blockIdx.x;
-  const int b = bh / p.Hkv, h = bh % p.Hkv;
-  float* stat = smem;                            // M[R], L[R]
-  if (threadIdx.x < R) {
-    const int r = threadIdx.x;
-    float M = -INFINITY, L = 0.0f;
-    for (int s = 0; s < p.S_ex; ++s) M = fmaxf(M, p.ex_m[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r]);
-    for (int s = 0; s < p.S_all; ++s) M = fmaxf(M, p.ws_m[(static_cast<int64_t>(bh) * p.S_all + s) * R + r]);
-    for (int s = 0; s < p.S_ex; ++s) {
-      const int64_t po = static_cast<int64_t>(bh) * p.S_ex + s;
-      if (p.ex_m[po * R + r] != -INFINITY) L += __builtin_amdgcn_exp2f(p.ex_m[po * R + r] - M) * p.ex_l[po * R + r];
-    }
-    for (int s = 0; s < p.S_all; ++s) {
-      const int64_t po = static_cast<int64_t>(bh) * p.S_all + s;
-      if (p.ws_m[po * R + r] != -INFINITY) L += __builtin_amdgcn_exp2f(p.ws_m[po * R + r] - M) * p.ws_l[po * R + r];
-    }
-    stat[r] = M;
-    stat[R + r] = L;
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < p.R_real * kDD; idx += kDThreads) {
-    const int r = idx / kDD, c = idx % kDD;
-    const float M = stat[r];
-    float O = 0.0f;
-    for (int s = 0; s < p.S_ex; ++s) {
-      const int64_t po = static_cast<int64_t>(bh) * p.S_ex + s;
-      if (p.ex_m[po * R + r] != -INFINITY) O += __builtin_amdgcn_exp2f(p.ex_m[po * R + r] - M) * p.ex_o[(po * R + r) * kDD + c];
-    }
-    for (int s = 0; s < p.S_all; ++s) {
-      const int64_t po = static_cast<int64_t>(bh) * p.S_all + s;
-      if (p.ws_m[po * R + r] != -INFINITY) O += __builtin_amdgcn_exp2f(p.ws_m[po * R + r] - M) * p.ws_o[(po * R + r) * kDD + c];
-    }
-    const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
-    store_from_f32<DT>(p.out, ((static_cast<int64_t>(b) * p.Tq + t) * p.Hq + hq) * kDD + c, O / stat[R + r]);
-  }
+  merge_partials<R, DT, kDD>(a, blockIdx.x, smem);
 }
 
 inline int dct_pow2(int64_t r) {
@@ -625,7 +592,9 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
     KVQ_LAUNCH_CHECK("kvq_dct_decode(split)");
   }
   const size_t msmem = 2 * R * sizeof(float);
-#define KVQ_DCT_MERGE(R_, DT_) hipLaunchKernelGGL((dct_merge<R_, DT_>), dim3(p.BH), dim3(kDThreads), msmem, s, p)
+  MergeArgs ma{p.ws_o, p.ws_m, p.ws_l, p.S_all, p.ex_o, p.ex_m, p.ex_l, p.S_ex,
+               p.Hq, p.Hkv, p.Tq, p.rep, p.R_real, p.out};
+#define KVQ_DCT_MERGE(R_, DT_) hipLaunchKernelGGL((dct_merge<R_, DT_>), dim3(p.BH), dim3(kDThreads), msmem, s, ma)
 #define KVQ_DCT_MR(DT_)                                  \
   switch (R) {                                           \
     case 1: KVQ_DCT_MERGE(1, DT_); break;                \

@@ -13,6 +13,7 @@
 //   code: clamp(rint(y / s + (2^b - 1) / 2), 0, 2^b - 1) with IEEE float32 division and add.
 #include "common.hpp"
 #include "mfma_common.hpp"
+#include "widths.hpp"
 
 namespace kvq {
 namespace {
@@ -142,12 +143,6 @@ __global__ __launch_bounds__(256) void strata_quantize_kernel(const float* __res
   if (lane == 0) scales[oi] = f32_to_f16(s);
 }
 
-// token of slot j of lane group g within a 32-token chunk (the order the decode's logits arrive in)
-__device__ __forceinline__ int slot_token(int g, int j) { return 16 * (j >> 2) + 4 * g + (j & 3); }
-
-__device__ __constant__ int kSlotOfNibble4[8] = {0, 2, 4, 6, 1, 3, 5, 7};
-__device__ __constant__ int kSlotOfByte8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-
 // Value tiles of one width from planar rows: one thread per 32-bit tile word.
 //   4 bits: word (blk/4)*256 + l*4 + blk%4 of a 2 KiB chunk; nibble k holds slot kSlotOfNibble4[k]
 //   8 bits: word (blk/2)*256 + l*4 + (blk%2)*2 + w of a 4 KiB chunk; byte k of the lane's 8 holds
@@ -165,28 +160,11 @@ __global__ void strata_vtile_kernel(const uint8_t* __restrict__ rows, int64_t n,
   const int64_t bh = chunk_all / nchunk, chunk = chunk_all % nchunk;
   const int row_bytes = kSD * bits / 8;
   const uint8_t* base = rows + bh * rows_bh;
-  uint32_t word = 0;
   auto code_at = [&](int slot, int g, int channel) -> uint32_t {
     const int64_t t = chunk * 32 + slot_token(g, slot);
     return t < n ? static_cast<uint32_t>(planar_code(base + t * row_bytes, channel, bits)) : 0u;
   };
-  if (bits == 4) {
-    const int blk = (w / 256) * 4 + (w % 4), l = (w % 256) / 4;
-    const int g = l / 16, ch = 16 * blk + (l % 16);
-    for (int k = 0; k < 8; ++k) word |= code_at(kSlotOfNibble4[k], g, ch) << (4 * k);
-  } else if (bits == 8) {
-    const int blk = (w / 256) * 2 + ((w % 4) / 2), l = (w % 256) / 4, half = w % 2;
-    const int g = l / 16, ch = 16 * blk + (l % 16);
-    for (int k = 0; k < 4; ++k) word |= code_at(kSlotOfByte8[4 * half + k], g, ch) << (8 * k);
-  } else {
-    const int l = w / 4, bp = w % 4;
-    const int g = l / 16;
-    for (int k = 0; k < 16; ++k) {
-      const int blk = 2 * bp + ((k >> 2) & 1), slot = 2 * (k & 3) + (k >> 3);
-      word |= code_at(slot, g, 16 * blk + (l % 16)) << (2 * k);
-    }
-  }
-  tiles[wi] = word;
+  tiles[wi] = vtile_word(bits, w, code_at);
 }
 
 // Per-token scales in slot order: vsl[bh][chunk][8g + j] = vs[bh][token slot_token(g, j)].
@@ -331,40 +309,6 @@ struct StrataParams {
 __device__ __forceinline__ int64_t strata_q_offset(const StrataParams& p, int b, int h, int r) {
   const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
   return static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq) * p.q_sh + static_cast<int64_t>(t) * p.q_st;
-}
-
-// Key operand element e of k-step w for lane group g: the channel it multiplies and log2 of the
-// factor its code carries (its position within the 16-bit half).
-template <int BITS>
-__device__ __forceinline__ int key_channel(int g, int w, int e) {
-  if constexpr (BITS == 4) {
-    const int byte = 16 * g + 4 * w + ((e >> 2) & 1) + 2 * (e & 1);
-    return ((e >> 1) & 1) ? 64 + byte : byte;
-  } else if constexpr (BITS == 8) {
-    constexpr int kOff[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-    return 32 * g + 8 * w + kOff[e];
-  } else {
-    return 32 * (e >> 1) + 8 * g + 4 * (w >> 1) + 2 * (e & 1) + (w & 1);
-  }
-}
-template <int BITS>
-__device__ __forceinline__ int code_shift(int e) {
-  if constexpr (BITS == 4) return ((e >> 1) & 1) ? 4 : 0;
-  else if constexpr (BITS == 8) return 0;
-  else return 2 * (e >> 1);
-}
-template <int BITS>
-constexpr int smax_shift() { return BITS == 4 ? 4 : (BITS == 8 ? 0 : 6); }
-
-__device__ __forceinline__ half8 unpack4(uint32_t w) {
-  const uint32_t w8 = w >> 8;
-  return as_half8(u32x4{w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u});
-}
-__device__ __forceinline__ half8 unpack8(uint32_t w0, uint32_t w1) {
-  return as_half8(u32x4{w0 & 0x00FF00FFu, (w0 >> 8) & 0x00FF00FFu, w1 & 0x00FF00FFu, (w1 >> 8) & 0x00FF00FFu});
-}
-__device__ __forceinline__ half8 unpack2(uint32_t x) {
-  return as_half8(u32x4{x & 0x00030003u, x & 0x000C000Cu, x & 0x00300030u, x & 0x00C000C0u});
 }
 
 template <int BITS>

@@ -12,6 +12,7 @@ from .evict import gather_dequant, retained_cache, topk_retain
 from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strata_center_rotate, strata_decode,
                      strata_quantize, strata_v_tile, strata_workspace_floats, uniform_step, unpack_planar)
 from .dct import DctCache, dct_decode, dct_encode, dct_table, dct_workspace_floats
+from .mixed import MixedKIVICache, c3_widths, mixed_decode, mixed_workspace_floats, offset_table
 
 __all__ = [
     "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes",
@@ -20,5 +21,5 @@ __all__ = [
     "gather_dequant", "retained_cache", "topk_retain", "pack_planar", "unpack_planar", "rotation_signs",
     "uniform_step", "strata_center_rotate", "strata_quantize", "strata_v_tile", "StrataCache", "StrataTier",
     "strata_decode", "strata_workspace_floats", "DctCache", "dct_decode", "dct_encode", "dct_table",
-    "dct_workspace_floats",
+    "dct_workspace_floats", "MixedKIVICache", "c3_widths", "mixed_decode", "mixed_workspace_floats", "offset_table",
 ]

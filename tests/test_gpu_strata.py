@@ -12,6 +12,7 @@ import pytest
 import torch
 
 import oracle.strata as os_
+from layouts import slot_token as _slot_token, tile_codes as _tile_codes
 
 pytestmark = pytest.mark.gpu
 
@@ -50,32 +51,6 @@ def test_center_rotate_and_quantize_bit_exact(dtype):
         want = os_.pack_planar(np.take_along_axis(c_o, ii[..., None], 1), bits)
         np.testing.assert_array_equal(cg.cpu().numpy().reshape(B * H, 50, -1), want)
         np.testing.assert_array_equal(sg.float().cpu().numpy().reshape(B * H, 50), np.take_along_axis(s_o, ii, 1))
-
-
-def _slot_token(g, j):
-    return 16 * (j >> 2) + 4 * g + (j & 3)
-
-
-def _tile_codes(tiles: np.ndarray, bits: int) -> np.ndarray:
-    """Read a chunk's tile words back to codes[token 0..31][channel 0..127] by the documented layout."""
-    words = tiles.view(np.uint32)
-    out = np.full((32, 128), -1, np.int64)
-    slot4, slot8 = [0, 2, 4, 6, 1, 3, 5, 7], [0, 2, 1, 3, 4, 6, 5, 7]
-    for w, word in enumerate(words.tolist()):
-        if bits == 4:
-            blk, l = (w // 256) * 4 + w % 4, (w % 256) // 4
-            for k in range(8):
-                out[_slot_token(l // 16, slot4[k]), 16 * blk + l % 16] = (word >> (4 * k)) & 15
-        elif bits == 8:
-            blk, l, half = (w // 256) * 2 + (w % 4) // 2, (w % 256) // 4, w % 2
-            for k in range(4):
-                out[_slot_token(l // 16, slot8[4 * half + k]), 16 * blk + l % 16] = (word >> (8 * k)) & 255
-        else:
-            l, bp = w // 4, w % 4
-            for k in range(16):
-                blk, slot = 2 * bp + ((k >> 2) & 1), 2 * (k & 3) + (k >> 3)
-                out[_slot_token(l // 16, slot), 16 * blk + l % 16] = (word >> (2 * k)) & 3
-    return out
 
 
 @pytest.mark.parametrize("bits", [2, 4, 8])
