@@ -1,22 +1,33 @@
 #!/usr/bin/env python3
 """Packed-KV decode benchmark on one MI355X (BASELINE.json metric, configuration C2).
 
-One step = one decode step of attention for one Llama-3-8B-shaped layer: batch 16, 32 query
-heads, 8 KV heads, head_dim 128, 32768 cached tokens (32640 4-bit packed + 128 exact bf16
-rows), over the packed KIVI cache already resident in HBM.  Prints ONE JSON line.
+Default (``--workload c2``): one step = one decode step of attention for one Llama-3-8B-shaped
+layer: batch 16, 32 query heads, 8 KV heads, head_dim 128, 32768 cached tokens (32640 4-bit
+packed + 128 exact bf16 rows), over the packed KIVI cache already resident in HBM.  Prints ONE
+JSON line.
 
-Timing: the step is captured once in a HIP graph (the reference's _time_callable protocol,
-STRATA_KV.py:3424-3447); W untimed warm-up replays, then K replays between HIP events on the
-launch stream (device synchronisation on both sides).  The eager (uncaptured) step time is
-reported too.  The dominant kernel (the split-K decode kernel) is timed the same way on its own
-(phase 1 only) for the roofline figure.  The CPU baseline is the
-oracle's restatement of the reference decode (dequantise + chunked_attention in float32) on a
-bounded sample of (batch, KV head) pairs of the same cache, scaled to the whole layer.
+The other rows of the path are measured by the same script with ``--workload``:
+  c1      the fp32 CPU-runnable configuration (B=1, 8 heads, T=4096, groups of 32)
+  c3      mixed 2/4/8-bit 64-token blocks (B=8, Hq=32, Hkv=8, T=16384, group 32)
+  c4      eviction: 32 score-accumulating decode steps, top-k 2048 + 256 window, retained decode
+  c5      DCT-coded context (B=1, Hq=64, Hkv=8, T=131072): decode, and the encoder
+  append  streaming append of one token per sequence at the C2 shape (µs/step)
+  quant   prefill quantise + pack of the C2 context (kivi_quant of K and V)
+Each prints one JSON line of the same form (its own metric, roofline and CPU baseline).
+
+Timing: W untimed warm-up steps, then K steps launched back to back between HIP events on the
+launch stream (device synchronisation on both sides).  The same step captured once in a HIP graph
+(the reference's _time_callable protocol, STRATA_KV.py:3424-3447) is timed too and reported as
+``graph_us``: on this ROCm stack graph replays of these launches measure slower than the eager
+launches.  The dominant kernel is timed the same way on its own for the roofline figure; its
+rocprofv3 kernel-trace average is committed beside the summaries.  The CPU baseline is the oracle's restatement of the
+reference path on a bounded sample of the same workload, scaled to the whole workload.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -26,6 +37,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "kv-project_amd"))
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E peak
+
+
+def log(m: str) -> None:
+    print(f"[bench] {m}", file=sys.stderr, flush=True)
 
 
 def _events_ms(fn, reps: int) -> float:
@@ -40,15 +55,85 @@ def _events_ms(fn, reps: int) -> float:
     return a.elapsed_time(b) / reps
 
 
-def cpu_baseline(q, K, V, shape, bytes_alg, seconds: float) -> dict:
+def graph_of(fn):
+    """Capture fn once in a HIP graph (as the reference's _time_callable, STRATA_KV.py:3424-3447)."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        fn()
+    return gr
+
+
+def graph_ms(fn, steps: int, warmup: int) -> float:
+    g = graph_of(fn)
+    for _ in range(warmup):
+        g.replay()
+    return _events_ms(g.replay, steps)
+
+
+def eager_ms(fn, steps: int, warmup: int) -> float:
+    """Back-to-back launches on the current stream between HIP events, after warm-up."""
+    for _ in range(warmup):
+        fn()
+    return _events_ms(fn, steps)
+
+
+def step_ms(fn, steps: int, warmup: int):
+    """(eager ms, graph-replay ms) of one step.  Eager launches are the figure reported: on this
+    ROCm stack a graph replay of these launches measures slower than the same launches issued
+    back to back (an extra ~5-20 us per replay), so the graph time is kept as a second figure."""
+    e = eager_ms(fn, steps, warmup)
+    g = graph_ms(fn, steps, warmup)
+    return e, g
+
+
+def _threads() -> int:
+    from threadpoolctl import threadpool_info
+    return int(max([x.get("num_threads", 1) for x in threadpool_info()] or [1]))
+
+
+def _result(args, *, metric, value, unit, ms_per_step, workload, config, dtype, roofline, hib=True, **extra):
+    res = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": hib,
+           "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic",
+           "config": {"workload": workload, **config}}
+    res.update(extra)
+    res["roofline"] = roofline
+    res["cpu_baseline"] = None
+    return res
+
+
+def _roof(bytes_alg: int, ms: float, kernel: str, traffic=None) -> dict:
+    achieved = bytes_alg / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
+            "kernel_us": round(ms * 1e3, 3), "kernel_bytes_alg": int(bytes_alg)}
+
+
+def _traffic(name: str):
+    tf = ROOT / "profiles" / name
+    if tf.exists():
+        return json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+    return None
+
+
+# ---------------------------------------------------------------------------------------------
+# C2 (default) and C1: packed 4-bit KIVI decode
+
+def cpu_kivi_decode(q, K, V, window, bits, group_k, group_v, bytes_alg, seconds: float) -> dict:
     """Oracle decode (kivi dequantisation + chunked_attention, float32) on whole (b, h) pairs."""
     import numpy as np
-    from threadpoolctl import threadpool_info
     from oracle.attention import chunked_attention
     from oracle.kivi import kivi_dequant, kivi_quant
     B, Hkv, T, d = K.shape
     rep = q.shape[1] // Hkv
-    W = shape.window
+    W = window
     n_q = T - W
     scaling = d ** -0.5
     times = []
@@ -57,12 +142,11 @@ def cpu_baseline(q, K, V, shape, bytes_alg, seconds: float) -> dict:
         Kbh = K[b:b + 1, h:h + 1].float().cpu().numpy()
         Vbh = V[b:b + 1, h:h + 1].float().cpu().numpy()
         qbh = q[b:b + 1, h * rep:(h + 1) * rep].float().cpu().numpy()
-        kq = kivi_quant(Kbh, shape.bits, shape.group_k, True, 0)          # compression: not timed
-        vq = kivi_quant(Vbh, shape.bits, shape.group_v, False, 0)
+        kq = kivi_quant(Kbh, bits, group_k, True, 0)          # compression: not timed
+        vq = kivi_quant(Vbh, bits, group_v, False, 0)
         t0 = time.perf_counter()
-        kh = kivi_dequant(kq["codes"], kq["lo"], kq["scale"], shape.group_k, True)[:, :, :n_q]
-        vh = kivi_dequant(vq["codes"][:, :, :n_q], vq["lo"][:, :, :n_q], vq["scale"][:, :, :n_q],
-                          shape.group_v, False)
+        kh = kivi_dequant(kq["codes"], kq["lo"], kq["scale"], group_k, True)[:, :, :n_q]
+        vh = kivi_dequant(vq["codes"][:, :, :n_q], vq["lo"][:, :, :n_q], vq["scale"][:, :, :n_q], group_v, False)
         tok = {"k": kh, "v": vh, "b": np.zeros((1, 1, n_q), np.float32), "tau": np.full(n_q, -1)}
         chunked_attention(qbh, scaling, np.array([T]), Kbh[:, :, n_q:], Vbh[:, :, n_q:], np.arange(W),
                           np.full(W, 1 << 40), tok, dtype=np.float32)
@@ -71,45 +155,18 @@ def cpu_baseline(q, K, V, shape, bytes_alg, seconds: float) -> dict:
             break
     per_pair = float(np.median(times))
     t_layer = per_pair * len(pairs)
-    threads = max([x.get("num_threads", 1) for x in threadpool_info()] or [1])
-    return {"value": bytes_alg / t_layer / 1e9, "unit": "GB/s", "cores": int(threads), "kind": "port",
+    return {"value": bytes_alg / t_layer / 1e9, "unit": "GB/s", "cores": _threads(), "kind": "port",
             "us_per_layer": t_layer * 1e6,
             "sample": f"{len(times)} of {len(pairs)} (batch, KV-head) pairs at full context; "
                       f"median per pair x {len(pairs)}; numpy float32 dequantise + chunked_attention"}
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--split-tokens", type=int, default=0)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a plain 1 GiB device-to-device copy (profiler counter calibration)")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this path is single-GPU by design (multi-GPU sharding is "
-              "described in DESIGN.md, not launched); run with --gpus 1", file=sys.stderr)
-        return 2
+def run_kivi(args, shape_name: str) -> dict:
     import torch
     import kvq
-    from kvq.synth import C2, decode_inputs
-    torch.cuda.set_device(0)
-    if args.copy_calibration:
-        # a copy of known size: FETCH_SIZE / WRITE_SIZE per dispatch of this kernel against the
-        # 1 GiB it must read and write gives the counters' scale on this device
-        src = torch.ones((1 << 28,), dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(args.steps):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": args.steps}), flush=True)
-        return 0
-    shape = C2
-    log = lambda m: print(f"[bench] {m}", file=sys.stderr, flush=True)
-    log("generating C2 inputs on the GPU")
+    from kvq.synth import C1, C2, decode_inputs
+    shape = C2 if shape_name == "c2" else C1
+    log(f"generating {shape.name} inputs on the GPU")
     q, K, V = decode_inputs(shape, device="cuda")
     log("quantising and packing the cache")
     cache = kvq.PackedKIVICache.from_context(K, V, window=shape.window, group_k=shape.group_k,
@@ -123,71 +180,405 @@ def main() -> int:
     def step():
         kvq.kivi_decode(q, scaling, cache, out=out, workspace=ws, split_tokens=args.split_tokens)
 
-
     def split_only():
         kvq.kivi_decode(q, scaling, cache, out=out, workspace=ws, split_tokens=args.split_tokens, phases=1)
 
-    def graph_of(fn):
-        """Capture fn once in a HIP graph (as the reference's _time_callable, STRATA_KV.py:3424-3447)."""
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(3):
-                fn()
-        torch.cuda.current_stream().wait_stream(side)
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
-            fn()
-        return gr
-
     log("timing")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    eager_ms = _events_ms(step, args.steps)
-    g_step, g_split = graph_of(step), graph_of(split_only)
-    for _ in range(args.warmup):
-        g_step.replay()
-    ms_per_step = _events_ms(g_step.replay, args.steps)
-    for _ in range(args.warmup):
-        g_split.replay()
-    split_ms = _events_ms(g_split.replay, args.steps)
-
+    ms_per_step, g_ms = step_ms(step, args.steps, args.warmup)
+    split_ms = eager_ms(split_only, args.steps, args.warmup)
     io_bytes = q.numel() * q.element_size() + out.numel() * out.element_size()
     bytes_alg = cache.payload_bytes() + io_bytes
     # the split kernel reads the packed rows, the exact rows and q; the output belongs to the merge
     split_bytes = cache.payload_bytes() + q.numel() * q.element_size()
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
-    achieved = split_bytes / (split_ms * 1e-3) / 1e9
-    traffic = None
-    tf = ROOT / "profiles" / "traffic_kivi_decode_split_c2.json"
-    if tf.exists():
-        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-    res = {
-        "metric": "packed-KV decode: effective HBM GB/s + µs/layer, 8B-shape 32k ctx b16",
-        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "C2: one decode step of one Llama-3-8B-shaped layer over a 4-bit KIVI "
-                               "cache (B=16, Hq=32, Hkv=8, d=128, T=32768 = 32640 packed + 128 exact)",
-                   "global_batch": shape.B, "seq_len": shape.T, "parallelism": "single GPU",
-                   "group_k": shape.group_k, "group_v": shape.group_v, "bits": shape.bits,
-                   "split_tokens": args.split_tokens},
-        "us_per_layer": round(ms_per_step * 1e3, 3),
-        "timer": "HIP graph replay, HIP events over the timed steps",
-        "eager_us_per_layer": round(eager_ms * 1e3, 3),
-        "bytes_alg": bytes_alg,
-        "packed_code_GBs": round(2 * shape.B * shape.Hkv * cache.n_q * shape.d // 2 / (ms_per_step * 1e-3) / 1e9, 2),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "kivi_decode_split", "kernel_us": round(split_ms * 1e3, 3),
-                     "kernel_bytes_alg": split_bytes},
-        "cpu_baseline": None,
-    }
+    if shape.name == "C2":
+        metric = "packed-KV decode: effective HBM GB/s + µs/layer, 8B-shape 32k ctx b16"
+        workload = ("C2: one decode step of one Llama-3-8B-shaped layer over a 4-bit KIVI cache (B=16, Hq=32, "
+                    "Hkv=8, d=128, T=32768 = 32640 packed + 128 exact)")
+        traffic = _traffic("traffic_kivi_decode_split_c2.json")
+    else:
+        metric = "packed-KV decode (C1, fp32): effective HBM GB/s + µs/layer"
+        workload = ("C1: one fp32 decode step (B=1, Hq=Hkv=8, d=128, T=4096 = 3968 packed + 128 exact, "
+                    "groups of 32)")
+        traffic = None
+    res = _result(args, metric=metric, value=value, unit="GB/s", ms_per_step=ms_per_step, workload=workload,
+                  config={"global_batch": shape.B, "seq_len": shape.T, "parallelism": "single GPU",
+                          "group_k": shape.group_k, "group_v": shape.group_v, "bits": shape.bits,
+                          "split_tokens": args.split_tokens},
+                  dtype="bf16" if shape.dtype == torch.bfloat16 else "fp32",
+                  roofline=_roof(split_bytes, split_ms, "kivi_decode_split", traffic),
+                  us_per_layer=round(ms_per_step * 1e3, 3),
+                  timer="back-to-back launches, HIP events over the timed steps",
+                  graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg,
+                  packed_code_GBs=round(2 * shape.B * shape.Hkv * cache.n_q * shape.d // 2 / (ms_per_step * 1e-3) / 1e9,
+                                        2))
     log(f"decode step {ms_per_step * 1e3:.1f} us, split kernel {split_ms * 1e3:.1f} us")
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        res["cpu_baseline"] = cpu_baseline(q, K, V, shape, bytes_alg, args.cpu_seconds)
+        res["cpu_baseline"] = cpu_kivi_decode(q, K, V, shape.window, shape.bits, shape.group_k, shape.group_v,
+                                              bytes_alg, args.cpu_seconds)
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+# C3: mixed-width blocks
+
+def run_c3(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    from kvq.synth import C3, c3_inputs
+    s = C3
+    log("generating C3 inputs")
+    q, K, V, imp = c3_inputs("cuda")
+    widths = kvq.c3_widths(imp)
+    cache = kvq.MixedKIVICache.from_context(K, V, widths, window=0)
+    scaling = s.d ** -0.5
+    out = torch.empty((s.B, 1, s.Hq, s.d), dtype=s.dtype, device="cuda")
+    ws = torch.empty((kvq.mixed_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.nb, 0),), dtype=torch.float32,
+                     device="cuda")
+    step = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws)
+    split = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
+    ms, g_ms = step_ms(step, args.steps, args.warmup)
+    split_ms = eager_ms(split, args.steps, args.warmup)
+    qb = q.numel() * q.element_size()
+    bytes_alg = cache.coded_bytes() + qb + out.numel() * out.element_size()
+    avg_bits = float(widths.float().mean())
+    res = _result(args, metric="mixed-width (2/4/8-bit block) decode: effective HBM GB/s + µs/layer",
+                  value=bytes_alg / (ms * 1e-3) / 1e9, unit="GB/s", ms_per_step=ms,
+                  workload="C3: one decode step over 64-token blocks of 2/4/8-bit KIVI codes (group 32), widths "
+                           "by LogNormal(0,1) block importance 10/30/60% (B=8, Hq=32, Hkv=8, d=128, T=16384)",
+                  config={"global_batch": s.B, "seq_len": s.T, "parallelism": "single GPU", "group": 32,
+                          "avg_bits": round(avg_bits, 4), "blocks_8_4_2": [int((widths == w).sum()) for w in (8, 4, 2)]},
+                  dtype="bf16", roofline=_roof(cache.coded_bytes() + qb, split_ms, "mixed_split"),
+                  us_per_layer=round(ms * 1e3, 3), graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg)
+    log(f"C3 step {ms * 1e3:.1f} us, split {split_ms * 1e3:.1f} us")
+    if not args.no_cpu_baseline:
+        from oracle.mixed import dequant_blocks, mixed_decode, mixed_quant
+        pairs = [(b, h) for b in range(s.B) for h in range(s.Hkv)]
+        times = []
+        rep = s.Hq // s.Hkv
+        for b, h in pairs:
+            Kb = K[b:b + 1, h:h + 1].float().cpu().numpy()
+            Vb = V[b:b + 1, h:h + 1].float().cpu().numpy()
+            m = mixed_quant(Kb, Vb, widths[b:b + 1, h:h + 1].cpu().numpy())          # compression: not timed
+            qb_ = q[b:b + 1, h * rep:(h + 1) * rep].float().cpu().numpy()
+            t0 = time.perf_counter()
+            xk, xv = dequant_blocks(m["kc"], m["k_lo"], m["k_sc"], m["vc"], m["v_lo"], m["v_sc"])
+            mixed_decode(qb_, scaling, xk, xv)
+            times.append(time.perf_counter() - t0)
+            if sum(times) >= args.cpu_seconds and len(times) >= 2:
+                break
+        t = float(np.median(times)) * len(pairs)
+        res["cpu_baseline"] = {"value": bytes_alg / t / 1e9, "unit": "GB/s", "cores": _threads(), "kind": "port",
+                               "us_per_layer": t * 1e6,
+                               "sample": f"{len(times)} of {len(pairs)} (batch, KV-head) pairs; median per pair x "
+                                         f"{len(pairs)}; numpy per-block dequantise + chunked_attention"}
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+# C5: DCT-coded context
+
+def run_c5(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    from kvq.synth import C5, c5_inputs
+    s = C5
+    log("generating C5 inputs (AR(1) series)")
+    q, K, V = c5_inputs("cuda")
+    cache = kvq.DctCache.from_context(K, V, window=0)
+    scaling = s.d ** -0.5
+    out = torch.empty((s.B, 1, s.Hq, s.d), dtype=s.dtype, device="cuda")
+    ws = torch.empty((kvq.dct_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.T, 0),), dtype=torch.float32,
+                     device="cuda")
+    step = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws)
+    split = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
+    ms, g_ms = step_ms(step, args.steps, args.warmup)
+    split_ms = eager_ms(split, args.steps, args.warmup)
+    # the encoder: keys and values of the whole context, one launch each
+    kc, ks = torch.empty_like(cache.kc), torch.empty_like(cache.ks)
+    ctab = kvq.dct_table()
+    from kvq import _lib
+
+    def enc():
+        for x, fv in ((K, 0), (V, 1)):
+            _lib.call("kvq_dct_encode", x.data_ptr(), _lib.DTYPE_CODE[x.dtype], s.B * s.Hkv, s.T, s.d, s.T * s.d,
+                      ctab.data_ptr(), fv, kc.data_ptr(), ks.data_ptr(), _lib.stream_of(x))
+    enc_ms = eager_ms(enc, max(5, args.steps // 5), 2)
+    enc_bytes = 2 * (K.numel() * K.element_size() + kc.numel() + ks.numel() * 2)
+    qb = q.numel() * q.element_size()
+    bytes_alg = cache.coded_bytes() + qb + out.numel() * out.element_size()
+    dense = 2 * K.numel() * K.element_size()
+    res = _result(args, metric="DCT-coded decode: effective HBM GB/s + µs/layer, 70B-shape 131k ctx",
+                  value=bytes_alg / (ms * 1e-3) / 1e9, unit="GB/s", ms_per_step=ms,
+                  workload="C5: one decode step over a blockwise-DCT-coded context (16 of 64 coefficients, 4-bit "
+                           "absmax, fp16 scales; B=1, Hq=64, Hkv=8, d=128, T=131072, AR(1) rho=0.95 + N(0,0.1))",
+                  config={"global_batch": s.B, "seq_len": s.T, "parallelism": "single GPU", "keep": 16, "block": 64},
+                  dtype="bf16", roofline=_roof(cache.coded_bytes() + qb, split_ms, "dct_split"),
+                  us_per_layer=round(ms * 1e3, 3), graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg,
+                  compression_vs_bf16=round(dense / cache.coded_bytes(), 3),
+                  encoder={"us": round(enc_ms * 1e3, 3), "bytes": enc_bytes,
+                           "GBs": round(enc_bytes / (enc_ms * 1e-3) / 1e9, 2),
+                           "frac": round(enc_bytes / (enc_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    log(f"C5 step {ms * 1e3:.1f} us, split {split_ms * 1e3:.1f} us, encode {enc_ms * 1e3:.1f} us")
+    if not args.no_cpu_baseline:
+        from oracle.dct import dct_decode, dct_encode
+        times = []
+        rep = s.Hq // s.Hkv
+        for h in range(s.Hkv):
+            Kh = K[:, h:h + 1].float().cpu().numpy().reshape(1, s.T, s.d)
+            Vh = V[:, h:h + 1].float().cpu().numpy().reshape(1, s.T, s.d)
+            kc_, ks_, _ = dct_encode(Kh)                                            # compression: not timed
+            vc_, vs_, _ = dct_encode(Vh)
+            qh = q[:, h * rep:(h + 1) * rep].float().cpu().numpy()
+            t0 = time.perf_counter()
+            dct_decode(qh, scaling, kc_, ks_, vc_, vs_)
+            times.append(time.perf_counter() - t0)
+            if sum(times) >= args.cpu_seconds and len(times) >= 1:
+                break
+        t = float(np.median(times)) * s.Hkv
+        res["cpu_baseline"] = {"value": bytes_alg / t / 1e9, "unit": "GB/s", "cores": _threads(), "kind": "port",
+                               "us_per_layer": t * 1e6,
+                               "sample": f"{len(times)} of {s.Hkv} KV heads; median per head x {s.Hkv}; numpy IDCT "
+                                         f"reconstruction + chunked_attention (float64)"}
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+# C4: eviction
+
+def run_c4(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    from kvq.synth import C4, C4_GROUP, C4_KEEP, C4_STEPS, C4_WINDOW, c4_inputs
+    s = C4
+    log("generating C4 inputs")
+    qs, K, V = c4_inputs("cuda")
+    cache = kvq.PackedKIVICache.from_context(K, V, window=C4_WINDOW, group_k=C4_GROUP, group_v=C4_GROUP)
+    scaling = s.d ** -0.5
+    out = torch.empty((s.B, 1, s.Hq, s.d), dtype=s.dtype, device="cuda")
+    ws = torch.empty((kvq.workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.n_q, cache.n_exact, C4_GROUP, C4_GROUP),),
+                     dtype=torch.float32, device="cuda")
+    scores = torch.zeros((s.B, s.Hkv, cache.n_q), dtype=torch.float32, device="cuda")
+    rep = s.Hq // s.Hkv
+    wgt = 1.0 / (rep * C4_STEPS)
+    q0 = qs[0]
+    plain = lambda: kvq.kivi_decode(q0, scaling, cache, out=out, workspace=ws)
+    scored = lambda: kvq.kivi_decode(q0, scaling, cache, out=out, workspace=ws, scores=scores, score_weight=wgt)
+    score_only = lambda: kvq.kivi_decode(q0, scaling, cache, out=out, workspace=ws, scores=scores,
+                                         score_weight=wgt, phases=4)
+    plain_ms = eager_ms(plain, args.steps, args.warmup)
+    scored_ms, g_ms = step_ms(scored, args.steps, args.warmup)
+    plain()
+    score_ms = eager_ms(score_only, args.steps, args.warmup)
+    # the eviction workload proper: 32 scored decode steps, top-k, gather, decode over the kept rows
+    scores.zero_()
+    torch.cuda.synchronize()
+    for t in range(C4_STEPS):
+        kvq.kivi_decode(qs[t], scaling, cache, out=out, workspace=ws, scores=scores, score_weight=wgt)
+    topk = lambda: kvq.topk_retain(scores, C4_KEEP)
+    topk_ms = eager_ms(topk, args.steps, args.warmup)
+    idx = kvq.topk_retain(scores, C4_KEEP)
+    kept = kvq.retained_cache(cache, idx)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        kvq.retained_cache(cache, idx)
+    torch.cuda.synchronize()
+    gather_ms = (time.perf_counter() - t0) * 1e3 / 5
+    out_k = torch.empty_like(out)
+    ws_k = torch.empty((kvq.workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, kept.n_q, kept.n_exact, C4_GROUP, C4_GROUP),),
+                       dtype=torch.float32, device="cuda")
+    kept_dec = lambda: kvq.kivi_decode(q0, scaling, kept, out=out_k, workspace=ws_k)
+    kept_ms = eager_ms(kept_dec, args.steps, args.warmup)
+    n_q, BH = cache.n_q, s.B * s.Hkv
+    kbytes = BH * n_q * (s.d // 2) + BH * (n_q // C4_GROUP) * s.d * 4
+    score_bytes = kbytes + 2 * BH * n_q * 4 + q0.numel() * q0.element_size()
+    ep_ms = C4_STEPS * scored_ms + topk_ms + gather_ms
+    res = _result(args, metric="eviction decode step: score-accumulating decode µs/layer (C4)",
+                  value=scored_ms * 1e3, unit="us", ms_per_step=scored_ms, hib=False,
+                  workload="C4: one score-accumulating decode step (decode + probability accumulation per KV head) "
+                           "over a 4-bit KIVI cache (B=4, Hq=32, Hkv=8, d=128, T=65536 = 65280 packed + 256 exact, "
+                           "group 64; 1% of keys +3); then top-k 2048 and the retained decode",
+                  config={"global_batch": s.B, "seq_len": s.T, "parallelism": "single GPU", "keep": C4_KEEP,
+                          "window": C4_WINDOW, "steps": C4_STEPS, "group": C4_GROUP},
+                  dtype="bf16", roofline=_roof(score_bytes, score_ms, "kivi_score_split"),
+                  graph_us=round(g_ms * 1e3, 3), plain_decode_us=round(plain_ms * 1e3, 3), score_pass_us=round(score_ms * 1e3, 3),
+                  topk_us=round(topk_ms * 1e3, 3), gather_us_host_timed=round(gather_ms * 1e3, 3),
+                  retained_decode_us=round(kept_ms * 1e3, 3),
+                  episode_ms=round(ep_ms, 4),
+                  decode_GBs=round((cache.payload_bytes() + 2 * q0.numel() * 2) / (plain_ms * 1e-3) / 1e9, 2))
+    log(f"C4 scored step {scored_ms * 1e3:.1f} us (plain {plain_ms * 1e3:.1f}, score pass {score_ms * 1e3:.1f}), "
+        f"top-k {topk_ms * 1e3:.1f} us, retained decode {kept_ms * 1e3:.1f} us")
+    if not args.no_cpu_baseline:
+        from oracle.evict import accumulate_decode_scores, decode_step_probs, topk_retain
+        from oracle.kivi import kivi_dequant, kivi_quant
+        pairs = [(b, h) for b in range(s.B) for h in range(s.Hkv)]
+        times = []
+        for b, h in pairs:
+            Kb = K[b:b + 1, h:h + 1].float().cpu().numpy()
+            kq = kivi_quant(Kb, 4, C4_GROUP, True, 0)                               # compression: not timed
+            qb = qs[0, b:b + 1, h * rep:(h + 1) * rep].float().cpu().numpy()
+            t0 = time.perf_counter()
+            kh = kivi_dequant(kq["codes"], kq["lo"], kq["scale"], C4_GROUP, True)[:, :, :n_q]
+            p = decode_step_probs(qb, scaling, kh, Kb[:, :, n_q:])
+            sc = accumulate_decode_scores(np.zeros((1, 1, n_q)), p, wgt)
+            topk_retain(sc, C4_KEEP)
+            times.append(time.perf_counter() - t0)
+            if sum(times) >= args.cpu_seconds and len(times) >= 2:
+                break
+        t = float(np.median(times)) * len(pairs)
+        res["cpu_baseline"] = {"value": t * 1e6, "unit": "us", "cores": _threads(), "kind": "port",
+                               "sample": f"{len(times)} of {len(pairs)} (batch, KV-head) pairs; one scored step "
+                                         f"(dequantise keys, softmax probabilities, accumulate) + top-k per pair, "
+                                         f"median x {len(pairs)}"}
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+# A2: streaming append, A1: prefill quantisation
+
+def run_append(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    from kvq.synth import C2, decode_inputs
+    s = C2
+    n_steps = 64 * max(1, args.steps // 64)
+    log("building a ring cache at the C2 shape")
+    q, K, V = decode_inputs(s, device="cuda", T=s.T - n_steps - 64)
+    cache = kvq.PackedKIVICache.from_context(K, V, window=s.window, group_k=s.group_k, group_v=s.group_v,
+                                             extra_tokens=n_steps + 128, ring=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    newk = torch.randn((n_steps + 64, s.B, s.Hkv, 1, s.d), generator=g, device="cuda").to(s.dtype)
+    newv = torch.randn_like(newk)
+    for t in range(64):                                   # warm-up, not timed
+        cache.append(newk[t], newv[t])
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for t in range(n_steps):
+        cache.append(newk[64 + t], newv[64 + t])
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / n_steps
+    # per step and (b, h): write the new K and V rows, read the value row leaving the window and
+    # write its codes and (scale, zero) pairs; per 64 steps: read the key group, write its codes
+    # and per-channel (scale, zero)
+    BH, d = s.B * s.Hkv, s.d
+    step_bytes = BH * (2 * d * 2 + d * 2 + d // 2 + (d // s.group_v) * 4) + \
+        BH * (s.group_k * d * 2 + s.group_k * d // 2 + d * 4) // s.group_k
+    res = _result(args, metric="streaming append (quantise + pack one token per sequence): µs/step",
+                  value=us, unit="us", ms_per_step=us * 1e-3, hib=False,
+                  workload="A2 at the C2 shape: one appended bf16 token per (b, KV head) per step (B=16, Hkv=8, "
+                           "d=128), the token leaving the 128-row window quantised into the packed cache, a key group "
+                           "of 64 flushed every 64 steps; mean over whole flush periods, eager launches",
+                  config={"global_batch": s.B, "seq_len": s.T, "parallelism": "single GPU", "steps_timed": n_steps},
+                  dtype="bf16", roofline=_roof(step_bytes, us * 1e-3, "kivi_append"), us_per_step=round(us, 3))
+    log(f"append {us:.2f} us/step")
+    if not args.no_cpu_baseline:
+        from oracle.kivi import kivi_quant
+        Kc = newk[:64].float().cpu().numpy().transpose(1, 2, 0, 3, 4).reshape(s.B, s.Hkv, 64, s.d)
+        Vc = newv[:64].float().cpu().numpy().transpose(1, 2, 0, 3, 4).reshape(s.B, s.Hkv, 64, s.d)
+        reps = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 5.0) or reps == 0:
+            for t in range(64):
+                kivi_quant(Vc[:, :, t:t + 1], 4, s.group_v, False, 0)
+            kivi_quant(Kc, 4, s.group_k, True, 0)
+            reps += 1
+        us_cpu = (time.perf_counter() - t0) / (64 * reps) * 1e6
+        res["cpu_baseline"] = {"value": us_cpu, "unit": "us", "cores": _threads(), "kind": "port",
+                               "sample": f"{reps} flush periods of 64 steps: numpy kivi_quant of each step's leaving "
+                                         f"value rows (B*Hkv) + one 64-token key group per period"}
+    return res
+
+
+def run_quant(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    from kvq.synth import C2, decode_inputs
+    s = C2
+    log("generating C2 inputs")
+    q, K, V = decode_inputs(s, device="cuda")
+    n = s.T - s.window
+    Kq, Vq = K[:, :, :n], V[:, :, :n]
+    kq = lambda: kvq.kivi_quant_stored(Kq, 4, s.group_k, True, 0)
+    vq = lambda: kvq.kivi_quant_stored(Vq, 4, s.group_v, False, 0)
+    k_ms = eager_ms(kq, max(5, args.steps // 5), 2)
+    v_ms = eager_ms(vq, max(5, args.steps // 5), 2)
+    xb = Kq.numel() * Kq.element_size()
+    k_bytes = xb + Kq.numel() // 2 + (n // s.group_k) * s.B * s.Hkv * s.d * 4
+    v_bytes = xb + Vq.numel() // 2 + n * s.B * s.Hkv * (s.d // s.group_v) * 4
+    ms = k_ms + v_ms
+    res = _result(args, metric="prefill KIVI quantise + pack (K and V of one C2 layer): effective GB/s",
+                  value=(k_bytes + v_bytes) / (ms * 1e-3) / 1e9, unit="GB/s", ms_per_step=ms,
+                  workload="A1 at the C2 shape: kivi_quant (4-bit, group 64) + MSB-first packing of the 32640 "
+                           "quantised rows of K (per channel) and V (per token), bf16 in, codes + fp16 metadata out",
+                  config={"global_batch": s.B, "seq_len": s.T, "parallelism": "single GPU", "group": s.group_k},
+                  dtype="bf16", roofline=_roof(k_bytes, k_ms, "kivi_quant_keys"),
+                  keys_us=round(k_ms * 1e3, 3), values_us=round(v_ms * 1e3, 3),
+                  values_GBs=round(v_bytes / (v_ms * 1e-3) / 1e9, 2))
+    log(f"quant keys {k_ms * 1e3:.1f} us, values {v_ms * 1e3:.1f} us")
+    if not args.no_cpu_baseline:
+        from oracle.kivi import kivi_quant
+        pairs = [(b, h) for b in range(s.B) for h in range(s.Hkv)]
+        times = []
+        for b, h in pairs:
+            Kb = Kq[b:b + 1, h:h + 1].float().cpu().numpy()
+            Vb = Vq[b:b + 1, h:h + 1].float().cpu().numpy()
+            t0 = time.perf_counter()
+            kivi_quant(Kb, 4, s.group_k, True, 0)
+            kivi_quant(Vb, 4, s.group_v, False, 0)
+            times.append(time.perf_counter() - t0)
+            if sum(times) >= args.cpu_seconds and len(times) >= 2:
+                break
+        t = float(np.median(times)) * len(pairs)
+        res["cpu_baseline"] = {"value": (k_bytes + v_bytes) / t / 1e9, "unit": "GB/s", "cores": _threads(),
+                               "kind": "port",
+                               "sample": f"{len(times)} of {len(pairs)} (batch, KV-head) pairs; numpy kivi_quant of "
+                                         f"K and V, median per pair x {len(pairs)}"}
+    return res
+
+
+WORKLOADS = {"c2": lambda a: run_kivi(a, "c2"), "c1": lambda a: run_kivi(a, "c1"), "c3": run_c3, "c4": run_c4,
+             "c5": run_c5, "append": run_append, "quant": run_quant}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (profiler counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this path is single-GPU by design (multi-GPU sharding is "
+              "described in DESIGN.md, not launched); run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+    torch.cuda.set_device(0)
+    if args.copy_calibration:
+        # a copy of known size: FETCH_SIZE / WRITE_SIZE per dispatch of this kernel against the
+        # 1 GiB it must read and write gives the counters' scale on this device
+        src = torch.ones((1 << 28,), dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": args.steps}), flush=True)
+        return 0
+    res = WORKLOADS[args.workload](args)
     print(json.dumps(res), flush=True)
     return 0
 

@@ -240,7 +240,8 @@ int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, in
  * Offset table: blk_bits (BH, nb) and blk_off (BH, nb) int32 units from bh_base[bh].
  * kvq_mixed_encode: k, v (BH, nb*64, 128) of dtype, head stride x_bh; one workgroup per block.
  * kvq_mixed_decode: seg (BH, 4) int64 = (bh_base, n8, n4, n2); every block visible; exact rows
- * as kvq_kivi_decode's (dtype = q_dtype).  out (B, Tq, Hq, 128) of q_dtype.
+ * as kvq_kivi_decode's (dtype = q_dtype).  out (B, Tq, Hq, 128) of q_dtype.  phases: 1 = the
+ * partials (exact rows and coded blocks) into the workspace, 2 = their merge into out, 3 = both.
  * ---------------------------------------------------------------------------------------- */
 int kvq_mixed_encode(const void* k, const void* v, int dtype, int64_t BH, int64_t nb, int64_t d, int64_t x_bh,
                      const uint8_t* blk_bits, const int32_t* blk_off, const int64_t* bh_base, uint8_t* buf,
@@ -251,7 +252,7 @@ int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      int64_t Hkv, int64_t Tq, int64_t d, float scaling, const uint8_t* buf, const int64_t* seg,
                      int64_t nb, const void* k_exact, const void* v_exact, int64_t cap_e, int64_t n_exact,
                      const int64_t* exact_pos, const int64_t* q_pos, void* out, float* workspace,
-                     int64_t workspace_floats, void* stream);
+                     int64_t workspace_floats, int phases, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * A9  Blockwise token-axis DCT coding (no counterpart in the reference; the contract follows its
@@ -273,7 +274,7 @@ int kvq_dct_encode(const void* x, int x_dtype, int64_t BH, int64_t T, int64_t d,
  * each (B*Hkv, T/64, ...)) plus n_exact exact rows (as kvq_kivi_decode's exact rows, dtype =
  * q_dtype): attention over the reconstructions x_n = sum_k C[k][n] s_k (code_k - 7), computed in
  * the coefficient domain (logits C^T (K-codes q), values (V-codes) (C p)).  out (B, Tq, Hq, d) of
- * q_dtype.  Workspace floats from kvq_dct_decode_workspace. */
+ * q_dtype.  Workspace floats from kvq_dct_decode_workspace.  phases as kvq_mixed_decode's. */
 int64_t kvq_dct_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t T,
                                  int64_t n_exact);
 int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B, int64_t Hq,
@@ -281,7 +282,7 @@ int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64
                    const uint8_t* kc, const uint16_t* ks, const uint8_t* vc, const uint16_t* vs,
                    const void* k_exact, const void* v_exact, int64_t cap_e, int64_t n_exact,
                    const int64_t* exact_pos, const int64_t* q_pos, void* out, float* workspace,
-                   int64_t workspace_floats, void* stream);
+                   int64_t workspace_floats, int phases, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * A2  Fused quantise + pack append of one token per sequence (streaming KIVI window).

@@ -449,24 +449,6 @@ void dct_split(DctParams p) {
   if (bh < p.BH) dct_block<R, DT>(p, bh, k % p.n_split, smem);
 }
 
-template <int R, int DT>
-__global__ __launch_bounds__(kDThreads) void dct_merge(MergeArgs a) {
-  extern __shared__ float smem[];
-  merge_partials<R, DT, kDD>(a, blockIdx.x, smem);
-}
-
-inline int dct_pow2(int64_t r) {
-  int R = 1;
-  while (R < r) R <<= 1;
-  return R;
-}
-
-// splits per (b, h): about one round of 768 resident blocks, at least one block per wavefront
-inline int dct_splits(int64_t BH, int64_t nb) {
-  int64_t s = (768 + BH - 1) / BH;
-  s = std::max<int64_t>(1, std::min<int64_t>(s, (nb + kDWaves - 1) / kDWaves));
-  return static_cast<int>(s);
-}
 
 }  // namespace
 }  // namespace kvq
@@ -503,9 +485,9 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
 namespace {
 int64_t dct_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t T, int64_t n_exact, int64_t* ex_floats,
                      int* S) {
-  *S = T > 0 ? kvq::dct_splits(B * Hkv, T / 64) : 0;
+  *S = T > 0 ? kvq::plan_block_splits(B * Hkv, T / 64, 4, 4) : 0;
   *ex_floats = n_exact > 0 ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
-  const int64_t R = kvq::dct_pow2((Hq / Hkv) * Tq);
+  const int64_t R = kvq::pow2_rows((Hq / Hkv) * Tq);
   return *ex_floats + B * Hkv * static_cast<int64_t>(*S) * R * (128 + 2);
 }
 }  // namespace
@@ -523,7 +505,8 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
                               int64_t T, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc, const uint16_t* vs,
                               const void* k_exact, const void* v_exact, int64_t cap_e, int64_t n_exact,
                               const int64_t* exact_pos, const int64_t* q_pos, void* out, float* workspace,
-                              int64_t workspace_floats, void* stream) {
+                              int64_t workspace_floats, int phases, void* stream) {
+  KVQ_REQUIRE(phases >= 1 && phases <= 3, "kvq_dct_decode: phases must be 1, 2 or 3");
   KVQ_REQUIRE(d == kDD, "kvq_dct_decode: head_dim must be 128");
   KVQ_REQUIRE(valid_dtype(q_dtype), "kvq_dct_decode: bad dtype");
   KVQ_REQUIRE(B > 0 && Hkv > 0 && Hq % Hkv == 0 && Tq > 0, "kvq_dct_decode: bad head counts");
@@ -540,7 +523,7 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
   KVQ_REQUIRE(workspace_floats >= need, "kvq_dct_decode: workspace too small (%lld < %lld floats)",
               (long long)workspace_floats, (long long)need);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int R = dct_pow2(R_real);
+  const int R = pow2_rows(R_real);
   DctParams p{};
   p.q = q; p.q_sb = q_sb; p.q_sh = q_sh; p.q_st = q_st;
   p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.Tq = (int)Tq; p.rep = (int)(Hq / Hkv); p.R_real = (int)R_real;
@@ -551,10 +534,12 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
   p.out = out;
   const int64_t S_ex = (n_exact + 31) / 32;
   if (n_exact > 0) {
-    const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,
-                                   nullptr, nullptr, 0, 0, 32, 32, k_exact, v_exact, q_dtype, cap_e, n_exact, exact_pos,
-                                   q_pos, out, q_dtype, workspace, ex_floats, nullptr, 0, 0.0f, 0, 1, stream);
-    if (rc != KVQ_OK) return rc;
+    if (phases & 1) {
+      const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,
+                                     nullptr, nullptr, 0, 0, 32, 32, k_exact, v_exact, q_dtype, cap_e, n_exact, exact_pos,
+                                     q_pos, out, q_dtype, workspace, ex_floats, nullptr, 0, 0.0f, 0, 1, stream);
+      if (rc != KVQ_OK) return rc;
+    }
     const int64_t nrow = B * Hkv * S_ex * R;
     p.ex_o = workspace;
     p.ex_m = workspace + nrow * 128;
@@ -572,7 +557,7 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
   const size_t split_smem = std::max<size_t>(
       (R * kDD + kDWaves * (2 * R * 64 + R * 16) + kDWaves * R * 18) * sizeof(float) + 12 * 64 * 16,
       (kDWaves * R * kDD + kDWaves * 2 * R) * sizeof(float));
-  if (S > 0) {
+  if (S > 0 && (phases & 1)) {
 #define KVQ_DCT_SPLIT(R_, DT_) \
     hipLaunchKernelGGL((dct_split<R_, DT_>), dim3(static_cast<unsigned>(S) * bh_pad), dim3(kDThreads), split_smem, s, p)
 #define KVQ_DCT_R(DT_)                                   \
@@ -591,24 +576,11 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
 #undef KVQ_DCT_SPLIT
     KVQ_LAUNCH_CHECK("kvq_dct_decode(split)");
   }
-  const size_t msmem = 2 * R * sizeof(float);
-  MergeArgs ma{p.ws_o, p.ws_m, p.ws_l, p.S_all, p.ex_o, p.ex_m, p.ex_l, p.S_ex,
-               p.Hq, p.Hkv, p.Tq, p.rep, p.R_real, p.out};
-#define KVQ_DCT_MERGE(R_, DT_) hipLaunchKernelGGL((dct_merge<R_, DT_>), dim3(p.BH), dim3(kDThreads), msmem, s, ma)
-#define KVQ_DCT_MR(DT_)                                  \
-  switch (R) {                                           \
-    case 1: KVQ_DCT_MERGE(1, DT_); break;                \
-    case 2: KVQ_DCT_MERGE(2, DT_); break;                \
-    case 4: KVQ_DCT_MERGE(4, DT_); break;                \
-    default: KVQ_DCT_MERGE(8, DT_); break;               \
+  if (phases & 2) {
+    const MergeArgs ma{p.ws_o, p.ws_m, p.ws_l, p.S_all, p.ex_o, p.ex_m, p.ex_l, p.S_ex,
+                       p.Hq, p.Hkv, p.Tq, p.rep, p.R_real, p.out, nullptr};
+    const int rc = launch_merge_rows(ma, R, p.BH, q_dtype, s);
+    if (rc != KVQ_OK) return rc;
   }
-  switch (q_dtype) {
-    case KVQ_F32: KVQ_DCT_MR(KVQ_F32) break;
-    case KVQ_F16: KVQ_DCT_MR(KVQ_F16) break;
-    default: KVQ_DCT_MR(KVQ_BF16) break;
-  }
-#undef KVQ_DCT_MR
-#undef KVQ_DCT_MERGE
-  KVQ_LAUNCH_CHECK("kvq_dct_decode(merge)");
   return KVQ_OK;
 }

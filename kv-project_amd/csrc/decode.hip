@@ -38,6 +38,7 @@
 
 #include "common.hpp"
 #include "mfma_common.hpp"
+#include "partials.hpp"
 
 namespace kvq {
 namespace {
@@ -590,40 +591,6 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   }
 }
 
-// exact log-sum-exp merge of the S1 partials of (b, h) and the output write
-template <int R, int DT>
-__device__ void merge_bh(const DecodeParams& p, int bh, float* smem) {
-  const int b = bh / p.Hkv, h = bh % p.Hkv;
-  float* wgt = smem;                             // [S1][R]
-  float* tot = smem + p.S1 * R;                  // L[R]
-  const int64_t pb = static_cast<int64_t>(bh) * p.S1;
-  if (threadIdx.x < R) {
-    const int r = threadIdx.x;
-    float M = -INFINITY;
-    for (int s = 0; s < p.S1; ++s) M = fmaxf(M, p.ws_m[(pb + s) * R + r]);
-    float L = 0.0f;
-    for (int s = 0; s < p.S1; ++s) {
-      const float m = p.ws_m[(pb + s) * R + r];
-      const float w = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - M);
-      wgt[s * R + r] = w;
-      L += w * p.ws_l[(pb + s) * R + r];
-    }
-    tot[r] = L;
-    if (p.row_ml != nullptr && r < p.R_real) {
-      p.row_ml[(static_cast<int64_t>(bh) * R + r) * 2] = M;
-      p.row_ml[(static_cast<int64_t>(bh) * R + r) * 2 + 1] = L;
-    }
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < p.R_real * kD; idx += kThreads) {
-    const int r = idx / kD, c = idx % kD;
-    float O = 0.0f;
-    for (int s = 0; s < p.S1; ++s) O += wgt[s * R + r] * p.ws_o[((pb + s) * R + r) * kD + c];
-    const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
-    const int64_t o = ((static_cast<int64_t>(b) * p.Tq + t) * p.Hq + hq) * kD + c;
-    store_from_f32<DT>(p.out, o, O / tot[r]);
-  }
-}
 
 // One block per (b, h, split).  Blocks are dispatched round-robin over the 8 XCDs by linear id,
 // so id -> (xcd = id % 8, k = id / 8) -> bh = xcd + 8*(k / S1), split = k % S1 keeps every
@@ -667,18 +634,11 @@ void kivi_score_split(DecodeParams p) {
   if (bh < p.BH) packed_block<R, GV, DT, true>(p, bh, k % p.n_split, smem);
 }
 
-template <int R, int DT>
-__global__ __launch_bounds__(kThreads) void kivi_decode_merge(DecodeParams p) {
-  extern __shared__ float smem[];
-  merge_bh<R, DT>(p, blockIdx.x, smem);
-}
-
 template <int R, int GV, int DT>
 int launch(DecodeParams& p, int phases, hipStream_t stream) {
   const size_t exact_smem = (R * kD + R * kExactRows + 2 * R + kWaves * R * kD) * sizeof(float);
   const size_t packed_smem = std::max<size_t>((R * kD) * sizeof(float) + kWaves * (2 * R * 64 + R * 16) * 4,
                                               (kWaves * R * kD + kWaves * 2 * R) * sizeof(float));
-  const size_t msmem = (static_cast<size_t>(p.S1) * R + R) * sizeof(float);
   const int bh_pad = (p.BH + 7) / 8 * 8;
   const dim3 grid(static_cast<unsigned>(p.S1) * bh_pad);
   if (phases & 1) {
@@ -687,8 +647,12 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(split)");
   }
   if (phases & 2) {
-    hipLaunchKernelGGL((kivi_decode_merge<R, DT>), dim3(p.BH), dim3(kThreads), msmem, stream, p);
-    KVQ_LAUNCH_CHECK("kvq_kivi_decode(merge)");
+    MergeArgs ma{};
+    ma.ws_o = p.ws_o; ma.ws_m = p.ws_m; ma.ws_l = p.ws_l; ma.S = p.S1;
+    ma.Hq = p.Hq; ma.Hkv = p.Hkv; ma.Tq = p.Tq; ma.rep = p.rep; ma.R_real = p.R_real;
+    ma.out = p.out; ma.row_ml = p.row_ml;
+    const int rc = launch_merge_rows(ma, R, p.BH, DT, stream);
+    if (rc != KVQ_OK) return rc;
   }
   if ((phases & 4) && p.scores != nullptr && p.n_split > 0) {
     hipLaunchKernelGGL((kivi_score_split<R, GV, DT>), dim3(static_cast<unsigned>(p.n_split) * bh_pad),
@@ -696,12 +660,6 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(score)");
   }
   return KVQ_OK;
-}
-
-inline int pow2_rows(int64_t r) {
-  int R = 1;
-  while (R < r) R <<= 1;
-  return R;
 }
 
 struct SplitPlan {

@@ -495,17 +495,6 @@ void mixed_split(MixedParams p) {
   if (bh < p.BH) mixed_block<R, DT>(p, bh, k % p.n_split, smem);
 }
 
-template <int R, int DT>
-__global__ __launch_bounds__(kMThreads) void mixed_merge(MergeArgs a) {
-  extern __shared__ float smem[];
-  merge_partials<R, DT, kMD>(a, blockIdx.x, smem);
-}
-
-inline int mixed_splits(int64_t BH, int64_t nb) {
-  int64_t s = (768 + BH - 1) / BH;
-  s = std::max<int64_t>(1, std::min<int64_t>(s, (nb + kMWaves - 1) / kMWaves));
-  return static_cast<int>(s);
-}
 
 }  // namespace
 }  // namespace kvq
@@ -543,7 +532,7 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
 namespace {
 int64_t mixed_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t nb, int64_t n_exact, int64_t* ex_floats,
                        int* S) {
-  *S = nb > 0 ? kvq::mixed_splits(B * Hkv, nb) : 0;
+  *S = nb > 0 ? kvq::plan_block_splits(B * Hkv, nb, 2, 4) : 0;
   *ex_floats = n_exact > 0 ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
   const int64_t R = kvq::pow2_rows((Hq / Hkv) * Tq);
   return *ex_floats + B * Hkv * static_cast<int64_t>(*S) * R * (128 + 2);
@@ -562,7 +551,8 @@ extern "C" int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_
                                 int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling, const uint8_t* buf,
                                 const int64_t* seg, int64_t nb, const void* k_exact, const void* v_exact,
                                 int64_t cap_e, int64_t n_exact, const int64_t* exact_pos, const int64_t* q_pos,
-                                void* out, float* workspace, int64_t workspace_floats, void* stream) {
+                                void* out, float* workspace, int64_t workspace_floats, int phases, void* stream) {
+  KVQ_REQUIRE(phases >= 1 && phases <= 3, "kvq_mixed_decode: phases must be 1, 2 or 3");
   KVQ_REQUIRE(d == kMD, "kvq_mixed_decode: head_dim must be 128");
   KVQ_REQUIRE(valid_dtype(q_dtype), "kvq_mixed_decode: bad dtype");
   KVQ_REQUIRE(B > 0 && Hkv > 0 && Hq % Hkv == 0 && Tq > 0, "kvq_mixed_decode: bad head counts");
@@ -583,10 +573,12 @@ extern "C" int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_
   ma.Hq = (int)Hq; ma.Hkv = (int)Hkv; ma.Tq = (int)Tq; ma.rep = (int)(Hq / Hkv); ma.R_real = (int)R_real;
   ma.out = out;
   if (n_exact > 0) {
-    const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,
-                                   nullptr, nullptr, 0, 0, 32, 32, k_exact, v_exact, q_dtype, cap_e, n_exact, exact_pos,
-                                   q_pos, out, q_dtype, workspace, ex_floats, nullptr, 0, 0.0f, 0, 1, stream);
-    if (rc != KVQ_OK) return rc;
+    if (phases & 1) {
+      const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,
+                                     nullptr, nullptr, 0, 0, 32, 32, k_exact, v_exact, q_dtype, cap_e, n_exact, exact_pos,
+                                     q_pos, out, q_dtype, workspace, ex_floats, nullptr, 0, 0.0f, 0, 1, stream);
+      if (rc != KVQ_OK) return rc;
+    }
     const int64_t S_ex = (n_exact + 31) / 32;
     const int64_t nrow = B * Hkv * S_ex * R;
     ma.ex_o = workspace;
@@ -609,7 +601,7 @@ extern "C" int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_
   const int bh_pad = (p.BH + 7) / 8 * 8;
   const size_t split_smem = std::max<size_t>((R * kMD + kMWaves * (2 * R * 64 + R * 16)) * sizeof(float),
                                              (kMWaves * R * kMD + kMWaves * 2 * R) * sizeof(float));
-  if (S > 0) {
+  if (S > 0 && (phases & 1)) {
 #define KVQ_MX_SPLIT(R_, DT_) \
     hipLaunchKernelGGL((mixed_split<R_, DT_>), dim3(static_cast<unsigned>(S) * bh_pad), dim3(kMThreads), split_smem, s, p)
 #define KVQ_MX_R(DT_)                                    \
@@ -628,22 +620,9 @@ extern "C" int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_
 #undef KVQ_MX_SPLIT
     KVQ_LAUNCH_CHECK("kvq_mixed_decode(split)");
   }
-  const size_t msmem = 2 * R * sizeof(float);
-#define KVQ_MX_MERGE(R_, DT_) hipLaunchKernelGGL((mixed_merge<R_, DT_>), dim3(p.BH), dim3(kMThreads), msmem, s, ma)
-#define KVQ_MX_MR(DT_)                                   \
-  switch (R) {                                           \
-    case 1: KVQ_MX_MERGE(1, DT_); break;                 \
-    case 2: KVQ_MX_MERGE(2, DT_); break;                 \
-    case 4: KVQ_MX_MERGE(4, DT_); break;                 \
-    default: KVQ_MX_MERGE(8, DT_); break;                \
+  if (phases & 2) {
+    const int rc = launch_merge_rows(ma, R, p.BH, q_dtype, s);
+    if (rc != KVQ_OK) return rc;
   }
-  switch (q_dtype) {
-    case KVQ_F32: KVQ_MX_MR(KVQ_F32) break;
-    case KVQ_F16: KVQ_MX_MR(KVQ_F16) break;
-    default: KVQ_MX_MR(KVQ_BF16) break;
-  }
-#undef KVQ_MX_MR
-#undef KVQ_MX_MERGE
-  KVQ_LAUNCH_CHECK("kvq_mixed_decode(merge)");
   return KVQ_OK;
 }

@@ -51,11 +51,11 @@ SIGNATURES = {
     "kvq_dct_encode": (i32, [vp, i32, i64, i64, i64, i64, vp, i32, vp, vp, vp]),
     "kvq_dct_decode_workspace": (i64, [i64, i64, i64, i64, i64, i64, i64]),
     "kvq_dct_decode": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32, vp, i64, vp, vp, vp, vp,
-                             vp, vp, i64, i64, vp, vp, vp, vp, i64, vp]),
+                             vp, vp, i64, i64, vp, vp, vp, vp, i64, i32, vp]),
     "kvq_mixed_encode": (i32, [vp, vp, i32, i64, i64, i64, i64, vp, vp, vp, vp, vp]),
     "kvq_mixed_decode_workspace": (i64, [i64, i64, i64, i64, i64, i64, i64]),
     "kvq_mixed_decode": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32, vp, vp, i64, vp, vp, i64, i64,
-                               vp, vp, vp, vp, i64, vp]),
+                               vp, vp, vp, vp, i64, i32, vp]),
     "kvq_kivi_append": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp, vp, i64,
                               vp, vp, vp, vp, vp, i64, i32, i32, vp]),
     "kvq_selftest_mfma_layout": (i32, [vp, vp, vp, vp]),

@@ -101,9 +101,11 @@ def dct_workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, T: int, n_e
 
 @torch.no_grad()
 def dct_decode(q: torch.Tensor, scaling: float, cache: DctCache, *, q_pos: Optional[torch.Tensor] = None,
-               out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+               out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+               phases: int = 3) -> torch.Tensor:
     """Attention of q (B, Hq, Tq, d) over the coded blocks (all visible) and the exact rows (visible
-    per q_pos / exact_pos when both are set) -> (B, Tq, Hq, d) of q's dtype."""
+    per q_pos / exact_pos when both are set) -> (B, Tq, Hq, d) of q's dtype.  ``phases`` 1 computes
+    only the partials into ``workspace``, 2 only merges them (timing hooks), 3 both."""
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.k_exact.shape[1]
@@ -122,5 +124,5 @@ def dct_decode(q: torch.Tensor, scaling: float, cache: DctCache, *, q_pos: Optio
               B, Hq, Hkv, Tq, d, float(scaling), dct_table(q.device).data_ptr(), cache.T, cache.kc.data_ptr(),
               cache.ks.data_ptr(), cache.vc.data_ptr(), cache.vs.data_ptr(), cache.k_exact.data_ptr(),
               cache.v_exact.data_ptr(), cache.k_exact.shape[2], cache.n_exact, _lib.ptr(ep), _lib.ptr(qp),
-              out.data_ptr(), workspace.data_ptr(), workspace.numel(), _lib.stream_of(q))
+              out.data_ptr(), workspace.data_ptr(), workspace.numel(), int(phases), _lib.stream_of(q))
     return out

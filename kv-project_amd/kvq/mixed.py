@@ -119,9 +119,11 @@ def mixed_workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, nb: int, 
 
 @torch.no_grad()
 def mixed_decode(q: torch.Tensor, scaling: float, cache: MixedKIVICache, *, q_pos: Optional[torch.Tensor] = None,
-                 out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                 phases: int = 3) -> torch.Tensor:
     """Attention of q (B, Hq, Tq, d) over every coded block (all visible) and the exact rows
-    (visible per q_pos / exact_pos when both are set) -> (B, Tq, Hq, d) of q's dtype."""
+    (visible per q_pos / exact_pos when both are set) -> (B, Tq, Hq, d) of q's dtype.  ``phases`` 1 computes
+    only the partials into ``workspace``, 2 only merges them (timing hooks), 3 both."""
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.k_exact.shape[1]
@@ -139,6 +141,6 @@ def mixed_decode(q: torch.Tensor, scaling: float, cache: MixedKIVICache, *, q_po
     _lib.call("kvq_mixed_decode", q.data_ptr(), _lib.DTYPE_CODE[q.dtype], q.stride(0), q.stride(1), q.stride(2),
               B, Hq, Hkv, Tq, d, float(scaling), cache.buf.data_ptr(), cache.seg.data_ptr(), cache.nb,
               cache.k_exact.data_ptr(), cache.v_exact.data_ptr(), cache.k_exact.shape[2], cache.n_exact,
-              _lib.ptr(ep), _lib.ptr(qp), out.data_ptr(), workspace.data_ptr(), workspace.numel(),
+              _lib.ptr(ep), _lib.ptr(qp), out.data_ptr(), workspace.data_ptr(), workspace.numel(), int(phases),
               _lib.stream_of(q))
     return out

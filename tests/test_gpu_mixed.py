@@ -121,3 +121,24 @@ def test_decode_peaked_logits():
     out = kvq.mixed_decode(q.cuda(), d ** -0.5, cache).cpu().numpy()
     ref = _oracle(cache, K, V, widths, q, d ** -0.5)
     assert float(np.abs(out - ref).max()) <= 2e-3
+
+
+def test_phases_split_then_merge_equals_full():
+    import kvq
+    g = torch.Generator().manual_seed(77)
+    B, Hq, Hkv, T, d = 1, 8, 2, 700, 128
+    K = torch.randn((B, Hkv, T, d), generator=g).to(torch.bfloat16)
+    V = torch.randn((B, Hkv, T, d), generator=g).to(torch.bfloat16)
+    q = torch.randn((B, Hq, 1, d), generator=g).to(torch.bfloat16)
+    nb = (T - 20) // 64
+    widths = torch.tensor([2, 4, 8])[torch.randint(0, 3, (B, Hkv, nb), generator=g)]
+    qc = q.cuda()
+    for make, dec in ((lambda: kvq.MixedKIVICache.from_context(K.cuda(), V.cuda(), widths, window=20), kvq.mixed_decode),
+                      (lambda: kvq.DctCache.from_context(K.cuda(), V.cuda(), window=20), kvq.dct_decode)):
+        cache = make()
+        full = dec(qc, d ** -0.5, cache)
+        ws = torch.empty((1 << 20,), dtype=torch.float32, device="cuda")
+        out = torch.empty_like(full)
+        dec(qc, d ** -0.5, cache, workspace=ws, out=out, phases=1)
+        dec(qc, d ** -0.5, cache, workspace=ws, out=out, phases=2)
+        assert torch.equal(out, full)
