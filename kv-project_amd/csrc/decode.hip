@@ -461,13 +461,14 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
         if constexpr (R >= 4) x[j] += dpp<kQuadSwap2>(x[j]);
         if constexpr (R >= 8) x[j] += __shfl_xor(x[j], 4, 64);
       }
-      if (n == 0) {
+      // every lane of group g now holds the row sums of its 8 slots: lane n < 8 adds slot n, so
+      // the 32 tokens of the chunk go out as one coalesced non-returning atomic add (no load to
+      // wait for, so the chunk pipeline keeps its loads in flight)
+      float v = x[0];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int tok = cb + 16 * (j >> 2) + 4 * g + (j & 3);
-          if (tok < t1) score_row[tok] = __builtin_fmaf(p.score_weight, x[j], score_row[tok]);
-        }
-      }
+      for (int j = 1; j < 8; ++j) v = (n == j) ? x[j] : v;
+      const int tok = cb + 16 * (n >> 2) + 4 * g + (n & 3);
+      if (n < 8 && tok < t1) unsafeAtomicAdd(score_row + tok, p.score_weight * v);
       return;
     }
     // ---- online softmax (base 2) with a lazy maximum: probabilities are taken against the running

@@ -2,12 +2,12 @@
 // rows that the retained-set decode reads.
 //
 // Top-k (SnapKV-style retention, STRATA_KV.py:975 topk, 1022-1023 position order): one block of
-// 1024 threads per (b, h) row of scores.  A 4-pass radix select over order-preserving uint32 keys
-// of the fp32 scores (8 bits per pass, LDS histogram) finds the k-th largest key T and how many
-// keys equal to T are kept; a counting pass and a writing pass over contiguous per-thread ranges,
-// with block-wide prefix sums, emit the retained positions in increasing order.  Among keys equal
-// to T the lowest positions are kept (torch.topk leaves that order unspecified).  The scores row
-// is re-read every pass; after the first it is served from L2.
+// 1024 threads per (b, h) row of scores.  A radix select over order-preserving uint32 keys of the
+// fp32 scores (8 bits per pass, LDS histograms) finds the k-th largest key T and how many keys
+// equal to T are kept; the retained positions are then written in increasing order.  Among keys
+// equal to T the lowest positions are kept (torch.topk leaves that order unspecified).  Rows of up
+// to 65536 scores take topk_retain_strided_kernel (common-prefix skip, per-wavefront histograms,
+// ballot-ordered output); longer rows take topk_retain_kernel.
 #include "common.hpp"
 
 namespace kvq {
@@ -104,6 +104,160 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_kernel(const float* 
   }
 }
 
+// Rows of at most kTopkSlots * 1024 scores (topk_retain_strided_kernel): element i = tid + 1024 e
+// is read by thread tid in slot e (coalesced); the row stays in L2 after the first read.
+//   * The leading bits shared by every key (found from the block's minimum and maximum) are
+//     skipped, so the first 8-bit digit splits the keys that actually differ; scores of one
+//     magnitude share their top bits and would otherwise pile into one or two histogram bins.
+//   * One 256-bin histogram per wavefront (LDS atomics contend only inside a wavefront), summed
+//     per bin; the digit of the k-th largest key is found by a parallel suffix sum.
+//   * Output in position order: per slot e, a ballot gives each wavefront's count; one block scan
+//     over the (e, wavefront) counts gives every selected position its output index.
+constexpr int kTopkSlots = 64;
+
+__device__ __forceinline__ uint32_t block_reduce_u32(uint32_t v, bool is_max, uint32_t* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t u = __shfl_xor(v, o, 64);
+    v = is_max ? max(v, u) : min(v, u);
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t r = red[0];
+  for (int w = 1; w < kTopkThreads / 64; ++w) r = is_max ? max(r, red[w]) : min(r, red[w]);
+  return r;
+}
+
+__device__ __forceinline__ int lane_rank(uint64_t ballot) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(ballot >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(ballot), 0u));
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_retain_strided_kernel(const float* __restrict__ scores,
+                                                                           int n, int64_t scores_bh, int k,
+                                                                           int32_t* __restrict__ idx, int64_t idx_bh) {
+  constexpr int NW = kTopkThreads / 64;
+  __shared__ uint32_t hist[NW][256];
+  __shared__ uint32_t cnt[kTopkSlots * NW];
+  __shared__ uint32_t wave_sums[32];
+  __shared__ uint32_t red[NW];
+  __shared__ uint32_t sh_prefix, sh_krem;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const float* s = scores + static_cast<int64_t>(blockIdx.x) * scores_bh;
+  int32_t* out = idx + static_cast<int64_t>(blockIdx.x) * idx_bh;
+  const int E = (n + kTopkThreads - 1) / kTopkThreads;           // slots in use (<= kTopkSlots)
+  uint32_t kmax = 0u, kmin = 0xFFFFFFFFu;
+#pragma unroll 8
+  for (int i = tid; i < n; i += kTopkThreads) {
+    const uint32_t u = order_key(s[i]);
+    kmax = max(kmax, u);
+    kmin = min(kmin, u);
+  }
+  kmax = block_reduce_u32(kmax, true, red);
+  kmin = block_reduce_u32(kmin, false, red);
+  const uint32_t diff = kmax ^ kmin;
+  int top = diff ? 31 - __builtin_clz(diff) : -1;     // highest bit in which keys differ
+  uint32_t mask = top < 0 ? 0xFFFFFFFFu : (top >= 31 ? 0u : ~((2u << top) - 1u));
+  uint32_t prefix = kmax & mask;
+  uint32_t krem = static_cast<uint32_t>(k);
+  while (top >= 0) {
+    const int width = min(8, top + 1);
+    const int shift = top - width + 1;
+    const uint32_t dmask = (1u << width) - 1u;
+    for (int b = lane; b < 256; b += 64) hist[wave][b] = 0u;
+    __syncthreads();
+#pragma unroll 8
+    for (int i = tid; i < n; i += kTopkThreads) {
+      const uint32_t u = order_key(s[i]);
+      if ((u & mask) == prefix) atomicAdd(&hist[wave][(u >> shift) & dmask], 1u);
+    }
+    __syncthreads();
+    // thread t < 256 holds bin 255 - t: its total and the inclusive sum over the bins above it
+    uint32_t tot = 0u;
+    if (tid < 256) {
+      for (int w = 0; w < NW; ++w) tot += hist[w][255 - tid];
+    }
+    uint32_t x = tot;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (tid < 256 && lane == 63) wave_sums[wave] = x;
+    __syncthreads();
+    if (tid < 256) {
+      uint32_t before = 0u;
+      for (int w = 0; w < wave; ++w) before += wave_sums[w];
+      const uint32_t incl = before + x, excl = incl - tot;
+      if (tot > 0u && excl < krem && incl >= krem) {
+        sh_prefix = prefix | (static_cast<uint32_t>(255 - tid) << shift);
+        sh_krem = krem - excl;
+      }
+    }
+    __syncthreads();
+    prefix = sh_prefix;
+    krem = sh_krem;
+    mask |= dmask << shift;
+    top = shift - 1;
+  }
+  // prefix = key of the k-th largest score; krem = how many keys equal to it are kept: the krem
+  // equal keys at the lowest positions.  Classify every slot once (bit e of gt / eq), with the
+  // loads batched, then rank and emit from the bit masks alone.
+  uint64_t gt = 0, eq = 0;
+  for (int e0 = 0; e0 < E; e0 += 16) {
+    uint32_t u[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int i = tid + kTopkThreads * (e0 + j);
+      u[j] = (e0 + j < E && i < n) ? order_key(s[i]) : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int i = tid + kTopkThreads * (e0 + j);
+      if (e0 + j < E && i < n) {
+        gt |= static_cast<uint64_t>(u[j] > prefix) << (e0 + j);
+        eq |= static_cast<uint64_t>(u[j] == prefix) << (e0 + j);
+      }
+    }
+  }
+  uint32_t total;
+  for (int e = 0; e < E; ++e) {
+    const uint64_t b = __ballot((eq >> e) & 1u);
+    if (lane == 0) cnt[e * NW + wave] = static_cast<uint32_t>(__builtin_popcountll(b));
+  }
+  __syncthreads();
+  {
+    const uint32_t c = tid < E * NW ? cnt[tid] : 0u;
+    const uint32_t pre = block_exclusive_scan(c, wave_sums, &total);
+    if (tid < E * NW) cnt[tid] = pre;
+  }
+  __syncthreads();
+  uint64_t sel = gt;                                  // + the kept ties
+  for (int e = 0; e < E; ++e) {
+    const bool is_eq = (eq >> e) & 1u;
+    const uint64_t b = __ballot(is_eq);
+    if (is_eq && cnt[e * NW + wave] + lane_rank(b) < krem) sel |= 1ull << e;
+  }
+  __syncthreads();
+  for (int e = 0; e < E; ++e) {
+    const uint64_t b = __ballot((sel >> e) & 1u);
+    if (lane == 0) cnt[e * NW + wave] = static_cast<uint32_t>(__builtin_popcountll(b));
+  }
+  __syncthreads();
+  {
+    const uint32_t c = tid < E * NW ? cnt[tid] : 0u;
+    const uint32_t pre = block_exclusive_scan(c, wave_sums, &total);
+    if (tid < E * NW) cnt[tid] = pre;
+  }
+  __syncthreads();
+  for (int e = 0; e < E; ++e) {
+    const bool take = (sel >> e) & 1u;
+    const uint64_t b = __ballot(take);
+    if (take) out[cnt[e * NW + wave] + lane_rank(b)] = tid + kTopkThreads * e;
+  }
+}
+
 // nibble (bit offset / 4) of the value-tile word that holds token slot j
 __device__ __constant__ int kNibbleOfSlotG[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 
@@ -185,8 +339,13 @@ extern "C" int kvq_topk_retain(const float* scores, int64_t BH, int64_t n, int64
   KVQ_REQUIRE(scores_bh >= n && idx_bh >= k, "kvq_topk_retain: row strides smaller than the rows");
   if (BH == 0 || k == 0) return KVQ_OK;
   KVQ_REQUIRE(scores && idx, "kvq_topk_retain: null pointer");
-  hipLaunchKernelGGL(topk_retain_kernel, dim3(static_cast<unsigned>(BH)), dim3(kTopkThreads), 0,
-                     static_cast<hipStream_t>(stream), scores, n, scores_bh, k, idx, idx_bh);
+  if (n <= static_cast<int64_t>(kTopkSlots) * kTopkThreads)
+    hipLaunchKernelGGL(topk_retain_strided_kernel, dim3(static_cast<unsigned>(BH)), dim3(kTopkThreads), 0,
+                       static_cast<hipStream_t>(stream), scores, static_cast<int>(n), scores_bh, static_cast<int>(k),
+                       idx, idx_bh);
+  else
+    hipLaunchKernelGGL(topk_retain_kernel, dim3(static_cast<unsigned>(BH)), dim3(kTopkThreads), 0,
+                       static_cast<hipStream_t>(stream), scores, n, scores_bh, k, idx, idx_bh);
   KVQ_LAUNCH_CHECK("kvq_topk_retain");
   return KVQ_OK;
 }

@@ -7,7 +7,15 @@
 //   xhat  = code * scale + lo                                   (two roundings, never fused)
 // All arithmetic that feeds a code or a metadata value uses the explicitly rounded intrinsics so
 // that no multiply-add contraction can change a bit.
+#include <algorithm>
+
 #include "common.hpp"
+
+// Build-time switch: blocks of the vectorised quantisers (grid-stride loops over their items);
+// 0 = one block per item.
+#ifndef KVQ_QUANT_GRID
+#define KVQ_QUANT_GRID 0
+#endif
 
 namespace kvq {
 namespace {
@@ -22,6 +30,22 @@ __device__ __forceinline__ float as_stored(float x) {
 
 __device__ __forceinline__ int quant_code(float x, float lo, float sc, int qmax) {
   float t = rintf(__fdiv_rn(__fsub_rn(x, lo), sc));
+  t = fminf(fmaxf(t, 0.0f), static_cast<float>(qmax));
+  return static_cast<int>(t);
+}
+
+// quant_code with the division replaced by a multiply with r = RN(1 / sc), exact by a bound:
+// |RN(d r) - RN(d / sc)| <= 1.5 * 2^-23 * |d / sc| <= 5.4e-5 for quotients up to 300 (codes are at
+// most 255 and d / sc exceeds qmax by at most a rounding of sc), so when RN(d r) is more than
+// 1e-4 from a half-integer both round to the same integer; otherwise the IEEE quotient is taken.
+// The IEEE division runs only in wavefronts where some lane needs it (a wave-uniform branch).
+__device__ __forceinline__ int quant_code_r(float x, float lo, float sc, float r, int qmax) {
+  const float d = __fsub_rn(x, lo);
+  float t = rintf(__fmul_rn(d, r));
+  const bool near = fabsf(__fmul_rn(d, r) - t) > 0.4999f;
+  if (__builtin_expect(__any(near), 0)) {
+    if (near) t = rintf(__fdiv_rn(d, sc));
+  }
   t = fminf(fmaxf(t, 0.0f), static_cast<float>(qmax));
   return static_cast<int>(t);
 }
@@ -153,6 +177,302 @@ __global__ void kivi_quant_values(const void* __restrict__ x, int H, int64_t sb,
     float* dst = xhat + (static_cast<int64_t>(bh) * T + n_sink + t) * d + s * 8;
 #pragma unroll
     for (int k = 0; k < 8; ++k) dst[k] = dequant(cd[k], lo, sc);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Vectorised variants for d == 128 and 16-byte aligned rows (the common case): the same
+// arithmetic as the kernels above (as_stored, quant_code, dequant), so the results are identical
+// bit for bit; only the memory access changes.  A thread owns 8 consecutive channels ("slab")
+// of a row: one 16-byte load per row (two for fp32), one word store per row for the packed codes.
+
+template <int DT>
+__device__ __forceinline__ void load_slab(const void* base, int64_t i, float (&v)[8]) {
+  if constexpr (DT == KVQ_F32) {
+    const float4* p4 = reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    const float4 a = p4[0], c = p4[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t a = static_cast<uint16_t>(ws[k] & 0xffffu), c = static_cast<uint16_t>(ws[k] >> 16);
+      v[2 * k] = DT == KVQ_F16 ? f16_to_f32(a) : bf16_to_f32(a);
+      v[2 * k + 1] = DT == KVQ_F16 ? f16_to_f32(c) : bf16_to_f32(c);
+    }
+  }
+}
+
+// codes of one slab: MSB-first packed bytes (`bits` of them), raw codes, dequantised values
+__device__ __forceinline__ void store_slab(const int (&cd)[8], int bits, uint8_t* packed_dst, uint8_t* codes_dst,
+                                           float* xhat_dst, const float (&lo)[8], const float (&sc)[8]) {
+  if (packed_dst != nullptr) {
+    if (bits == 4) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w |= static_cast<uint32_t>((cd[2 * k] << 4) | cd[2 * k + 1]) << (8 * k);
+      *reinterpret_cast<uint32_t*>(packed_dst) = w;
+    } else if (bits == 2) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        w |= static_cast<uint32_t>((cd[4 * k] << 6) | (cd[4 * k + 1] << 4) | (cd[4 * k + 2] << 2) | cd[4 * k + 3]) << (8 * k);
+      *reinterpret_cast<uint16_t*>(packed_dst) = static_cast<uint16_t>(w);
+    } else {
+      uint2 w;
+      w.x = cd[0] | (cd[1] << 8) | (cd[2] << 16) | (static_cast<uint32_t>(cd[3]) << 24);
+      w.y = cd[4] | (cd[5] << 8) | (cd[6] << 16) | (static_cast<uint32_t>(cd[7]) << 24);
+      *reinterpret_cast<uint2*>(packed_dst) = w;
+    }
+  }
+  if (codes_dst != nullptr) {
+    uint2 w;
+    w.x = cd[0] | (cd[1] << 8) | (cd[2] << 16) | (static_cast<uint32_t>(cd[3]) << 24);
+    w.y = cd[4] | (cd[5] << 8) | (cd[6] << 16) | (static_cast<uint32_t>(cd[7]) << 24);
+    *reinterpret_cast<uint2*>(codes_dst) = w;
+  }
+  if (xhat_dst != nullptr) {
+    float4 a, c;
+    a.x = dequant(cd[0], lo[0], sc[0]); a.y = dequant(cd[1], lo[1], sc[1]);
+    a.z = dequant(cd[2], lo[2], sc[2]); a.w = dequant(cd[3], lo[3], sc[3]);
+    c.x = dequant(cd[4], lo[4], sc[4]); c.y = dequant(cd[5], lo[5], sc[5]);
+    c.z = dequant(cd[6], lo[6], sc[6]); c.w = dequant(cd[7], lo[7], sc[7]);
+    reinterpret_cast<float4*>(xhat_dst)[0] = a;
+    reinterpret_cast<float4*>(xhat_dst)[1] = c;
+  }
+}
+
+// Raw 16-byte slab (8 elements; fp32 needs two) and its conversion: loads are issued one work
+// item ahead and converted when the item is processed.
+template <int DT>
+struct Slab {
+  uint4 a, b;
+};
+template <int DT>
+__device__ __forceinline__ void slab_load(const void* base, int64_t i, Slab<DT>& r) {
+  if constexpr (DT == KVQ_F32) {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(base) + i);
+    r.a = p[0];
+    r.b = p[1];
+  } else {
+    r.a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+  }
+}
+template <int DT>
+__device__ __forceinline__ void slab_values(const Slab<DT>& r, float (&v)[8]) {
+  if constexpr (DT == KVQ_F32) {
+    v[0] = __uint_as_float(r.a.x); v[1] = __uint_as_float(r.a.y); v[2] = __uint_as_float(r.a.z); v[3] = __uint_as_float(r.a.w);
+    v[4] = __uint_as_float(r.b.x); v[5] = __uint_as_float(r.b.y); v[6] = __uint_as_float(r.b.z); v[7] = __uint_as_float(r.b.w);
+  } else {
+    const uint32_t ws[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t a = static_cast<uint16_t>(ws[k] & 0xffffu), c = static_cast<uint16_t>(ws[k] >> 16);
+      v[2 * k] = DT == KVQ_F16 ? f16_to_f32(a) : bf16_to_f32(a);
+      v[2 * k + 1] = DT == KVQ_F16 ? f16_to_f32(c) : bf16_to_f32(c);
+    }
+  }
+}
+
+// Keys, d == 128: a 256-thread block walks the (group, b*h) items with a grid stride, loading the
+// next item while it reduces and codes the current one.  Thread t owns slab s = t % 16 of rows
+// t / 16 + 16 j (j < RPT, RPT = ceil(group / 16)); per-channel min / max reduce over the rows of
+// the thread, then over the 16 row lanes (shuffles inside a wavefront, LDS across the four).
+template <int DT, int RPT>
+__global__ __launch_bounds__(256) void kivi_quant_keys_v(const void* __restrict__ x, int H, int64_t sb, int64_t sh,
+                                                          int64_t st, int n_sink, int n, int bits, int group,
+                                                          uint8_t* __restrict__ codes, int64_t codes_bh,
+                                                          uint8_t* __restrict__ packed, int64_t packed_bh,
+                                                          uint16_t* __restrict__ lo_out, uint16_t* __restrict__ sc_out,
+                                                          int64_t meta_bh, float* __restrict__ xhat, int T,
+                                                          int n_g, int64_t n_items) {
+  constexpr int D = 128;
+  __shared__ float red_mn[4][D], red_mx[4][D];
+  __shared__ float meta_l[D], meta_s[D], meta_r[D];
+  const int s = threadIdx.x & 15, rl = threadIdx.x >> 4, wave = threadIdx.x >> 6;
+  const int qmax = (1 << bits) - 1;
+  Slab<DT> cur[RPT], nxt[RPT];
+  auto row_ok = [&](int64_t item, int j) -> bool {
+    const int gi = static_cast<int>(item % n_g);
+    return rl + 16 * j < group && gi * group + rl + 16 * j < n;
+  };
+  auto issue = [&](int64_t item, Slab<DT> (&r)[RPT]) {
+    if (item >= n_items) return;
+    const int gi = static_cast<int>(item % n_g), bh = static_cast<int>(item / n_g);
+    const int b = bh / H, h = bh % H;
+    const int64_t base = static_cast<int64_t>(b) * sb + static_cast<int64_t>(h) * sh + s * 8;
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+      if (row_ok(item, j)) slab_load<DT>(x, base + static_cast<int64_t>(n_sink + gi * group + rl + 16 * j) * st, r[j]);
+  };
+  int64_t item = blockIdx.x;
+  issue(item, cur);
+  for (; item < n_items; item += gridDim.x) {
+    issue(item + gridDim.x, nxt);
+    const int gi = static_cast<int>(item % n_g), bh = static_cast<int>(item / n_g);
+    const int t0 = gi * group;
+    float v[RPT][8];
+    float mn[8], mx[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      mn[k] = INFINITY;
+      mx[k] = -INFINITY;
+    }
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      if (row_ok(item, j)) {
+        slab_values<DT>(cur[j], v[j]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          mn[k] = fminf(mn[k], v[j][k]);
+          mx[k] = fmaxf(mx[k], v[j][k]);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        mn[k] = fminf(mn[k], __shfl_xor(mn[k], o, 64));
+        mx[k] = fmaxf(mx[k], __shfl_xor(mx[k], o, 64));
+      }
+    }
+    __syncthreads();                              // the previous item's reads of red_* / meta are done
+    if ((threadIdx.x & 63) < 16) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        red_mn[wave][s * 8 + k] = mn[k];
+        red_mx[wave][s * 8 + k] = mx[k];
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < D) {                        // one thread per channel: lo, scale, 1 / scale
+      const int c = threadIdx.x;
+      const float a = fminf(fminf(red_mn[0][c], red_mn[1][c]), fminf(red_mn[2][c], red_mn[3][c]));
+      const float z = fmaxf(fmaxf(red_mx[0][c], red_mx[1][c]), fmaxf(red_mx[2][c], red_mx[3][c]));
+      const float l = as_stored(a);
+      const float q = fmaxf(as_stored(__fdiv_rn(__fsub_rn(z, l), static_cast<float>(qmax))), kMinScale);
+      meta_l[c] = l;
+      meta_s[c] = q;
+      meta_r[c] = __fdiv_rn(1.0f, q);
+    }
+    __syncthreads();
+    float lo[8], sc[8], rc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      lo[k] = meta_l[s * 8 + k];
+      sc[k] = meta_s[s * 8 + k];
+      rc[k] = meta_r[s * 8 + k];
+    }
+    if (rl == 0) {
+      const int64_t mo = static_cast<int64_t>(bh) * meta_bh + static_cast<int64_t>(gi) * D + s * 8;
+      uint4 wl, ws_;
+      wl.x = f32_to_f16(lo[0]) | (static_cast<uint32_t>(f32_to_f16(lo[1])) << 16);
+      wl.y = f32_to_f16(lo[2]) | (static_cast<uint32_t>(f32_to_f16(lo[3])) << 16);
+      wl.z = f32_to_f16(lo[4]) | (static_cast<uint32_t>(f32_to_f16(lo[5])) << 16);
+      wl.w = f32_to_f16(lo[6]) | (static_cast<uint32_t>(f32_to_f16(lo[7])) << 16);
+      ws_.x = f32_to_f16(sc[0]) | (static_cast<uint32_t>(f32_to_f16(sc[1])) << 16);
+      ws_.y = f32_to_f16(sc[2]) | (static_cast<uint32_t>(f32_to_f16(sc[3])) << 16);
+      ws_.z = f32_to_f16(sc[4]) | (static_cast<uint32_t>(f32_to_f16(sc[5])) << 16);
+      ws_.w = f32_to_f16(sc[6]) | (static_cast<uint32_t>(f32_to_f16(sc[7])) << 16);
+      *reinterpret_cast<uint4*>(lo_out + mo) = wl;
+      *reinterpret_cast<uint4*>(sc_out + mo) = ws_;
+    }
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      if (!row_ok(item, j)) continue;
+      const int t = t0 + rl + 16 * j;
+      int cd[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cd[k] = quant_code_r(v[j][k], lo[k], sc[k], rc[k], qmax);
+      store_slab(cd, bits,
+                 packed ? packed + static_cast<int64_t>(bh) * packed_bh + static_cast<int64_t>(t) * (D * bits / 8) + s * bits
+                        : nullptr,
+                 codes ? codes + static_cast<int64_t>(bh) * codes_bh + static_cast<int64_t>(t) * D + s * 8 : nullptr,
+                 xhat ? xhat + (static_cast<int64_t>(bh) * T + n_sink + t) * D + s * 8 : nullptr, lo, sc);
+    }
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) cur[j] = nxt[j];
+  }
+}
+
+// Values, d == 128: a 256-thread block walks items of 16 x VR rows with a grid stride (thread:
+// slab s = t % 16 of rows 16 r + t / 16, r < VR), loading the next item while coding the current
+// one; a channel group of `width` channels is width / 8 consecutive lanes (butterfly shuffles).
+template <int DT, int VR>
+__global__ __launch_bounds__(256) void kivi_quant_values_v(const void* __restrict__ x, int H, int64_t sb, int64_t sh,
+                                                            int64_t st, int n_sink, int n, int bits, int width,
+                                                            uint8_t* __restrict__ codes, int64_t codes_bh,
+                                                            uint8_t* __restrict__ packed, int64_t packed_bh,
+                                                            uint16_t* __restrict__ lo_out, uint16_t* __restrict__ sc_out,
+                                                            int64_t meta_bh, float* __restrict__ xhat, int T,
+                                                            int n_rb, int64_t n_items) {
+  constexpr int D = 128;
+  const int s = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const int lanes = width / 8;
+  const int qmax = (1 << bits) - 1;
+  Slab<DT> cur[VR], nxt[VR];
+  auto issue = [&](int64_t item, Slab<DT> (&r)[VR]) {
+    if (item >= n_items) return;
+    const int rb = static_cast<int>(item % n_rb), bh = static_cast<int>(item / n_rb);
+    const int b = bh / H, h = bh % H;
+    const int64_t base = static_cast<int64_t>(b) * sb + static_cast<int64_t>(h) * sh + s * 8;
+#pragma unroll
+    for (int j = 0; j < VR; ++j) {
+      const int t = rb * 16 * VR + 16 * j + rl;
+      if (t < n) slab_load<DT>(x, base + static_cast<int64_t>(n_sink + t) * st, r[j]);
+    }
+  };
+  int64_t item = blockIdx.x;
+  issue(item, cur);
+  for (; item < n_items; item += gridDim.x) {
+    issue(item + gridDim.x, nxt);
+    const int rb = static_cast<int>(item % n_rb), bh = static_cast<int>(item / n_rb);
+#pragma unroll
+    for (int j = 0; j < VR; ++j) {
+      const int t = rb * 16 * VR + 16 * j + rl;
+      const bool valid = t < n;
+      float v[8];
+      float mn = INFINITY, mx = -INFINITY;
+      if (valid) {
+        slab_values<DT>(cur[j], v);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          mn = fminf(mn, v[k]);
+          mx = fmaxf(mx, v[k]);
+        }
+      }
+      for (int off = 1; off < lanes; off <<= 1) {
+        mn = fminf(mn, __shfl_xor(mn, off, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      }
+      if (!valid) continue;
+      const float l1 = as_stored(mn);
+      const float s1 = fmaxf(as_stored(__fdiv_rn(__fsub_rn(mx, l1), static_cast<float>(qmax))), kMinScale);
+      if ((s * 8) % width == 0) {
+        const int64_t mo = static_cast<int64_t>(bh) * meta_bh + static_cast<int64_t>(t) * (D / width) + (s * 8) / width;
+        lo_out[mo] = f32_to_f16(l1);
+        sc_out[mo] = f32_to_f16(s1);
+      }
+      float lo[8], sc[8];
+      int cd[8];
+      const float r1 = __fdiv_rn(1.0f, s1);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        lo[k] = l1;
+        sc[k] = s1;
+        cd[k] = quant_code_r(v[k], l1, s1, r1, qmax);
+      }
+      store_slab(cd, bits,
+                 packed ? packed + static_cast<int64_t>(bh) * packed_bh + static_cast<int64_t>(t) * (D * bits / 8) + s * bits
+                        : nullptr,
+                 codes ? codes + static_cast<int64_t>(bh) * codes_bh + static_cast<int64_t>(t) * D + s * 8 : nullptr,
+                 xhat ? xhat + (static_cast<int64_t>(bh) * T + n_sink + t) * D + s * 8 : nullptr, lo, sc);
+    }
+#pragma unroll
+    for (int j = 0; j < VR; ++j) cur[j] = nxt[j];
   }
 }
 
@@ -313,6 +633,43 @@ extern "C" int kvq_kivi_quant(const void* x, int x_dtype, int64_t B, int64_t H, 
     KVQ_LAUNCH_CHECK("kvq_kivi_quant(sinks)");
   }
   if (n == 0) return KVQ_OK;
+  auto al = [](const void* p, uintptr_t a) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % a == 0; };
+  const bool vec = d == 128 && al(x, 16) && sb % 8 == 0 && sh % 8 == 0 && st % 8 == 0 && al(packed, 16) &&
+                   packed_bh % 8 == 0 && al(codes, 16) && codes_bh % 8 == 0 && al(xhat, 16) && al(lo, 16) &&
+                   al(scale, 16) && meta_bh % 8 == 0;
+  if (along_tokens && vec && group <= 128) {
+    const int n_g = (n + group - 1) / group;
+    const int rpt = (group + 15) / 16;
+    // one resident round of blocks (256 CUs x 4 blocks at these kernels' register use)
+    const int64_t n_items = static_cast<int64_t>(n_g) * B * H;
+    const unsigned grid = static_cast<unsigned>(KVQ_QUANT_GRID > 0 ? std::min<int64_t>(n_items, KVQ_QUANT_GRID) : n_items);
+#define KVQ_KEYS_V(RPT_)                                                                                     \
+    KVQ_DISPATCH_DTYPE(x_dtype, hipLaunchKernelGGL((kivi_quant_keys_v<DT_, RPT_>), dim3(grid), dim3(256), 0, s,  \
+                                                   x, (int)H, sb, sh, st, n_sink, n, bits, group, codes, codes_bh,      \
+                                                   packed, packed_bh, lo, scale, meta_bh, xhat, (int)T, n_g, n_items))
+    if (rpt <= 1) { KVQ_KEYS_V(1); }
+    else if (rpt <= 2) { KVQ_KEYS_V(2); }
+    else if (rpt <= 4) { KVQ_KEYS_V(4); }
+    else { KVQ_KEYS_V(8); }
+#undef KVQ_KEYS_V
+    KVQ_LAUNCH_CHECK("kvq_kivi_quant(keys)");
+    return KVQ_OK;
+  }
+  if (!along_tokens && vec) {
+    const int64_t width = (d % group == 0) ? group : d;
+    if (width % 8 == 0 && ((width / 8) & (width / 8 - 1)) == 0) {
+      constexpr int kVR = 4;
+      const int n_rb = (n + 16 * kVR - 1) / (16 * kVR);
+      const int64_t n_items = static_cast<int64_t>(n_rb) * B * H;
+      const unsigned grid = static_cast<unsigned>(KVQ_QUANT_GRID > 0 ? std::min<int64_t>(n_items, KVQ_QUANT_GRID) : n_items);
+      KVQ_DISPATCH_DTYPE(x_dtype, hipLaunchKernelGGL((kivi_quant_values_v<DT_, kVR>), dim3(grid), dim3(256), 0, s,
+                                                     x, (int)H, sb, sh, st, n_sink, n, bits, (int)width, codes,
+                                                     codes_bh, packed, packed_bh, lo, scale, meta_bh, xhat, (int)T,
+                                                     n_rb, n_items));
+      KVQ_LAUNCH_CHECK("kvq_kivi_quant(values)");
+      return KVQ_OK;
+    }
+  }
   if (along_tokens) {
     KVQ_REQUIRE(d <= 1024 && d % 64 == 0, "kvq_kivi_quant(keys): d must be a multiple of 64 <= 1024");
     const int n_g = (n + group - 1) / group;
