@@ -11,6 +11,7 @@ The other rows of the path are measured by the same script with ``--workload``:
   c3      mixed 2/4/8-bit 64-token blocks (B=8, Hq=32, Hkv=8, T=16384, group 32)
   c4      eviction: 32 score-accumulating decode steps, top-k 2048 + 256 window, retained decode
   c5      DCT-coded context (B=1, Hq=64, Hkv=8, T=131072): decode, and the encoder
+  strata  STRATA strata (per-token 8/4/2-bit tiers) at the C3 shape
   append  streaming append of one token per sequence at the C2 shape (µs/step)
   quant   prefill quantise + pack of the C2 context (kivi_quant of K and V)
 Each prints one JSON line of the same form (its own metric, roofline and CPU baseline).
@@ -274,6 +275,67 @@ def run_c3(args) -> dict:
                                "us_per_layer": t * 1e6,
                                "sample": f"{len(times)} of {len(pairs)} (batch, KV-head) pairs; median per pair x "
                                          f"{len(pairs)}; numpy per-block dequantise + chunked_attention"}
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+# A6 at the C3 shape: STRATA strata (per-token widths 8/4/2 by the C3 importance rule)
+
+def run_strata(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    from kvq.synth import C3, c3_inputs
+    s = C3
+    log("generating C3 inputs (per-token strata)")
+    q, K, V, imp = c3_inputs("cuda")
+    tok_imp = imp.repeat_interleave(64, dim=-1)                       # the block importance, per token
+    order = torch.argsort(-tok_imp, dim=-1, stable=True).to(torch.int32)
+    n8 = int(0.1 * s.T)
+    n4 = int(0.4 * s.T) - n8
+    assign = [(8, order[..., :n8].contiguous()), (4, order[..., n8:n8 + n4].contiguous()),
+              (2, order[..., n8 + n4:].contiguous())]
+    cache = kvq.StrataCache.from_context(K, V, window=0, assign=assign)
+    scaling = s.d ** -0.5
+    out = torch.empty((s.B, 1, s.Hq, s.d), dtype=s.dtype, device="cuda")
+    ws = torch.empty((kvq.strata_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.n_exact, [t.n for t in cache.tiers],
+                                                  [t.bits for t in cache.tiers]),), dtype=torch.float32, device="cuda")
+    step = lambda: kvq.strata_decode(q, scaling, cache, out=out, workspace=ws)
+    ms, g_ms = step_ms(step, args.steps, args.warmup)
+    qb = q.numel() * q.element_size()
+    bytes_alg = cache.coded_bytes() + qb + out.numel() * out.element_size()
+    res = _result(args, metric="STRATA strata decode (per-token 8/4/2-bit tiers): effective HBM GB/s + µs/layer",
+                  value=bytes_alg / (ms * 1e-3) / 1e9, unit="GB/s", ms_per_step=ms,
+                  workload="A6 at the C3 shape: one decode step over STRATA strata (rotated, per-token scales; "
+                           "tokens ranked by the C3 block importance, top 10% 8-bit, next 30% 4-bit, rest 2-bit; "
+                           "B=8, Hq=32, Hkv=8, d=128, T=16384, no exact rows)",
+                  config={"global_batch": s.B, "seq_len": s.T, "parallelism": "single GPU",
+                          "tokens_8_4_2": [n8, n4, s.T - n8 - n4]},
+                  dtype="bf16", roofline=_roof(bytes_alg, ms, "strata_split_all + strata_merge (whole step)"),
+                  us_per_layer=round(ms * 1e3, 3), graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg)
+    log(f"STRATA step {ms * 1e3:.1f} us")
+    if not args.no_cpu_baseline:
+        import oracle.strata as os_
+        Rm = os_.rotation_matrix(s.d)
+        times = []
+        for b in range(s.B):
+            tiers = []
+            for t in cache.tiers:
+                tiers.append((t.bits, os_.unpack_planar(t.kc[b].cpu().numpy(), t.bits), t.ks[b, :, :t.n].float().cpu().numpy(),
+                              os_.unpack_planar(t.vc[b].cpu().numpy(), t.bits), t.vs[b].float().cpu().numpy()))
+            qb_ = q[b:b + 1].float().cpu().numpy()
+            empty = np.zeros((s.Hkv, 0, s.d))
+            t0 = time.perf_counter()
+            os_.strata_attend(qb_, scaling, empty, empty, tiers, cache.mu_k[b].float().cpu().numpy(),
+                              cache.mu_v[b].float().cpu().numpy(), Rm)
+            times.append(time.perf_counter() - t0)
+            if sum(times) >= args.cpu_seconds and len(times) >= 1:
+                break
+        t = float(np.median(times)) * s.B
+        res["cpu_baseline"] = {"value": bytes_alg / t / 1e9, "unit": "GB/s", "cores": _threads(), "kind": "port",
+                               "us_per_layer": t * 1e6,
+                               "sample": f"{len(times)} of {s.B} sequences (all 8 KV heads each); median x {s.B}; "
+                                         f"numpy tier_reference per stratum + merge (float64)"}
     return res
 
 
@@ -547,7 +609,7 @@ def run_quant(args) -> dict:
 
 
 WORKLOADS = {"c2": lambda a: run_kivi(a, "c2"), "c1": lambda a: run_kivi(a, "c1"), "c3": run_c3, "c4": run_c4,
-             "c5": run_c5, "append": run_append, "quant": run_quant}
+             "c5": run_c5, "strata": run_strata, "append": run_append, "quant": run_quant}
 
 
 def main() -> int:

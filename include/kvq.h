@@ -217,7 +217,7 @@ int kvq_strata_v_tile(const uint8_t* rows, int64_t BH, int64_t n, int64_t rows_b
  * output = [w_e o_exact + (sum_t w_t acc_t) R + (sum_t w_t l_t) mu_V] / (sum of all w l).
  * ---------------------------------------------------------------------------------------- */
 int64_t kvq_strata_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t n_exact,
-                                    int n_tiers, const int64_t* tier_n);
+                                    int n_tiers, const int* tier_bits, const int64_t* tier_n);
 int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B, int64_t Hq,
                       int64_t Hkv, int64_t Tq, int64_t d, float scaling, const float* signs, const uint16_t* mu_k,
                       const uint16_t* mu_v, int n_tiers, const int* tier_bits, const int64_t* tier_n,

@@ -264,8 +264,12 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
 // summed over the rows of the KV head and accumulated into the scores row (no value work).
 template <int R, int GV, int DT, bool SCORE>
 __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* smem) {
-  constexpr int VPB = 16 / R;                       // PV columns per row: (group, hi/lo) variants
-  constexpr int GPB = VPB / 2;                      // channel groups per PV B operand
+  // fp32 output: p * sv enters the PV product as hi + lo fp16 parts (two column variants per
+  // group); 16-bit outputs take the single fp16 rounding (relative error 2^-12 per term, far
+  // below the output's own rounding), one column per group
+  constexpr bool LO = DT == KVQ_F32;
+  constexpr int VPB = 16 / R;                       // PV columns per row: (group[, hi/lo]) variants
+  constexpr int GPB = LO ? VPB / 2 : VPB;           // channel groups per PV B operand
   constexpr int NGV = kD / GV;                      // channel groups of a value row
   constexpr int NB = (NGV + GPB - 1) / GPB;         // PV B operands
   const int b = bh / p.Hkv, h = bh % p.Hkv;
@@ -282,7 +286,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   const int r_n = n % R;
   const int hl_qk = (n / R) & 1;
   const int v_pv = n / R;
-  const int gcl = v_pv >> 1, hl_pv = v_pv & 1;
+  const int gcl = LO ? (v_pv >> 1) : v_pv, hl_pv = LO ? (v_pv & 1) : 0;
   // cooperative operand preparation: this lane owns channels c0, c1 (slots 2ck, 2ck+1 of k-step ci)
   const int ci = (l >> 2) & 3, ck = l & 3;
   const int c0 = 32 * g + 8 * ci + kCos[2 * ck];
@@ -512,10 +516,14 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
         // lo = fp16(p * sv - hi), again from the exact product
         const half2v hi = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], static_cast<float>(m0[0]), 0.0f)),
                                  static_cast<_Float16>(__builtin_fmaf(pr[j1], static_cast<float>(m1[0]), 0.0f))};
-        const half2v cn = hi * hl_neg;                                  // 0 (hi lanes) or -hi (lo lanes)
-        const half2v val = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], static_cast<float>(m0[0]), static_cast<float>(cn[0]))),
-                                  static_cast<_Float16>(__builtin_fmaf(pr[j1], static_cast<float>(m1[0]), static_cast<float>(cn[1])))};
-        words[jj] = w2(val);
+        if constexpr (LO) {
+          const half2v cn = hi * hl_neg;                                // 0 (hi lanes) or -hi (lo lanes)
+          const half2v val = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], static_cast<float>(m0[0]), static_cast<float>(cn[0]))),
+                                    static_cast<_Float16>(__builtin_fmaf(pr[j1], static_cast<float>(m1[0]), static_cast<float>(cn[1])))};
+          words[jj] = w2(val);
+        } else {
+          words[jj] = w2(hi);
+        }
         float& z = ((j0 & 3) >= 2) ? Zb[bb] : Za[bb];
         z = __builtin_fmaf(pr[j0], static_cast<float>(m0[1]), z);
         z = __builtin_fmaf(pr[j1], static_cast<float>(m1[1]), z);
@@ -557,11 +565,12 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     const int gcb = (16 * blk) / GV;
-    const bool mine = hl_pv == 1 && (gcb % GPB) == gcl;
+    const bool mine = (!LO || hl_pv == 1) && (gcb % GPB) == gcl;
     const float Zv = Z[gcb / GPB];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float a = acc[blk][i] + dpp<kRowShr + R>(acc[blk][i]);   // hi + lo columns
+      float a = acc[blk][i];
+      if constexpr (LO) a += dpp<kRowShr + R>(acc[blk][i]);            // hi + lo columns
       if (mine) red_o[(wave * R + r_n) * kD + 16 * blk + 4 * g + i] = __builtin_fmaf(a, kTwo24, Zv);
     }
   }

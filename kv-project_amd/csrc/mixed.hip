@@ -136,18 +136,21 @@ struct MixedParams {
   float* ws_l;
 };
 
-template <int R>
+// LO (fp32 output): p * scale enters the PV product as hi + lo fp16 parts, two column variants
+// per channel group; 16-bit outputs take the single fp16 rounding (relative error 2^-12 per
+// term, below the output's own rounding), one column per group.
+template <int R, bool LO>
 struct MixedGeom {
-  static constexpr int VPB = 16 / R;               // PV columns per row: (group, hi/lo) variants
-  static constexpr int GPB = VPB / 2;              // channel groups per PV B operand
+  static constexpr int VPB = 16 / R;               // PV columns per row: (group[, hi/lo]) variants
+  static constexpr int GPB = LO ? VPB / 2 : VPB;   // channel groups per PV B operand
   static constexpr int NB = (4 + GPB - 1) / GPB;   // PV B operands (4 groups of 32 channels)
 };
 
-template <int R>
+template <int R, bool LO>
 struct MixedState {
   f32x4 acc[8];
   float m_run, la;
-  float Z[MixedGeom<R>::NB];
+  float Z[MixedGeom<R, LO>::NB];
 };
 
 struct MixedLane {
@@ -155,10 +158,10 @@ struct MixedLane {
 };
 
 // Blocks [kb0, kb1) of one width segment starting at byte seg_so of the (b, h) region.
-template <int BITS, int R>
-__device__ __forceinline__ void mixed_run(MixedState<R>& st, const MixedLane& L, const float (*qs)[kMD], uint32_t* bq,
+template <int BITS, int R, bool LO>
+__device__ __forceinline__ void mixed_run(MixedState<R, LO>& st, const MixedLane& L, const float (*qs)[kMD], uint32_t* bq,
                                           uint32_t* bv, __amdgpu_buffer_rsrc_t rs, uint32_t seg_so, int kb0, int kb1) {
-  using Geo = MixedGeom<R>;
+  using Geo = MixedGeom<R, LO>;
   constexpr int NB = Geo::NB, GPB = Geo::GPB;
   constexpr int RB = 16 * BITS;                    // bytes per planar key row
   constexpr int SEG = (BITS + 1) * kUnit;
@@ -324,10 +327,14 @@ __device__ __forceinline__ void mixed_run(MixedState<R>& st, const MixedLane& L,
         const half2v m1 = h2(c.mw[bb][j1 >> 2][j1 & 3]);
         const half2v hi = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], static_cast<float>(m0[0]), 0.0f)),
                                  static_cast<_Float16>(__builtin_fmaf(pr[j1], static_cast<float>(m1[0]), 0.0f))};
-        const half2v cn = hi * hl_neg;
-        const half2v val = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], static_cast<float>(m0[0]), static_cast<float>(cn[0]))),
-                                  static_cast<_Float16>(__builtin_fmaf(pr[j1], static_cast<float>(m1[0]), static_cast<float>(cn[1])))};
-        words[jj] = w2(val);
+        if constexpr (LO) {
+          const half2v cn = hi * hl_neg;
+          const half2v val = half2v{static_cast<_Float16>(__builtin_fmaf(pr[j0], static_cast<float>(m0[0]), static_cast<float>(cn[0]))),
+                                    static_cast<_Float16>(__builtin_fmaf(pr[j1], static_cast<float>(m1[0]), static_cast<float>(cn[1])))};
+          words[jj] = w2(val);
+        } else {
+          words[jj] = w2(hi);
+        }
         zc[cls(j0)][bb] = __builtin_fmaf(pr[j0], static_cast<float>(m0[1]), zc[cls(j0)][bb]);
         zc[cls(j1)][bb] = __builtin_fmaf(pr[j1], static_cast<float>(m1[1]), zc[cls(j1)][bb]);
       }
@@ -376,7 +383,8 @@ __device__ __forceinline__ int mixed_first_block(int64_t c, int n8, int n4, int 
 
 template <int R, int DT>
 __device__ void mixed_block(const MixedParams& p, int bh, int sidx, float* smem) {
-  using Geo = MixedGeom<R>;
+  constexpr bool LO = DT == KVQ_F32;
+  using Geo = MixedGeom<R, LO>;
   constexpr int NB = Geo::NB, GPB = Geo::GPB;
   const int b = bh / p.Hkv, h = bh % p.Hkv;
   float (*qs)[kMD] = reinterpret_cast<float (*)[kMD]>(smem);
@@ -401,8 +409,8 @@ __device__ void mixed_block(const MixedParams& p, int bh, int sidx, float* smem)
   L.r_n = L.n % R;
   L.hl_qk = (L.n / R) & 1;
   const int v_pv = L.n / R;
-  L.gcl = v_pv >> 1;
-  L.hl_pv = v_pv & 1;
+  L.gcl = LO ? (v_pv >> 1) : v_pv;
+  L.hl_pv = LO ? (v_pv & 1) : 0;
   L.ci = (L.l >> 2) & 3;
   L.ck = L.l & 3;
   uint32_t* bq = bq_all + wave * 2 * R * 64;
@@ -419,7 +427,7 @@ __device__ void mixed_block(const MixedParams& p, int bh, int sidx, float* smem)
   const int i1 = mixed_first_block(C * (w_all + 1) / NW, n8, n4, n2);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.buf + base * kUnit, static_cast<uint32_t>(C * kUnit));
 
-  MixedState<R> st;
+  MixedState<R, LO> st;
 #pragma unroll
   for (int k = 0; k < 8; ++k) st.acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
   st.m_run = -INFINITY;
@@ -428,15 +436,15 @@ __device__ void mixed_block(const MixedParams& p, int bh, int sidx, float* smem)
   for (int bb = 0; bb < NB; ++bb) st.Z[bb] = 0.0f;
   {
     const int a = i0, e = min(i1, n8);
-    if (a < e) mixed_run<8, R>(st, L, qs, bq, bv, rs, 0u, a, e);
+    if (a < e) mixed_run<8, R, LO>(st, L, qs, bq, bv, rs, 0u, a, e);
   }
   {
     const int a = max(i0, n8) - n8, e = min(i1, n8 + n4) - n8;
-    if (a < e) mixed_run<4, R>(st, L, qs, bq, bv, rs, static_cast<uint32_t>(9 * n8) * kUnit, a, e);
+    if (a < e) mixed_run<4, R, LO>(st, L, qs, bq, bv, rs, static_cast<uint32_t>(9 * n8) * kUnit, a, e);
   }
   {
     const int a = max(i0, n8 + n4) - (n8 + n4), e = i1 - (n8 + n4);
-    if (a < e) mixed_run<2, R>(st, L, qs, bq, bv, rs, static_cast<uint32_t>(9 * n8 + 5 * n4) * kUnit, a, e);
+    if (a < e) mixed_run<2, R, LO>(st, L, qs, bq, bv, rs, static_cast<uint32_t>(9 * n8 + 5 * n4) * kUnit, a, e);
   }
 
   // ---- wavefront epilogue (as the packed 4-bit kernel) ----
@@ -451,11 +459,12 @@ __device__ void mixed_block(const MixedParams& p, int bh, int sidx, float* smem)
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     const int gcb = blk >> 1;
-    const bool mine = L.hl_pv == 1 && (gcb % GPB) == L.gcl;
+    const bool mine = (!LO || L.hl_pv == 1) && (gcb % GPB) == L.gcl;
     const float Zv = Z[gcb / GPB];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float a = st.acc[blk][i] + dpp<kRowShr + R>(st.acc[blk][i]);
+      float a = st.acc[blk][i];
+      if constexpr (LO) a += dpp<kRowShr + R>(st.acc[blk][i]);
       if (mine) red_o[(wave * R + L.r_n) * kMD + 16 * blk + 4 * L.g + i] = __builtin_fmaf(a, kTwo24, Zv);
     }
   }
@@ -486,8 +495,18 @@ __device__ void mixed_block(const MixedParams& p, int bh, int sidx, float* smem)
   }
 }
 
+// waves per SIMD the split kernel's registers target: 3 where that fits without spilling in the
+// loop (16-bit output, R <= 4), else 2; KVQ_MIXED_WAVES overrides it at build time
+#ifndef KVQ_MIXED_WAVES
+#define KVQ_MIXED_WAVES 0
+#endif
 template <int R, int DT>
-__global__ __launch_bounds__(kMThreads) __attribute__((amdgpu_waves_per_eu(2)))
+constexpr int mixed_waves() {
+  return KVQ_MIXED_WAVES > 0 ? KVQ_MIXED_WAVES : ((DT != KVQ_F32 && R <= 4) ? 3 : 2);
+}
+
+template <int R, int DT>
+__global__ __launch_bounds__(kMThreads) __attribute__((amdgpu_waves_per_eu(mixed_waves<R, DT>())))
 void mixed_split(MixedParams p) {
   extern __shared__ float smem[];
   const int k = blockIdx.x / 8;
@@ -532,7 +551,9 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
 namespace {
 int64_t mixed_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t nb, int64_t n_exact, int64_t* ex_floats,
                        int* S) {
-  *S = nb > 0 ? kvq::plan_block_splits(B * Hkv, nb, 2, 4) : 0;
+  // resident blocks per CU = waves per SIMD of the variant (one wavefront of each block per SIMD)
+  const int64_t Rr = kvq::pow2_rows((Hq / Hkv) * Tq);
+  *S = nb > 0 ? kvq::plan_block_splits(B * Hkv, nb, (Rr <= 4) ? 3 : 2, 4) : 0;
   *ex_floats = n_exact > 0 ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
   const int64_t R = kvq::pow2_rows((Hq / Hkv) * Tq);
   return *ex_floats + B * Hkv * static_cast<int64_t>(*S) * R * (128 + 2);

@@ -281,6 +281,18 @@ namespace {
 constexpr int kSThreads = 256;
 constexpr int kSWaves = 4;
 
+constexpr int kMaxTiers = 16;
+
+// One stratum of the launch: its codes, scales and split range [s_base, s_base + n_split).
+struct StrataTierArg {
+  const uint8_t* kc;            // (BH, n_t, d*bits/8) planar rows
+  const uint16_t* ks;           // (BH, cap_t) fp16, zero past n_t
+  const uint8_t* vt;            // (BH, cap_t/32, 512*bits) value tiles
+  const uint16_t* vsl;          // (BH, cap_t/32, 32) fp16 slot-ordered value scales
+  int64_t n_t, cap_t;           // tier tokens, tile capacity
+  int n_split, s_base, bits;
+};
+
 struct StrataParams {
   const void* q;
   int64_t q_sb, q_sh, q_st;
@@ -289,16 +301,12 @@ struct StrataParams {
   const float* signs;           // (d) +-1
   const uint16_t* mu_k;         // (BH, d) fp16
   const uint16_t* mu_v;
-  int64_t n_t, cap_t;           // tier tokens, tile capacity
-  const uint8_t* kc;            // (BH, n_t, d*bits/8) planar rows
-  const uint16_t* ks;           // (BH, cap_t) fp16, zero past n_t
-  const uint8_t* vt;            // (BH, cap_t/32, 512*bits) value tiles
-  const uint16_t* vsl;          // (BH, cap_t/32, 32) fp16 slot-ordered value scales
-  int n_split;
+  int n_tiers;                  // strata with tokens, in launch order
+  StrataTierArg tiers[kMaxTiers];
   float* ws_o;                  // tier partials (BH * S_all partials)
   float* ws_m;
   float* ws_l;
-  int S_all, s_base;
+  int S_all;
   const float* ex_o;            // exact-row partials (BH * S_ex partials)
   const float* ex_m;
   const float* ex_l;
@@ -322,7 +330,7 @@ struct StrataChunk {
 };
 
 template <int BITS, int R, int DT>
-__device__ void strata_block(const StrataParams& p, int bh, int sidx, float* smem) {
+__device__ void strata_block(const StrataParams& p, const StrataTierArg& ta, int bh, int sidx, float* smem) {
   constexpr int NCLS = BITS == 2 ? 4 : (BITS == 4 ? 2 : 1);   // probability classes (code factors)
   constexpr int RB = 16 * BITS;                 // bytes per planar row
   const int b = bh / p.Hkv, h = bh % p.Hkv;
@@ -384,23 +392,23 @@ __device__ void strata_block(const StrataParams& p, int bh, int sidx, float* sme
   constexpr float kDotScale = static_cast<float>(1 << (24 - smax_shift<BITS>()));   // dot = D * this
 
   // ---- this wavefront's chunk range (balanced over the split's 4 wavefronts and all splits) ----
-  const int NC = static_cast<int>((p.n_t + 31) / 32);
-  const int NW = p.n_split * kSWaves;
+  const int NC = static_cast<int>((ta.n_t + 31) / 32);
+  const int NW = ta.n_split * kSWaves;
   const int w_all = sidx * kSWaves + wave;
   const int t0 = 32 * static_cast<int>(static_cast<int64_t>(w_all) * NC / NW);
-  const int t1 = min(32 * static_cast<int>(static_cast<int64_t>(w_all + 1) * NC / NW), static_cast<int>(p.n_t));
+  const int t1 = min(32 * static_cast<int>(static_cast<int64_t>(w_all + 1) * NC / NW), static_cast<int>(ta.n_t));
   const int t_last = t0 < t1 ? t0 + ((t1 - 1 - t0) & ~31) : t0;
 
   const __amdgpu_buffer_rsrc_t rk =
-      make_rsrc(p.kc + static_cast<int64_t>(bh) * p.n_t * RB, static_cast<uint32_t>(p.n_t * RB));
+      make_rsrc(ta.kc + static_cast<int64_t>(bh) * ta.n_t * RB, static_cast<uint32_t>(ta.n_t * RB));
   // key scales padded to the tile capacity: a 4-token load never straddles the end of the row
   const __amdgpu_buffer_rsrc_t rks =
-      make_rsrc(p.ks + static_cast<int64_t>(bh) * p.cap_t, static_cast<uint32_t>(p.cap_t * 2));
+      make_rsrc(ta.ks + static_cast<int64_t>(bh) * ta.cap_t, static_cast<uint32_t>(ta.cap_t * 2));
   const __amdgpu_buffer_rsrc_t rv =
-      make_rsrc(p.vt + static_cast<int64_t>(bh) * (p.cap_t / 32) * 512 * BITS,
-                static_cast<uint32_t>((p.cap_t / 32) * 512 * BITS));
+      make_rsrc(ta.vt + static_cast<int64_t>(bh) * (ta.cap_t / 32) * 512 * BITS,
+                static_cast<uint32_t>((ta.cap_t / 32) * 512 * BITS));
   const __amdgpu_buffer_rsrc_t rvs =
-      make_rsrc(p.vsl + static_cast<int64_t>(bh) * p.cap_t, static_cast<uint32_t>(p.cap_t * 2));
+      make_rsrc(ta.vsl + static_cast<int64_t>(bh) * ta.cap_t, static_cast<uint32_t>(ta.cap_t * 2));
   const int vo_k = n * RB + g * 4 * BITS;
 
   using Chunk = StrataChunk<BITS>;
@@ -557,7 +565,7 @@ __device__ void strata_block(const StrataParams& p, int bh, int sidx, float* sme
     red_ml[(wave * 2 + 1) * R + n] = l_run;
   }
   __syncthreads();
-  const int64_t po = static_cast<int64_t>(bh) * p.S_all + p.s_base + sidx;
+  const int64_t po = static_cast<int64_t>(bh) * p.S_all + ta.s_base + sidx;
   for (int idx = threadIdx.x; idx < p.R_real * kSD; idx += kSThreads) {
     const int r = idx / kSD, c = idx % kSD;
     float M = -INFINITY;
@@ -579,74 +587,93 @@ __device__ void strata_block(const StrataParams& p, int bh, int sidx, float* sme
   }
 }
 
-template <int BITS, int R, int DT>
-__global__ __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(BITS == 8 ? 2 : 3)))
-void strata_tier_split(StrataParams p) {
+// Every stratum in one launch: block id -> (XCD-aware) bh and split index over all strata; the
+// stratum owning the split picks the width-specialised body.  W: waves per SIMD the registers
+// target (3: every width's body fits 164 VGPRs).
+template <int R, int DT, int W>
+__global__ __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(W)))
+void strata_split_all(StrataParams p) {
   extern __shared__ float smem[];
   const int k = blockIdx.x / 8;
-  const int bh = blockIdx.x % 8 + 8 * (k / p.n_split);
-  if (bh < p.BH) strata_block<BITS, R, DT>(p, bh, k % p.n_split, smem);
+  const int bh = blockIdx.x % 8 + 8 * (k / p.S_all);
+  if (bh >= p.BH) return;
+  const int sa = k % p.S_all;
+  int t = 0;
+  while (t + 1 < p.n_tiers && sa >= p.tiers[t + 1].s_base) ++t;
+  const StrataTierArg& ta = p.tiers[t];
+  const int sidx = sa - ta.s_base;
+  if (ta.bits == 8) strata_block<8, R, DT>(p, ta, bh, sidx, smem);
+  else if (ta.bits == 4) strata_block<4, R, DT>(p, ta, bh, sidx, smem);
+  else strata_block<2, R, DT>(p, ta, bh, sidx, smem);
 }
 
-// Merge of one (b, h): exact-row partials (unrotated) and every tier partial (rotated basis):
-// o = [sum_e w o_e + (sum_t w o_t) R + (sum_t w l_t) mu_V] / sum_all w l   (STRATA_KV.py:1784-1792)
+// Merge of one (b, h, row): exact-row partials (unrotated) and every tier partial (rotated basis):
+// o = [sum_e w o_e + (sum_t w o_t) R + (sum_t w l_t) mu_V] / sum_all w l   (STRATA_KV.py:1784-1792).
+// The partials are spread over the block's 256 threads (block reductions for the maximum and the
+// sums, 128 channels x 2 partial halves for the output columns); one wavefront rotates the coded
+// sum back to the channel basis (FWHT).
 template <int R, int DT>
 __global__ __launch_bounds__(kSThreads) void strata_merge(StrataParams p) {
-  extern __shared__ float smem[];
-  const int bh = blockIdx.x;
+  __shared__ float red[4];
+  __shared__ float oc[2][kSD], oe[2][kSD];
+  const int bh = blockIdx.x / p.R_real, r = blockIdx.x % p.R_real;
   const int b = bh / p.Hkv, h = bh % p.Hkv;
-  float* oc = smem;                              // [R][d] coded sum, then rotated back
-  float* stat = smem + R * kSD;                  // M[R], L[R], Lc[R]
-  const int wave = threadIdx.x / 64, l = threadIdx.x % 64;
-  if (threadIdx.x < R) {
-    const int r = threadIdx.x;
-    float M = -INFINITY;
-    for (int s = 0; s < p.S_ex; ++s) M = fmaxf(M, p.ex_m[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r]);
-    for (int s = 0; s < p.S_all; ++s) M = fmaxf(M, p.ws_m[(static_cast<int64_t>(bh) * p.S_all + s) * R + r]);
-    float L = 0.0f, Lc = 0.0f;
-    for (int s = 0; s < p.S_ex; ++s) {
-      const float m = p.ex_m[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r];
-      if (m != -INFINITY) L += __builtin_amdgcn_exp2f(m - M) * p.ex_l[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r];
+  const int tid = threadIdx.x, lane = tid % 64;
+  auto reduce = [&](float v, bool is_max) -> float {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float u = __shfl_xor(v, o, 64);
+      v = is_max ? fmaxf(v, u) : v + u;
     }
-    for (int s = 0; s < p.S_all; ++s) {
-      const float m = p.ws_m[(static_cast<int64_t>(bh) * p.S_all + s) * R + r];
-      if (m != -INFINITY) Lc += __builtin_amdgcn_exp2f(m - M) * p.ws_l[(static_cast<int64_t>(bh) * p.S_all + s) * R + r];
-    }
-    stat[r] = M;
-    stat[R + r] = L + Lc;
-    stat[2 * R + r] = Lc;
+    __syncthreads();
+    if (lane == 0) red[tid / 64] = v;
+    __syncthreads();
+    return is_max ? fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) : (red[0] + red[1]) + (red[2] + red[3]);
+  };
+  auto em = [&](int s) { return p.ex_m[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r]; };
+  auto cm = [&](int s) { return p.ws_m[(static_cast<int64_t>(bh) * p.S_all + s) * R + r]; };
+  float m = -INFINITY;
+  for (int s = tid; s < p.S_ex; s += kSThreads) m = fmaxf(m, em(s));
+  for (int s = tid; s < p.S_all; s += kSThreads) m = fmaxf(m, cm(s));
+  const float M = reduce(m, true);
+  float le = 0.0f, lc = 0.0f;
+  for (int s = tid; s < p.S_ex; s += kSThreads) {
+    const float x = em(s);
+    if (x != -INFINITY) le += __builtin_amdgcn_exp2f(x - M) * p.ex_l[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r];
+  }
+  for (int s = tid; s < p.S_all; s += kSThreads) {
+    const float x = cm(s);
+    if (x != -INFINITY) lc += __builtin_amdgcn_exp2f(x - M) * p.ws_l[(static_cast<int64_t>(bh) * p.S_all + s) * R + r];
+  }
+  const float Le = reduce(le, false);
+  const float Lc = reduce(lc, false);
+  const int c = tid % kSD, part = tid / kSD;
+  float o_c = 0.0f, o_e = 0.0f;
+#pragma unroll 4
+  for (int s = part; s < p.S_all; s += 2) {
+    const float x = cm(s);
+    const float w = x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x - M);
+    o_c = __builtin_fmaf(w, p.ws_o[((static_cast<int64_t>(bh) * p.S_all + s) * R + r) * kSD + c], o_c);
+  }
+  for (int s = part; s < p.S_ex; s += 2) {
+    const float x = em(s);
+    const float w = x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x - M);
+    o_e = __builtin_fmaf(w, p.ex_o[((static_cast<int64_t>(bh) * p.S_ex + s) * R + r) * kSD + c], o_e);
+  }
+  oc[part][c] = o_c;
+  oe[part][c] = o_e;
+  __syncthreads();
+  if (tid < 64) {                                 // coded sum back to the channel basis: x R
+    float v0 = oc[0][tid] + oc[1][tid], v1 = oc[0][tid + 64] + oc[1][tid + 64];
+    fwht128(v0, v1, tid);
+    oc[0][tid] = v0 * 0.08838834764831845f * p.signs[tid];
+    oc[0][tid + 64] = v1 * 0.08838834764831845f * p.signs[tid + 64];
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < R * kSD; idx += kSThreads) {
-    const int r = idx / kSD, c = idx % kSD;
-    float O = 0.0f;
-    const float M = stat[r];
-    for (int s = 0; s < p.S_all; ++s) {
-      const int64_t po = static_cast<int64_t>(bh) * p.S_all + s;
-      const float m = p.ws_m[po * R + r];
-      if (m != -INFINITY) O += __builtin_amdgcn_exp2f(m - M) * p.ws_o[(po * R + r) * kSD + c];
-    }
-    oc[r * kSD + c] = O;
-  }
-  __syncthreads();
-  for (int r = wave; r < R; r += kSWaves) {       // coded sum back to the channel basis: x R
-    float v0 = oc[r * kSD + l], v1 = oc[r * kSD + l + 64];
-    fwht128(v0, v1, l);
-    oc[r * kSD + l] = v0 * 0.08838834764831845f * p.signs[l];
-    oc[r * kSD + l + 64] = v1 * 0.08838834764831845f * p.signs[l + 64];
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < p.R_real * kSD; idx += kSThreads) {
-    const int r = idx / kSD, c = idx % kSD;
-    const float M = stat[r];
-    float O = oc[r * kSD + c] + stat[2 * R + r] * f16_to_f32(p.mu_v[static_cast<int64_t>(bh) * kSD + c]);
-    for (int s = 0; s < p.S_ex; ++s) {
-      const int64_t po = static_cast<int64_t>(bh) * p.S_ex + s;
-      const float m = p.ex_m[po * R + r];
-      if (m != -INFINITY) O += __builtin_amdgcn_exp2f(m - M) * p.ex_o[(po * R + r) * kSD + c];
-    }
+  if (part == 0) {
+    const float O = oc[0][c] + Lc * f16_to_f32(p.mu_v[static_cast<int64_t>(bh) * kSD + c]) + oe[0][c] + oe[1][c];
     const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
-    store_from_f32<DT>(p.out, ((static_cast<int64_t>(b) * p.Tq + t) * p.Hq + hq) * kSD + c, O / stat[R + r]);
+    store_from_f32<DT>(p.out, ((static_cast<int64_t>(b) * p.Tq + t) * p.Hq + hq) * kSD + c, O / (Le + Lc));
   }
 }
 
@@ -658,13 +685,16 @@ inline int strata_pow2(int64_t r) {
 
 // splits of each tier: fill about one round of resident blocks across all tiers, in proportion to
 // each tier's tokens, at least one 32-token chunk per wavefront
-inline void strata_plan(int64_t BH, int n_tiers, const int64_t* tier_n, int* ns) {
-  int64_t total = 0;
-  for (int t = 0; t < n_tiers; ++t) total += tier_n[t];
-  const int64_t target = 768;
+// Splits per stratum: about one round of resident blocks (resident_per_cu x 256 CUs) shared in
+// proportion to each stratum's bytes (tokens x (32 bits + 8) B: K and V codes and scales).
+inline void strata_plan(int64_t BH, int n_tiers, const int* tier_bits, const int64_t* tier_n, int* ns) {
+  double total = 0.0;
+  for (int t = 0; t < n_tiers; ++t) total += static_cast<double>(tier_n[t]) * (32 * tier_bits[t] + 8);
+  const double target = 256.0 * 3 / static_cast<double>(BH);             // splits per (b, h)
   for (int t = 0; t < n_tiers; ++t) {
     const int64_t nc = (tier_n[t] + 31) / 32;
-    int64_t s = total > 0 ? (target * tier_n[t] + total * BH - 1) / (total * BH) : 1;
+    const double share = total > 0 ? target * static_cast<double>(tier_n[t]) * (32 * tier_bits[t] + 8) / total : 1.0;
+    int64_t s = static_cast<int64_t>(share + 0.5);
     s = std::max<int64_t>(1, std::min<int64_t>(s, (nc + kSWaves - 1) / kSWaves));
     ns[t] = tier_n[t] > 0 ? static_cast<int>(s) : 0;
   }
@@ -686,9 +716,9 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
 
 namespace {
 int64_t strata_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t n_exact, int n_tiers,
-                        const int64_t* tier_n, int64_t* ex_floats, int* S_all) {
+                        const int* tier_bits, const int64_t* tier_n, int64_t* ex_floats, int* S_all) {
   int ns[16];
-  kvq::strata_plan(B * Hkv, n_tiers, tier_n, ns);
+  kvq::strata_plan(B * Hkv, n_tiers, tier_bits, tier_n, ns);
   int S = 0;
   for (int t = 0; t < n_tiers; ++t) S += ns[t];
   *S_all = S;
@@ -699,12 +729,15 @@ int64_t strata_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t 
 }  // namespace
 
 extern "C" int64_t kvq_strata_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
-                                               int64_t n_exact, int n_tiers, const int64_t* tier_n) {
+                                               int64_t n_exact, int n_tiers, const int* tier_bits,
+                                               const int64_t* tier_n) {
   if (d != 128 || B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Tq <= 0 || n_tiers < 0 || n_tiers > 16) return -1;
-  if (n_tiers > 0 && tier_n == nullptr) return -1;
+  if (n_tiers > 0 && (tier_n == nullptr || tier_bits == nullptr)) return -1;
+  for (int t = 0; t < n_tiers; ++t)
+    if (tier_bits[t] != 2 && tier_bits[t] != 4 && tier_bits[t] != 8) return -1;
   int64_t ex;
   int S;
-  return strata_ws_parts(B, Hq, Hkv, Tq, n_exact, n_tiers, tier_n, &ex, &S);
+  return strata_ws_parts(B, Hq, Hkv, Tq, n_exact, n_tiers, tier_bits, tier_n, &ex, &S);
 }
 
 extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B,
@@ -737,7 +770,7 @@ extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64
   KVQ_REQUIRE(q && out && workspace, "kvq_strata_decode: null q / out / workspace");
   int64_t ex_floats;
   int S_all;
-  const int64_t need = strata_ws_parts(B, Hq, Hkv, Tq, n_exact, n_tiers, tier_n, &ex_floats, &S_all);
+  const int64_t need = strata_ws_parts(B, Hq, Hkv, Tq, n_exact, n_tiers, tier_bits, tier_n, &ex_floats, &S_all);
   KVQ_REQUIRE(workspace_floats >= need, "kvq_strata_decode: workspace too small (%lld < %lld floats)",
               (long long)workspace_floats, (long long)need);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -769,47 +802,44 @@ extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64
   p.ws_l = p.ws_m + trow;
   p.S_all = S_all;
   int ns[16];
-  strata_plan(B * Hkv, n_tiers, tier_n, ns);
+  strata_plan(B * Hkv, n_tiers, tier_bits, tier_n, ns);
+  // strata with tokens, widest first (their blocks carry the most bytes: dispatched first)
+  int base = 0;
+  for (int pass_bits : {8, 4, 2}) {
+    for (int t = 0; t < n_tiers; ++t) {
+      if (ns[t] == 0 || tier_bits[t] != pass_bits) continue;
+      StrataTierArg& ta = p.tiers[p.n_tiers++];
+      ta.kc = tier_kc[t]; ta.ks = tier_ks[t]; ta.vt = tier_vt[t]; ta.vsl = tier_vsl[t];
+      ta.n_t = tier_n[t]; ta.cap_t = tier_cap[t];
+      ta.n_split = ns[t]; ta.s_base = base; ta.bits = tier_bits[t];
+      base += ns[t];
+    }
+  }
   const int bh_pad = (p.BH + 7) / 8 * 8;
   const size_t split_smem = std::max<size_t>((R * kSD + 2 * R) * sizeof(float),
                                              (kSWaves * R * kSD + kSWaves * 2 * R) * sizeof(float));
-  int base = 0;
-  for (int t = 0; t < n_tiers; ++t) {
-    if (ns[t] == 0) continue;
-    p.n_t = tier_n[t]; p.cap_t = tier_cap[t];
-    p.kc = tier_kc[t]; p.ks = tier_ks[t]; p.vt = tier_vt[t]; p.vsl = tier_vsl[t];
-    p.n_split = ns[t];
-    p.s_base = base;
-    base += ns[t];
-    const dim3 grid(static_cast<unsigned>(ns[t]) * bh_pad);
-#define KVQ_STRATA_LAUNCH(BITS_, R_, DT_) \
-    hipLaunchKernelGGL((strata_tier_split<BITS_, R_, DT_>), grid, dim3(kSThreads), split_smem, s, p)
-#define KVQ_STRATA_R(BITS_, DT_)                                         \
+  if (S_all > 0) {
+    const dim3 grid(static_cast<unsigned>(S_all) * bh_pad);
+#define KVQ_STRATA_LAUNCH(R_, DT_) \
+    hipLaunchKernelGGL((strata_split_all<R_, DT_, 3>), grid, dim3(kSThreads), split_smem, s, p)
+#define KVQ_STRATA_R(DT_)                                                \
     switch (R) {                                                         \
-      case 1: KVQ_STRATA_LAUNCH(BITS_, 1, DT_); break;                   \
-      case 2: KVQ_STRATA_LAUNCH(BITS_, 2, DT_); break;                   \
-      case 4: KVQ_STRATA_LAUNCH(BITS_, 4, DT_); break;                   \
-      default: KVQ_STRATA_LAUNCH(BITS_, 8, DT_); break;                  \
-    }
-#define KVQ_STRATA_BITS(DT_)                                             \
-    switch (tier_bits[t]) {                                              \
-      case 2: KVQ_STRATA_R(2, DT_) break;                                \
-      case 4: KVQ_STRATA_R(4, DT_) break;                                \
-      default: KVQ_STRATA_R(8, DT_) break;                               \
+      case 1: KVQ_STRATA_LAUNCH(1, DT_); break;                          \
+      case 2: KVQ_STRATA_LAUNCH(2, DT_); break;                          \
+      case 4: KVQ_STRATA_LAUNCH(4, DT_); break;                          \
+      default: KVQ_STRATA_LAUNCH(8, DT_); break;                         \
     }
     switch (q_dtype) {
-      case KVQ_F32: KVQ_STRATA_BITS(KVQ_F32) break;
-      case KVQ_F16: KVQ_STRATA_BITS(KVQ_F16) break;
-      default: KVQ_STRATA_BITS(KVQ_BF16) break;
+      case KVQ_F32: KVQ_STRATA_R(KVQ_F32) break;
+      case KVQ_F16: KVQ_STRATA_R(KVQ_F16) break;
+      default: KVQ_STRATA_R(KVQ_BF16) break;
     }
-#undef KVQ_STRATA_BITS
 #undef KVQ_STRATA_R
 #undef KVQ_STRATA_LAUNCH
-    KVQ_LAUNCH_CHECK("kvq_strata_decode(tier)");
+    KVQ_LAUNCH_CHECK("kvq_strata_decode(tiers)");
   }
-  const size_t msmem = (R * kSD + 3 * R) * sizeof(float);
-#define KVQ_STRATA_MERGE(R_, DT_) \
-  hipLaunchKernelGGL((strata_merge<R_, DT_>), dim3(p.BH), dim3(kSThreads), msmem, s, p)
+  const dim3 mgrid(static_cast<unsigned>(p.BH) * p.R_real);
+#define KVQ_STRATA_MERGE(R_, DT_) hipLaunchKernelGGL((strata_merge<R_, DT_>), mgrid, dim3(kSThreads), 0, s, p)
 #define KVQ_STRATA_MR(DT_)                                               \
   switch (R) {                                                           \
     case 1: KVQ_STRATA_MERGE(1, DT_); break;                             \

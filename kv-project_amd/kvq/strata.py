@@ -194,10 +194,12 @@ class StrataCache:
         return tot
 
 
-def strata_workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_exact: int, tier_n: Sequence[int]) -> int:
+def strata_workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_exact: int, tier_n: Sequence[int],
+                            tier_bits: Sequence[int]) -> int:
     import ctypes
     arr = (ctypes.c_int64 * max(1, len(tier_n)))(*tier_n)
-    n = _lib.load().kvq_strata_decode_workspace(B, Hq, Hkv, Tq, d, n_exact, len(tier_n), arr)
+    bits = (ctypes.c_int * max(1, len(tier_bits)))(*tier_bits)
+    n = _lib.load().kvq_strata_decode_workspace(B, Hq, Hkv, Tq, d, n_exact, len(tier_n), bits, arr)
     if n < 0:
         raise _lib.KVQError("kvq_strata_decode_workspace rejected the shape")
     return n
@@ -219,7 +221,7 @@ def strata_decode(q: torch.Tensor, scaling: float, cache: StrataCache, *, q_pos:
         raise TypeError("q and the exact rows must share a dtype")
     tiers = [t for t in cache.tiers if t.n > 0]
     nt = len(tiers)
-    need = strata_workspace_floats(B, Hq, Hkv, Tq, d, cache.n_exact, [t.n for t in tiers])
+    need = strata_workspace_floats(B, Hq, Hkv, Tq, d, cache.n_exact, [t.n for t in tiers], [t.bits for t in tiers])
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty((need,), dtype=torch.float32, device=q.device)
     if out is None:
