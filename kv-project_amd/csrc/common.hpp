@@ -66,6 +66,44 @@ __device__ __forceinline__ void store_from_f32(void* p, int64_t i, float v) {
   else static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
 }
 
+// 8 consecutive elements (16-byte aligned) as floats: one 16-byte load for 16-bit types, two for fp32
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t i, float (&x)[8]) {
+  if constexpr (DT == KVQ_F32) {
+    const float4* p4 = reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    const float4 a = p4[0], c = p4[1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t lo = static_cast<uint16_t>(ws[k] & 0xffffu), hi = static_cast<uint16_t>(ws[k] >> 16);
+      x[2 * k] = DT == KVQ_F16 ? f16_to_f32(lo) : bf16_to_f32(lo);
+      x[2 * k + 1] = DT == KVQ_F16 ? f16_to_f32(hi) : bf16_to_f32(hi);
+    }
+  }
+}
+
+// 4 consecutive elements (8-byte aligned for 16-bit types, 16-byte for fp32) as floats: one load
+template <int DT>
+__device__ __forceinline__ void load4(const void* base, int64_t i, float (&x)[4]) {
+  if constexpr (DT == KVQ_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + i);
+    const uint32_t ws[2] = {w.x, w.y};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint16_t lo = static_cast<uint16_t>(ws[k] & 0xffffu), hi = static_cast<uint16_t>(ws[k] >> 16);
+      x[2 * k] = DT == KVQ_F16 ? f16_to_f32(lo) : bf16_to_f32(lo);
+      x[2 * k + 1] = DT == KVQ_F16 ? f16_to_f32(hi) : bf16_to_f32(hi);
+    }
+  }
+}
+
 inline bool valid_dtype(int dt) { return dt == KVQ_F32 || dt == KVQ_F16 || dt == KVQ_BF16; }
 
 }  // namespace kvq

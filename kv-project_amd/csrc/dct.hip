@@ -129,9 +129,9 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
   const int b = bh / p.Hkv, h = bh % p.Hkv;
   float (*qs)[kDD] = reinterpret_cast<float (*)[kDD]>(smem);                    // q * qscale
   uint32_t* bq_all = reinterpret_cast<uint32_t*>(smem + R * kDD);               // [wave][2R][64]
-  uint32_t* bv_all = bq_all + kDWaves * 2 * R * 64;                            // [wave][R][16]
-  float* wsm_all = reinterpret_cast<float*>(bv_all + kDWaves * R * 16);         // [wave][R][16 + 2]
-  u32x4* cst = reinterpret_cast<u32x4*>(wsm_all + kDWaves * R * 18);            // [12][64] lane constants
+  uint32_t* bv_all = bq_all + kDWaves * 2 * R * kBqStride;                            // [wave][R][16]
+  float* wsm_all = reinterpret_cast<float*>(bv_all + kDWaves * R * 16);         // [wave][R][17] + [R] + [R]
+  u32x4* cst = reinterpret_cast<u32x4*>(wsm_all + kDWaves * R * 19);            // [12][64] lane constants
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   const int l = threadIdx.x % 64;
   const int g = l >> 4, n = l & 15;
@@ -141,24 +141,30 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
   const int c0 = 32 * g + 8 * ci + kCosD[2 * ck];
   const int c1 = 32 * g + 8 * ci + kCosD[2 * ck + 1];
   const float kinv = (ck & 1) ? 1.0f : 16.0f;
-  uint32_t* bq = bq_all + wave * 2 * R * 64;
+  uint32_t* bq = bq_all + wave * 2 * R * kBqStride;
   uint32_t* bv = bv_all + wave * R * 16;
-  float* wsm = wsm_all + wave * R * 18;            // [R][16] w values, [R] sum w, [R] alpha
+  float* wsm = wsm_all + wave * R * 19;            // [R][17] w values (stride 17: bank-spread), [R] sum w, [R] alpha
 
   for (int idx = threadIdx.x; idx < R * kDD; idx += kDThreads) {
     const int r = idx / kDD, c = idx % kDD;
     qs[r][c] = r < p.R_real ? load_as_f32<DT>(p.q, dct_q_offset(p, b, h, r) + c) * p.qscale : 0.0f;
   }
-  // lane constants (the same for every wavefront; wave 0 writes them): C^T tiles of the logit
-  // stage, hi / lo, 4 nonzero slots each; C slices of the coefficient stage, hi / lo per k-step
-  if (wave == 0) {
+  // the DCT table, staged once: (16, 64) float32 = 256 float4, one per thread
+  float* ct = reinterpret_cast<float*>(cst + 12 * 64);
+  reinterpret_cast<float4*>(ct)[threadIdx.x] = reinterpret_cast<const float4*>(p.ctab)[threadIdx.x];
+  __syncthreads();
+  // lane constants (the same for every wavefront; each wavefront builds three of the twelve):
+  // C^T tiles of the logit stage, hi / lo, 4 nonzero slots each (waves 0, 1: tiles 2w, 2w+1);
+  // C slices of the coefficient stage, hi / lo per k-step (waves 2, 3: k-step w - 2)
+  if (wave < 2) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int tt = 0; tt < 2; ++tt) {
+      const int t = 2 * wave + tt;
       uint32_t hi[2], lo[2];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const float a = p.ctab[(4 * g + 2 * kk) * kDB + 16 * t + n];
-        const float bb = p.ctab[(4 * g + 2 * kk + 1) * kDB + 16 * t + n];
+        const float a = ct[(4 * g + 2 * kk) * kDB + 16 * t + n];
+        const float bb = ct[(4 * g + 2 * kk + 1) * kDB + 16 * t + n];
         const _Float16 ah = static_cast<_Float16>(a), bh16 = static_cast<_Float16>(bb);
         hi[kk] = pack_h2(ah, bh16);
         lo[kk] = pack_h2(static_cast<_Float16>(a - static_cast<float>(ah)), static_cast<_Float16>(bb - static_cast<float>(bh16)));
@@ -166,27 +172,26 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
       cst[(2 * t) * 64 + l] = u32x4{hi[0], hi[1], 0u, 0u};
       cst[(2 * t + 1) * 64 + l] = u32x4{lo[0], lo[1], 0u, 0u};
     }
+  } else {
+    const int ks = wave - 2;
+    uint32_t hi[4], lo[4];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      uint32_t hi[4], lo[4];
+    for (int jj = 0; jj < 4; ++jj) {
+      float v[2];
+      _Float16 vh[2];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        float v[2];
-        _Float16 vh[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int j = 2 * jj + u;
-          const int tok = 32 * ks + 16 * (j >> 2) + 4 * g + (j & 3);
-          v[u] = p.ctab[n * kDB + tok];                 // row n = coefficient (M index m = n)
-          vh[u] = static_cast<_Float16>(v[u]);
-        }
-        hi[jj] = pack_h2(vh[0], vh[1]);
-        lo[jj] = pack_h2(static_cast<_Float16>(v[0] - static_cast<float>(vh[0])),
-                         static_cast<_Float16>(v[1] - static_cast<float>(vh[1])));
+      for (int u = 0; u < 2; ++u) {
+        const int j = 2 * jj + u;
+        const int tok = 32 * ks + 16 * (j >> 2) + 4 * g + (j & 3);
+        v[u] = ct[n * kDB + tok];                       // row n = coefficient (M index m = n)
+        vh[u] = static_cast<_Float16>(v[u]);
       }
-      cst[(8 + 2 * ks) * 64 + l] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-      cst[(8 + 2 * ks + 1) * 64 + l] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+      hi[jj] = pack_h2(vh[0], vh[1]);
+      lo[jj] = pack_h2(static_cast<_Float16>(v[0] - static_cast<float>(vh[0])),
+                       static_cast<_Float16>(v[1] - static_cast<float>(vh[1])));
     }
+    cst[(8 + 2 * ks) * 64 + l] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    cst[(8 + 2 * ks + 1) * 64 + l] = u32x4{lo[0], lo[1], lo[2], lo[3]};
   }
   __syncthreads();
 
@@ -235,7 +240,7 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
   const half8 tiny = as_half8(u32x4{0x00100010u, 0x00100010u, 0x00100010u, 0x00100010u});   // 2^-20
   const half2v hl_neg = hl ? half2v{static_cast<_Float16>(-1.0f), static_cast<_Float16>(-1.0f)}
                            : half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
-  const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl) * 64 + g * 16);
+  const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl) * kBqStride + g * 16);
   const u32x4* bv_src = reinterpret_cast<const u32x4*>(bv + r_n * 16 + g * 4);
 
   float acc[8][2];
@@ -261,8 +266,8 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
         const _Float16 h1 = static_cast<_Float16>(qbk * sc1);
         const _Float16 e0 = static_cast<_Float16>(qak * sc0 - static_cast<float>(h0));
         const _Float16 e1 = static_cast<_Float16>(qbk * sc1 - static_cast<float>(h1));
-        bq[(2 * r) * 64 + l] = pack_h2(h0, h1);
-        bq[(2 * r + 1) * 64 + l] = pack_h2(e0, e1);
+        bq[(2 * r) * kBqStride + l] = pack_h2(h0, h1);
+        bq[(2 * r + 1) * kBqStride + l] = pack_h2(e0, e1);
         float P = -7.0f * (qa * sc0 + qb * sc1);
         P += dpp<kQuadSwap1>(P);
         P += dpp<kQuadSwap2>(P);
@@ -306,12 +311,12 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       la *= alpha;
       m_run = m_new;
-      if (g == 0 && n < R) wsm[R * 17 + n] = alpha;           // alpha of row n for the value lanes
+      if (g == 0 && n < R) wsm[R * 18 + n] = alpha;           // alpha of row n for the value lanes
       wave_lds_fence();
 #pragma unroll
       for (int jr = 0; jr < 2; ++jr) {
         const int r = 2 * g + jr;
-        const float a = r < R ? wsm[R * 17 + r] : 1.0f;
+        const float a = r < R ? wsm[R * 18 + r] : 1.0f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) acc[k][jr] *= a;
       }
@@ -347,10 +352,10 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
     for (int i = 0; i < 4; ++i) {
       const float w = dw[i] + dpp<kRowRor + R>(dw[i]);
       wsum += w;
-      if (n < R) wsm[n * 16 + 4 * g + i] = w;
+      if (n < R) wsm[n * 17 + 4 * g + i] = w;
     }
     wsum = xsum32(xsum16(wsum));
-    if (g == 0 && n < R) wsm[R * 16 + n] = wsum;
+    if (g == 0 && n < R) wsm[R * 17 + n] = wsum;
     wave_lds_fence();
     // A operand: row m = 2r + hl5 of w (hi / lo), coefficients 8g .. 8g+7 (g < 2), element e / 16
     // for the high-nibble elements 2, 3, 6, 7
@@ -363,7 +368,7 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
 #pragma unroll
         for (int u2 = 0; u2 < 2; ++u2) {
           const int e = 2 * jj + u2;
-          x[u2] = wsm[m_r * 16 + 8 * g + e] * (((e >> 1) & 1) ? 0.0625f : 1.0f);
+          x[u2] = wsm[m_r * 17 + 8 * g + e] * (((e >> 1) & 1) ? 0.0625f : 1.0f);
         }
         _Float16 hh[2];
 #pragma unroll
@@ -375,8 +380,8 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
       }
     }
     const half8 a5 = as_half8(u32x4{aw[0], aw[1], aw[2], aw[3]});
-    const float W0 = 2 * g < R ? wsm[R * 16 + 2 * g] : 0.0f;
-    const float W1 = 2 * g + 1 < R ? wsm[R * 16 + 2 * g + 1] : 0.0f;
+    const float W0 = 2 * g < R ? wsm[R * 17 + 2 * g] : 0.0f;
+    const float W1 = 2 * g + 1 < R ? wsm[R * 17 + 2 * g + 1] : 0.0f;
     // ---- out rows 2g, 2g+1, channel 16*blk + n ----
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
@@ -486,7 +491,8 @@ namespace {
 int64_t dct_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t T, int64_t n_exact, int64_t* ex_floats,
                      int* S) {
   *S = T > 0 ? kvq::plan_block_splits(B * Hkv, T / 64, 4, 4) : 0;
-  *ex_floats = n_exact > 0 ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
+  *ex_floats = (n_exact > 0 && !kvq::exact_in_merge(n_exact))
+                   ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
   const int64_t R = kvq::pow2_rows((Hq / Hkv) * Tq);
   return *ex_floats + B * Hkv * static_cast<int64_t>(*S) * R * (128 + 2);
 }
@@ -515,6 +521,7 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
   KVQ_REQUIRE(T >= 0 && T % kDB == 0, "kvq_dct_decode: T must be a multiple of 64");
   KVQ_REQUIRE(T / kDB * 1024 < (1LL << 31), "kvq_dct_decode: more than 2^21 blocks per head");
   KVQ_REQUIRE(T == 0 || (ctab && kc && ks && vc && vs), "kvq_dct_decode: null coded cache");
+  KVQ_REQUIRE(T == 0 || reinterpret_cast<uintptr_t>(ctab) % 16 == 0, "kvq_dct_decode: ctab must be 16-byte aligned");
   KVQ_REQUIRE(T + n_exact > 0, "kvq_dct_decode: empty cache");
   KVQ_REQUIRE(q && out && workspace, "kvq_dct_decode: null q / out / workspace");
   int64_t ex_floats;
@@ -532,8 +539,9 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
   p.nb = T / kDB;
   p.kc = kc; p.ks = ks; p.vc = vc; p.vs = vs; p.ctab = ctab;
   p.out = out;
-  const int64_t S_ex = (n_exact + 31) / 32;
-  if (n_exact > 0) {
+  const bool ex_merge = exact_in_merge(n_exact);
+  const int64_t S_ex = ex_merge ? 0 : (n_exact + kExactRowsPerBlock - 1) / kExactRowsPerBlock;
+  if (n_exact > 0 && !ex_merge) {
     if (phases & 1) {
       const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,
                                      nullptr, nullptr, 0, 0, 32, 32, k_exact, v_exact, q_dtype, cap_e, n_exact, exact_pos,
@@ -555,7 +563,7 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
   p.n_split = S;
   const int bh_pad = (p.BH + 7) / 8 * 8;
   const size_t split_smem = std::max<size_t>(
-      (R * kDD + kDWaves * (2 * R * 64 + R * 16) + kDWaves * R * 18) * sizeof(float) + 12 * 64 * 16,
+      (R * kDD + kDWaves * (2 * R * kBqStride + R * 16) + kDWaves * R * 19) * sizeof(float) + 12 * 64 * 16 + kDK * kDB * 4,
       (kDWaves * R * kDD + kDWaves * 2 * R) * sizeof(float));
   if (S > 0 && (phases & 1)) {
 #define KVQ_DCT_SPLIT(R_, DT_) \
@@ -577,8 +585,10 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
     KVQ_LAUNCH_CHECK("kvq_dct_decode(split)");
   }
   if (phases & 2) {
-    const MergeArgs ma{p.ws_o, p.ws_m, p.ws_l, p.S_all, p.ex_o, p.ex_m, p.ex_l, p.S_ex,
-                       p.Hq, p.Hkv, p.Tq, p.rep, p.R_real, p.out, nullptr};
+    MergeArgs ma{p.ws_o, p.ws_m, p.ws_l, p.S_all, p.ex_o, p.ex_m, p.ex_l, p.S_ex,
+                 p.Hq, p.Hkv, p.Tq, p.rep, p.R_real, p.out, nullptr, ExactArgs{}};
+    if (ex_merge)
+      ma.ex = ExactArgs{q, q_sb, q_sh, q_st, p.qscale, k_exact, v_exact, cap_e, static_cast<int>(n_exact), exact_pos, q_pos};
     const int rc = launch_merge_rows(ma, R, p.BH, q_dtype, s);
     if (rc != KVQ_OK) return rc;
   }

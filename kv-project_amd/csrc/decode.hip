@@ -10,10 +10,13 @@
 // group and into the probabilities per token (the affine identity of STRATA_KV.py:1419/1427-1435
 // applied per channel / per channel group).
 //
-// Work decomposition.  Grid (n_exact_wg + n_split, B*Hkv), 256 threads = 4 wavefronts.
-//   blockIdx.x <  n_exact_wg : exact rows [512*x, 512*x+512), plain fp32 VALU.
-//   blockIdx.x >= n_exact_wg : packed split s, tokens [s*ST, (s+1)*ST), one contiguous quarter
-//                              per wavefront; every wavefront streams 32-token chunks.
+// Work decomposition.  One launch of 256-thread blocks (4 wavefronts), XCD-aware over (b, h):
+//   packed split s of (b, h): tokens [s*ST, (s+1)*ST), one contiguous quarter per wavefront;
+//                             every wavefront streams 32-token chunks.
+//   exact window: up to kFusedExact rows per packed split are attended by the packed blocks
+//                 themselves (fp32 VALU, staged in LDS with the query rows); longer windows of
+//                 up to kExactInMerge rows by the merge; longer still by exact-row blocks of
+//                 kExactRows rows dispatched after the packed blocks.
 // Each block writes one flash-decoding partial (m, l, acc) per row (base-2 logits); a second
 // kernel merges the partials exactly (log-sum-exp) and writes the output.
 //
@@ -59,7 +62,11 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kD = 128;            // head_dim supported by the matrix-core path
-constexpr int kExactRows = 32;     // exact rows per exact-row block (16 per pass of 4 wavefronts)
+constexpr int kExactRows = kExactRowsPerBlock;   // exact rows per exact-row block (16 per pass of 4 wavefronts)
+// A window of at most kFusedExact rows per packed split is attended by the packed blocks
+// themselves: each stages its share in LDS together with the query rows and folds it into its
+// partial as one more wavefront state, so the window adds neither blocks nor merge work.
+constexpr int kFusedExact = 32;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 
@@ -92,6 +99,7 @@ struct DecodeParams {
   float score_weight;
   float* ws_o;
   int n_exact_wg, n_split, split_tokens, S1;
+  int fused_per;                      // exact rows each packed split attends itself (0: none)
   int BH;
   void* out;
 };
@@ -116,26 +124,6 @@ __device__ void load_q_rows(const DecodeParams& p, int b, int h, float (*qs)[kD]
 
 // ---------------------------------------------------------------------------------------------
 // exact rows: fp32 attention over rows [e0, e0 + kExactRows) of the residual buffer
-
-// 8 consecutive elements (16-byte aligned) as floats: one 16-byte load for 16-bit types, two for fp32
-template <int DT>
-__device__ __forceinline__ void load8(const void* base, int64_t i, float (&x)[8]) {
-  if constexpr (DT == KVQ_F32) {
-    const float4* p4 = reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
-    const float4 a = p4[0], c = p4[1];
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-    x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
-  } else {
-    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint16_t lo = static_cast<uint16_t>(ws[k] & 0xffffu), hi = static_cast<uint16_t>(ws[k] >> 16);
-      x[2 * k] = DT == KVQ_F16 ? f16_to_f32(lo) : bf16_to_f32(lo);
-      x[2 * k + 1] = DT == KVQ_F16 ? f16_to_f32(hi) : bf16_to_f32(hi);
-    }
-  }
-}
 
 // Partial (m, l, o) of exact-row block `sidx`.  A wavefront takes 4 rows at a time, 16 lanes per
 // row and 8 channels per lane (coalesced 16-byte loads); logits are reduced over the 16 lanes,
@@ -262,6 +250,20 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
 // SCORE = false: flash-decoding partials of this split.  SCORE = true: the score pass of the
 // eviction path -- the same logits, normalised by the row's global (max, sum) from the merge,
 // summed over the rows of the KV head and accumulated into the scores row (no value work).
+// LDS of a packed block (floats): query rows + per-wavefront operand scratch, reused by the
+// wavefront partials of the epilogue; the fused exact-row region follows it.
+template <int R>
+constexpr int packed_lds_floats() {
+  constexpr int loop = R * kD + kWaves * (2 * R * kBqStride + R * 16);
+  constexpr int epi = kWaves * R * kD + kWaves * 2 * R;
+  return loop > epi ? loop : epi;
+}
+template <int R, int DT>
+constexpr int fused_lds_floats() {
+  constexpr int esz = DT == KVQ_F32 ? 4 : 2;
+  return 2 * kFusedExact * kD * esz / 4 + R * kFusedExact + R;   // keys, values, logits, masks
+}
+
 template <int R, int GV, int DT, bool SCORE>
 __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* smem) {
   // fp32 output: p * sv enters the PV product as hi + lo fp16 parts (two column variants per
@@ -275,8 +277,61 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   const int b = bh / p.Hkv, h = bh % p.Hkv;
   float (*qs)[kD] = reinterpret_cast<float (*)[kD]>(smem);
   uint32_t* bq_all = reinterpret_cast<uint32_t*>(smem + R * kD);   // [wave][2R][64]
-  uint32_t* bv_all = bq_all + kWaves * 2 * R * 64;                  // [wave][R][16]
+  uint32_t* bv_all = bq_all + kWaves * 2 * R * kBqStride;                  // [wave][R][16]
+
+  // fused exact rows [fe0, fe0 + fne) of the window: raw rows staged in LDS (their loads are in
+  // flight together with the query rows'), visibility of row i to query row r in bit i of emask[r]
+  constexpr int kEsz = DT == KVQ_F32 ? 4 : 2;
+  constexpr int kRowU4 = kD * kEsz / 16;                       // 16-byte words of one row
+  constexpr int kExU4 = kFusedExact * kRowU4 / kThreads;       // words per thread and tensor
+  static_assert(kFusedExact * kRowU4 % kThreads == 0, "fused rows must spread evenly");
+  u32x4* const ek4 = reinterpret_cast<u32x4*>(smem + packed_lds_floats<R>());
+  u32x4* const ev4 = ek4 + kFusedExact * kRowU4;
+  float* const esl = reinterpret_cast<float*>(ev4 + kFusedExact * kRowU4);   // [R][kFusedExact]
+  uint32_t* const emask = reinterpret_cast<uint32_t*>(esl + R * kFusedExact);
+  int fe0 = 0, fne = 0;
+  if constexpr (!SCORE) {
+    if (p.fused_per > 0) {
+      fe0 = min(sidx * p.fused_per, p.n_exact);
+      fne = min(p.fused_per, p.n_exact - fe0);
+    }
+  }
+  u32x4 ekr[kExU4], evr[kExU4];
+  if (fne > 0) {
+    const int64_t row0 = static_cast<int64_t>(bh) * p.cap_e + fe0;
+    const u32x4* gk = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.k_exact) + row0 * kD * kEsz);
+    const u32x4* gv = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.v_exact) + row0 * kD * kEsz);
+#pragma unroll
+    for (int u = 0; u < kExU4; ++u) {
+      const int w = threadIdx.x + kThreads * u;
+      if (w < fne * kRowU4) {
+        ekr[u] = gk[w];
+        evr[u] = gv[w];
+      }
+    }
+  }
   load_q_rows<R, DT>(p, b, h, qs);
+  if (fne > 0) {
+#pragma unroll
+    for (int u = 0; u < kExU4; ++u) {
+      const int w = threadIdx.x + kThreads * u;
+      if (w < fne * kRowU4) {
+        ek4[w] = ekr[u];
+        ev4[w] = evr[u];
+      }
+    }
+    if (threadIdx.x < 64) {
+      const int i = threadIdx.x;
+      const bool masked = p.exact_pos != nullptr && p.q_pos != nullptr;
+      const int64_t ep = (masked && i < fne) ? p.exact_pos[fe0 + i] : 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const bool vis = i < fne && (!masked || ep <= p.q_pos[r % p.Tq]);
+        const uint64_t bal = __ballot(vis);
+        if (i == 0) emask[r] = static_cast<uint32_t>(bal);
+      }
+    }
+  }
   __syncthreads();
 
   // wave index made explicitly uniform: every token offset derived from it lives in SGPRs
@@ -295,7 +350,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   // slots' is 16*q*scale, so every product is 16 * code * q*scale * 2^-24 and the fp16 low part
   // of the operand stays out of the subnormal range
   const float kinv = (ck & 1) ? 1.0f : 16.0f;
-  uint32_t* bq = bq_all + wave * 2 * R * 64;
+  uint32_t* bq = bq_all + wave * 2 * R * kBqStride;
   uint32_t* bv = bv_all + wave * R * 16;
 
   // wavefront w = sidx * 4 + wave of this (b, h) takes chunks [w * NC / NW, (w + 1) * NC / NW) of
@@ -388,7 +443,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   const half8 tiny = as_half8(u32x4{0x00100010u, 0x00100010u, 0x00100010u, 0x00100010u});   // 2^-20
   const half2v hl_neg = hl_pv ? half2v{static_cast<_Float16>(-1.0f), static_cast<_Float16>(-1.0f)}
                               : half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
-  const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl_qk) * 64 + g * 16);
+  const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * r_n + hl_qk) * kBqStride + g * 16);
   const u32x4* bv_src = reinterpret_cast<const u32x4*>(bv + r_n * 16 + g * 4);
   half8 bqk[4];                                      // query operand of the current key group
   half8 bvirt;
@@ -418,8 +473,8 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
         const _Float16 h1 = static_cast<_Float16>(qbk * static_cast<float>(sc1));
         const _Float16 e0 = static_cast<_Float16>(qak * static_cast<float>(sc0) - static_cast<float>(h0));
         const _Float16 e1 = static_cast<_Float16>(qbk * static_cast<float>(sc1) - static_cast<float>(h1));
-        bq[(2 * r) * 64 + l] = pack_h2(h0, h1);
-        bq[(2 * r + 1) * 64 + l] = pack_h2(e0, e1);
+        bq[(2 * r) * kBqStride + l] = pack_h2(h0, h1);
+        bq[(2 * r + 1) * kBqStride + l] = pack_h2(e0, e1);
         // logit bias q.lo of this key group (added through the virtual k-step)
         float P = qa * static_cast<float>(lo0) + qb * static_cast<float>(lo1);
         P += dpp<kQuadSwap1>(P);
@@ -554,6 +609,26 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   }
 
   if constexpr (SCORE) return;
+  // ---- fused exact rows: logits of rows 16u + 4*wave + g (16 lanes per row, 8 channels per lane),
+  // read from LDS while the query rows are still there; rows past fne are computed, not stored ----
+  if (fne > 0) {
+    const void* ekr_lds = ek4;
+#pragma unroll
+    for (int u = 0; u < kFusedExact / 16; ++u) {
+      const int i = 16 * u + 4 * wave + g;
+      float kx[8];
+      load8<DT>(ekr_lds, static_cast<int64_t>(i) * kD + 8 * n, kx);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) d = __builtin_fmaf(qs[r][8 * n + k], kx[k], d);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
+        if (n == 0 && i < fne) esl[r * kFusedExact + i] = ((emask[r] >> i) & 1u) ? d : -INFINITY;
+      }
+    }
+  }
   // ---- wavefront epilogue: row sums over lane groups, hi+lo columns, offset and zero terms ----
   const float l_run = xsum32(xsum16(la + 16.0f * lb));
   float Z[NB];
@@ -585,7 +660,26 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_ml[(w * 2) * R + r]);
+    // the fused exact rows' own state (me, le, oe) joins the wavefronts'
+    float me = -INFINITY, le = 0.0f, oe = 0.0f;
+    if (fne > 0) {
+      for (int i = 0; i < fne; ++i) me = fmaxf(me, esl[r * kFusedExact + i]);
+      if (me != -INFINITY) {
+        const void* evr_lds = ev4;
+        for (int i = 0; i < fne; ++i) {
+          const float pr = __builtin_amdgcn_exp2f(esl[r * kFusedExact + i] - me);
+          le += pr;
+          oe = __builtin_fmaf(pr, load_as_f32<DT>(evr_lds, static_cast<int64_t>(i) * kD + c), oe);
+        }
+      }
+      M = fmaxf(M, me);
+    }
     float O = 0.0f, L = 0.0f;
+    if (me != -INFINITY) {
+      const float we = __builtin_amdgcn_exp2f(me - M);
+      O = we * oe;
+      L = we * le;
+    }
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
       const float mw_ = red_ml[(w * 2) * R + r];
@@ -625,8 +719,7 @@ void kivi_decode_split(DecodeParams p) {
     const int bh = id % 8 + 8 * (k / p.n_split);
     if (bh < p.BH) packed_block<R, GV, DT, false>(p, bh, k % p.n_split, smem);
   } else {
-    // exact-row blocks come last in dispatch order: they take the slots that packed blocks free
-    // at the end of their round
+    // exact-row blocks (windows too long for the merge) come last in dispatch order
     const int e_id = id - n_packed;
     const int k = e_id / 8;
     const int bh = e_id % 8 + 8 * (k / p.n_exact_wg);
@@ -647,12 +740,12 @@ void kivi_score_split(DecodeParams p) {
 template <int R, int GV, int DT>
 int launch(DecodeParams& p, int phases, hipStream_t stream) {
   const size_t exact_smem = (R * kD + R * kExactRows + 2 * R + kWaves * R * kD) * sizeof(float);
-  const size_t packed_smem = std::max<size_t>((R * kD) * sizeof(float) + kWaves * (2 * R * 64 + R * 16) * 4,
-                                              (kWaves * R * kD + kWaves * 2 * R) * sizeof(float));
+  const size_t packed_smem = packed_lds_floats<R>() * sizeof(float);
+  const size_t fused_smem = p.fused_per > 0 ? fused_lds_floats<R, DT>() * sizeof(float) : 0;
   const int bh_pad = (p.BH + 7) / 8 * 8;
   const dim3 grid(static_cast<unsigned>(p.S1) * bh_pad);
-  if (phases & 1) {
-    hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), grid, dim3(kThreads), std::max(packed_smem, exact_smem),
+  if ((phases & 1) && p.S1 > 0) {
+    hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), grid, dim3(kThreads), std::max(packed_smem + fused_smem, exact_smem),
                        stream, p);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(split)");
   }
@@ -661,6 +754,9 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
     ma.ws_o = p.ws_o; ma.ws_m = p.ws_m; ma.ws_l = p.ws_l; ma.S = p.S1;
     ma.Hq = p.Hq; ma.Hkv = p.Hkv; ma.Tq = p.Tq; ma.rep = p.rep; ma.R_real = p.R_real;
     ma.out = p.out; ma.row_ml = p.row_ml;
+    if (p.fused_per == 0 && p.n_exact_wg == 0 && p.n_exact > 0)
+      ma.ex = ExactArgs{p.q, p.q_sb, p.q_sh, p.q_st, p.qscale, p.k_exact, p.v_exact, p.cap_e, p.n_exact,
+                        p.exact_pos, p.q_pos};
     const int rc = launch_merge_rows(ma, R, p.BH, DT, stream);
     if (rc != KVQ_OK) return rc;
   }
@@ -673,7 +769,7 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
 }
 
 struct SplitPlan {
-  int n_exact_wg, n_split, split_tokens, S1, R;
+  int n_exact_wg, n_split, split_tokens, S1, R, fused_per;
 };
 
 constexpr int kCUs = 256;          // MI355X compute units
@@ -692,7 +788,6 @@ inline SplitPlan plan_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int6
     default: resident_blocks = group_v == 128 ? split_waves<8, 128>() : group_v == 64 ? split_waves<8, 64>() : split_waves<8, 32>(); break;
   }
   const int64_t nc = (n_q + 31) / 32;                   // 32-token chunks per (b, h)
-  sp.n_exact_wg = static_cast<int>((n_exact + kExactRows - 1) / kExactRows);
   int64_t ns = 0;
   if (nc > 0 && split_tokens > 0) {
     ns = (n_q + split_tokens - 1) / split_tokens;
@@ -717,6 +812,12 @@ inline SplitPlan plan_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int6
   ns = std::min<int64_t>(ns, (nc + kWaves - 1) / kWaves);
   sp.n_split = static_cast<int>(ns);
   sp.split_tokens = ns > 0 ? static_cast<int>((n_q + ns - 1) / ns) : 0;
+  // exact window: in the packed splits (at most kFusedExact rows each), else in the merge (at
+  // most kExactInMerge rows), else in exact-row blocks
+  const int64_t per = ns > 0 ? (n_exact + ns - 1) / ns : 0;
+  sp.fused_per = (n_exact > 0 && ns > 0 && per <= kFusedExact) ? static_cast<int>(per) : 0;
+  sp.n_exact_wg = (sp.fused_per > 0 || exact_in_merge(n_exact))
+                      ? 0 : static_cast<int>((n_exact + kExactRows - 1) / kExactRows);
   sp.S1 = sp.n_exact_wg + sp.n_split;
   return sp;
 }
@@ -793,6 +894,7 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   p.score_weight = score_weight;
   p.BH = static_cast<int>(B * Hkv);
   p.n_exact_wg = sp.n_exact_wg; p.n_split = sp.n_split; p.split_tokens = sp.split_tokens; p.S1 = sp.S1;
+  p.fused_per = sp.fused_per;
   p.out = out;
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define KVQ_GV(R_, DT_)                                                             \

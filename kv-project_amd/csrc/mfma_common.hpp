@@ -10,6 +10,11 @@
 namespace kvq {
 namespace {
 
+// Row stride (dwords) of the per-wavefront staging rows of the query B operand: 64 + 4, so that
+// the rows (one per (query row, hi/lo) column pair) start in different LDS banks and the 16-byte
+// operand reads of one lane group do not all collide in the same four banks.
+constexpr int kBqStride = 68;
+
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

@@ -232,7 +232,7 @@ __device__ __forceinline__ void mixed_run(MixedState<R, LO>& st, const MixedLane
   const half8 tiny = as_half8(u32x4{0x00100010u, 0x00100010u, 0x00100010u, 0x00100010u});   // 2^-20
   const half2v hl_neg = L.hl_pv ? half2v{static_cast<_Float16>(-1.0f), static_cast<_Float16>(-1.0f)}
                                 : half2v{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
-  const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * L.r_n + L.hl_qk) * 64 + g * 16);
+  const u32x4* bq_src = reinterpret_cast<const u32x4*>(bq + (2 * L.r_n + L.hl_qk) * kBqStride + g * 16);
   const u32x4* bv_src = reinterpret_cast<const u32x4*>(bv + L.r_n * 16 + g * 4);
   // probability and zero-point sums per code-factor class, folded into the state at the end
   float lc[NCLS], zc[NCLS][NB];
@@ -255,8 +255,8 @@ __device__ __forceinline__ void mixed_run(MixedState<R, LO>& st, const MixedLane
         const float qa = qs[r][c0], qb = qs[r][c1];
         const float x0 = qa * kinv * sc0, x1 = qb * kinv * sc1;
         const _Float16 h0 = static_cast<_Float16>(x0), h1 = static_cast<_Float16>(x1);
-        bq[(2 * r) * 64 + l] = pack_h2(h0, h1);
-        bq[(2 * r + 1) * 64 + l] = pack_h2(static_cast<_Float16>(x0 - static_cast<float>(h0)),
+        bq[(2 * r) * kBqStride + l] = pack_h2(h0, h1);
+        bq[(2 * r + 1) * kBqStride + l] = pack_h2(static_cast<_Float16>(x0 - static_cast<float>(h0)),
                                            static_cast<_Float16>(x1 - static_cast<float>(h1)));
         float P = qa * lo0 + qb * lo1;
         P += dpp<kQuadSwap1>(P);
@@ -389,7 +389,7 @@ __device__ void mixed_block(const MixedParams& p, int bh, int sidx, float* smem)
   const int b = bh / p.Hkv, h = bh % p.Hkv;
   float (*qs)[kMD] = reinterpret_cast<float (*)[kMD]>(smem);
   uint32_t* bq_all = reinterpret_cast<uint32_t*>(smem + R * kMD);    // [wave][2R][64]
-  uint32_t* bv_all = bq_all + kMWaves * 2 * R * 64;                  // [wave][R][16]
+  uint32_t* bv_all = bq_all + kMWaves * 2 * R * kBqStride;                  // [wave][R][16]
   for (int idx = threadIdx.x; idx < R * kMD; idx += kMThreads) {
     const int r = idx / kMD, c = idx % kMD;
     float x = 0.0f;
@@ -413,7 +413,7 @@ __device__ void mixed_block(const MixedParams& p, int bh, int sidx, float* smem)
   L.hl_pv = LO ? (v_pv & 1) : 0;
   L.ci = (L.l >> 2) & 3;
   L.ck = L.l & 3;
-  uint32_t* bq = bq_all + wave * 2 * R * 64;
+  uint32_t* bq = bq_all + wave * 2 * R * kBqStride;
   uint32_t* bv = bv_all + wave * R * 16;
 
   const int64_t base = p.seg[bh * 4];
@@ -554,7 +554,8 @@ int64_t mixed_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t n
   // resident blocks per CU = waves per SIMD of the variant (one wavefront of each block per SIMD)
   const int64_t Rr = kvq::pow2_rows((Hq / Hkv) * Tq);
   *S = nb > 0 ? kvq::plan_block_splits(B * Hkv, nb, (Rr <= 4) ? 3 : 2, 4) : 0;
-  *ex_floats = n_exact > 0 ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
+  *ex_floats = (n_exact > 0 && !kvq::exact_in_merge(n_exact))
+                   ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
   const int64_t R = kvq::pow2_rows((Hq / Hkv) * Tq);
   return *ex_floats + B * Hkv * static_cast<int64_t>(*S) * R * (128 + 2);
 }
@@ -593,14 +594,17 @@ extern "C" int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_
   MergeArgs ma{};
   ma.Hq = (int)Hq; ma.Hkv = (int)Hkv; ma.Tq = (int)Tq; ma.rep = (int)(Hq / Hkv); ma.R_real = (int)R_real;
   ma.out = out;
-  if (n_exact > 0) {
+  if (exact_in_merge(n_exact)) {
+    ma.ex = ExactArgs{q, q_sb, q_sh, q_st, scaling * 1.4426950408889634f, k_exact, v_exact, cap_e,
+                      static_cast<int>(n_exact), exact_pos, q_pos};
+  } else if (n_exact > 0) {
     if (phases & 1) {
       const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,
                                      nullptr, nullptr, 0, 0, 32, 32, k_exact, v_exact, q_dtype, cap_e, n_exact, exact_pos,
                                      q_pos, out, q_dtype, workspace, ex_floats, nullptr, 0, 0.0f, 0, 1, stream);
       if (rc != KVQ_OK) return rc;
     }
-    const int64_t S_ex = (n_exact + 31) / 32;
+    const int64_t S_ex = (n_exact + kExactRowsPerBlock - 1) / kExactRowsPerBlock;
     const int64_t nrow = B * Hkv * S_ex * R;
     ma.ex_o = workspace;
     ma.ex_m = workspace + nrow * 128;
@@ -620,7 +624,7 @@ extern "C" int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_
   p.ws_l = p.ws_m + trow;
   ma.ws_o = p.ws_o; ma.ws_m = p.ws_m; ma.ws_l = p.ws_l; ma.S = S;
   const int bh_pad = (p.BH + 7) / 8 * 8;
-  const size_t split_smem = std::max<size_t>((R * kMD + kMWaves * (2 * R * 64 + R * 16)) * sizeof(float),
+  const size_t split_smem = std::max<size_t>((R * kMD + kMWaves * (2 * R * kBqStride + R * 16)) * sizeof(float),
                                              (kMWaves * R * kMD + kMWaves * 2 * R) * sizeof(float));
   if (S > 0 && (phases & 1)) {
 #define KVQ_MX_SPLIT(R_, DT_) \

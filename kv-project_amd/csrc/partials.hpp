@@ -6,8 +6,8 @@
 // (the combination StrataState.attend performs in base e, STRATA_KV.py:1784-1792).
 //
 // One workgroup per (b, h, row): the partials are spread over all 256 threads (max and sum by
-// block reduction; the output columns by 128 channels x 2 partial halves), so the merge costs a
-// few dependent loads whatever the split count.
+// block reduction; the output columns by 32 channel quads x 8 partial slices), so the merge
+// costs a few dependent loads whatever the split count.
 #pragma once
 #include <algorithm>
 
@@ -15,6 +15,30 @@
 
 namespace kvq {
 namespace {
+
+constexpr int kMergeThreadsEx = 256;              // threads of the merge blocks
+
+// Exact rows (the residual window, appended tokens) a merge may attend itself instead of reading
+// their partials: rows [0, n) of k_exact / v_exact (BH, cap_e, D) in the output dtype, visible to
+// query t when exact_pos[i] <= q_pos[t] (both null: all visible).  The query row is read from q.
+struct ExactArgs {
+  const void* q;
+  int64_t q_sb, q_sh, q_st;
+  float qscale;                   // scaling * log2(e)
+  const void* k_exact;
+  const void* v_exact;
+  int64_t cap_e;
+  int n;                          // 0: no exact rows in the merge
+  const int64_t* exact_pos;
+  const int64_t* q_pos;
+};
+
+// Exact windows up to this many rows are attended inside the merge (one pass over them per query
+// row, overlapping nothing but also adding no tail blocks to the split launch); longer ones are
+// split into blocks of kExactRowsPerBlock rows of the split launch.
+constexpr int64_t kExactInMerge = 1024;
+constexpr int kExactRowsPerBlock = 64;
+inline bool exact_in_merge(int64_t n_exact) { return n_exact > 0 && n_exact <= kExactInMerge; }
 
 struct MergeArgs {
   const float* ws_o;
@@ -28,7 +52,93 @@ struct MergeArgs {
   int Hq, Hkv, Tq, rep, R_real;
   void* out;
   float* row_ml;                  // optional (BH, R, 2): the row's M and L
+  ExactArgs ex;                   // exact rows attended here (ex.n > 0)
 };
+
+// The exact-row partial of query row (b, hq, t) over the rows of (b, h) = bh, computed by the 256
+// threads of a merge block: logits by 16-lane dot products (8 channels a lane), base-2 softmax
+// statistics by block reductions, and the value sum of channel quad c4 over rows part, part + 8,
+// ... (the merge's output layout).  Loads go out in batches with row indices clamped to n - 1 (a
+// clamped row is loaded, never used), so a window of up to 128 rows costs one key and one value
+// round trip.  sl: LDS for kExactInMerge logits.
+template <int DT, int D>
+__device__ void exact_partial(const ExactArgs& e, int b, int hq, int t, int bh, float* sl, float* red, float& me,
+                              float& le, float4& oe, int c4, int part) {
+  constexpr int kRowsPerPass = kMergeThreadsEx / 16;   // key rows one pass of the block covers
+  constexpr int kKeyBatch = 8;                         // passes whose key loads are in flight together
+  constexpr int kParts = kMergeThreadsEx / (D / 4);    // value row slices
+  constexpr int kValBatch = 16;                        // value rows in flight per thread
+  const int tid = threadIdx.x, lane = tid % 64;
+  const int j = tid >> 4, pt = tid & 15;
+  const int n = e.n;
+  const int64_t qo = static_cast<int64_t>(b) * e.q_sb + static_cast<int64_t>(hq) * e.q_sh +
+                     static_cast<int64_t>(t) * e.q_st + 8 * pt;
+  float qv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) qv[k] = load_as_f32<DT>(e.q, qo + k) * e.qscale;
+  const int64_t base = static_cast<int64_t>(bh) * e.cap_e * D;
+  const bool masked = e.exact_pos != nullptr && e.q_pos != nullptr;
+  const int64_t qp = masked ? e.q_pos[t] : 0;
+  for (int i0 = 0; i0 < n; i0 += kRowsPerPass * kKeyBatch) {
+    float kx[kKeyBatch][8];
+    bool vis[kKeyBatch];
+#pragma unroll
+    for (int u = 0; u < kKeyBatch; ++u) {
+      const int i = min(i0 + u * kRowsPerPass + j, n - 1);
+      load8<DT>(e.k_exact, base + static_cast<int64_t>(i) * D + 8 * pt, kx[u]);
+      vis[u] = !masked || e.exact_pos[i] <= qp;
+    }
+#pragma unroll
+    for (int u = 0; u < kKeyBatch; ++u) {
+      float s = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s = __builtin_fmaf(qv[k], kx[u][k], s);
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
+      const int i = i0 + u * kRowsPerPass + j;
+      if (pt == 0 && i < n) sl[i] = vis[u] ? s : -INFINITY;
+    }
+  }
+  __syncthreads();
+  float m = -INFINITY;
+  for (int i = tid; i < n; i += kMergeThreadsEx) m = fmaxf(m, sl[i]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if (lane == 0) red[tid / 64] = m;
+  __syncthreads();
+  me = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float l = 0.0f;
+  for (int i = tid; i < n; i += kMergeThreadsEx) {
+    const float pr = me == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sl[i] - me);
+    sl[i] = pr;
+    l += pr;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+  __syncthreads();                                  // red[] reads of the maximum are done
+  if (lane == 0) red[tid / 64] = l;
+  __syncthreads();
+  le = (red[0] + red[1]) + (red[2] + red[3]);
+  oe = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int i0 = part; i0 < n; i0 += kParts * kValBatch) {
+    float vx[kValBatch][4];
+#pragma unroll
+    for (int u = 0; u < kValBatch; ++u) {
+      const int i = min(i0 + u * kParts, n - 1);
+      load4<DT>(e.v_exact, base + static_cast<int64_t>(i) * D + 4 * c4, vx[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kValBatch; ++u) {
+      const int i = i0 + u * kParts;
+      const float pr = i < n ? sl[i] : 0.0f;
+      oe.x = __builtin_fmaf(pr, vx[u][0], oe.x);
+      oe.y = __builtin_fmaf(pr, vx[u][1], oe.y);
+      oe.z = __builtin_fmaf(pr, vx[u][2], oe.z);
+      oe.w = __builtin_fmaf(pr, vx[u][3], oe.w);
+    }
+  }
+  __syncthreads();                                  // red[] free for the caller
+}
 
 constexpr int kMergeThreads = 256;
 
@@ -45,13 +155,15 @@ __device__ __forceinline__ float block_reduce_256(float v, bool is_max, float* r
   return is_max ? fmaxf(fmaxf(a, b), fmaxf(c, d)) : (a + b) + (c + d);
 }
 
-// grid = BH * R_real workgroups of kMergeThreads
+// grid = BH * R_real workgroups of kMergeThreads; thread t sums channels 4 (t % (D/4)) .. +3 of
+// the partials s = t / (D/4) (mod PARTS) with 16-byte loads, the PARTS slices meet in LDS.
 template <int R, int DT, int D>
 __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(MergeArgs a) {
-  static_assert(kMergeThreads % D == 0, "channels must divide the workgroup");
-  constexpr int PARTS = kMergeThreads / D;
+  static_assert(kMergeThreads % (D / 4) == 0, "channel quads must divide the workgroup");
+  constexpr int PARTS = kMergeThreads / (D / 4);
   __shared__ float red[4];
-  __shared__ float part_o[PARTS][D];
+  __shared__ float4 part_o[PARTS][D / 4];
+  __shared__ float sl[kExactInMerge];
   const int bh = blockIdx.x / a.R_real, r = blockIdx.x % a.R_real;
   const int tid = threadIdx.x;
   const int S_all = a.S_ex + a.S;
@@ -64,39 +176,66 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(MergeArgs a) 
     return s < a.S_ex ? a.ex_l[(static_cast<int64_t>(bh) * a.S_ex + s) * R + r]
                       : a.ws_l[(static_cast<int64_t>(bh) * a.S + (s - a.S_ex)) * R + r];
   };
-  auto o_of = [&](int s, int c) -> float {
-    return s < a.S_ex ? a.ex_o[((static_cast<int64_t>(bh) * a.S_ex + s) * R + r) * D + c]
-                      : a.ws_o[((static_cast<int64_t>(bh) * a.S + (s - a.S_ex)) * R + r) * D + c];
+  auto o_of = [&](int s, int c4) -> float4 {
+    const float* base = s < a.S_ex ? a.ex_o + ((static_cast<int64_t>(bh) * a.S_ex + s) * R + r) * D
+                                   : a.ws_o + ((static_cast<int64_t>(bh) * a.S + (s - a.S_ex)) * R + r) * D;
+    return reinterpret_cast<const float4*>(base)[c4];
   };
-  float m = -INFINITY;
-  for (int s = tid; s < S_all; s += kMergeThreads) m = fmaxf(m, m_of(s));
+  const int c4 = tid % (D / 4), part = tid / (D / 4);
+  const int b = bh / a.Hkv, h = bh % a.Hkv;
+  const int hq = h * a.rep + r / a.Tq, t = r % a.Tq;
+  // the first coded partials are loaded before the exact pass so their latency overlaps it
+  const float m0 = tid < S_all ? m_of(tid) : -INFINITY;
+  const float l0 = tid < S_all ? l_of(tid) : 0.0f;
+  const float mp0 = part < S_all ? m_of(part) : -INFINITY;
+  const float4 op0 = part < S_all ? o_of(part, c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  // exact rows attended here: their own partial (me, le, oe) joins the coded ones
+  float me = -INFINITY, le = 0.0f;
+  float4 oe = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (a.ex.n > 0) exact_partial<DT, D>(a.ex, b, hq, t, bh, sl, red, me, le, oe, c4, part);
+  float m = m0;
+  for (int s = tid + kMergeThreads; s < S_all; s += kMergeThreads) m = fmaxf(m, m_of(s));
   const float M = block_reduce_256(m, true, red);
-  float l = 0.0f;
-  for (int s = tid; s < S_all; s += kMergeThreads) {
+  float l = m0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0 - M) * l0;
+  for (int s = tid + kMergeThreads; s < S_all; s += kMergeThreads) {
     const float ms = m_of(s);
     if (ms != -INFINITY) l += __builtin_amdgcn_exp2f(ms - M) * l_of(s);
   }
-  const float L = block_reduce_256(l, false, red);
-  const int c = tid % D, part = tid / D;
-  float o = 0.0f;
+  const float Lc = block_reduce_256(l, false, red);
+  const float Mx = fmaxf(M, me);
+  const float wc = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mx);
+  const float we = me == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(me - Mx);
+  const float L = wc * Lc + we * le;
+  const float w0 = mp0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp0 - M);
+  float4 o = make_float4(w0 * op0.x, w0 * op0.y, w0 * op0.z, w0 * op0.w);
 #pragma unroll 4
-  for (int s = part; s < S_all; s += PARTS) {
+  for (int s = part + PARTS; s < S_all; s += PARTS) {
     const float ms = m_of(s);
     const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-    o = __builtin_fmaf(w, o_of(s, c), o);
+    const float4 v = o_of(s, c4);
+    o.x = __builtin_fmaf(w, v.x, o.x);
+    o.y = __builtin_fmaf(w, v.y, o.y);
+    o.z = __builtin_fmaf(w, v.z, o.z);
+    o.w = __builtin_fmaf(w, v.w, o.w);
   }
-  part_o[part][c] = o;
+  o.x = __builtin_fmaf(we, oe.x, wc * o.x);
+  o.y = __builtin_fmaf(we, oe.y, wc * o.y);
+  o.z = __builtin_fmaf(we, oe.z, wc * o.z);
+  o.w = __builtin_fmaf(we, oe.w, wc * o.w);
+  part_o[part][c4] = o;
   __syncthreads();
-  if (part == 0) {
+  if (tid < D) {
+    const int c = tid;
     float O = 0.0f;
 #pragma unroll
-    for (int k = 0; k < PARTS; ++k) O += part_o[k][c];
-    const int b = bh / a.Hkv, h = bh % a.Hkv;
-    const int hq = h * a.rep + r / a.Tq, t = r % a.Tq;
+    for (int k = 0; k < PARTS; ++k) {
+      const float4 v = part_o[k][c >> 2];
+      O += (c & 3) == 0 ? v.x : (c & 3) == 1 ? v.y : (c & 3) == 2 ? v.z : v.w;
+    }
     store_from_f32<DT>(a.out, ((static_cast<int64_t>(b) * a.Tq + t) * a.Hq + hq) * D + c, O / L);
   }
   if (tid == 0 && a.row_ml != nullptr) {
-    a.row_ml[(static_cast<int64_t>(bh) * R + r) * 2] = M;
+    a.row_ml[(static_cast<int64_t>(bh) * R + r) * 2] = Mx;
     a.row_ml[(static_cast<int64_t>(bh) * R + r) * 2 + 1] = L;
   }
 }

@@ -14,6 +14,7 @@
 #include "common.hpp"
 #include "mfma_common.hpp"
 #include "widths.hpp"
+#include "partials.hpp"
 
 namespace kvq {
 namespace {
@@ -307,6 +308,7 @@ struct StrataParams {
   float* ws_m;
   float* ws_l;
   int S_all;
+  ExactArgs ex;                 // exact rows attended in the merge (ex.n > 0)
   const float* ex_o;            // exact-row partials (BH * S_ex partials)
   const float* ex_m;
   const float* ex_l;
@@ -607,7 +609,8 @@ void strata_split_all(StrataParams p) {
   else strata_block<2, R, DT>(p, ta, bh, sidx, smem);
 }
 
-// Merge of one (b, h, row): exact-row partials (unrotated) and every tier partial (rotated basis):
+// Merge of one (b, h, row): exact rows (unrotated; as partials of exact-row blocks, or attended
+// here when the window fits the merge) and every tier partial (rotated basis):
 // o = [sum_e w o_e + (sum_t w o_t) R + (sum_t w l_t) mu_V] / sum_all w l   (STRATA_KV.py:1784-1792).
 // The partials are spread over the block's 256 threads (block reductions for the maximum and the
 // sums, 128 channels x 2 partial halves for the output columns); one wavefront rotates the coded
@@ -616,8 +619,11 @@ template <int R, int DT>
 __global__ __launch_bounds__(kSThreads) void strata_merge(StrataParams p) {
   __shared__ float red[4];
   __shared__ float oc[2][kSD], oe[2][kSD];
+  __shared__ float4 oi[8][kSD / 4];
+  __shared__ float sl[kExactInMerge];
   const int bh = blockIdx.x / p.R_real, r = blockIdx.x % p.R_real;
   const int b = bh / p.Hkv, h = bh % p.Hkv;
+  const int hq = h * p.rep + r / p.Tq, tq = r % p.Tq;
   const int tid = threadIdx.x, lane = tid % 64;
   auto reduce = [&](float v, bool is_max) -> float {
 #pragma unroll
@@ -632,21 +638,31 @@ __global__ __launch_bounds__(kSThreads) void strata_merge(StrataParams p) {
   };
   auto em = [&](int s) { return p.ex_m[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r]; };
   auto cm = [&](int s) { return p.ws_m[(static_cast<int64_t>(bh) * p.S_all + s) * R + r]; };
-  float m = -INFINITY;
+  auto cl = [&](int s) { return p.ws_l[(static_cast<int64_t>(bh) * p.S_all + s) * R + r]; };
+  // the first coded statistics are loaded before the exact pass so their latency overlaps it
+  const float mc0 = tid < p.S_all ? cm(tid) : -INFINITY;
+  const float lc0 = tid < p.S_all ? cl(tid) : 0.0f;
+  // exact rows attended here (their partial: mi, li, and the value sums in channel-quad layout)
+  float mi = -INFINITY, li = 0.0f;
+  float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (p.ex.n > 0) exact_partial<DT, kSD>(p.ex, b, hq, tq, bh, sl, red, mi, li, o4, tid % 32, tid / 32);
+  float m = fmaxf(mi, mc0);
   for (int s = tid; s < p.S_ex; s += kSThreads) m = fmaxf(m, em(s));
-  for (int s = tid; s < p.S_all; s += kSThreads) m = fmaxf(m, cm(s));
+  for (int s = tid + kSThreads; s < p.S_all; s += kSThreads) m = fmaxf(m, cm(s));
   const float M = reduce(m, true);
-  float le = 0.0f, lc = 0.0f;
+  const float wi = mi == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mi - M);
+  float le = 0.0f, lc = mc0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc0 - M) * lc0;
   for (int s = tid; s < p.S_ex; s += kSThreads) {
     const float x = em(s);
     if (x != -INFINITY) le += __builtin_amdgcn_exp2f(x - M) * p.ex_l[(static_cast<int64_t>(bh) * p.S_ex + s) * R + r];
   }
-  for (int s = tid; s < p.S_all; s += kSThreads) {
+  for (int s = tid + kSThreads; s < p.S_all; s += kSThreads) {
     const float x = cm(s);
-    if (x != -INFINITY) lc += __builtin_amdgcn_exp2f(x - M) * p.ws_l[(static_cast<int64_t>(bh) * p.S_all + s) * R + r];
+    if (x != -INFINITY) lc += __builtin_amdgcn_exp2f(x - M) * cl(s);
   }
-  const float Le = reduce(le, false);
+  const float Le = reduce(le, false) + wi * li;
   const float Lc = reduce(lc, false);
+  oi[tid / 32][tid % 32] = make_float4(wi * o4.x, wi * o4.y, wi * o4.z, wi * o4.w);
   const int c = tid % kSD, part = tid / kSD;
   float o_c = 0.0f, o_e = 0.0f;
 #pragma unroll 4
@@ -671,9 +687,13 @@ __global__ __launch_bounds__(kSThreads) void strata_merge(StrataParams p) {
   }
   __syncthreads();
   if (part == 0) {
-    const float O = oc[0][c] + Lc * f16_to_f32(p.mu_v[static_cast<int64_t>(bh) * kSD + c]) + oe[0][c] + oe[1][c];
-    const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
-    store_from_f32<DT>(p.out, ((static_cast<int64_t>(b) * p.Tq + t) * p.Hq + hq) * kSD + c, O / (Le + Lc));
+    float O = oc[0][c] + Lc * f16_to_f32(p.mu_v[static_cast<int64_t>(bh) * kSD + c]) + oe[0][c] + oe[1][c];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 v = oi[k][c >> 2];
+      O += (c & 3) == 0 ? v.x : (c & 3) == 1 ? v.y : (c & 3) == 2 ? v.z : v.w;
+    }
+    store_from_f32<DT>(p.out, ((static_cast<int64_t>(b) * p.Tq + tq) * p.Hq + hq) * kSD + c, O / (Le + Lc));
   }
 }
 
@@ -683,8 +703,6 @@ inline int strata_pow2(int64_t r) {
   return R;
 }
 
-// splits of each tier: fill about one round of resident blocks across all tiers, in proportion to
-// each tier's tokens, at least one 32-token chunk per wavefront
 // Splits per stratum: about one round of resident blocks (resident_per_cu x 256 CUs) shared in
 // proportion to each stratum's bytes (tokens x (32 bits + 8) B: K and V codes and scales).
 inline void strata_plan(int64_t BH, int n_tiers, const int* tier_bits, const int64_t* tier_n, int* ns) {
@@ -722,7 +740,8 @@ int64_t strata_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t 
   int S = 0;
   for (int t = 0; t < n_tiers; ++t) S += ns[t];
   *S_all = S;
-  *ex_floats = n_exact > 0 ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
+  *ex_floats = (n_exact > 0 && !kvq::exact_in_merge(n_exact))
+                   ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
   const int64_t R = kvq::strata_pow2((Hq / Hkv) * Tq);
   return *ex_floats + B * Hkv * static_cast<int64_t>(S) * R * (128 + 2);
 }
@@ -783,8 +802,11 @@ extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64
   p.signs = signs; p.mu_k = mu_k; p.mu_v = mu_v;
   p.out = out;
   // exact rows: partials of the KIVI exact-row blocks (no packed rows), into the first region
-  const int64_t S_ex = (n_exact + 31) / 32;
-  if (n_exact > 0) {
+  const bool ex_merge = exact_in_merge(n_exact);
+  const int64_t S_ex = ex_merge ? 0 : (n_exact + kExactRowsPerBlock - 1) / kExactRowsPerBlock;
+  if (ex_merge) {
+    p.ex = ExactArgs{q, q_sb, q_sh, q_st, p.qscale, k_exact, v_exact, cap_e, static_cast<int>(n_exact), exact_pos, q_pos};
+  } else if (n_exact > 0) {
     const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,
                                    nullptr, nullptr, 0, 0, 32, 32, k_exact, v_exact, q_dtype, cap_e, n_exact, exact_pos,
                                    q_pos, out, q_dtype, workspace, ex_floats, nullptr, 0, 0.0f, 0, 1, stream);

@@ -46,16 +46,18 @@ def test_argument_validation_without_gpu():
 
 def test_split_plan_fills_one_round():
     """Automatic split (16x8 (b, h), 32640 packed + 128 exact tokens, 3 resident blocks per CU on
-    256 CUs): 6 packed splits per (b, h) = 768 blocks, one round; the 128 exact rows are 4 blocks of
-    32 rows per (b, h), dispatched after the packed blocks.  The workspace holds S1 * rows * (d + 2) + 2 * rows floats
-    per (b, h), S1 = exact partials + packed splits (partials, then each row's max and sum)."""
+    256 CUs): 6 packed splits per (b, h) = 768 blocks, one round.  Exact windows of at most 1024
+    rows are attended by the merge (no exact-row blocks, no partials); longer ones are blocks of 64
+    rows dispatched after the packed blocks.  The workspace holds S1 * rows * (d + 2) + 2 * rows
+    floats per (b, h), S1 = exact-row blocks + packed splits (partials, then each row's max and sum)."""
     from kvq import _lib
     lib = _lib.load()
     BH, R, d = 16 * 8, 4, 128
-    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 0) == BH * ((4 + 6) * R * (d + 2) + 2 * R)
+    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 0) == BH * (6 * R * (d + 2) + 2 * R)
     # explicit split size: ceil(n_q / split_tokens) splits
-    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 3000) == BH * ((4 + 11) * R * (d + 2) + 2 * R)
+    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 3000) == BH * (11 * R * (d + 2) + 2 * R)
     assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 48, 0) == -1
-    # exact rows only / packed rows only
-    assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 0, 100, 32, 32, 0) == 8 * (4 * 1 * (d + 2) + 2)
+    # exact rows only (in the merge / in blocks of 64) / packed rows only
+    assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 0, 100, 32, 32, 0) == 8 * (0 * 1 * (d + 2) + 2)
+    assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 0, 2304, 32, 32, 0) == 8 * (36 * 1 * (d + 2) + 2)
     assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 64, 0, 32, 32, 0) == 8 * (1 * 1 * (d + 2) + 2)

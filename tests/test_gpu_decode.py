@@ -87,14 +87,21 @@ def test_exact_rows_only_and_packed_only():
     assert err <= 2e-3, err
     err, _, _ = _run(1, 32, 8, 1024, 0, 64, 64, torch.float32, seed=2)      # n_exact = 0
     assert err <= 2e-3, err
-    err, _, _ = _run(1, 32, 8, 3000, 700, 64, 64, torch.float32, seed=3)    # two exact blocks
+    err, _, _ = _run(1, 32, 8, 3000, 700, 64, 64, torch.float32, seed=3)    # window in the merge
+    assert err <= 2e-3, err
+    err, _, _ = _run(1, 32, 8, 3000, 2000, 64, 64, torch.float32, seed=4)   # exact-row blocks
     assert err <= 2e-3, err
 
 
-def test_multi_token_queries_causal_exact_rows():
+@pytest.mark.parametrize("W", [40, 400, 1500])
+def test_multi_token_queries_causal_exact_rows(W):
+    """560 packed tokens over 4 KV heads give at most 5 packed splits per head: a window of
+    40 (+2 appended) rows is attended inside the packed splits (9 rows each), 400 inside the
+    merge, 1500 by exact-row blocks; every placement applies the causal visibility."""
     import kvq
-    g = torch.Generator().manual_seed(5)
-    B, Hq, Hkv, T, W, Tq, d = 1, 8, 4, 600, 40, 2, 128
+    g = torch.Generator().manual_seed(5 + W)
+    B, Hq, Hkv, Tq, d = 1, 8, 4, 2, 128
+    T = 560 + W
     K = torch.randn((B, Hkv, T + Tq, d), generator=g)
     V = torch.randn((B, Hkv, T + Tq, d), generator=g)
     q = torch.randn((B, Hq, Tq, d), generator=g)
