@@ -261,7 +261,8 @@ constexpr int packed_lds_floats() {
 template <int R, int DT>
 constexpr int fused_lds_floats() {
   constexpr int esz = DT == KVQ_F32 ? 4 : 2;
-  return 2 * kFusedExact * kD * esz / 4 + R * kFusedExact + R;   // keys, values, logits, masks
+  static_assert(R * kD <= kFusedExact * kD * esz / 4, "value sums must fit over the staged keys");
+  return 2 * kFusedExact * kD * esz / 4 + R * kFusedExact + R + 2 * R;   // keys, values, logits, masks, stats
 }
 
 template <int R, int GV, int DT, bool SCORE>
@@ -289,6 +290,8 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   u32x4* const ev4 = ek4 + kFusedExact * kRowU4;
   float* const esl = reinterpret_cast<float*>(ev4 + kFusedExact * kRowU4);   // [R][kFusedExact]
   uint32_t* const emask = reinterpret_cast<uint32_t*>(esl + R * kFusedExact);
+  float* const estat = reinterpret_cast<float*>(emask + R);                   // row max [R], sum [R]
+  float* const eo = reinterpret_cast<float*>(ek4);                            // [R][kD] value sums
   int fe0 = 0, fne = 0;
   if constexpr (!SCORE) {
     if (p.fused_per > 0) {
@@ -595,9 +598,49 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
 
   // ---- software pipeline over chunks: two register buffers used in turn; the load of the next
   // chunk is always issued (clamped) before the current chunk is computed ----
+  Chunk ca, cb_;
+  if (t0 < t1) load_chunk(t0, ca);
+  // ---- fused exact rows, while the first chunk is in flight: logits of rows 16u + 4*wave + g
+  // (16 lanes per row, 8 channels per lane; rows past fne are computed, not stored), then each
+  // row's maximum, sum and value sums, left in LDS for the epilogue ----
+  if (fne > 0) {
+    const void* ek_lds = ek4;
+#pragma unroll
+    for (int u = 0; u < kFusedExact / 16; ++u) {
+      const int i = 16 * u + 4 * wave + g;
+      float kx[8];
+      load8<DT>(ek_lds, static_cast<int64_t>(i) * kD + 8 * n, kx);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) d = __builtin_fmaf(qs[r][8 * n + k], kx[k], d);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
+        if (n == 0 && i < fne) esl[r * kFusedExact + i] = ((emask[r] >> i) & 1u) ? d : -INFINITY;
+      }
+    }
+    __syncthreads();                               // logits complete; key rows no longer read
+    const void* ev_lds = ev4;
+    for (int idx = threadIdx.x; idx < p.R_real * kD; idx += kThreads) {
+      const int r = idx / kD, c = idx % kD;
+      float me = -INFINITY, le = 0.0f, oe = 0.0f;
+      for (int i = 0; i < fne; ++i) me = fmaxf(me, esl[r * kFusedExact + i]);
+      if (me != -INFINITY) {
+        for (int i = 0; i < fne; ++i) {
+          const float pr = __builtin_amdgcn_exp2f(esl[r * kFusedExact + i] - me);
+          le += pr;
+          oe = __builtin_fmaf(pr, load_as_f32<DT>(ev_lds, static_cast<int64_t>(i) * kD + c), oe);
+        }
+      }
+      eo[idx] = oe;
+      if (c == 0) {
+        estat[r] = me;
+        estat[R + r] = le;
+      }
+    }
+  }
   if (t0 < t1) {
-    Chunk ca, cb_;
-    load_chunk(t0, ca);
     for (int cb = t0;; cb += 64) {
       load_chunk(cb + 32, cb_);
       step(cb, ca);
@@ -609,26 +652,6 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   }
 
   if constexpr (SCORE) return;
-  // ---- fused exact rows: logits of rows 16u + 4*wave + g (16 lanes per row, 8 channels per lane),
-  // read from LDS while the query rows are still there; rows past fne are computed, not stored ----
-  if (fne > 0) {
-    const void* ekr_lds = ek4;
-#pragma unroll
-    for (int u = 0; u < kFusedExact / 16; ++u) {
-      const int i = 16 * u + 4 * wave + g;
-      float kx[8];
-      load8<DT>(ekr_lds, static_cast<int64_t>(i) * kD + 8 * n, kx);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float d = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) d = __builtin_fmaf(qs[r][8 * n + k], kx[k], d);
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
-        if (n == 0 && i < fne) esl[r * kFusedExact + i] = ((emask[r] >> i) & 1u) ? d : -INFINITY;
-      }
-    }
-  }
   // ---- wavefront epilogue: row sums over lane groups, hi+lo columns, offset and zero terms ----
   const float l_run = xsum32(xsum16(la + 16.0f * lb));
   float Z[NB];
@@ -663,15 +686,9 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     // the fused exact rows' own state (me, le, oe) joins the wavefronts'
     float me = -INFINITY, le = 0.0f, oe = 0.0f;
     if (fne > 0) {
-      for (int i = 0; i < fne; ++i) me = fmaxf(me, esl[r * kFusedExact + i]);
-      if (me != -INFINITY) {
-        const void* evr_lds = ev4;
-        for (int i = 0; i < fne; ++i) {
-          const float pr = __builtin_amdgcn_exp2f(esl[r * kFusedExact + i] - me);
-          le += pr;
-          oe = __builtin_fmaf(pr, load_as_f32<DT>(evr_lds, static_cast<int64_t>(i) * kD + c), oe);
-        }
-      }
+      me = estat[r];
+      le = estat[R + r];
+      oe = eo[idx];
       M = fmaxf(M, me);
     }
     float O = 0.0f, L = 0.0f;
