@@ -540,7 +540,8 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
   p.kc = kc; p.ks = ks; p.vc = vc; p.vs = vs; p.ctab = ctab;
   p.out = out;
   const bool ex_merge = exact_in_merge(n_exact);
-  const int64_t S_ex = ex_merge ? 0 : (n_exact + kExactRowsPerBlock - 1) / kExactRowsPerBlock;
+  int ex_rows = 0;
+  const int64_t S_ex = (ex_merge || n_exact == 0) ? 0 : plan_exact_blocks(B * Hkv, n_exact, &ex_rows);
   if (n_exact > 0 && !ex_merge) {
     if (phases & 1) {
       const int rc = kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, nullptr, nullptr, nullptr,

@@ -15,8 +15,8 @@
 //                             every wavefront streams 32-token chunks.
 //   exact window: up to kFusedExact rows per packed split are attended by the packed blocks
 //                 themselves (fp32 VALU, staged in LDS with the query rows); longer windows of
-//                 up to kExactInMerge rows by the merge; longer still by exact-row blocks of
-//                 kExactRows rows dispatched after the packed blocks.
+//                 up to kExactInMerge rows by the merge; longer still by exact-row blocks
+//                 (streaming, about one round of them) dispatched after the packed blocks.
 // Each block writes one flash-decoding partial (m, l, acc) per row (base-2 logits); a second
 // kernel merges the partials exactly (log-sum-exp) and writes the output.
 //
@@ -62,7 +62,6 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kD = 128;            // head_dim supported by the matrix-core path
-constexpr int kExactRows = kExactRowsPerBlock;   // exact rows per exact-row block (16 per pass of 4 wavefronts)
 // A window of at most kFusedExact rows per packed split is attended by the packed blocks
 // themselves: each stages its share in LDS together with the query rows and folds it into its
 // partial as one more wavefront state, so the window adds neither blocks nor merge work.
@@ -100,6 +99,7 @@ struct DecodeParams {
   float* ws_o;
   int n_exact_wg, n_split, split_tokens, S1;
   int fused_per;                      // exact rows each packed split attends itself (0: none)
+  int exact_rows;                     // rows of each exact-row block
   int BH;
   void* out;
 };
@@ -123,124 +123,159 @@ __device__ void load_q_rows(const DecodeParams& p, int b, int h, float (*qs)[kD]
 }
 
 // ---------------------------------------------------------------------------------------------
-// exact rows: fp32 attention over rows [e0, e0 + kExactRows) of the residual buffer
+// exact rows: fp32 attention over rows [e0, e1) of the residual buffer (e0 = sidx * exact_rows)
 
-// Partial (m, l, o) of exact-row block `sidx`.  A wavefront takes 4 rows at a time, 16 lanes per
-// row and 8 channels per lane (coalesced 16-byte loads); logits are reduced over the 16 lanes,
-// values are accumulated per lane and reduced over row slots and wavefronts at the end.
+// Partial (m, l, o) of exact-row block `sidx`.  Each wavefront streams a contiguous quarter of the
+// block's rows, four at a time: lane group j = lane / 16 takes one row, 8 channels per lane
+// (coalesced 16-byte loads, kept raw until used), the loads of the next three row quads in flight
+// while one is computed.  Every
+// lane group keeps its own base-2 online softmax per query row (lazy maximum: rescaled only when a
+// logit exceeds it by more than kLazy); the 16 states of the block are merged at the end.
 template <int R, int DT>
 __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem) {
+  constexpr float kLazy = 4.0f;
   const int b = bh / p.Hkv, h = bh % p.Hkv;
   float (*qs)[kD] = reinterpret_cast<float (*)[kD]>(smem);
-  float* sl = smem + R * kD;                        // logits / probabilities [R][kExactRows]
-  float* stat = sl + R * kExactRows;                // m[R], l[R]
-  float* red = stat + 2 * R;                        // [wave][R][kD] value sums
+  float* red_o = smem + R * kD;                     // [wave][R][kD]
+  float* red_ml = red_o + kWaves * R * kD;          // [wave][2][R]
   load_q_rows<R, DT>(p, b, h, qs);
   __syncthreads();
-  const int e0 = sidx * kExactRows;
-  const int ne = min(kExactRows, p.n_exact - e0);
-  const int64_t kbase = static_cast<int64_t>(bh) * p.cap_e * kD;
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int e0 = sidx * p.exact_rows;
+  const int e1 = min(e0 + p.exact_rows, p.n_exact);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
   const int j = lane >> 4, part = lane & 15;       // row slot of 4, 8-channel slice of 16
+  const int w0 = e0 + (e1 - e0) * wave / kWaves, w1 = e0 + (e1 - e0) * (wave + 1) / kWaves;
+  const int64_t kbase = static_cast<int64_t>(bh) * p.cap_e * kD;
   const bool masked = p.exact_pos != nullptr && p.q_pos != nullptr;
   float qv[R][8];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int k = 0; k < 8; ++k) qv[r][k] = qs[r][8 * part + k];
-  // every key and value row slice of this lane is loaded before any is used, so all the block's
-  // loads are in flight together (kExactRows = 16 rows per pass x kPass passes)
-  constexpr int kStride = 4 * kWaves;
-  constexpr int kPass = kExactRows / kStride;
-  float kx[kPass][8], vx[kPass][8];
+  int64_t qp[R];
 #pragma unroll
-  for (int u = 0; u < kPass; ++u) {
-    const int i = 4 * wave + kStride * u + j;
+  for (int r = 0; r < R; ++r) qp[r] = masked ? p.q_pos[r % p.Tq] : 0;
+  float m[R], l[R], o[R][8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) kx[u][k] = vx[u][k] = 0.0f;
-    if (i < ne) {
-      load8<DT>(p.k_exact, kbase + static_cast<int64_t>(e0 + i) * kD + 8 * part, kx[u]);
-      load8<DT>(p.v_exact, kbase + static_cast<int64_t>(e0 + i) * kD + 8 * part, vx[u]);
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kPass; ++u) {
-    const int i = 4 * wave + kStride * u + j;
-    float d[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float t = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) t = __builtin_fmaf(qv[r][k], kx[u][k], t);
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) t += __shfl_xor(t, o, 16);
-      d[r] = t;
-    }
-    if (part == 0 && i < ne) {
-      const int64_t ep = masked ? p.exact_pos[e0 + i] : 0;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const bool vis = !masked || ep <= p.q_pos[r % p.Tq];
-        sl[r * kExactRows + i] = r < p.R_real ? (vis ? d[r] : -INFINITY) : 0.0f;
-      }
-    }
-  }
-  __syncthreads();
-  for (int r = wave; r < p.R_real; r += kWaves) {
-    float mx = -INFINITY;
-    for (int i = lane; i < ne; i += 64) mx = fmaxf(mx, sl[r * kExactRows + i]);
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    float sum = 0.0f;
-    for (int i = lane; i < ne; i += 64) {
-      const float s = sl[r * kExactRows + i];
-      const float e = (mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s - mx);
-      sl[r * kExactRows + i] = e;
-      sum += e;
-    }
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    if (lane == 0) {
-      stat[r] = mx;
-      stat[R + r] = sum;
-    }
-  }
-  __syncthreads();
-  float o[R][8];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
+  for (int r = 0; r < R; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) o[r][k] = 0.0f;
+  }
+  constexpr int kW = DT == KVQ_F32 ? 2 : 1;          // 16-byte words of 8 channels
+  struct Rows {
+    u32x4 kw[kW], vw[kW];
+    int64_t pos;
+  };
+  // loads of row i (clamped to the wavefront's last row, so every load is unconditional)
+  auto load_rows = [&](int i, Rows& x) {
+    i = min(i, w1 - 1);
+    const int64_t off = (kbase + static_cast<int64_t>(i) * kD + 8 * part) * (DT == KVQ_F32 ? 4 : 2);
+    const u32x4* kp = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.k_exact) + off);
+    const u32x4* vp = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.v_exact) + off);
 #pragma unroll
-  for (int u = 0; u < kPass; ++u) {
-    const int i = 4 * wave + kStride * u + j;
-    if (i < ne) {
+    for (int w = 0; w < kW; ++w) {
+      x.kw[w] = kp[w];
+      x.vw[w] = vp[w];
+    }
+    x.pos = masked ? p.exact_pos[i] : 0;
+  };
+  auto to_f32 = [&](const u32x4 (&w)[kW], float (&x)[8]) {
+    if constexpr (DT == KVQ_F32) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float pr = sl[r * kExactRows + i];
+      for (int k = 0; k < 8; ++k) x[k] = __uint_as_float(w[k / 4][k % 4]);
+    } else {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) o[r][k] = __builtin_fmaf(pr, vx[u][k], o[r][k]);
+      for (int k = 0; k < 4; ++k) {
+        const uint16_t lo = static_cast<uint16_t>(w[0][k] & 0xffffu), hi = static_cast<uint16_t>(w[0][k] >> 16);
+        x[2 * k] = DT == KVQ_F16 ? f16_to_f32(lo) : bf16_to_f32(lo);
+        x[2 * k + 1] = DT == KVQ_F16 ? f16_to_f32(hi) : bf16_to_f32(hi);
       }
     }
-  }
+  };
+  auto attend = [&](int i, const Rows& x) {
+    float kx[8], vx[8];
+    to_f32(x.kw, kx);
+    to_f32(x.vw, vx);
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+    for (int r = 0; r < R; ++r) {
+      float s = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s = __builtin_fmaf(qv[r][k], kx[k], s);
+      s = row_sum16(s);
+      if (i >= w1 || (masked && x.pos > qp[r])) s = -INFINITY;
+      if (s > m[r] + kLazy) {                        // m[r] = -inf: first visible row
+        const float a = __builtin_amdgcn_exp2f(m[r] - s);
+        l[r] *= a;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[r][k] *= a;
+        m[r] = s;
+      }
+      const float pr = s == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s - m[r]);
+      l[r] += pr;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[r][k] = __builtin_fmaf(pr, vx[k], o[r][k]);
+    }
+  };
+  if (w0 < w1) {
+    Rows x0, x1, x2, x3;
+    load_rows(w0 + j, x0);
+    load_rows(w0 + 4 + j, x1);
+    load_rows(w0 + 8 + j, x2);
+    for (int i0 = w0;; i0 += 16) {
+      load_rows(i0 + 12 + j, x3);
+      attend(i0 + j, x0);
+      if (i0 + 4 >= w1) break;
+      load_rows(i0 + 16 + j, x0);
+      attend(i0 + 4 + j, x1);
+      if (i0 + 8 >= w1) break;
+      load_rows(i0 + 20 + j, x1);
+      attend(i0 + 8 + j, x2);
+      if (i0 + 12 >= w1) break;
+      load_rows(i0 + 24 + j, x2);
+      attend(i0 + 12 + j, x3);
+      if (i0 + 16 >= w1) break;
+    }
+  }
+  // the four lane groups' states of each row meet by shuffles, then the wavefronts' in LDS
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float M = m[r];
+    M = xmax32(xmax16(M));
+    const float w = m[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[r] - M);
+    float L = l[r] * w;
+    L = xsum32(xsum16(L));
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      float t = o[r][k];
-      t += __shfl_xor(t, 16, 64);
-      t += __shfl_xor(t, 32, 64);
-      if (j == 0) red[(wave * R + r) * kD + 8 * part + k] = t;
+      float t = o[r][k] * w;
+      t = xsum32(xsum16(t));
+      if (j == 0) red_o[(wave * R + r) * kD + 8 * part + k] = t;
     }
+    if (lane == 0) {
+      red_ml[(wave * 2) * R + r] = M;
+      red_ml[(wave * 2 + 1) * R + r] = L;
+    }
+  }
   __syncthreads();
   const int64_t po = static_cast<int64_t>(bh) * p.S1 + sidx;
   for (int idx = threadIdx.x; idx < p.R_real * kD; idx += kThreads) {
     const int r = idx / kD, c = idx % kD;
-    float acc = 0.0f;
+    float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) acc += red[(w * R + r) * kD + c];
-    p.ws_o[(po * R + r) * kD + c] = acc;
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_ml[(w * 2) * R + r]);
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw_ = red_ml[(w * 2) * R + r];
+      const float wgt = (mw_ == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw_ - M);
+      O += wgt * red_o[(w * R + r) * kD + c];
+      L += wgt * red_ml[(w * 2 + 1) * R + r];
+    }
+    p.ws_o[(po * R + r) * kD + c] = O;
     if (c == 0) {
-      p.ws_m[po * R + r] = stat[r];
-      p.ws_l[po * R + r] = stat[R + r];
+      p.ws_m[po * R + r] = M;
+      p.ws_l[po * R + r] = L;
     }
   }
 }
@@ -615,8 +650,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
         float d = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) d = __builtin_fmaf(qs[r][8 * n + k], kx[k], d);
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
+        d = row_sum16(d);
         if (n == 0 && i < fne) esl[r * kFusedExact + i] = ((emask[r] >> i) & 1u) ? d : -INFINITY;
       }
     }
@@ -735,13 +769,17 @@ void kivi_decode_split(DecodeParams p) {
     const int k = id / 8;
     const int bh = id % 8 + 8 * (k / p.n_split);
     if (bh < p.BH) packed_block<R, GV, DT, false>(p, bh, k % p.n_split, smem);
-  } else {
-    // exact-row blocks (windows too long for the merge) come last in dispatch order
-    const int e_id = id - n_packed;
-    const int k = e_id / 8;
-    const int bh = e_id % 8 + 8 * (k / p.n_exact_wg);
-    if (bh < p.BH) exact_block<R, DT>(p, bh, k % p.n_exact_wg, smem);
   }
+}
+
+// Exact-row blocks (windows attended neither by the packed splits nor by the merge): their own
+// launch, so their registers do not bound the packed kernel's occupancy; same XCD-aware mapping.
+template <int R, int DT>
+__global__ __launch_bounds__(kThreads) void kivi_decode_exact(DecodeParams p) {
+  extern __shared__ float smem[];
+  const int k = blockIdx.x / 8;
+  const int bh = blockIdx.x % 8 + 8 * (k / p.n_exact_wg);
+  if (bh < p.BH) exact_block<R, DT>(p, bh, k % p.n_exact_wg, smem);
 }
 
 // Score pass of the eviction path: packed blocks only, same split grid and mapping.
@@ -756,15 +794,19 @@ void kivi_score_split(DecodeParams p) {
 
 template <int R, int GV, int DT>
 int launch(DecodeParams& p, int phases, hipStream_t stream) {
-  const size_t exact_smem = (R * kD + R * kExactRows + 2 * R + kWaves * R * kD) * sizeof(float);
+  const size_t exact_smem = (R * kD + kWaves * R * kD + kWaves * 2 * R) * sizeof(float);
   const size_t packed_smem = packed_lds_floats<R>() * sizeof(float);
   const size_t fused_smem = p.fused_per > 0 ? fused_lds_floats<R, DT>() * sizeof(float) : 0;
   const int bh_pad = (p.BH + 7) / 8 * 8;
-  const dim3 grid(static_cast<unsigned>(p.S1) * bh_pad);
-  if ((phases & 1) && p.S1 > 0) {
-    hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), grid, dim3(kThreads), std::max(packed_smem + fused_smem, exact_smem),
-                       stream, p);
+  if ((phases & 1) && p.n_split > 0) {
+    hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), dim3(static_cast<unsigned>(p.n_split) * bh_pad),
+                       dim3(kThreads), packed_smem + fused_smem, stream, p);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(split)");
+  }
+  if ((phases & 1) && p.n_exact_wg > 0) {
+    hipLaunchKernelGGL((kivi_decode_exact<R, DT>), dim3(static_cast<unsigned>(p.n_exact_wg) * bh_pad),
+                       dim3(kThreads), exact_smem, stream, p);
+    KVQ_LAUNCH_CHECK("kvq_kivi_decode(exact)");
   }
   if (phases & 2) {
     MergeArgs ma{};
@@ -786,7 +828,7 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
 }
 
 struct SplitPlan {
-  int n_exact_wg, n_split, split_tokens, S1, R, fused_per;
+  int n_exact_wg, n_split, split_tokens, S1, R, fused_per, exact_rows;
 };
 
 constexpr int kCUs = 256;          // MI355X compute units
@@ -833,8 +875,9 @@ inline SplitPlan plan_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int6
   // most kExactInMerge rows), else in exact-row blocks
   const int64_t per = ns > 0 ? (n_exact + ns - 1) / ns : 0;
   sp.fused_per = (n_exact > 0 && ns > 0 && per <= kFusedExact) ? static_cast<int>(per) : 0;
-  sp.n_exact_wg = (sp.fused_per > 0 || exact_in_merge(n_exact))
-                      ? 0 : static_cast<int>((n_exact + kExactRows - 1) / kExactRows);
+  sp.exact_rows = 0;
+  sp.n_exact_wg = (n_exact == 0 || sp.fused_per > 0 || exact_in_merge(n_exact))
+                      ? 0 : plan_exact_blocks(B * Hkv, n_exact, &sp.exact_rows);
   sp.S1 = sp.n_exact_wg + sp.n_split;
   return sp;
 }
@@ -912,6 +955,7 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   p.BH = static_cast<int>(B * Hkv);
   p.n_exact_wg = sp.n_exact_wg; p.n_split = sp.n_split; p.split_tokens = sp.split_tokens; p.S1 = sp.S1;
   p.fused_per = sp.fused_per;
+  p.exact_rows = sp.exact_rows;
   p.out = out;
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define KVQ_GV(R_, DT_)                                                             \

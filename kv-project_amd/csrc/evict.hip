@@ -9,6 +9,7 @@
 // to 65536 scores take topk_retain_strided_kernel (common-prefix skip, per-wavefront histograms,
 // ballot-ordered output); longer rows take topk_retain_kernel.
 #include "common.hpp"
+#include "mfma_common.hpp"
 
 namespace kvq {
 namespace {
@@ -105,7 +106,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_kernel(const float* 
 }
 
 // Rows of at most kTopkSlots * 1024 scores (topk_retain_strided_kernel): element i = tid + 1024 e
-// is read by thread tid in slot e (coalesced); the row stays in L2 after the first read.
+// is read once, by thread tid into register slot e (coalesced); every pass runs from registers.
 //   * The leading bits shared by every key (found from the block's minimum and maximum) are
 //     skipped, so the first 8-bit digit splits the keys that actually differ; scores of one
 //     magnitude share their top bits and would otherwise pile into one or two histogram bins.
@@ -147,12 +148,21 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_strided_kernel(const
   const float* s = scores + static_cast<int64_t>(blockIdx.x) * scores_bh;
   int32_t* out = idx + static_cast<int64_t>(blockIdx.x) * idx_bh;
   const int E = (n + kTopkThreads - 1) / kTopkThreads;           // slots in use (<= kTopkSlots)
+  // the whole row, loaded once (every load in flight together): slot e of thread tid holds the
+  // order key of element tid + 1024 e, which exists for e < nv (a buffer resource over the row:
+  // one offset register, slot offsets in the scalar operand, slots past n read as zero)
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(s, static_cast<uint32_t>(n) * 4u);
+  const int nv = tid < n ? (n - tid + kTopkThreads - 1) / kTopkThreads : 0;
+  uint32_t u[kTopkSlots];
+#pragma unroll
+  for (int e = 0; e < kTopkSlots; ++e)
+    u[e] = __builtin_amdgcn_raw_buffer_load_b32(rs, tid * 4, kTopkThreads * 4 * e, 0);
   uint32_t kmax = 0u, kmin = 0xFFFFFFFFu;
-#pragma unroll 8
-  for (int i = tid; i < n; i += kTopkThreads) {
-    const uint32_t u = order_key(s[i]);
-    kmax = max(kmax, u);
-    kmin = min(kmin, u);
+#pragma unroll
+  for (int e = 0; e < kTopkSlots; ++e) {
+    u[e] = order_key(__uint_as_float(u[e]));
+    kmax = max(kmax, e < nv ? u[e] : 0u);
+    kmin = min(kmin, e < nv ? u[e] : 0xFFFFFFFFu);
   }
   kmax = block_reduce_u32(kmax, true, red);
   kmin = block_reduce_u32(kmin, false, red);
@@ -167,10 +177,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_strided_kernel(const
     const uint32_t dmask = (1u << width) - 1u;
     for (int b = lane; b < 256; b += 64) hist[wave][b] = 0u;
     __syncthreads();
-#pragma unroll 8
-    for (int i = tid; i < n; i += kTopkThreads) {
-      const uint32_t u = order_key(s[i]);
-      if ((u & mask) == prefix) atomicAdd(&hist[wave][(u >> shift) & dmask], 1u);
+#pragma unroll
+    for (int e = 0; e < kTopkSlots; ++e) {
+      if (e < nv && (u[e] & mask) == prefix) atomicAdd(&hist[wave][(u[e] >> shift) & dmask], 1u);
     }
     __syncthreads();
     // thread t < 256 holds bin 255 - t: its total and the inclusive sum over the bins above it
@@ -202,24 +211,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_strided_kernel(const
     top = shift - 1;
   }
   // prefix = key of the k-th largest score; krem = how many keys equal to it are kept: the krem
-  // equal keys at the lowest positions.  Classify every slot once (bit e of gt / eq), with the
-  // loads batched, then rank and emit from the bit masks alone.
+  // equal keys at the lowest positions.  Classify every slot (bit e of gt / eq), then rank and
+  // emit from the bit masks alone.
   uint64_t gt = 0, eq = 0;
-  for (int e0 = 0; e0 < E; e0 += 16) {
-    uint32_t u[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int i = tid + kTopkThreads * (e0 + j);
-      u[j] = (e0 + j < E && i < n) ? order_key(s[i]) : 0u;
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int i = tid + kTopkThreads * (e0 + j);
-      if (e0 + j < E && i < n) {
-        gt |= static_cast<uint64_t>(u[j] > prefix) << (e0 + j);
-        eq |= static_cast<uint64_t>(u[j] == prefix) << (e0 + j);
-      }
-    }
+  for (int e = 0; e < kTopkSlots; ++e) {
+    gt |= static_cast<uint64_t>(e < nv && u[e] > prefix) << e;
+    eq |= static_cast<uint64_t>(e < nv && u[e] == prefix) << e;
   }
   uint32_t total;
   for (int e = 0; e < E; ++e) {
@@ -261,44 +259,90 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_strided_kernel(const
 // nibble (bit offset / 4) of the value-tile word that holds token slot j
 __device__ __constant__ int kNibbleOfSlotG[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 
-// Dequantised key and value rows of the retained positions: thread (row i, channel c) of
-// (b, h) reads position t = idx[i] from the packed cache (key codes in pack_codes rows, key
-// metadata of group t / group_k; value code from the 32-token tile, its (scale, lo) pair) and
-// writes code * scale + lo (fp32 multiply then add, as kivi_quant's xhat, STRATA_KV.py:855)
-// rounded to the output type.  An index outside [0, n_valid) writes NaN rows.
+// Dequantised key and value rows of the retained positions: thread (row i, 8-channel slice sl) of
+// (b, h) reads position t = idx[i] from the packed cache -- the 4 key-code bytes of its channels
+// (pack_codes rows), their key scale and zero (16-byte loads from group t / group_k), the value
+// codes of its channels from the 32-token tile (one word per channel) and the token's (scale, lo)
+// pair of its channel group -- and writes code * scale + lo (fp32 multiply then add, as
+// kivi_quant's xhat, STRATA_KV.py:855) rounded to the output type, 8 channels per store.  An index
+// outside [0, n_valid) writes NaN rows.  16 rows per 256-thread block, every load of a thread
+// issued together after its index.
+constexpr int kGatherRows = 16;
+
+template <int DT>
+__device__ __forceinline__ void store8(void* base, int64_t i, const float (&x)[8]) {
+  if constexpr (DT == KVQ_F32) {
+    float4* p = reinterpret_cast<float4*>(static_cast<float*>(base) + i);
+    p[0] = make_float4(x[0], x[1], x[2], x[3]);
+    p[1] = make_float4(x[4], x[5], x[6], x[7]);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = DT == KVQ_F16 ? f32_to_f16(x[2 * k]) : f32_to_bf16(x[2 * k]);
+      const uint32_t hi = DT == KVQ_F16 ? f32_to_f16(x[2 * k + 1]) : f32_to_bf16(x[2 * k + 1]);
+      w[k] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void gather_dequant_kernel(
     const uint8_t* __restrict__ kc, const uint16_t* __restrict__ k_lo, const uint16_t* __restrict__ k_sc,
     const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vmeta, int64_t cap_t, int64_t n_valid,
-    int group_k, int group_v, int d, const int32_t* __restrict__ idx, int64_t count, int64_t idx_bh,
+    int group_k, int group_v, const int32_t* __restrict__ idx, int64_t count, int64_t idx_bh,
     void* __restrict__ k_out, void* __restrict__ v_out, int64_t out_bh, int64_t total) {
-  const int64_t flat = static_cast<int64_t>(blockIdx.x) * (256 / 128) + threadIdx.x / 128;
+  constexpr int d = 128;
+  const int64_t flat = static_cast<int64_t>(blockIdx.x) * kGatherRows + threadIdx.x / 16;
   if (flat >= total) return;
-  const int c = threadIdx.x % 128;
+  const int sl = threadIdx.x % 16;                   // channels 8 sl .. 8 sl + 7
   const int64_t bh = flat / count, i = flat % count;
   const int64_t t = idx[bh * idx_bh + i];
-  const int64_t o = bh * out_bh + i * d + c;
+  const int64_t o = bh * out_bh + i * d + 8 * sl;
+  float kx[8], vx[8];
   if (t < 0 || t >= n_valid) {
-    store_from_f32<DT>(k_out, o, __int_as_float(0x7fc00000));
-    store_from_f32<DT>(v_out, o, __int_as_float(0x7fc00000));
-    return;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) kx[k] = vx[k] = __int_as_float(0x7fc00000);
+  } else {
+    // keys: byte 4 sl + b holds channels 8 sl + 2b (high nibble) and 8 sl + 2b + 1 (low nibble)
+    const uint32_t kw = *reinterpret_cast<const uint32_t*>(kc + (bh * cap_t + t) * (d / 2) + 4 * sl);
+    const int64_t km = (bh * (cap_t / group_k) + t / group_k) * d + 8 * sl;
+    const uint4 sc4 = *reinterpret_cast<const uint4*>(k_sc + km);
+    const uint4 lo4 = *reinterpret_cast<const uint4*>(k_lo + km);
+    // values: channel c's word of the tile holds its 8 token slots of lane group g
+    const int64_t chunk = t / 32;
+    const int u = static_cast<int>(t % 32);
+    const int g = (u % 16) / 4, j = 4 * (u / 16) + (u % 4);
+    const int blk = sl / 2;                          // 16-channel block of the tile
+    const uint32_t* tile = reinterpret_cast<const uint32_t*>(vc + bh * cap_t * (d / 2) + chunk * 16 * d) +
+                           (blk / 4) * 256 + (16 * g + 8 * (sl % 2)) * 4 + (blk % 4);
+    uint32_t vw[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vw[e] = tile[4 * e];
+    const int ngv = d / group_v;
+    const uint32_t vm = *reinterpret_cast<const uint32_t*>(
+        vmeta + ((bh * (cap_t / 32) + chunk) * ngv + (8 * sl) / group_v) * 64 + (8 * g + j) * 2);
+    const uint32_t scw[4] = {sc4.x, sc4.y, sc4.z, sc4.w}, low[4] = {lo4.x, lo4.y, lo4.z, lo4.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t byte = (kw >> (8 * (k / 2))) & 0xffu;
+      const int kcode = (k & 1) ? static_cast<int>(byte & 15u) : static_cast<int>(byte >> 4);
+      const float sc = f16_to_f32(static_cast<uint16_t>(scw[k / 2] >> (16 * (k & 1))));
+      const float lo = f16_to_f32(static_cast<uint16_t>(low[k / 2] >> (16 * (k & 1))));
+      kx[k] = __fadd_rn(__fmul_rn(static_cast<float>(kcode), sc), lo);
+    }
+    const float sv = f16_to_f32(static_cast<uint16_t>(vm & 0xffffu));
+    const float lv = f16_to_f32(static_cast<uint16_t>(vm >> 16));
+    const int shift = 4 * kNibbleOfSlotG[j];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int vcode = static_cast<int>((vw[e] >> shift) & 15u);
+      vx[e] = __fadd_rn(__fmul_rn(static_cast<float>(vcode), sv), lv);
+    }
   }
-  const uint8_t kb = kc[(bh * cap_t + t) * (d / 2) + c / 2];
-  const int kcode = (c & 1) ? (kb & 15) : (kb >> 4);
-  const int64_t km = (bh * (cap_t / group_k) + t / group_k) * d + c;
-  const float kx = __fadd_rn(__fmul_rn(static_cast<float>(kcode), f16_to_f32(k_sc[km])), f16_to_f32(k_lo[km]));
-  const int64_t chunk = t / 32;
-  const int u = static_cast<int>(t % 32);
-  const int g = (u % 16) / 4, j = 4 * (u / 16) + (u % 4);
-  const int blk = c / 16;
-  const uint32_t* word = reinterpret_cast<const uint32_t*>(vc + bh * cap_t * (d / 2) + chunk * 16 * d) +
-                         (blk / 4) * 256 + (16 * g + c % 16) * 4 + (blk % 4);
-  const int vcode = static_cast<int>((*word >> (4 * kNibbleOfSlotG[j])) & 15u);
-  const int ngv = d / group_v;
-  const uint16_t* vm = vmeta + ((bh * (cap_t / 32) + chunk) * ngv + c / group_v) * 64 + (8 * g + j) * 2;
-  const float vx = __fadd_rn(__fmul_rn(static_cast<float>(vcode), f16_to_f32(vm[0])), f16_to_f32(vm[1]));
-  store_from_f32<DT>(k_out, o, kx);
-  store_from_f32<DT>(v_out, o, vx);
+  store8<DT>(k_out, o, kx);
+  store8<DT>(v_out, o, vx);
 }
 
 }  // namespace
@@ -321,12 +365,16 @@ extern "C" int kvq_kivi_gather_dequant(const uint8_t* kc, const uint16_t* k_lo, 
   const int64_t total = BH * count;
   if (total == 0) return KVQ_OK;
   KVQ_REQUIRE(kc && k_lo && k_sc && vc && vmeta && idx && k_out && v_out, "kvq_kivi_gather_dequant: null pointer");
-  const int64_t blocks = (total + 1) / 2;
+  KVQ_REQUIRE(out_bh % 8 == 0, "kvq_kivi_gather_dequant: out_bh must be a multiple of 8 (16-byte row slices)");
+  KVQ_REQUIRE(reinterpret_cast<uintptr_t>(k_out) % 16 == 0 && reinterpret_cast<uintptr_t>(v_out) % 16 == 0 &&
+              reinterpret_cast<uintptr_t>(k_sc) % 16 == 0 && reinterpret_cast<uintptr_t>(k_lo) % 16 == 0,
+              "kvq_kivi_gather_dequant: outputs and key metadata must be 16-byte aligned");
+  const int64_t blocks = (total + kGatherRows - 1) / kGatherRows;
   KVQ_REQUIRE(blocks < (1LL << 31), "kvq_kivi_gather_dequant: too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
   KVQ_DISPATCH_DTYPE(out_dtype, hipLaunchKernelGGL((gather_dequant_kernel<DT_>), dim3(static_cast<unsigned>(blocks)),
                                                   dim3(256), 0, s, kc, k_lo, k_sc, vc, vmeta, cap_t, n_valid,
-                                                  group_k, group_v, static_cast<int>(d), idx, count, idx_bh,
+                                                  group_k, group_v, idx, count, idx_bh,
                                                   k_out, v_out, out_bh, total));
   KVQ_LAUNCH_CHECK("kvq_kivi_gather_dequant");
   return KVQ_OK;

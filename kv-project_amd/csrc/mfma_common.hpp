@@ -62,6 +62,26 @@ __device__ __forceinline__ float xsum32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// sum / max over the 16 lanes of a row, every lane receiving the same value (DPP row rotations by
+// 8, 4, 2, 1: each step adds a commutative pair, so all lanes round alike; no LDS trip)
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp<kRowRor + 8>(x);
+  x += dpp<kRowRor + 4>(x);
+  x += dpp<kRowRor + 2>(x);
+  x += dpp<kRowRor + 1>(x);
+  return x;
+}
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp<kRowRor + 8>(x));
+  x = fmaxf(x, dpp<kRowRor + 4>(x));
+  x = fmaxf(x, dpp<kRowRor + 2>(x));
+  x = fmaxf(x, dpp<kRowRor + 1>(x));
+  return x;
+}
+// over the whole wavefront (rows, then the xor-16 and xor-32 partners)
+__device__ __forceinline__ float wave_sum(float x) { return xsum32(xsum16(row_sum16(x))); }
+__device__ __forceinline__ float wave_max(float x) { return xmax32(xmax16(row_max16(x))); }
+
 __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);

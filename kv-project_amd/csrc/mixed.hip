@@ -604,7 +604,8 @@ extern "C" int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_
                                      q_pos, out, q_dtype, workspace, ex_floats, nullptr, 0, 0.0f, 0, 1, stream);
       if (rc != KVQ_OK) return rc;
     }
-    const int64_t S_ex = (n_exact + kExactRowsPerBlock - 1) / kExactRowsPerBlock;
+    int ex_rows = 0;
+    const int64_t S_ex = plan_exact_blocks(B * Hkv, n_exact, &ex_rows);
     const int64_t nrow = B * Hkv * S_ex * R;
     ma.ex_o = workspace;
     ma.ex_m = workspace + nrow * 128;

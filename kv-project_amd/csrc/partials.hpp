@@ -12,6 +12,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "mfma_common.hpp"
 
 namespace kvq {
 namespace {
@@ -39,6 +40,18 @@ struct ExactArgs {
 constexpr int64_t kExactInMerge = 1024;
 constexpr int kExactRowsPerBlock = 64;
 inline bool exact_in_merge(int64_t n_exact) { return n_exact > 0 && n_exact <= kExactInMerge; }
+
+// Exact-row blocks of a window attended neither by packed splits nor by the merge: about one round
+// of 768 workgroups over the BH (b, h) pairs, at least kExactRowsPerBlock rows each, rows per block
+// a multiple of 16.  Returns the blocks per (b, h); *rows receives the rows of each block.
+inline int plan_exact_blocks(int64_t BH, int64_t n_exact, int* rows) {
+  const int64_t per_bh = std::max<int64_t>(1, 768 / std::max<int64_t>(BH, 1));
+  const int64_t most = (n_exact + kExactRowsPerBlock - 1) / kExactRowsPerBlock;
+  const int64_t nb = std::max<int64_t>(1, std::min(per_bh, most));
+  const int64_t r = ((n_exact + nb - 1) / nb + 15) / 16 * 16;
+  *rows = static_cast<int>(r);
+  return static_cast<int>((n_exact + r - 1) / r);
+}
 
 struct MergeArgs {
   const float* ws_o;
@@ -93,8 +106,7 @@ __device__ void exact_partial(const ExactArgs& e, int b, int hq, int t, int bh, 
       float s = 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) s = __builtin_fmaf(qv[k], kx[u][k], s);
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
+      s = row_sum16(s);
       const int i = i0 + u * kRowsPerPass + j;
       if (pt == 0 && i < n) sl[i] = vis[u] ? s : -INFINITY;
     }
@@ -102,8 +114,7 @@ __device__ void exact_partial(const ExactArgs& e, int b, int hq, int t, int bh, 
   __syncthreads();
   float m = -INFINITY;
   for (int i = tid; i < n; i += kMergeThreadsEx) m = fmaxf(m, sl[i]);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  m = wave_max(m);
   if (lane == 0) red[tid / 64] = m;
   __syncthreads();
   me = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -113,8 +124,7 @@ __device__ void exact_partial(const ExactArgs& e, int b, int hq, int t, int bh, 
     sl[i] = pr;
     l += pr;
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+  l = wave_sum(l);
   __syncthreads();                                  // red[] reads of the maximum are done
   if (lane == 0) red[tid / 64] = l;
   __syncthreads();
@@ -143,11 +153,7 @@ __device__ void exact_partial(const ExactArgs& e, int b, int hq, int t, int bh, 
 constexpr int kMergeThreads = 256;
 
 __device__ __forceinline__ float block_reduce_256(float v, bool is_max, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float u = __shfl_xor(v, o, 64);
-    v = is_max ? fmaxf(v, u) : v + u;
-  }
+  v = is_max ? wave_max(v) : wave_sum(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();

@@ -364,12 +364,8 @@ __device__ void strata_block(const StrataParams& p, const StrataTierArg& ta, int
     }
     qs[r][l] = v0;
     qs[r][l + 64] = v1;
-    float su = v0 + v1;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      su += __shfl_xor(su, o, 64);
-      mk += __shfl_xor(mk, o, 64);
-    }
+    const float su = wave_sum(v0 + v1);
+    mk = wave_sum(mk);
     if (l == 0) {
       qsum[r] = su;
       qbias[r] = mk * p.qscale;
@@ -626,11 +622,7 @@ __global__ __launch_bounds__(kSThreads) void strata_merge(StrataParams p) {
   const int hq = h * p.rep + r / p.Tq, tq = r % p.Tq;
   const int tid = threadIdx.x, lane = tid % 64;
   auto reduce = [&](float v, bool is_max) -> float {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float u = __shfl_xor(v, o, 64);
-      v = is_max ? fmaxf(v, u) : v + u;
-    }
+    v = is_max ? wave_max(v) : wave_sum(v);
     __syncthreads();
     if (lane == 0) red[tid / 64] = v;
     __syncthreads();
@@ -803,7 +795,8 @@ extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64
   p.out = out;
   // exact rows: partials of the KIVI exact-row blocks (no packed rows), into the first region
   const bool ex_merge = exact_in_merge(n_exact);
-  const int64_t S_ex = ex_merge ? 0 : (n_exact + kExactRowsPerBlock - 1) / kExactRowsPerBlock;
+  int ex_rows = 0;
+  const int64_t S_ex = (ex_merge || n_exact == 0) ? 0 : plan_exact_blocks(B * Hkv, n_exact, &ex_rows);
   if (ex_merge) {
     p.ex = ExactArgs{q, q_sb, q_sh, q_st, p.qscale, k_exact, v_exact, cap_e, static_cast<int>(n_exact), exact_pos, q_pos};
   } else if (n_exact > 0) {

@@ -41,9 +41,10 @@ def topk_retain(scores: torch.Tensor, k: int) -> torch.Tensor:
 
 
 @torch.no_grad()
-def gather_dequant(cache: PackedKIVICache, idx: torch.Tensor, dtype: torch.dtype):
+def gather_dequant(cache: PackedKIVICache, idx: torch.Tensor, dtype: torch.dtype, out=None):
     """Dequantised key / value rows (B, Hkv, k, d) of ``dtype`` at packed positions idx (B, Hkv, k)
-    (code * scale + lo in fp32, as kivi_quant's xhat; STRATA_KV.py:855)."""
+    (code * scale + lo in fp32, as kivi_quant's xhat; STRATA_KV.py:855).  ``out`` = (ko, vo): rows
+    [0, k) of the third axis of two (B, Hkv, >= k, d) tensors receive them instead."""
     _lib.require_gpu(idx)
     B, H = cache.kc.shape[:2]
     d = cache.kc.shape[3] * 2
@@ -51,12 +52,18 @@ def gather_dequant(cache: PackedKIVICache, idx: torch.Tensor, dtype: torch.dtype
         raise ValueError("idx must be int32 (B, Hkv, k)")
     idx = idx.contiguous()
     k = idx.shape[2]
-    ko = torch.empty((B, H, k, d), dtype=dtype, device=idx.device)
-    vo = torch.empty_like(ko)
+    if out is None:
+        ko = torch.empty((B, H, k, d), dtype=dtype, device=idx.device)
+        vo = torch.empty_like(ko)
+    else:
+        ko, vo = out
+        if (ko.shape[:2] != (B, H) or ko.shape[2] < k or ko.shape[3] != d or vo.shape != ko.shape
+                or ko.dtype != dtype or vo.dtype != dtype or not ko.is_contiguous() or not vo.is_contiguous()):
+            raise ValueError("out must be two contiguous (B, Hkv, >= k, d) tensors of dtype")
     _lib.call("kvq_kivi_gather_dequant", cache.kc.data_ptr(), cache.k_lo.data_ptr(), cache.k_sc.data_ptr(),
               cache.vc.data_ptr(), cache.vmeta.data_ptr(), cache.cap_t, cache.n_q, cache.group_k, cache.group_v,
-              B * H, d, idx.data_ptr(), k, k, ko.data_ptr(), vo.data_ptr(), _lib.DTYPE_CODE[dtype], k * d,
-              _lib.stream_of(idx))
+              B * H, d, idx.data_ptr(), k, k, ko.data_ptr(), vo.data_ptr(), _lib.DTYPE_CODE[dtype],
+              ko.shape[2] * d, _lib.stream_of(idx))
     return ko, vo
 
 
@@ -64,8 +71,14 @@ def gather_dequant(cache: PackedKIVICache, idx: torch.Tensor, dtype: torch.dtype
 def retained_cache(cache: PackedKIVICache, idx: torch.Tensor) -> PackedKIVICache:
     """The cache after eviction: the retained packed positions idx (B, Hkv, k), dequantised, followed
     by the cache's exact rows (the recent window, always kept) -- all read as exact rows by the
-    decode kernel (n_q = 0)."""
-    ko, vo = gather_dequant(cache, idx, cache.k_exact.dtype)
-    ke = torch.cat([ko, cache.k_exact[:, :, :cache.n_exact]], 2).contiguous()
-    ve = torch.cat([vo, cache.v_exact[:, :, :cache.n_exact]], 2).contiguous()
-    return replace(cache, n_q=0, k_exact=ke, v_exact=ve, n_exact=ke.shape[2], exact_pos=None, ring=False)
+    decode kernel (n_q = 0).  The gather writes straight into the combined rows."""
+    B, H, k = idx.shape
+    ne = cache.n_exact
+    d = cache.kc.shape[3] * 2
+    ke = torch.empty((B, H, k + ne, d), dtype=cache.k_exact.dtype, device=idx.device)
+    ve = torch.empty_like(ke)
+    gather_dequant(cache, idx, cache.k_exact.dtype, out=(ke, ve))
+    if ne > 0:
+        ke[:, :, k:].copy_(cache.k_exact[:, :, :ne])
+        ve[:, :, k:].copy_(cache.v_exact[:, :, :ne])
+    return replace(cache, n_q=0, k_exact=ke, v_exact=ve, n_exact=k + ne, exact_pos=None, ring=False)

@@ -85,6 +85,8 @@ def test_forced_small_splits(split):
 def test_exact_rows_only_and_packed_only():
     err, _, _ = _run(1, 32, 8, 300, 300, 64, 64, torch.float32, seed=1)     # n_q = 0
     assert err <= 2e-3, err
+    err, _, _ = _run(2, 32, 8, 2500, 2500, 64, 64, torch.bfloat16, seed=6)  # n_q = 0, exact-row blocks
+    assert err <= TOL[torch.bfloat16], err
     err, _, _ = _run(1, 32, 8, 1024, 0, 64, 64, torch.float32, seed=2)      # n_exact = 0
     assert err <= 2e-3, err
     err, _, _ = _run(1, 32, 8, 3000, 700, 64, 64, torch.float32, seed=3)    # window in the merge

@@ -76,20 +76,29 @@ def test_decode_score_accumulation(Hq, Hkv, Tq):
     np.testing.assert_allclose(got, want, rtol=2e-4, atol=1e-9)
 
 
-def test_gather_dequant_bit_exact():
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gather_dequant_bit_exact(dtype):
+    """Retained rows equal kivi_quant's xhat (fp32, then rounded once to the output type); an index
+    outside [0, n_q) gives a NaN row."""
     import kvq
     B, Hkv, T, W, gk, gv = 2, 2, 1000, 40, 64, 32
     cache, K, V, kh, vh, g = _packed(B, Hkv, T, W, gk, gv, seed=7)
     n_q = T - W
     idx = torch.stack([torch.sort(torch.randperm(n_q, generator=g)[:77]).values for _ in range(B * Hkv)])
     idx[0, -1] = n_q - 1                                                   # last row of the last tile
+    idx[1, 3] = -1                                                         # outside the packed rows
+    idx[2, 5] = n_q
     idx = idx.reshape(B, Hkv, 77).to(torch.int32)
-    ko, vo = kvq.gather_dequant(cache, idx.cuda(), torch.float32)
+    ko, vo = kvq.gather_dequant(cache, idx.cuda(), dtype)
     ii = idx.long().numpy()
-    want_k = np.take_along_axis(kh.astype(np.float32), ii[..., None], 2)
-    want_v = np.take_along_axis(vh.astype(np.float32), ii[..., None], 2)
-    np.testing.assert_array_equal(ko.cpu().numpy(), want_k)
-    np.testing.assert_array_equal(vo.cpu().numpy(), want_v)
+    bad = (ii < 0) | (ii >= n_q)
+    jj = np.where(bad, 0, ii)
+    want_k = torch.from_numpy(np.take_along_axis(kh.astype(np.float32), jj[..., None], 2)).to(dtype).float().numpy()
+    want_v = torch.from_numpy(np.take_along_axis(vh.astype(np.float32), jj[..., None], 2)).to(dtype).float().numpy()
+    want_k[bad] = np.nan
+    want_v[bad] = np.nan
+    np.testing.assert_array_equal(ko.float().cpu().numpy(), want_k)
+    np.testing.assert_array_equal(vo.float().cpu().numpy(), want_v)
 
 
 def test_c4_reduced_eviction_end_to_end():
