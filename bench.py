@@ -19,9 +19,10 @@ Each prints one JSON line of the same form (its own metric, roofline and CPU bas
 Timing: W untimed warm-up steps, then K steps launched back to back between HIP events on the
 launch stream (device synchronisation on both sides).  The same step captured once in a HIP graph
 (the reference's _time_callable protocol, STRATA_KV.py:3424-3447) is timed too and reported as
-``graph_us``: on this ROCm stack graph replays of these launches measure slower than the eager
-launches.  The dominant kernel is timed the same way on its own for the roofline figure; its
-rocprofv3 kernel-trace average is committed beside the summaries.  The CPU baseline is the oracle's restatement of the
+``graph_us``: on this ROCm stack a replay of a one-step graph costs more than the eager launches.
+The dominant kernel is timed on its own as K launches captured in ONE graph and replayed once
+(``kernel_us``: the GPU time per launch without host dispatch between launches, the figure a
+rocprofv3 kernel-trace average gives); its rocprofv3 summary is committed under profiles/.  The CPU baseline is the oracle's restatement of the
 reference path on a bounded sample of the same workload, scaled to the whole workload.
 """
 from __future__ import annotations
@@ -76,6 +77,25 @@ def graph_ms(fn, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         g.replay()
     return _events_ms(g.replay, steps)
+
+
+def graph_k_ms(fn, steps: int, warmup: int) -> float:
+    """K back-to-back calls of fn captured in one HIP graph, replayed once untimed and once timed:
+    GPU time per call, no host dispatch between the launches (launch-bound kernels included)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for _ in range(steps):
+            fn()
+    gr.replay()
+    return _events_ms(gr.replay, 1) / steps
 
 
 def eager_ms(fn, steps: int, warmup: int) -> float:
@@ -186,7 +206,8 @@ def run_kivi(args, shape_name: str) -> dict:
 
     log("timing")
     ms_per_step, g_ms = step_ms(step, args.steps, args.warmup)
-    split_ms = eager_ms(split_only, args.steps, args.warmup)
+    split_ms = graph_k_ms(split_only, args.steps, args.warmup)
+    step_gpu_ms = graph_k_ms(step, args.steps, args.warmup)
     io_bytes = q.numel() * q.element_size() + out.numel() * out.element_size()
     bytes_alg = cache.payload_bytes() + io_bytes
     # the split kernel reads the packed rows, the exact rows and q; the output belongs to the merge
@@ -210,7 +231,7 @@ def run_kivi(args, shape_name: str) -> dict:
                   roofline=_roof(split_bytes, split_ms, "kivi_decode_split", traffic),
                   us_per_layer=round(ms_per_step * 1e3, 3),
                   timer="back-to-back launches, HIP events over the timed steps",
-                  graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg,
+                  graph_us=round(g_ms * 1e3, 3), step_gpu_us=round(step_gpu_ms * 1e3, 3), bytes_alg=bytes_alg,
                   packed_code_GBs=round(2 * shape.B * shape.Hkv * cache.n_q * shape.d // 2 / (ms_per_step * 1e-3) / 1e9,
                                         2))
     log(f"decode step {ms_per_step * 1e3:.1f} us, split kernel {split_ms * 1e3:.1f} us")
@@ -241,7 +262,7 @@ def run_c3(args) -> dict:
     step = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws)
     split = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
-    split_ms = eager_ms(split, args.steps, args.warmup)
+    split_ms = graph_k_ms(split, args.steps, args.warmup)
     qb = q.numel() * q.element_size()
     bytes_alg = cache.coded_bytes() + qb + out.numel() * out.element_size()
     avg_bits = float(widths.float().mean())
@@ -302,6 +323,7 @@ def run_strata(args) -> dict:
                                                   [t.bits for t in cache.tiers]),), dtype=torch.float32, device="cuda")
     step = lambda: kvq.strata_decode(q, scaling, cache, out=out, workspace=ws)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
+    k_ms = graph_k_ms(step, args.steps, args.warmup)
     qb = q.numel() * q.element_size()
     bytes_alg = cache.coded_bytes() + qb + out.numel() * out.element_size()
     res = _result(args, metric="STRATA strata decode (per-token 8/4/2-bit tiers): effective HBM GB/s + µs/layer",
@@ -311,7 +333,7 @@ def run_strata(args) -> dict:
                            "B=8, Hq=32, Hkv=8, d=128, T=16384, no exact rows)",
                   config={"global_batch": s.B, "seq_len": s.T, "parallelism": "single GPU",
                           "tokens_8_4_2": [n8, n4, s.T - n8 - n4]},
-                  dtype="bf16", roofline=_roof(bytes_alg, ms, "strata_split_all + strata_merge (whole step)"),
+                  dtype="bf16", roofline=_roof(bytes_alg, k_ms, "strata_split_all + strata_merge (whole step)"),
                   us_per_layer=round(ms * 1e3, 3), graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg)
     log(f"STRATA step {ms * 1e3:.1f} us")
     if not args.no_cpu_baseline:
@@ -358,7 +380,7 @@ def run_c5(args) -> dict:
     step = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws)
     split = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
-    split_ms = eager_ms(split, args.steps, args.warmup)
+    split_ms = graph_k_ms(split, args.steps, args.warmup)
     # the encoder: keys and values of the whole context, one launch each
     kc, ks = torch.empty_like(cache.kc), torch.empty_like(cache.ks)
     ctab = kvq.dct_table()
@@ -435,7 +457,7 @@ def run_c4(args) -> dict:
     plain_ms = eager_ms(plain, args.steps, args.warmup)
     scored_ms, g_ms = step_ms(scored, args.steps, args.warmup)
     plain()
-    score_ms = eager_ms(score_only, args.steps, args.warmup)
+    score_ms = graph_k_ms(score_only, args.steps, args.warmup)
     # the eviction workload proper: 32 scored decode steps, top-k, gather, decode over the kept rows
     scores.zero_()
     torch.cuda.synchronize()
@@ -444,6 +466,8 @@ def run_c4(args) -> dict:
     topk = lambda: kvq.topk_retain(scores, C4_KEEP)
     topk_ms = eager_ms(topk, args.steps, args.warmup)
     idx = kvq.topk_retain(scores, C4_KEEP)
+    idx_buf = torch.empty_like(idx)
+    topk_fixed = lambda: kvq.topk_retain(scores, C4_KEEP, out=idx_buf)
     kept = kvq.retained_cache(cache, idx)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -456,6 +480,8 @@ def run_c4(args) -> dict:
                        dtype=torch.float32, device="cuda")
     kept_dec = lambda: kvq.kivi_decode(q0, scaling, kept, out=out_k, workspace=ws_k)
     kept_ms = eager_ms(kept_dec, args.steps, args.warmup)
+    kept_gpu_ms = graph_k_ms(kept_dec, args.steps, args.warmup)
+    topk_gpu_ms = graph_k_ms(topk_fixed, args.steps, args.warmup)
     n_q, BH = cache.n_q, s.B * s.Hkv
     kbytes = BH * n_q * (s.d // 2) + BH * (n_q // C4_GROUP) * s.d * 4
     score_bytes = kbytes + 2 * BH * n_q * 4 + q0.numel() * q0.element_size()
@@ -470,7 +496,8 @@ def run_c4(args) -> dict:
                   dtype="bf16", roofline=_roof(score_bytes, score_ms, "kivi_score_split"),
                   graph_us=round(g_ms * 1e3, 3), plain_decode_us=round(plain_ms * 1e3, 3), score_pass_us=round(score_ms * 1e3, 3),
                   topk_us=round(topk_ms * 1e3, 3), gather_us_host_timed=round(gather_ms * 1e3, 3),
-                  retained_decode_us=round(kept_ms * 1e3, 3),
+                  retained_decode_us=round(kept_ms * 1e3, 3), retained_decode_gpu_us=round(kept_gpu_ms * 1e3, 3),
+                  topk_gpu_us=round(topk_gpu_ms * 1e3, 3),
                   episode_ms=round(ep_ms, 4),
                   decode_GBs=round((cache.payload_bytes() + 2 * q0.numel() * 2) / (plain_ms * 1e-3) / 1e9, 2))
     log(f"C4 scored step {scored_ms * 1e3:.1f} us (plain {plain_ms * 1e3:.1f}, score pass {score_ms * 1e3:.1f}), "

@@ -22,9 +22,10 @@ from .decode import PackedKIVICache
 
 
 @torch.no_grad()
-def topk_retain(scores: torch.Tensor, k: int) -> torch.Tensor:
+def topk_retain(scores: torch.Tensor, k: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """scores (..., n) float32 on the GPU -> int32 (..., k): the positions of the k largest scores of
-    each row in increasing order (lowest positions kept among scores tied at the k-th)."""
+    each row in increasing order (lowest positions kept among scores tied at the k-th).  ``out``: a
+    contiguous int32 (..., k) tensor to write them into."""
     _lib.require_gpu(scores)
     if scores.dtype != torch.float32:
         raise TypeError("scores must be float32")
@@ -34,7 +35,12 @@ def topk_retain(scores: torch.Tensor, k: int) -> torch.Tensor:
     rows = scores.reshape(-1, n)
     if rows.stride(-1) != 1:
         rows = rows.contiguous()
-    idx = torch.empty(rows.shape[0], k, dtype=torch.int32, device=scores.device)
+    if out is None:
+        idx = torch.empty(rows.shape[0], k, dtype=torch.int32, device=scores.device)
+    else:
+        if out.dtype != torch.int32 or out.shape != scores.shape[:-1] + (k,) or not out.is_contiguous():
+            raise ValueError("out must be a contiguous int32 (..., k) tensor")
+        idx = out.view(rows.shape[0], k)
     _lib.call("kvq_topk_retain", rows.data_ptr(), rows.shape[0], n, rows.stride(0), k, idx.data_ptr(), k,
               _lib.stream_of(scores))
     return idx.reshape(scores.shape[:-1] + (k,))
