@@ -156,7 +156,9 @@ int kvq_topk_retain(const float* scores, int64_t BH, int64_t n, int64_t scores_b
  * kivi_quant's xhat is (code * scale + lo in fp32, STRATA_KV.py:855) and written, rounded to
  * out_dtype, to k_out / v_out (B*Hkv, out_bh elements per (b,h), row i at i*d).  Positions must
  * lie in [0, n_valid); others produce NaN rows.  The decode over the retained set is then
- * kvq_kivi_decode with these rows (plus the recent window) as exact rows and n_q = 0.
+ * kvq_kivi_decode with these rows (plus the recent window) as exact rows and n_q = 0.  d = 128;
+ * k_out, v_out, k_lo and k_sc 16-byte aligned; out_bh a multiple of 8 (so a caller can write
+ * the rows straight into a larger buffer that also holds the window).
  * ---------------------------------------------------------------------------------------- */
 int kvq_kivi_gather_dequant(const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_sc,
                             const uint8_t* vc, const uint16_t* vmeta, int64_t cap_t, int64_t n_valid,
