@@ -257,7 +257,7 @@ def run_c3(args) -> dict:
     cache = kvq.MixedKIVICache.from_context(K, V, widths, window=0)
     scaling = s.d ** -0.5
     out = torch.empty((s.B, 1, s.Hq, s.d), dtype=s.dtype, device="cuda")
-    ws = torch.empty((kvq.mixed_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.nb, 0),), dtype=torch.float32,
+    ws = torch.zeros((kvq.mixed_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.nb, 0),), dtype=torch.float32,
                      device="cuda")
     step = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws)
     split = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
@@ -319,7 +319,7 @@ def run_strata(args) -> dict:
     cache = kvq.StrataCache.from_context(K, V, window=0, assign=assign)
     scaling = s.d ** -0.5
     out = torch.empty((s.B, 1, s.Hq, s.d), dtype=s.dtype, device="cuda")
-    ws = torch.empty((kvq.strata_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.n_exact, [t.n for t in cache.tiers],
+    ws = torch.zeros((kvq.strata_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.n_exact, [t.n for t in cache.tiers],
                                                   [t.bits for t in cache.tiers]),), dtype=torch.float32, device="cuda")
     step = lambda: kvq.strata_decode(q, scaling, cache, out=out, workspace=ws)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
@@ -375,7 +375,7 @@ def run_c5(args) -> dict:
     cache = kvq.DctCache.from_context(K, V, window=0)
     scaling = s.d ** -0.5
     out = torch.empty((s.B, 1, s.Hq, s.d), dtype=s.dtype, device="cuda")
-    ws = torch.empty((kvq.dct_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.T, 0),), dtype=torch.float32,
+    ws = torch.zeros((kvq.dct_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.T, 0),), dtype=torch.float32,
                      device="cuda")
     step = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws)
     split = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
@@ -444,7 +444,7 @@ def run_c4(args) -> dict:
     cache = kvq.PackedKIVICache.from_context(K, V, window=C4_WINDOW, group_k=C4_GROUP, group_v=C4_GROUP)
     scaling = s.d ** -0.5
     out = torch.empty((s.B, 1, s.Hq, s.d), dtype=s.dtype, device="cuda")
-    ws = torch.empty((kvq.workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.n_q, cache.n_exact, C4_GROUP, C4_GROUP),),
+    ws = torch.zeros((kvq.workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.n_q, cache.n_exact, C4_GROUP, C4_GROUP),),
                      dtype=torch.float32, device="cuda")
     scores = torch.zeros((s.B, s.Hkv, cache.n_q), dtype=torch.float32, device="cuda")
     rep = s.Hq // s.Hkv
@@ -476,7 +476,7 @@ def run_c4(args) -> dict:
     torch.cuda.synchronize()
     gather_ms = (time.perf_counter() - t0) * 1e3 / 5
     out_k = torch.empty_like(out)
-    ws_k = torch.empty((kvq.workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, kept.n_q, kept.n_exact, C4_GROUP, C4_GROUP),),
+    ws_k = torch.zeros((kvq.workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, kept.n_q, kept.n_exact, C4_GROUP, C4_GROUP),),
                        dtype=torch.float32, device="cuda")
     kept_dec = lambda: kvq.kivi_decode(q0, scaling, kept, out=out_k, workspace=ws_k)
     kept_ms = eager_ms(kept_dec, args.steps, args.warmup)

@@ -178,7 +178,7 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
     need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, cache.group_v,
                             split_tokens)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty((need,), dtype=torch.float32, device=q.device)
+        workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)
     if phases is None:
         phases = 7 if scores is not None else 3
     if scores is not None:

@@ -223,7 +223,7 @@ def strata_decode(q: torch.Tensor, scaling: float, cache: StrataCache, *, q_pos:
     nt = len(tiers)
     need = strata_workspace_floats(B, Hq, Hkv, Tq, d, cache.n_exact, [t.n for t in tiers], [t.bits for t in tiers])
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty((need,), dtype=torch.float32, device=q.device)
+        workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)
     if out is None:
         out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
     P = ctypes.c_void_p
