@@ -490,7 +490,8 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
 namespace {
 int64_t dct_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t T, int64_t n_exact, int64_t* ex_floats,
                      int* S) {
-  *S = T > 0 ? kvq::plan_block_splits(B * Hkv, T / 64, 4, 4) : 0;
+  // 3 workgroups per CU: LDS-bound (~41 KB each at 8 rows)
+  *S = T > 0 ? kvq::plan_block_splits(B * Hkv, T / 64, 3, 4) : 0;
   *ex_floats = (n_exact > 0 && !kvq::exact_in_merge(n_exact))
                    ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
   const int64_t R = kvq::pow2_rows((Hq / Hkv) * Tq);
