@@ -6,8 +6,8 @@
 // fp32 scores (8 bits per pass, LDS histograms) finds the k-th largest key T and how many keys
 // equal to T are kept; the retained positions are then written in increasing order.  Among keys
 // equal to T the lowest positions are kept (torch.topk leaves that order unspecified).  Rows of up
-// to 65536 scores take topk_retain_strided_kernel (common-prefix skip, per-wavefront histograms,
-// ballot-ordered output); longer rows take topk_retain_kernel.
+// to 65536 scores take topk_retain_rows_kernel (row in registers, a 12-bit float-bucket first
+// pass, scan-ordered output); longer rows take topk_retain_kernel.
 #include "common.hpp"
 #include "mfma_common.hpp"
 
@@ -105,77 +105,91 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_kernel(const float* 
   }
 }
 
-// Rows of at most kTopkSlots * 1024 scores (topk_retain_strided_kernel): element i = tid + 1024 e
-// is read once, by thread tid into register slot e (coalesced); every pass runs from registers.
-//   * The leading bits shared by every key (found from the block's minimum and maximum) are
-//     skipped, so the first 8-bit digit splits the keys that actually differ; scores of one
-//     magnitude share their top bits and would otherwise pile into one or two histogram bins.
-//   * One 256-bin histogram per wavefront (LDS atomics contend only inside a wavefront), summed
-//     per bin; the digit of the k-th largest key is found by a parallel suffix sum.
-//   * Output in position order: per slot e, a ballot gives each wavefront's count; one block scan
-//     over the (e, wavefront) counts gives every selected position its output index.
+// Rows of at most kTopkSlots * 1024 scores (topk_retain_rows_kernel): thread t holds elements
+// 64 t .. 64 t + 63, read once with 16-byte loads and kept in registers as order keys.
+//   * First pass: one 4096-bin LDS histogram of the top 12 bits of every key (sign, exponent and
+//     3 mantissa bits: 8 bins per octave of magnitude, so scores of one magnitude spread over
+//     several bins instead of colliding in one); a suffix scan over the bins (one block scan)
+//     finds the bin of the k-th largest key.
+//   * The remaining 20 bits by 8-, 8- and 4-bit passes over the keys still matching the prefix
+//     (per-wavefront 256-bin histograms).
+//   * Output in position order: per-thread bit masks of the kept slots; one block scan of the
+//     tie counts (ties beyond the kept ones dropped, lowest positions first) and one of the kept
+//     counts gives every thread its output offset.
 constexpr int kTopkSlots = 64;
+constexpr int kTopkBins1 = 4096;
 
-__device__ __forceinline__ uint32_t block_reduce_u32(uint32_t v, bool is_max, uint32_t* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t u = __shfl_xor(v, o, 64);
-    v = is_max ? max(v, u) : min(v, u);
-  }
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint32_t r = red[0];
-  for (int w = 1; w < kTopkThreads / 64; ++w) r = is_max ? max(r, red[w]) : min(r, red[w]);
-  return r;
-}
-
-__device__ __forceinline__ int lane_rank(uint64_t ballot) {
-  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(ballot >> 32),
-                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(ballot), 0u));
-}
-
-__global__ __launch_bounds__(kTopkThreads) void topk_retain_strided_kernel(const float* __restrict__ scores,
-                                                                           int n, int64_t scores_bh, int k,
-                                                                           int32_t* __restrict__ idx, int64_t idx_bh) {
+__global__ __launch_bounds__(kTopkThreads) void topk_retain_rows_kernel(const float* __restrict__ scores,
+                                                                        int n, int64_t scores_bh, int k,
+                                                                        int32_t* __restrict__ idx, int64_t idx_bh) {
   constexpr int NW = kTopkThreads / 64;
+  __shared__ uint32_t hist1[kTopkBins1];
   __shared__ uint32_t hist[NW][256];
-  __shared__ uint32_t cnt[kTopkSlots * NW];
   __shared__ uint32_t wave_sums[32];
-  __shared__ uint32_t red[NW];
   __shared__ uint32_t sh_prefix, sh_krem;
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
   const float* s = scores + static_cast<int64_t>(blockIdx.x) * scores_bh;
   int32_t* out = idx + static_cast<int64_t>(blockIdx.x) * idx_bh;
-  const int E = (n + kTopkThreads - 1) / kTopkThreads;           // slots in use (<= kTopkSlots)
-  // the whole row, loaded once (every load in flight together): slot e of thread tid holds the
-  // order key of element tid + 1024 e, which exists for e < nv (a buffer resource over the row:
-  // one offset register, slot offsets in the scalar operand, slots past n read as zero)
+  const int base = tid * kTopkSlots;
+  const int nv = min(max(n - base, 0), kTopkSlots);            // slots of this thread that exist
+  // buffer loads past n read zero; every load in flight together
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(s, static_cast<uint32_t>(n) * 4u);
-  const int nv = tid < n ? (n - tid + kTopkThreads - 1) / kTopkThreads : 0;
   uint32_t u[kTopkSlots];
 #pragma unroll
-  for (int e = 0; e < kTopkSlots; ++e)
-    u[e] = __builtin_amdgcn_raw_buffer_load_b32(rs, tid * 4, kTopkThreads * 4 * e, 0);
-  uint32_t kmax = 0u, kmin = 0xFFFFFFFFu;
+  for (int j = 0; j < kTopkSlots / 4; ++j) {
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, base * 4 + 16 * j, 0, 0);
+    u[4 * j] = w[0];
+    u[4 * j + 1] = w[1];
+    u[4 * j + 2] = w[2];
+    u[4 * j + 3] = w[3];
+  }
+  // a 16-byte load that straddles n may be range-checked as a whole: the thread holding the
+  // row's ragged last chunk (n % 4 != 0) reloads that chunk with 4-byte loads
+  if ((n & 3) != 0 && base <= n - 1 && n - 1 < base + kTopkSlots) {
+    const int jb = (n - 1 - base) >> 2;
+#pragma unroll
+    for (int j = 0; j < kTopkSlots / 4; ++j) {
+      if (j == jb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) u[4 * j + i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (base + 4 * j + i) * 4, 0, 0);
+      }
+    }
+  }
+  for (int bn = tid; bn < kTopkBins1; bn += kTopkThreads) hist1[bn] = 0u;
+  __syncthreads();
 #pragma unroll
   for (int e = 0; e < kTopkSlots; ++e) {
     u[e] = order_key(__uint_as_float(u[e]));
-    kmax = max(kmax, e < nv ? u[e] : 0u);
-    kmin = min(kmin, e < nv ? u[e] : 0xFFFFFFFFu);
+    if (e < nv) atomicAdd(&hist1[u[e] >> 20], 1u);
   }
-  kmax = block_reduce_u32(kmax, true, red);
-  kmin = block_reduce_u32(kmin, false, red);
-  const uint32_t diff = kmax ^ kmin;
-  int top = diff ? 31 - __builtin_clz(diff) : -1;     // highest bit in which keys differ
-  uint32_t mask = top < 0 ? 0xFFFFFFFFu : (top >= 31 ? 0u : ~((2u << top) - 1u));
-  uint32_t prefix = kmax & mask;
-  uint32_t krem = static_cast<uint32_t>(k);
+  __syncthreads();
+  // thread t owns bins 4095 - 4t - i (i = 0..3, descending); keys in higher bins come first
+  uint32_t c4[4], tot = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c4[i] = hist1[kTopkBins1 - 1 - 4 * tid - i];
+    tot += c4[i];
+  }
+  uint32_t total;
+  uint32_t run = block_exclusive_scan(tot, wave_sums, &total);
+  const uint32_t kk = static_cast<uint32_t>(k);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (c4[i] > 0u && run < kk && run + c4[i] >= kk) {
+      sh_prefix = static_cast<uint32_t>(kTopkBins1 - 1 - 4 * tid - i) << 20;
+      sh_krem = kk - run;
+    }
+    run += c4[i];
+  }
+  __syncthreads();
+  uint32_t prefix = sh_prefix, krem = sh_krem;
+  uint32_t mask = 0xFFF00000u;
+  int top = 19;
   while (top >= 0) {
     const int width = min(8, top + 1);
     const int shift = top - width + 1;
     const uint32_t dmask = (1u << width) - 1u;
-    for (int b = lane; b < 256; b += 64) hist[wave][b] = 0u;
+    for (int bn = lane; bn < 256; bn += 64) hist[wave][bn] = 0u;
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < kTopkSlots; ++e) {
@@ -183,11 +197,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_strided_kernel(const
     }
     __syncthreads();
     // thread t < 256 holds bin 255 - t: its total and the inclusive sum over the bins above it
-    uint32_t tot = 0u;
+    uint32_t bt = 0u;
     if (tid < 256) {
-      for (int w = 0; w < NW; ++w) tot += hist[w][255 - tid];
+      for (int w = 0; w < NW; ++w) bt += hist[w][255 - tid];
     }
-    uint32_t x = tot;
+    uint32_t x = bt;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const uint32_t y = __shfl_up(x, o, 64);
@@ -198,8 +212,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_strided_kernel(const
     if (tid < 256) {
       uint32_t before = 0u;
       for (int w = 0; w < wave; ++w) before += wave_sums[w];
-      const uint32_t incl = before + x, excl = incl - tot;
-      if (tot > 0u && excl < krem && incl >= krem) {
+      const uint32_t incl = before + x, excl = incl - bt;
+      if (bt > 0u && excl < krem && incl >= krem) {
         sh_prefix = prefix | (static_cast<uint32_t>(255 - tid) << shift);
         sh_krem = krem - excl;
       }
@@ -210,50 +224,25 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_strided_kernel(const
     mask |= dmask << shift;
     top = shift - 1;
   }
-  // prefix = key of the k-th largest score; krem = how many keys equal to it are kept: the krem
-  // equal keys at the lowest positions.  Classify every slot (bit e of gt / eq), then rank and
-  // emit from the bit masks alone.
+  // prefix = key of the k-th largest score; krem = how many keys equal to it are kept (those at
+  // the lowest positions)
   uint64_t gt = 0, eq = 0;
 #pragma unroll
   for (int e = 0; e < kTopkSlots; ++e) {
     gt |= static_cast<uint64_t>(e < nv && u[e] > prefix) << e;
     eq |= static_cast<uint64_t>(e < nv && u[e] == prefix) << e;
   }
-  uint32_t total;
-  for (int e = 0; e < E; ++e) {
-    const uint64_t b = __ballot((eq >> e) & 1u);
-    if (lane == 0) cnt[e * NW + wave] = static_cast<uint32_t>(__builtin_popcountll(b));
+  uint32_t total_eq;
+  const uint32_t eq_before = block_exclusive_scan(static_cast<uint32_t>(__builtin_popcountll(eq)), wave_sums, &total_eq);
+  uint64_t sel = gt;
+  if (total_eq == krem) {
+    sel |= eq;
+  } else {
+    uint32_t r = eq_before;
+    for (uint64_t m = eq; m != 0 && r < krem; m &= m - 1, ++r) sel |= m & (~m + 1);
   }
-  __syncthreads();
-  {
-    const uint32_t c = tid < E * NW ? cnt[tid] : 0u;
-    const uint32_t pre = block_exclusive_scan(c, wave_sums, &total);
-    if (tid < E * NW) cnt[tid] = pre;
-  }
-  __syncthreads();
-  uint64_t sel = gt;                                  // + the kept ties
-  for (int e = 0; e < E; ++e) {
-    const bool is_eq = (eq >> e) & 1u;
-    const uint64_t b = __ballot(is_eq);
-    if (is_eq && cnt[e * NW + wave] + lane_rank(b) < krem) sel |= 1ull << e;
-  }
-  __syncthreads();
-  for (int e = 0; e < E; ++e) {
-    const uint64_t b = __ballot((sel >> e) & 1u);
-    if (lane == 0) cnt[e * NW + wave] = static_cast<uint32_t>(__builtin_popcountll(b));
-  }
-  __syncthreads();
-  {
-    const uint32_t c = tid < E * NW ? cnt[tid] : 0u;
-    const uint32_t pre = block_exclusive_scan(c, wave_sums, &total);
-    if (tid < E * NW) cnt[tid] = pre;
-  }
-  __syncthreads();
-  for (int e = 0; e < E; ++e) {
-    const bool take = (sel >> e) & 1u;
-    const uint64_t b = __ballot(take);
-    if (take) out[cnt[e * NW + wave] + lane_rank(b)] = tid + kTopkThreads * e;
-  }
+  uint32_t off = block_exclusive_scan(static_cast<uint32_t>(__builtin_popcountll(sel)), wave_sums, &total);
+  for (uint64_t m = sel; m != 0; m &= m - 1) out[off++] = base + __builtin_ctzll(m);
 }
 
 // nibble (bit offset / 4) of the value-tile word that holds token slot j
@@ -388,7 +377,7 @@ extern "C" int kvq_topk_retain(const float* scores, int64_t BH, int64_t n, int64
   if (BH == 0 || k == 0) return KVQ_OK;
   KVQ_REQUIRE(scores && idx, "kvq_topk_retain: null pointer");
   if (n <= static_cast<int64_t>(kTopkSlots) * kTopkThreads)
-    hipLaunchKernelGGL(topk_retain_strided_kernel, dim3(static_cast<unsigned>(BH)), dim3(kTopkThreads), 0,
+    hipLaunchKernelGGL(topk_retain_rows_kernel, dim3(static_cast<unsigned>(BH)), dim3(kTopkThreads), 0,
                        static_cast<hipStream_t>(stream), scores, static_cast<int>(n), scores_bh, static_cast<int>(k),
                        idx, idx_bh);
   else
