@@ -49,12 +49,17 @@ namespace {
 
 // Build-time switches of the split kernel (defaults are the tuned values):
 //   KVQ_WAVES       waves per SIMD the register allocation targets (0: per-variant default)
+//   KVQ_SCORE_SPLITS splits of the score pass per split of the decode (its registers allow more
+//                   resident blocks)
 //   KVQ_LOAD_AUX    cache-policy bits of the streaming code/metadata loads (gfx950: 1 = sc0,
 //                   2 = nt, 16 = sc1).  Default nt: every code byte is read once per launch, so
 //                   marking it non-temporal keeps it from displacing reused lines (measured ~4%
 //                   faster on the 16x32x32768 workload than the default policy)
 #ifndef KVQ_WAVES
 #define KVQ_WAVES 0
+#endif
+#ifndef KVQ_SCORE_SPLITS
+#define KVQ_SCORE_SPLITS 2
 #endif
 #ifndef KVQ_LOAD_AUX
 #define KVQ_LOAD_AUX 2
@@ -446,7 +451,13 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     u32x4 kw[2], vw[2];
     u32x4 mw[NB][2];
     uint32_t ks0, ks1, kl0, kl1;
+    uint32_t sc;                                     // score pass: the token's score so far
   };
+  // score pass: token of this lane's score slot (lane n < 8 of lane group g carries slot n) and
+  // a buffer over the (b, h) scores row (reads past n_q are zero)
+  const int sc_tok = 16 * ((n & 7) >> 2) + 4 * g + (n & 3);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(SCORE ? p.scores + static_cast<int64_t>(bh) * p.scores_bh : p.ws_o,
+                                               SCORE ? static_cast<uint32_t>(p.n_q) * 4u : 0u);
   auto load_chunk = [&](int cb, Chunk& c) {
     cb = min(cb, t_last);
     // scalar offsets: uniform by construction (readfirstlane keeps them out of waterfall loops)
@@ -468,6 +479,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
     c.ks1 = __builtin_amdgcn_raw_buffer_load_b16(rks, c1 * 2, sok, 0);
     c.kl0 = __builtin_amdgcn_raw_buffer_load_b16(rkl, c0 * 2, sok, 0);
     c.kl1 = __builtin_amdgcn_raw_buffer_load_b16(rkl, c1 * 2, sok, 0);
+    if constexpr (SCORE) c.sc = __builtin_amdgcn_raw_buffer_load_b32(rsc, (cb + sc_tok) * 4, 0, 0);
   };
 
   f32x4 acc[8];
@@ -558,14 +570,14 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
         if constexpr (R >= 4) x[j] += dpp<kQuadSwap2>(x[j]);
         if constexpr (R >= 8) x[j] += __shfl_xor(x[j], 4, 64);
       }
-      // every lane of group g now holds the row sums of its 8 slots: lane n < 8 adds slot n, so
-      // the 32 tokens of the chunk go out as one coalesced non-returning atomic add (no load to
-      // wait for, so the chunk pipeline keeps its loads in flight)
+      // every lane of group g now holds the row sums of its 8 slots: lane n < 8 adds slot n to
+      // the token's score, read with the chunk's loads (each token belongs to one wavefront of
+      // the launch, so a plain read-add-write is exact); the 32 tokens go out as one store
       float v = x[0];
 #pragma unroll
       for (int j = 1; j < 8; ++j) v = (n == j) ? x[j] : v;
-      const int tok = cb + 16 * (n >> 2) + 4 * g + (n & 3);
-      if (n < 8 && tok < t1) unsafeAtomicAdd(score_row + tok, p.score_weight * v);
+      const int tok = cb + sc_tok;
+      if (n < 8 && tok < t1) score_row[tok] = __uint_as_float(c.sc) + p.score_weight * v;
       return;
     }
     // ---- online softmax (base 2) with a lazy maximum: probabilities are taken against the running
@@ -820,8 +832,13 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
     if (rc != KVQ_OK) return rc;
   }
   if ((phases & 4) && p.scores != nullptr && p.n_split > 0) {
-    hipLaunchKernelGGL((kivi_score_split<R, GV, DT>), dim3(static_cast<unsigned>(p.n_split) * bh_pad),
-                       dim3(kThreads), packed_smem, stream, p);
+    // the score pass writes no partials, so its split count is its own: its registers allow
+    // twice the decode's resident blocks, so twice the splits (at least one chunk per wavefront)
+    DecodeParams ps = p;
+    const int nc = (p.n_q + 31) / 32;
+    ps.n_split = std::max(1, std::min(KVQ_SCORE_SPLITS * p.n_split, (nc + kWaves - 1) / kWaves));
+    hipLaunchKernelGGL((kivi_score_split<R, GV, DT>), dim3(static_cast<unsigned>(ps.n_split) * bh_pad),
+                       dim3(kThreads), packed_smem, stream, ps);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(score)");
   }
   return KVQ_OK;
