@@ -8,7 +8,8 @@
 //   2. if additionally o % group_k == 0, key group o / group_k (tokens o .. o+group_k-1, all in
 //      the ring because W >= group_k) is quantised per channel into key rows and key metadata;
 //   3. the new key/value rows are written into slot pos % W.
-// Reads of step 1-2 happen before the write of step 3 (one block per (b, h), barrier between).
+// Thread c owns channel c of every row it reads and writes, so the write of step 3 needs no
+// barrier after the reads of steps 1-2; every independent load is issued first.
 // Codes and metadata are bit-identical to kivi_quant over the whole sequence (STRATA_KV.py:
 // 826-856): a key group is quantised only when complete, a value row only needs itself.  This is
 // the streaming restatement of KIVIMethod's window rule (a token is read exact until it leaves
@@ -45,14 +46,29 @@ __global__ void kivi_append_kernel(const void* __restrict__ k_new, const void* _
   extern __shared__ float red[];                  // [d] values of the leaving row
   const int bh = blockIdx.x;
   const int b = bh / Hkv, h = bh % Hkv;
-  const int c = threadIdx.x;
+  const int c = threadIdx.x;                      // thread c owns channel c of every row it touches
   const int qmax = 15;
   const int64_t ring_bh = static_cast<int64_t>(bh) * W * d;
-  if (pos >= W) {
-    const int64_t o = pos - W;
-    const int64_t slot_o = o % W;
+  const int64_t slot = pos % W;                   // the new row's slot = the leaving row's slot
+  const bool leaving = pos >= W;
+  const int64_t o = pos - W;                      // token leaving the window (when leaving)
+  // ---- every independent load first: the new rows, the leaving value row, its tile word ----
+  const float kv = load_as_f32<DT>(k_new, static_cast<int64_t>(b) * k_sb + static_cast<int64_t>(h) * k_sh + c);
+  const float vv = load_as_f32<DT>(v_new, static_cast<int64_t>(b) * v_sb + static_cast<int64_t>(h) * v_sh + c);
+  const int64_t chunk = leaving ? o / 32 : 0;
+  const int u = leaving ? static_cast<int>(o % 32) : 0;
+  const int g = (u % 16) / 4, j = 4 * (u / 16) + (u % 4);
+  const int blk = c / 16;
+  uint32_t* word = reinterpret_cast<uint32_t*>(vc + static_cast<int64_t>(bh) * cap_t * (d / 2) + chunk * 16 * d) +
+                   (blk / 4) * 256 + (16 * g + c % 16) * 4 + (blk % 4);
+  float x = 0.0f;
+  uint32_t wold = 0u;
+  if (leaving) {
+    x = load_as_f32<DT>(v_ring, ring_bh + slot * d + c);
+    wold = *word;
+  }
+  if (leaving) {
     // ---- value row of token o, per channel group ----
-    const float x = load_as_f32<DT>(v_ring, ring_bh + slot_o * d + c);
     red[c] = x;
     __syncthreads();
     const int gc = c / group_v;
@@ -64,48 +80,49 @@ __global__ void kivi_append_kernel(const void* __restrict__ k_new, const void* _
     const float lo = as_stored(mn);
     const float sc = fmaxf(as_stored(__fdiv_rn(__fsub_rn(mx, lo), static_cast<float>(qmax))), kMinScale);
     const int code = quant_code(x, lo, sc, qmax);
-    const int64_t chunk = o / 32;
-    const int u = static_cast<int>(o % 32);
-    const int g = (u % 16) / 4, j = 4 * (u / 16) + (u % 4);
-    const int blk = c / 16;
-    uint32_t* word = reinterpret_cast<uint32_t*>(vc + static_cast<int64_t>(bh) * cap_t * (d / 2) + chunk * 16 * d) +
-                     (blk / 4) * 256 + (16 * g + c % 16) * 4 + (blk % 4);
     const int sh = 4 * kNibbleOfSlot[j];
-    *word = (*word & ~(0xfu << sh)) | (static_cast<uint32_t>(code) << sh);
+    *word = (wold & ~(0xfu << sh)) | (static_cast<uint32_t>(code) << sh);
     const int ngv = d / group_v;
     if (c % group_v == 0) {
       uint16_t* vm = vmeta + ((static_cast<int64_t>(bh) * (cap_t / 32) + chunk) * ngv + gc) * 64 + (8 * g + j) * 2;
       vm[0] = f32_to_f16(sc);
       vm[1] = f32_to_f16(lo);
     }
-    // ---- key group starting at token o ----
+    // ---- key group starting at token o (every group_k steps): rows o .. o + group_k - 1 ----
     if (o % group_k == 0) {
+      constexpr int kB = 16;                      // rows loaded together
       float kmn = INFINITY, kmx = -INFINITY;
-      for (int t = 0; t < group_k; ++t) {
-        const float v = load_as_f32<DT>(k_ring, ring_bh + ((o + t) % W) * d + c);
-        kmn = fminf(kmn, v);
-        kmx = fmaxf(kmx, v);
+      for (int t0 = 0; t0 < group_k; t0 += kB) {
+        float kx[kB];
+#pragma unroll
+        for (int t = 0; t < kB; ++t) kx[t] = load_as_f32<DT>(k_ring, ring_bh + ((o + t0 + t) % W) * d + c);
+#pragma unroll
+        for (int t = 0; t < kB; ++t) {
+          kmn = fminf(kmn, kx[t]);
+          kmx = fmaxf(kmx, kx[t]);
+        }
       }
       const float klo = as_stored(kmn);
       const float ksc = fmaxf(as_stored(__fdiv_rn(__fsub_rn(kmx, klo), static_cast<float>(qmax))), kMinScale);
-      const int64_t gi = o / group_k;
-      const int64_t mo = static_cast<int64_t>(bh) * (cap_t / group_k) * d + gi * d + c;
+      const int64_t mo = static_cast<int64_t>(bh) * (cap_t / group_k) * d + (o / group_k) * d + c;
       k_lo[mo] = f32_to_f16(klo);
       k_sc[mo] = f32_to_f16(ksc);
       uint8_t* rows = kc + static_cast<int64_t>(bh) * cap_t * (d / 2);
-      for (int t = 0; t < group_k; ++t) {
-        const float v = load_as_f32<DT>(k_ring, ring_bh + ((o + t) % W) * d + c);
-        const int kcode = quant_code(v, klo, ksc, qmax);
-        const int other = __shfl_down(kcode, 1, 64);
-        if ((c & 1) == 0) rows[(o + t) * (d / 2) + c / 2] = static_cast<uint8_t>((kcode << 4) | other);
+      for (int t0 = 0; t0 < group_k; t0 += kB) {
+        float kx[kB];
+#pragma unroll
+        for (int t = 0; t < kB; ++t) kx[t] = load_as_f32<DT>(k_ring, ring_bh + ((o + t0 + t) % W) * d + c);
+#pragma unroll
+        for (int t = 0; t < kB; ++t) {
+          const int kcode = quant_code(kx[t], klo, ksc, qmax);
+          // channel c + 1's code (lanes 2i, 2i+1 are a quad-swap pair): byte = c[2i] << 4 | c[2i+1]
+          const int other = __builtin_amdgcn_update_dpp(0, kcode, 0xB1, 0xF, 0xF, true);
+          if ((c & 1) == 0) rows[(o + t0 + t) * (d / 2) + c / 2] = static_cast<uint8_t>((kcode << 4) | other);
+        }
       }
     }
-    __syncthreads();                              // every read of the leaving slot is done
   }
-  // ---- the new token into its ring slot ----
-  const int64_t slot = pos % W;
-  const float kv = load_as_f32<DT>(k_new, static_cast<int64_t>(b) * k_sb + static_cast<int64_t>(h) * k_sh + c);
-  const float vv = load_as_f32<DT>(v_new, static_cast<int64_t>(b) * v_sb + static_cast<int64_t>(h) * v_sh + c);
+  // ---- the new token into its ring slot (each thread writes the channel it alone has read) ----
   store_from_f32<DT>(k_ring, ring_bh + slot * d + c, kv);
   store_from_f32<DT>(v_ring, ring_bh + slot * d + c, vv);
 }

@@ -86,9 +86,16 @@ def load() -> C.CDLL:
     return _lib
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> int:
-    """Call an int-status entry point; raise KVQError with the library's message on failure."""
-    rc = getattr(load(), name)(*args)
+    """Call an int-status entry point; raise KVQError with the library's message on failure.
+    (The bound entry points are looked up once: a decode step pays no lock or attribute lookup.)"""
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
+    rc = fn(*args)
     if rc != 0:
         msg = load().kvq_last_error().decode(errors="replace")
         raise KVQError(f"{name} failed ({rc}): {msg}")
@@ -99,7 +106,13 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    """The current stream of t's device as a raw hipStream_t (one call, no Stream object)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

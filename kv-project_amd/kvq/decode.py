@@ -175,9 +175,9 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
         raise TypeError("q and the exact rows must share a dtype")
     if out is None:
         out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
-    need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, cache.group_v,
-                            split_tokens)
-    if workspace is None or workspace.numel() < need:
+    if workspace is None:                      # a caller's workspace is size-checked by the library
+        need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, cache.group_v,
+                                split_tokens)
         workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)
     if phases is None:
         phases = 7 if scores is not None else 3

@@ -131,9 +131,8 @@ def mixed_decode(q: torch.Tensor, scaling: float, cache: MixedKIVICache, *, q_po
         q = q.contiguous()
     if cache.k_exact.dtype != q.dtype:
         raise TypeError("q and the exact rows must share a dtype")
-    need = mixed_workspace_floats(B, Hq, Hkv, Tq, d, cache.nb, cache.n_exact)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)
+    if workspace is None:                      # a caller's workspace is size-checked by the library
+        workspace = torch.zeros((mixed_workspace_floats(B, Hq, Hkv, Tq, d, cache.nb, cache.n_exact),), dtype=torch.float32, device=q.device)
     if out is None:
         out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
     ep = cache.exact_pos if q_pos is not None else None

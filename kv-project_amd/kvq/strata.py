@@ -221,8 +221,8 @@ def strata_decode(q: torch.Tensor, scaling: float, cache: StrataCache, *, q_pos:
         raise TypeError("q and the exact rows must share a dtype")
     tiers = [t for t in cache.tiers if t.n > 0]
     nt = len(tiers)
-    need = strata_workspace_floats(B, Hq, Hkv, Tq, d, cache.n_exact, [t.n for t in tiers], [t.bits for t in tiers])
-    if workspace is None or workspace.numel() < need:
+    if workspace is None:                      # a caller's workspace is size-checked by the library
+        need = strata_workspace_floats(B, Hq, Hkv, Tq, d, cache.n_exact, [t.n for t in tiers], [t.bits for t in tiers])
         workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)
     if out is None:
         out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
