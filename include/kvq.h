@@ -70,6 +70,12 @@ int kvq_kivi_quant(const void* x, int x_dtype, int64_t B, int64_t H, int64_t T, 
  * ---------------------------------------------------------------------------------------- */
 int kvq_pack_codes(const uint8_t* codes, int64_t count, int bits, uint8_t* out, void* stream);
 int kvq_unpack_codes(const uint8_t* packed, int64_t count, int bits, uint8_t* out, void* stream);
+/* A3  Decode of pack_rows bytes (QUASAR_KV.py:1185-1190: per row, first code in the most
+ * significant bits; for rows of whole bytes the same bytes as kvq_pack_codes row by row) through
+ * the byte table of QUASAR_KV.py:1194-1202: out[i * 8/bits + s] = levels[code s of byte i].
+ * levels: 2^bits float32 (device).  bits in {1, 2, 4, 8}. */
+int kvq_unpack_rows_lut(const uint8_t* packed, int64_t n_bytes, int bits, const float* levels, float* out,
+                        void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * A3  KIVI value-code decode layout (no reference counterpart: the reference never reads

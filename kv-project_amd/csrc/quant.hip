@@ -694,6 +694,29 @@ extern "C" int kvq_kivi_quant(const void* x, int x_dtype, int64_t B, int64_t H, 
   return KVQ_OK;
 }
 
+namespace kvq {
+namespace {
+// Decode of pack_rows bytes through a byte table (QUASAR_KV.py:1185-1202): byte i holds 8/bits
+// codes, the first in the most significant bits; each code becomes levels[code].  One thread per
+// byte; the 2^bits levels sit in LDS, so a byte costs one load and 8/bits table reads.
+__global__ __launch_bounds__(256) void unpack_rows_lut_kernel(const uint8_t* __restrict__ packed, int64_t n_bytes,
+                                                              int bits, const float* __restrict__ levels,
+                                                              float* __restrict__ out) {
+  __shared__ float lv[256];
+  const int nl = 1 << bits;
+  for (int i = threadIdx.x; i < nl; i += blockDim.x) lv[i] = levels[i];
+  __syncthreads();
+  const int per = 8 / bits;
+  const uint32_t mask = static_cast<uint32_t>(nl - 1);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_bytes;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const uint32_t byte = packed[i];
+    for (int s = 0; s < per; ++s) out[i * per + s] = lv[(byte >> (bits * (per - 1 - s))) & mask];
+  }
+}
+}  // namespace
+}  // namespace kvq
+
 extern "C" int kvq_pack_codes(const uint8_t* codes, int64_t count, int bits, uint8_t* out, void* stream) {
   KVQ_REQUIRE(bits == 1 || bits == 2 || bits == 4 || bits == 8, "kvq_pack_codes: bits in {1,2,4,8}");
   KVQ_REQUIRE(count >= 0 && (count == 0 || (codes && out)), "kvq_pack_codes: bad arguments");
@@ -712,6 +735,18 @@ extern "C" int kvq_unpack_codes(const uint8_t* packed, int64_t count, int bits, 
   hipLaunchKernelGGL(unpack_codes_kernel, grid1d(count, 256), dim3(256), 0,
                      static_cast<hipStream_t>(stream), packed, count, bits, out);
   KVQ_LAUNCH_CHECK("kvq_unpack_codes");
+  return KVQ_OK;
+}
+
+extern "C" int kvq_unpack_rows_lut(const uint8_t* packed, int64_t n_bytes, int bits, const float* levels,
+                                   float* out, void* stream) {
+  KVQ_REQUIRE(bits == 1 || bits == 2 || bits == 4 || bits == 8, "kvq_unpack_rows_lut: bits in {1,2,4,8}");
+  KVQ_REQUIRE(n_bytes >= 0 && (n_bytes == 0 || (packed && levels && out)), "kvq_unpack_rows_lut: bad arguments");
+  if (n_bytes == 0) return KVQ_OK;
+  const int64_t blocks = std::min<int64_t>((n_bytes + 255) / 256, 65536);
+  hipLaunchKernelGGL(unpack_rows_lut_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), packed, n_bytes, bits, levels, out);
+  KVQ_LAUNCH_CHECK("kvq_unpack_rows_lut");
   return KVQ_OK;
 }
 

@@ -5,7 +5,8 @@ kernels in ``libkvq.so`` through the C ABI of ``include/kvq.h``.  No CPU fallbac
 op requires GPU tensors and raises ``KVQError`` when the library is missing.
 """
 from ._lib import KVQError, load as load_library
-from .kivi import kivi_quant, kivi_quant_stored, pack_codes, unpack_codes, v_tile, v_untile, vmeta_tile
+from .kivi import (kivi_quant, kivi_quant_stored, pack_codes, pack_rows, unpack_codes, unpack_rows, v_tile,
+                   v_untile, vmeta_tile)
 from .decode import PackedKIVICache, kivi_decode, workspace_floats
 from .state import DecodeCtl, KIVIState, Router, register, routed, router_attention
 from .evict import gather_dequant, retained_cache, topk_retain
@@ -15,7 +16,7 @@ from .dct import DctCache, dct_decode, dct_encode, dct_table, dct_workspace_floa
 from .mixed import MixedKIVICache, c3_widths, mixed_decode, mixed_workspace_floats, offset_table
 
 __all__ = [
-    "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes",
+    "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes", "pack_rows", "unpack_rows",
     "v_tile", "v_untile", "vmeta_tile", "PackedKIVICache", "kivi_decode", "workspace_floats",
     "DecodeCtl", "KIVIState", "Router", "register", "routed", "router_attention",
     "gather_dequant", "retained_cache", "topk_retain", "pack_planar", "unpack_planar", "rotation_signs",

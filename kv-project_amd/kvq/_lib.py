@@ -30,6 +30,7 @@ SIGNATURES = {
                              vp, i64, vp, i64, vp, vp, i64, vp, vp]),
     "kvq_pack_codes": (i32, [vp, i64, i32, vp, vp]),
     "kvq_unpack_codes": (i32, [vp, i64, i32, vp, vp]),
+    "kvq_unpack_rows_lut": (i32, [vp, i64, i32, vp, vp, vp]),
     "kvq_v_tile": (i32, [vp, i64, i64, i64, i64, i64, vp, vp]),
     "kvq_v_untile": (i32, [vp, i64, i64, i64, i64, vp, i64, vp]),
     "kvq_vmeta_tile": (i32, [vp, vp, i64, i64, i64, i64, i64, vp, vp]),

@@ -99,6 +99,36 @@ def unpack_codes(packed: torch.Tensor, bits: int, count: int) -> torch.Tensor:
 
 
 @torch.no_grad()
+def pack_rows(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """Drop-in for pack_rows (QUASAR_KV.py:1185-1190): codes (..., w) < 2^bits -> uint8
+    (..., w * bits / 8), first code of each byte in its most significant bits.  For rows of whole
+    bytes these are pack_codes' bytes row by row, computed on the codes' GPU."""
+    if bits not in (1, 2, 4, 8):
+        raise ValueError("bits in {1, 2, 4, 8}")
+    w = codes.shape[-1]
+    if (w * bits) % 8:
+        raise ValueError("a row must fill whole bytes (w * bits % 8 == 0)")
+    return pack_codes(codes, bits).reshape(*codes.shape[:-1], w * bits // 8)
+
+
+@torch.no_grad()
+def unpack_rows(packed: torch.Tensor, bits: int, levels: torch.Tensor) -> torch.Tensor:
+    """Decode of pack_rows bytes through the byte table of QUASAR_KV.py:1194-1202: float32
+    (..., nbytes * 8 / bits) with every code replaced by levels[code] (levels: 2^bits float32)."""
+    _lib.require_gpu(packed, levels)
+    if bits not in (1, 2, 4, 8):
+        raise ValueError("bits in {1, 2, 4, 8}")
+    lv = levels.to(torch.float32).reshape(-1).contiguous()
+    if lv.numel() != 1 << bits:
+        raise ValueError("levels must hold 2^bits entries")
+    p = packed.contiguous()
+    out = torch.empty(p.shape[:-1] + (p.shape[-1] * (8 // bits),), dtype=torch.float32, device=p.device)
+    _lib.call("kvq_unpack_rows_lut", p.data_ptr(), p.numel(), bits, lv.data_ptr(), out.data_ptr(),
+              _lib.stream_of(p))
+    return out
+
+
+@torch.no_grad()
 def v_tile(rows: torch.Tensor, cap_t: int) -> torch.Tensor:
     """4-bit value rows (B, H, n, d/2) (pack_codes order) -> decode tiles (B, H, cap_t/32, 16*d)."""
     _lib.require_gpu(rows)

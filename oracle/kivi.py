@@ -107,6 +107,31 @@ def pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
     return out
 
 
+def pack_rows(codes: np.ndarray, bits: int) -> np.ndarray:
+    """QUASAR_KV.py:1185-1190: codes (..., w) -> uint8 (..., w * bits / 8), the 8/bits codes of a
+    byte placed from its most significant bits down (w * bits must be a multiple of 8)."""
+    c = np.asarray(codes).astype(np.uint32)
+    per = 8 // bits
+    g = c.reshape(*c.shape[:-1], c.shape[-1] // per, per)
+    shifts = (np.arange(per - 1, -1, -1) * bits).astype(np.uint32)
+    return (g << shifts).sum(-1).astype(np.uint8)
+
+
+def byte_lut(levels: np.ndarray, bits: int) -> np.ndarray:
+    """QUASAR_KV.py:1194-1202: the (256, 8/bits) table taking one stored byte to the levels of its
+    codes, first code first."""
+    per = 8 // bits
+    byte = np.arange(256)[:, None]
+    shifts = np.arange(per - 1, -1, -1)[None, :] * bits
+    return np.asarray(levels)[(byte >> shifts) & ((1 << bits) - 1)]
+
+
+def unpack_rows_lut(packed: np.ndarray, bits: int, levels: np.ndarray) -> np.ndarray:
+    """Decode of pack_rows bytes by one gather per byte through byte_lut."""
+    p = np.asarray(packed, dtype=np.uint8)
+    return byte_lut(levels, bits)[p].reshape(*p.shape[:-1], p.shape[-1] * (8 // bits))
+
+
 def unpack_codes(packed: np.ndarray, bits: int, count: int) -> np.ndarray:
     """Inverse of pack_codes: the first ``count`` codes (uint8)."""
     p = np.asarray(packed, dtype=np.uint8)

@@ -93,3 +93,18 @@ def test_vmeta_tile_layout():
                 tok = chunk * 32 + 16 * (j // 4) + 4 * g + (j % 4)
                 want = (sc[0, 1, tok, gc], lo[0, 1, tok, gc]) if tok < n else (0, 0)
                 assert tuple(vm[0, 1, chunk, gc, p]) == tuple(np.float16(w) for w in want)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_pack_rows_and_lut_decode(bits):
+    """kvq.pack_rows bit-exact to the restated pack_rows (QUASAR_KV.py:1185-1190); kvq.unpack_rows
+    (one table lookup per byte, QUASAR_KV.py:1194-1202) returns levels[code] exactly."""
+    import kvq
+    rng = np.random.default_rng(40 + bits)
+    c = rng.integers(0, 2 ** bits, (3, 5, 256)).astype(np.uint8)
+    packed = kvq.pack_rows(torch.from_numpy(c).cuda(), bits)
+    np.testing.assert_array_equal(packed.cpu().numpy(), ok.pack_rows(c, bits))
+    levels = rng.standard_normal(2 ** bits).astype(np.float32)
+    got = kvq.unpack_rows(packed, bits, torch.from_numpy(levels).cuda())
+    np.testing.assert_array_equal(got.cpu().numpy(), levels[c])
+    np.testing.assert_array_equal(got.cpu().numpy(), ok.unpack_rows_lut(ok.pack_rows(c, bits), bits, levels))

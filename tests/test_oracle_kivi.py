@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.kivi import as_stored, kivi_dequant, kivi_quant, pack_codes, unpack_codes
+from oracle.kivi import (as_stored, byte_lut, kivi_dequant, kivi_quant, pack_codes, pack_rows, unpack_codes,
+                         unpack_rows_lut)
 
 
 def test_as_stored_kat():
@@ -120,3 +121,32 @@ def test_pack_codes_kat():
     np.testing.assert_array_equal(pack_codes(np.array([1, 2, 3, 4, 15]), 4), [0x12, 0x34, 0xF0])
     np.testing.assert_array_equal(pack_codes(np.array([3, 2, 1, 0, 1]), 2), [0b11100100, 0b01000000])
     np.testing.assert_array_equal(pack_codes(np.array([200, 7]), 8), [200, 7])
+
+
+def test_pack_rows_kat_and_row_wise_pack_codes():
+    """pack_rows (QUASAR_KV.py:1185-1190): first code of a byte in its top bits; for rows of whole
+    bytes it is pack_codes applied row by row."""
+    np.testing.assert_array_equal(pack_rows(np.array([[1, 2, 3, 4]]), 4), [[0x12, 0x34]])
+    np.testing.assert_array_equal(pack_rows(np.array([[0, 1, 2, 3, 3, 2, 1, 0]]), 2), [[0x1B, 0xE4]])
+    np.testing.assert_array_equal(pack_rows(np.array([[1, 0, 1, 1, 0, 0, 0, 1]]), 1), [[0b10110001]])
+    rng = np.random.default_rng(3)
+    for bits in (1, 2, 4, 8):
+        c = rng.integers(0, 2 ** bits, (5, 3, 64)).astype(np.uint8)
+        got = pack_rows(c, bits)
+        for idx in np.ndindex(5, 3):
+            np.testing.assert_array_equal(got[idx], pack_codes(c[idx], bits))
+
+
+def test_byte_lut_kat_and_decode():
+    """byte_lut (QUASAR_KV.py:1194-1202): byte -> the levels of its codes, first code first; the
+    one-gather decode of pack_rows bytes equals levels[code]."""
+    lv = np.arange(16, dtype=np.float32) * 0.5 - 3.0
+    lut = byte_lut(lv, 4)
+    assert lut.shape == (256, 2)
+    np.testing.assert_array_equal(lut[0xAB], [lv[10], lv[11]])
+    np.testing.assert_array_equal(byte_lut(np.array([7.0, -1.0, 2.5, 9.0]), 2)[0b11100100], [9.0, 2.5, -1.0, 7.0])
+    rng = np.random.default_rng(5)
+    for bits in (1, 2, 4, 8):
+        levels = rng.standard_normal(2 ** bits).astype(np.float32)
+        c = rng.integers(0, 2 ** bits, (4, 128))
+        np.testing.assert_array_equal(unpack_rows_lut(pack_rows(c, bits), bits, levels), levels[c])
