@@ -107,12 +107,14 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_kernel(const float* 
 
 // Rows of at most kTopkSlots * 1024 scores (topk_retain_rows_kernel): thread t holds elements
 // 64 t .. 64 t + 63, read once with 16-byte loads and kept in registers as order keys.
-//   * First pass: one 4096-bin LDS histogram of the top 12 bits of every key (sign, exponent and
-//     3 mantissa bits: 8 bins per octave of magnitude, so scores of one magnitude spread over
-//     several bins instead of colliding in one); a suffix scan over the bins (one block scan)
-//     finds the bin of the k-th largest key.
-//   * The remaining 20 bits by 8-, 8- and 4-bit passes over the keys still matching the prefix
-//     (per-wavefront 256-bin histograms).
+//   * The keys are taken relative to the row's smallest key (v = key - min; the order is kept) and
+//     the first pass bins the top 12 of the bits the row's key range spans: one 4096-bin LDS
+//     histogram of v >> s1 with s1 = max(0, bits(max - min) - 12).  The bins cover the scores
+//     the row actually holds, so a row whose scores share their sign and most of their exponent
+//     (softmax probabilities do) still spreads over the bins instead of colliding in a few hot
+//     ones; a suffix scan over the bins (one block scan) finds the bin of the k-th largest key.
+//   * The remaining s1 bits by 8-bit passes (the last one narrower) over the keys still matching
+//     the prefix (per-wavefront 256-bin histograms).
 //   * Output in position order: per-thread bit masks of the kept slots; one block scan of the
 //     tie counts (ties beyond the kept ones dropped, lowest positions first) and one of the kept
 //     counts gives every thread its output offset.
@@ -155,12 +157,38 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_rows_kernel(const fl
       }
     }
   }
-  for (int bn = tid; bn < kTopkBins1; bn += kTopkThreads) hist1[bn] = 0u;
-  __syncthreads();
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
 #pragma unroll
   for (int e = 0; e < kTopkSlots; ++e) {
     u[e] = order_key(__uint_as_float(u[e]));
-    if (e < nv) atomicAdd(&hist1[u[e] >> 20], 1u);
+    if (e < nv) {
+      kmin = min(kmin, u[e]);
+      kmax = max(kmax, u[e]);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmin), o, 64)));
+    kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), o, 64)));
+  }
+  if (lane == 0) {
+    wave_sums[wave] = kmin;
+    wave_sums[16 + wave] = kmax;
+  }
+  for (int bn = tid; bn < kTopkBins1; bn += kTopkThreads) hist1[bn] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    kmin = min(kmin, wave_sums[w]);
+    kmax = max(kmax, wave_sums[16 + w]);
+  }
+  // every valid key lies in [kmin, kmax] (kmin <= kmax: a row holds at least one score)
+  const int span = 32 - __builtin_clz(kmax - kmin | 1u);           // bits of max - min (>= 1)
+  const int s1 = max(0, span - 12);
+#pragma unroll
+  for (int e = 0; e < kTopkSlots; ++e) {
+    u[e] -= kmin;                                                  // wraps for e >= nv: never read
+    if (e < nv) atomicAdd(&hist1[u[e] >> s1], 1u);
   }
   __syncthreads();
   // thread t owns bins 4095 - 4t - i (i = 0..3, descending); keys in higher bins come first
@@ -176,15 +204,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_rows_kernel(const fl
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (c4[i] > 0u && run < kk && run + c4[i] >= kk) {
-      sh_prefix = static_cast<uint32_t>(kTopkBins1 - 1 - 4 * tid - i) << 20;
+      sh_prefix = static_cast<uint32_t>(kTopkBins1 - 1 - 4 * tid - i) << s1;
       sh_krem = kk - run;
     }
     run += c4[i];
   }
   __syncthreads();
   uint32_t prefix = sh_prefix, krem = sh_krem;
-  uint32_t mask = 0xFFF00000u;
-  int top = 19;
+  uint32_t mask = 0xFFFFFFFFu << s1;
+  int top = s1 - 1;
   while (top >= 0) {
     const int width = min(8, top + 1);
     const int shift = top - width + 1;
@@ -224,8 +252,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_retain_rows_kernel(const fl
     mask |= dmask << shift;
     top = shift - 1;
   }
-  // prefix = key of the k-th largest score; krem = how many keys equal to it are kept (those at
-  // the lowest positions)
+  // prefix = key of the k-th largest score (relative to kmin); krem = how many keys equal to it
+  // are kept (those at the lowest positions)
   uint64_t gt = 0, eq = 0;
 #pragma unroll
   for (int e = 0; e < kTopkSlots; ++e) {

@@ -29,6 +29,9 @@ def test_topk_retain_bit_exact(n, k):
         rng.integers(0, 5, n).astype(np.float32) * 0.25,                    # heavy ties
         np.full(n, 3.0, np.float32),                                        # all equal
         (rng.standard_normal(n) * 10).astype(np.float32),                   # signed
+        (1.0 + rng.integers(0, 3000, n) * 2.0 ** -23).astype(np.float32),   # keys span < 12 bits
+        (1.0 + rng.integers(0, 1 << 13, n) * 2.0 ** -23).astype(np.float32),  # span 13 bits
+        rng.choice(np.array([-np.inf, np.inf, -3.4e38, 3.4e38, 0.0, 1e-45, -1e-45, 1.0], np.float32), n),
     ])
     got = kvq.topk_retain(torch.from_numpy(rows).cuda(), k).cpu().numpy()
     want = topk_retain(rows, k)
