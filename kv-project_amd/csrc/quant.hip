@@ -10,6 +10,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "mfma_common.hpp"
 
 // Build-time switch: blocks of the vectorised quantisers (grid-stride loops over their items);
 // 0 = one block per item.
@@ -476,6 +477,194 @@ __global__ __launch_bounds__(256) void kivi_quant_values_v(const void* __restric
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Packed-only 4-bit variants (16-bit input, d == 128, no unpacked codes or xhat: the prefill
+// path of the decode cache).  One wavefront per item, no barriers: lane (s = lane % 16, rq =
+// lane / 16) owns the 8-channel slab s of rows rq + 4 j.  Every row of the item is loaded at
+// once through a buffer resource that ends at the item's last valid row (rows past it read
+// zero and are masked), so the load path has no branches.  The arithmetic is that of
+// quant_code_r; the check for quotients near a half-integer is taken once per row and the IEEE
+// division redone only where a lane needs it.  Results are bit-identical to the kernels above.
+
+template <int DT>
+__device__ __forceinline__ void cvt_slab(const u32x4 w, float (&v)[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint16_t a = static_cast<uint16_t>(w[k] & 0xffffu), c = static_cast<uint16_t>(w[k] >> 16);
+    v[2 * k] = DT == KVQ_F16 ? f16_to_f32(a) : bf16_to_f32(a);
+    v[2 * k + 1] = DT == KVQ_F16 ? f16_to_f32(c) : bf16_to_f32(c);
+  }
+}
+
+// 4-bit codes of 8 values: t = rint(RN(RN(x - lo) * r)) with r = v_rcp_f32(sc), and where some
+// lane's product is within 1e-4 of a half-integer, rint(RN(RN(x - lo) / sc)).  Exact: r is within
+// 1 ulp of 1 / sc (the instruction's documented accuracy; sc is a normal fp16 value >= 2^-24), so
+// |RN(d r) - RN(d / sc)| <= (2^-23 + 2^-24 + 2^-24) |d / sc| = 2^-22 |d / sc|, under 1e-4 while
+// |d / sc| <= 400, so a product more than 1e-4 from a half-integer rounds to the same integer as
+// the IEEE quotient; larger quotients (inputs beyond the fp16 range that lo and sc clamp to) give
+// the same clamped code 0 or 15 either way.
+__device__ __forceinline__ uint32_t code_word4(const float (&v)[8], const float (&lo)[8], const float (&sc)[8],
+                                               const float (&rc)[8]) {
+  float t[8];
+  bool near = false;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float p = __fmul_rn(__fsub_rn(v[k], lo[k]), rc[k]);
+    t[k] = rintf(p);
+    near |= fabsf(p - t[k]) > 0.4999f;
+  }
+  if (__builtin_expect(__any(near), 0)) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float dd = __fsub_rn(v[k], lo[k]);
+      if (fabsf(__fmul_rn(dd, rc[k]) - t[k]) > 0.4999f) t[k] = rintf(__fdiv_rn(dd, sc[k]));
+    }
+  }
+  uint32_t w = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t c = static_cast<uint32_t>(fminf(fmaxf(t[k], 0.0f), 15.0f));
+    w |= c << ((k & 1) ? 8 * (k / 2) : 8 * (k / 2) + 4);       // MSB-first: even channel high nibble
+  }
+  return w;
+}
+
+// Keys: item = (group gi, b*h), group <= 4 RPL rows; per-channel min / max over the rows of the
+// lane, then over the four row lanes (permlane swaps).
+template <int DT, int RPL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void kivi_quant_keys_p4(
+    const void* __restrict__ x, int H, int64_t sb, int64_t sh, int64_t st, int n_sink, int n, int group,
+    uint8_t* __restrict__ packed, int64_t packed_bh, uint16_t* __restrict__ lo_out, uint16_t* __restrict__ sc_out,
+    int64_t meta_bh, int n_g, int64_t n_items) {
+  constexpr int D = 128;
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= n_items) return;
+  const int s = lane & 15, rq = lane >> 4;
+  const int gi = static_cast<int>(item % n_g), bh = static_cast<int>(item / n_g);
+  const int b = bh / H, h = bh % H;
+  const int t0 = gi * group;
+  const int rv = min(group, n - t0);                          // valid rows of the item (>= 1)
+  const uint16_t* src = static_cast<const uint16_t*>(x) + static_cast<int64_t>(b) * sb + static_cast<int64_t>(h) * sh +
+                        static_cast<int64_t>(n_sink + t0) * st;
+  const uint32_t rstride = static_cast<uint32_t>(st * 2);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, static_cast<uint32_t>(rv) * rstride);
+  u32x4 raw[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) raw[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (rq + 4 * j) * rstride + s * 16, 0, 0);
+  float mn[8], mx[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    mn[k] = INFINITY;
+    mx[k] = -INFINITY;
+  }
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    const bool ok = rq + 4 * j < rv;
+    float v[8];
+    cvt_slab<DT>(raw[j], v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      mn[k] = fminf(mn[k], ok ? v[k] : INFINITY);
+      mx[k] = fmaxf(mx[k], ok ? v[k] : -INFINITY);
+    }
+  }
+  // the rows are converted again when coded: only the raw words stay live across the reduction
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) asm volatile("" : "+v"(raw[j]));
+  float lo[8], sc[8], rc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float a = xmin32(xmin16(mn[k])), z = xmax32(xmax16(mx[k]));
+    const float l = as_stored(a);
+    const float q = fmaxf(as_stored(__fdiv_rn(__fsub_rn(z, l), 15.0f)), kMinScale);
+    lo[k] = l;
+    sc[k] = q;
+    rc[k] = __builtin_amdgcn_rcpf(q);
+  }
+  if (rq == 0) {
+    const int64_t mo = static_cast<int64_t>(bh) * meta_bh + static_cast<int64_t>(gi) * D + s * 8;
+    u32x4 wl, ws;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      wl[k] = f32_to_f16(lo[2 * k]) | (static_cast<uint32_t>(f32_to_f16(lo[2 * k + 1])) << 16);
+      ws[k] = f32_to_f16(sc[2 * k]) | (static_cast<uint32_t>(f32_to_f16(sc[2 * k + 1])) << 16);
+    }
+    *reinterpret_cast<u32x4*>(lo_out + mo) = wl;
+    *reinterpret_cast<u32x4*>(sc_out + mo) = ws;
+  }
+  uint32_t* dst = reinterpret_cast<uint32_t*>(packed + static_cast<int64_t>(bh) * packed_bh + static_cast<int64_t>(t0) * (D / 2)) + s;
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    float v[8];
+    cvt_slab<DT>(raw[j], v);
+    const uint32_t w = code_word4(v, lo, sc, rc);
+    if (rq + 4 * j < rv) dst[(rq + 4 * j) * (D / 8)] = w;
+  }
+}
+
+// min / max over runs of L lanes (L = 1, 2, 4, 8, 16) inside a row of 16, every lane of a run
+// receiving the result (quad swaps, then the half-row and row mirrors)
+template <int L>
+__device__ __forceinline__ void run_minmax(float& mn, float& mx) {
+  if constexpr (L >= 2) { mn = fminf(mn, dpp<kQuadSwap1>(mn)); mx = fmaxf(mx, dpp<kQuadSwap1>(mx)); }
+  if constexpr (L >= 4) { mn = fminf(mn, dpp<kQuadSwap2>(mn)); mx = fmaxf(mx, dpp<kQuadSwap2>(mx)); }
+  if constexpr (L >= 8) { mn = fminf(mn, dpp<0x141>(mn)); mx = fmaxf(mx, dpp<0x141>(mx)); }    // row_half_mirror
+  if constexpr (L >= 16) { mn = fminf(mn, dpp<0x140>(mn)); mx = fmaxf(mx, dpp<0x140>(mx)); }   // row_mirror
+}
+
+// Values: item = 64 consecutive rows of one b*h; a channel group of 8 L channels is L lanes.
+template <int DT, int L>
+__global__ __launch_bounds__(256) void kivi_quant_values_p4(
+    const void* __restrict__ x, int H, int64_t sb, int64_t sh, int64_t st, int n_sink, int n,
+    uint8_t* __restrict__ packed, int64_t packed_bh, uint16_t* __restrict__ lo_out, uint16_t* __restrict__ sc_out,
+    int64_t meta_bh, int n_rb, int64_t n_items) {
+  constexpr int D = 128, RPL = 16, NG = D / (8 * L);
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= n_items) return;
+  const int s = lane & 15, rq = lane >> 4;
+  const int rb = static_cast<int>(item % n_rb), bh = static_cast<int>(item / n_rb);
+  const int b = bh / H, h = bh % H;
+  const int t0 = rb * 4 * RPL;
+  const int rv = min(4 * RPL, n - t0);
+  const uint16_t* src = static_cast<const uint16_t*>(x) + static_cast<int64_t>(b) * sb + static_cast<int64_t>(h) * sh +
+                        static_cast<int64_t>(n_sink + t0) * st;
+  const uint32_t rstride = static_cast<uint32_t>(st * 2);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, static_cast<uint32_t>(rv) * rstride);
+  u32x4 raw[RPL];
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) raw[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (rq + 4 * j) * rstride + s * 16, 0, 0);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(packed + static_cast<int64_t>(bh) * packed_bh + static_cast<int64_t>(t0) * (D / 2)) + s;
+  const int64_t mrow = static_cast<int64_t>(bh) * meta_bh + static_cast<int64_t>(t0) * NG + s / L;
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    const int r = rq + 4 * j;
+    float v[8];
+    cvt_slab<DT>(raw[j], v);
+    float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      mn = fminf(mn, v[k]);
+      mx = fmaxf(mx, v[k]);
+    }
+    run_minmax<L>(mn, mx);
+    const float l1 = as_stored(mn);
+    const float s1 = fmaxf(as_stored(__fdiv_rn(__fsub_rn(mx, l1), 15.0f)), kMinScale);
+    const float r1 = __builtin_amdgcn_rcpf(s1);
+    const float lo[8] = {l1, l1, l1, l1, l1, l1, l1, l1}, sc[8] = {s1, s1, s1, s1, s1, s1, s1, s1};
+    const float rc[8] = {r1, r1, r1, r1, r1, r1, r1, r1};
+    const uint32_t w = code_word4(v, lo, sc, rc);
+    if (r < rv) {
+      dst[r * (D / 8)] = w;
+      if (s % L == 0) {
+        lo_out[mrow + static_cast<int64_t>(r) * NG] = f32_to_f16(l1);
+        sc_out[mrow + static_cast<int64_t>(r) * NG] = f32_to_f16(s1);
+      }
+    }
+  }
+}
+
 template <int DT>
 __global__ void copy_sinks(const void* __restrict__ x, int H, int64_t sb, int64_t sh, int64_t st,
                            int n_sink, int d, int T, float* __restrict__ xhat) {
@@ -637,6 +826,48 @@ extern "C" int kvq_kivi_quant(const void* x, int x_dtype, int64_t B, int64_t H, 
   const bool vec = d == 128 && al(x, 16) && sb % 8 == 0 && sh % 8 == 0 && st % 8 == 0 && al(packed, 16) &&
                    packed_bh % 8 == 0 && al(codes, 16) && codes_bh % 8 == 0 && al(xhat, 16) && al(lo, 16) &&
                    al(scale, 16) && meta_bh % 8 == 0;
+  // packed-only 4-bit output of 16-bit input: one wavefront per item (the decode cache's prefill)
+  const bool p4 = vec && bits == 4 && packed != nullptr && codes == nullptr && xhat == nullptr &&
+                  x_dtype != KVQ_F32 && st < (1LL << 25);
+  if (p4 && along_tokens && group <= 64) {
+    const int n_g = (n + group - 1) / group;
+    const int64_t n_items = static_cast<int64_t>(n_g) * B * H;
+    KVQ_REQUIRE(n_items < (1LL << 33), "kvq_kivi_quant: too many key groups");
+    const dim3 grid(static_cast<unsigned>((n_items + 3) / 4));
+#define KVQ_KEYS_P4(RPL_)                                                                                      \
+    KVQ_DISPATCH_DTYPE(x_dtype, if constexpr (DT_ != KVQ_F32) hipLaunchKernelGGL((kivi_quant_keys_p4<DT_, RPL_>), grid, \
+                       dim3(256), 0, s, x, (int)H, sb, sh, st, n_sink, n, group, packed, packed_bh, lo, scale,      \
+                       meta_bh, n_g, n_items))
+    if (group <= 16) { KVQ_KEYS_P4(4); }
+    else if (group <= 32) { KVQ_KEYS_P4(8); }
+    else { KVQ_KEYS_P4(16); }
+#undef KVQ_KEYS_P4
+    KVQ_LAUNCH_CHECK("kvq_kivi_quant(keys)");
+    return KVQ_OK;
+  }
+  if (p4 && !along_tokens) {
+    const int64_t width = (d % group == 0) ? group : d;
+    if (width % 8 == 0 && ((width / 8) & (width / 8 - 1)) == 0) {
+      const int n_rb = (n + 63) / 64;
+      const int64_t n_items = static_cast<int64_t>(n_rb) * B * H;
+      KVQ_REQUIRE(n_items < (1LL << 33), "kvq_kivi_quant: too many value rows");
+      const dim3 grid(static_cast<unsigned>((n_items + 3) / 4));
+#define KVQ_VALUES_P4(L_)                                                                                      \
+      KVQ_DISPATCH_DTYPE(x_dtype, if constexpr (DT_ != KVQ_F32) hipLaunchKernelGGL((kivi_quant_values_p4<DT_, L_>), grid, \
+                         dim3(256), 0, s, x, (int)H, sb, sh, st, n_sink, n, packed, packed_bh, lo, scale, meta_bh,  \
+                         n_rb, n_items))
+      switch (width / 8) {
+        case 1: KVQ_VALUES_P4(1); break;
+        case 2: KVQ_VALUES_P4(2); break;
+        case 4: KVQ_VALUES_P4(4); break;
+        case 8: KVQ_VALUES_P4(8); break;
+        default: KVQ_VALUES_P4(16); break;
+      }
+#undef KVQ_VALUES_P4
+      KVQ_LAUNCH_CHECK("kvq_kivi_quant(values)");
+      return KVQ_OK;
+    }
+  }
   if (along_tokens && vec && group <= 128) {
     const int n_g = (n + group - 1) / group;
     const int rpt = (group + 15) / 16;

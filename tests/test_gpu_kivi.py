@@ -24,8 +24,9 @@ def _data(shape, seed, dtype, heavy=False):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("along,group,n_sink,T", [(True, 32, 0, 4096), (True, 64, 4, 203),
-                                                  (False, 32, 0, 300), (False, 64, 3, 129),
-                                                  (False, 48, 0, 17)])
+                                                  (True, 16, 0, 100), (False, 32, 0, 300),
+                                                  (False, 64, 3, 129), (False, 48, 0, 17),
+                                                  (False, 8, 0, 70), (False, 16, 5, 200)])
 def test_kivi_quant_bit_exact(dtype, bits, along, group, n_sink, T):
     import kvq
     x = _data((2, 3, T, 128), 1000 + T + bits, dtype, heavy=along)
@@ -36,10 +37,34 @@ def test_kivi_quant_bit_exact(dtype, bits, along, group, n_sink, T):
     np.testing.assert_array_equal(got["scale"].cpu().numpy(), ref["scale"])
     np.testing.assert_array_equal(got["xhat"].cpu().numpy(), ref["xhat"])
     st = kvq.kivi_quant_stored(x.cuda(), bits, group, along, n_sink)
-    for b_ in range(2):
-        for h in range(3):
+    _check_stored(st, ref, bits, along)
+
+
+def _check_stored(st, ref, bits, along):
+    """The packed-only output (the decode cache's prefill path) against the oracle."""
+    ax = 3 if along else 4
+    np.testing.assert_array_equal(st["lo"].float().unsqueeze(ax).cpu().numpy(), ref["lo"])
+    np.testing.assert_array_equal(st["scale"].float().unsqueeze(ax).cpu().numpy(), ref["scale"])
+    B, H = ref["codes"].shape[:2]
+    for b_ in range(B):
+        for h in range(H):
             want = ok.pack_codes(ref["codes"][b_, h], bits)
             np.testing.assert_array_equal(st["packed"][b_, h].cpu().numpy().ravel(), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("along,group", [(True, 64), (True, 32), (False, 64), (False, 128)])
+def test_kivi_quant_stored_strided_input(dtype, along, group):
+    """A view of the first n rows of a longer cache (row stride kept, as the prefill quantises
+    K[:, :, :n]), with a ragged last group and rows whose quotients sit on half-integers."""
+    import kvq
+    full = _data((2, 4, 700, 128), 77 + group, dtype, heavy=along)
+    full[:, :, 10:20] = (torch.arange(128) % 16).to(dtype) * 0.5          # exact code grid
+    ref = ok.kivi_quant(full[:, :, :613].float().numpy(), 4, group, along, 0)
+    x = full.cuda()[:, :, :613]
+    assert x.stride(2) == 128 and x.stride(1) == 700 * 128
+    st = kvq.kivi_quant_stored(x, 4, group, along, 0)
+    _check_stored(st, ref, 4, along)
 
 
 @pytest.mark.parametrize("bits", [1, 2, 4, 8])
