@@ -14,6 +14,7 @@ The other rows of the path are measured by the same script with ``--workload``:
   strata  STRATA strata (per-token 8/4/2-bit tiers) at the C3 shape
   append  streaming append of one token per sequence at the C2 shape (µs/step)
   quant   prefill quantise + pack of the C2 context (kivi_quant of K and V)
+  quasar  QUASAR compressed-domain decode (embedded spectral code, 64k context, batch 1)
 Each prints one JSON line of the same form (its own metric, roofline and CPU baseline).
 
 Timing: W untimed warm-up steps, then K steps launched back to back between HIP events on the
@@ -431,6 +432,71 @@ def run_c5(args) -> dict:
 
 
 # ---------------------------------------------------------------------------------------------
+# F2: QUASAR compressed-domain decode
+
+QUASAR_CTX, QUASAR_NC, QUASAR_N0 = 65536, 45056, 656
+
+
+def run_quasar(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    from kvq.quasar import synthetic_packed
+    Hq, Hkv, d, stages = 32, 8, 128, (2, 2, 4)
+    log("generating the QUASAR stored code (codebooks, embedded quantisation)")
+    packed = synthetic_packed(Hkv, d, QUASAR_NC, stages=stages, seed=42)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(42)
+    K = torch.randn((1, Hkv, QUASAR_N0, d), generator=g, device="cuda").to(torch.bfloat16)
+    V = torch.randn((1, Hkv, QUASAR_N0, d), generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randn((1, Hq, 1, d), generator=g, device="cuda").to(torch.bfloat16)
+    H = QUASAR_CTX
+    st = kvq.QuasarState(K, V, packed, stages, 0, H)
+    scaling = d ** -0.5
+    qpos = torch.tensor([H], device="cuda")
+    out = torch.empty((1, 1, Hq, d), dtype=torch.bfloat16, device="cuda")
+    step = lambda: st.attend(q, scaling, qpos, out=out)
+    split = lambda: st.attend(q, scaling, qpos, out=out, phases=2)
+    ms, g_ms = step_ms(step, args.steps, args.warmup)
+    step_gpu_ms = graph_k_ms(step, args.steps, args.warmup)
+    split_ms = graph_k_ms(split, args.steps, args.warmup)
+    codes = sum(s_["flat"].numel() for s_ in st.sides)
+    rho = 2 * 2 * Hkv * QUASAR_NC
+    exact = 2 * K.numel() * K.element_size()
+    mats = 4 * (st.T_k.numel() + st.T_v.numel() + st.mu_k.numel() + st.mu_v.numel())
+    io = q.numel() * q.element_size() + out.numel() * out.element_size()
+    bytes_split = codes + rho + exact
+    bytes_alg = bytes_split + mats + io
+    res = _result(args, metric="QUASAR compressed-domain decode: µs/layer (64k context, embedded 2+2+4-bit code)",
+                  value=step_gpu_ms * 1e3, unit="us", ms_per_step=step_gpu_ms, hib=False,
+                  workload=f"F2: one decode step of QuasarState.attend over a {QUASAR_CTX}-token context kept as "
+                           f"{QUASAR_NC} coded tokens (12 levels: bands 16/16/32/64 x stages 2/2/4 bits, the level-l "
+                           f"prefix holding 1.0 .. 0.1 of them) + {QUASAR_N0} exact rows; B=1, Hq=32, Hkv=8, d=128, "
+                           "bf16 exact rows, synthetic N(0, 1) coefficients",
+                  config={"global_batch": 1, "seq_len": QUASAR_CTX, "parallelism": "single GPU", "coded": QUASAR_NC,
+                          "exact": QUASAR_N0, "stages": list(stages)},
+                  dtype="bf16", roofline=_roof(bytes_split, split_ms, "quasar_split"),
+                  eager_us=round(ms * 1e3, 3), graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg,
+                  code_bytes=codes, context_bytes=st.context_bytes(),
+                  reference_published_us_64k="4100-39000 (A100-class MIG slice, STRATA_KV.py:30-32)")
+    log(f"QUASAR step {step_gpu_ms * 1e3:.1f} us GPU ({ms * 1e3:.1f} eager), split {split_ms * 1e3:.1f} us")
+    if not args.no_cpu_baseline:
+        import oracle.quasar as oq
+        qn = q.float().cpu().numpy()
+        Kn, Vn = K.float().cpu().numpy(), V.float().cpu().numpy()
+        times = []
+        while sum(times) < args.cpu_seconds or len(times) < 2:
+            t0 = time.perf_counter()
+            oq.attend(qn, scaling, np.array([H]), Kn, Vn, QUASAR_N0, H, packed, stages)
+            times.append(time.perf_counter() - t0)
+        t = float(np.median(times))
+        res["cpu_baseline"] = {"value": t * 1e6, "unit": "us", "cores": _threads(), "kind": "port",
+                               "sample": f"the whole step, {len(times)} runs, median; numpy float64 restatement of "
+                                         "QuasarState.attend (byte-table gather + matmul per step)"}
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
 # C4: eviction
 
 def run_c4(args) -> dict:
@@ -637,7 +703,7 @@ def run_quant(args) -> dict:
 
 
 WORKLOADS = {"c2": lambda a: run_kivi(a, "c2"), "c1": lambda a: run_kivi(a, "c1"), "c3": run_c3, "c4": run_c4,
-             "c5": run_c5, "strata": run_strata, "append": run_append, "quant": run_quant}
+             "c5": run_c5, "strata": run_strata, "append": run_append, "quant": run_quant, "quasar": run_quasar}
 
 
 def main() -> int:

@@ -311,6 +311,45 @@ int kvq_kivi_append(const void* k_new, const void* v_new, int dtype, int64_t k_s
                     int group_v, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * F2  QUASAR compressed-domain decode: replaces QuasarState.attend (QUASAR_KV.py:1945-1968) with
+ * its coded part read from the packed bytes (the reference's _quasar_scores_kernel /
+ * _quasar_values_kernel, 1498-1551, and their torch path, 1920-1943), batch 1.
+ *   q (1, Hq, Tq, d = 128) of q_dtype, strides q_sh, q_st; exact rows k_exact / v_exact (1, Hkv,
+ *   cap_e, d) of q_dtype, the first n_exact attended, row i visible to query t iff exact_pos[i] <=
+ *   q_pos[t] when both are given (the causal rule of appended rows, 1950-1953).
+ *   Per side (k_ / v_): codes (`bytes` long) = the steps' (Hkv, n_s, nb) pack_rows blocks, in step
+ *   order, described by the side's step table, int32 rows [byte offset, n_s, nb, a, w, bits, level
+ *   offset] (1883-1898; n_s non-increasing, nb in {4, 8, 16, 32, 64}, at most 128 bytes per token
+ *   and side).  levels = the stage codebooks concatenated (float32, at most 256).  rho_k / rho_v
+ *   (Hkv, n_c) fp16; T_k / T_v (Hkv, d, R) float32 (R a multiple of 4); mu_k / mu_v (Hkv, d)
+ *   float32.  bounds (`splits` + 1 int32 chunk boundaries, 64-token chunks), slots (int32 [2][32][8])
+ *   and the slot counts come from kvq_quasar_plan (device copies).  out (1, Tq, Hq, d) of
+ *   q_dtype.  rep x Tq <= 8.  phases: mask of 1 (the
+ *   query's coefficients), 2 (the split launch), 4 (the merge); 7 for a decode step (the others
+ *   are timing hooks that reuse the workspace of an earlier call).
+ * kvq_quasar_plan: host-memory step tables in (checked); out, in host memory: cost-balanced chunk
+ * boundaries (bounds needs max_splits + 1 entries; *n_splits receives the split count) and the
+ * slot table (2 x 32 x 8 int32: per 4-byte slot of a token's rows, the step offset + 4 dw, n_s, nb,
+ * first coefficient, bits, level offset, step) with n_slots[2].  No reference counterpart (the
+ * reference launches one program per 64-token block).
+ * ---------------------------------------------------------------------------------------- */
+int kvq_quasar_plan(const int32_t* k_table, int k_steps, const int32_t* v_table, int v_steps, int64_t n_c,
+                    int64_t Hkv, int max_splits, int32_t* bounds, int32_t* n_splits, int32_t* slots,
+                    int32_t* n_slots);
+int64_t kvq_quasar_decode_workspace(int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t R_k,
+                                    int64_t n_exact, int splits);
+int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64_t q_st, int64_t Hq, int64_t Hkv,
+                      int64_t Tq, int64_t d, float scaling, const void* k_exact, const void* v_exact,
+                      int64_t cap_e, int64_t n_exact, const int64_t* exact_pos, const int64_t* q_pos,
+                      const uint8_t* k_codes, int64_t k_bytes, const uint8_t* v_codes, int64_t v_bytes,
+                      const int32_t* slots, int nslots_k,
+                      int nslots_v, const float* levels, int n_levels,
+                      const uint16_t* rho_k, const uint16_t* rho_v, int64_t n_c, const float* T_k,
+                      const float* T_v, int64_t R_k, int64_t R_v, const float* mu_k, const float* mu_v,
+                      const int32_t* bounds, int splits, void* out, float* workspace,
+                      int64_t workspace_floats, int phases, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Self-test of the matrix-core operand layout the decode kernel is written against
  * (v_mfma_f32_16x16x32_f16 on gfx950): writes, for A = I-pattern inputs, the 16x16 product
  * as each lane sees it, followed by the lane each lane reads under row_shr:4 and row_ror:4 and

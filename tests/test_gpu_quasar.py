@@ -1,0 +1,72 @@
+"""GPU QUASAR compressed-domain decode (kvq.QuasarState.attend) against the oracle
+(oracle/quasar.py: QuasarState.attend, QUASAR_KV.py:1945-1968, in float64).
+
+Tolerances (relative to the output's max magnitude): float32 2e-3, bfloat16 1e-2.  Cases: GQA 4
+with one and two query rows, codes at (2, 2, 4), (4, 4) and (8,) bits, coded-token counts around
+the 64-token chunk (1, 63, 64, 65) and long ones, exact rows across several 128-row blocks, appended
+causal rows, no coded tokens, and the state's own kernel check.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.quasar as oq
+
+pytestmark = pytest.mark.gpu
+
+
+def _state(Hkv, n_c, n0, extra, stages, dtype, seed):
+    import kvq
+    from kvq.quasar import synthetic_packed
+    g = torch.Generator().manual_seed(seed)
+    p = synthetic_packed(Hkv, 128, n_c, stages=stages, seed=seed) if n_c > 0 else {"steps": [], "n_c": 0}
+    K = torch.randn((1, Hkv, n0, 128), generator=g).to(dtype)
+    V = torch.randn((1, Hkv, n0, 128), generator=g).to(dtype)
+    H = 5000
+    st = kvq.QuasarState(K.cuda(), V.cuda(), p, stages, extra, H)
+    return st, p, K, V, H, g
+
+
+def _check(st, p, K_all, V_all, n0, H, q, qpos, stages, tol):
+    got = st.attend(q.cuda(), 128 ** -0.5, qpos).float().cpu().numpy()
+    want = oq.attend(q.float().numpy(), 128 ** -0.5, np.asarray(qpos), K_all.float().numpy(), V_all.float().numpy(),
+                     n0, H, p, stages)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err < tol, err
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-3), (torch.bfloat16, 1e-2)])
+@pytest.mark.parametrize("n_c,n0", [(1, 40), (63, 40), (64, 300), (65, 129), (1000, 36), (5000, 700)])
+def test_quasar_decode_matches_oracle(dtype, tol, n_c, n0):
+    st, p, K, V, H, g = _state(2, n_c, n0, 0, (2, 2, 4), dtype, 100 + n_c)
+    q = torch.randn((1, 8, 1, 128), generator=g).to(dtype)
+    _check(st, p, K, V, n0, H, q, [H], (2, 2, 4), tol)
+
+
+@pytest.mark.parametrize("stages", [(4, 4), (8,), (2, 2, 4)])
+def test_quasar_decode_stages_two_rows_and_appends(stages):
+    dtype = torch.bfloat16
+    st, p, K, V, H, g = _state(4, 777, 200, 4, stages, dtype, 7)
+    k = torch.randn((1, 4, 3, 128), generator=g).to(dtype)
+    v = torch.randn((1, 4, 3, 128), generator=g).to(dtype)
+    st.append(k.cuda(), v.cuda(), torch.tensor([H, H + 1, H + 2]))
+    q = torch.randn((1, 16, 2, 128), generator=g).to(dtype)
+    qpos = [H + 1, H + 2]                                   # row H+2 visible to the second query only
+    _check(st, p, torch.cat([K, k], 2), torch.cat([V, v], 2), 200, H, q, qpos, stages, 1e-2)
+
+
+def test_quasar_exact_only_and_kernel_check():
+    st, p, K, V, H, g = _state(2, 0, 300, 0, (2, 2, 4), torch.float32, 3)
+    q = torch.randn((1, 8, 1, 128), generator=g)
+    _check(st, p, K, V, 300, H, q, [H], (2, 2, 4), 2e-3)
+    st2, *_ = _state(2, 3000, 100, 2, (2, 2, 4), torch.bfloat16, 4)
+    assert st2.check_kernel()["kernel"]
+
+
+def test_quasar_rejects_bad_input():
+    import kvq
+    st, p, K, V, H, g = _state(2, 100, 40, 0, (2, 2, 4), torch.float32, 9)
+    with pytest.raises(ValueError):
+        st.attend(torch.randn((1, 8, 1, 128)).cuda(), 0.1, [H, H + 1])
+    with pytest.raises(RuntimeError):
+        st.append(torch.zeros((1, 2, 1, 128)).cuda(), torch.zeros((1, 2, 1, 128)).cuda(), [H])
