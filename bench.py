@@ -236,6 +236,18 @@ def run_kivi(args, shape_name: str) -> dict:
                   packed_code_GBs=round(2 * shape.B * shape.Hkv * cache.n_q * shape.d // 2 / (ms_per_step * 1e-3) / 1e9,
                                         2))
     log(f"decode step {ms_per_step * 1e3:.1f} us, split kernel {split_ms * 1e3:.1f} us")
+    # measured cache bytes from the stored format itself (the wire-format export of the layer, context
+    # window included) against the analytic bits of state_bits: 2 d (bits + 32/group) per quantised
+    # token, 2 d 16 per exact row
+    wire = cache.export()
+    export_ms = eager_ms(lambda: cache.export(out=wire), max(5, args.steps // 20), 2)
+    analytic = shape.B * shape.Hkv * (cache.n_q * 2 * shape.d * (shape.bits + 32.0 / shape.group_k) +
+                                      cache.n_exact * 2 * shape.d * 16.0) / 8.0
+    res["payload"] = {"bytes": int(wire.numel()), "analytic_bytes": analytic,
+                      "payload_vs_analytic": wire.numel() / analytic - 1.0,
+                      "export_us": round(export_ms * 1e3, 3),
+                      "export_GBs": round(2 * wire.numel() / (export_ms * 1e-3) / 1e9, 2)}
+    del wire
     if not args.no_cpu_baseline:
         log("cpu baseline")
         res["cpu_baseline"] = cpu_kivi_decode(q, K, V, shape.window, shape.bits, shape.group_k, shape.group_v,

@@ -311,6 +311,24 @@ int kvq_kivi_append(const void* k_new, const void* v_new, int dtype, int64_t k_s
                     int group_v, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * F4  Wire format and measured bytes of a packed KIVI layer: replaces payload_bytes
+ * (STRATA_KV.py:2736-2769) for KIVI states, whose total must match the analytic state_bits
+ * (773-783, entry_bits 798-799).  kvq_kivi_export writes, from the decode layout of
+ * kvq_kivi_decode (same kc / k_lo / k_sc / vc / vmeta arguments), the sections
+ *   key codes (pack_codes rows, n_q x d/2 bytes per bh), key lo, key scale (fp16, ceil(n_q /
+ *   group_k) x d per bh), value codes (pack_codes rows), value lo, value scale (fp16, n_q x
+ *   d/group_v per bh), exact keys, exact values (n_exact x d per bh as fp16, the reference's .half()
+ *   of rows stored in exact_dtype; oldest first: slot (first_slot + i) % cap_e),
+ * each (b, h)-major, into out (out_bytes >= kvq_kivi_payload_bytes(...)).  4-bit codes, d = 128.
+ * ---------------------------------------------------------------------------------------- */
+int64_t kvq_kivi_payload_bytes(int64_t BH, int64_t n_q, int64_t d, int group_k, int group_v, int64_t n_exact,
+                               int exact_dtype);
+int kvq_kivi_export(const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_sc, const uint8_t* vc,
+                    const uint16_t* vmeta, int64_t BH, int64_t cap_t, int64_t n_q, int64_t d, int group_k,
+                    int group_v, const void* k_exact, const void* v_exact, int exact_dtype, int64_t cap_e,
+                    int64_t n_exact, int64_t first_slot, uint8_t* out, int64_t out_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * F2  QUASAR compressed-domain decode: replaces QuasarState.attend (QUASAR_KV.py:1945-1968) with
  * its coded part read from the packed bytes (the reference's _quasar_scores_kernel /
  * _quasar_values_kernel, 1498-1551, and their torch path, 1920-1943), batch 1.

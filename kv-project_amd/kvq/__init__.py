@@ -8,7 +8,7 @@ from ._lib import KVQError, load as load_library
 from .kivi import (kivi_quant, kivi_quant_stored, pack_codes, pack_rows, unpack_codes, unpack_rows, v_tile,
                    v_untile, vmeta_tile)
 from .decode import PackedKIVICache, kivi_decode, workspace_floats
-from .state import DecodeCtl, KIVIState, Router, register, routed, router_attention
+from .state import DecodeCtl, KIVIState, Router, payload_bytes, register, routed, router_attention
 from .evict import gather_dequant, retained_cache, topk_retain
 from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strata_center_rotate, strata_decode,
                      strata_quantize, strata_v_tile, strata_workspace_floats, uniform_step, unpack_planar)
@@ -24,5 +24,5 @@ __all__ = [
     "uniform_step", "strata_center_rotate", "strata_quantize", "strata_v_tile", "StrataCache", "StrataTier",
     "strata_decode", "strata_workspace_floats", "DctCache", "dct_decode", "dct_encode", "dct_table",
     "dct_workspace_floats", "MixedKIVICache", "c3_widths", "mixed_decode", "mixed_workspace_floats", "offset_table",
-    "QuasarState", "stage_codebooks",
+    "QuasarState", "stage_codebooks", "payload_bytes",
 ]

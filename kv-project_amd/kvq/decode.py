@@ -141,6 +141,42 @@ class PackedKIVICache:
         """Bytes a decode step reads: codes and metadata of the n_q packed rows + exact rows."""
         return self.packed_bytes() + self.exact_bytes()
 
+    def _exact_window(self, n_exact: Optional[int]):
+        n_exact = self.n_exact if n_exact is None else int(n_exact)
+        if not 0 <= n_exact <= self.n_exact:
+            raise ValueError("n_exact must be in [0, cache.n_exact]")
+        # oldest exact row first: a ring holds position p in slot p % cap_e
+        first = ((self.next_pos - self.n_exact) % self.cap_e) if self.ring else 0
+        return n_exact, first
+
+    def wire_bytes(self, n_exact: Optional[int] = None) -> int:
+        """Size of the wire-format payload (``export``) without writing it."""
+        n_ex, _ = self._exact_window(n_exact)
+        B, H = self.kc.shape[:2]
+        n = _lib.load().kvq_kivi_payload_bytes(B * H, self.n_q, self.kc.shape[3] * 2, self.group_k, self.group_v, n_ex,
+                                              _lib.DTYPE_CODE[self.k_exact.dtype])
+        if n < 0:
+            raise _lib.KVQError("kvq_kivi_payload_bytes rejected the shape")
+        return int(n)
+
+    @torch.no_grad()
+    def export(self, n_exact: Optional[int] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The layer's payload in the reference's storage format (payload_bytes, STRATA_KV.py:2736-2769),
+        written on the device by libkvq kvq_kivi_export: pack_codes key codes, fp16 key lo / scale
+        of every group, pack_codes value codes, fp16 value lo / scale, then the first ``n_exact``
+        exact rows (all by default) oldest first as fp16, each section (b, h)-major.  Its length is
+        the measured cache size."""
+        n_ex, first = self._exact_window(n_exact)
+        nbytes = self.wire_bytes(n_ex)
+        if out is None:
+            out = torch.empty((nbytes,), dtype=torch.uint8, device=self.kc.device)
+        B, H = self.kc.shape[:2]
+        _lib.call("kvq_kivi_export", self.kc.data_ptr(), self.k_lo.data_ptr(), self.k_sc.data_ptr(), self.vc.data_ptr(),
+                  self.vmeta.data_ptr(), B * H, self.cap_t, self.n_q, self.kc.shape[3] * 2, self.group_k, self.group_v,
+                  self.k_exact.data_ptr(), self.v_exact.data_ptr(), _lib.DTYPE_CODE[self.k_exact.dtype], self.cap_e,
+                  n_ex, first, out.data_ptr(), out.numel(), _lib.stream_of(self.kc))
+        return out[:nbytes]
+
 
 def workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_q: int, n_exact: int,
                      group_k: int, group_v: int, split_tokens: int = 0) -> int:

@@ -73,6 +73,12 @@ def routed(controller):
         Router.active = previous
 
 
+def payload_bytes(states: Dict[int, "KIVIState"]) -> int:
+    """MEASURED bytes of the compressed context over the layers (payload_bytes, STRATA_KV.py:
+    2736-2769): the wire-format size of every state that owns its cache (shared ones excluded)."""
+    return sum(st.payload_bytes() for st in states.values() if st.shared is None)
+
+
 class DecodeCtl:
     """Single- or multi-token decode steps against per-layer states (STRATA_KV.py:2817-2834)."""
 
@@ -123,6 +129,18 @@ class KIVIState:
         d = c.kc.shape[3] * 2
         window = self.n0 - c.n_q
         return c.packed_bytes() + 2 * B * Hkv * window * d * c.k_exact.element_size()
+
+    def payload(self) -> torch.Tensor:
+        """The stored context in the reference's storage format (payload_bytes, STRATA_KV.py:
+        2736-2769), written on the device: codes and fp16 metadata of the quantised rows, then the
+        context's exact rows (the window; appended tokens are not context)."""
+        c = self.cache
+        return c.export(n_exact=self.n0 - c.n_q)
+
+    def payload_bytes(self) -> int:
+        """MEASURED bytes of the stored context: the length of ``payload()``."""
+        c = self.cache
+        return c.wire_bytes(n_exact=self.n0 - c.n_q)
 
     def append(self, k: torch.Tensor, v: torch.Tensor, pos) -> None:
         """Append t tokens (B, Hkv, t, d) at positions ``pos`` exactly (STRATA_KV.py:707-714)."""

@@ -138,3 +138,32 @@ def unpack_codes(packed: np.ndarray, bits: int, count: int) -> np.ndarray:
     bitsarr = np.unpackbits(p)[:count * bits].reshape(count, bits).astype(np.uint16)
     w = (1 << np.arange(bits - 1, -1, -1)).astype(np.uint16)
     return (bitsarr * w).sum(1).astype(np.uint8)
+
+
+def kivi_state_bits(n_q: int, n_exact: int, d: int, bits: int, group: int) -> float:
+    """Analytic stored bits of one (b, h) pair of a KIVI layer (LayerMethod.state_bits,
+    STRATA_KV.py:773-783, with KIVIMethod.entry_bits 798-799 and kivi_effective_bits 465-466):
+    2 d (bits + 32 / group) per quantised token, 2 d 16 per exact row."""
+    return n_q * 2 * d * (bits + 32.0 / group) + n_exact * 2 * d * 16.0
+
+
+def kivi_payload_sections(K: np.ndarray, V: np.ndarray, bits: int, group_k: int, group_v: int, n_q: int):
+    """The quantised part of the KIVI payload (payload_bytes, STRATA_KV.py:2736-2769) of K, V
+    (B, H, T, d) float32 whose first n_q rows are read quantised: per section, the bytes of every
+    (b, h) in order -- pack_codes of the key codes, fp16 key lo, fp16 key scale (the ceil(n_q /
+    group_k) groups that hold those rows), pack_codes of the value codes, fp16 value lo and scale
+    of the n_q rows.  Keys are grouped over all T rows, as kivi_quant over the whole tensor does."""
+    B, H, T, d = K.shape
+    kq = kivi_quant(K, bits, group_k, True, 0)
+    vq = kivi_quant(V, bits, group_v, False, 0)
+    n_g = -(-n_q // group_k)
+    sec = [b"", b"", b"", b"", b"", b""]
+    for b in range(B):
+        for h in range(H):
+            sec[0] += pack_codes(kq["codes"][b, h, :n_q], bits).tobytes()
+            sec[1] += kq["lo"][b, h, :n_g].astype(np.float16).tobytes()
+            sec[2] += kq["scale"][b, h, :n_g].astype(np.float16).tobytes()
+            sec[3] += pack_codes(vq["codes"][b, h, :n_q], bits).tobytes()
+            sec[4] += vq["lo"][b, h, :n_q].astype(np.float16).tobytes()
+            sec[5] += vq["scale"][b, h, :n_q].astype(np.float16).tobytes()
+    return sec

@@ -150,3 +150,22 @@ def test_byte_lut_kat_and_decode():
         levels = rng.standard_normal(2 ** bits).astype(np.float32)
         c = rng.integers(0, 2 ** bits, (4, 128))
         np.testing.assert_array_equal(unpack_rows_lut(pack_rows(c, bits), bits, levels), levels[c])
+
+
+@pytest.mark.parametrize("n_q,W,group,bits", [(256, 44, 64, 4), (320, 128, 32, 4), (0, 16, 64, 4)])
+def test_kivi_payload_size_is_the_analytic_bits(n_q, W, group, bits):
+    """payload == analytic bits (STRATA_KV.py:2742-2743: 'Must agree with the analytic state_bits'):
+    the oracle's payload sections plus 2-byte exact rows against state_bits' per-token charge, and
+    the library's size function against both (no GPU needed)."""
+    from oracle.kivi import kivi_payload_sections, kivi_state_bits
+    rng = np.random.default_rng(n_q + W)
+    B, H, d = 2, 3, 128
+    K = rng.standard_normal((B, H, n_q + W, d)).astype(np.float32)
+    V = rng.standard_normal((B, H, n_q + W, d)).astype(np.float32)
+    sec = kivi_payload_sections(K, V, bits, group, group, n_q)
+    total = sum(len(x) for x in sec) + 2 * B * H * W * d * 2
+    assert total * 8 == B * H * kivi_state_bits(n_q, W, d, bits, group)
+    from kvq import _lib
+    if _lib.LIB_PATH.exists():
+        for dt in (_lib.KVQ_BF16, _lib.KVQ_F32):
+            assert _lib.load().kvq_kivi_payload_bytes(B * H, n_q, d, group, group, W, dt) == total
