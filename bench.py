@@ -15,6 +15,7 @@ The other rows of the path are measured by the same script with ``--workload``:
   append  streaming append of one token per sequence at the C2 shape (µs/step)
   quant   prefill quantise + pack of the C2 context (kivi_quant of K and V)
   quasar  QUASAR compressed-domain decode (embedded spectral code, 64k context, batch 1)
+  micro   the reference's decode-attention microbenchmark: SDPA (full, evicting) vs the packed kernels
 Each prints one JSON line of the same form (its own metric, roofline and CPU baseline).
 
 Timing: W untimed warm-up steps, then K steps launched back to back between HIP events on the
@@ -509,6 +510,143 @@ def run_quasar(args) -> dict:
 
 
 # ---------------------------------------------------------------------------------------------
+# F3: decode-attention microbenchmark (the reference's attention_microbench, STRATA_KV.py:3363-3421)
+
+def _graph_median_us(fn, reps: int) -> float:
+    """Median µs of one graph replay of fn (captured once after 3 warm-up calls on a side stream),
+    each replay bracketed by its own events: the reference's _time_callable (STRATA_KV.py:3424-3444)."""
+    import numpy as np
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(10):
+        graph.replay()
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) * 1000.0)
+    return float(np.median(ts))
+
+
+def run_micro(args) -> dict:
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+    import kvq
+    from kvq.quasar import synthetic_packed
+    d, Hkv, rep = args.micro_shape
+    keeps = args.micro_keep
+    dt = torch.bfloat16
+    reps = 50
+    g = torch.Generator(device="cpu").manual_seed(42)
+    rows = []
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        sdpa_ctx = lambda: sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION])
+    except ImportError:                                              # older torch: no backend selection
+        sdpa_ctx = None
+    for H in args.micro_lengths:
+        log(f"microbench H={H}")
+        spec = torch.exp(-torch.arange(d) / (d / 8.0))               # decaying key spectrum + shared offset
+        Kc = (torch.randn(1, Hkv, H, d, generator=g) * spec.sqrt() + 2.0).to("cuda", dt).contiguous()
+        Vc = torch.randn(1, Hkv, H, d, generator=g).to("cuda", dt).contiguous()
+        q1 = torch.randn(1, Hkv * rep, 1, d, generator=g).to("cuda", dt)
+        scaling = d ** -0.5
+        full_bytes = 2 * Kc.numel() * Kc.element_size()
+        res = {}
+
+        def sdpa(K_, V_):
+            if sdpa_ctx is None:
+                raise RuntimeError("no SDPA backend selection in this torch")
+            with sdpa_ctx():                                         # fused kernels only, never the math path
+                return F.scaled_dot_product_attention(q1, K_, V_, enable_gqa=True)
+        try:
+            sdpa(Kc, Vc)
+            res["full_sdpa"] = (_graph_median_us(lambda: sdpa(Kc, Vc), reps), full_bytes)
+            for keep in keeps:
+                n_keep = max(1, int(H * keep))
+                Ke, Ve = Kc[:, :, :n_keep].contiguous(), Vc[:, :, :n_keep].contiguous()
+                res[f"evict_sdpa@{keep:g}"] = (_graph_median_us(lambda Ke=Ke, Ve=Ve: sdpa(Ke, Ve), reps),
+                                               2 * Ke.numel() * Ke.element_size())
+        except RuntimeError as e:                                    # a fused backend refused: recorded
+            log(f"  SDPA rows skipped: {e}")
+            res["full_sdpa"] = (float("nan"), full_bytes)
+        # the full bf16 cache through this build's exact-row decode (every row exact): the fair
+        # full-cache baseline on this GPU (torch's fused SDPA is not a decode kernel here)
+        full = kvq.PackedKIVICache.from_context(Kc, Vc, window=H, group_k=64, group_v=64)
+        out = torch.empty((1, 1, Hkv * rep, d), dtype=dt, device="cuda")
+        fws = torch.zeros((kvq.workspace_floats(1, Hkv * rep, Hkv, 1, d, full.n_q, full.n_exact, 64, 64),),
+                          dtype=torch.float32, device="cuda")
+        res["full_exact_kernel"] = (_graph_median_us(lambda: kvq.kivi_decode(q1, scaling, full, out=out, workspace=fws), reps),
+                                    full_bytes)
+        del full, fws
+        # packed 4-bit KIVI (window 128, groups of 64): the path's headline kernel
+        W = 128
+        cache = kvq.PackedKIVICache.from_context(Kc, Vc, window=W, group_k=64, group_v=64)
+        ws = torch.zeros((kvq.workspace_floats(1, Hkv * rep, Hkv, 1, d, cache.n_q, cache.n_exact, 64, 64),),
+                         dtype=torch.float32, device="cuda")
+        res["kivi4_kernel"] = (_graph_median_us(lambda: kvq.kivi_decode(q1, scaling, cache, out=out, workspace=ws), reps),
+                               cache.wire_bytes())
+        for keep in keeps:
+            # STRATA at about keep x the full bytes: a synthetic per-token allocation (tokens ranked by a
+            # random importance; the compression-side search is not part of this build)
+            imp = torch.rand((1, Hkv, H), generator=g).to("cuda")
+            order = torch.argsort(-imp, dim=-1).to(torch.int32)
+            frac = {0.25: (0.15, 0.30, 0.45), 0.125: (0.04, 0.10, 0.60)}.get(keep, (0.04, 0.10, 0.60))
+            n8, n4, n2 = (int(f * H) for f in frac)
+            assign = [(8, order[..., :n8].contiguous()), (4, order[..., n8:n8 + n4].contiguous()),
+                      (2, order[..., n8 + n4:n8 + n4 + n2].contiguous())]
+            sc = kvq.StrataCache.from_context(Kc, Vc, window=0, assign=assign)
+            sws = torch.zeros((kvq.strata_workspace_floats(1, Hkv * rep, Hkv, 1, d, sc.n_exact, [t.n for t in sc.tiers],
+                                                           [t.bits for t in sc.tiers]),), dtype=torch.float32, device="cuda")
+            res[f"strata_kernel@{keep:g}"] = (_graph_median_us(lambda sc=sc, sws=sws: kvq.strata_decode(q1, scaling, sc, out=out,
+                                                                                                   workspace=sws), reps),
+                                              sc.coded_bytes())
+        # QUASAR at about 1/8 of the full bytes: half the tokens coded (12 embedded levels), 1% exact
+        n_c = H // 2
+        n0 = max(36, H // 100)
+        qs = kvq.QuasarState(Kc[:, :, :n0].contiguous(), Vc[:, :, :n0].contiguous(),
+                             synthetic_packed(Hkv, d, n_c, seed=H), (2, 2, 4), 0, H)
+        qpos = torch.tensor([H], device="cuda")
+        res["quasar_kernel@~0.125"] = (_graph_median_us(lambda: qs.attend(q1, scaling, qpos, out=out), reps),
+                                       qs.context_bytes())
+        base, fair = res["full_sdpa"][0], res["full_exact_kernel"][0]
+        for name, (us, nbytes) in res.items():
+            rows.append({"context": H, "method": name, "us_per_step": round(us, 2), "cache_bytes": int(nbytes),
+                         "speedup_vs_full": round(base / us, 3) if us > 0 and base == base else None,
+                         "speedup_vs_full_exact_kernel": round(fair / us, 3) if us > 0 else None})
+        log("  " + ", ".join(f"{k_}={v_[0]:.1f}us/{v_[1] / 2**20:.2f}MiB" for k_, v_ in res.items()))
+        del cache, ws, qs
+        torch.cuda.empty_cache()
+    last = [r for r in rows if r["context"] == args.micro_lengths[-1]]
+    kivi = next(r for r in last if r["method"] == "kivi4_kernel")
+    res_line = _result(args, metric="decode-attention microbenchmark: packed 4-bit KIVI µs/step at the longest context "
+                                    "(full table under rows)",
+                       value=kivi["us_per_step"], unit="us", ms_per_step=kivi["us_per_step"] / 1e3, hib=False,
+                       workload=f"F3: the reference's attention_microbench (one layer, one decode step, graph replay, "
+                                f"median of {reps}) at contexts {list(args.micro_lengths)}, d={d}, Hkv={Hkv}, rep={rep}: "
+                                "full and eviction SDPA (fused backends only), the full bf16 cache through this build's exact-row "
+                                "decode, packed KIVI-4, STRATA tiers (synthetic allocation) and QUASAR codes (synthetic); keys "
+                                "with a decaying spectrum and a shared offset, random values",
+                       config={"global_batch": 1, "seq_len": args.micro_lengths[-1], "parallelism": "single GPU",
+                               "keep": list(keeps)},
+                       dtype="bf16", roofline=_roof(kivi["cache_bytes"], kivi["us_per_step"] / 1e3, "kivi4 step (graph)"),
+                       rows=rows, timer="one graph replay per sample, median")
+    return res_line
+
+
+# ---------------------------------------------------------------------------------------------
 # C4: eviction
 
 def run_c4(args) -> dict:
@@ -715,7 +853,8 @@ def run_quant(args) -> dict:
 
 
 WORKLOADS = {"c2": lambda a: run_kivi(a, "c2"), "c1": lambda a: run_kivi(a, "c1"), "c3": run_c3, "c4": run_c4,
-             "c5": run_c5, "strata": run_strata, "append": run_append, "quant": run_quant, "quasar": run_quasar}
+             "c5": run_c5, "strata": run_strata, "append": run_append, "quant": run_quant, "quasar": run_quasar,
+             "micro": run_micro}
 
 
 def main() -> int:
@@ -729,6 +868,10 @@ def main() -> int:
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--micro-lengths", type=int, nargs="+", default=[4096, 16384, 65536],
+                    help="contexts of --workload micro (the reference's MICRO_LENGTHS)")
+    ap.add_argument("--micro-shape", type=int, nargs=3, default=[128, 8, 4], metavar=("D", "HKV", "REP"))
+    ap.add_argument("--micro-keep", type=float, nargs="+", default=[0.25, 0.125])
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (profiler counter calibration)")
     args = ap.parse_args()
