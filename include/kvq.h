@@ -339,12 +339,13 @@ int kvq_kivi_export(const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_s
  *   order, described by the side's step table, int32 rows [byte offset, n_s, nb, a, w, bits, level
  *   offset] (1883-1898; n_s non-increasing, nb in {4, 8, 16, 32, 64}, at most 128 bytes per token
  *   and side).  levels = the stage codebooks concatenated (float32, at most 256).  rho_k / rho_v
- *   (Hkv, n_c) fp16; T_k / T_v (Hkv, d, R) float32 (R a multiple of 4); mu_k / mu_v (Hkv, d)
- *   float32.  bounds (`splits` + 1 int32 chunk boundaries, 64-token chunks), slots (int32 [2][32][8])
+ *   (Hkv, n_c) fp16; T_k (Hkv, d, R_k) float32 (R_k a multiple of 4) and T_v transposed,
+ *   (Hkv, R_v, d) float32; mu_k / mu_v (Hkv, d) float32.  bounds (`splits` + 1 int32 chunk boundaries, 64-token chunks), slots (int32 [2][32][8])
  *   and the slot counts come from kvq_quasar_plan (device copies).  out (1, Tq, Hq, d) of
  *   q_dtype.  rep x Tq <= 8.  phases: mask of 1 (the
- *   query's coefficients), 2 (the split launch), 4 (the merge); 7 for a decode step (the others
- *   are timing hooks that reuse the workspace of an earlier call).
+ *   query's coefficients), 2 (the split launch), 4 (the row merge, where up to 128 exact rows are
+ *   attended); 7 for a decode step (the others are timing hooks that reuse the workspace of an
+ *   earlier call).
  * kvq_quasar_plan: host-memory step tables in (checked); out, in host memory: cost-balanced chunk
  * boundaries (bounds needs max_splits + 1 entries; *n_splits receives the split count) and the
  * slot table (2 x 32 x 8 int32: per 4-byte slot of a token's rows, the step offset + 4 dw, n_s, nb,

@@ -7,14 +7,16 @@
 //           bits) of the step's band [a, a + w) at b bits, for the n_s most important coded tokens
 //   table   int32 rows [byte offset of the step's block, n_s, nb, a, w, b, level offset]
 //   levels  float32 stage codebooks, concatenated (one list for both sides)
-// plus rho (Hkv, n_c) fp16 per coded token and side, the read-out matrices T (Hkv, d, R) and the
-// means mu (Hkv, d) (float32 here).  Coded token j of head h contributes
+// plus rho (Hkv, n_c) fp16 per coded token and side, the read-out matrices T_K (Hkv, d, R) and
+// T_V^T (Hkv, R, d, transposed) and the means mu (Hkv, d), float32 here.  Coded token j of head h contributes
 //   logit  (sum over the K steps with n_s > j of qt[band] . level[code]) rho_K[j] + q . mu_K
 //   value  p_j rho_V[j] level[code] into coefficient a + i of each V step it owns,
 // with qt = q T_K; the value coefficients are lifted once per query row: o += acc T_V^T + P mu_V.
 //
 // Launches: quasar_prologue (qt and q . mu_K, log2 units), quasar_split (coded workgroups over
-// cost-balanced token ranges, then exact-row workgroups), quasar_merge (rows combined, lift).
+// cost-balanced token ranges, each lifting its coefficient sums by T_V into an output partial, then
+// exact-row workgroups when the exact part is long), merge_rows_kernel (the shared row merge; a short
+// exact part is attended there).
 #include <algorithm>
 #include <vector>
 
@@ -54,7 +56,9 @@ struct QuasarParams {
   int S;
   float* ws_m;                            // [Hkv][S][R]
   float* ws_l;
-  float* ws_acc;                          // [Hkv][S][R][Rv]
+  float* ws_o;                            // [Hkv][S][R][128]: the split's lifted output (acc T_V^T + l mu_V)
+  const float* tvt;                       // [Hkv][Rv][128] read-out T_V transposed
+  const float* muv;                       // [Hkv][128]
   ExactArgs ex;                           // exact rows of the split launch (ex.n rows)
   int S_ex;                               // exact-row workgroups per (h, row)
   float* ex_m;                            // [Hkv][S_ex][R]
@@ -371,8 +375,9 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     }
     wave_lds_fence();                                             // staging, pch, accw of this chunk done
   }
-  // ---- epilogue: the four wavefronts' (m, l, acc) into this split's partial ----
-  float* mw = &pch_all[0][0];                                     // [wave][R] maxima, then [wave][R] sums
+  // ---- epilogue: the four wavefronts' (m, l, acc) combined, lifted by T_V into this split's
+  // output partial (the exact-row partials' form, so the shared row merge combines them) ----
+  float* mw = &pch_all[0][0];                                     // [wave][R] maxima, then [wave][R] sums, then [R] M, [R] L
   float l_w[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) l_w[r] = wave_sum(l_lane[r]);
@@ -385,7 +390,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     }
   }
   __syncthreads();
-  const int64_t pr0 = (static_cast<int64_t>(h) * p.S + sidx) * R;
+  float* accc = reinterpret_cast<float*>(&stage_all[0][0][0]);   // [R][kQRowCoef] combined coefficients
   for (int i = tid; i < R * p.Rv; i += kQThreads) {
     const int r = i / p.Rv, c = i % p.Rv;
     float M = -INFINITY;
@@ -399,102 +404,44 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
       a = __builtin_fmaf(sc, acc_all[w][r * kQRowCoef + c], a);
       L = __builtin_fmaf(sc, mw[kQWaves * R + w * R + r], L);
     }
-    p.ws_acc[pr0 * p.Rv + i] = a;
+    accc[r * kQRowCoef + c] = a;
     if (c == 0) {
-      p.ws_m[pr0 + r] = M;
-      p.ws_l[pr0 + r] = L;
+      mw[2 * kQWaves * R + r] = M;
+      mw[2 * kQWaves * R + R + r] = L;
     }
   }
-}
-
-// One workgroup per (h, row r): partials combined, coefficients lifted by T_V, mu_V added.
-// Weights of every partial first (LDS), then the coefficient sums (thread k over the splits,
-// loads independent of the sum), then the lift with one wavefront per output channel group
-// (coalesced rows of T_V, wave sums).
-constexpr int kQMaxParts = 2048;
-template <int R, int DT>
-__global__ __launch_bounds__(256) void quasar_merge(const float* __restrict__ ws_m, const float* __restrict__ ws_l,
-                                                    const float* __restrict__ ws_acc, int S, const float* __restrict__ ex_m,
-                                                    const float* __restrict__ ex_l, const float* __restrict__ ex_o, int S_ex,
-                                                    const float* __restrict__ Tv, const float* __restrict__ muv, int Rv,
-                                                    int R_real, int rep, int Tq, int Hq, void* __restrict__ out) {
-  constexpr int D = 128;
-  __shared__ float acc[kQMaxR];
-  __shared__ float wts[kQMaxParts];                               // [S coded][S_ex exact]
-  __shared__ float oex[D];
-  __shared__ float red[8];
-  const int h = blockIdx.x / R_real, r = blockIdx.x % R_real;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int NP = S + S_ex;
-  auto mof = [&](int s) {
-    return s < S ? ws_m[(static_cast<int64_t>(h) * S + s) * R + r] : ex_m[(static_cast<int64_t>(h) * S_ex + s - S) * R + r];
-  };
-  auto lof = [&](int s) {
-    return s < S ? ws_l[(static_cast<int64_t>(h) * S + s) * R + r] : ex_l[(static_cast<int64_t>(h) * S_ex + s - S) * R + r];
-  };
-  float m = -INFINITY;
-  for (int s = tid; s < NP; s += 256) m = fmaxf(m, mof(s));
-  m = wave_max(m);
-  if (lane == 0) red[wave] = m;
   __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float lc = 0.0f, le = 0.0f;
-  for (int s = tid; s < NP; s += 256) {
-    const float ms = mof(s);
-    const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-    wts[s] = w;
-    if (s < S) lc += w * lof(s);
-    else le += w * lof(s);
-  }
-  lc = wave_sum(lc);
-  le = wave_sum(le);
-  __syncthreads();                                                // red[] reads of the maximum done
-  if (lane == 0) {
-    red[wave] = lc;
-    red[4 + wave] = le;
-  }
-  __syncthreads();
-  const float Pc = (red[0] + red[1]) + (red[2] + red[3]);
-  const float L = Pc + ((red[4] + red[5]) + (red[6] + red[7]));
-  {                                                               // thread (k, half): half the splits each
-    const int k = tid % kQRowCoef, half = tid / kQRowCoef;
-    float a = 0.0f;
-    if (k < Rv) {
-      const float* src = ws_acc + (static_cast<int64_t>(h) * S * R + r) * Rv + k;
-#pragma unroll 16
-      for (int s = half; s < S; s += 2) a = __builtin_fmaf(wts[s], src[static_cast<int64_t>(s) * R * Rv], a);
-    }
-    if (half == 1) acc[k] = a;
-    __syncthreads();
-    if (half == 0) acc[k] += a;
-  }
-  if (tid < D) {
-    float o = 0.0f;
-    const float* src = ex_o + (static_cast<int64_t>(h) * S_ex * R + r) * D + tid;
+  const int64_t pr0 = (static_cast<int64_t>(h) * p.S + sidx) * R;
+  if (tid < 128) {                                                // thread = output channel
+    const int c = tid;
+    float o[R];
+    const float mu = p.muv[static_cast<int64_t>(h) * 128 + c];
+#pragma unroll
+    for (int r = 0; r < R; ++r) o[r] = mw[2 * kQWaves * R + R + r] * mu;
+    const float* tcol = p.tvt + static_cast<int64_t>(h) * p.Rv * 128 + c;
 #pragma unroll 4
-    for (int s = 0; s < S_ex; ++s) o = __builtin_fmaf(wts[S + s], src[static_cast<int64_t>(s) * R * D], o);
-    oex[tid] = o;
+    for (int k = 0; k < p.Rv; ++k) {
+      const float t = tcol[static_cast<int64_t>(k) * 128];
+#pragma unroll
+      for (int r = 0; r < R; ++r) o[r] = __builtin_fmaf(accc[r * kQRowCoef + k], t, o[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) p.ws_o[(pr0 + r) * 128 + c] = o[r];
   }
-  __syncthreads();
-  const int hq = h * rep + r / Tq, t = r % Tq;
-#pragma unroll 8
-  for (int c = wave; c < D; c += 4) {                             // wavefront per output channel
-    float x = 0.0f;
-    if (S > 0) {
-      const float* trow = Tv + (static_cast<int64_t>(h) * D + c) * Rv;
-      x = lane < Rv ? acc[lane] * trow[lane] : 0.0f;
-      if (lane + 64 < Rv) x = __builtin_fmaf(acc[lane + 64], trow[lane + 64], x);
-    }
-    x = wave_sum(x);
-    if (lane == 0) {
-      const float mu = S > 0 ? Pc * muv[static_cast<int64_t>(h) * D + c] : 0.0f;
-      store_from_f32<DT>(out, (static_cast<int64_t>(t) * Hq + hq) * D + c, (oex[c] + x + mu) / L);
-    }
+  if (tid < R) {
+    p.ws_m[pr0 + tid] = mw[2 * kQWaves * R + tid];
+    p.ws_l[pr0 + tid] = mw[2 * kQWaves * R + R + tid];
   }
 }
 
 inline int64_t quasar_ws_floats(int64_t Hkv, int R, int64_t Rk, int64_t S, int64_t S_ex) {
-  return Hkv * R * Rk + Hkv * R + 2 * Hkv * S * R + Hkv * S * R * kQMaxR + 2 * Hkv * S_ex * R + Hkv * S_ex * R * 128;
+  return Hkv * R * Rk + Hkv * R + 2 * Hkv * S * R + Hkv * S * R * 128 + 2 * Hkv * S_ex * R + Hkv * S_ex * R * 128;
+}
+
+// exact rows: in the merge up to kQExRows of them (one key and one value round trip there), else
+// workgroups of kQExRows rows in the split launch, overlapping the coded work
+inline int64_t quasar_exact_blocks(int64_t n_exact) {
+  return n_exact <= kQExRows ? 0 : (n_exact + kQExRows - 1) / kQExRows;
 }
 
 }  // namespace
@@ -585,8 +532,7 @@ extern "C" int64_t kvq_quasar_decode_workspace(int64_t Hq, int64_t Hkv, int64_t 
     return -1;
   const int64_t R = pow2_rows(Hq / Hkv * Tq);
   if (R > 8) return -1;
-  const int64_t S_ex = (n_exact + kQExRows - 1) / kQExRows;
-  return quasar_ws_floats(Hkv, static_cast<int>(R), R_k, splits, S_ex);
+  return quasar_ws_floats(Hkv, static_cast<int>(R), R_k, splits, quasar_exact_blocks(n_exact));
 }
 
 extern "C" int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64_t q_st, int64_t Hq, int64_t Hkv,
@@ -626,7 +572,7 @@ extern "C" int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64
   }
   const int R = pow2_rows(R_real);
   const int S = n_c > 0 ? splits : 0;
-  const int64_t S_ex = (n_exact + kQExRows - 1) / kQExRows;
+  const int64_t S_ex = quasar_exact_blocks(n_exact);
   const int64_t need = quasar_ws_floats(Hkv, R, std::max<int64_t>(R_k, 1), std::max(S, 1), S_ex);
   KVQ_REQUIRE(workspace_floats >= need, "kvq_quasar_decode: workspace of %lld floats, need %lld",
               static_cast<long long>(workspace_floats), static_cast<long long>(need));
@@ -636,8 +582,8 @@ extern "C" int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64
   float* qmu = qt + Hkv * R * std::max<int64_t>(R_k, 1);
   float* ws_m = qmu + Hkv * R;
   float* ws_l = ws_m + Hkv * std::max(S, 1) * R;
-  float* ws_acc = ws_l + Hkv * std::max(S, 1) * R;
-  float* ex_m = ws_acc + Hkv * std::max(S, 1) * R * kQMaxR;
+  float* ws_o = ws_l + Hkv * std::max(S, 1) * R;
+  float* ex_m = ws_o + Hkv * std::max(S, 1) * R * 128;
   float* ex_l = ex_m + Hkv * S_ex * R;
   float* ex_o = ex_l + Hkv * S_ex * R;
   if (n_c > 0 && (phases & 1)) {
@@ -674,7 +620,9 @@ extern "C" int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64
   p.S = S;
   p.ws_m = ws_m;
   p.ws_l = ws_l;
-  p.ws_acc = ws_acc;
+  p.ws_o = ws_o;
+  p.tvt = T_v;
+  p.muv = mu_v;
   p.ex = ExactArgs{q, 0, q_sh, q_st, qscale, k_exact, v_exact, cap_e, static_cast<int>(n_exact), exact_pos, q_pos};
   p.S_ex = static_cast<int>(S_ex);
   p.ex_m = ex_m;
@@ -682,7 +630,6 @@ extern "C" int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64
   p.ex_o = ex_o;
   const int64_t n_wg = Hkv * S + Hkv * R_real * S_ex;
   const size_t lds = 0;                                           // static LDS (stage, coefficients, levels)
-  KVQ_REQUIRE(S + S_ex <= kQMaxParts, "kvq_quasar_decode: too many partials per row");
 #define KVQ_QSPLIT(R_, DT_) hipLaunchKernelGGL((quasar_split<R_, DT_>), dim3(static_cast<unsigned>(n_wg)), dim3(kQThreads), lds, st, p)
 #define KVQ_QSPLIT_R(DT_)                  \
   switch (R) {                             \
@@ -691,24 +638,31 @@ extern "C" int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64
     case 4: KVQ_QSPLIT(4, DT_); break;     \
     default: KVQ_QSPLIT(8, DT_); break;    \
   }
-  if (phases & 2) KVQ_DISPATCH_DTYPE(q_dtype, KVQ_QSPLIT_R(DT_));
+  if ((phases & 2) && n_wg > 0) {                               // nothing to split: the merge does it all
+    KVQ_DISPATCH_DTYPE(q_dtype, KVQ_QSPLIT_R(DT_));
+    KVQ_LAUNCH_CHECK("kvq_quasar_decode(split)");
+  }
 #undef KVQ_QSPLIT_R
 #undef KVQ_QSPLIT
-  KVQ_LAUNCH_CHECK("kvq_quasar_decode(split)");
-#define KVQ_QMERGE(R_, DT_)                                                                                       \
-  hipLaunchKernelGGL((quasar_merge<R_, DT_>), dim3(static_cast<unsigned>(Hkv * R_real)), dim3(256), 0, st, ws_m, ws_l, \
-                     ws_acc, S, ex_m, ex_l, ex_o, static_cast<int>(S_ex), T_v, mu_v, p.Rv, static_cast<int>(R_real),   \
-                     p.rep, static_cast<int>(Tq), static_cast<int>(Hq), out)
-#define KVQ_QMERGE_R(DT_)                  \
-  switch (R) {                             \
-    case 1: KVQ_QMERGE(1, DT_); break;     \
-    case 2: KVQ_QMERGE(2, DT_); break;     \
-    case 4: KVQ_QMERGE(4, DT_); break;     \
-    default: KVQ_QMERGE(8, DT_); break;    \
+  if (phases & 4) {                                              // the shared row merge (partials.hpp)
+    MergeArgs ma{};
+    ma.ws_o = ws_o;
+    ma.ws_m = ws_m;
+    ma.ws_l = ws_l;
+    ma.S = S;
+    ma.ex_o = ex_o;
+    ma.ex_m = ex_m;
+    ma.ex_l = ex_l;
+    ma.S_ex = static_cast<int>(S_ex);
+    ma.Hq = static_cast<int>(Hq);
+    ma.Hkv = static_cast<int>(Hkv);
+    ma.Tq = static_cast<int>(Tq);
+    ma.rep = p.rep;
+    ma.R_real = static_cast<int>(R_real);
+    ma.out = out;
+    if (S_ex == 0 && n_exact > 0) ma.ex = p.ex;                    // short exact part: attended in the merge
+    const int rc = launch_merge_rows(ma, R, static_cast<int>(Hkv), q_dtype, st);
+    if (rc != KVQ_OK) return rc;
   }
-  if (phases & 4) KVQ_DISPATCH_DTYPE(q_dtype, KVQ_QMERGE_R(DT_));
-#undef KVQ_QMERGE_R
-#undef KVQ_QMERGE
-  KVQ_LAUNCH_CHECK("kvq_quasar_decode(merge)");
   return KVQ_OK;
 }

@@ -160,6 +160,7 @@ class QuasarState:
             f32 = lambda x: torch.as_tensor(x).to(dev, torch.float32).contiguous()
             self.rho_k, self.rho_v = f16(packed["rho_k"]), f16(packed["rho_v"])
             self.T_k, self.T_v = f32(packed["T_k"]), f32(packed["T_v"])
+            self.T_vt = self.T_v.transpose(1, 2).contiguous()         # (Hkv, R_v, d): the lift reads it by channel
             self.mu_k, self.mu_v = f32(packed["mu_k"]), f32(packed["mu_v"])
             for nm, t, shape in (("rho_k", self.rho_k, (Hkv, self.n_c)), ("rho_v", self.rho_v, (Hkv, self.n_c)),
                                  ("mu_k", self.mu_k, (Hkv, d)), ("mu_v", self.mu_v, (Hkv, d))):
@@ -254,7 +255,7 @@ class QuasarState:
                   self.n_slots[0] if coded else 0, self.n_slots[1] if coded else 0,
                   P(self.levels) if coded else None, self.levels.numel() if coded else 0,
                   P(self.rho_k) if coded else None, P(self.rho_v) if coded else None, self.n_c,
-                  P(self.T_k) if coded else None, P(self.T_v) if coded else None,
+                  P(self.T_k) if coded else None, P(self.T_vt) if coded else None,
                   self.T_k.shape[-1] if coded else 0, self.T_v.shape[-1] if coded else 0,
                   P(self.mu_k) if coded else None, P(self.mu_v) if coded else None,
                   P(self.bounds) if coded else None, self.splits if coded else 0,

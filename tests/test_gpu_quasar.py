@@ -3,7 +3,7 @@
 
 Tolerances (relative to the output's max magnitude): float32 2e-3, bfloat16 1e-2.  Cases: GQA 4
 with one and two query rows, codes at (2, 2, 4), (4, 4) and (8,) bits, coded-token counts around
-the 64-token chunk (1, 63, 64, 65) and long ones, exact rows across several 128-row blocks, appended
+the 64-token chunk (1, 63, 64, 65) and long ones, exact rows in the merge (up to 128) and in 128-row blocks of the split launch (129 .. 1500), appended
 causal rows, no coded tokens, and the state's own kernel check.
 """
 import numpy as np
@@ -36,7 +36,7 @@ def _check(st, p, K_all, V_all, n0, H, q, qpos, stages, tol):
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-3), (torch.bfloat16, 1e-2)])
-@pytest.mark.parametrize("n_c,n0", [(1, 40), (63, 40), (64, 300), (65, 129), (1000, 36), (5000, 700)])
+@pytest.mark.parametrize("n_c,n0", [(1, 40), (63, 40), (64, 300), (65, 129), (1000, 36), (5000, 700), (2000, 1500)])
 def test_quasar_decode_matches_oracle(dtype, tol, n_c, n0):
     st, p, K, V, H, g = _state(2, n_c, n0, 0, (2, 2, 4), dtype, 100 + n_c)
     q = torch.randn((1, 8, 1, 128), generator=g).to(dtype)
