@@ -339,8 +339,8 @@ int kvq_kivi_export(const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_s
  *   order, described by the side's step table, int32 rows [byte offset, n_s, nb, a, w, bits, level
  *   offset] (1883-1898; n_s non-increasing, nb in {4, 8, 16, 32, 64}, at most 128 bytes per token
  *   and side).  levels = the stage codebooks concatenated (float32, at most 256).  rho_k / rho_v
- *   (Hkv, n_c) fp16; T_k (Hkv, d, R_k) float32 (R_k a multiple of 4) and T_v transposed,
- *   (Hkv, R_v, d) float32; mu_k / mu_v (Hkv, d) float32.  bounds (`splits` + 1 int32 chunk boundaries, 64-token chunks), slots (int32 [2][32][8])
+ *   (Hkv, n_c) fp16; T_k (Hkv, d, R_k) float32 and T_v transposed, (Hkv, R_v, d) fp16 (the
+ *   precision the reference stores it at; R_k, R_v multiples of 4); mu_k / mu_v (Hkv, d) float32.  bounds (`splits` + 1 int32 chunk boundaries, 64-token chunks), slots (int32 [2][32][8])
  *   and the slot counts come from kvq_quasar_plan (device copies).  out (1, Tq, Hq, d) of
  *   q_dtype.  rep x Tq <= 8.  phases: mask of 1 (the
  *   query's coefficients), 2 (the split launch), 4 (the row merge, where up to 128 exact rows are
@@ -364,7 +364,7 @@ int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64_t q_st, in
                       const int32_t* slots, int nslots_k,
                       int nslots_v, const float* levels, int n_levels,
                       const uint16_t* rho_k, const uint16_t* rho_v, int64_t n_c, const float* T_k,
-                      const float* T_v, int64_t R_k, int64_t R_v, const float* mu_k, const float* mu_v,
+                      const uint16_t* T_v, int64_t R_k, int64_t R_v, const float* mu_k, const float* mu_v,
                       const int32_t* bounds, int splits, void* out, float* workspace,
                       int64_t workspace_floats, int phases, void* stream);
 

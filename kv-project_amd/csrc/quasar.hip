@@ -7,8 +7,9 @@
 //           bits) of the step's band [a, a + w) at b bits, for the n_s most important coded tokens
 //   table   int32 rows [byte offset of the step's block, n_s, nb, a, w, b, level offset]
 //   levels  float32 stage codebooks, concatenated (one list for both sides)
-// plus rho (Hkv, n_c) fp16 per coded token and side, the read-out matrices T_K (Hkv, d, R) and
-// T_V^T (Hkv, R, d, transposed) and the means mu (Hkv, d), float32 here.  Coded token j of head h contributes
+// plus rho (Hkv, n_c) fp16 per coded token and side, the read-out matrices T_K (Hkv, d, R) float32
+// and T_V^T (Hkv, R, d, transposed) fp16 -- the precision the reference stores them at -- and the
+// means mu (Hkv, d) float32.  Coded token j of head h contributes
 //   logit  (sum over the K steps with n_s > j of qt[band] . level[code]) rho_K[j] + q . mu_K
 //   value  p_j rho_V[j] level[code] into coefficient a + i of each V step it owns,
 // with qt = q T_K; the value coefficients are lifted once per query row: o += acc T_V^T + P mu_V.
@@ -57,7 +58,7 @@ struct QuasarParams {
   float* ws_m;                            // [Hkv][S][R]
   float* ws_l;
   float* ws_o;                            // [Hkv][S][R][128]: the split's lifted output (acc T_V^T + l mu_V)
-  const float* tvt;                       // [Hkv][Rv][128] read-out T_V transposed
+  const uint16_t* tvt;                    // [Hkv][Rv][128] read-out T_V transposed, fp16 (its stored precision)
   const float* muv;                       // [Hkv][128]
   ExactArgs ex;                           // exact rows of the split launch (ex.n rows)
   int S_ex;                               // exact-row workgroups per (h, row)
@@ -230,6 +231,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   __shared__ float lv[kQMaxLevels];
   __shared__ __align__(16) float pch_all[kQWaves][kQChunk * R];
   __shared__ float acc_all[kQWaves][R * kQRowCoef];
+  __shared__ int next_chunk;                                      // the split's next unclaimed chunk
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_coded_wg = p.Hkv * p.S;
@@ -284,6 +286,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   }
   for (int i = tid; i < p.n_levels; i += kQThreads) lv[i] = p.levels[i];
   for (int i = lane; i < R * kQRowCoef; i += 64) accw[i] = 0.0f;
+  if (tid == 0) next_chunk = p.bounds[sidx];
   __syncthreads();
   const int32_t* __restrict__ ks = p.slots;                       // scalar loads: wave-uniform indices
   const int32_t* __restrict__ vs = p.slots + kQSlots * kQSlotInts;
@@ -297,10 +300,16 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     m_run[r] = -INFINITY;
     l_lane[r] = 0.0f;
   }
-  const int c_lo = p.bounds[sidx], c_hi = p.bounds[sidx + 1];
+  const int c_hi = p.bounds[sidx + 1];
   const uint16_t* rk = p.rho_k + static_cast<int64_t>(h) * p.n_c;
   const uint16_t* rvv = p.rho_v + static_cast<int64_t>(h) * p.n_c;
-  for (int ch = c_lo + wave; ch < c_hi; ch += kQWaves) {
+  // chunks are claimed one at a time (their costs differ: early tokens own more steps), so the
+  // wavefronts of the split finish together
+  for (;;) {
+    int ch = 0;
+    if (lane == 0) ch = atomicAdd(&next_chunk, 1);
+    ch = __builtin_amdgcn_readfirstlane(ch);
+    if (ch >= c_hi) break;
     const int j0 = ch * kQChunk;
     const int tok = j0 + lane;
     const bool valid = tok < p.n_c;
@@ -381,7 +390,15 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   float l_w[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) l_w[r] = wave_sum(l_lane[r]);
-  __syncthreads();                                                // every wavefront's pch / accw done
+  __syncthreads();                                                // every wavefront's pch / accw / staging done
+  // the head's T_V^T (fp16, Rv x 128) into the free staging area, one LDS DMA burst
+  {
+    uint8_t* tdst = &stage_all[0][0][0];
+    const uint8_t* tsrc = reinterpret_cast<const uint8_t*>(p.tvt + static_cast<int64_t>(h) * p.Rv * 128);
+    const int pieces = p.Rv * 128 * 2 / 1024;                     // 1 KB per wavefront instruction
+    for (int q = wave; q < pieces; q += kQWaves)
+      __builtin_amdgcn_global_load_lds((qgvoid*)(tsrc + q * 1024 + lane * 16), (qlvoid*)(tdst + q * 1024), 16, 0, 0);
+  }
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -390,7 +407,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     }
   }
   __syncthreads();
-  float* accc = reinterpret_cast<float*>(&stage_all[0][0][0]);   // [R][kQRowCoef] combined coefficients
+  float* accc = mw + 16 * R;                                      // [R][kQRowCoef] combined coefficients (past mw's 10 R)
   for (int i = tid; i < R * p.Rv; i += kQThreads) {
     const int r = i / p.Rv, c = i % p.Rv;
     float M = -INFINITY;
@@ -410,6 +427,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
       mw[2 * kQWaves * R + R + r] = L;
     }
   }
+  __builtin_amdgcn_s_waitcnt(0);                                  // this wavefront's share of T_V^T landed
   __syncthreads();
   const int64_t pr0 = (static_cast<int64_t>(h) * p.S + sidx) * R;
   if (tid < 128) {                                                // thread = output channel
@@ -418,10 +436,10 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     const float mu = p.muv[static_cast<int64_t>(h) * 128 + c];
 #pragma unroll
     for (int r = 0; r < R; ++r) o[r] = mw[2 * kQWaves * R + R + r] * mu;
-    const float* tcol = p.tvt + static_cast<int64_t>(h) * p.Rv * 128 + c;
-#pragma unroll 4
+    const uint16_t* tcol = reinterpret_cast<const uint16_t*>(&stage_all[0][0][0]) + c;
+#pragma unroll 8
     for (int k = 0; k < p.Rv; ++k) {
-      const float t = tcol[static_cast<int64_t>(k) * 128];
+      const float t = f16_to_f32(tcol[k * 128]);
 #pragma unroll
       for (int r = 0; r < R; ++r) o[r] = __builtin_fmaf(accc[r * kQRowCoef + k], t, o[r]);
     }
@@ -542,7 +560,7 @@ extern "C" int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64
                                  const int32_t* slots, int nslots_k,
                                  int nslots_v, const float* levels, int n_levels,
                                  const uint16_t* rho_k, const uint16_t* rho_v, int64_t n_c, const float* T_k,
-                                 const float* T_v, int64_t R_k, int64_t R_v, const float* mu_k, const float* mu_v,
+                                 const uint16_t* T_v, int64_t R_k, int64_t R_v, const float* mu_k, const float* mu_v,
                                  const int32_t* bounds, int splits, void* out, float* workspace,
                                  int64_t workspace_floats, int phases, void* stream) {
   KVQ_REQUIRE(q != nullptr && out != nullptr && workspace != nullptr, "kvq_quasar_decode: null pointer");
@@ -564,7 +582,7 @@ extern "C" int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64
                 "kvq_quasar_decode: null code pointer");
     KVQ_REQUIRE(nslots_k > 0 && nslots_k <= kQSlots && nslots_v > 0 && nslots_v <= kQSlots && splits > 0,
                 "kvq_quasar_decode: slot counts must be in [1, %d], splits > 0", kQSlots);
-    KVQ_REQUIRE(R_k % 4 == 0, "kvq_quasar_decode: R_k must be a multiple of 4");
+    KVQ_REQUIRE(R_k % 4 == 0 && R_v % 4 == 0, "kvq_quasar_decode: R_k, R_v must be multiples of 4");
     KVQ_REQUIRE(k_bytes > 0 && k_bytes < (1LL << 31) && v_bytes > 0 && v_bytes < (1LL << 31),
                 "kvq_quasar_decode: code buffers must hold 1 byte .. 2 GiB");
     KVQ_REQUIRE(R_k > 0 && R_k <= d && R_v > 0 && R_v <= d, "kvq_quasar_decode: R_k, R_v must be in [1, d]");

@@ -159,8 +159,10 @@ class QuasarState:
             f16 = lambda x: torch.as_tensor(x).to(dev, torch.float16).contiguous()
             f32 = lambda x: torch.as_tensor(x).to(dev, torch.float32).contiguous()
             self.rho_k, self.rho_v = f16(packed["rho_k"]), f16(packed["rho_v"])
-            self.T_k, self.T_v = f32(packed["T_k"]), f32(packed["T_v"])
-            self.T_vt = self.T_v.transpose(1, 2).contiguous()         # (Hkv, R_v, d): the lift reads it by channel
+            # T_V is taken at fp16 (its stored precision) by the lift and by the torch path alike
+            self.T_k, self.T_v = f32(packed["T_k"]), f32(torch.as_tensor(packed["T_v"]).to(torch.float16))
+            # (Hkv, R_v, d) fp16: the lift reads it by channel; fp16 is the precision the code stores
+            self.T_vt = torch.as_tensor(packed["T_v"]).to(dev, torch.float16).transpose(1, 2).contiguous()
             self.mu_k, self.mu_v = f32(packed["mu_k"]), f32(packed["mu_v"])
             for nm, t, shape in (("rho_k", self.rho_k, (Hkv, self.n_c)), ("rho_v", self.rho_v, (Hkv, self.n_c)),
                                  ("mu_k", self.mu_k, (Hkv, d)), ("mu_v", self.mu_v, (Hkv, d))):
@@ -168,6 +170,8 @@ class QuasarState:
                     raise ValueError(f"{nm} must be {shape}")
             if self.T_k.shape[:2] != (Hkv, d) or self.T_v.shape[:2] != (Hkv, d):
                 raise ValueError("T_k, T_v must be (Hkv, d, R)")
+            if self.T_k.shape[-1] % 4 or self.T_v.shape[-1] % 4:
+                raise ValueError("the read-out matrices' R must be a multiple of 4")
             for side, T in ((0, self.T_k), (1, self.T_v)):
                 tab = self.sides[side]["table_np"]
                 if int((tab[:, 3] + tab[:, 4]).max()) > T.shape[-1]:
