@@ -16,6 +16,7 @@ The other rows of the path are measured by the same script with ``--workload``:
   quant   prefill quantise + pack of the C2 context (kivi_quant of K and V)
   quasar  QUASAR compressed-domain decode (embedded spectral code, 64k context, batch 1)
   micro   the reference's decode-attention microbenchmark: SDPA (full, evicting) vs the packed kernels
+  alloc   STRATA rate allocation of one layer (compression side: order, head sum, Lagrangian search)
 Each prints one JSON line of the same form (its own metric, roofline and CPU baseline).
 
 Timing: W untimed warm-up steps, then K steps launched back to back between HIP events on the
@@ -852,9 +853,56 @@ def run_quant(args) -> dict:
     return res
 
 
+# ---------------------------------------------------------------------------------------------
+# F1: STRATA rate allocation of one layer (compression side)
+
+def run_alloc(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    Hkv, d, H, bits, keep = 8, 128, 32768, (2, 4, 8), 0.125
+    rs, re = 4, H - 32
+    n, nlev = re - rs, len(bits) + 2
+    rng = np.random.default_rng(42)
+    imp = np.exp(rng.normal(0, 2.0, (Hkv, n, 1)))
+    cols = [imp * rng.uniform(0.5, 2.0, (Hkv, n, 1))]
+    cols += [imp * 4.0 ** (-2 * l) * rng.uniform(0.5, 2.0, (Hkv, n, 1)) for l in range(1, nlev - 1)]
+    D = np.concatenate(cols + [np.zeros((Hkv, n, 1))], -1).astype(np.float32)
+    Dg = torch.from_numpy(D).cuda()
+    cost, fixed, budget, hist, _ = kvq.layer_costs(bits, d, Hkv, H, keep, rs, re)
+    ws = kvq.AllocWorkspace(Hkv, n, nlev, Dg.device)
+    step = lambda: kvq.strata_allocate(Dg, cost, fixed, budget, 4, True, ws)
+    ms = eager_ms(step, args.steps, args.warmup)
+    bytes_alg = D.nbytes + 4 * Hkv * n + 4 * n * nlev + 2 * 4 * n
+    al = kvq.allocate_layer(Dg, bits, d, H, keep, rs, re, workspace=ws)
+    res = _result(args, metric="STRATA rate allocation: µs/layer (order, head sum, Lagrangian search, histogram)",
+                  value=ms * 1e3, unit="us", ms_per_step=ms, hib=False,
+                  workload=f"F1: the allocation steps of StrataMethod.compress_layer for one Llama-3-8B-shaped layer: "
+                           f"Hkv=8, {H}-token context, {n} coded candidates, options drop / 2 / 4 / 8 bits / exact, "
+                           f"keep {keep}, 4 rounds of 32 multipliers; synthetic distortion table",
+                  config={"global_batch": 1, "seq_len": H, "parallelism": "single GPU", "n": n, "nlev": nlev,
+                          "keep": keep, "rounds": 4},
+                  dtype="f64", roofline=_roof(bytes_alg, ms, "kvq_strata_allocate (whole call, ~30 launches)"),
+                  bytes_alg=bytes_alg, counts=al["counts"], bits=al["bits"], budget=budget,
+                  distortion=round(al["distortion"], 6))
+    log(f"allocation {ms * 1e3:.1f} us, counts {al['counts']}")
+    if not args.no_cpu_baseline:
+        import oracle.strata_alloc as oa
+        times = []
+        while sum(times) < args.cpu_seconds or len(times) < 2:
+            t0 = time.perf_counter()
+            oa.allocate(D, cost, fixed, budget, rounds=4)
+            times.append(time.perf_counter() - t0)
+        t = float(np.median(times))
+        res["cpu_baseline"] = {"value": t * 1e6, "unit": "us", "cores": _threads(), "kind": "port",
+                               "sample": f"the whole allocation, {len(times)} runs, median; numpy restatement "
+                                         "(stable argsort, float32 head sum, float64 search)"}
+    return res
+
+
 WORKLOADS = {"c2": lambda a: run_kivi(a, "c2"), "c1": lambda a: run_kivi(a, "c1"), "c3": run_c3, "c4": run_c4,
              "c5": run_c5, "strata": run_strata, "append": run_append, "quant": run_quant, "quasar": run_quasar,
-             "micro": run_micro}
+             "micro": run_micro, "alloc": run_alloc}
 
 
 def main() -> int:

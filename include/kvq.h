@@ -369,6 +369,29 @@ int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64_t q_st, in
                       int64_t workspace_floats, int phases, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * F1  STRATA rate allocation of one layer (the compression side): replaces the allocation steps
+ * of StrataMethod.compress_layer (STRATA_KV.py:1559-1581) -- nan_to_num of D, the per-head
+ * importance order (1560), the head-summed table Dsort (1561), head_sync_allocate (1307-1351,
+ * called at 1569), lev = choice sorted descending and its histogram (1570-1571), the distortion
+ * ratio (1577-1581).
+ *   D (Hkv, n, nlev) float32, columns [drop | level 1 .. level nlev-2 | exact]; cost (nlev) and
+ *   fixed (nlev - 1) float64 HOST arrays (option bits summed over heads; fixed bits per cap);
+ *   budget in bits; rounds of 32 multipliers (the reference's STRATA_ROUNDS), or rounds < 0 for
+ *   the all-drop allocation (the reference's branch when the budget cannot pay the histogram).
+ * Outputs (device): order (Hkv, n) int32, dsort (n, nlev) float32, choice (n) int32, lev (n)
+ * int32, counts (nlev) int32, summary [bits, cap, distortion] float64.  The search runs in
+ * float64 (products rounded before sums; drop wins ties against exact, the running minimum over
+ * levels takes the later level, the cap is the first of minimal total); ties of the importance
+ * key go to the lower token index.  workspace: 256-byte aligned, >= kvq_strata_allocate_workspace(...)
+ *  bytes (-1: bad shape).  Hkv < 256, Hkv n < 2^31, 2 <= nlev <= 16.
+ * ---------------------------------------------------------------------------------------- */
+int64_t kvq_strata_allocate_workspace(int64_t Hkv, int64_t n, int nlev);
+int kvq_strata_allocate(const float* D, int64_t Hkv, int64_t n, int nlev, const double* cost,
+                        const double* fixed, double budget, int rounds, int32_t* order, float* dsort,
+                        int32_t* choice, int32_t* lev, int32_t* counts, double* summary,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Self-test of the matrix-core operand layout the decode kernel is written against
  * (v_mfma_f32_16x16x32_f16 on gfx950): writes, for A = I-pattern inputs, the 16x16 product
  * as each lane sees it, followed by the lane each lane reads under row_shr:4 and row_ror:4 and
