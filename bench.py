@@ -885,7 +885,19 @@ def run_alloc(args) -> dict:
                   dtype="f64", roofline=_roof(bytes_alg, ms, "kvq_strata_allocate (whole call, ~30 launches)"),
                   bytes_alg=bytes_alg, counts=al["counts"], bits=al["bits"], budget=budget,
                   distortion=round(al["distortion"], 6))
-    log(f"allocation {ms * 1e3:.1f} us, counts {al['counts']}")
+    # the distortion table the allocation reads (rotation, per-width errors e^T Mt e, D), same layer
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    Kc = torch.randn((Hkv, n, d), generator=g, device="cuda").to(torch.bfloat16)
+    Vc = torch.randn((Hkv, n, d), generator=g, device="cuda").to(torch.bfloat16)
+    Gm = torch.randn((2, Hkv, d, d), generator=g, device="cuda")
+    Sm, Mm = (Gm[0] @ Gm[0].transpose(1, 2) / d).contiguous(), (Gm[1] @ Gm[1].transpose(1, 2) / d).contiguous()
+    Am, Wm, DDm = torch.rand((3, Hkv, n), generator=g, device="cuda")
+    dist = lambda: kvq.strata_distortion(Kc, Vc, Am, Wm, DDm, Sm, Mm, bits)
+    d_ms = eager_ms(dist, max(5, args.steps // 5), 3)
+    res["distortion_table_us"] = round(d_ms * 1e3, 3)
+    res["distortion_table_tflops"] = round(2 * Hkv * n * len(bits) * 2 * d * d / (d_ms * 1e-3) / 1e12, 2)
+    log(f"allocation {ms * 1e3:.1f} us, counts {al['counts']}; distortion table {d_ms * 1e3:.1f} us")
     if not args.no_cpu_baseline:
         import oracle.strata_alloc as oa
         times = []

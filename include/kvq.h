@@ -385,6 +385,20 @@ int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64_t q_st, in
  * key go to the lower token index.  workspace: 256-byte aligned, >= kvq_strata_allocate_workspace(...)
  *  bytes (-1: bad shape).  Hkv < 256, Hkv n < 2^31, 2 <= nlev <= 16.
  * ---------------------------------------------------------------------------------------- */
+/* The distortion table the allocation reads, from the coverage statistics: replaces
+ * compress_layer's metrics in the code basis (STRATA_KV.py:1543, R S R^T and R Mbar R^T), the
+ * error term of each width on both sides (1546-1553: e = y_hat - y of strata_quantize, e^T Mt e)
+ * and the table D = [DD | A errK_b + W errV_b per width | 0] (1555-1557).  yk / yv (Hkv, n, 128)
+ * float32 are the centred, rotated coded rows (kvq_strata_center_rotate); S, Mbar (Hkv, 128, 128)
+ * float32 in the original basis; signs the rotation signs; A, W, DD (Hkv, n) float32; bits /
+ * steps (host, nbits <= 3 widths in {2, 4, 8} and their uniform_step); D (Hkv, n, nbits + 2)
+ * float32 out.  workspace >= kvq_strata_distortion_workspace(...) bytes (-1: bad sizes). */
+int64_t kvq_strata_distortion_workspace(int64_t Hkv, int64_t n, int nbits);
+int kvq_strata_distortion(const float* yk, const float* yv, int64_t Hkv, int64_t n, int64_t d, const float* S,
+                          const float* Mbar, const float* signs, const float* A, const float* W,
+                          const float* DD, int nbits, const int* bits, const float* steps, float* D,
+                          float* workspace, int64_t workspace_bytes, void* stream);
+
 int64_t kvq_strata_allocate_workspace(int64_t Hkv, int64_t n, int nlev);
 int kvq_strata_allocate(const float* D, int64_t Hkv, int64_t n, int nlev, const double* cost,
                         const double* fixed, double budget, int rounds, int32_t* order, float* dsort,

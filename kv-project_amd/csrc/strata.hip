@@ -11,6 +11,8 @@
 //         h = 1, 2, ..., d/2 (pairs (a, b) -> (a + b, a - b)), then * float32(1 / sqrt(d));
 //   s:    rms = sqrt(float32(float64 sum of y^2 / d)); s = max(fp16(float32(step) * rms), 2^-24);
 //   code: clamp(rint(y / s + (2^b - 1) / 2), 0, 2^b - 1) with IEEE float32 division and add.
+#include <algorithm>
+
 #include "common.hpp"
 #include "mfma_common.hpp"
 #include "widths.hpp"
@@ -72,6 +74,34 @@ __global__ __launch_bounds__(1024) void strata_mean_kernel(const void* __restric
     for (int k = 0; k < 8; ++k) s += part[k][c];
     mu[static_cast<int64_t>(blockIdx.x) * kSD + c] = f32_to_f16(as_stored16(static_cast<float>(s / static_cast<double>(n))));
   }
+}
+
+// Long contexts: the same sums split over P token chunks (grid (BH, P), 8 strides per chunk in
+// float64), the per-chunk partials then combined in chunk order by strata_mean_combine_kernel.
+template <int DT>
+__global__ __launch_bounds__(1024) void strata_mean_part_kernel(const void* __restrict__ x, int64_t n, int64_t x_bh,
+                                                                int64_t chunk, double* __restrict__ part) {
+  __shared__ double red[8][kSD];
+  const int c = threadIdx.x % kSD, j = threadIdx.x / kSD;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * x_bh;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * chunk, t1 = min(n, t0 + chunk);
+  double acc = 0.0;
+  for (int64_t t = t0 + j; t < t1; t += 8) acc += static_cast<double>(load_as_f32<DT>(x, base + t * kSD + c));
+  red[j][c] = acc;
+  __syncthreads();
+  if (j == 0) {
+    double sum = 0.0;
+    for (int k = 0; k < 8; ++k) sum += red[k][c];
+    part[(static_cast<int64_t>(blockIdx.x) * gridDim.y + blockIdx.y) * kSD + c] = sum;
+  }
+}
+
+__global__ __launch_bounds__(kSD) void strata_mean_combine_kernel(const double* __restrict__ part, int P, int64_t n,
+                                                                  uint16_t* __restrict__ mu) {
+  const int c = threadIdx.x;
+  double sum = 0.0;
+  for (int p = 0; p < P; ++p) sum += part[(static_cast<int64_t>(blockIdx.x) * P + p) * kSD + c];
+  mu[static_cast<int64_t>(blockIdx.x) * kSD + c] = f32_to_f16(as_stored16(static_cast<float>(sum / static_cast<double>(n))));
 }
 
 // In-wave FWHT of a 128-vector held as (v0 = x[lane], v1 = x[lane + 64]), stages h = 1 .. 64.
@@ -187,6 +217,127 @@ int blocks_for(int64_t items, int per) { return static_cast<int>((items + per - 
 
 using namespace kvq;
 
+// ---- distortion table of the compression side (STRATA_KV.py:1543-1559) ----
+// Metric in the code basis, written transposed: out[h] = (R (R S[h]^T)^T ... ) computed as
+// rot(rows of (rot(rows of S))^T) = R S^T R^T, whose quadratic form equals that of R S R^T.
+// One block per matrix; both passes through LDS.
+__global__ __launch_bounds__(256) void strata_metric_kernel(const float* __restrict__ S, const float* __restrict__ signs,
+                                                            float* __restrict__ out) {
+  __shared__ float a[kSD][kSD + 1];
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const float* src = S + static_cast<int64_t>(blockIdx.x) * kSD * kSD;
+  const float inv = 0.08838834764831845f;         // float32(1 / sqrt(128))
+  for (int pass = 0; pass < 2; ++pass) {
+    float r0[kSD / 4], r1[kSD / 4];
+    for (int i = wave, u = 0; i < kSD; i += 4, ++u) {           // rows of the current matrix, rotated
+      float v0 = pass == 0 ? src[i * kSD + lane] : a[i][lane];
+      float v1 = pass == 0 ? src[i * kSD + lane + 64] : a[i][lane + 64];
+      v0 = __fmul_rn(v0, signs[lane]);
+      v1 = __fmul_rn(v1, signs[lane + 64]);
+      fwht128(v0, v1, lane);
+      r0[u] = __fmul_rn(v0, inv);
+      r1[u] = __fmul_rn(v1, inv);
+    }
+    __syncthreads();
+    for (int i = wave, u = 0; i < kSD; i += 4, ++u) {
+      if (pass == 0) {                                            // transposed for the second pass
+        a[lane][i] = r0[u];
+        a[lane + 64][i] = r1[u];
+      } else {
+        out[static_cast<int64_t>(blockIdx.x) * kSD * kSD + i * kSD + lane] = r0[u];
+        out[static_cast<int64_t>(blockIdx.x) * kSD * kSD + i * kSD + lane + 64] = r1[u];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// err[bh][t][b] = e^T M e with e = y_hat - y of token t quantised at width bits[b] (the codes of
+// strata_quantize_kernel), M = Mt[bh] read as columns (M^T e gives the same form).  A block holds
+// one bh and kSErrTok tokens, one wavefront per token at a time; M staged in LDS once.
+constexpr int kSErrTok = 256;
+constexpr int kSMaxBits = 3;
+
+struct ErrWidths {
+  int n;
+  int bits[kSMaxBits];
+  float step[kSMaxBits];
+};
+
+__global__ __launch_bounds__(256) void strata_err_kernel(const float* __restrict__ y, int64_t n,
+                                                         const float* __restrict__ Mt, ErrWidths w,
+                                                         float* __restrict__ err) {
+  __shared__ float M[kSD * kSD];
+  __shared__ float e_l[4][kSMaxBits][kSD];
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const int64_t bh = blockIdx.y;
+  const float* mg = Mt + bh * kSD * kSD;
+  for (int i = threadIdx.x; i < kSD * kSD; i += 256) M[i] = mg[i];
+  __syncthreads();
+  const int64_t t_end = min<int64_t>(n, static_cast<int64_t>(blockIdx.x + 1) * kSErrTok);
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * kSErrTok + wave; t < t_end; t += 4) {
+    const float* row = y + (bh * n + t) * kSD;
+    const float y0 = row[lane], y1 = row[lane + 64];
+    double ss = static_cast<double>(y0) * y0 + static_cast<double>(y1) * y1;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float rms = __fsqrt_rn(static_cast<float>(ss / kSD));
+    float e0[kSMaxBits], e1[kSMaxBits], m0[kSMaxBits], m1[kSMaxBits];
+#pragma unroll
+    for (int b = 0; b < kSMaxBits; ++b) {
+      e0[b] = e1[b] = m0[b] = m1[b] = 0.0f;
+      if (b >= w.n) continue;
+      const int bits = w.bits[b];
+      const float sc = fmaxf(as_stored16(__fmul_rn(w.step[b], rms)), kMinScale);
+      const float half = static_cast<float>((1 << bits) - 1) * 0.5f;
+      const float qmax = static_cast<float>((1 << bits) - 1);
+      const float c0 = fminf(fmaxf(rintf(__fadd_rn(__fdiv_rn(y0, sc), half)), 0.0f), qmax);
+      const float c1 = fminf(fmaxf(rintf(__fadd_rn(__fdiv_rn(y1, sc), half)), 0.0f), qmax);
+      e0[b] = __fsub_rn(__fmul_rn(__fsub_rn(c0, half), sc), y0);
+      e1[b] = __fsub_rn(__fmul_rn(__fsub_rn(c1, half), sc), y1);
+      e_l[wave][b][lane] = e0[b];
+      e_l[wave][b][lane + 64] = e1[b];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll 4
+    for (int j = 0; j < kSD; ++j) {                               // (M^T e)_lane, (M^T e)_lane+64
+      const float a0 = M[j * kSD + lane], a1 = M[j * kSD + lane + 64];
+#pragma unroll
+      for (int b = 0; b < kSMaxBits; ++b) {
+        const float ej = e_l[wave][b][j];
+        m0[b] = __builtin_fmaf(a0, ej, m0[b]);
+        m1[b] = __builtin_fmaf(a1, ej, m1[b]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kSMaxBits; ++b) {
+      float q = __builtin_fmaf(e0[b], m0[b], e1[b] * m1[b]);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+      if (lane == 0 && b < w.n) err[(bh * n + t) * w.n + b] = q;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();                              // e_l of this token consumed
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+}
+
+// D[h][t] = [DD, A errK_b + W errV_b for each width, 0] (float32, products rounded before the sum)
+__global__ __launch_bounds__(256) void strata_dtable_kernel(const float* __restrict__ ek, const float* __restrict__ ev,
+                                                            const float* __restrict__ A, const float* __restrict__ W,
+                                                            const float* __restrict__ DD, int nb, int64_t total,
+                                                            float* __restrict__ D) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    float* row = D + i * (nb + 2);
+    row[0] = DD[i];
+    for (int b = 0; b < nb; ++b) row[1 + b] = __fadd_rn(__fmul_rn(A[i], ek[i * nb + b]), __fmul_rn(W[i], ev[i * nb + b]));
+    row[nb + 1] = 0.0f;
+  }
+}
+
 extern "C" int kvq_pack_planar(const uint8_t* codes, int64_t rows, int64_t d, int bits, uint8_t* out, void* stream) {
   KVQ_REQUIRE(bits == 2 || bits == 4 || bits == 8, "kvq_pack_planar: bits must be 2, 4 or 8");
   KVQ_REQUIRE(rows >= 0 && d > 0 && d % (8 / bits) == 0, "kvq_pack_planar: d must be a multiple of 8/bits");
@@ -220,8 +371,21 @@ extern "C" int kvq_strata_center_rotate(const void* x, int x_dtype, int64_t BH, 
   KVQ_REQUIRE(x && signs && mu && y, "kvq_strata_center_rotate: null pointer");
   KVQ_REQUIRE(BH < (1LL << 31) && BH * n / 4 < (1LL << 31), "kvq_strata_center_rotate: too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  KVQ_DISPATCH_DTYPE(x_dtype, hipLaunchKernelGGL((strata_mean_kernel<DT_>), dim3(static_cast<unsigned>(BH)),
-                                                dim3(1024), 0, s, x, n, x_bh, mu));
+  if (n >= 1024) {
+    // P chunks of >= 256 tokens; their float64 partials (BH P 128 doubles <= BH n 128 floats) sit
+    // in y until the rotation overwrites it
+    const int64_t P = std::min<int64_t>(64, n / 256);
+    const int64_t chunk = (n + P - 1) / P;
+    double* part = reinterpret_cast<double*>(y);
+    KVQ_DISPATCH_DTYPE(x_dtype, hipLaunchKernelGGL((strata_mean_part_kernel<DT_>),
+                                                  dim3(static_cast<unsigned>(BH), static_cast<unsigned>(P)), dim3(1024),
+                                                  0, s, x, n, x_bh, chunk, part));
+    hipLaunchKernelGGL(strata_mean_combine_kernel, dim3(static_cast<unsigned>(BH)), dim3(kSD), 0, s, part,
+                       static_cast<int>(P), n, mu);
+  } else {
+    KVQ_DISPATCH_DTYPE(x_dtype, hipLaunchKernelGGL((strata_mean_kernel<DT_>), dim3(static_cast<unsigned>(BH)),
+                                                  dim3(1024), 0, s, x, n, x_bh, mu));
+  }
   KVQ_LAUNCH_CHECK("kvq_strata_center_rotate(mean)");
   KVQ_DISPATCH_DTYPE(x_dtype, hipLaunchKernelGGL((strata_rotate_kernel<DT_>), dim3(blocks_for(BH * n, 4)), dim3(256),
                                                 0, s, x, n, x_bh, mu, signs, y, BH * n));
@@ -870,5 +1034,45 @@ extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64
 #undef KVQ_STRATA_MR
 #undef KVQ_STRATA_MERGE
   KVQ_LAUNCH_CHECK("kvq_strata_decode(merge)");
+  return KVQ_OK;
+}
+
+extern "C" int64_t kvq_strata_distortion_workspace(int64_t Hkv, int64_t n, int nbits) {
+  if (Hkv <= 0 || n <= 0 || nbits < 1 || nbits > kSMaxBits) return -1;
+  return 4 * (2 * Hkv * kSD * kSD + 2 * Hkv * n * nbits);
+}
+
+extern "C" int kvq_strata_distortion(const float* yk, const float* yv, int64_t Hkv, int64_t n, int64_t d,
+                                     const float* S, const float* Mbar, const float* signs, const float* A,
+                                     const float* W, const float* DD, int nbits, const int* bits, const float* steps,
+                                     float* D, float* workspace, int64_t workspace_bytes, void* stream) {
+  KVQ_REQUIRE(d == kSD, "kvq_strata_distortion: head_dim must be 128");
+  KVQ_REQUIRE(Hkv > 0 && n > 0 && Hkv < 65536 && Hkv * n < (1LL << 31), "kvq_strata_distortion: bad sizes");
+  KVQ_REQUIRE(nbits >= 1 && nbits <= kSMaxBits && bits && steps, "kvq_strata_distortion: 1 to %d widths", kSMaxBits);
+  KVQ_REQUIRE(yk && yv && S && Mbar && signs && A && W && DD && D && workspace, "kvq_strata_distortion: null pointer");
+  KVQ_REQUIRE(workspace_bytes >= kvq_strata_distortion_workspace(Hkv, n, nbits),
+              "kvq_strata_distortion: workspace too small");
+  ErrWidths w{};
+  w.n = nbits;
+  for (int b = 0; b < nbits; ++b) {
+    KVQ_REQUIRE(bits[b] == 2 || bits[b] == 4 || bits[b] == 8, "kvq_strata_distortion: widths must be 2, 4 or 8");
+    KVQ_REQUIRE(steps[b] > 0.0f, "kvq_strata_distortion: steps must be positive");
+    w.bits[b] = bits[b];
+    w.step[b] = steps[b];
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* mk = workspace;
+  float* mv = mk + Hkv * kSD * kSD;
+  float* ek = mv + Hkv * kSD * kSD;
+  float* ev = ek + Hkv * n * nbits;
+  hipLaunchKernelGGL(strata_metric_kernel, dim3(static_cast<unsigned>(Hkv)), dim3(256), 0, st, S, signs, mk);
+  hipLaunchKernelGGL(strata_metric_kernel, dim3(static_cast<unsigned>(Hkv)), dim3(256), 0, st, Mbar, signs, mv);
+  const dim3 eg(static_cast<unsigned>((n + kSErrTok - 1) / kSErrTok), static_cast<unsigned>(Hkv));
+  hipLaunchKernelGGL(strata_err_kernel, eg, dim3(256), 0, st, yk, n, mk, w, ek);
+  hipLaunchKernelGGL(strata_err_kernel, eg, dim3(256), 0, st, yv, n, mv, w, ev);
+  const int64_t total = Hkv * n;
+  hipLaunchKernelGGL(strata_dtable_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 4096))),
+                     dim3(256), 0, st, ek, ev, A, W, DD, nbits, total, D);
+  KVQ_LAUNCH_CHECK("kvq_strata_distortion");
   return KVQ_OK;
 }

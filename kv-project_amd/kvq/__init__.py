@@ -15,7 +15,7 @@ from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strat
 from .dct import DctCache, dct_decode, dct_encode, dct_table, dct_workspace_floats
 from .mixed import MixedKIVICache, c3_widths, mixed_decode, mixed_workspace_floats, offset_table
 from .quasar import QuasarState, stage_codebooks
-from .alloc import AllocWorkspace, allocate_layer, layer_costs, strata_allocate
+from .alloc import AllocWorkspace, allocate_layer, layer_costs, strata_allocate, strata_distortion
 
 __all__ = [
     "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes", "pack_rows", "unpack_rows",
@@ -26,5 +26,5 @@ __all__ = [
     "strata_decode", "strata_workspace_floats", "DctCache", "dct_decode", "dct_encode", "dct_table",
     "dct_workspace_floats", "MixedKIVICache", "c3_widths", "mixed_decode", "mixed_workspace_floats", "offset_table",
     "QuasarState", "stage_codebooks", "payload_bytes", "AllocWorkspace", "allocate_layer", "layer_costs",
-    "strata_allocate",
+    "strata_allocate", "strata_distortion",
 ]

@@ -63,6 +63,8 @@ SIGNATURES = {
     "kvq_kivi_payload_bytes": (i64, [i64, i64, i64, i32, i32, i64, i32]),
     "kvq_kivi_export": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i32, i32, vp, vp, i32, i64, i64, i64, vp, i64, vp]),
     "kvq_quasar_plan": (i32, [vp, i32, vp, i32, i64, i64, i32, vp, vp, vp, vp]),
+    "kvq_strata_distortion_workspace": (i64, [i64, i64, i32]),
+    "kvq_strata_distortion": (i32, [vp, vp, i64, i64, i64, vp, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp, i64, vp]),
     "kvq_strata_allocate_workspace": (i64, [i64, i64, i32]),
     "kvq_strata_allocate": (i32, [vp, i64, i64, i32, vp, vp, C.c_double, i32, vp, vp, vp, vp, vp, vp, vp, i64, vp]),
     "kvq_quasar_decode_workspace": (i64, [i64, i64, i64, i64, i64, i64, i32]),

@@ -77,6 +77,40 @@ def strata_allocate(D: torch.Tensor, cost, fixed, budget: float, rounds: int = 4
 
 
 @torch.no_grad()
+def strata_distortion(K: torch.Tensor, V: torch.Tensor, A: torch.Tensor, W: torch.Tensor, DD: torch.Tensor,
+                      S: torch.Tensor, Mbar: torch.Tensor, bits) -> dict:
+    """The distortion table of compress_layer (STRATA_KV.py:1541-1559) from the coverage statistics:
+    K, V (Hkv, n, 128) the coded rows [rs, re) of one layer (any float dtype); A, W, DD (Hkv, n) and
+    S, Mbar (Hkv, 128, 128) float32 as ``coverage_stats`` returns them.  Returns D (Hkv, n,
+    len(bits) + 2) float32 [drop | widths | exact] and the centred, rotated rows (mu_k, y_k, mu_v,
+    y_v) the code is then cut from (``kvq.strata_quantize`` with the allocation's order)."""
+    from .strata import rotation_signs, strata_center_rotate, uniform_step
+    _lib.require_gpu(K, V, A, W, DD, S, Mbar)
+    Hkv, n, d = K.shape
+    if V.shape != K.shape or d != 128:
+        raise ValueError("K, V must be (Hkv, n, 128)")
+    for nm, t, shape in (("A", A, (Hkv, n)), ("W", W, (Hkv, n)), ("DD", DD, (Hkv, n)), ("S", S, (Hkv, d, d)),
+                         ("Mbar", Mbar, (Hkv, d, d))):
+        if t.dtype != torch.float32 or tuple(t.shape) != shape:
+            raise ValueError(f"{nm} must be float32 {shape}")
+    signs = rotation_signs(d, device=K.device)
+    mu_k, yk = strata_center_rotate(K[None], signs)
+    mu_v, yv = strata_center_rotate(V[None], signs)
+    nb = len(bits)
+    D = torch.empty((Hkv, n, nb + 2), dtype=torch.float32, device=K.device)
+    ws = torch.empty(int(_lib.load().kvq_strata_distortion_workspace(Hkv, n, nb)) // 4 + 1, dtype=torch.float32,
+                     device=K.device)
+    b_arr = (C.c_int * nb)(*bits)
+    s_arr = (C.c_float * nb)(*[uniform_step(b) for b in bits])
+    c = lambda t: t.contiguous()
+    S_, M_, A_, W_, DD_ = c(S), c(Mbar), c(A), c(W), c(DD)
+    _lib.call("kvq_strata_distortion", yk.data_ptr(), yv.data_ptr(), Hkv, n, d, S_.data_ptr(), M_.data_ptr(),
+              signs.data_ptr(), A_.data_ptr(), W_.data_ptr(), DD_.data_ptr(), nb, b_arr, s_arr, D.data_ptr(),
+              ws.data_ptr(), ws.numel() * 4, _lib.stream_of(K))
+    return {"D": D, "mu_k": mu_k[0], "y_k": yk[0], "mu_v": mu_v[0], "y_v": yv[0]}
+
+
+@torch.no_grad()
 def allocate_layer(D: torch.Tensor, bits, d: int, H: int, keep: float, rs: int, re: int, rounds: int = 4,
                    workspace: AllocWorkspace | None = None) -> dict:
     """The allocation part of compress_layer (STRATA_KV.py:1559-1581) for a layer whose table D

@@ -25,6 +25,9 @@ Arithmetic fixed here (the GPU kernels compute the same, so both agree bit for b
     float32, so its choices agree except where two options' costs differ by less than float32
     rounding.
 
+``distortion_table`` (1543-1559) is pinned by the identity e^T (R S R^T) e = (x_hat - x)^T S
+(x_hat - x) for the reconstruction x_hat = mu + y_hat R (1597-1609), checked in the original basis.
+
 Pinning (tests/test_oracle_alloc.py): Everett's theorem by brute force on tiny inputs (no
 allocation using at most the returned bits has a smaller distortion), the reference's own
 allocator checks (1945-1961: feasible, distortion non-increasing in the budget, all exact when
@@ -146,3 +149,21 @@ def layer_costs(bits, d: int, Hkv: int, H: int, keep: float, rs: int, re: int):
     fixed = np.where(np.arange(nb + 1) > 0, Hkv * 2 * d * 16.0, 0.0) + hist_bits
     budget = keep * H * Hkv * 2 * d * 16.0 - (rs + (H - re)) * Hkv * 2 * d * 16.0
     return cost_tok * Hkv, fixed, float(budget), hist_bits, cost_tok
+
+
+def distortion_table(Yk, Yv, S, Mbar, A, W, DD, bits, key: str = "strata"):
+    """D (Hkv, n, nb + 2) float64 = [DD | A e_K^T Mt_K e_K + W e_V^T Mt_V e_V per width | 0] with
+    Mt = R S R^T, R Mbar R^T and e = y_hat - y of strata_quantize (STRATA_KV.py:1543-1559)."""
+    from oracle.strata import rotation_matrix, strata_quantize, uniform_step
+    d = Yk.shape[-1]
+    R = rotation_matrix(d, key).astype(np.float64)
+    cols = [np.asarray(DD, np.float64)]
+    for b in bits:
+        errs = []
+        for Y, M in ((Yk, S), (Yv, Mbar)):
+            Mt = R @ np.asarray(M, np.float64) @ R.T
+            e = strata_quantize(Y, b, uniform_step(b)[0])[2].astype(np.float64) - np.asarray(Y, np.float64)
+            errs.append(np.einsum("hnd,hde,hne->hn", e, Mt, e))
+        cols.append(np.asarray(A, np.float64) * errs[0] + np.asarray(W, np.float64) * errs[1])
+    cols.append(np.zeros_like(cols[0]))
+    return np.stack(cols, -1)

@@ -120,3 +120,31 @@ def test_rejects_bad_arguments():
         kvq.strata_allocate(D, np.zeros(17), np.zeros(16), 1e6)
     with pytest.raises(ValueError):
         kvq.strata_allocate(torch.zeros((2, 10, 5), device="cuda"), np.zeros(4), np.zeros(4), 1e6)
+
+
+@pytest.mark.parametrize("Hkv,n,dtype", [(2, 3, torch.float32), (4, 700, torch.bfloat16), (8, 4093, torch.float32)])
+def test_distortion_matches_oracle_and_feeds_allocation(Hkv, n, dtype):
+    import kvq
+    import oracle.strata as os_
+    g = torch.Generator().manual_seed(n)
+    K = (torch.randn((Hkv, n, 128), generator=g) * 2 + 0.5).to(dtype)
+    V = torch.randn((Hkv, n, 128), generator=g).to(dtype)
+    G = torch.randn((2, Hkv, 128, 128), generator=g)
+    S, Mbar = (G[0] @ G[0].transpose(1, 2) / 128).contiguous(), (G[1] @ G[1].transpose(1, 2) / 128).contiguous()
+    A, W, DD = torch.rand((3, Hkv, n), generator=g)
+    bits = (2, 4, 8)
+    out = kvq.strata_distortion(K.cuda(), V.cuda(), A.cuda(), W.cuda(), DD.cuda(), S.cuda(), Mbar.cuda(), bits)
+    signs = os_.rotation_signs(128)
+    (_, Yk), (_, Yv) = os_.strata_center_rotate(K.float().numpy(), signs), os_.strata_center_rotate(V.float().numpy(), signs)
+    np.testing.assert_array_equal(out["y_k"].cpu().numpy(), Yk)                 # the codec is bit-exact
+    want = oa.distortion_table(Yk, Yv, S.numpy(), Mbar.numpy(), A.numpy(), W.numpy(), DD.numpy(), bits)
+    got = out["D"].cpu().numpy()
+    # fp32 quadratic forms (128-term sums): within 2e-3 of each width column's largest value
+    scale = np.abs(want).max(axis=(0, 1), keepdims=True)
+    assert (np.abs(got - want) <= 2e-3 * scale).all(), float((np.abs(got - want) / np.maximum(scale, 1e-30)).max())
+    H = n + 36
+    al = kvq.allocate_layer(out["D"], bits, 128, H, 0.3, 4, H - 32)
+    cost, fixed, budget, hist, _ = oa.layer_costs(bits, 128, Hkv, H, 0.3, 4, H - 32)
+    ref = oa.allocate(got, cost, fixed, budget, search=budget >= hist)
+    np.testing.assert_array_equal(al["lev"].cpu().numpy(), ref["lev"])
+    np.testing.assert_array_equal(al["order"].cpu().numpy(), ref["order"])

@@ -119,3 +119,35 @@ def test_sanitize_and_all_drop():
     assert budget < hist
     out = oa.allocate(np.ones((2, 32, 5), np.float32), cost, fixed, budget, search=False)
     assert (out["choice"] == 0).all() and out["counts"].tolist() == [32, 0, 0, 0, 0]
+
+
+def test_distortion_table_equals_reconstruction_error():
+    """e^T (R S R^T) e in the code basis == (x_hat - x)^T S (x_hat - x) for x_hat = mu + y_hat R
+    (the reader's reconstruction, STRATA_KV.py:1597-1609); a transposed rotation breaks it."""
+    import oracle.strata as os_
+    rng = np.random.default_rng(9)
+    Hkv, n, d, bits = 2, 40, 128, (2, 4, 8)
+    Xk = rng.normal(size=(Hkv, n, d)).astype(np.float32)
+    Xv = rng.normal(size=(Hkv, n, d)).astype(np.float32)
+    G = rng.normal(size=(2, Hkv, d, d))
+    S, Mbar = G[0] @ G[0].transpose(0, 2, 1) / d, G[1] @ G[1].transpose(0, 2, 1) / d
+    A, W, DD = rng.random((3, Hkv, n))
+    signs = os_.rotation_signs(d)
+    R = os_.rotation_matrix(d).astype(np.float64)
+    (mk, Yk), (mv, Yv) = os_.strata_center_rotate(Xk, signs), os_.strata_center_rotate(Xv, signs)
+    D = oa.distortion_table(Yk, Yv, S, Mbar, A, W, DD, bits)
+    assert D.shape == (Hkv, n, len(bits) + 2) and (D[..., -1] == 0).all() and (D[..., 0] == DD).all()
+    for i, b in enumerate(bits):
+        step = os_.uniform_step(b)[0]
+        want = 0.0
+        for Y, mu, X, M, wgt in ((Yk, mk, Xk, S, A), (Yv, mv, Xv, Mbar, W)):
+            xh = mu[:, None, :].astype(np.float64) + os_.strata_quantize(Y, b, step)[2].astype(np.float64) @ R
+            xr = mu[:, None, :].astype(np.float64) + Y.astype(np.float64) @ R      # == X up to fp32 rounding
+            e = xh - xr
+            want = want + wgt * np.einsum("hnd,hde,hne->hn", e, M, e)
+        np.testing.assert_allclose(D[..., 1 + i], want, rtol=1e-9)
+        bad = 0.0
+        for Y, M, wgt in ((Yk, S, A), (Yv, Mbar, W)):
+            e = os_.strata_quantize(Y, b, step)[2].astype(np.float64) - Y
+            bad = bad + wgt * np.einsum("hnd,hde,hne->hn", e, R.T @ M @ R, e)
+        assert np.abs(bad - want).max() > 1e-3 * np.abs(want).max()
