@@ -254,7 +254,7 @@ __global__ __launch_bounds__(256) void strata_metric_kernel(const float* __restr
 
 // err[bh][t][b] = e^T M e with e = y_hat - y of token t quantised at width bits[b] (the codes of
 // strata_quantize_kernel), M = Mt[bh] read as columns (M^T e gives the same form).  A block holds
-// one bh and kSErrTok tokens, one wavefront per token at a time; M staged in LDS once.
+// one bh and kSErrTok tokens, two tokens per wavefront at a time; M staged in LDS once.
 constexpr int kSErrTok = 256;
 constexpr int kSMaxBits = 3;
 
@@ -268,35 +268,41 @@ __global__ __launch_bounds__(256) void strata_err_kernel(const float* __restrict
                                                          const float* __restrict__ Mt, ErrWidths w,
                                                          float* __restrict__ err) {
   __shared__ float M[kSD * kSD];
-  __shared__ float e_l[4][kSMaxBits][kSD];
+  __shared__ float e_l[4][2][kSMaxBits][kSD];
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const int64_t bh = blockIdx.y;
   const float* mg = Mt + bh * kSD * kSD;
   for (int i = threadIdx.x; i < kSD * kSD; i += 256) M[i] = mg[i];
   __syncthreads();
   const int64_t t_end = min<int64_t>(n, static_cast<int64_t>(blockIdx.x + 1) * kSErrTok);
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * kSErrTok + wave; t < t_end; t += 4) {
-    const float* row = y + (bh * n + t) * kSD;
-    const float y0 = row[lane], y1 = row[lane + 64];
-    double ss = static_cast<double>(y0) * y0 + static_cast<double>(y1) * y1;
+  // two tokens (t, t + 4) per wavefront iteration share each metric read
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * kSErrTok + wave; t < t_end; t += 8) {
+    float e0[2][kSMaxBits], e1[2][kSMaxBits], m0[2][kSMaxBits], m1[2][kSMaxBits];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    const float rms = __fsqrt_rn(static_cast<float>(ss / kSD));
-    float e0[kSMaxBits], e1[kSMaxBits], m0[kSMaxBits], m1[kSMaxBits];
+    for (int u = 0; u < 2; ++u) {
+      const bool ok = t + 4 * u < t_end;                          // wave-uniform
+      const float* row = y + (bh * n + (ok ? t + 4 * u : t)) * kSD;
+      const float y0 = row[lane], y1 = row[lane + 64];
+      double ss = static_cast<double>(y0) * y0 + static_cast<double>(y1) * y1;
 #pragma unroll
-    for (int b = 0; b < kSMaxBits; ++b) {
-      e0[b] = e1[b] = m0[b] = m1[b] = 0.0f;
-      if (b >= w.n) continue;
-      const int bits = w.bits[b];
-      const float sc = fmaxf(as_stored16(__fmul_rn(w.step[b], rms)), kMinScale);
-      const float half = static_cast<float>((1 << bits) - 1) * 0.5f;
-      const float qmax = static_cast<float>((1 << bits) - 1);
-      const float c0 = fminf(fmaxf(rintf(__fadd_rn(__fdiv_rn(y0, sc), half)), 0.0f), qmax);
-      const float c1 = fminf(fmaxf(rintf(__fadd_rn(__fdiv_rn(y1, sc), half)), 0.0f), qmax);
-      e0[b] = __fsub_rn(__fmul_rn(__fsub_rn(c0, half), sc), y0);
-      e1[b] = __fsub_rn(__fmul_rn(__fsub_rn(c1, half), sc), y1);
-      e_l[wave][b][lane] = e0[b];
-      e_l[wave][b][lane + 64] = e1[b];
+      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      const float rms = __fsqrt_rn(static_cast<float>(ss / kSD));
+#pragma unroll
+      for (int b = 0; b < kSMaxBits; ++b) {
+        e0[u][b] = e1[u][b] = m0[u][b] = m1[u][b] = 0.0f;
+        if (b < w.n) {
+          const int bits = w.bits[b];
+          const float sc = fmaxf(as_stored16(__fmul_rn(w.step[b], rms)), kMinScale);
+          const float half = static_cast<float>((1 << bits) - 1) * 0.5f;
+          const float qmax = static_cast<float>((1 << bits) - 1);
+          const float c0 = fminf(fmaxf(rintf(__fadd_rn(__fdiv_rn(y0, sc), half)), 0.0f), qmax);
+          const float c1 = fminf(fmaxf(rintf(__fadd_rn(__fdiv_rn(y1, sc), half)), 0.0f), qmax);
+          e0[u][b] = __fsub_rn(__fmul_rn(__fsub_rn(c0, half), sc), y0);
+          e1[u][b] = __fsub_rn(__fmul_rn(__fsub_rn(c1, half), sc), y1);
+        }
+        e_l[wave][u][b][lane] = e0[u][b];
+        e_l[wave][u][b][lane + 64] = e1[u][b];
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_wave_barrier();
@@ -305,21 +311,25 @@ __global__ __launch_bounds__(256) void strata_err_kernel(const float* __restrict
     for (int j = 0; j < kSD; ++j) {                               // (M^T e)_lane, (M^T e)_lane+64
       const float a0 = M[j * kSD + lane], a1 = M[j * kSD + lane + 64];
 #pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int b = 0; b < kSMaxBits; ++b) {
+          const float ej = e_l[wave][u][b][j];
+          m0[u][b] = __builtin_fmaf(a0, ej, m0[u][b]);
+          m1[u][b] = __builtin_fmaf(a1, ej, m1[u][b]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
       for (int b = 0; b < kSMaxBits; ++b) {
-        const float ej = e_l[wave][b][j];
-        m0[b] = __builtin_fmaf(a0, ej, m0[b]);
-        m1[b] = __builtin_fmaf(a1, ej, m1[b]);
+        float q = __builtin_fmaf(e0[u][b], m0[u][b], e1[u][b] * m1[u][b]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+        if (lane == 0 && b < w.n && t + 4 * u < t_end) err[(bh * n + t + 4 * u) * w.n + b] = q;
       }
-    }
-#pragma unroll
-    for (int b = 0; b < kSMaxBits; ++b) {
-      float q = __builtin_fmaf(e0[b], m0[b], e1[b] * m1[b]);
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
-      if (lane == 0 && b < w.n) err[(bh * n + t) * w.n + b] = q;
-    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();                              // e_l of this token consumed
+    __builtin_amdgcn_wave_barrier();                              // e_l of these tokens consumed
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   }
 }
