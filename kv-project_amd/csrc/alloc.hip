@@ -73,7 +73,8 @@ __device__ __forceinline__ void write_grid(AllocState* st, double lo, double hi)
 // stable, so tied keys keep ascending index)
 __global__ __launch_bounds__(kAThreads) void alloc_keys_kernel(const float* __restrict__ D, int64_t n, int nlev,
                                                                int Hkv, uint64_t* __restrict__ keys,
-                                                               int32_t* __restrict__ vals, AllocState* st) {
+                                                               int32_t* __restrict__ vals, AllocState* st,
+                                                               int32_t* __restrict__ counts) {
   const int64_t total = static_cast<int64_t>(Hkv) * n;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kAThreads + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * kAThreads) {
@@ -85,6 +86,7 @@ __global__ __launch_bounds__(kAThreads) void alloc_keys_kernel(const float* __re
     vals[i] = static_cast<int32_t>(i % n);
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) write_grid(st, kALo, kAHi);
+  if (blockIdx.x == 0 && threadIdx.x < static_cast<unsigned>(nlev)) counts[threadIdx.x] = 0;   // histogram target
 }
 
 // order from the sorted values; Dsort rows (heads summed in float32, head order)
@@ -309,22 +311,21 @@ __global__ void alloc_final_kernel(AllocState* st) {
   st->M = 1;
 }
 
-// histogram of the choice; bits and cap of the final pass (or the all-drop allocation)
-__global__ __launch_bounds__(1024) void alloc_count_kernel(AllocConst k, const AllocState* __restrict__ st,
-                                                           const double* __restrict__ partb,
-                                                           const int32_t* __restrict__ choice, int search,
-                                                           int32_t* __restrict__ counts, double* __restrict__ summary) {
+// histogram of the choice (per-block counts added to the zeroed histogram: integer, so exact in
+// any order); block 0 also writes bits and cap of the final pass (or of the all-drop allocation)
+__global__ __launch_bounds__(kAThreads) void alloc_count_kernel(AllocConst k, const AllocState* __restrict__ st,
+                                                                const double* __restrict__ partb,
+                                                                const int32_t* __restrict__ choice, int search,
+                                                                int32_t* __restrict__ counts,
+                                                                double* __restrict__ summary) {
   __shared__ int hist[kAMaxLev];
   if (threadIdx.x < kAMaxLev) hist[threadIdx.x] = 0;
   __syncthreads();
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * kAThreads + threadIdx.x;
+  const int ch = j < k.n ? choice[j] : -1;
   int cnt[kAMaxLev];
 #pragma unroll
-  for (int o = 0; o < kAMaxLev; ++o) cnt[o] = 0;
-  for (int64_t j = threadIdx.x; j < k.n; j += blockDim.x) {
-    const int ch = choice[j];
-#pragma unroll
-    for (int o = 0; o < kAMaxLev; ++o) cnt[o] += ch == o;
-  }
+  for (int o = 0; o < kAMaxLev; ++o) cnt[o] = ch == o;
 #pragma unroll
   for (int sh = 32; sh > 0; sh >>= 1)
 #pragma unroll
@@ -332,13 +333,14 @@ __global__ __launch_bounds__(1024) void alloc_count_kernel(AllocConst k, const A
   if ((threadIdx.x & 63) == 0)
 #pragma unroll
     for (int o = 0; o < kAMaxLev; ++o)
-      if (o < k.nlev) atomicAdd(&hist[o], cnt[o]);
+      if (o < k.nlev && cnt[o]) atomicAdd(&hist[o], cnt[o]);
   __syncthreads();
-  if (static_cast<int>(threadIdx.x) < k.nlev) counts[threadIdx.x] = hist[threadIdx.x];
-  const double s = threadIdx.x < 64 ? wave_sum_blocks(partb, k.nblk, 1, threadIdx.x) : 0.0;
+  if (static_cast<int>(threadIdx.x) < k.nlev && hist[threadIdx.x]) atomicAdd(&counts[threadIdx.x], hist[threadIdx.x]);
+  if (blockIdx.x != 0) return;
+  const double sb = threadIdx.x < 64 ? wave_sum_blocks(partb, k.nblk, 1, threadIdx.x) : 0.0;
   if (threadIdx.x == 0) {
     if (search) {
-      summary[0] = s + k.fixed[st->cap[0]];
+      summary[0] = sb + k.fixed[st->cap[0]];
       summary[1] = st->cap[0];
     } else {
       summary[0] = k.fixed[0];
@@ -478,7 +480,7 @@ extern "C" int kvq_strata_allocate(const float* D, int64_t Hkv, int64_t n, int n
   const int64_t total = Hkv * n;
   const unsigned kb = static_cast<unsigned>(std::min<int64_t>((total + kAThreads - 1) / kAThreads, 4096));
   hipLaunchKernelGGL(alloc_keys_kernel, dim3(kb), dim3(kAThreads), 0, st, D, n, nlev, static_cast<int>(Hkv), keys_in,
-                     vals_in, state);
+                     vals_in, state, counts);
   KVQ_LAUNCH_CHECK("kvq_strata_allocate(keys)");
   size_t temp_bytes = lay.temp_bytes;
   const hipError_t se = hipcub::DeviceRadixSort::SortPairs(ws + lay.temp, temp_bytes, keys_in, keys_out, vals_in,
@@ -513,7 +515,8 @@ extern "C" int kvq_strata_allocate(const float* D, int64_t Hkv, int64_t n, int n
     hipLaunchKernelGGL(alloc_zero_kernel, dim3(nb), dim3(kAThreads), 0, st, choice, n);
   }
   KVQ_LAUNCH_CHECK("kvq_strata_allocate(search)");
-  hipLaunchKernelGGL(alloc_count_kernel, dim3(1), dim3(1024), 0, st, k, state, partb, choice, search, counts, summary);
+  hipLaunchKernelGGL(alloc_count_kernel, dim3(nb), dim3(kAThreads), 0, st, k, state, partb, choice, search, counts,
+                     summary);
   hipLaunchKernelGGL(alloc_lev_kernel, dim3(nb), dim3(kAThreads), 0, st, k, counts, dsort, lev, part);
   hipLaunchKernelGGL(alloc_ratio_kernel, dim3(1), dim3(64), 0, st, k, part, summary);
   KVQ_LAUNCH_CHECK("kvq_strata_allocate(finish)");
