@@ -23,10 +23,13 @@ Timing: W untimed warm-up steps, then K steps launched back to back between HIP 
 launch stream (device synchronisation on both sides).  The same step captured once in a HIP graph
 (the reference's _time_callable protocol, STRATA_KV.py:3424-3447) is timed too and reported as
 ``graph_us``: on this ROCm stack a replay of a one-step graph costs more than the eager launches.
-The dominant kernel is timed on its own as K launches captured in ONE graph and replayed once
-(``kernel_us``: the GPU time per launch without host dispatch between launches, the figure a
-rocprofv3 kernel-trace average gives); its rocprofv3 summary is committed under profiles/.  The CPU baseline is the oracle's restatement of the
-reference path on a bounded sample of the same workload, scaled to the whole workload.
+The dominant kernel is timed inside K more eager steps of the same sequence, with HIP events
+recorded on the launch stream right before and after each of its launches (``kernel_us``: the
+figure a rocprofv3 kernel-trace average gives; its summary is committed under profiles/).  The
+CPU baseline is the oracle's restatement of the reference path on a bounded sample of the same
+workload, scaled to the whole workload, at the box's thread count and at 4 threads; for C1/C2 the
+oracle's outputs of the sampled (b, h) pairs are compared with the GPU step's (``parity``), and a
+mismatch beyond the bar makes the run exit non-zero.
 """
 from __future__ import annotations
 
@@ -101,6 +104,33 @@ def graph_k_ms(fn, steps: int, warmup: int) -> float:
     return _events_ms(gr.replay, 1) / steps
 
 
+def kernel_in_step_ms(kern, steps: int, warmup: int, pre=None, post=None) -> float:
+    """Average GPU time of ``kern`` launched inside back-to-back eager steps (pre(); kern(); post()):
+    HIP events recorded on the launch stream (torch's current stream, the one every kvq call
+    launches on) right before and right after each kern() launch.  The host runs ahead of the GPU,
+    so each pair brackets the kernel alone; it is the same eager sequence ms_per_step times, so
+    the kernel's time cannot exceed the step's."""
+    import torch
+    for _ in range(warmup):
+        if pre is not None:
+            pre()
+        kern()
+        if post is not None:
+            post()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        if pre is not None:
+            pre()
+        a.record()
+        kern()
+        b.record()
+        if post is not None:
+            post()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / steps
+
+
 def eager_ms(fn, steps: int, warmup: int) -> float:
     """Back-to-back launches on the current stream between HIP events, after warm-up."""
     for _ in range(warmup):
@@ -150,9 +180,13 @@ def _traffic(name: str):
 # ---------------------------------------------------------------------------------------------
 # C2 (default) and C1: packed 4-bit KIVI decode
 
-def cpu_kivi_decode(q, K, V, window, bits, group_k, group_v, bytes_alg, seconds: float) -> dict:
-    """Oracle decode (kivi dequantisation + chunked_attention, float32) on whole (b, h) pairs."""
+def cpu_kivi_decode(q, K, V, window, bits, group_k, group_v, bytes_alg, seconds: float, gpu_out=None) -> dict:
+    """Oracle decode (kivi dequantisation + chunked_attention, float32) on whole (b, h) pairs, timed
+    at the box's BLAS thread count and at 4 threads (the reference's default, STRATA_KV.py:225-226).
+    With ``gpu_out`` (B, 1, Hq, d) the oracle's output of every pair it computes is compared with the
+    GPU step's (``parity``)."""
     import numpy as np
+    from threadpoolctl import threadpool_limits
     from oracle.attention import chunked_attention
     from oracle.kivi import kivi_dequant, kivi_quant
     B, Hkv, T, d = K.shape
@@ -160,9 +194,8 @@ def cpu_kivi_decode(q, K, V, window, bits, group_k, group_v, bytes_alg, seconds:
     W = window
     n_q = T - W
     scaling = d ** -0.5
-    times = []
-    pairs = [(b, h) for b in range(B) for h in range(Hkv)]
-    for b, h in pairs:
+
+    def pair(b, h):
         Kbh = K[b:b + 1, h:h + 1].float().cpu().numpy()
         Vbh = V[b:b + 1, h:h + 1].float().cpu().numpy()
         qbh = q[b:b + 1, h * rep:(h + 1) * rep].float().cpu().numpy()
@@ -172,17 +205,38 @@ def cpu_kivi_decode(q, K, V, window, bits, group_k, group_v, bytes_alg, seconds:
         kh = kivi_dequant(kq["codes"], kq["lo"], kq["scale"], group_k, True)[:, :, :n_q]
         vh = kivi_dequant(vq["codes"][:, :, :n_q], vq["lo"][:, :, :n_q], vq["scale"][:, :, :n_q], group_v, False)
         tok = {"k": kh, "v": vh, "b": np.zeros((1, 1, n_q), np.float32), "tau": np.full(n_q, -1)}
-        chunked_attention(qbh, scaling, np.array([T]), Kbh[:, :, n_q:], Vbh[:, :, n_q:], np.arange(W),
-                          np.full(W, 1 << 40), tok, dtype=np.float32)
-        times.append(time.perf_counter() - t0)
+        o = chunked_attention(qbh, scaling, np.array([T]), Kbh[:, :, n_q:], Vbh[:, :, n_q:], np.arange(W),
+                              np.full(W, 1 << 40), tok, dtype=np.float32)
+        return time.perf_counter() - t0, o[0]                   # (1, rep, d)
+
+    pairs = [(b, h) for b in range(B) for h in range(Hkv)]
+    times, errs = [], []
+    for b, h in pairs:
+        dt, o = pair(b, h)
+        times.append(dt)
+        if gpu_out is not None:
+            errs.append(float(np.abs(gpu_out[b, :, h * rep:(h + 1) * rep] - o).max()))
         if sum(times) >= seconds and len(times) >= 2:
             break
     per_pair = float(np.median(times))
     t_layer = per_pair * len(pairs)
-    return {"value": bytes_alg / t_layer / 1e9, "unit": "GB/s", "cores": _threads(), "kind": "port",
-            "us_per_layer": t_layer * 1e6,
-            "sample": f"{len(times)} of {len(pairs)} (batch, KV-head) pairs at full context; "
-                      f"median per pair x {len(pairs)}; numpy float32 dequantise + chunked_attention"}
+    times4 = []
+    with threadpool_limits(4):
+        for b, h in pairs:
+            times4.append(pair(b, h)[0])
+            if sum(times4) >= seconds / 2 and len(times4) >= 2:
+                break
+    t4 = float(np.median(times4)) * len(pairs)
+    res = {"value": bytes_alg / t_layer / 1e9, "unit": "GB/s", "cores": _threads(), "kind": "port",
+           "us_per_layer": t_layer * 1e6,
+           "sample": f"{len(times)} of {len(pairs)} (batch, KV-head) pairs at full context; "
+                     f"median per pair x {len(pairs)}; numpy float32 dequantise + chunked_attention",
+           "at_4_threads": {"value": bytes_alg / t4 / 1e9, "unit": "GB/s", "cores": 4, "us_per_layer": t4 * 1e6,
+                            "sample": f"{len(times4)} of {len(pairs)} pairs, median per pair x {len(pairs)}"}}
+    if gpu_out is not None:
+        res["parity"] = {"pairs": len(errs), "max_abs_err": max(errs),
+                         "oracle": "oracle.kivi kivi_quant + chunked_attention (numpy float32), same inputs"}
+    return res
 
 
 def run_kivi(args, shape_name: str) -> dict:
@@ -207,9 +261,12 @@ def run_kivi(args, shape_name: str) -> dict:
     def split_only():
         kvq.kivi_decode(q, scaling, cache, out=out, workspace=ws, split_tokens=args.split_tokens, phases=1)
 
+    def merge_only():
+        kvq.kivi_decode(q, scaling, cache, out=out, workspace=ws, split_tokens=args.split_tokens, phases=2)
+
     log("timing")
     ms_per_step, g_ms = step_ms(step, args.steps, args.warmup)
-    split_ms = graph_k_ms(split_only, args.steps, args.warmup)
+    split_ms = kernel_in_step_ms(split_only, args.steps, 0, post=merge_only)
     step_gpu_ms = graph_k_ms(step, args.steps, args.warmup)
     io_bytes = q.numel() * q.element_size() + out.numel() * out.element_size()
     bytes_alg = cache.payload_bytes() + io_bytes
@@ -251,9 +308,17 @@ def run_kivi(args, shape_name: str) -> dict:
                       "export_GBs": round(2 * wire.numel() / (export_ms * 1e-3) / 1e9, 2)}
     del wire
     if not args.no_cpu_baseline:
-        log("cpu baseline")
-        res["cpu_baseline"] = cpu_kivi_decode(q, K, V, shape.window, shape.bits, shape.group_k, shape.group_v,
-                                              bytes_alg, args.cpu_seconds)
+        log("cpu baseline (and the oracle's outputs of the pairs it computes against this step's)")
+        step()
+        gpu_out = out.float().cpu().numpy()
+        cb = cpu_kivi_decode(q, K, V, shape.window, shape.bits, shape.group_k, shape.group_v, bytes_alg,
+                             args.cpu_seconds, gpu_out=gpu_out)
+        par = cb.pop("parity")
+        par["bar"] = 2e-3 if shape.dtype == torch.float32 else 1e-2
+        par["ok"] = par["max_abs_err"] <= par["bar"]
+        res["parity"] = par
+        res["cpu_baseline"] = cb
+        log(f"parity over {par['pairs']} (b, h) pairs: max-abs-err {par['max_abs_err']:.3e} (bar {par['bar']})")
     return res
 
 
@@ -276,8 +341,9 @@ def run_c3(args) -> dict:
                      device="cuda")
     step = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws)
     split = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
+    merge = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws, phases=2)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
-    split_ms = graph_k_ms(split, args.steps, args.warmup)
+    split_ms = kernel_in_step_ms(split, args.steps, 0, post=merge)
     qb = q.numel() * q.element_size()
     bytes_alg = cache.coded_bytes() + qb + out.numel() * out.element_size()
     avg_bits = float(widths.float().mean())
@@ -338,7 +404,7 @@ def run_strata(args) -> dict:
                                                   [t.bits for t in cache.tiers]),), dtype=torch.float32, device="cuda")
     step = lambda: kvq.strata_decode(q, scaling, cache, out=out, workspace=ws)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
-    k_ms = graph_k_ms(step, args.steps, args.warmup)
+    k_ms = kernel_in_step_ms(step, args.steps, 0)
     qb = q.numel() * q.element_size()
     bytes_alg = cache.coded_bytes() + qb + out.numel() * out.element_size()
     res = _result(args, metric="STRATA strata decode (per-token 8/4/2-bit tiers): effective HBM GB/s + µs/layer",
@@ -394,8 +460,9 @@ def run_c5(args) -> dict:
                      device="cuda")
     step = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws)
     split = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
+    merge = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws, phases=2)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
-    split_ms = graph_k_ms(split, args.steps, args.warmup)
+    split_ms = kernel_in_step_ms(split, args.steps, 0, post=merge)
     # the encoder: keys and values of the whole context, one launch each
     kc, ks = torch.empty_like(cache.kc), torch.empty_like(cache.ks)
     ctab = kvq.dct_table()
@@ -473,7 +540,8 @@ def run_quasar(args) -> dict:
     split = lambda: st.attend(q, scaling, qpos, out=out, phases=2)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
     step_gpu_ms = graph_k_ms(step, args.steps, args.warmup)
-    split_ms = graph_k_ms(split, args.steps, args.warmup)
+    split_ms = kernel_in_step_ms(split, args.steps, 0, pre=lambda: st.attend(q, scaling, qpos, out=out, phases=1),
+                                 post=lambda: st.attend(q, scaling, qpos, out=out, phases=4))
     codes = sum(s_["flat"].numel() for s_ in st.sides)
     rho = 2 * 2 * Hkv * QUASAR_NC
     exact = 2 * K.numel() * K.element_size()
@@ -673,8 +741,7 @@ def run_c4(args) -> dict:
                                          score_weight=wgt, phases=4)
     plain_ms = eager_ms(plain, args.steps, args.warmup)
     scored_ms, g_ms = step_ms(scored, args.steps, args.warmup)
-    plain()
-    score_ms = graph_k_ms(score_only, args.steps, args.warmup)
+    score_ms = kernel_in_step_ms(score_only, args.steps, 0, pre=plain)
     # the eviction workload proper: 32 scored decode steps, top-k, gather, decode over the kept rows
     scores.zero_()
     torch.cuda.synchronize()
@@ -953,6 +1020,9 @@ def main() -> int:
         return 0
     res = WORKLOADS[args.workload](args)
     print(json.dumps(res), flush=True)
+    if res.get("parity") is not None and not res["parity"].get("ok", True):
+        log(f"PARITY FAILURE: {res['parity']}")
+        return 1
     return 0
 
 

@@ -145,7 +145,9 @@ extern "C" int kvq_kivi_append(const void* k_new, const void* v_new, int dtype, 
   KVQ_REQUIRE(group_k > 0 && group_k % 32 == 0 && W >= group_k, "kvq_kivi_append: need W >= group_k, group_k %% 32 == 0");
   KVQ_REQUIRE(group_v == 32 || group_v == 64 || group_v == 128, "kvq_kivi_append: group_v in {32,64,128}");
   KVQ_REQUIRE(pos >= 0 && cap_t % group_k == 0 && cap_t % 32 == 0, "kvq_kivi_append: bad pos / capacity");
-  KVQ_REQUIRE(pos < W || (pos - W) + group_k <= cap_t, "kvq_kivi_append: packed capacity exhausted");
+  // token o = pos - W takes packed row o; a key group is written only when o % group_k == 0, and
+  // cap_t % group_k == 0, so every o < cap_t keeps its group's rows inside the capacity
+  KVQ_REQUIRE(pos < W || pos - W < cap_t, "kvq_kivi_append: packed capacity exhausted");
   KVQ_REQUIRE(B > 0 && Hkv > 0 && B * Hkv < (1LL << 31), "kvq_kivi_append: bad batch/heads");
   hipStream_t s = static_cast<hipStream_t>(stream);
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((kivi_append_kernel<DT_>), dim3(B * Hkv), dim3(d),

@@ -17,6 +17,7 @@ import torch
 
 from . import _lib
 from .kivi import kivi_quant_stored, v_tile, vmeta_tile
+from .query import decode_in_pieces, query_pieces
 
 
 def _round_up(x: int, m: int) -> int:
@@ -110,7 +111,7 @@ class PackedKIVICache:
         if t != 1:
             raise ValueError("append() takes one token per sequence")
         W, pos = self.cap_e, self.next_pos
-        if pos >= W and (pos - W) + self.group_k > self.cap_t:
+        if pos >= W and pos - W >= self.cap_t:          # token pos - W would take packed row >= cap_t
             raise RuntimeError("decode buffer exhausted")
         _lib.call("kvq_kivi_append", k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[k.dtype], k.stride(0),
                   k.stride(1), v.stride(0), v.stride(1), B, H, d, pos, self.k_exact.data_ptr(),
@@ -192,8 +193,12 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
                 q_pos: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                 workspace: Optional[torch.Tensor] = None, split_tokens: int = 0,
                 phases: Optional[int] = None, scores: Optional[torch.Tensor] = None,
-                score_weight: float = 1.0) -> torch.Tensor:
+                score_weight: float = 1.0, chunk: Optional[int] = None) -> torch.Tensor:
     """Attention of q (B, Hq, Tq, d) over the packed cache; returns (B, Tq, Hq, d) in q's dtype.
+
+    Any Tq: a step with more than 8 // rep query tokens (or more than ``chunk``) runs as
+    consecutive launches over query-token pieces (kvq.query), as chunked_attention takes query
+    chunks (STRATA_KV.py:641-675).
 
     With ``q_pos`` (Tq,) int64 and ``cache.exact_pos`` set, exact row i is visible to query t iff
     exact_pos[i] <= q_pos[t] (the causal rule of chunked_attention among appended rows); every
@@ -205,6 +210,14 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.kc.shape[1]
+    pieces = query_pieces(Hq // Hkv, Tq, chunk)
+    if len(pieces) > 1:
+        if phases not in (None, 3, 7):
+            raise ValueError("a chunked query step runs whole steps (phases 3 or 7)")
+        return decode_in_pieces(
+            lambda qs, qp: kivi_decode(qs, scaling, cache, q_pos=qp, workspace=workspace, split_tokens=split_tokens,
+                                       phases=phases, scores=scores, score_weight=score_weight),
+            q, q_pos, out, pieces)
     if q.stride(-1) != 1:
         q = q.contiguous()
     if cache.k_exact.dtype != q.dtype:

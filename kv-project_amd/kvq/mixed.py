@@ -14,6 +14,7 @@ from typing import Optional
 import torch
 
 from . import _lib
+from .query import decode_in_pieces, query_pieces
 
 BLOCK = 64
 UNIT = 2048                 # bytes; a block of width b occupies b + 1 units
@@ -120,13 +121,20 @@ def mixed_workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, nb: int, 
 @torch.no_grad()
 def mixed_decode(q: torch.Tensor, scaling: float, cache: MixedKIVICache, *, q_pos: Optional[torch.Tensor] = None,
                  out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
-                 phases: int = 3) -> torch.Tensor:
+                 phases: int = 3, chunk: Optional[int] = None) -> torch.Tensor:
     """Attention of q (B, Hq, Tq, d) over every coded block (all visible) and the exact rows
     (visible per q_pos / exact_pos when both are set) -> (B, Tq, Hq, d) of q's dtype.  ``phases`` 1 computes
-    only the partials into ``workspace``, 2 only merges them (timing hooks), 3 both."""
+    only the partials into ``workspace``, 2 only merges them (timing hooks), 3 both.  Any Tq (query-token
+    pieces of at most 8 // rep tokens, and at most ``chunk``; kvq.query)."""
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.k_exact.shape[1]
+    pieces = query_pieces(Hq // Hkv, Tq, chunk)
+    if len(pieces) > 1:
+        if phases != 3:
+            raise ValueError("a chunked query step runs whole steps (phases 3)")
+        return decode_in_pieces(lambda qs, qp: mixed_decode(qs, scaling, cache, q_pos=qp, workspace=workspace),
+                                q, q_pos, out, pieces)
     if q.stride(-1) != 1:
         q = q.contiguous()
     if cache.k_exact.dtype != q.dtype:

@@ -20,6 +20,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from .query import decode_in_pieces, query_pieces
 
 MAX_SPLITS = 1024
 
@@ -232,11 +233,20 @@ class QuasarState:
                phases: int = 7) -> torch.Tensor:
         """One decode step (QUASAR_KV.py:1945-1968): q (1, Hq, Tq, d) -> (1, Tq, Hq, d) in q's dtype.
         Appended rows are causal (row at position H + i visible to query t iff H + i <= qpos[t]).
-        ``phases`` (timing hooks): mask of 1 (query coefficients), 2 (split launch), 4 (merge)."""
+        ``phases`` (timing hooks): mask of 1 (query coefficients), 2 (split launch), 4 (merge).
+        Any Tq: query-token pieces of at most 8 // rep tokens, and at most ``chunk`` (kvq.query)."""
         _lib.require_gpu(q)
         B, Hq, Tq, d = q.shape
         if B != 1:
             raise ValueError("QuasarState.attend takes batch 1")
+        pieces = query_pieces(Hq // self.K.shape[1], Tq, chunk)
+        if len(pieces) > 1:
+            if phases != 7:
+                raise ValueError("a chunked query step runs whole steps (phases 7)")
+            qp_all = torch.as_tensor(qpos, dtype=torch.int64).reshape(-1)
+            if qp_all.numel() != Tq:
+                raise ValueError("qpos needs one position per query row")
+            return decode_in_pieces(lambda qs, qp: self.attend(qs, scaling, qp), q, qp_all, out, pieces)
         if q.dtype != self.dtype:
             q = q.to(self.dtype)
         if q.stride(-1) != 1:

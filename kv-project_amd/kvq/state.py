@@ -158,15 +158,16 @@ class KIVIState:
     def attend(self, q: torch.Tensor, scaling: float, qpos, chunk=None) -> torch.Tensor:
         """q (B, Hq, Tq, d) at positions ``qpos`` (Tq,) -> (B, Tq, Hq, d) in q's dtype.  Query t
         reads every quantised row, the window rows and the appended rows at positions <= qpos[t]
-        (chunked_attention's visibility, STRATA_KV.py:641-675).  ``chunk`` is accepted for the
-        protocol; the kernel has no query chunking to configure."""
+        (chunked_attention's visibility, STRATA_KV.py:641-675).  Any Tq: the step runs in
+        query-token pieces of at most 8 // rep tokens, and at most ``chunk`` when it is given
+        (the reference's ATTN_CHUNK query chunks)."""
         if not self.use_kernel:
             raise RuntimeError("KIVIState: the HIP decode kernel is disabled (check_kernel failed)")
         c = self.cache
         qp = torch.as_tensor(qpos, dtype=torch.int64).reshape(-1).to(q.device)
         if qp.numel() != q.shape[2]:
             raise ValueError("qpos must hold one position per query token")
-        return kivi_decode(q.to(c.k_exact.dtype), scaling, c, q_pos=qp).to(q.dtype)
+        return kivi_decode(q.to(c.k_exact.dtype), scaling, c, q_pos=qp, chunk=chunk).to(q.dtype)
 
     @torch.no_grad()
     def reference_attend(self, q: torch.Tensor, scaling: float, qpos) -> torch.Tensor:

@@ -15,6 +15,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from .query import decode_in_pieces, query_pieces
 
 
 @lru_cache(maxsize=None)
@@ -207,14 +208,20 @@ def strata_workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_exact:
 
 @torch.no_grad()
 def strata_decode(q: torch.Tensor, scaling: float, cache: StrataCache, *, q_pos: Optional[torch.Tensor] = None,
-                  out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                  chunk: Optional[int] = None) -> torch.Tensor:
     """StrataState.attend (STRATA_KV.py:1762-1795) for q (B, Hq, Tq, d) -> (B, Tq, Hq, d): the exact
     rows (visible per q_pos / exact_pos when both are set) and every stratum, merged exactly, the
-    coded part rotated back once and the value mean added."""
+    coded part rotated back once and the value mean added.  Any Tq (query-token pieces of at most
+    8 // rep tokens, and at most ``chunk``; kvq.query)."""
     import ctypes
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.k_exact.shape[1]
+    pieces = query_pieces(Hq // Hkv, Tq, chunk)
+    if len(pieces) > 1:
+        return decode_in_pieces(lambda qs, qp: strata_decode(qs, scaling, cache, q_pos=qp, workspace=workspace),
+                                q, q_pos, out, pieces)
     if q.stride(-1) != 1:
         q = q.contiguous()
     if cache.k_exact.dtype != q.dtype:

@@ -61,3 +61,30 @@ def test_append_capacity_exhausted():
     with pytest.raises(RuntimeError):
         for _ in range(200):
             st.append(K[:, :, :1], K[:, :, :1])
+
+
+def test_append_fills_capacity_to_last_row():
+    """The packed capacity fills to its last row: with cap_t = 128 rows, appends continue until token
+    127 leaves the window (its key group was written when token 64 left), the next append raises,
+    and the full cache decodes as the one-shot compression of the same 192 tokens."""
+    import kvq
+    g = torch.Generator().manual_seed(5)
+    B, Hq, Hkv, d, W, gk, gv, T0 = 1, 8, 2, 128, 64, 64, 64, 128
+    K = torch.randn((B, Hkv, 192, d), generator=g).to(torch.bfloat16)
+    V = torch.randn((B, Hkv, 192, d), generator=g).to(torch.bfloat16)
+    q = torch.randn((B, Hq, 1, d), generator=g).to(torch.bfloat16)
+    Kc, Vc = K.cuda(), V.cuda()
+    st = kvq.PackedKIVICache.from_context(Kc[:, :, :T0], Vc[:, :, :T0], window=W, group_k=gk, group_v=gv,
+                                          extra_tokens=64, ring=True)
+    assert st.cap_t == 128
+    for i in range(T0, 192):
+        st.append(Kc[:, :, i:i + 1], Vc[:, :, i:i + 1])
+    assert st.n_q == st.cap_t == 128
+    with pytest.raises(RuntimeError, match="exhausted"):
+        st.append(Kc[:, :, :1], Vc[:, :, :1])
+    out = kvq.kivi_decode(q.cuda(), d ** -0.5, st).float().cpu().numpy()
+    Kf, Vf = K.float().numpy(), V.float().numpy()
+    kq, vq = ok.kivi_quant(Kf, 4, gk, True, 0), ok.kivi_quant(Vf, 4, gv, False, 0)
+    ref = kivi_decode_reference(q.float().numpy(), d ** -0.5, Kf[:, :, 128:], Vf[:, :, 128:], kq["codes"], kq["lo"],
+                                kq["scale"], vq["codes"], vq["lo"], vq["scale"], gk, gv, 128)
+    assert np.abs(out - ref).max() <= 1e-2

@@ -102,6 +102,41 @@ def test_decode_matches_oracle(dtype, Hq, Hkv, Tq, T, W):
     assert err <= tol, err
 
 
+@pytest.mark.parametrize("T,W", [(4096, 0), (4096 + 64, 64), (8192 + 37, 37)])
+def test_decode_c5_shape_bf16(T, W):
+    """The C5 instantiation itself: bf16, Hq 64 over Hkv 8 (R = 8, the dct_split<8, bf16> kernel the
+    c5 workload times) on the C5 generator's AR(1) + noise rows at a reduced context, with and
+    without an exact tail.  bf16 bar (1e-2) against the float64 oracle."""
+    import kvq
+    from kvq.synth import C5, c5_inputs
+    q, K, V = c5_inputs("cpu", T=T)
+    assert q.dtype == torch.bfloat16 and q.shape[1] == 64 and K.shape[1] == 8
+    cache = kvq.DctCache.from_context(K.cuda(), V.cuda(), window=W)
+    assert cache.T == (T - W) // 64 * 64
+    scaling = C5.d ** -0.5
+    out = kvq.dct_decode(q.cuda(), scaling, cache).float().cpu().numpy()
+    ref = _oracle(cache, q, scaling)
+    err = float(np.abs(out - ref).max())
+    print(f"C5-shaped bf16 T={T} W={W}: max-abs-err {err:.3e}")
+    assert err <= 1e-2, err
+
+
+def test_decode_r8_bf16_gqa8():
+    """bf16 at R = 8 with GQA 8 over two KV heads and batch 2 (a second bh layout of the same kernel).
+    Values are unit-scale: the 1e-2 bar is absolute, and bf16 rounding of outputs near 16 alone is
+    ~0.03 (a random-walk V of this length gave exactly that error, equal to bf16(ref) - ref)."""
+    import kvq
+    g = torch.Generator().manual_seed(808)
+    B, Hq, Hkv, T, W, d = 2, 16, 2, 3000, 56, 128
+    K = (torch.randn((B, Hkv, T, d), generator=g).cumsum(2) * 0.1).to(torch.bfloat16)
+    V = torch.randn((B, Hkv, T, d), generator=g).to(torch.bfloat16)
+    q = torch.randn((B, Hq, 1, d), generator=g).to(torch.bfloat16)
+    cache = kvq.DctCache.from_context(K.cuda(), V.cuda(), window=W)
+    out = kvq.dct_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
+    ref = _oracle(cache, q, d ** -0.5)
+    assert float(np.abs(out - ref).max()) <= 1e-2
+
+
 def test_decode_peaked_logits():
     """Large logits (one block dominates): the online maximum and lazy rescale path."""
     import kvq
@@ -115,3 +150,19 @@ def test_decode_peaked_logits():
     out = kvq.dct_decode(q.cuda(), d ** -0.5, cache).cpu().numpy()
     ref = _oracle(cache, q, d ** -0.5)
     assert float(np.abs(out - ref).max()) <= 2e-3
+
+
+def test_decode_many_query_tokens():
+    """Tq 7 at rep 4, in pieces of 2 query tokens and with an explicit chunk of 3 (pieces of 2):
+    against the oracle over all seven queries."""
+    import kvq
+    g = torch.Generator().manual_seed(77)
+    B, Hq, Hkv, Tq, T, W, d = 1, 8, 2, 7, 1300, 20, 128
+    K = (torch.randn((B, Hkv, T, d), generator=g).cumsum(2) * 0.2)
+    V = torch.randn((B, Hkv, T, d), generator=g)
+    q = torch.randn((B, Hq, Tq, d), generator=g)
+    cache = kvq.DctCache.from_context(K.cuda(), V.cuda(), window=W)
+    ref = _oracle(cache, q, d ** -0.5)
+    for chunk in (None, 3):
+        out = kvq.dct_decode(q.cuda(), d ** -0.5, cache, chunk=chunk).cpu().numpy()
+        assert float(np.abs(out - ref).max()) <= 2e-3

@@ -142,3 +142,19 @@ def test_phases_split_then_merge_equals_full():
         dec(qc, d ** -0.5, cache, workspace=ws, out=out, phases=1)
         dec(qc, d ** -0.5, cache, workspace=ws, out=out, phases=2)
         assert torch.equal(out, full)
+
+
+def test_decode_many_query_tokens():
+    """Tq 6 at rep 4: query-token pieces of 2 tokens (one launch each) against the oracle."""
+    import kvq
+    g = torch.Generator().manual_seed(66)
+    B, Hq, Hkv, Tq, T, W, d = 1, 8, 2, 6, 1100, 76, 128
+    K = (torch.randn((B, Hkv, T, d), generator=g) * 1.5 + 0.3)
+    V = torch.randn((B, Hkv, T, d), generator=g)
+    q = torch.randn((B, Hq, Tq, d), generator=g)
+    nb = (T - W) // 64
+    widths = torch.tensor([2, 4, 8])[torch.randint(0, 3, (B, Hkv, nb), generator=g)]
+    cache = kvq.MixedKIVICache.from_context(K.cuda(), V.cuda(), widths, window=W)
+    out = kvq.mixed_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
+    ref = _oracle(cache, K, V, widths.to(torch.int64), q, d ** -0.5)
+    assert float(np.abs(out - ref).max()) <= 2e-3

@@ -70,3 +70,15 @@ def test_quasar_rejects_bad_input():
         st.attend(torch.randn((1, 8, 1, 128)).cuda(), 0.1, [H, H + 1])
     with pytest.raises(RuntimeError):
         st.append(torch.zeros((1, 2, 1, 128)).cuda(), torch.zeros((1, 2, 1, 128)).cuda(), [H])
+
+
+def test_quasar_question_step_of_many_tokens():
+    """A 6-token step at rep 4 (24 rows per KV head): query pieces of 2 tokens, the appended rows
+    causal among them, against the oracle."""
+    dtype = torch.float32
+    st, p, K, V, H, g = _state(2, 900, 120, 6, (2, 2, 4), dtype, 21)
+    k = torch.randn((1, 2, 6, 128), generator=g).to(dtype)
+    v = torch.randn((1, 2, 6, 128), generator=g).to(dtype)
+    st.append(k.cuda(), v.cuda(), torch.arange(H, H + 6))
+    q = torch.randn((1, 8, 6, 128), generator=g).to(dtype)
+    _check(st, p, torch.cat([K, k], 2), torch.cat([V, v], 2), 120, H, q, list(range(H, H + 6)), (2, 2, 4), 2e-3)

@@ -78,3 +78,38 @@ def test_kivi_state_buffer_exhausted():
     st.append(K[:, :, :1], K[:, :, :1], [256])
     with pytest.raises(RuntimeError, match="decode buffer exhausted"):
         st.append(K[:, :, :1], K[:, :, :1], [257])
+
+
+@pytest.mark.parametrize("dtype,chunk", [(torch.bfloat16, None), (torch.float32, 3)])
+def test_question_step_of_many_tokens(dtype, chunk):
+    """The reference's run_tokens feeds a whole question in one step (STRATA_KV.py:3238-3248): 40
+    tokens at rep 4 through DecodeCtl (query pieces of 2 tokens, or of the controller's chunk),
+    causal among the appended rows, then a one-token step; against the oracle."""
+    import kvq
+    g = torch.Generator().manual_seed(40)
+    B, Hq, Hkv, H, W, d, gk, gv = 1, 32, 8, 700, 64, 128, 64, 64
+    steps = [40, 1]
+    T_all = H + sum(steps)
+    K = torch.randn((B, Hkv, T_all, d), generator=g).to(dtype)
+    V = torch.randn((B, Hkv, T_all, d), generator=g).to(dtype)
+    Q = torch.randn((B, Hq, sum(steps), d), generator=g).to(dtype)
+    st = kvq.KIVIState(K[:, :, :H].cuda(), V[:, :, :H].cuda(), window=W, group_k=gk, group_v=gv, extra=48)
+    ctl = kvq.DecodeCtl({0: st}, chunk=chunk)
+    module = SimpleNamespace(layer_idx=0, scaling=d ** -0.5)
+    tol = 2e-3 if dtype == torch.float32 else 1e-2
+    kn, vn = K.float().numpy(), V.float().numpy()
+    pos = H
+    with kvq.routed(ctl):
+        for t in steps:
+            qpos = torch.arange(pos, pos + t)
+            ctl.begin(qpos)
+            q = Q[:, :, pos - H:pos - H + t]
+            out, _ = kvq.router_attention(module, q.cuda(), K[:, :, pos:pos + t].cuda(), V[:, :, pos:pos + t].cuda(),
+                                          None)
+            assert out.shape == (B, t, Hq, d)
+            ref = _oracle_step(q.float().numpy(), kn[:, :, :pos + t], vn[:, :, :pos + t], H, W, gk, gv,
+                               qpos.numpy(), d ** -0.5)
+            err = float(np.abs(out.float().cpu().numpy() - ref).max())
+            assert err <= tol, (t, err)
+            pos += t
+

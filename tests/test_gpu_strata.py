@@ -139,3 +139,20 @@ def test_strata_decode_single_width_no_exact_rows(bits):
     out = kvq.strata_decode(q.cuda(), d ** -0.5, cache).cpu().numpy()
     ref = _oracle_out(cache, q, K, V, 0, d ** -0.5)
     assert float(np.abs(out - ref).max()) <= 2e-3
+
+
+def test_strata_decode_many_query_tokens():
+    """Tq 5 at rep 4 (20 rows per KV head): query-token pieces of 2, 2 and 1 tokens, each a full
+    decode launch, against the oracle over the whole block of queries."""
+    import kvq
+    g = torch.Generator().manual_seed(55)
+    B, Hq, Hkv, Tq, T, W, d = 1, 8, 2, 5, 600, 32, 128
+    K = (torch.randn((B, Hkv, T, d), generator=g) * 1.5 + 0.3)
+    V = torch.randn((B, Hkv, T, d), generator=g)
+    q = torch.randn((B, Hq, Tq, d), generator=g)
+    assign = _assign(B, Hkv, T - W, (0.1, 0.3, 0.5), g)
+    cache = kvq.StrataCache.from_context(K.cuda(), V.cuda(), window=W, assign=assign)
+    out = kvq.strata_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
+    ref = _oracle_out(cache, q, K, V, W, d ** -0.5)
+    assert out.shape == (B, Tq, Hq, d)
+    assert float(np.abs(out - ref).max()) <= 2e-3
