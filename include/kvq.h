@@ -146,6 +146,35 @@ int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int6
                     int64_t split_tokens, int phases, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * A4  kvq_kivi_decode without a workspace: the allocation-free variant.
+ * No counterpart in the reference.  It is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the caller
+ * passes inputs and outputs only, and the call allocates nothing.
+ *
+ * Arguments and results as kvq_kivi_decode, minus (workspace, workspace_floats).  The split
+ * partials and row statistics live in a static device array of KVQ_NOALLOC_SCRATCH_FLOATS
+ * floats (8 MiB), one copy per GPU, held until the process ends; its device address is looked
+ * up on the first call on each device.  The stream must belong to the current device.  A step
+ * whose kvq_kivi_decode_workspace(...) exceeds KVQ_NOALLOC_SCRATCH_FLOATS is rejected
+ * (KVQ_EINVAL) before any launch (C2, the 8B-shape layer at batch 16 and 32k tokens, needs
+ * 400,384).  Nothing in the scratch has to start at zero: every partial and statistic the merge
+ * and the score pass read is written earlier in the same call.  The scratch keeps the last
+ * call's contents, and every call on a GPU shares it: calls that overlap in time on one GPU
+ * (different streams without ordering) race and give wrong results.  Unlike every other entry
+ * point, this one keeps state between calls (the scratch and its per-device address).
+ * ---------------------------------------------------------------------------------------- */
+#define KVQ_NOALLOC_SCRATCH_FLOATS (1 << 21)
+int kvq_kivi_decode_noalloc(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling,
+                            const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_sc,
+                            const uint8_t* vc, const uint16_t* vmeta, int64_t cap_t, int64_t n_q,
+                            int group_k, int group_v, const void* k_exact, const void* v_exact,
+                            int exact_dtype, int64_t cap_e, int64_t n_exact, const int64_t* exact_pos,
+                            const int64_t* q_pos, void* out, int out_dtype, float* scores,
+                            int64_t scores_bh, float score_weight, int64_t split_tokens, int phases,
+                            void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * A7  Top-k retention of accumulated scores.  Replaces scores.topk(k).indices.sort() of the
  * SnapKV / MTLP selection (STRATA_KV.py:975, 1022-1023): for each of BH rows of n float32
  * scores (row stride scores_bh), writes the positions of the k largest in increasing order to

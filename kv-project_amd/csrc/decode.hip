@@ -37,6 +37,8 @@
 //   Codes become fp16 operands with one and each: a nibble masked in place is the fp16 subnormal
 //   c*2^-24 (low nibble) or 16c*2^-24 (high nibble, its operand column pre-divided by 16); the
 //   matrix core keeps subnormal inputs, so codes enter exactly and no offset has to be cancelled.
+#include <atomic>
+#include <mutex>
 #include <algorithm>
 
 #include "common.hpp"
@@ -899,6 +901,59 @@ inline SplitPlan plan_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int6
   return sp;
 }
 
+// ---- the allocation-free entry point's scratch ------------------------------------------------
+// kvq_kivi_decode_noalloc keeps the split partials and row statistics (what kvq_kivi_decode keeps in
+// its workspace argument) in this array.  Every GPU the library runs on holds its own copy for the
+// life of the process.  In host code `scratch` names a host-side stand-in, never the device array:
+// the device address of each GPU's copy comes from hipGetSymbolAddress, once per device, with that
+// device current, and only that address is passed to kernels.
+constexpr int64_t kScratchFloats = KVQ_NOALLOC_SCRATCH_FLOATS;      // 8 MiB per GPU
+__device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch (looked up on the first call on that device).
+// The stream must belong to the current device: its kernels read that device's copy.
+int current_scratch(void* stream, float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("kvq_kivi_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return KVQ_EHIP;
+  }
+  KVQ_REQUIRE(dev >= 0 && dev < kMaxDevices, "kvq_kivi_decode_noalloc: device %d out of range", dev);
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) {
+      set_error("kvq_kivi_decode_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+      return KVQ_EHIP;
+    }
+    KVQ_REQUIRE(sdev == dev, "kvq_kivi_decode_noalloc: the stream belongs to device %d but device %d is current",
+                (int)sdev, dev);
+  }
+  float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || addr == nullptr) {
+        set_error("kvq_kivi_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+        return KVQ_EHIP;
+      }
+      p = static_cast<float*>(addr);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return KVQ_OK;
+}
+
 }  // namespace
 }  // namespace kvq
 
@@ -995,4 +1050,27 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   }
 #undef KVQ_R
 #undef KVQ_GV
+}
+
+extern "C" int kvq_kivi_decode_noalloc(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
+                                       float scaling, const uint8_t* kc, const uint16_t* k_lo,
+                                       const uint16_t* k_sc, const uint8_t* vc, const uint16_t* vmeta,
+                                       int64_t cap_t, int64_t n_q, int group_k, int group_v,
+                                       const void* k_exact, const void* v_exact, int exact_dtype,
+                                       int64_t cap_e, int64_t n_exact, const int64_t* exact_pos,
+                                       const int64_t* q_pos, void* out, int out_dtype, float* scores,
+                                       int64_t scores_bh, float score_weight, int64_t split_tokens,
+                                       int phases, void* stream) {
+  // shapes the planner rejects fall through to kvq_kivi_decode, which names what is wrong
+  const int64_t need = kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, d, n_q, n_exact, group_k, group_v, split_tokens);
+  KVQ_REQUIRE(need <= kScratchFloats,
+              "kvq_kivi_decode_noalloc: this step needs %lld scratch floats, more than the static scratch of "
+              "%lld (call kvq_kivi_decode with a workspace instead)", (long long)need, (long long)kScratchFloats);
+  float* ws = nullptr;
+  const int rc = current_scratch(stream, &ws);
+  if (rc != KVQ_OK) return rc;
+  return kvq_kivi_decode(q, q_dtype, q_sb, q_sh, q_st, B, Hq, Hkv, Tq, d, scaling, kc, k_lo, k_sc, vc, vmeta, cap_t,
+                         n_q, group_k, group_v, k_exact, v_exact, exact_dtype, cap_e, n_exact, exact_pos, q_pos, out,
+                         out_dtype, ws, kScratchFloats, scores, scores_bh, score_weight, split_tokens, phases, stream);
 }

@@ -193,7 +193,8 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
                 q_pos: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                 workspace: Optional[torch.Tensor] = None, split_tokens: int = 0,
                 phases: Optional[int] = None, scores: Optional[torch.Tensor] = None,
-                score_weight: float = 1.0, chunk: Optional[int] = None) -> torch.Tensor:
+                score_weight: float = 1.0, chunk: Optional[int] = None,
+                static_scratch: bool = False) -> torch.Tensor:
     """Attention of q (B, Hq, Tq, d) over the packed cache; returns (B, Tq, Hq, d) in q's dtype.
 
     Any Tq: a step with more than 8 // rep query tokens (or more than ``chunk``) runs as
@@ -206,7 +207,12 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
 
     ``scores`` (B, Hkv, >= n_q) float32 on the GPU: the step also adds ``score_weight`` times the
     probability mass each packed token received from the query heads of its KV group (the
-    decode-time accumulation of the eviction path)."""
+    decode-time accumulation of the eviction path).
+
+    ``static_scratch``: run through kvq_kivi_decode_noalloc, which keeps the split partials in the
+    library's static per-GPU scratch instead of a workspace (no device allocation in the call;
+    pass ``out`` too for a step that allocates nothing).  Steps on one GPU that use it must not
+    overlap in time."""
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.kc.shape[1]
@@ -216,7 +222,8 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
             raise ValueError("a chunked query step runs whole steps (phases 3 or 7)")
         return decode_in_pieces(
             lambda qs, qp: kivi_decode(qs, scaling, cache, q_pos=qp, workspace=workspace, split_tokens=split_tokens,
-                                       phases=phases, scores=scores, score_weight=score_weight),
+                                       phases=phases, scores=scores, score_weight=score_weight,
+                                       static_scratch=static_scratch),
             q, q_pos, out, pieces)
     if q.stride(-1) != 1:
         q = q.contiguous()
@@ -224,7 +231,9 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
         raise TypeError("q and the exact rows must share a dtype")
     if out is None:
         out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
-    if workspace is None:                      # a caller's workspace is size-checked by the library
+    if static_scratch and workspace is not None:
+        raise ValueError("static_scratch takes no workspace")
+    if workspace is None and not static_scratch:   # a caller's workspace is size-checked by the library
         need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, cache.group_v,
                                 split_tokens)
         workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)
@@ -238,6 +247,16 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
     ep = cache.exact_pos if q_pos is not None else None
     qp = q_pos if ep is not None else None
     dt = _lib.DTYPE_CODE[q.dtype]
+    if static_scratch:
+        _lib.call("kvq_kivi_decode_noalloc", q.data_ptr(), dt, q.stride(0), q.stride(1), q.stride(2),
+                  B, Hq, Hkv, Tq, d, float(scaling),
+                  cache.kc.data_ptr(), cache.k_lo.data_ptr(), cache.k_sc.data_ptr(), cache.vc.data_ptr(),
+                  cache.vmeta.data_ptr(), cache.cap_t, cache.n_q, cache.group_k, cache.group_v,
+                  cache.k_exact.data_ptr(), cache.v_exact.data_ptr(), dt, cache.cap_e, cache.n_exact,
+                  _lib.ptr(ep), _lib.ptr(qp), out.data_ptr(), dt,
+                  _lib.ptr(scores), scores.stride(1) if scores is not None else 0, float(score_weight),
+                  split_tokens, phases, _lib.stream_of(q))
+        return out
     _lib.call("kvq_kivi_decode", q.data_ptr(), dt, q.stride(0), q.stride(1), q.stride(2),
               B, Hq, Hkv, Tq, d, float(scaling),
               cache.kc.data_ptr(), cache.k_lo.data_ptr(), cache.k_sc.data_ptr(), cache.vc.data_ptr(),

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/kvq.h but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert lib.kvq_abi_version() == 10
+    assert lib.kvq_abi_version() == 11
     assert lib.kvq_last_error() == b""
 
 
@@ -61,3 +61,16 @@ def test_split_plan_fills_one_round():
     assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 0, 100, 32, 32, 0) == 8 * (0 * 1 * (d + 2) + 2)
     assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 0, 2304, 32, 32, 0) == 8 * (36 * 1 * (d + 2) + 2)
     assert lib.kvq_kivi_decode_workspace(1, 8, 8, 1, 128, 64, 0, 32, 32, 0) == 8 * (1 * 1 * (d + 2) + 2)
+
+
+def test_noalloc_rejects_steps_beyond_the_static_scratch():
+    """kvq_kivi_decode_noalloc refuses, before touching the device, a step whose partials exceed its
+    static scratch (KVQ_NOALLOC_SCRATCH_FLOATS = 2^21 floats); C2 itself fits (400,384)."""
+    from kvq import _lib
+    lib = _lib.load()
+    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 0) <= 1 << 21
+    assert lib.kvq_kivi_decode_workspace(512, 32, 8, 1, 128, 32640, 128, 64, 64, 0) > 1 << 21
+    rc = lib.kvq_kivi_decode_noalloc(None, 2, 0, 0, 0, 512, 32, 8, 1, 128, 0.1, None, None, None, None, None,
+                                     32640, 32640, 64, 64, None, None, 2, 128, 128, None, None, None, 2, None, 0,
+                                     0.0, 0, 3, None)
+    assert rc == 1 and b"static scratch" in lib.kvq_last_error()
