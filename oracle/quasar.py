@@ -14,7 +14,10 @@ Reference:
   * ``QuasarState.__init__`` step table (1883-1898): per side, in step order, [byte offset in the
     side's flat code buffer, n_s, bytes per row, first coefficient a, width w, bits, level offset].
 
-Pinning (tests/test_oracle_quasar.py):
+Pinning (tests/test_oracle_quasar.py, tests/test_golden.py):
+  * golden vectors written by the reference's own functions (tests/golden/quasar_codebooks.npz):
+    ``lloyd_max_gaussian`` levels at 1-4 bits, the stage codebooks of (2, 2, 4), (4, 4) and (8,)
+    and ``embedded_quantize`` codes of seeded coefficients, all bit-equal.
   * ``lloyd_max_gaussian`` against Max's (1960) table of the Gaussian Lloyd-Max MSE at 1-4 bits
     (0.3634 / 0.1175 / 0.03454 / 0.009497, the values STRATA_KV.py:1085-1087 quotes).
   * ``stage_codebooks`` against the MSE the reference states for the (2, 2, 4) embedded code

@@ -22,13 +22,17 @@ Fixed arithmetic order (what the GPU kernels compute, restated here so both agre
     stages h = 1, 2, 4, ..., d/2, then a float32 multiply by float32(1/sqrt(d)); it equals the
     reference's dense (X - mu) @ R.T up to float32 rounding.
 
-Pinning (tests/test_oracle_strata.py): rotation orthogonality (1e-6; the reference's own check is
-1e-5 at 1918) and FWHT == dense product with the reference's matrix; uniform_step against the
-reference's KAT UNIFORM_1960 (four decimals, 1912) -- its exact float is otherwise PARITY
-UNPINNED (only an import of the reference could fix it; this restates the same procedure);
-strata_quantize by hand KATs and a nearest-level brute force; planar packing by KAT bytes and
-round trips; the tier decode by the reference's identity "decode over the strata == attention
-over the reconstructions mu + y_hat R" (1e-4 at 1983-1985) against chunked_attention.
+Pinning (tests/test_oracle_strata.py, tests/test_golden.py): golden vectors written by the
+reference's own functions (tests/golden/strata_codec.npz): uniform_step floats for 1..8 bits
+bit-equal, the rotation signs for d = 64, 128 equal, and one side's compression on seeded fp32
+rows -- fp16 means bit-equal, the FWHT rows within 1e-6 of the reference's dense product, codes
+and scales at 2, 4 and 8 bits bit-equal on the reference's rows and end to end (the float64 sums
+and the FWHT order give the reference's codes on these rows: no mismatch in 73,728); also
+rotation orthogonality (1e-6; the reference's own check is 1e-5 at 1918), the reference's KAT
+UNIFORM_1960 (1912), strata_quantize by hand KATs and a nearest-level brute force, planar packing
+by KAT bytes and round trips, and the tier decode by the reference's identity "decode over the
+strata == attention over the reconstructions mu + y_hat R" (1e-4 at 1983-1985) against
+chunked_attention.
 """
 from __future__ import annotations
 

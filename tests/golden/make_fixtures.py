@@ -1,0 +1,122 @@
+"""Write the golden vectors under tests/golden/ from the reference's own functions.
+
+Runs only in the build container, where the reference (TahirSher/KV-Project) is readable:
+
+    python tests/golden/make_fixtures.py [--reference /root/reference]
+
+It imports STRATA_KV.py and QUASAR_KV.py with KV_PROJECT_ROOT / KV_STRATA_OUTPUT_DIR pointed at a
+temporary directory (their Config() creates output folders under the project root) and writes,
+for the functions whose exact floats or draws nothing but the reference itself fixes:
+
+  strata_codec.npz     uniform_step(b) for b = 1..8 (step, mse; STRATA_KV.py:1132-1155);
+                       rotation signs of rotation_matrix(d, "strata") for d = 64, 128 (1110-1128);
+                       one side's compression as compress_layer does it (1546-1548): seeded fp32
+                       rows X (Hkv, n, d), mu = as_stored(X.mean(1)), Y = (X - mu) @ R.T, and
+                       strata_quantize(Y, b) codes and scales for b = 2, 4, 8 (1158-1168)
+  quasar_codebooks.npz lloyd_max_gaussian(b), b = 1..4 (STRATA_KV.py:1082-1098); stage_codebooks
+                       for (2, 2, 4), (4, 4), (8,) (QUASAR_KV.py:1143-1169) and
+                       embedded_quantize codes of seeded coefficients (1172-1183)
+  coverage_groups.npz  coverage_groups(H, cfg) (STRATA_KV.py:1206-1222) for several H under the
+                       default Config and the reference's test config (1964)
+
+The tests load these files; nothing on the GPU box reads the reference.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import os
+import sys
+import tempfile
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+
+
+def _load(ref: Path, name: str):
+    spec = importlib.util.spec_from_file_location(name, ref / f"{name}.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def strata_codec(S) -> dict:
+    import torch
+    out = {}
+    steps = np.array([S.uniform_step(b)[0] for b in range(1, 9)], np.float64)
+    mses = np.array([S.uniform_step(b)[1] for b in range(1, 9)], np.float64)
+    out["uniform_step"], out["uniform_mse"] = steps, mses
+    for d in (64, 128):
+        R = S.rotation_matrix(d, "strata").double().numpy()
+        out[f"signs_{d}"] = np.round(R[0] * np.sqrt(d)).astype(np.int8)    # row 0 of H_d is all ones
+    rng = np.random.default_rng(20260101)
+    Hkv, n, d = 2, 96, 128
+    mag = np.abs(rng.standard_t(3, size=(Hkv, 1, d))) + 0.1            # heavy-tailed channel scales
+    X = (rng.standard_normal((Hkv, n, d)) * mag + rng.standard_normal((Hkv, 1, d))).astype(np.float32)
+    X[0, 5] = X[0, 5].mean()                                           # a row equal to its mean: tiny rms
+    X[1, 7] *= 40.0                                                    # one large row
+    Xt = torch.from_numpy(X)
+    R = S.rotation_matrix(d, "strata")
+    mu = S.as_stored(Xt.mean(1, keepdim=True))
+    Y = (Xt - mu) @ R.T
+    out["X"], out["mu"], out["Y"] = X, mu.numpy().astype(np.float32), Y.numpy().astype(np.float32)
+    for b in (2, 4, 8):
+        c, s, _ = S.strata_quantize(Y, b)
+        out[f"codes_{b}"], out[f"scales_{b}"] = c.numpy(), s.numpy().astype(np.float32)
+    return out
+
+
+def quasar_codebooks(S, Q) -> dict:
+    import torch
+    out = {}
+    for b in range(1, 5):
+        out[f"lloyd_{b}"] = S.lloyd_max_gaussian(b).numpy()
+    rng = np.random.default_rng(20260102)
+    u = torch.from_numpy(rng.standard_normal((2, 64, 16)).astype(np.float32))
+    out["u"] = u.numpy()
+    for stages in ((2, 2, 4), (4, 4), (8,)):
+        tag = "_".join(map(str, stages))
+        for t, cb in enumerate(Q.stage_codebooks(stages)):
+            out[f"levels_{tag}_{t}"] = cb.numpy()
+        codes, _ = Q.embedded_quantize(u, stages)
+        for t, c in enumerate(codes):
+            out[f"codes_{tag}_{t}"] = c.numpy()
+    return out
+
+
+def coverage_groups(S) -> dict:
+    from dataclasses import replace
+    out = {}
+    cfgs = {"default": S.Config(), "test": replace(S.Config(), STRATA_SEGMENT=64, STRATA_QUERIES=8, STRATA_LOCAL=16)}
+    for name, cfg in cfgs.items():
+        out[f"{name}_params"] = np.array([cfg.N_SINK, cfg.STRATA_LOCAL, cfg.W_OBS, cfg.STRATA_SEGMENT,
+                                          cfg.STRATA_QUERIES], np.int64)
+        for H in (200, 700, 1500, 4100):
+            groups = S.coverage_groups(H, cfg)
+            out[f"{name}_{H}_lengths"] = np.array([len(g) for g in groups], np.int64)
+            out[f"{name}_{H}_positions"] = np.concatenate(groups).astype(np.int64)
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--reference", default="/root/reference")
+    a = ap.parse_args()
+    ref = Path(a.reference)
+    tmp = tempfile.mkdtemp(prefix="kvref_")
+    os.environ["KV_PROJECT_ROOT"] = tmp
+    os.environ["KV_STRATA_OUTPUT_DIR"] = tmp
+    S = _load(ref, "STRATA_KV")
+    Q = _load(ref, "QUASAR_KV")
+    for name, data in (("strata_codec", strata_codec(S)), ("quasar_codebooks", quasar_codebooks(S, Q)),
+                       ("coverage_groups", coverage_groups(S))):
+        np.savez_compressed(HERE / f"{name}.npz", **data)
+        print(f"wrote {name}.npz ({(HERE / f'{name}.npz').stat().st_size} bytes, {len(data)} arrays)")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

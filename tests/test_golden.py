@@ -1,0 +1,74 @@
+"""The oracle and the package's host-side restatements against golden vectors written by the
+reference's own functions (tests/golden/make_fixtures.py, run in the build container only).
+
+These pin what only the reference fixes exactly:
+  * uniform_step(b) floats, b = 1..8 (STRATA_KV.py:1132-1155): bit-equal;
+  * rotation_matrix(d, "strata") signs, d = 64, 128 (1110-1128, _rng 306-307): equal;
+  * one side's compression (1546-1548 + strata_quantize 1158-1168) on seeded fp32 rows: the fp16
+    means bit-equal; Y within float32 rounding of the reference's dense (X - mu) @ R.T (the
+    oracle's FWHT order); codes and fp16 scales at 2, 4 and 8 bits bit-equal both on the
+    reference's own Y and end to end from X;
+  * lloyd_max_gaussian levels, b = 1..4 (STRATA_KV.py:1082-1098), the QUASAR stage codebooks
+    (QUASAR_KV.py:1143-1169) and embedded_quantize codes (1172-1183): bit-equal.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle.quasar as oq
+import oracle.strata as os_
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.fixture(scope="module")
+def codec():
+    return np.load(GOLD / "strata_codec.npz")
+
+
+@pytest.fixture(scope="module")
+def books():
+    return np.load(GOLD / "quasar_codebooks.npz")
+
+
+def test_uniform_step_floats(codec):
+    from kvq.strata import uniform_step
+    for b in range(1, 9):
+        step, mse = os_.uniform_step(b)
+        assert step == codec["uniform_step"][b - 1] and mse == codec["uniform_mse"][b - 1], b
+        assert uniform_step(b) == codec["uniform_step"][b - 1], b      # the package's host copy
+
+
+def test_rotation_signs(codec):
+    from kvq.strata import _signs_np
+    for d in (64, 128):
+        np.testing.assert_array_equal(os_.rotation_signs(d).astype(np.int8), codec[f"signs_{d}"])
+        np.testing.assert_array_equal(_signs_np(d, "strata").astype(np.int8), codec[f"signs_{d}"])
+
+
+def test_center_rotate_and_quantize(codec):
+    X, mu, Y = codec["X"], codec["mu"], codec["Y"]
+    mu_o, Y_o = os_.strata_center_rotate(X, os_.rotation_signs(128))
+    np.testing.assert_array_equal(mu_o, mu[:, 0])
+    assert np.abs(Y_o - Y).max() <= 1e-6 * np.abs(Y).max()
+    for b in (2, 4, 8):
+        step = os_.uniform_step(b)[0]
+        for y in (Y, Y_o):
+            c, s, _ = os_.strata_quantize(y, b, step)
+            np.testing.assert_array_equal(c, codec[f"codes_{b}"])
+            np.testing.assert_array_equal(s, codec[f"scales_{b}"])
+
+
+def test_lloyd_max_and_stage_codebooks(books):
+    from kvq.quasar import stage_codebooks as pkg_books
+    for b in range(1, 5):
+        np.testing.assert_array_equal(np.asarray(oq.lloyd_max_gaussian(b), np.float32), books[f"lloyd_{b}"])
+    for stages in ((2, 2, 4), (4, 4), (8,)):
+        tag = "_".join(map(str, stages))
+        for t, (cb_o, cb_p) in enumerate(zip(oq.stage_codebooks(stages), pkg_books(stages))):
+            np.testing.assert_array_equal(np.asarray(cb_o, np.float32), books[f"levels_{tag}_{t}"])
+            np.testing.assert_array_equal(np.asarray(cb_p, np.float32), books[f"levels_{tag}_{t}"])
+        codes = oq.embedded_quantize(books["u"], stages)
+        for t, c in enumerate(codes):
+            np.testing.assert_array_equal(np.asarray(c, np.uint8), books[f"codes_{tag}_{t}"])
