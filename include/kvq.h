@@ -264,6 +264,25 @@ int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, in
                       const int64_t* q_pos, void* out, float* workspace, int64_t workspace_floats, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * A6  Flash-decoding partials of ONE stratum for a pre-rotated query.  Replaces the reference's
+ * kernel wrapper strata_tier_kernel(qr, qb, t, target_programs) (STRATA_KV.py:1450-1469, the
+ * Triton kernel 1374-1447), whose partials StrataState.attend merges (1782-1792).
+ *
+ * qr (BH, rows, d) float32 = scaling * q R^T (rotated, scaled query rows), qb (BH, rows) float32 =
+ * scaling * q . mu_K.  The stratum: n tokens, kc (BH, n, d*bits/8) pack_planar rows, ks (BH, cap)
+ * fp16 key scales zero past n, vt / vsl its value tiles and slot-ordered scales of capacity cap
+ * (kvq_strata_v_tile).  The n tokens are cut into n_split splits (1 <= n_split <= ceil(n/32)).
+ * Outputs, as the reference's: m, l, z (BH, n_split, rows) and acc (BH, n_split, rows, d) float32
+ * in the rotated value basis, natural exponent: m = max logit, l = sum e^(s - m),
+ * acc + z = sum e^(s - m) vs (c - (2^bits - 1)/2) (the offset is folded into acc; z = 0, as the
+ * reference's tier_reference returns).  Any rows (launches of 8 rows).  d = 128.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_strata_tier_partials(const float* qr, const float* qb, int64_t BH, int64_t rows, int64_t d, int bits,
+                             int64_t n, const uint8_t* kc, const uint16_t* ks, const uint8_t* vt,
+                             const uint16_t* vsl, int64_t cap, int64_t n_split, float* m, float* l, float* acc,
+                             float* z, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * C3  Mixed-width KIVI blocks.  Every 64-token block of a (b, h) has its own width b in
  * {2, 4, 8}; inside it the codes and fp16 metadata are kivi_quant's (STRATA_KV.py:826-856) at
  * that width with group 32.  The reference keeps one dense tensor per width and launches once per

@@ -488,7 +488,22 @@ struct StrataParams {
   const float* ex_l;
   int S_ex;
   void* out;
+  // pre-rotated query rows (kvq_strata_tier_partials): qr (BH, qr_rows, d) = scaling * q R^T and
+  // qb (BH, qr_rows) = scaling * q . mu_K; the launch takes rows [qr_r0, qr_r0 + R_real).  Null: the
+  // query is read from q and rotated here.
+  const float* qr;
+  const float* qb;
+  int qr_rows, qr_r0;
+  // partials in the reference's layout and units (natural exponent): m, l, z (BH, S_all, qr_rows),
+  // acc (BH, S_all, qr_rows, d).  Null: partials go to the decode's workspace (base 2).
+  float* t_m;
+  float* t_l;
+  float* t_acc;
+  float* t_z;
 };
+
+constexpr float kStrataLog2e = 1.4426950408889634f;
+constexpr float kStrataLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ int64_t strata_q_offset(const StrataParams& p, int b, int h, int r) {
   const int hq = h * p.rep + r / p.Tq, t = r % p.Tq;
@@ -523,8 +538,13 @@ __device__ void strata_block(const StrataParams& p, const StrataTierArg& ta, int
 
   // ---- query rows: q^ = FWHT(q * s) / sqrt(d) * qscale, sum(q^), qb = qscale * q . mu_K ----
   for (int r = wave; r < R; r += kSWaves) {
-    float v0 = 0.0f, v1 = 0.0f, mk = 0.0f;
-    if (r < p.R_real) {
+    float v0 = 0.0f, v1 = 0.0f, mk = 0.0f, qbv = 0.0f;
+    if (r < p.R_real && p.qr != nullptr) {
+      const int64_t qo = static_cast<int64_t>(bh) * p.qr_rows + p.qr_r0 + r;
+      v0 = p.qr[qo * kSD + l] * kStrataLog2e;
+      v1 = p.qr[qo * kSD + l + 64] * kStrataLog2e;
+      qbv = p.qb[qo] * kStrataLog2e;
+    } else if (r < p.R_real) {
       const int64_t qo = strata_q_offset(p, b, h, r);
       const float x0 = load_as_f32<DT>(p.q, qo + l), x1 = load_as_f32<DT>(p.q, qo + l + 64);
       mk = x0 * f16_to_f32(p.mu_k[static_cast<int64_t>(bh) * kSD + l]) +
@@ -542,7 +562,7 @@ __device__ void strata_block(const StrataParams& p, const StrataTierArg& ta, int
     mk = wave_sum(mk);
     if (l == 0) {
       qsum[r] = su;
-      qbias[r] = mk * p.qscale;
+      qbias[r] = p.qr != nullptr ? qbv : mk * p.qscale;
     }
   }
   __syncthreads();
@@ -751,10 +771,21 @@ __device__ void strata_block(const StrataParams& p, const StrataTierArg& ta, int
       O += wgt * red_o[(w * R + r) * kSD + c];
       L += wgt * red_ml[(w * 2 + 1) * R + r];
     }
-    p.ws_o[(po * R + r) * kSD + c] = O;
-    if (c == 0) {
-      p.ws_m[po * R + r] = M;
-      p.ws_l[po * R + r] = L;
+    if (p.t_m != nullptr) {
+      // the reference's partial (m, l, acc, z): natural exponent, the value offset folded into acc
+      const int64_t to = po * p.qr_rows + p.qr_r0 + r;
+      p.t_acc[to * kSD + c] = O;
+      if (c == 0) {
+        p.t_m[to] = M * kStrataLn2;
+        p.t_l[to] = L;
+        p.t_z[to] = 0.0f;
+      }
+    } else {
+      p.ws_o[(po * R + r) * kSD + c] = O;
+      if (c == 0) {
+        p.ws_m[po * R + r] = M;
+        p.ws_l[po * R + r] = L;
+      }
     }
   }
 }
@@ -1044,6 +1075,52 @@ extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64
 #undef KVQ_STRATA_MR
 #undef KVQ_STRATA_MERGE
   KVQ_LAUNCH_CHECK("kvq_strata_decode(merge)");
+  return KVQ_OK;
+}
+
+extern "C" int kvq_strata_tier_partials(const float* qr, const float* qb, int64_t BH, int64_t rows, int64_t d,
+                                        int bits, int64_t n, const uint8_t* kc, const uint16_t* ks,
+                                        const uint8_t* vt, const uint16_t* vsl, int64_t cap, int64_t n_split,
+                                        float* m, float* l, float* acc, float* z, void* stream) {
+  using namespace kvq;
+  KVQ_REQUIRE(d == 128, "kvq_strata_tier_partials: head_dim must be 128");
+  KVQ_REQUIRE(bits == 2 || bits == 4 || bits == 8, "kvq_strata_tier_partials: bits in {2,4,8}");
+  KVQ_REQUIRE(BH > 0 && BH < 65536 && rows > 0 && rows < (1 << 20), "kvq_strata_tier_partials: bad head / row counts");
+  KVQ_REQUIRE(n > 0 && n < (1LL << 30) && cap % 32 == 0 && n <= cap,
+              "kvq_strata_tier_partials: need 0 < n <= cap, cap a multiple of 32");
+  KVQ_REQUIRE(n_split > 0 && n_split <= (n + 31) / 32 && n_split * BH < (1LL << 31),
+              "kvq_strata_tier_partials: n_split must be in [1, ceil(n / 32)]");
+  KVQ_REQUIRE(qr && qb && kc && ks && vt && vsl && m && l && acc && z, "kvq_strata_tier_partials: null pointer");
+  StrataParams p{};
+  p.BH = static_cast<int>(BH);
+  p.Hkv = static_cast<int>(BH);
+  p.qr = qr;
+  p.qb = qb;
+  p.qr_rows = static_cast<int>(rows);
+  p.t_m = m; p.t_l = l; p.t_acc = acc; p.t_z = z;
+  p.n_tiers = 1;
+  StrataTierArg& ta = p.tiers[0];
+  ta.kc = kc; ta.ks = ks; ta.vt = vt; ta.vsl = vsl;
+  ta.n_t = n; ta.cap_t = cap; ta.n_split = static_cast<int>(n_split); ta.s_base = 0; ta.bits = bits;
+  p.S_all = static_cast<int>(n_split);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int bh_pad = (p.BH + 7) / 8 * 8;
+  const dim3 grid(static_cast<unsigned>(n_split) * bh_pad);
+  // the split kernel holds at most 8 query rows per KV head: rows go in launches of 8
+  for (int64_t r0 = 0; r0 < rows; r0 += 8) {
+    p.qr_r0 = static_cast<int>(r0);
+    p.R_real = static_cast<int>(std::min<int64_t>(8, rows - r0));
+    const int R = strata_pow2(p.R_real);
+    const size_t smem = std::max<size_t>((R * kSD + 2 * R) * sizeof(float),
+                                         (kSWaves * R * kSD + kSWaves * 2 * R) * sizeof(float));
+    switch (R) {
+      case 1: hipLaunchKernelGGL((strata_split_all<1, KVQ_F32, 3>), grid, dim3(kSThreads), smem, s, p); break;
+      case 2: hipLaunchKernelGGL((strata_split_all<2, KVQ_F32, 3>), grid, dim3(kSThreads), smem, s, p); break;
+      case 4: hipLaunchKernelGGL((strata_split_all<4, KVQ_F32, 3>), grid, dim3(kSThreads), smem, s, p); break;
+      default: hipLaunchKernelGGL((strata_split_all<8, KVQ_F32, 3>), grid, dim3(kSThreads), smem, s, p); break;
+    }
+    KVQ_LAUNCH_CHECK("kvq_strata_tier_partials");
+  }
   return KVQ_OK;
 }
 

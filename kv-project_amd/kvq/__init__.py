@@ -14,6 +14,7 @@ from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strat
                      strata_quantize, strata_v_tile, strata_workspace_floats, uniform_step, unpack_planar)
 from .dct import DctCache, dct_decode, dct_encode, dct_table, dct_workspace_floats
 from .mixed import MixedKIVICache, c3_widths, mixed_decode, mixed_workspace_floats, offset_table
+from .strata_state import StrataState, strata_pack, strata_tier_kernel
 from .quasar import QuasarState, stage_codebooks
 from .alloc import AllocWorkspace, allocate_layer, layer_costs, strata_allocate, strata_distortion
 
@@ -25,6 +26,6 @@ __all__ = [
     "uniform_step", "strata_center_rotate", "strata_quantize", "strata_v_tile", "StrataCache", "StrataTier",
     "strata_decode", "strata_workspace_floats", "DctCache", "dct_decode", "dct_encode", "dct_table",
     "dct_workspace_floats", "MixedKIVICache", "c3_widths", "mixed_decode", "mixed_workspace_floats", "offset_table",
-    "QuasarState", "stage_codebooks", "payload_bytes", "AllocWorkspace", "allocate_layer", "layer_costs",
+    "StrataState", "strata_pack", "strata_tier_kernel", "QuasarState", "stage_codebooks", "payload_bytes", "AllocWorkspace", "allocate_layer", "layer_costs",
     "strata_allocate", "strata_distortion",
 ]

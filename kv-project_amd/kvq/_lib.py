@@ -52,6 +52,7 @@ SIGNATURES = {
     "kvq_strata_decode_workspace": (i64, [i64, i64, i64, i64, i64, i64, i32, vp, vp]),
     "kvq_strata_decode": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32, vp, vp, vp, i32, vp, vp, vp,
                                 vp, vp, vp, vp, vp, vp, i64, i64, vp, vp, vp, vp, i64, vp]),
+    "kvq_strata_tier_partials": (i32, [vp, vp, i64, i64, i64, i32, i64, vp, vp, vp, vp, i64, i64, vp, vp, vp, vp, vp]),
     "kvq_dct_encode": (i32, [vp, i32, i64, i64, i64, i64, vp, i32, vp, vp, vp]),
     "kvq_dct_decode_workspace": (i64, [i64, i64, i64, i64, i64, i64, i64]),
     "kvq_dct_decode": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32, vp, i64, vp, vp, vp, vp,
