@@ -186,6 +186,26 @@ int kvq_topk_retain(const float* scores, int64_t BH, int64_t n, int64_t scores_b
                     int32_t* idx, int64_t idx_bh, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * A7  SnapKV scores of a prefilled context.  Replaces snapkv_scores (STRATA_KV.py:932-954), the
+ * selection of SnapKVMethod.entries (969-981) and of MTLP (1010-1023).
+ *
+ * q: the `window` observation queries of every query head, element (b, head, i, c) at
+ *    q + b*q_sb + head*q_sh + i*q_st + c (query i at position H - window + i; the caller passes the
+ *    view q[:, :, H - window:H]); k: (b, h, j, c) at k + b*k_sb + h*k_sh + j*k_st + c, j < H.  Both
+ *    of `dtype`, channels contiguous, rows 16-byte aligned, d = 128; KV head h serves query heads
+ *    h*rep .. h*rep + rep - 1 (STRATA_KV.py:527-529).
+ * out (B*Hkv, H) float32: for j < H - window, the probability of key j under the causal fp32 softmax
+ *    of scaling * q.k, averaged over the window queries and the rep heads, then avg_pool1d(kernel,
+ *    padding kernel / 2, zeros counted); columns j >= H - window get (largest score of the whole
+ *    call) + 1.  kernel odd, at most 65.  workspace: kvq_snapkv_scores_workspace(...) floats.
+ * ---------------------------------------------------------------------------------------- */
+int64_t kvq_snapkv_scores_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t window, int64_t H, int dtype);
+int kvq_snapkv_scores(const void* q, int dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k,
+                      int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t B, int64_t Hq, int64_t Hkv, int64_t d,
+                      int64_t window, int64_t H, float scaling, int kernel, float* out, float* workspace,
+                      int64_t workspace_floats, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * A7  Retained-set rows for the gathered decode.  For each (b, h) and i < count, position
  * t = idx[bh*idx_bh + i] of the packed cache (layout as kvq_kivi_decode) is dequantised the way
  * kivi_quant's xhat is (code * scale + lo in fp32, STRATA_KV.py:855) and written, rounded to

@@ -21,6 +21,55 @@ from . import _lib
 from .decode import PackedKIVICache
 
 
+SNAPKV_WINDOW, SNAPKV_KERNEL = 64, 5           # the reference's defaults (STRATA_KV.py:418-419)
+
+
+def _window_rows(q, H: int, w: int) -> torch.Tensor:
+    """The observation queries at positions H - w .. H - 1: q (B, Hq, >= H, d), or an object with
+    the reference's QRows.at(positions) (q_at, STRATA_KV.py:3173-3175)."""
+    pos = torch.arange(H - w, H)
+    if hasattr(q, "at"):
+        return q.at(pos)
+    return q[:, :, H - w:H]
+
+
+@torch.no_grad()
+def snapkv_scores(q, k: torch.Tensor, H: int, scaling: float, cfg=None, out: torch.Tensor | None = None,
+                  workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """SnapKV scores (STRATA_KV.py:932-954) on the device: q (B, Hq, >= H, d) (or QRows), k (B, Hkv, >= H, d)
+    -> (B, Hkv, H) float32.  The last SNAPKV_WINDOW context queries attend causally to the keys [0, H);
+    the probabilities of the non-window keys, averaged over those queries and over the query heads of
+    each KV group and pooled by avg_pool1d(SNAPKV_KERNEL, padding // 2), are the scores; the window gets
+    the largest score + 1.  ``cfg``: any object with SNAPKV_WINDOW / SNAPKV_KERNEL (the reference's
+    Config), else the reference's defaults 64 / 5."""
+    w = int(getattr(cfg, "SNAPKV_WINDOW", SNAPKV_WINDOW))
+    kern = int(getattr(cfg, "SNAPKV_KERNEL", SNAPKV_KERNEL))
+    qw = _window_rows(q, H, w)
+    _lib.require_gpu(qw, k)
+    B, Hq, _, d = qw.shape
+    Hkv = k.shape[1]
+    if k.shape[2] < H or qw.shape[2] != w or k.dtype != qw.dtype:
+        raise ValueError("need k with >= H rows and the window queries in k's dtype")
+    if qw.stride(-1) != 1:
+        qw = qw.contiguous()
+    if k.stride(-1) != 1:
+        k = k.contiguous()
+    dt = _lib.DTYPE_CODE[k.dtype]
+    if out is None:
+        out = torch.empty((B, Hkv, H), dtype=torch.float32, device=k.device)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (B, Hkv, H) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float32 (B, Hkv, H) tensor")
+    if workspace is None:
+        need = _lib.load().kvq_snapkv_scores_workspace(B, Hq, Hkv, w, H, dt)
+        if need < 0:
+            raise _lib.KVQError("kvq_snapkv_scores_workspace rejected the shape")
+        workspace = torch.empty((need,), dtype=torch.float32, device=k.device)
+    _lib.call("kvq_snapkv_scores", qw.data_ptr(), dt, qw.stride(0), qw.stride(1), qw.stride(2), k.data_ptr(),
+              k.stride(0), k.stride(1), k.stride(2), B, Hq, Hkv, d, w, H, float(scaling), kern, out.data_ptr(),
+              workspace.data_ptr(), workspace.numel(), _lib.stream_of(k))
+    return out
+
+
 @torch.no_grad()
 def topk_retain(scores: torch.Tensor, k: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """scores (..., n) float32 on the GPU -> int32 (..., k): the positions of the k largest scores of
