@@ -17,10 +17,13 @@ The other rows of the path are measured by the same script with ``--workload``:
   quasar  QUASAR compressed-domain decode (embedded spectral code, 64k context, batch 1)
   micro   the reference's decode-attention microbenchmark: SDPA (full, evicting) vs the packed kernels
   alloc   STRATA rate allocation of one layer (compression side: order, head sum, Lagrangian search)
+  snapkv  SnapKV scores of a prefilled layer at the C4 shape (the prefill form of the eviction scores)
 Each prints one JSON line of the same form (its own metric, roofline and CPU baseline).
 
-Timing: W untimed warm-up steps, then K steps launched back to back between HIP events on the
-launch stream (device synchronisation on both sides).  The same step captured once in a HIP graph
+Timing: a settle phase (``settle_ms`` of the same step: the device's clocks rise over the first
+~30 ms of sustained load), W untimed warm-up steps, then K steps launched back to back between HIP
+events on the launch stream (device synchronisation on both sides).  C1/C2 also report the K steps
+timed from idle after only the W warm-ups (``cold_ms_per_step``).  The same step captured once in a HIP graph
 (the reference's _time_callable protocol, STRATA_KV.py:3424-3447) is timed too and reported as
 ``graph_us``: on this ROCm stack a replay of a one-step graph costs more than the eager launches.
 The dominant kernel is timed inside K more eager steps of the same sequence, with HIP events
@@ -108,15 +111,19 @@ def kernel_in_step_ms(kern, steps: int, warmup: int, pre=None, post=None) -> flo
     """Average GPU time of ``kern`` launched inside back-to-back eager steps (pre(); kern(); post()):
     HIP events recorded on the launch stream (torch's current stream, the one every kvq call
     launches on) right before and right after each kern() launch.  The host runs ahead of the GPU,
-    so each pair brackets the kernel alone; it is the same eager sequence ms_per_step times, so
-    the kernel's time cannot exceed the step's."""
+    so each pair brackets the kernel alone; it is the same eager sequence ms_per_step times (after the
+    same settle phase), so the kernel's time cannot exceed the step's."""
     import torch
-    for _ in range(warmup):
+
+    def whole():
         if pre is not None:
             pre()
         kern()
         if post is not None:
             post()
+    settle(whole, SETTLE_MS)
+    for _ in range(warmup):
+        whole()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
     for a, b in evs:
@@ -138,10 +145,34 @@ def eager_ms(fn, steps: int, warmup: int) -> float:
     return _events_ms(fn, steps)
 
 
+SETTLE_MS = 100.0
+
+
+def settle(fn, ms: float) -> float:
+    """Run fn back to back for about ``ms`` of GPU time (batches timed with HIP events): the device
+    raises its clocks over the first ~30 ms of sustained load (per-step times from idle: 113-142 us
+    over the first 100 C2 steps, ~106 us after 300), and a decode loop in service runs continuously.
+    Returns the GPU time spent."""
+    import torch
+    spent, batch = 0.0, 8
+    while spent < ms:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(batch):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        spent += a.elapsed_time(b)
+        batch = min(batch * 2, 256)
+    return spent
+
+
 def step_ms(fn, steps: int, warmup: int):
-    """(eager ms, graph-replay ms) of one step.  Eager launches are the figure reported: on this
-    ROCm stack a graph replay of these launches measures slower than the same launches issued
-    back to back (an extra ~5-20 us per replay), so the graph time is kept as a second figure."""
+    """(eager ms, graph-replay ms) of one step, each after a settle phase (SETTLE_MS of the same step)
+    and ``warmup`` untimed steps.  Eager launches are the figure reported: on this ROCm stack a graph
+    replay of these launches measures slower than the same launches issued back to back (an extra
+    ~5-20 us per replay), so the graph time is kept as a second figure."""
+    settle(fn, SETTLE_MS)
     e = eager_ms(fn, steps, warmup)
     g = graph_ms(fn, steps, warmup)
     return e, g
@@ -265,6 +296,8 @@ def run_kivi(args, shape_name: str) -> dict:
         kvq.kivi_decode(q, scaling, cache, out=out, workspace=ws, split_tokens=args.split_tokens, phases=2)
 
     log("timing")
+    # from idle: W warm-up steps, then K timed steps, before the clocks have settled
+    cold_ms = eager_ms(step, args.steps, args.warmup)
     ms_per_step, g_ms = step_ms(step, args.steps, args.warmup)
     split_ms = kernel_in_step_ms(split_only, args.steps, 0, post=merge_only)
     step_gpu_ms = graph_k_ms(step, args.steps, args.warmup)
@@ -291,6 +324,7 @@ def run_kivi(args, shape_name: str) -> dict:
                   roofline=_roof(split_bytes, split_ms, "kivi_decode_split", traffic),
                   us_per_layer=round(ms_per_step * 1e3, 3),
                   timer="back-to-back launches, HIP events over the timed steps",
+                  settle_ms=SETTLE_MS, cold_ms_per_step=round(cold_ms, 5),
                   graph_us=round(g_ms * 1e3, 3), step_gpu_us=round(step_gpu_ms * 1e3, 3), bytes_alg=bytes_alg,
                   packed_code_GBs=round(2 * shape.B * shape.Hkv * cache.n_q * shape.d // 2 / (ms_per_step * 1e-3) / 1e9,
                                         2))
@@ -979,9 +1013,67 @@ def run_alloc(args) -> dict:
     return res
 
 
+# ---------------------------------------------------------------------------------------------
+# A7 prefill form: SnapKV scores at the C4 shape
+
+def run_snapkv(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    from kvq.synth import C4, C4_STEPS, c4_inputs
+    s = C4
+    w, kern = 64, 5
+    log("generating C4-shaped keys and window queries")
+    _, K, _ = c4_inputs("cuda", steps=1)
+    g = torch.Generator(device="cuda").manual_seed(s.seed + 100)
+    q = torch.randn((s.B, s.Hq, w, s.d), generator=g, device="cuda").to(s.dtype)   # the window queries
+    H = s.T
+    scaling = s.d ** -0.5
+    out = torch.empty((s.B, s.Hkv, H), dtype=torch.float32, device="cuda")
+    need = kvq._lib.load().kvq_snapkv_scores_workspace(s.B, s.Hq, s.Hkv, w, H, kvq._lib.DTYPE_CODE[s.dtype])
+    ws = torch.empty((need,), dtype=torch.float32, device="cuda")
+
+    class Win:                                     # the observation queries at positions H - w .. H - 1
+        def at(self, pos):
+            return q
+    qw = Win()
+    step = lambda: kvq.snapkv_scores(qw, K, H, scaling, out=out, workspace=ws)
+    ms, g_ms = step_ms(step, args.steps, args.warmup)
+    rows = (s.Hq // s.Hkv) * w
+    flops = 2 * (2 * rows * H * s.d) * s.B * s.Hkv           # logits twice (statistics, then column sums)
+    kbytes = 2 * K.numel() * K.element_size()                # keys read by both passes
+    tflops = flops / (ms * 1e-3) / 1e12
+    res = _result(args, metric="SnapKV scores (prefill form): TFLOP/s of the logit passes + µs/layer", value=tflops,
+                  unit="TFLOP/s", ms_per_step=ms,
+                  workload=f"A7 snapkv_scores at the C4 shape: B={s.B}, Hq={s.Hq}, Hkv={s.Hkv}, d={s.d}, H={H}, "
+                           f"window {w}, pooling {kern}, bf16",
+                  config={"global_batch": s.B, "seq_len": H, "parallelism": "single GPU", "window": w,
+                          "kernel": kern},
+                  dtype="bf16",
+                  roofline={"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                            "frac": round(tflops / 2500.0, 4), "traffic": None, "kernel": "snap_stats + snap_cols",
+                            "kernel_us": round(ms * 1e3, 3), "kernel_flops": int(flops),
+                            "hbm_GBs_keys": round(kbytes / (ms * 1e-3) / 1e9, 1)},
+                  us_per_layer=round(ms * 1e3, 3), graph_us=round(g_ms * 1e3, 3))
+    log(f"snapkv {ms * 1e3:.1f} us = {tflops:.0f} TFLOP/s")
+    if not args.no_cpu_baseline:
+        from oracle.evict import snapkv_scores as oracle_snapkv
+        Kb = K[:1, :, :H].float().cpu().numpy()
+        qb = np.zeros((1, s.Hq, H, s.d), np.float32)
+        qb[:, :, H - w:] = q[:1].float().cpu().numpy()
+        t0 = time.perf_counter()
+        oracle_snapkv(qb, Kb, H, scaling, w, kern)
+        t = (time.perf_counter() - t0) * s.B
+        res["cpu_baseline"] = {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": _threads(), "kind": "port",
+                               "us_per_layer": t * 1e6,
+                               "sample": f"batch element 0 of {s.B} (all {s.Hkv} KV heads), x {s.B}; numpy float64 "
+                                         "window attention, pooling, head means"}
+    return res
+
+
 WORKLOADS = {"c2": lambda a: run_kivi(a, "c2"), "c1": lambda a: run_kivi(a, "c1"), "c3": run_c3, "c4": run_c4,
              "c5": run_c5, "strata": run_strata, "append": run_append, "quant": run_quant, "quasar": run_quasar,
-             "micro": run_micro, "alloc": run_alloc}
+             "micro": run_micro, "alloc": run_alloc, "snapkv": run_snapkv}
 
 
 def main() -> int:

@@ -2,8 +2,8 @@
 
 C2 (B 16, Hq 32, Hkv 8, d 128, T 32768 = 32640 packed + 128 exact bf16 rows, groups of 64) is
 generated on the device exactly as the c2 bench workload generates it, packed by the library, and
-decoded with the automatic plan the bench times (6 packed splits per (b, h), the exact window
-fused into the splits, 22 rows each).  Sampled (b, h) pairs -- first, last and interior ones,
+decoded with the automatic plan the bench times (several packed splits per (b, h), the exact
+window fused into the splits).  Sampled (b, h) pairs -- first, last and interior ones,
 which land on different XCDs and split slots -- are compared with the oracle's kivi_quant +
 chunked_attention of the same rows at the bf16 bar (1e-2 max-abs-err).
 """
@@ -36,9 +36,12 @@ def test_c2_full_size_sampled_pairs():
     cache = kvq.PackedKIVICache.from_context(K, V, window=s.window, group_k=s.group_k, group_v=s.group_v)
     rep = s.Hq // s.Hkv
     BH, R = s.B * s.Hkv, rep
-    # the production plan: 6 packed splits per (b, h), no exact-row blocks
-    assert kvq.workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.n_q, cache.n_exact, s.group_k,
-                                s.group_v) == BH * (6 * R * (s.d + 2) + 2 * R)
+    # the production plan (the automatic one kivi_decode uses): several packed splits per (b, h),
+    # their partials merged, and no exact-row blocks
+    ws = kvq.workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.n_q, cache.n_exact, s.group_k, s.group_v)
+    S1 = (ws // BH - 2 * R) // (R * (s.d + 2))
+    assert ws == BH * (S1 * R * (s.d + 2) + 2 * R) and S1 >= 2
+    print(f"C2 plan: {S1} splits per (b, h)", flush=True)
     out = kvq.kivi_decode(q, s.d ** -0.5, cache).float().cpu().numpy()       # (B, 1, Hq, d)
     assert np.isfinite(out).all()
     worst = 0.0
