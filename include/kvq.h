@@ -206,6 +206,32 @@ int kvq_snapkv_scores(const void* q, int dtype, int64_t q_sb, int64_t q_sh, int6
                       int64_t workspace_floats, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * F1  STRATA coverage statistics: replaces coverage_stats, STRATA_KV.py:1225-1298 (the groups of
+ * coverage_groups 1206-1222 are drawn by the host, as the reference draws them, and passed as a plan).
+ *
+ * Plan (host-built, int32, device memory): G kept groups (those reaching the coded range); group g
+ *    owns rows [row_base, row_base + rep*nq_pad) of every KV head, laid out [query head r][query i <
+ *    nq_pad] (nq_pad = nq rounded up to 16).  gtab (G, 8): row_base, nq, nq_pad, mmax (max position
+ *    + 1), te = min(re, mmax), local (1 for the window group, STRATA_LOCAL otherwise), 0, 0.
+ *    rowpos (NR): the position of each row, -1 for padding; rowgrp (NR): its group; rlist (rep,
+ *    n_rlist): the rows of query head r (-1 for padding); items (n_items, 2): (group, 64-row block)
+ *    for every 64-row block of every group.  NR a multiple of 16.
+ * qr: (Hkv, NR, d) of `dtype`, contiguous: row (h, row) = q[0, h*rep + r, position] (unscaled).
+ * k, v: (h, j, c) at k + h*k_sh + j*k_st + c, j < T (batch element 0, as the reference), 16-byte
+ *    aligned rows; M (Hq, d, d) float32: the output metric of each query head.  d = 128.
+ * Outputs float32: A, W, DD (Hkv, re - rs); S, Mbar (Hkv, d, d) -- the reference's A, W, DD, S and
+ *    Mbar with floor eta (STRATA_FLOOR).  workspace: kvq_coverage_stats_workspace(...) floats.
+ *    Eleven launches on `stream`, no host synchronisation, deterministic (no atomics).
+ * ---------------------------------------------------------------------------------------- */
+int64_t kvq_coverage_stats_workspace(int64_t Hkv, int64_t rep, int64_t n, int64_t NR, int64_t G);
+int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const int32_t* rowpos, const int32_t* rowgrp,
+                       const int32_t* rlist, int64_t n_rlist, const int32_t* gtab, int64_t G, const int32_t* items,
+                       int64_t n_items, const void* k, int64_t k_sh, int64_t k_st, const void* v, int64_t v_sh,
+                       int64_t v_st, int64_t T, const float* M, int64_t Hkv, int64_t rep, int64_t d, int64_t rs,
+                       int64_t re, float scaling, float eta, float* A, float* W, float* DD, float* S, float* Mbar,
+                       float* workspace, int64_t workspace_floats, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * A7  Retained-set rows for the gathered decode.  For each (b, h) and i < count, position
  * t = idx[bh*idx_bh + i] of the packed cache (layout as kvq_kivi_decode) is dequantised the way
  * kivi_quant's xhat is (code * scale + lo in fp32, STRATA_KV.py:855) and written, rounded to

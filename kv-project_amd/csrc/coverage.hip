@@ -1,0 +1,747 @@
+// STRATA coverage statistics on the device (gfx950): coverage_stats, STRATA_KV.py:1225-1298.
+//
+// For every coverage group g (host-drawn query positions, coverage_groups 1206-1222) and KV head h,
+// the rows r = (query head of h, query) attend causally to the keys [0, max position]; their
+// probabilities p and outputs o give, for the coded tokens j in [rs, min(re, max position + 1)) read
+// at distance >= local: pR = p_j, u = ||v_j - o||^2_M (M the query head's output metric), the drop
+// term (pR / max(1 - pR, 1e-6))^2 u, the key term a = pR^2 u and the read mass pR^2, averaged over
+// the group's queries and normalised by the group's drop total N (over every head and token); then
+// averaged over the live groups, S = sum of alpha q q^T (alpha = a row's key-term mass) normalised
+// by sum_j A_j, Mbar = read-weighted mean metric, and every output + floor x its mean.
+//
+// Rows are laid out per KV head as [group][query head r][query, padded to 16] (row_base of a group in
+// the group table); padded rows have position -1 and contribute nothing.  Launches (one stream, no
+// host synchronisation, no atomics: every sum has a fixed order):
+//   cov_rowstats  per (group, 64-row block, h): logits of 16-key tiles on the matrix cores
+//                 (row_tiles.hpp), online max / sum per row -> row max (base 2) and 1 / sum.
+//   cov_output    same grid: the logits again, p = 2^(s - max) in registers as the A operand of the
+//                 PV product (hi + lo parts; the two 16-key tiles of a 32-key step give every lane 8
+//                 keys of its row, in an order the B operand follows), B = values of the step from an
+//                 LDS tile; o = PV / sum, fp32.
+//   cov_metric    x M and x M x for 32 vectors per workgroup with the query head's metric staged in
+//                 LDS: the row outputs (o M replaces o) and the coded values (v M v).
+//   cov_terms<A>  per (h, 256-token chunk): for every group reaching the chunk, logits and v.(oM) of
+//                 16-token tiles on the matrix cores, then the per-(row, token) terms: the group's
+//                 drop total and every row's key-term mass, as partials per chunk.
+//   cov_groups    N per group -> weight 1 / N (0 if N = 0), live count.
+//   cov_roww      per row: its group's weight x its key-term mass.
+//   cov_terms<B>  the same tiles with the weights: A, DD and the read mass per query head.
+//   cov_smat      S = sum over rows of weight * alpha * (scaling q)(scaling q)^T.
+//   cov_final     live average, S / sum_j A_j, Mbar, floors (one workgroup for the sums, then all).
+#include <algorithm>
+
+#include "common.hpp"
+#include "mfma_common.hpp"
+#include "row_tiles.hpp"
+
+namespace kvq {
+namespace {
+
+constexpr int kCD = 128;
+constexpr int kCThreads = 256;
+constexpr int kCWaves = 4;
+constexpr int kChunkTok = 256;          // tokens of a cov_terms workgroup
+constexpr int kGT = 8;                  // ints per group-table entry
+constexpr int kMetricRows = 32;         // vectors of a cov_metric workgroup
+constexpr float kCLog2e = 1.4426950408889634f;
+
+// group table entry (kGT ints): row_base, nq, nq_pad, mmax, te, local, 0, 0
+struct CovParams {
+  const void* qr;                        // (Hkv, NR, d) group query rows (unscaled), DT
+  const int32_t* rowpos;                 // (NR): position of each row (-1: padding)
+  const int32_t* gtab;                   // (G, kGT)
+  const int32_t* items;                  // (n_items, 2): (group, 64-row block)
+  const void* k;
+  const void* v;
+  int64_t k_sh, k_st, v_sh, v_st;        // element strides of the (head, token) axes
+  const float* M;                        // (Hq, d, d)
+  int Hkv, rep, NR, G, n_items, rs, re, n, n_chunks, T;
+  float qscale;                          // scaling * log2(e)
+  float scaling, eta;
+  float* row_m;                          // (Hkv, NR) row max (base 2)
+  float* row_il;                         // (Hkv, NR) 1 / row sum
+  float* o;                              // (Hkv, NR, d) fp32 outputs, then o M
+  float* oMo;                            // (Hkv, NR)
+  float* vmv;                            // (Hkv, rep, n)
+  float* ddpart;                         // (G, Hkv, n_chunks)
+  float* alpha_part;                     // (Hkv, n_chunks, NR)
+  float* gw;                             // (G): 1 / N or 0; [G]: live count
+  float* roww;                           // (Hkv, NR): weight * alpha
+  float* red;                            // finalisation sums
+  float* A;                              // (Hkv, n)
+  float* W;                              // (Hkv, n)
+  float* DD;                             // (Hkv, n)
+  float* WVa;                            // (Hkv, rep, n)
+  float* S;                              // (Hkv, d, d)
+  float* Mbar;                           // (Hkv, d, d)
+};
+
+// the rows of head h as a buffer resource covering T token rows (reads past it return zero)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void* base, int64_t sh, int64_t st, int h, int T,
+                                                           int esz) {
+  const char* b = static_cast<const char*>(base) + static_cast<int64_t>(h) * sh * esz;
+  return make_rsrc(b, static_cast<uint32_t>((static_cast<int64_t>(T - 1) * st + kCD) * esz));
+}
+
+template <int DT>
+__device__ __forceinline__ void zero_ops(u32x4 (&op)[4][TileOps<DT>::NH]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int hh = 0; hh < TileOps<DT>::NH; ++hh) op[ks][hh] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// query operands (B) of the 16 rows starting at row0 of head h; returns this lane's row position
+template <int DT>
+__device__ __forceinline__ int load_rows(const CovParams& p, int h, int row0, int g, int n,
+                                         u32x4 (&qop)[4][TileOps<DT>::NH]) {
+  const int row = row0 + n;
+  const int pos = row < p.NR ? p.rowpos[row] : -1;
+  if (pos >= 0) {
+    const int64_t base = (static_cast<int64_t>(h) * p.NR + row) * kCD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) load_op<DT>(p.qr, base + 32 * ks + 8 * g, qop[ks]);
+  } else {
+    zero_ops<DT>(qop);
+  }
+  return pos;
+}
+
+// A operand (tokens) of the 16-token tile at t0: this lane's token t0 + n
+template <int DT>
+__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rs, int64_t st, int t0, int g, int n,
+                                          u32x4 (&op)[4][TileOps<DT>::NH]) {
+  const int64_t tok = t0 + n;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    load_op_buf<DT>(rs, static_cast<int>((tok * st + 32 * ks + 8 * g) * TileOps<DT>::ESZ), op[ks]);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kCThreads) void cov_rowstats(CovParams p) {
+  const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
+  const int item = blockIdx.x % p.n_items, h = blockIdx.x / p.n_items;
+  const int grp = p.items[2 * item], rb = p.items[2 * item + 1];
+  const int32_t* gt = p.gtab + kGT * grp;
+  const int rows_g = p.rep * gt[2];
+  const int row0 = gt[0] + 64 * rb + 16 * wave;
+  if (64 * rb + 16 * wave >= rows_g) return;                 // whole wavefront past the group's rows
+  u32x4 qop[4][TileOps<DT>::NH];
+  const int pos = load_rows<DT>(p, h, row0, g, n, qop);
+  const int mmax = gt[3];
+  const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, TileOps<DT>::ESZ);
+  float m = -INFINITY, ls = 0.0f;
+  for (int t0 = 0; t0 < mmax; t0 += 16) {
+    u32x4 kop[4][TileOps<DT>::NH];
+    load_tile<DT>(rk, p.k_st, t0, g, n, kop);
+    const f32x4 d = tile_dots<DT, TileOps<DT>::NH, TileOps<DT>::NH>(kop, qop);
+    float sv[4], mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = t0 + 4 * g + i;
+      sv[i] = (j <= pos && j < mmax) ? d[i] * p.qscale : -INFINITY;
+      mt = fmaxf(mt, sv[i]);
+    }
+    if (mt > m) {
+      ls *= __builtin_amdgcn_exp2f(m - mt);
+      m = mt;
+    }
+    if (m != -INFINITY) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ls += __builtin_amdgcn_exp2f(sv[i] - m);
+    }
+  }
+  // lanes (0..3, n) hold disjoint keys of row n
+  const float M = xmax32(xmax16(m));
+  const float part = (M == -INFINITY || m == -INFINITY) ? 0.0f : ls * __builtin_amdgcn_exp2f(m - M);
+  const float L = xsum32(xsum16(part));
+  if (g == 0 && row0 + n < p.NR) {
+    const int64_t o = static_cast<int64_t>(h) * p.NR + row0 + n;
+    p.row_m[o] = M == -INFINITY ? 0.0f : M;                  // padding rows: every p is masked to 0 below
+    p.row_il[o] = L > 0.0f ? 1.0f / L : 0.0f;
+  }
+}
+
+// values of one 32-key step in LDS: [key][channel], rows padded by 8 bytes against bank conflicts
+template <int DT>
+constexpr int vrow_words() { return (kCD * TileOps<DT>::ESZ + 8) / 4; }
+
+template <int DT>
+__global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
+  constexpr int ESZ = TileOps<DT>::ESZ;
+  constexpr int VRW = vrow_words<DT>();
+  constexpr int U16 = kCD * ESZ / 16;                        // 16-byte units of a value row
+  __shared__ uint32_t vt[32 * VRW];
+  const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
+  const int item = blockIdx.x % p.n_items, h = blockIdx.x / p.n_items;
+  const int grp = p.items[2 * item], rb = p.items[2 * item + 1];
+  const int32_t* gt = p.gtab + kGT * grp;
+  const int rows_g = p.rep * gt[2];
+  const int row0 = gt[0] + 64 * rb + 16 * wave;
+  const bool active = 64 * rb + 16 * wave < rows_g;        // inactive wavefronts still join the barriers
+  u32x4 qop[4][TileOps<DT>::NH];
+  int pos = -1;
+  if (active)
+    pos = load_rows<DT>(p, h, row0, g, n, qop);
+  else
+    zero_ops<DT>(qop);
+  const float rm = (active && row0 + n < p.NR) ? p.row_m[static_cast<int64_t>(h) * p.NR + row0 + n] : 0.0f;
+  const int mmax = gt[3];
+  const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, ESZ);
+  const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v, p.v_sh, p.v_st, h, p.T, ESZ);
+  f32x4 acc[8];
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t0 = 0; t0 < mmax; t0 += 32) {
+    // the step's 32 value rows (rows at or past mmax as zeros: p = 0 there must not meet a NaN)
+    __syncthreads();
+    for (int u = threadIdx.x; u < 32 * U16; u += kCThreads) {
+      const int key = u / U16, w16 = u % U16;
+      u32x4 x = u32x4{0u, 0u, 0u, 0u};
+      if (t0 + key < mmax)
+        x = __builtin_amdgcn_raw_buffer_load_b128(
+            rv, static_cast<int>((static_cast<int64_t>(t0 + key) * p.v_st) * ESZ + 16 * w16), 0, 0);
+      uint32_t* dst = vt + key * VRW + 4 * w16;
+      dst[0] = x[0];
+      dst[1] = x[1];
+      dst[2] = x[2];
+      dst[3] = x[3];
+    }
+    __syncthreads();
+    // probabilities of the two 16-key tiles: lane (g, n) holds keys t0 + 4g + i and t0 + 16 + 4g + i
+    // of row n
+    float pr[8];
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+      u32x4 kop[4][TileOps<DT>::NH];
+      load_tile<DT>(rk, p.k_st, t0 + 16 * tau, g, n, kop);
+      const f32x4 d = tile_dots<DT, TileOps<DT>::NH, TileOps<DT>::NH>(kop, qop);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = t0 + 16 * tau + 4 * g + i;
+        pr[4 * tau + i] = (j <= pos && j < mmax) ? __builtin_amdgcn_exp2f(d[i] * p.qscale - rm) : 0.0f;
+      }
+    }
+    // A operand: row n, k-index 8g + kk <-> key kk < 4 ? 4g + kk : 16 + 4g + kk - 4 (hi and lo parts)
+    u32x4 ph, pl;
+    f32_parts<DT>(pr, ph, pl);
+    // B operand per 16-channel block cb: lane (g, n) holds the values of those keys at channel 16cb + n
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) {
+      const int c = 16 * cb + n;
+      if constexpr (DT == KVQ_F32) {
+        float x[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const int key = kk < 4 ? 4 * g + kk : 16 + 4 * g + kk - 4;
+          x[kk] = __uint_as_float(vt[key * VRW + c]);
+        }
+        u32x4 vh, vl;
+        f32_parts<DT>(x, vh, vl);
+        acc[cb] = tile_mfma<DT>(ph, vh, acc[cb]);
+        acc[cb] = tile_mfma<DT>(pl, vh, acc[cb]);
+        acc[cb] = tile_mfma<DT>(ph, vl, acc[cb]);
+      } else {
+        const uint16_t* v16 = reinterpret_cast<const uint16_t*>(vt);
+        uint32_t wv[4];
+#pragma unroll
+        for (int kk = 0; kk < 8; kk += 2) {
+          const int k0 = kk < 4 ? 4 * g + kk : 16 + 4 * g + kk - 4;
+          wv[kk / 2] = static_cast<uint32_t>(v16[k0 * 2 * VRW + c]) |
+                       (static_cast<uint32_t>(v16[(k0 + 1) * 2 * VRW + c]) << 16);
+        }
+        const u32x4 vb = u32x4{wv[0], wv[1], wv[2], wv[3]};
+        acc[cb] = tile_mfma<DT>(ph, vb, acc[cb]);
+        acc[cb] = tile_mfma<DT>(pl, vb, acc[cb]);
+      }
+    }
+  }
+  if (!active) return;
+  // D lane (g, n) register i: row 4g + i of the block, channel 16cb + n
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + 4 * g + i;
+    if (row >= p.NR) continue;
+    const float il = p.row_il[static_cast<int64_t>(h) * p.NR + row];
+    float* dst = p.o + (static_cast<int64_t>(h) * p.NR + row) * kCD + n;
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) dst[16 * cb] = acc[cb][i] * il;
+  }
+}
+
+// x M and x M x for 32 vectors per workgroup, M = the metric of query head (h, r) staged in LDS in
+// two halves of 64 rows.  ROWS: the row outputs of query head r (o M replaces o, o M o out);
+// otherwise the coded values (v M v out).  Grid: (h, r, tile of 32 vectors).
+template <int DT, bool ROWS>
+__global__ __launch_bounds__(kCThreads) void cov_metric(CovParams p, const int32_t* rlist, int n_rlist) {
+  constexpr int XS = kCD + 1;                          // odd stride: the rows' reads hit distinct banks
+  __shared__ float Ms[64 * kCD];                       // 32 KiB
+  __shared__ float xs[kMetricRows * XS];
+  __shared__ float red[kMetricRows][8];
+  const int count = ROWS ? n_rlist : p.n;
+  const int per = (count + kMetricRows - 1) / kMetricRows;
+  const int hr = blockIdx.x / per, tile = blockIdx.x % per;
+  const int h = hr / p.rep, r = hr % p.rep;
+  const float* Mg = p.M + static_cast<int64_t>(h * p.rep + r) * kCD * kCD;
+  const int32_t* rl = ROWS ? rlist + static_cast<int64_t>(r) * n_rlist : nullptr;
+  for (int u = threadIdx.x; u < kMetricRows * kCD; u += kCThreads) {
+    const int k = u / kCD, c = u % kCD;
+    const int idx = kMetricRows * tile + k;
+    float x = 0.0f;
+    if (idx < count) {
+      if constexpr (ROWS) {
+        if (rl[idx] >= 0) x = p.o[(static_cast<int64_t>(h) * p.NR + rl[idx]) * kCD + c];
+      } else {
+        x = load_as_f32<DT>(p.v, static_cast<int64_t>(h) * p.v_sh + static_cast<int64_t>(p.rs + idx) * p.v_st + c);
+      }
+    }
+    xs[k * XS + c] = x;
+  }
+  // thread: vector k = t / 8, output channels 16 (t % 8) .. + 15
+  const int k = threadIdx.x / 8, c8 = threadIdx.x % 8;
+  float y[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) y[e] = 0.0f;
+  for (int hf = 0; hf < 2; ++hf) {
+    __syncthreads();
+    for (int u = threadIdx.x; u < 64 * kCD / 4; u += kCThreads)
+      reinterpret_cast<float4*>(Ms)[u] = reinterpret_cast<const float4*>(Mg + 64 * hf * kCD)[u];
+    __syncthreads();
+    for (int d = 0; d < 64; ++d) {
+      const float xd = xs[k * XS + 64 * hf + d];
+      const float4* mr = reinterpret_cast<const float4*>(Ms + d * kCD + 16 * c8);
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const float4 mv = mr[e4];
+        y[4 * e4] = __builtin_fmaf(xd, mv.x, y[4 * e4]);
+        y[4 * e4 + 1] = __builtin_fmaf(xd, mv.y, y[4 * e4 + 1]);
+        y[4 * e4 + 2] = __builtin_fmaf(xd, mv.z, y[4 * e4 + 2]);
+        y[4 * e4 + 3] = __builtin_fmaf(xd, mv.w, y[4 * e4 + 3]);
+      }
+    }
+  }
+  float dot = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) dot = __builtin_fmaf(y[e], xs[k * XS + 16 * c8 + e], dot);
+  red[k][c8] = dot;
+  __syncthreads();
+  const int idx = kMetricRows * tile + k;
+  if (idx >= count) return;
+  const float tot = ((red[k][0] + red[k][1]) + (red[k][2] + red[k][3])) +
+                    ((red[k][4] + red[k][5]) + (red[k][6] + red[k][7]));
+  if constexpr (ROWS) {
+    if (rl[idx] < 0) return;
+    const int64_t rid = static_cast<int64_t>(h) * p.NR + rl[idx];
+    float* dst = p.o + rid * kCD + 16 * c8;             // this workgroup staged its rows before any write
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dst[e] = y[e];
+    if (c8 == 0) p.oMo[rid] = tot;
+  } else {
+    if (c8 == 0) p.vmv[(static_cast<int64_t>(h) * p.rep + r) * p.n + idx] = tot;
+  }
+}
+
+__global__ __launch_bounds__(kCThreads) void cov_clear(float* x, int64_t count) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kCThreads + threadIdx.x;
+  if (t < count) x[t] = 0.0f;
+}
+
+// per (h, 256-token chunk): every group reaching the chunk, its rows in 64-row blocks (one 16-row
+// block per wavefront, one query head per block since nq_pad is a multiple of 16), 16-token tiles.
+// WEIGHTED = false: drop totals and key-term masses; true: the weighted per-token sums.
+template <int DT, bool WEIGHTED>
+__global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
+  constexpr int NH = TileOps<DT>::NH;
+  __shared__ float accA[kCWaves][kChunkTok];
+  __shared__ float accD[kCWaves][kChunkTok];
+  __shared__ float accW[kCWaves][kChunkTok];             // read mass of the wavefront's current block
+  __shared__ float red[kCWaves];
+  const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
+  const int h = blockIdx.x / p.n_chunks, chunk = blockIdx.x % p.n_chunks;
+  const int c0 = p.rs + chunk * kChunkTok;               // first token of the chunk
+  const int c1 = min(c0 + kChunkTok, p.re);
+  const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, TileOps<DT>::ESZ);
+  const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v, p.v_sh, p.v_st, h, p.T, TileOps<DT>::ESZ);
+  if constexpr (WEIGHTED) {
+    for (int u = threadIdx.x; u < kCWaves * kChunkTok; u += kCThreads) {
+      (&accA[0][0])[u] = 0.0f;
+      (&accD[0][0])[u] = 0.0f;
+    }
+  }
+  for (int grp = 0; grp < p.G; ++grp) {
+    const int32_t* gt = p.gtab + kGT * grp;
+    const int row_base = gt[0], nq = gt[1], nq_pad = gt[2], te = gt[4], local = gt[5];
+    const int rows_g = p.rep * nq_pad;
+    if (te <= c0) {                                      // the group does not reach this chunk
+      if constexpr (!WEIGHTED) {
+        for (int u = threadIdx.x; u < rows_g; u += kCThreads)
+          p.alpha_part[(static_cast<int64_t>(h) * p.n_chunks + chunk) * p.NR + row_base + u] = 0.0f;
+        if (threadIdx.x == 0) p.ddpart[(static_cast<int64_t>(grp) * p.Hkv + h) * p.n_chunks + chunk] = 0.0f;
+      }
+      continue;
+    }
+    if (WEIGHTED && p.gw[grp] == 0.0f) continue;        // N = 0: every term of the group is zero
+    const int t_end = min(c1, te);
+    const float wq = (WEIGHTED ? p.gw[grp] : 1.0f) / static_cast<float>(nq);
+    float dsum = 0.0f;                                   // drop terms of this wavefront (pass A)
+    for (int rb0 = 0; rb0 < rows_g; rb0 += 64) {
+      const int rbl = rb0 + 16 * wave;                    // this wavefront's first row in the group
+      const bool act = rbl < rows_g;
+      const int r = act ? rbl / nq_pad : 0;
+      const int row0 = row_base + rbl;
+      u32x4 qop[4][NH], mop[4][2];
+      int pos = -1;
+      float rm = 0.0f, ril = 0.0f, omo = 0.0f, mscale = 1.0f;
+      if (act) {
+        pos = load_rows<DT>(p, h, row0, g, n, qop);
+        const int64_t rid = static_cast<int64_t>(h) * p.NR + row0 + n;
+        rm = p.row_m[rid];
+        ril = p.row_il[rid];
+        omo = p.oMo[rid];
+        // B operand of v.(oM): the row's o M times a power of two that brings its largest entry to
+        // [128, 256) (inside the range of fp16 parts), in two parts of the operand type
+        float x[4][8], mx = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const float4* src = reinterpret_cast<const float4*>(p.o + rid * kCD + 32 * ks + 8 * g);
+          const float4 a = src[0], b = src[1];
+          x[ks][0] = a.x; x[ks][1] = a.y; x[ks][2] = a.z; x[ks][3] = a.w;
+          x[ks][4] = b.x; x[ks][5] = b.y; x[ks][6] = b.z; x[ks][7] = b.w;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(x[ks][e]));
+        }
+        mx = xmax32(xmax16(mx));                          // over the four lanes of row n
+        int ex = 0;
+        if (mx > 0.0f) (void)frexpf(mx, &ex);
+        const float up = ldexpf(1.0f, 8 - ex);
+        mscale = ldexpf(1.0f, ex - 8);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          float xs8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xs8[e] = x[ks][e] * up;
+          f32_parts<DT>(xs8, mop[ks][0], mop[ks][1]);
+        }
+      } else {
+        zero_ops<DT>(qop);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) mop[ks][0] = mop[ks][1] = u32x4{0u, 0u, 0u, 0u};
+      }
+      if constexpr (WEIGHTED) {
+        for (int u = l; u < kChunkTok; u += 64) accW[wave][u] = 0.0f;
+        wave_lds_fence();
+      }
+      float alpha = 0.0f;                                 // key-term mass of this lane's row (pass A)
+      for (int t0 = c0; t0 < t_end; t0 += 16) {
+        u32x4 kop[4][NH], vop[4][NH];
+        load_tile<DT>(rk, p.k_st, t0, g, n, kop);
+        load_tile<DT>(rv, p.v_st, t0, g, n, vop);
+        const f32x4 s = tile_dots<DT, NH, NH>(kop, qop);
+        const f32x4 ov = tile_dots<DT, NH, 2>(vop, mop);
+        float ta[4], td[4], tw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = t0 + 4 * g + i;
+          const bool far = act && j < t_end && j <= pos - local;
+          const float pr = far ? __builtin_amdgcn_exp2f(s[i] * p.qscale - rm) * ril : 0.0f;
+          const float vmv = far ? p.vmv[(static_cast<int64_t>(h) * p.rep + r) * p.n + (j - p.rs)] : 0.0f;
+          const float u2 = far ? fmaxf(vmv - 2.0f * (ov[i] * mscale) + omo, 0.0f) : 0.0f;
+          const float qd = pr / fmaxf(1.0f - pr, 1e-6f);
+          td[i] = qd * qd * u2;
+          ta[i] = pr * pr * u2;
+          tw[i] = pr * pr;
+        }
+        if constexpr (!WEIGHTED) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dsum += td[i];
+            alpha += ta[i];
+          }
+        } else {
+          // per token: the sums over the block's 16 rows; token 4g + i is owned by lane (g, n = i)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float sa = row_sum16(ta[i]), sd = row_sum16(td[i]), sw = row_sum16(tw[i]);
+            const int jj = t0 + 4 * g + i - c0;
+            if (n == i && act) {
+              accA[wave][jj] += sa * wq;
+              accD[wave][jj] += sd * wq;
+              accW[wave][jj] += sw * wq;
+            }
+          }
+        }
+      }
+      if constexpr (!WEIGHTED) {
+        // the row's key-term mass over this chunk (its four lanes hold disjoint tokens)
+        const float a_row = xsum32(xsum16(alpha));
+        if (act && g == 0)
+          p.alpha_part[(static_cast<int64_t>(h) * p.n_chunks + chunk) * p.NR + row0 + n] = a_row / static_cast<float>(nq);
+      } else {
+        // the wavefronts' read masses into their query heads' rows of WVa, in wavefront order
+        __syncthreads();
+        for (int u = threadIdx.x; u < t_end - c0; u += kCThreads) {
+          for (int w = 0; w < kCWaves; ++w) {
+            const int rbw = rb0 + 16 * w;
+            if (rbw >= rows_g) break;
+            p.WVa[(static_cast<int64_t>(h) * p.rep + rbw / nq_pad) * p.n + (c0 + u - p.rs)] += accW[w][u];
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if constexpr (!WEIGHTED) {
+      dsum = wave_sum(dsum);
+      if (l == 0) red[wave] = dsum;
+      __syncthreads();
+      if (threadIdx.x == 0)
+        p.ddpart[(static_cast<int64_t>(grp) * p.Hkv + h) * p.n_chunks + chunk] =
+            ((red[0] + red[1]) + (red[2] + red[3])) / static_cast<float>(nq);
+      __syncthreads();
+    }
+  }
+  if constexpr (WEIGHTED) {
+    __syncthreads();
+    for (int u = threadIdx.x; u < c1 - c0; u += kCThreads) {
+      const int64_t o = static_cast<int64_t>(h) * p.n + (c0 + u - p.rs);
+      p.A[o] = (accA[0][u] + accA[1][u]) + (accA[2][u] + accA[3][u]);
+      p.DD[o] = (accD[0][u] + accD[1][u]) + (accD[2][u] + accD[3][u]);
+    }
+  }
+}
+
+// N per group (over heads and chunks) -> weights; live count in gw[G]
+__global__ __launch_bounds__(kCThreads) void cov_groups(CovParams p) {
+  __shared__ float red[kCWaves];
+  float live = 0.0f;
+  const int per = p.Hkv * p.n_chunks;
+  for (int grp = 0; grp < p.G; ++grp) {
+    float s = 0.0f;
+    for (int u = threadIdx.x; u < per; u += kCThreads) s += p.ddpart[static_cast<int64_t>(grp) * per + u];
+    s = wave_sum(s);
+    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = s;
+    __syncthreads();
+    const float N = (red[0] + red[1]) + (red[2] + red[3]);
+    if (threadIdx.x == 0) p.gw[grp] = N > 0.0f ? 1.0f / N : 0.0f;
+    live += N > 0.0f ? 1.0f : 0.0f;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) p.gw[p.G] = live;
+}
+
+// per row: its group's weight x its key-term mass (summed over the chunks)
+__global__ __launch_bounds__(kCThreads) void cov_roww(CovParams p, const int32_t* rowgrp) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kCThreads + threadIdx.x;
+  if (t >= static_cast<int64_t>(p.Hkv) * p.NR) return;
+  const int h = static_cast<int>(t / p.NR), row = static_cast<int>(t % p.NR);
+  const int grp = rowgrp[row];
+  if (grp < 0 || p.rowpos[row] < 0) {
+    p.roww[t] = 0.0f;
+    return;
+  }
+  float a = 0.0f;
+  for (int c = 0; c < p.n_chunks; ++c) a += p.alpha_part[(static_cast<int64_t>(h) * p.n_chunks + c) * p.NR + row];
+  p.roww[t] = a * p.gw[grp];
+}
+
+// S[h] = sum over rows of roww * (scaling q)(scaling q)^T: per (h, 16 output rows), 64 rows per stage
+template <int DT>
+__global__ __launch_bounds__(kCThreads) void cov_smat(CovParams p) {
+  __shared__ float qs[64][kCD + 4];
+  __shared__ float ws[64];
+  const int h = blockIdx.x / (kCD / 16), c1b = blockIdx.x % (kCD / 16);
+  const int c1 = 16 * c1b + threadIdx.x / 16, c2 = 8 * (threadIdx.x % 16);   // 8 output columns per thread
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int r0 = 0; r0 < p.NR; r0 += 64) {
+    __syncthreads();
+    for (int u = threadIdx.x; u < 64 * kCD; u += kCThreads) {
+      const int k = u / kCD, c = u % kCD;
+      const int row = r0 + k;
+      qs[k][c] = (row < p.NR && p.rowpos[row] >= 0)
+                     ? load_as_f32<DT>(p.qr, (static_cast<int64_t>(h) * p.NR + row) * kCD + c) * p.scaling
+                     : 0.0f;
+    }
+    if (threadIdx.x < 64)
+      ws[threadIdx.x] = r0 + threadIdx.x < p.NR ? p.roww[static_cast<int64_t>(h) * p.NR + r0 + threadIdx.x] : 0.0f;
+    __syncthreads();
+    for (int k = 0; k < 64; ++k) {
+      const float a = ws[k] * qs[k][c1];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(a, qs[k][c2 + e], acc[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p.S[(static_cast<int64_t>(h) * kCD + c1) * kCD + c2 + e] = acc[e];
+}
+
+// finalisation sums (one workgroup): red[0..2] the means of the live-averaged A, DD, W; red[3] the
+// live count; red[4 + h rep + r] omega (live-averaged read mass per query head); red[4 + Hkv rep + h]
+// sum_j A (live-averaged)
+__global__ __launch_bounds__(1024) void cov_final_sums(CovParams p) {
+  __shared__ float part[16];
+  const float live = fmaxf(p.gw[p.G], 1.0f);
+  auto block_sum = [&](float v) -> float {
+    v = wave_sum(v);
+    if (threadIdx.x % 64 == 0) part[threadIdx.x / 64] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int w = 0; w < 16; ++w) t += part[w];
+    __syncthreads();
+    return t;
+  };
+  float gA = 0.0f, gD = 0.0f, gW = 0.0f;
+  for (int h = 0; h < p.Hkv; ++h) {
+    float sA = 0.0f, sD = 0.0f;
+    for (int j = threadIdx.x; j < p.n; j += 1024) {
+      sA += p.A[static_cast<int64_t>(h) * p.n + j];
+      sD += p.DD[static_cast<int64_t>(h) * p.n + j];
+    }
+    sA = block_sum(sA);
+    sD = block_sum(sD);
+    float sW = 0.0f;
+    for (int r = 0; r < p.rep; ++r) {
+      float om = 0.0f;
+      for (int j = threadIdx.x; j < p.n; j += 1024) om += p.WVa[(static_cast<int64_t>(h) * p.rep + r) * p.n + j];
+      om = block_sum(om);
+      if (threadIdx.x == 0) p.red[4 + h * p.rep + r] = om / live;
+      sW += om;
+    }
+    if (threadIdx.x == 0) p.red[4 + p.Hkv * p.rep + h] = sA / live;
+    gA += sA;
+    gD += sD;
+    gW += sW;
+  }
+  if (threadIdx.x == 0) {
+    const float cnt = static_cast<float>(p.Hkv) * static_cast<float>(p.n);
+    p.red[0] = gA / live / cnt;
+    p.red[1] = gD / live / cnt;
+    p.red[2] = gW / live / cnt;
+    p.red[3] = live;
+  }
+}
+
+__global__ __launch_bounds__(kCThreads) void cov_final(CovParams p) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kCThreads + threadIdx.x;
+  const float live = p.red[3];
+  const int64_t nA = static_cast<int64_t>(p.Hkv) * p.n;
+  const int64_t nS = static_cast<int64_t>(p.Hkv) * kCD * kCD;
+  if (t < nA) {
+    const int h = static_cast<int>(t / p.n), j = static_cast<int>(t % p.n);
+    float w = 0.0f;
+    for (int r = 0; r < p.rep; ++r) w += p.WVa[(static_cast<int64_t>(h) * p.rep + r) * p.n + j];
+    p.A[t] = p.A[t] / live + p.eta * p.red[0];
+    p.DD[t] = p.DD[t] / live + p.eta * p.red[1];
+    p.W[t] = w / live + p.eta * p.red[2];
+  }
+  if (t < nS) {
+    const int h = static_cast<int>(t / (kCD * kCD)), e = static_cast<int>(t % (kCD * kCD));
+    const float sA = p.red[4 + p.Hkv * p.rep + h];
+    p.S[t] = p.S[t] / live / fmaxf(sA, 1e-30f);
+    float om = 0.0f, acc = 0.0f, mean = 0.0f;
+    for (int r = 0; r < p.rep; ++r) {
+      const float o = p.red[4 + h * p.rep + r];
+      const float mv = p.M[static_cast<int64_t>(h * p.rep + r) * kCD * kCD + e];
+      om += o;
+      acc = __builtin_fmaf(o, mv, acc);
+      mean += mv;
+    }
+    p.Mbar[t] = om > 0.0f ? acc / om : mean / static_cast<float>(p.rep);
+  }
+}
+
+}  // namespace
+}  // namespace kvq
+
+using namespace kvq;
+
+// workspace layout (floats): row_m, row_il, oMo, roww (Hkv NR each); o (Hkv NR d); vmv (Hkv rep n);
+// ddpart (G Hkv n_chunks); alpha_part (Hkv n_chunks NR); gw (G + 1); red (4 + Hkv rep + Hkv);
+// WVa (Hkv rep n)
+extern "C" int64_t kvq_coverage_stats_workspace(int64_t Hkv, int64_t rep, int64_t n, int64_t NR, int64_t G) {
+  if (Hkv <= 0 || rep <= 0 || n <= 0 || NR <= 0 || G <= 0) return -1;
+  const int64_t nch = (n + kChunkTok - 1) / kChunkTok;
+  return 4 * Hkv * NR + Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch + Hkv * nch * NR + (G + 1) +
+         (4 + Hkv * rep + Hkv) + Hkv * rep * n;
+}
+
+extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const int32_t* rowpos, const int32_t* rowgrp,
+                                  const int32_t* rlist, int64_t n_rlist, const int32_t* gtab, int64_t G,
+                                  const int32_t* items, int64_t n_items, const void* k, int64_t k_sh, int64_t k_st,
+                                  const void* v, int64_t v_sh, int64_t v_st, int64_t T, const float* M, int64_t Hkv,
+                                  int64_t rep, int64_t d, int64_t rs, int64_t re, float scaling, float eta, float* A,
+                                  float* W, float* DD, float* S, float* Mbar, float* workspace,
+                                  int64_t workspace_floats, void* stream) {
+  KVQ_REQUIRE(valid_dtype(dtype), "kvq_coverage_stats: bad dtype");
+  KVQ_REQUIRE(d == kCD, "kvq_coverage_stats: head_dim must be 128");
+  KVQ_REQUIRE(Hkv > 0 && rep > 0 && Hkv * rep <= 1024, "kvq_coverage_stats: bad head counts");
+  KVQ_REQUIRE(0 <= rs && rs < re && re <= T && T < (1 << 28), "kvq_coverage_stats: need 0 <= rs < re <= T");
+  KVQ_REQUIRE(G > 0 && n_items > 0 && NR > 0 && NR % 16 == 0 && Hkv * NR < (1LL << 31) / kCD && n_rlist > 0 &&
+                  n_rlist * rep <= NR,
+              "kvq_coverage_stats: bad group plan");
+  KVQ_REQUIRE(qr && rowpos && rowgrp && rlist && gtab && items && k && v && M && A && W && DD && S && Mbar && workspace,
+              "kvq_coverage_stats: null pointer");
+  const int esz = dtype == KVQ_F32 ? 4 : 2;
+  KVQ_REQUIRE((k_sh * esz) % 16 == 0 && (k_st * esz) % 16 == 0 && (v_sh * esz) % 16 == 0 && (v_st * esz) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(qr) % 16 == 0 && reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(M) % 16 == 0 && k_st >= kCD && v_st >= kCD,
+              "kvq_coverage_stats: rows must be 16-byte aligned and not overlap");
+  KVQ_REQUIRE((T + 48) * std::max(k_st, v_st) * esz < (1LL << 31), "kvq_coverage_stats: one head's rows must span < 2 GiB");
+  const int64_t n = re - rs;
+  const int64_t need = kvq_coverage_stats_workspace(Hkv, rep, n, NR, G);
+  KVQ_REQUIRE(workspace_floats >= need, "kvq_coverage_stats: workspace too small (%lld < %lld floats)",
+              (long long)workspace_floats, (long long)need);
+  CovParams p{};
+  p.qr = qr; p.rowpos = rowpos; p.gtab = gtab; p.items = items;
+  p.k = k; p.v = v; p.k_sh = k_sh; p.k_st = k_st; p.v_sh = v_sh; p.v_st = v_st;
+  p.M = M;
+  p.Hkv = (int)Hkv; p.rep = (int)rep; p.NR = (int)NR; p.G = (int)G; p.n_items = (int)n_items;
+  p.rs = (int)rs; p.re = (int)re; p.n = (int)n; p.n_chunks = (int)((n + kChunkTok - 1) / kChunkTok); p.T = (int)T;
+  p.scaling = scaling; p.qscale = scaling * kCLog2e; p.eta = eta;
+  float* w = workspace;
+  p.row_m = w; w += Hkv * NR;
+  p.row_il = w; w += Hkv * NR;
+  p.oMo = w; w += Hkv * NR;
+  p.roww = w; w += Hkv * NR;
+  p.o = w; w += Hkv * NR * kCD;
+  p.vmv = w; w += Hkv * rep * n;
+  p.ddpart = w; w += G * Hkv * p.n_chunks;
+  p.alpha_part = w; w += Hkv * p.n_chunks * NR;
+  p.gw = w; w += G + 1;
+  p.red = w; w += 4 + Hkv * rep + Hkv;
+  p.WVa = w;
+  p.A = A; p.W = W; p.DD = DD; p.S = S; p.Mbar = Mbar;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 blk(kCThreads);
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowstats<DT_>), dim3(n_items * Hkv), blk, 0, s, p));
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(rowstats)");
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_output<DT_>), dim3(n_items * Hkv), blk, 0, s, p));
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(output)");
+  hipLaunchKernelGGL((cov_metric<KVQ_F32, true>), dim3(Hkv * rep * ((n_rlist + kMetricRows - 1) / kMetricRows)), blk,
+                     0, s, p, rlist, (int)n_rlist);
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(o M)");
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_metric<DT_, false>),
+                                               dim3(Hkv * rep * ((n + kMetricRows - 1) / kMetricRows)), blk, 0, s, p,
+                                               rlist, (int)n_rlist));
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(v M v)");
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, false>), dim3(Hkv * p.n_chunks), blk, 0, s, p));
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(terms)");
+  hipLaunchKernelGGL(cov_groups, dim3(1), blk, 0, s, p);
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(groups)");
+  hipLaunchKernelGGL(cov_roww, dim3((Hkv * NR + kCThreads - 1) / kCThreads), blk, 0, s, p, rowgrp);
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(row weights)");
+  // WVa is accumulated by the weighted pass: cleared by a fill kernel (graph-capture safe)
+  hipLaunchKernelGGL(cov_clear, dim3((Hkv * rep * n + kCThreads - 1) / kCThreads), blk, 0, s, p.WVa, Hkv * rep * n);
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(clear)");
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, true>), dim3(Hkv * p.n_chunks), blk, 0, s, p));
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(weighted terms)");
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_smat<DT_>), dim3(Hkv * (kCD / 16)), blk, 0, s, p));
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(S)");
+  hipLaunchKernelGGL(cov_final_sums, dim3(1), dim3(1024), 0, s, p);
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(sums)");
+  const int64_t nmax = std::max<int64_t>(Hkv * n, Hkv * kCD * kCD);
+  hipLaunchKernelGGL(cov_final, dim3((nmax + kCThreads - 1) / kCThreads), blk, 0, s, p);
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(final)");
+  return KVQ_OK;
+}

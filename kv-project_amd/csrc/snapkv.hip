@@ -25,6 +25,7 @@
 
 #include "common.hpp"
 #include "mfma_common.hpp"
+#include "row_tiles.hpp"
 
 namespace kvq {
 namespace {
@@ -36,14 +37,12 @@ constexpr int kSnapPool = 1024;       // keys of a pooling workgroup
 constexpr int kSnapMaxPad = 32;       // largest pooling half-width
 constexpr float kSnapLog2e = 1.4426950408889634f;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
 template <int DT>
 struct SnapTraits {
-  static constexpr int NH = DT == KVQ_F32 ? 2 : 1;          // operand parts (fp32: fp16 hi, lo)
+  static constexpr int NH = TileOps<DT>::NH;                // operand parts (fp32: fp16 hi, lo)
   static constexpr int NBW = DT == KVQ_F32 ? 2 : 4;         // row blocks of 16 per wavefront
   static constexpr int RG = 16 * NBW * kSnapWaves;          // rows per workgroup
-  static constexpr int ESZ = DT == KVQ_F32 ? 4 : 2;
+  static constexpr int ESZ = TileOps<DT>::ESZ;
 };
 
 struct SnapParams {
@@ -62,71 +61,6 @@ struct SnapParams {
   float* blockmax;                      // (BH, n_pool)
   float* out;                           // (BH, H)
 };
-
-template <int DT>
-__device__ __forceinline__ f32x4 snap_mfma(u32x4 a, u32x4 b, f32x4 c) {
-  if constexpr (DT == KVQ_BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
-                                                  0, 0);
-}
-
-// fp32 x[8] -> fp16 hi parts and lo parts (hi + lo = x to ~2^-22 relative)
-__device__ __forceinline__ void split_hi_lo(const float (&x)[8], u32x4& hi, u32x4& lo) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const _Float16 h0 = static_cast<_Float16>(x[2 * k]), h1 = static_cast<_Float16>(x[2 * k + 1]);
-    const _Float16 l0 = static_cast<_Float16>(x[2 * k] - static_cast<float>(h0));
-    const _Float16 l1 = static_cast<_Float16>(x[2 * k + 1] - static_cast<float>(h1));
-    hi[k] = pack_h2(h0, h1);
-    lo[k] = pack_h2(l0, l1);
-  }
-}
-
-// the operand parts of 8 consecutive channels at element i of a row (plain loads, in bounds)
-template <int DT>
-__device__ __forceinline__ void load_op(const void* base, int64_t i, u32x4 (&op)[SnapTraits<DT>::NH]) {
-  if constexpr (DT == KVQ_F32) {
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
-    const float4 a = p[0], c = p[1];
-    const float x[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-    split_hi_lo(x, op[0], op[1]);
-  } else {
-    op[0] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i);
-  }
-}
-
-// the same through a buffer resource (keys past the slice read as zero)
-template <int DT>
-__device__ __forceinline__ void load_op_buf(__amdgpu_buffer_rsrc_t rs, int byte_off, u32x4 (&op)[SnapTraits<DT>::NH]) {
-  if constexpr (DT == KVQ_F32) {
-    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, 0);
-    const u32x4 c = __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off + 16, 0, 0);
-    const float x[8] = {__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]),
-                        __uint_as_float(c[0]), __uint_as_float(c[1]), __uint_as_float(c[2]), __uint_as_float(c[3])};
-    split_hi_lo(x, op[0], op[1]);
-  } else {
-    op[0] = __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, 0);
-  }
-}
-
-// logits (dot products, before scaling) of one 16-key tile for one 16-row block
-template <int DT>
-__device__ __forceinline__ f32x4 tile_dots(const u32x4 (&kop)[4][SnapTraits<DT>::NH],
-                                           const u32x4 (&qop)[4][SnapTraits<DT>::NH]) {
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    acc = snap_mfma<DT>(kop[ks][0], qop[ks][0], acc);
-    if constexpr (DT == KVQ_F32) {
-      acc = snap_mfma<DT>(kop[ks][0], qop[ks][1], acc);
-      acc = snap_mfma<DT>(kop[ks][1], qop[ks][0], acc);
-    }
-  }
-  return acc;
-}
 
 // query operands of this wavefront's row blocks and the position of each lane's row (-1: no row)
 template <int DT>
@@ -189,7 +123,7 @@ __global__ __launch_bounds__(kSnapThreads) void snap_stats(SnapParams p) {
       load_op_buf<DT>(rk, static_cast<int>((static_cast<int64_t>(kj) * p.k_st + 32 * ks + 8 * g) * T::ESZ), kop[ks]);
 #pragma unroll
     for (int bw = 0; bw < T::NBW; ++bw) {
-      const f32x4 acc = tile_dots<DT>(kop, qop[bw]);
+      const f32x4 acc = tile_dots<DT, SnapTraits<DT>::NH, SnapTraits<DT>::NH>(kop, qop[bw]);
       float sv[4];
       float mt = -INFINITY;
 #pragma unroll
@@ -272,7 +206,7 @@ __global__ __launch_bounds__(kSnapThreads) void snap_cols(SnapParams p) {
                         kop[ks]);
 #pragma unroll
       for (int bw = 0; bw < T::NBW; ++bw) {
-        const f32x4 acc = tile_dots<DT>(kop, qop[bw]);
+        const f32x4 acc = tile_dots<DT, SnapTraits<DT>::NH, SnapTraits<DT>::NH>(kop, qop[bw]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) colv[i] += __builtin_amdgcn_exp2f(acc[i] * p.qscale - rm[bw]) * ril[bw];
       }

@@ -17,6 +17,7 @@ from .mixed import MixedKIVICache, c3_widths, mixed_decode, mixed_workspace_floa
 from .strata_state import StrataState, strata_pack, strata_tier_kernel
 from .quasar import QuasarState, stage_codebooks
 from .alloc import AllocWorkspace, allocate_layer, layer_costs, strata_allocate, strata_distortion
+from .coverage import coverage_groups, coverage_plan, coverage_stats
 
 __all__ = [
     "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes", "pack_rows", "unpack_rows",
@@ -27,5 +28,5 @@ __all__ = [
     "strata_decode", "strata_workspace_floats", "DctCache", "dct_decode", "dct_encode", "dct_table",
     "dct_workspace_floats", "MixedKIVICache", "c3_widths", "mixed_decode", "mixed_workspace_floats", "offset_table",
     "StrataState", "strata_pack", "strata_tier_kernel", "QuasarState", "stage_codebooks", "payload_bytes", "AllocWorkspace", "allocate_layer", "layer_costs",
-    "strata_allocate", "strata_distortion",
+    "strata_allocate", "strata_distortion", "coverage_groups", "coverage_plan", "coverage_stats",
 ]

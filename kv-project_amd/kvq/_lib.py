@@ -42,6 +42,9 @@ SIGNATURES = {
                                       vp, vp, vp, vp, vp, i64, i64, i32, i32, vp, vp, i32, i64, i64,
                                       vp, vp, vp, i32, vp, i64, f32, i64, i32, vp]),
     "kvq_snapkv_scores_workspace": (i64, [i64, i64, i64, i64, i64, i32]),
+    "kvq_coverage_stats_workspace": (i64, [i64, i64, i64, i64, i64]),
+    "kvq_coverage_stats": (i32, [vp, i32, i64, vp, vp, vp, i64, vp, i64, vp, i64, vp, i64, i64, vp, i64, i64, i64,
+                                 vp, i64, i64, i64, i64, i64, f32, f32, vp, vp, vp, vp, vp, vp, i64, vp]),
     "kvq_snapkv_scores": (i32, [vp, i32, i64, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64, f32, i32,
                                 vp, vp, i64, vp]),
     "kvq_topk_retain": (i32, [vp, i64, i64, i64, i64, vp, i64, vp]),
