@@ -364,8 +364,9 @@ int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
  * without fused multiply-add; s = max(fp16(max|X| / 7), 2^-24); code = clamp(rint(X / s), -7, 7) + 7.
  * x: (BH, T, d) of x_dtype, row stride d, head stride x_bh; T % 64 == 0, d == 128.
  * ctab: (16, 64) float32 (float32 of the closed form).  Per block, 1024 code bytes and 128 fp16
- * scales: for_values == 0 -> key layout (16 pack_codes rows of 64 bytes by coefficient; scales by
- * channel); for_values == 1 -> value tile (word (gp*16 + n)*8 + blk holds coefficients
+ * scales: for_values == 0 -> key layout (16 rows of 16 32-bit words by coefficient: word D holds
+ * channels 8D .. 8D+7, channel 8D + e at nibble {0,4,1,5,2,6,3,7}[e]; scales by channel);
+ * for_values == 1 -> value tile (word (gp*16 + n)*8 + blk holds coefficients
  * 8gp .. 8gp+7 of channel 16*blk + n, coefficient 8gp + e at nibble {0,4,1,5,2,6,3,7}[e]; scales
  * ordered [n][blk]).
  * ---------------------------------------------------------------------------------------- */
@@ -375,8 +376,9 @@ int kvq_dct_encode(const void* x, int x_dtype, int64_t BH, int64_t T, int64_t d,
 /* Decode over a DCT-coded context of T tokens (T % 64 == 0, kc/ks key blocks, vc/vs value blocks,
  * each (B*Hkv, T/64, ...)) plus n_exact exact rows (as kvq_kivi_decode's exact rows, dtype =
  * q_dtype): attention over the reconstructions x_n = sum_k C[k][n] s_k (code_k - 7), computed in
- * the coefficient domain (logits C^T (K-codes q), values (V-codes) (C p)).  out (B, Tq, Hq, d) of
- * q_dtype.  Workspace floats from kvq_dct_decode_workspace.  phases as kvq_mixed_decode's. */
+ * the coefficient domain (logits C^T (K-codes q), values (V-codes) (C p)).  ctab: 2048 float32,
+ * 16-byte aligned: the encoder's (16, 64) table followed by its transpose (64, 16).  out (B, Tq, Hq, d)
+ * of q_dtype.  Workspace floats from kvq_dct_decode_workspace.  phases as kvq_mixed_decode's. */
 int64_t kvq_dct_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t T,
                                  int64_t n_exact);
 int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B, int64_t Hq,

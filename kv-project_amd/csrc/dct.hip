@@ -11,7 +11,10 @@
 // float32 table of the kept rows (passed in); s and codes in float32 with IEEE division.
 //
 // Stored per (b, h, block):
-//   key codes   16 rows (coefficients) x 64 bytes in pack_codes order (byte i = c[2i] << 4 | c[2i+1])
+//   key codes   16 rows (coefficients) x 16 words: word D of row k holds the codes of channels
+//               8D .. 8D+7 of coefficient k, channel 8D + e at nibble kNib[e] = {0,4,1,5,2,6,3,7}[e]
+//               (the value tiles' nibble order: masking a word in place yields the 8 codes as fp16
+//               subnormals in channel order)
 //   key scales  128 fp16 (by channel)
 //   value codes 1 KiB decode tile: word (gp * 16 + n) * 8 + blk (gp = coefficient half 0/1, n = 0..15,
 //               blk = 0..7) holds the codes of coefficients 8gp .. 8gp+7 of channel 16*blk + n, code
@@ -74,10 +77,16 @@ __global__ __launch_bounds__(256) void dct_encode_kernel(const void* __restrict_
   uint8_t* out = codes + blk_all * 1024;
   if (!for_values) {
     scales[blk_all * kDD + c] = f32_to_f16(s);
+    // the 8 channels of a word are 8 consecutive lanes (total is a multiple of 128, so every
+    // wavefront that reaches here is whole): OR their nibbles together across the lanes
+    uint32_t* words = reinterpret_cast<uint32_t*>(out);
 #pragma unroll
     for (int k = 0; k < kDK; ++k) {
-      const int other = __shfl_down(q[k], 1, 64);
-      if ((c & 1) == 0) out[k * 64 + c / 2] = static_cast<uint8_t>((q[k] << 4) | other);
+      uint32_t w = static_cast<uint32_t>(q[k]) << (4 * kNibOfElem[c & 7]);
+      w |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), 1, 64));
+      w |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), 2, 64));
+      w |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), 4, 64));
+      if ((c & 7) == 0) words[k * 16 + c / 8] = w;
     }
   } else {
     const int n = c % 16, b8 = c / 16;
@@ -93,8 +102,6 @@ __global__ __launch_bounds__(256) void dct_encode_kernel(const void* __restrict_
   }
 }
 
-// Channel of slot s within an 8-channel k-slice of a pack_codes row (as the KIVI key kernels).
-__device__ __constant__ int kCosD[8] = {1, 5, 0, 4, 3, 7, 2, 6};
 
 struct DctParams {
   const void* q;
@@ -138,8 +145,8 @@ __device__ void dct_block(const DctParams& p, int bh, int sidx, float* smem) {
   const int r_n = n % R;
   const int hl = (n / R) & 1;
   const int ci = (l >> 2) & 3, ck = l & 3;
-  const int c0 = 32 * g + 8 * ci + kCosD[2 * ck];
-  const int c1 = 32 * g + 8 * ci + kCosD[2 * ck + 1];
+  const int c0 = 32 * g + 8 * ci + 2 * ck;          // key words unpack in channel order
+  const int c1 = c0 + 1;
   const float kinv = (ck & 1) ? 1.0f : 16.0f;
   uint32_t* bq = bq_all + wave * 2 * R * kBqStride;
   uint32_t* bv = bv_all + wave * R * 16;
@@ -454,6 +461,383 @@ void dct_split(DctParams p) {
   if (bh < p.BH) dct_block<R, DT>(p, bh, k % p.n_split, smem);
 }
 
+// ---------------------------------------------------------------------------------------------
+// dct_pair_split<DT>: 16-bit queries and outputs with R = 8 rows (rep * Tq in 5..8; C5's GQA 8).
+//
+// Each wavefront takes its blocks two at a time (slots A and B).  The 16 columns of every matrix
+// product are (slot, row) = (n / 8, n % 8): the logit and coefficient stages, whose constant operand
+// (the DCT table) is the same for every block, cover both blocks in one product, and the softmax
+// works on 16 useful values per lane.  One fp16 rounding each for q s^K, u, p and w (the bar of
+// 16-bit outputs); the -7 offset of the stored codes enters through products with a constant
+// operand K7 (-7 2^-24 at low-nibble positions, -112 2^-24 at high-nibble ones).
+//
+//   key stage    D_c = sum_i K7 x qt_i; D_A = D_c + sum_i codes_A,i x qt_i; D_B likewise.  qt_i is
+//                the lane's column's (q x s^K) over channels 32g + 8i + 0..7 with the scales of the
+//                column's own block, so D_A is right in slot A's columns and D_B in slot B's:
+//                u = n < 8 ? D_A : D_B (coefficient 4g + i), in units of 2^-20
+//   logit stage  s = C^T u                       (v_mfma_f32_16x16x16_f16, 4 tiles of 16 tokens)
+//   softmax      online, per column, lazy maximum; p carries 2^kPOff
+//   coef stage   w' = f C p                      (2 products over 64 tokens; f = 1/16 on the
+//                                                 coefficients whose value code is a high nibble)
+//   value stage  A = w' block-diagonal (rows of slot A against k < 16, slot B against k >= 16),
+//                D_v = A x K7, D_blk = D_v + A x codes_blk; acc += s^V D_blk (units of 2^-24)
+//
+// Memory: per pair 6 loads of distinct bytes (key words of A and B, 1 KiB each; value words, two
+// 1 KiB loads; key and value scales of both blocks, 8 bytes per lane each, handed out through the
+// wavefront's LDS).  Two pairs are in flight behind the one computed; every load is unconditional
+// (exact compiler wait counts), and a prefetch past the wavefront's range goes through a resource
+// of zero size, which returns zeros without touching memory.  No workgroup barrier before the
+// loop: the query operand and the DCT constants load straight into registers.
+constexpr int kPWaveLds = 424;     // dwords per wavefront: scales 256, w' 128, zero 4, alpha 16, m 16, pad
+
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma16(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4 c) {
+  // v_mfma_f32_16x16x16_f16: lane l holds A[l%16][4(l/16) + k], B[4(l/16) + k][l%16], k = 0..3
+  const half4v a = __builtin_bit_cast(half4v, (uint64_t)a0 | ((uint64_t)a1 << 32));
+  const half4v b = __builtin_bit_cast(half4v, (uint64_t)b0 | ((uint64_t)b1 << 32));
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pk_mul_h(uint32_t a, uint32_t b) { return w2(h2(a) * h2(b)); }
+
+template <int DT>
+__device__ __forceinline__ float half_as_f32(uint32_t w, int hi) {
+  const uint32_t hbits = hi ? (w >> 16) : (w & 0xffffu);
+  if constexpr (DT == KVQ_BF16) return __uint_as_float(hbits << 16);
+  else return f16_to_f32(static_cast<uint16_t>(hbits));
+}
+
+template <int DT, int kDepth>
+__device__ void dct_pair_block(const DctParams& p, int bh, int sidx, float* smem) {
+  constexpr int R = 8;
+  const int b = bh / p.Hkv, h = bh % p.Hkv;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const int l = threadIdx.x & 63;
+  const int g = l >> 4, n = l & 15;
+  const bool colB = n >= 8, rowB = g >= 2;
+  // epilogue partials [wave][row][d] + [wave][row][m, l], then the per-wavefront loop buffers
+  float* red_o = smem;
+  float* red_ml = smem + kDWaves * R * kDD;
+  uint32_t* wl = reinterpret_cast<uint32_t*>(red_ml + kDWaves * R * 2) + wave * kPWaveLds;
+  uint32_t* sc_l = wl;                 // [0, 128) key scales of A | B, [128, 256) value scales of A | B
+  uint32_t* wt = wl + 256;             // w' [16 columns][8 words], then 4 zero words
+  float* al = reinterpret_cast<float*>(wl + 388);       // 16 alphas
+  float* mlw = reinterpret_cast<float*>(wl + 404);      // 16 column maxima (epilogue)
+
+  // ---- this wavefront's pairs ----
+  const int64_t np = (p.nb + 1) / 2;
+  const int NW = p.n_split * kDWaves;
+  const int w_all = sidx * kDWaves + wave;
+  const int p0 = static_cast<int>(static_cast<int64_t>(w_all) * np / NW);
+  const int p1 = static_cast<int>(static_cast<int64_t>(w_all + 1) * np / NW);
+  const int p_last = static_cast<int>(np) - 1;
+
+  const int64_t blk0 = static_cast<int64_t>(bh) * p.nb;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.kc + blk0 * 1024, static_cast<uint32_t>(p.nb * 1024));
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(p.ks + blk0 * kDD, static_cast<uint32_t>(p.nb * kDD * 2));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vc + blk0 * 1024, static_cast<uint32_t>(p.nb * 1024));
+  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(p.vs + blk0 * kDD, static_cast<uint32_t>(p.nb * kDD * 2));
+  // zero-size resources: a prefetch past the range reads zeros and no memory
+  const __amdgpu_buffer_rsrc_t rk0 = make_rsrc(p.kc, 0), rks0 = make_rsrc(p.ks, 0);
+  const __amdgpu_buffer_rsrc_t rv0 = make_rsrc(p.vc, 0), rvs0 = make_rsrc(p.vs, 0);
+  const int vk = n * 64 + 16 * g;                  // key words 4g .. 4g+3 of coefficient row n
+  const int vv = ((g & 1) * 16 + n) * 32;          // value words ((g & 1) * 16 + n) * 8 + 0..7
+  const int vsc = (l & 31) * 8;                    // 8 scale bytes of block A (l < 32) or B
+
+  struct Pair {
+    u32x4 ka, kb;          // key words of both blocks
+    u32x4 vw[2];           // value words of the row slot's block
+    uint2 ks, vs;          // 8 bytes of the key / value scales of A (lanes 0-31) or B (32-63)
+  };
+  // each pair's loads stay one group in program order (the scheduler may not interleave groups):
+  // the hardware counts outstanding loads in issue order, so interleaving would make every wait
+  // also wait for later pairs
+  auto load_pair = [&](int pi, Pair& c) {
+    __builtin_amdgcn_sched_barrier(0);
+    const bool live = pi < p1;                     // uniform
+    pi = max(0, min(pi, p_last));
+    const int bA = 2 * pi;
+    const int dB = (bA + 1 < p.nb) ? 1 : 0;        // a final single block stands in for its own slot B
+    const int sA = __builtin_amdgcn_readfirstlane(bA * 1024);
+    const int sB = __builtin_amdgcn_readfirstlane((bA + dB) * 1024);
+    const int sS = __builtin_amdgcn_readfirstlane(bA * kDD * 2);
+    const __amdgpu_buffer_rsrc_t k_ = live ? rk : rk0, ks_ = live ? rks : rks0;
+    const __amdgpu_buffer_rsrc_t v_ = live ? rv : rv0, vs_ = live ? rvs : rvs0;
+    // scales first: the step's first wait (for the LDS hand-off) then leaves the codes in flight
+    const int os = vsc + ((l >= 32) ? dB * 256 : 0);
+    const auto kk = __builtin_amdgcn_raw_buffer_load_b64(ks_, os, sS, 0);
+    const auto vv2 = __builtin_amdgcn_raw_buffer_load_b64(vs_, os, sS, 0);
+    c.ka = __builtin_amdgcn_raw_buffer_load_b128(k_, vk, sA, 2);
+    c.kb = __builtin_amdgcn_raw_buffer_load_b128(k_, vk, sB, 2);
+    const int ov = vv + (rowB ? dB * 1024 : 0);
+    c.vw[0] = __builtin_amdgcn_raw_buffer_load_b128(v_, ov, sA, 2);
+    c.vw[1] = __builtin_amdgcn_raw_buffer_load_b128(v_, ov + 16, sA, 2);
+    c.ks = make_uint2(kk[0], kk[1]);
+    c.vs = make_uint2(vv2[0], vv2[1]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ---- prologue: the first kDepth pairs, then the query operand and the DCT constants, all in flight ----
+  // (query and table loads first: the wait for them then leaves the pairs' loads outstanding)
+  // query operand of the key stage: row n % 8 (rows past R_real read the last row, then zero),
+  // channels 32g + 8i + 2jj, +1; x16 on the low-nibble pairs (jj even)
+  const int rq = n & 7;
+  const uint4* qrow = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) +
+                                                     dct_q_offset(p, b, h, min(rq, p.R_real - 1)) + 32 * g);
+  uint4 qw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qw[i] = qrow[i];
+  // DCT constants: C (16, 64) then C^T (64, 16) in ctab
+  const float4* c4 = reinterpret_cast<const float4*>(p.ctab);
+  float4 ctl[4], cwl[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) ctl[t] = c4[256 + ((16 * t + n) * 16 + 4 * g) / 4];             // C^T[16t+n][4g..]
+#pragma unroll
+  for (int k = 0; k < 4; ++k) cwl[k] = c4[(n * kDB + 32 * (k >> 1) + 16 * (k & 1) + 4 * g) / 4];  // C[n][..]
+  __builtin_amdgcn_sched_barrier(0);
+  Pair buf[kDepth + 1];
+#pragma unroll
+  for (int j = 0; j < kDepth; ++j) load_pair(p0 + j, buf[j]);
+  if (l < 4) wt[128 + l] = 0u;
+
+  const float qsc = rq < p.R_real ? p.qscale : 0.0f;
+  uint32_t qh[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t wv[4] = {qw[i].x, qw[i].y, qw[i].z, qw[i].w};
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const float f = (jj & 1) ? qsc : 16.0f * qsc;
+      qh[i][jj] = pack_h2(static_cast<_Float16>(half_as_f32<DT>(wv[jj], 0) * f),
+                          static_cast<_Float16>(half_as_f32<DT>(wv[jj], 1) * f));
+    }
+  }
+  // logit tiles: A[token 16t + n][coefficient 4g + k] = C[4g + k][16t + n]
+  uint32_t cl[4][2];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    cl[t][0] = pack_h2(static_cast<_Float16>(ctl[t].x), static_cast<_Float16>(ctl[t].y));
+    cl[t][1] = pack_h2(static_cast<_Float16>(ctl[t].z), static_cast<_Float16>(ctl[t].w));
+  }
+  // coefficient stage: A[coefficient n][8g + j] = f_n C[n][32ks + 16(j >> 2) + 4g + (j & 3)]
+  const float fn = ((n >> 1) & 1) ? 0.0625f : 1.0f;
+  uint32_t cw[2][4];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int jh = 0; jh < 2; ++jh) {
+      const float4 v = cwl[2 * ks + jh];
+      cw[ks][2 * jh] = pack_h2(static_cast<_Float16>(fn * v.x), static_cast<_Float16>(fn * v.y));
+      cw[ks][2 * jh + 1] = pack_h2(static_cast<_Float16>(fn * v.z), static_cast<_Float16>(fn * v.w));
+    }
+  const u32x4 k7 = u32x4{0x80078007u, 0x80708070u, 0x80078007u, 0x80708070u};
+
+  auto unpack = [](uint32_t w) -> half8 {
+    const uint32_t w8 = w >> 8;
+    return as_half8(u32x4{w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u});
+  };
+  constexpr float kTwo20 = 1048576.0f;
+  constexpr float kTwo24 = 16777216.0f;
+  constexpr float kLazy = 4.0f;
+  constexpr float kPOff = 6.0f;
+
+  float acc[8][4];                                 // rows (slot, row) 4g + i, channel 16 blk + n
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.0f;
+  float m_run = -INFINITY, la = 0.0f;              // column n
+
+  auto step = [&](const Pair& c, bool hasB) {
+    // ---- scales through the wavefront's LDS ----
+    *reinterpret_cast<uint2*>(sc_l + 2 * l) = c.ks;
+    *reinterpret_cast<uint2*>(sc_l + 128 + 2 * l) = c.vs;
+    wave_lds_fence();
+    u32x4 sk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sk[i] = *reinterpret_cast<const u32x4*>(sc_l + (colB ? 64 : 0) + 16 * g + 4 * i);
+    const u32x4 sv4 = *reinterpret_cast<const u32x4*>(sc_l + 128 + (rowB ? 64 : 0) + 4 * n);
+    // ---- key stage ----
+    u32x4 qt[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) qt[i][jj] = pk_mul_h(qh[i][jj], sk[i][jj]);
+    // three independent chains (offset, codes of A, codes of B), joined after the select
+    f32x4 dc = f32x4{0.f, 0.f, 0.f, 0.f}, da = dc, db = dc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dc = mfma(as_half8(k7), as_half8(qt[i]), dc);
+      da = mfma(unpack(c.ka[i]), as_half8(qt[i]), da);
+      db = mfma(unpack(c.kb[i]), as_half8(qt[i]), db);
+    }
+    const f32x4 du = (colB ? db : da) + dc;
+    const uint32_t ub0 = pack_h2(static_cast<_Float16>(du[0] * kTwo20), static_cast<_Float16>(du[1] * kTwo20));
+    const uint32_t ub1 = pack_h2(static_cast<_Float16>(du[2] * kTwo20), static_cast<_Float16>(du[3] * kTwo20));
+    // ---- logits: token 16t + 4g + i of column n ----
+    float s[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const f32x4 e = mfma16(cl[t][0], cl[t][1], ub0, ub1, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[t][i] = e[i];
+    }
+    if (!hasB && colB) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[t][i] = -INFINITY;
+    }
+    // ---- online softmax, lazy maximum ----
+    float lm = s[0][0];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lm = fmaxf(lm, s[t][i]);
+    if (__any(lm > m_run + kLazy)) {
+      const float m_new = fmaxf(m_run, xmax32(xmax16(lm)));
+      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      la *= alpha;
+      m_run = m_new;
+      if (g == 0) al[n] = alpha;                   // alpha of column n for the value-stage rows
+      wave_lds_fence();
+      const float4 a4 = reinterpret_cast<const float4*>(al)[g];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        acc[k][0] *= a4.x;
+        acc[k][1] *= a4.y;
+        acc[k][2] *= a4.z;
+        acc[k][3] *= a4.w;
+      }
+    }
+    const float mo = (m_run == -INFINITY ? 0.0f : m_run) - kPOff;
+    float pr[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[t][i] = __builtin_amdgcn_exp2f(s[t][i] - mo);
+        la += pr[t][i];
+      }
+    // ---- coefficient stage: w'[coefficient 4g + i] of column n ----
+    f32x4 dw = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x4 pb = u32x4{pack_h2(static_cast<_Float16>(pr[2 * ks][0]), static_cast<_Float16>(pr[2 * ks][1])),
+                             pack_h2(static_cast<_Float16>(pr[2 * ks][2]), static_cast<_Float16>(pr[2 * ks][3])),
+                             pack_h2(static_cast<_Float16>(pr[2 * ks + 1][0]), static_cast<_Float16>(pr[2 * ks + 1][1])),
+                             pack_h2(static_cast<_Float16>(pr[2 * ks + 1][2]), static_cast<_Float16>(pr[2 * ks + 1][3]))};
+      dw = mfma(as_half8(u32x4{cw[ks][0], cw[ks][1], cw[ks][2], cw[ks][3]}), as_half8(pb), dw);
+    }
+    // ---- w' transposed through LDS into the block-diagonal A operand of the value stage ----
+    *reinterpret_cast<uint2*>(wt + n * 8 + 2 * g) =
+        make_uint2(pack_h2(static_cast<_Float16>(dw[0]), static_cast<_Float16>(dw[1])),
+                   pack_h2(static_cast<_Float16>(dw[2]), static_cast<_Float16>(dw[3])));
+    wave_lds_fence();
+    const u32x4 aw = *reinterpret_cast<const u32x4*>(wt + (colB == rowB ? n * 8 + 4 * (g & 1) : 128));
+    const f32x4 dv = mfma(as_half8(aw), as_half8(k7), f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      const f32x4 d5 = mfma(as_half8(aw), unpack(c.vw[blk >> 2][blk & 3]), dv);
+      const float sv = h2f(sv4[blk >> 1], blk & 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[blk][i] = __builtin_fmaf(sv, d5[i], acc[blk][i]);
+    }
+  };
+
+  {
+    const int last_full = (p.nb & 1) ? p_last : static_cast<int>(np);   // pairs below it have a block B
+    // kDepth pairs in flight behind the one being computed; loads unconditional, steps guarded
+    for (int pi = p0; pi < p1; pi += kDepth + 1) {
+#pragma unroll
+      for (int j = 0; j <= kDepth; ++j) {
+        load_pair(pi + j + kDepth, buf[(j + kDepth) % (kDepth + 1)]);
+        if (j == 0 || pi + j < p1) step(buf[j], pi + j < last_full);
+      }
+    }
+  }
+
+  // ---- epilogue ----
+  // per column (m, l) to the value-stage layout: lane (g, n) needs columns 4g .. 4g+3
+  const float l_col = xsum32(xsum16(la));
+  if (g == 0) {
+    mlw[n] = m_run;
+    reinterpret_cast<float*>(wt)[n] = l_col;        // w' buffer is free now
+  }
+  wave_lds_fence();
+  const float4 m4 = reinterpret_cast<const float4*>(mlw)[g];
+  const float4 l4 = reinterpret_cast<const float4*>(wt)[g];
+  // slots merged in registers: lanes l and l ^ 32 hold rows 4(g & 1) + i of slots A and B; after a
+  // permlane32 swap element 0 is slot A's value and element 1 slot B's in both halves
+  const float mi[4] = {m4.x, m4.y, m4.z, m4.w}, li[4] = {l4.x, l4.y, l4.z, l4.w};
+  float Mr[4], Lr[4], wA[4], wB[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto ms = __builtin_amdgcn_permlane32_swap(__float_as_uint(mi[i]), __float_as_uint(mi[i]), false, false);
+    const auto ls = __builtin_amdgcn_permlane32_swap(__float_as_uint(li[i]), __float_as_uint(li[i]), false, false);
+    const float ma = __uint_as_float(ms[0]), mb = __uint_as_float(ms[1]);
+    const float M = fmaxf(ma, mb);
+    wA[i] = ma == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ma - M);
+    wB[i] = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - M);
+    Mr[i] = M;
+    Lr[i] = wA[i] * __uint_as_float(ls[0]) + wB[i] * __uint_as_float(ls[1]);
+  }
+  if (g < 2) {
+    if (n == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        red_ml[(wave * R + 4 * g + i) * 2 + 0] = Mr[i];
+        red_ml[(wave * R + 4 * g + i) * 2 + 1] = Lr[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const auto as = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[blk][i]), __float_as_uint(acc[blk][i]),
+                                                       false, false);
+      const float o = (wA[i] * __uint_as_float(as[0]) + wB[i] * __uint_as_float(as[1])) * kTwo24;
+      if (g < 2) red_o[(wave * R + 4 * g + i) * kDD + 16 * blk + n] = o;
+    }
+  __syncthreads();
+  const int64_t po = static_cast<int64_t>(bh) * p.S_all + sidx;
+  for (int idx = threadIdx.x; idx < p.R_real * kDD; idx += kDThreads) {
+    const int r = idx / kDD, c = idx % kDD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDWaves; ++w) M = fmaxf(M, red_ml[(w * R + r) * 2]);
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kDWaves; ++w) {
+      const float mw_ = red_ml[(w * R + r) * 2];
+      const float wgt = (mw_ == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw_ - M);
+      O += wgt * red_o[(w * R + r) * kDD + c];
+      L += wgt * red_ml[(w * R + r) * 2 + 1];
+    }
+    p.ws_o[(po * R + r) * kDD + c] = O;
+    if (c == 0) {
+      p.ws_m[po * R + r] = M - kPOff;
+      p.ws_l[po * R + r] = L;
+    }
+  }
+}
+
+// one workgroup per CU (one wavefront per SIMD) with kPairDepth pairs in flight per wavefront: a
+// wavefront's prologue and epilogue are paid over more pairs, and the registers a single
+// wavefront may hold carry the deep prefetch
+constexpr int kPairDepth = 2;
+
+template <int DT>
+__global__ __launch_bounds__(kDThreads) __attribute__((amdgpu_waves_per_eu(1)))
+void dct_pair_split(DctParams p) {
+  extern __shared__ float smem[];
+  const int k = blockIdx.x / 8;
+  const int bh = blockIdx.x % 8 + 8 * (k / p.n_split);
+  if (bh < p.BH) dct_pair_block<DT, kPairDepth>(p, bh, k % p.n_split, smem);
+}
+
+// LDS of the pair kernel: the epilogue's partials and the wavefronts' loop buffers, disjoint
+constexpr size_t kPairSmem = (kDWaves * 8 * kDD + kDWaves * 8 * 2 + kDWaves * kPWaveLds) * 4;
 
 }  // namespace
 }  // namespace kvq
@@ -488,14 +872,28 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
                                float score_weight, int64_t split_tokens, int phases, void* stream);
 
 namespace {
-int64_t dct_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t T, int64_t n_exact, int64_t* ex_floats,
-                     int* S) {
-  // 3 workgroups per CU: LDS-bound (~41 KB each at 8 rows)
-  *S = T > 0 ? kvq::plan_block_splits(B * Hkv, T / 64, 3, 4) : 0;
+// split counts: dct_split runs 3 workgroups per CU (LDS-bound, ~41 KB each at 8 rows) over single
+// blocks; dct_pair_split (16-bit, R = 8) 1 per CU over pairs of blocks
+int dct_splits_single(int64_t BH, int64_t T) { return T > 0 ? kvq::plan_block_splits(BH, T / 64, 3, 4) : 0; }
+int dct_splits_pair(int64_t BH, int64_t T) { return T > 0 ? kvq::plan_block_splits(BH, (T / 64 + 1) / 2, 1, 1) : 0; }
+// the pair kernel: 16-bit q with R = 8, query rows 16-byte aligned (it loads them as 16-byte words)
+bool dct_uses_pairs(int R, int q_dtype, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st) {
+  return R == 8 && q_dtype != KVQ_F32 && reinterpret_cast<uintptr_t>(q) % 16 == 0 && q_sb % 8 == 0 &&
+         q_sh % 8 == 0 && q_st % 8 == 0;
+}
+
+// workspace floats; *S receives the split count of the kernel `kind` names (1 pairs, 0 single
+// blocks, -1 the larger of the two: a size query that does not know the kernel)
+int64_t dct_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t T, int64_t n_exact, int kind,
+                     int64_t* ex_floats, int* S) {
+  const int R = kvq::pow2_rows((Hq / Hkv) * Tq);
+  const int s1 = dct_splits_single(B * Hkv, T);
+  const int s2 = R == 8 ? dct_splits_pair(B * Hkv, T) : 0;
+  *S = kind < 0 ? std::max(s1, s2) : (kind == 1 ? s2 : s1);
   *ex_floats = (n_exact > 0 && !kvq::exact_in_merge(n_exact))
                    ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
-  const int64_t R = kvq::pow2_rows((Hq / Hkv) * Tq);
-  return *ex_floats + B * Hkv * static_cast<int64_t>(*S) * R * (128 + 2);
+  const int Smax = std::max(s1, s2);
+  return *ex_floats + B * Hkv * static_cast<int64_t>(Smax) * R * (128 + 2);
 }
 }  // namespace
 
@@ -504,7 +902,7 @@ extern "C" int64_t kvq_dct_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, 
   if (d != 128 || B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Tq <= 0 || T < 0 || T % 64 != 0) return -1;
   int64_t ex;
   int S;
-  return dct_ws_parts(B, Hq, Hkv, Tq, T, n_exact, &ex, &S);
+  return dct_ws_parts(B, Hq, Hkv, Tq, T, n_exact, -1, &ex, &S);
 }
 
 extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B,
@@ -527,7 +925,8 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
   KVQ_REQUIRE(q && out && workspace, "kvq_dct_decode: null q / out / workspace");
   int64_t ex_floats;
   int S;
-  const int64_t need = dct_ws_parts(B, Hq, Hkv, Tq, T, n_exact, &ex_floats, &S);
+  const bool pairs = dct_uses_pairs(pow2_rows(R_real), q_dtype, q, q_sb, q_sh, q_st);
+  const int64_t need = dct_ws_parts(B, Hq, Hkv, Tq, T, n_exact, pairs ? 1 : 0, &ex_floats, &S);
   KVQ_REQUIRE(workspace_floats >= need, "kvq_dct_decode: workspace too small (%lld < %lld floats)",
               (long long)workspace_floats, (long long)need);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -567,7 +966,13 @@ extern "C" int kvq_dct_decode(const void* q, int q_dtype, int64_t q_sb, int64_t 
   const size_t split_smem = std::max<size_t>(
       (R * kDD + kDWaves * (2 * R * kBqStride + R * 16) + kDWaves * R * 19) * sizeof(float) + 12 * 64 * 16 + kDK * kDB * 4,
       (kDWaves * R * kDD + kDWaves * 2 * R) * sizeof(float));
-  if (S > 0 && (phases & 1)) {
+  if (S > 0 && (phases & 1) && pairs) {
+    if (q_dtype == KVQ_F16)
+      hipLaunchKernelGGL((dct_pair_split<KVQ_F16>), dim3(static_cast<unsigned>(S) * bh_pad), dim3(kDThreads), kPairSmem, s, p);
+    else
+      hipLaunchKernelGGL((dct_pair_split<KVQ_BF16>), dim3(static_cast<unsigned>(S) * bh_pad), dim3(kDThreads), kPairSmem, s, p);
+    KVQ_LAUNCH_CHECK("kvq_dct_decode(pair split)");
+  } else if (S > 0 && (phases & 1)) {
 #define KVQ_DCT_SPLIT(R_, DT_) \
     hipLaunchKernelGGL((dct_split<R_, DT_>), dim3(static_cast<unsigned>(S) * bh_pad), dim3(kDThreads), split_smem, s, p)
 #define KVQ_DCT_R(DT_)                                   \

@@ -37,10 +37,21 @@ def dct_table(device="cuda") -> torch.Tensor:
     return _TABLES[key]
 
 
+def dct_decode_table(device="cuda") -> torch.Tensor:
+    """(2048,) float32: the table C (16, 64) followed by its transpose (64, 16), the decode's constant
+    operands (each lane reads 16-byte runs of either)."""
+    key = "dec:" + str(device)
+    if key not in _TABLES:
+        C = dct_table(device)
+        _TABLES[key] = torch.cat([C.reshape(-1), C.t().contiguous().reshape(-1)])
+    return _TABLES[key]
+
+
 @torch.no_grad()
 def dct_encode(x: torch.Tensor, for_values: bool = False):
     """x (B, Hkv, T, 128), T % 64 == 0 -> (codes (B, Hkv, T/64, 1024) uint8, scales (B, Hkv, T/64, 128)
-    fp16) in the key layout (16 pack_codes rows by coefficient, scales by channel) or, with
+    fp16) in the key layout (16 rows of 16 words by coefficient: word D holds channels 8D .. 8D+7, channel
+    8D + e at nibble (0, 4, 1, 5, 2, 6, 3, 7)[e]; scales by channel) or, with
     ``for_values``, the value-tile layout the decode reads."""
     _lib.require_gpu(x)
     B, H, T, d = x.shape
@@ -128,7 +139,7 @@ def dct_decode(q: torch.Tensor, scaling: float, cache: DctCache, *, q_pos: Optio
     ep = cache.exact_pos if q_pos is not None else None
     qp = q_pos if ep is not None else None
     _lib.call("kvq_dct_decode", q.data_ptr(), _lib.DTYPE_CODE[q.dtype], q.stride(0), q.stride(1), q.stride(2),
-              B, Hq, Hkv, Tq, d, float(scaling), dct_table(q.device).data_ptr(), cache.T, cache.kc.data_ptr(),
+              B, Hq, Hkv, Tq, d, float(scaling), dct_decode_table(q.device).data_ptr(), cache.T, cache.kc.data_ptr(),
               cache.ks.data_ptr(), cache.vc.data_ptr(), cache.vs.data_ptr(), cache.k_exact.data_ptr(),
               cache.v_exact.data_ptr(), cache.k_exact.shape[2], cache.n_exact, _lib.ptr(ep), _lib.ptr(qp),
               out.data_ptr(), workspace.data_ptr(), workspace.numel(), int(phases), _lib.stream_of(q))

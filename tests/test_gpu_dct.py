@@ -18,11 +18,12 @@ _NIB = [0, 4, 1, 5, 2, 6, 3, 7]
 
 
 def _keys_to_oracle(codes: np.ndarray) -> np.ndarray:
-    """(BH, nb, 1024) key layout -> (BH, nb, 16, 128) codes."""
-    rows = codes.reshape(codes.shape[0], codes.shape[1], 16, 64)
-    out = np.empty(rows.shape[:3] + (128,), np.uint8)
-    out[..., 0::2] = rows >> 4
-    out[..., 1::2] = rows & 15
+    """(BH, nb, 1024) key layout -> (BH, nb, 16, 128) codes: row k = 16 words, word D holds channel
+    8D + e of coefficient k at nibble _NIB[e]."""
+    words = codes.view(np.uint32).reshape(codes.shape[0], codes.shape[1], 16, 16)      # k, D
+    out = np.empty(words.shape[:3] + (128,), np.uint8)
+    for e in range(8):
+        out[..., e::8] = (words >> (4 * _NIB[e])) & 15
     return out
 
 
@@ -132,6 +133,47 @@ def test_decode_r8_bf16_gqa8():
     V = torch.randn((B, Hkv, T, d), generator=g).to(torch.bfloat16)
     q = torch.randn((B, Hq, 1, d), generator=g).to(torch.bfloat16)
     cache = kvq.DctCache.from_context(K.cuda(), V.cuda(), window=W)
+    out = kvq.dct_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
+    ref = _oracle(cache, q, d ** -0.5)
+    assert float(np.abs(out - ref).max()) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype,B,Hq,Hkv,Tq,T,W,seed", [
+    (torch.float16, 2, 16, 2, 1, 64 * 33 + 50, 50, 1),     # fp16, odd block count: a final single block
+    (torch.bfloat16, 1, 4, 2, 3, 64 + 10, 10, 2),          # rep 2 x Tq 3 = 6 rows padded to 8, one block
+    (torch.bfloat16, 1, 8, 2, 2, 640, 0, 3),               # rep 4 x Tq 2 = 8 rows, coded only
+    (torch.bfloat16, 1, 64, 8, 1, 64 * 259, 0, 4),         # C5 heads, odd block count, many splits
+])
+def test_decode_r8_pairs(dtype, B, Hq, Hkv, Tq, T, W, seed):
+    """The 16-bit R = 8 kernel (dct_pair_split: blocks two at a time) against the float64 oracle:
+    fp16 and bf16, 6 or 8 rows, a single block, odd block counts (the last pair's slot B masked)."""
+    import kvq
+    g = torch.Generator().manual_seed(seed)
+    d = 128
+    K = (torch.randn((B, Hkv, T, d), generator=g).cumsum(2) * 0.15).to(dtype)
+    V = torch.randn((B, Hkv, T, d), generator=g).to(dtype)
+    q = torch.randn((B, Hq, Tq, d), generator=g).to(dtype)
+    cache = kvq.DctCache.from_context(K.cuda(), V.cuda(), window=W)
+    out = kvq.dct_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
+    ref = _oracle(cache, q, d ** -0.5)
+    err = float(np.abs(out - ref).max())
+    print(f"pairs {dtype} B={B} Hq={Hq} Hkv={Hkv} Tq={Tq} T={T}: max-abs-err {err:.3e}")
+    assert err <= 1e-2, err
+
+
+def test_decode_r8_pairs_peaked_logits():
+    """bf16 R = 8 with one dominant block late in the context: the lazy maximum rescales the value
+    accumulators of both slots through the alpha hand-off."""
+    import kvq
+    g = torch.Generator().manual_seed(5)
+    B, Hq, Hkv, T, d = 1, 16, 2, 64 * 40, 128
+    K = torch.randn((B, Hkv, T, d), generator=g) * 0.3
+    K[:, :, 1920:1984] += 3.0
+    K[:, :, 640:704] += 1.5
+    V = torch.randn((B, Hkv, T, d), generator=g)
+    q = (torch.ones((B, Hq, 1, d)) * 0.5).to(torch.bfloat16)
+    K, V = K.to(torch.bfloat16), V.to(torch.bfloat16)
+    cache = kvq.DctCache.from_context(K.cuda(), V.cuda(), window=0)
     out = kvq.dct_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
     ref = _oracle(cache, q, d ** -0.5)
     assert float(np.abs(out - ref).max()) <= 1e-2
