@@ -18,6 +18,7 @@ The other rows of the path are measured by the same script with ``--workload``:
   micro   the reference's decode-attention microbenchmark: SDPA (full, evicting) vs the packed kernels
   alloc   STRATA rate allocation of one layer (compression side: order, head sum, Lagrangian search)
   snapkv  SnapKV scores of a prefilled layer at the C4 shape (the prefill form of the eviction scores)
+  compress  STRATA compression of one Llama-3-8B-shaped layer from its own queries, end to end on the device
 Each prints one JSON line of the same form (its own metric, roofline and CPU baseline).
 
 Timing: a settle phase (``settle_ms`` of the same step: the device's clocks rise over the first
@@ -1071,9 +1072,118 @@ def run_snapkv(args) -> dict:
     return res
 
 
+# ---------------------------------------------------------------------------------------------
+# F1: STRATA compression of one layer, end to end on the device
+
+def run_compress(args) -> dict:
+    import numpy as np
+    import torch
+    import kvq
+    from kvq.strata_compress import StrataCompressor
+    B, Hq, Hkv, d, H, keep = 1, 32, 8, 128, 32768, 0.125
+    log("generating one Llama-3-8B-shaped layer (queries at every position, keys, values, output metric)")
+    g = torch.Generator(device="cuda").manual_seed(47)
+    q = torch.randn((B, Hq, H, d), generator=g, device="cuda").to(torch.bfloat16)
+    t3 = torch.distributions.StudentT(3.0).sample((Hkv, 1, d)).abs().clamp(0.2, 8.0).cuda()
+    k = (torch.randn((B, Hkv, H, d), generator=g, device="cuda") * t3).to(torch.bfloat16)
+    v = torch.randn((B, Hkv, H, d), generator=g, device="cuda").to(torch.bfloat16)
+    Wo = torch.randn((Hq, 64, d), generator=g, device="cuda") / 8
+    M = (Wo.transpose(1, 2) @ Wo).contiguous()
+    scaling = d ** -0.5
+    comp = StrataCompressor(keep)
+
+    def compress():
+        al_ = comp.compress_layer(q, k, v, scaling, H, M)
+        return al_, comp.pack(al_)
+
+    for _ in range(2):                                       # warm-up: plans, workspaces, clocks
+        compress()
+    torch.cuda.synchronize()
+    reps = max(3, args.steps // 20)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        al, packed = compress()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    # phases, HIP events on the launch stream (each phase's own host work included)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    e = [ev() for _ in range(5)]
+    rs, re = al["rs"], al["re"]
+    e[0].record()
+    st = kvq.coverage_stats(q, k, v, scaling, H, rs, re, M)
+    e[1].record()
+    dist = kvq.strata_distortion(k[0, :, rs:re], v[0, :, rs:re], st["A"], st["W"], st["DD"], st["S"], st["Mbar"],
+                                 comp.bits)
+    e[2].record()
+    kvq.allocate_layer(dist["D"], comp.bits, d, H, keep, rs, re)
+    e[3].record()
+    comp.pack(al)
+    e[4].record()
+    torch.cuda.synchronize()
+    phase = {nm: e[i].elapsed_time(e[i + 1]) for i, nm in enumerate(("coverage", "distortion", "allocation", "pack"))}
+    # coverage work: logits and value sums of every kept group's rows over its causal keys
+    plan = kvq.coverage_plan(H, rs, re, Hq // Hkv, None, False, "cuda")
+    cov_flops = sum(2 * 2 * (Hq // Hkv) * len(plan.groups[gi]) * (int(plan.groups[gi].max()) + 1) * d * Hkv
+                    for gi in plan.kept)
+    dist_flops = 2 * Hkv * (re - rs) * len(comp.bits) * 2 * d * d
+    tf_cov = cov_flops / (phase["coverage"] * 1e-3) / 1e12
+    # the compressed layer decodes through the native state (one appended token, one query step)
+    state = comp.native_state(al, packed, k, v, 4, torch.bfloat16)
+    kn = torch.randn((1, Hkv, 1, d), generator=g, device="cuda").to(torch.bfloat16)
+    state.append(kn, kn, torch.tensor([H]))
+    qn = torch.randn((1, Hq, 1, d), generator=g, device="cuda").to(torch.bfloat16)
+    dec_ms = eager_ms(lambda: state.attend(qn, scaling, torch.tensor([H])), 50, 10)
+    res = _result(args, metric="STRATA compression of one layer on the device: ms/layer (coverage statistics, "
+                               "distortion table, allocation, codes)",
+                  value=ms, unit="ms", ms_per_step=ms, hib=False,
+                  workload=f"F1: StrataMethod.compress_layer + pack for one Llama-3-8B-shaped layer from its own "
+                           f"queries (B=1, Hq={Hq}, Hkv={Hkv}, d={d}, H={H}, bf16, keep {keep}, widths 2/4/8 + "
+                           f"drop/exact, 4 rounds), synthetic Student-t keys and random o_proj metric",
+                  config={"global_batch": B, "seq_len": H, "parallelism": "single GPU", "keep": keep,
+                          "bits": list(comp.bits)},
+                  dtype="bf16",
+                  roofline={"bound": "mfma", "achieved": round(tf_cov, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                            "frac": round(tf_cov / 2500.0, 4), "traffic": None,
+                            "kernel": "kvq_coverage_stats (logits and value sums of the coverage groups)",
+                            "kernel_us": round(phase["coverage"] * 1e3, 3), "kernel_flops": int(cov_flops)},
+                  phases_ms={k_: round(v_, 4) for k_, v_ in phase.items()},
+                  distortion_tflops=round(dist_flops / (phase["distortion"] * 1e-3) / 1e12, 2),
+                  counts=al["counts"], bits=al["bits"], payload_bytes=comp.payload(packed),
+                  payload_vs_bits=comp.payload(packed) * 8 / al["bits"] - 1.0, distortion=round(al["distortion"], 6),
+                  native_decode_us=round(dec_ms * 1e3, 3), native_context_bytes=state.context_bytes())
+    log(f"compress {ms:.2f} ms/layer ({phase}); counts {al['counts']}; native decode {dec_ms * 1e3:.1f} us")
+    if not args.no_cpu_baseline:
+        # the oracle chain (float64 numpy) on one KV head at an 8192-token context, scaled to the layer:
+        # coverage x (H / Hs)^2 (groups and their causal key ranges both grow with H), the rest x H / Hs,
+        # then x Hkv
+        import oracle.coverage as oc
+        import oracle.strata as os_
+        import oracle.strata_alloc as oa
+        Hs, rep = 8192, Hq // Hkv
+        qs = q[0, :rep, :Hs].float().cpu().numpy()
+        ks_, vs_ = k[0, :1, :Hs].float().cpu().numpy(), v[0, :1, :Hs].float().cpu().numpy()
+        Ms = M[:rep].double().cpu().numpy()
+        c0 = time.perf_counter()
+        sto = oc.coverage_stats(qs, np.arange(Hs), ks_, vs_, scaling, Hs, 4, Hs - 32, Ms, oc.CoverageParams())
+        c1 = time.perf_counter()
+        signs = os_.rotation_signs(d)
+        _, Yk = os_.strata_center_rotate(ks_[:, 4:Hs - 32], signs)
+        _, Yv = os_.strata_center_rotate(vs_[:, 4:Hs - 32], signs)
+        Dt = oa.distortion_table(Yk, Yv, sto["S"], sto["Mbar"], sto["A"], sto["W"], sto["DD"], comp.bits)
+        cost, fixed, budget, _, _ = oa.layer_costs(comp.bits, d, 1, Hs, keep, 4, Hs - 32)
+        oa.allocate(Dt, cost, fixed, budget, 4)
+        c2 = time.perf_counter()
+        t_layer = ((c1 - c0) * (H / Hs) ** 2 + (c2 - c1) * (H / Hs)) * Hkv
+        res["cpu_baseline"] = {"value": t_layer * 1e3, "unit": "ms", "cores": _threads(), "kind": "port",
+                               "sample": f"one KV head at an {Hs}-token context ({c1 - c0:.1f} s coverage, "
+                                         f"{c2 - c1:.1f} s distortion table + allocation), scaled to the layer: "
+                                         f"coverage x (H/{Hs})^2, the rest x H/{Hs}, x {Hkv} heads; numpy float64"}
+    return res
+
+
 WORKLOADS = {"c2": lambda a: run_kivi(a, "c2"), "c1": lambda a: run_kivi(a, "c1"), "c3": run_c3, "c4": run_c4,
              "c5": run_c5, "strata": run_strata, "append": run_append, "quant": run_quant, "quasar": run_quasar,
-             "micro": run_micro, "alloc": run_alloc, "snapkv": run_snapkv}
+             "micro": run_micro, "alloc": run_alloc, "snapkv": run_snapkv, "compress": run_compress}
 
 
 def main() -> int:

@@ -18,6 +18,7 @@ from .strata_state import StrataState, strata_pack, strata_tier_kernel
 from .quasar import QuasarState, stage_codebooks
 from .alloc import AllocWorkspace, allocate_layer, layer_costs, strata_allocate, strata_distortion
 from .coverage import coverage_groups, coverage_plan, coverage_stats
+from .strata_compress import StrataCompressor, rotation_matrix
 
 __all__ = [
     "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes", "pack_rows", "unpack_rows",
@@ -29,4 +30,5 @@ __all__ = [
     "dct_workspace_floats", "MixedKIVICache", "c3_widths", "mixed_decode", "mixed_workspace_floats", "offset_table",
     "StrataState", "strata_pack", "strata_tier_kernel", "QuasarState", "stage_codebooks", "payload_bytes", "AllocWorkspace", "allocate_layer", "layer_costs",
     "strata_allocate", "strata_distortion", "coverage_groups", "coverage_plan", "coverage_stats",
+    "StrataCompressor", "rotation_matrix",
 ]
