@@ -126,15 +126,27 @@ int kvq_vmeta_tile(const uint16_t* lo, const uint16_t* scale, int64_t BH, int64_
  *    decode-time form of SnapKV's scores (STRATA_KV.py:932-954: mean over the query heads of a
  *    KV group and over queries, with score_weight = 1 / (rep * Tq * steps)).  The softmax runs over
  *    packed and visible exact rows, as the decode's.
+ *    With a workspace of at least kvq_kivi_score_workspace(...) floats, a scored step's split
+ *    kernel also spills its logits (fp32, into the workspace after the partials) and the scores
+ *    come from them in one light pass; with kvq_kivi_decode_workspace(...) floats the score pass
+ *    reads the keys again.  Both give the same scores bit for bit.
  * phases (bit mask): 1 = split kernel (partials of the packed splits and the exact rows into the
- *    workspace); 2 = merge kernel (log-sum-exp merge, output write, and each row's global max/sum
- *    into the workspace); 4 = score pass (needs scores; reads the row statistics of a merge of
- *    the same call or an earlier one with the same args).  3 = decode, 7 = decode + scores.
+ *    workspace; with scores and a score workspace, the logits too); 2 = merge kernel (log-sum-exp
+ *    merge, output write, and each row's global max/sum into the workspace); 4 = score pass (needs
+ *    scores; reads the row statistics of a merge of the same call or an earlier one with the same
+ *    args, and with a score workspace the logits of that call's phase 1).  3 = decode, 7 = decode
+ *    + scores.
  * Requires d == 128, 4-bit codes, group_k % 32 == 0, group_v in {32, 64, 128}.
  * ---------------------------------------------------------------------------------------- */
 int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
                                   int64_t n_q, int64_t n_exact, int group_k, int group_v,
                                   int64_t split_tokens);
+/* Workspace floats of a scored step that spills its logits: kvq_kivi_decode_workspace's, rounded up
+ * to 4, plus 32 * R floats per 32-token chunk and (b, h).  No reference counterpart of its own:
+ * the scores it serves replace snapkv_scores (STRATA_KV.py:932-954) at decode time. */
+int64_t kvq_kivi_score_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
+                                 int64_t n_q, int64_t n_exact, int group_k, int group_v,
+                                 int64_t split_tokens);
 int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
                     int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling,
                     const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_sc,

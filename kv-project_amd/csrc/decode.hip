@@ -103,6 +103,8 @@ struct DecodeParams {
   float* scores;                      // score pass: (BH, scores_bh) accumulated probabilities
   int64_t scores_bh;
   float score_weight;
+  float* spill;                       // scored step: the split's logits (BH, spill_bh), or null
+  int64_t spill_bh;
   float* ws_o;
   int n_exact_wg, n_split, split_tokens, S1;
   int fused_per;                      // exact rows each packed split attends itself (0: none)
@@ -289,9 +291,11 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
 
 // ---------------------------------------------------------------------------------------------
 // packed split: 4 wavefronts, each streaming its quarter of the split in 32-token chunks
-// SCORE = false: flash-decoding partials of this split.  SCORE = true: the score pass of the
-// eviction path -- the same logits, normalised by the row's global (max, sum) from the merge,
-// summed over the rows of the KV head and accumulated into the scores row (no value work).
+// MODE 0: flash-decoding partials of this split.  MODE 1: the score pass of the eviction path --
+// the same logits, normalised by the row's global (max, sum) from the merge, summed over the rows
+// of the KV head and accumulated into the scores row (no value work).  MODE 2: the partials, and
+// every logit of the split spilled (chunk-local layout, see spill_index) for score_from_logits,
+// which then needs neither the keys nor their metadata again.
 // LDS of a packed block (floats): query rows + per-wavefront operand scratch, reused by the
 // wavefront partials of the epilogue; the fused exact-row region follows it.
 template <int R>
@@ -307,7 +311,7 @@ constexpr int fused_lds_floats() {
   return 2 * kFusedExact * kD * esz / 4 + R * kFusedExact + R + 2 * R;   // keys, values, logits, masks, stats
 }
 
-template <int R, int GV, int DT, bool SCORE>
+template <int R, int GV, int DT, int MODE>
 __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* smem) {
   // fp32 output: p * sv enters the PV product as hi + lo fp16 parts (two column variants per
   // group); 16-bit outputs take the single fp16 rounding (relative error 2^-12 per term, far
@@ -335,6 +339,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   float* const estat = reinterpret_cast<float*>(emask + R);                   // row max [R], sum [R]
   float* const eo = reinterpret_cast<float*>(ek4);                            // [R][kD] value sums
   int fe0 = 0, fne = 0;
+  constexpr bool SCORE = MODE == 1;
   if constexpr (!SCORE) {
     if (p.fused_per > 0) {
       fe0 = min(sidx * p.fused_per, p.n_exact);
@@ -521,14 +526,16 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
       for (int r = 0; r < R; ++r) {
         const float qa = qs[r][c0], qb = qs[r][c1];
         const float qak = qa * kinv, qbk = qb * kinv;
+        // hi part: the rounded product; lo part: the product's exact residual (one fma), so the
+        // split is the same in every instantiation whatever the optimiser shares between them
         const _Float16 h0 = static_cast<_Float16>(qak * static_cast<float>(sc0));
         const _Float16 h1 = static_cast<_Float16>(qbk * static_cast<float>(sc1));
-        const _Float16 e0 = static_cast<_Float16>(qak * static_cast<float>(sc0) - static_cast<float>(h0));
-        const _Float16 e1 = static_cast<_Float16>(qbk * static_cast<float>(sc1) - static_cast<float>(h1));
+        const _Float16 e0 = static_cast<_Float16>(__builtin_fmaf(qak, static_cast<float>(sc0), -static_cast<float>(h0)));
+        const _Float16 e1 = static_cast<_Float16>(__builtin_fmaf(qbk, static_cast<float>(sc1), -static_cast<float>(h1)));
         bq[(2 * r) * kBqStride + l] = pack_h2(h0, h1);
         bq[(2 * r + 1) * kBqStride + l] = pack_h2(e0, e1);
         // logit bias q.lo of this key group (added through the virtual k-step)
-        float P = qa * static_cast<float>(lo0) + qb * static_cast<float>(lo1);
+        float P = __builtin_fmaf(qa, static_cast<float>(lo0), __fmul_rn(qb, static_cast<float>(lo1)));
         P += dpp<kQuadSwap1>(P);
         P += dpp<kQuadSwap2>(P);
         if (ck == 0) {
@@ -560,7 +567,20 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
       for (int j = 0; j < 8; ++j)
         if (cb + 16 * (j >> 2) + 4 * g + (j & 3) >= t1) s[j] = -INFINITY;
     }
+    if constexpr (MODE == 2) {
+      // logits (log2 units) of this chunk: lane (g, n < R) writes its 8 tokens of row n as two
+      // 16-byte stores, [chunk][g][row][j], token cb + 16 (j >> 2) + 4 g + (j & 3)
+      if (n < R) {
+        float4* sp = reinterpret_cast<float4*>(p.spill + static_cast<int64_t>(bh) * p.spill_bh +
+                                               (static_cast<int64_t>(cb / 32) * 4 * R + g * R + n) * 8);
+        sp[0] = make_float4(s[0] * kTwo20, s[1] * kTwo20, s[2] * kTwo20, s[3] * kTwo20);
+        sp[1] = make_float4(s[4] * kTwo20, s[5] * kTwo20, s[6] * kTwo20, s[7] * kTwo20);
+      }
+    }
     if constexpr (SCORE) {
+      // every product rounded before the cross-lane sums (no contraction into the row pairs' adds,
+      // which would round the lanes of a pair differently); score_from_logits computes the same
+#pragma clang fp contract(off)
       // probability of each (row, token) under the row's global softmax, summed over the rows
       // of this KV head (lanes n = 0 .. R-1 hold rows 0 .. R-1 of one column variant)
       float x[8];
@@ -579,7 +599,7 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
 #pragma unroll
       for (int j = 1; j < 8; ++j) v = (n == j) ? x[j] : v;
       const int tok = cb + sc_tok;
-      if (n < 8 && tok < t1) score_row[tok] = __uint_as_float(c.sc) + p.score_weight * v;
+      if (n < 8 && tok < t1) score_row[tok] = __builtin_fmaf(p.score_weight, v, __uint_as_float(c.sc));
       return;
     }
     // ---- online softmax (base 2) with a lazy maximum: probabilities are taken against the running
@@ -782,7 +802,86 @@ void kivi_decode_split(DecodeParams p) {
   if (id < n_packed) {
     const int k = id / 8;
     const int bh = id % 8 + 8 * (k / p.n_split);
-    if (bh < p.BH) packed_block<R, GV, DT, false>(p, bh, k % p.n_split, smem);
+    if (bh < p.BH) packed_block<R, GV, DT, 0>(p, bh, k % p.n_split, smem);
+  }
+}
+
+// The split of a scored step: partials as kivi_decode_split, and its logits spilled.
+template <int R, int GV, int DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(split_waves<R, GV>())))
+void kivi_decode_split_spill(DecodeParams p) {
+  extern __shared__ float smem[];
+  const int bh_pad = (p.BH + 7) / 8 * 8;
+  const int id = blockIdx.x;
+  if (id < p.n_split * bh_pad) {
+    const int k = id / 8;
+    const int bh = id % 8 + 8 * (k / p.n_split);
+    if (bh < p.BH) packed_block<R, GV, DT, 2>(p, bh, k % p.n_split, smem);
+  }
+}
+
+// Scores of a scored step from the spilled logits.  One thread per (chunk, lane group g) of one
+// (b, h): the 8 tokens 4g + 0..3 and 16 + 4g + 0..3 of the chunk (two runs of 4 in the scores row,
+// 16-byte loads and stores), their R rows' logits as 2R 16-byte loads.  p = sum over the rows r of
+// exp2(logit - M_r) / L_r in the score pass's order and roundings (rows paired as its quad swaps
+// pair them, every product rounded), score += weight * p.  The keys are not read again.
+template <int R>
+__global__ __launch_bounds__(256) void score_from_logits(DecodeParams p) {
+#pragma clang fp contract(off)
+  const int nc = (p.n_q + 31) / 32;
+  const int per_bh = (nc + 63) / 64;
+  const int bh = blockIdx.x / per_bh;
+  const int c = (blockIdx.x % per_bh) * 64 + threadIdx.x / 4;
+  const int g = threadIdx.x % 4;
+  if (bh >= p.BH || c >= nc) return;
+  float M[R], IL[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t ri = (static_cast<int64_t>(bh) * R + r) * 2;
+    M[r] = r < p.R_real ? p.row_ml[ri] : 0.0f;
+    IL[r] = r < p.R_real ? 1.0f / p.row_ml[ri + 1] : 0.0f;
+  }
+  const float4* lg = reinterpret_cast<const float4*>(p.spill + static_cast<int64_t>(bh) * p.spill_bh +
+                                                     (static_cast<int64_t>(c) * 4 * R + g * R) * 8);
+  float4 L[R][2];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    L[r][0] = lg[2 * r];
+    L[r][1] = lg[2 * r + 1];
+  }
+  float* row = p.scores + static_cast<int64_t>(bh) * p.scores_bh + c * 32 + 4 * g;
+  const int left = p.n_q - (c * 32 + 4 * g);             // tokens of this thread's first run left in the row
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {                          // run h: tokens 16 h + 4 g + 0..3 = slots 4 h .. 4 h + 3
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float4 q = L[r][h];
+        const float lgt = i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
+        x[r] = __builtin_amdgcn_exp2f(lgt - M[r]) * IL[r];
+      }
+      if constexpr (R == 1) v[i] = x[0];
+      else if constexpr (R == 2) v[i] = x[0] + x[1];
+      else if constexpr (R == 4) v[i] = (x[0] + x[1]) + (x[2] + x[3]);
+      else v[i] = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+    }
+    float* sc = row + 16 * h;
+    const int n = left - 16 * h;                         // valid tokens of this run
+    if (n >= 4 && p.scores_bh % 4 == 0 && reinterpret_cast<uintptr_t>(p.scores) % 16 == 0) {
+      float4 o = *reinterpret_cast<const float4*>(sc);
+      o.x = __builtin_fmaf(p.score_weight, v[0], o.x);
+      o.y = __builtin_fmaf(p.score_weight, v[1], o.y);
+      o.z = __builtin_fmaf(p.score_weight, v[2], o.z);
+      o.w = __builtin_fmaf(p.score_weight, v[3], o.w);
+      *reinterpret_cast<float4*>(sc) = o;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i < n) sc[i] = __builtin_fmaf(p.score_weight, v[i], sc[i]);
+    }
   }
 }
 
@@ -803,7 +902,7 @@ void kivi_score_split(DecodeParams p) {
   extern __shared__ float smem[];
   const int k = blockIdx.x / 8;
   const int bh = blockIdx.x % 8 + 8 * (k / p.n_split);
-  if (bh < p.BH) packed_block<R, GV, DT, true>(p, bh, k % p.n_split, smem);
+  if (bh < p.BH) packed_block<R, GV, DT, 1>(p, bh, k % p.n_split, smem);
 }
 
 template <int R, int GV, int DT>
@@ -813,8 +912,12 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
   const size_t fused_smem = p.fused_per > 0 ? fused_lds_floats<R, DT>() * sizeof(float) : 0;
   const int bh_pad = (p.BH + 7) / 8 * 8;
   if ((phases & 1) && p.n_split > 0) {
-    hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), dim3(static_cast<unsigned>(p.n_split) * bh_pad),
-                       dim3(kThreads), packed_smem + fused_smem, stream, p);
+    if (p.spill != nullptr)
+      hipLaunchKernelGGL((kivi_decode_split_spill<R, GV, DT>), dim3(static_cast<unsigned>(p.n_split) * bh_pad),
+                         dim3(kThreads), packed_smem + fused_smem, stream, p);
+    else
+      hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), dim3(static_cast<unsigned>(p.n_split) * bh_pad),
+                         dim3(kThreads), packed_smem + fused_smem, stream, p);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(split)");
   }
   if ((phases & 1) && p.n_exact_wg > 0) {
@@ -833,7 +936,11 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
     const int rc = launch_merge_rows(ma, R, p.BH, DT, stream);
     if (rc != KVQ_OK) return rc;
   }
-  if ((phases & 4) && p.scores != nullptr && p.n_split > 0) {
+  if ((phases & 4) && p.scores != nullptr && p.n_split > 0 && p.spill != nullptr) {
+    const int per_bh = ((p.n_q + 31) / 32 + 63) / 64;
+    hipLaunchKernelGGL((score_from_logits<R>), dim3(static_cast<unsigned>(per_bh) * p.BH), dim3(256), 0, stream, p);
+    KVQ_LAUNCH_CHECK("kvq_kivi_decode(score)");
+  } else if ((phases & 4) && p.scores != nullptr && p.n_split > 0) {
     // the score pass writes no partials, so its split count is its own: its registers allow
     // twice the decode's resident blocks, so twice the splits (at least one chunk per wavefront)
     DecodeParams ps = p;
@@ -968,6 +1075,18 @@ extern "C" int64_t kvq_kivi_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv,
   return B * Hkv * (static_cast<int64_t>(sp.S1) * sp.R * (kD + 2) + 2 * sp.R);
 }
 
+// A scored step's workspace: the decode's, then its logits (32 R floats per 32-token chunk and
+// (b, h)).  Given at least this much, a scored step spills its logits and scores them without
+// reading the keys again; given only kvq_kivi_decode_workspace's floats, it runs the score pass.
+extern "C" int64_t kvq_kivi_score_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
+                                            int64_t n_q, int64_t n_exact, int group_k, int group_v,
+                                            int64_t split_tokens) {
+  const int64_t base = kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, d, n_q, n_exact, group_k, group_v, split_tokens);
+  if (base < 0) return base;
+  const int R = pow2_rows((Hq / Hkv) * Tq);
+  return (base + 3) / 4 * 4 + B * Hkv * ((n_q + 31) / 32) * 32 * R;    // logits 16-byte aligned
+}
+
 extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
                                int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
                                float scaling, const uint8_t* kc, const uint16_t* k_lo,
@@ -1024,6 +1143,13 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   p.scores = scores;
   p.scores_bh = scores_bh;
   p.score_weight = score_weight;
+  // a scored step with room for its logits after the decode's workspace spills them
+  const int64_t spill_bh = ((n_q + 31) / 32) * 32 * sp.R;
+  const int64_t spill_off = (need + 3) / 4 * 4;
+  if (scores != nullptr && n_q > 0 && workspace_floats >= spill_off + B * Hkv * spill_bh) {
+    p.spill = workspace + spill_off;
+    p.spill_bh = spill_bh;
+  }
   p.BH = static_cast<int>(B * Hkv);
   p.n_exact_wg = sp.n_exact_wg; p.n_split = sp.n_split; p.split_tokens = sp.split_tokens; p.S1 = sp.S1;
   p.fused_per = sp.fused_per;

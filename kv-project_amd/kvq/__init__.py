@@ -7,7 +7,7 @@ op requires GPU tensors and raises ``KVQError`` when the library is missing.
 from ._lib import KVQError, load as load_library
 from .kivi import (kivi_quant, kivi_quant_stored, pack_codes, pack_rows, unpack_codes, unpack_rows, v_tile,
                    v_untile, vmeta_tile)
-from .decode import PackedKIVICache, kivi_decode, workspace_floats
+from .decode import PackedKIVICache, kivi_decode, score_workspace_floats, workspace_floats
 from .state import DecodeCtl, KIVIState, Router, payload_bytes, register, routed, router_attention
 from .evict import gather_dequant, retained_cache, snapkv_scores, topk_retain
 from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strata_center_rotate, strata_decode,
@@ -22,7 +22,7 @@ from .strata_compress import StrataCompressor, rotation_matrix
 
 __all__ = [
     "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes", "pack_rows", "unpack_rows",
-    "v_tile", "v_untile", "vmeta_tile", "PackedKIVICache", "kivi_decode", "workspace_floats",
+    "v_tile", "v_untile", "vmeta_tile", "PackedKIVICache", "kivi_decode", "workspace_floats", "score_workspace_floats",
     "DecodeCtl", "KIVIState", "Router", "register", "routed", "router_attention",
     "gather_dequant", "retained_cache", "snapkv_scores", "topk_retain", "pack_planar", "unpack_planar", "rotation_signs",
     "uniform_step", "strata_center_rotate", "strata_quantize", "strata_v_tile", "StrataCache", "StrataTier",

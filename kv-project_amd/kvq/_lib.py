@@ -35,6 +35,7 @@ SIGNATURES = {
     "kvq_v_untile": (i32, [vp, i64, i64, i64, i64, vp, i64, vp]),
     "kvq_vmeta_tile": (i32, [vp, vp, i64, i64, i64, i64, i64, vp, vp]),
     "kvq_kivi_decode_workspace": (i64, [i64, i64, i64, i64, i64, i64, i64, i32, i32, i64]),
+    "kvq_kivi_score_workspace": (i64, [i64, i64, i64, i64, i64, i64, i64, i32, i32, i64]),
     "kvq_kivi_decode": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32,
                               vp, vp, vp, vp, vp, i64, i64, i32, i32, vp, vp, i32, i64, i64,
                               vp, vp, vp, i32, vp, i64, vp, i64, f32, i64, i32, vp]),

@@ -188,6 +188,16 @@ def workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_q: int, n_exa
     return n
 
 
+def score_workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_q: int, n_exact: int,
+                           group_k: int, group_v: int, split_tokens: int = 0) -> int:
+    """Workspace floats of a scored step that spills its logits (kvq_kivi_score_workspace): the
+    scores then come from the logits without a second pass over the keys."""
+    n = _lib.load().kvq_kivi_score_workspace(B, Hq, Hkv, Tq, d, n_q, n_exact, group_k, group_v, split_tokens)
+    if n < 0:
+        raise _lib.KVQError("kvq_kivi_score_workspace rejected the shape")
+    return n
+
+
 @torch.no_grad()
 def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
                 q_pos: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
@@ -207,7 +217,9 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
 
     ``scores`` (B, Hkv, >= n_q) float32 on the GPU: the step also adds ``score_weight`` times the
     probability mass each packed token received from the query heads of its KV group (the
-    decode-time accumulation of the eviction path).
+    decode-time accumulation of the eviction path).  With a workspace of score_workspace_floats
+    (the default here when scores are given) the split kernel spills its logits and the scores
+    come from them; a workspace of workspace_floats makes the score pass read the keys again.
 
     ``static_scratch``: run through kvq_kivi_decode_noalloc, which keeps the split partials in the
     library's static per-GPU scratch instead of a workspace (no device allocation in the call;
@@ -234,7 +246,8 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
     if static_scratch and workspace is not None:
         raise ValueError("static_scratch takes no workspace")
     if workspace is None and not static_scratch:   # a caller's workspace is size-checked by the library
-        need = workspace_floats(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, cache.group_v,
+        size = workspace_floats if scores is None else score_workspace_floats
+        need = size(B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, cache.group_k, cache.group_v,
                                 split_tokens)
         workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)
     if phases is None:

@@ -106,6 +106,33 @@ def test_decode_score_accumulation(Hq, Hkv, Tq, dtype):
     np.testing.assert_allclose(got, want, rtol=rtol, atol=1e-9)
 
 
+@pytest.mark.parametrize("Hq,Hkv,Tq,T,dtype", [(8, 8, 1, 1200, torch.float32), (8, 4, 1, 1111, torch.float32),
+                                               (16, 4, 1, 2077, torch.bfloat16), (8, 2, 2, 1300, torch.bfloat16),
+                                               (16, 2, 1, 999, torch.bfloat16)])
+def test_scored_step_spill_equals_score_pass(Hq, Hkv, Tq, T, dtype):
+    """A scored step with a score workspace (the split spills its logits, score_from_logits sums them)
+    and with a plain workspace (the score pass reads the keys again): outputs and scores bit-equal
+    over three steps, R = 1, 2, 4, 8, packed lengths not a multiple of 32."""
+    import kvq
+    B, W, gk, gv, d, steps = 2, 40, 64, 64, 128, 3
+    cache, K, V, kh, vh, g = _packed(B, Hkv, T, W, gk, gv, seed=T + Hq, dtype=dtype)
+    n_q = T - W
+    args = (B, Hq, Hkv, Tq, d, cache.n_q, cache.n_exact, gk, gv)
+    ws_spill = torch.zeros((kvq.score_workspace_floats(*args),), dtype=torch.float32, device="cuda")
+    ws_plain = torch.zeros((kvq.workspace_floats(*args),), dtype=torch.float32, device="cuda")
+    assert ws_spill.numel() > ws_plain.numel()
+    sc_a = torch.zeros((B, Hkv, n_q), dtype=torch.float32, device="cuda")
+    sc_b = torch.zeros_like(sc_a)
+    w = 1.0 / ((Hq // Hkv) * Tq * steps)
+    for _ in range(steps):
+        q = torch.randn((B, Hq, Tq, d), generator=g).to(dtype).cuda()
+        oa = kvq.kivi_decode(q, d ** -0.5, cache, workspace=ws_spill, scores=sc_a, score_weight=w)
+        ob = kvq.kivi_decode(q, d ** -0.5, cache, workspace=ws_plain, scores=sc_b, score_weight=w)
+        assert torch.equal(oa, ob)
+    assert torch.equal(sc_a, sc_b)
+    assert float(sc_a.sum()) > 0
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_gather_dequant_bit_exact(dtype):
     """Retained rows equal kivi_quant's xhat (fp32, then rounded once to the output type); an index
