@@ -11,12 +11,17 @@
 // applied per channel / per channel group).
 //
 // Work decomposition.  One launch of 256-thread blocks (4 wavefronts), XCD-aware over (b, h):
-//   packed split s of (b, h): tokens [s*ST, (s+1)*ST), one contiguous quarter per wavefront;
-//                             every wavefront streams 32-token chunks.
-//   exact window: up to kFusedExact rows per packed split are attended by the packed blocks
-//                 themselves (fp32 VALU, staged in LDS with the query rows); longer windows of
-//                 up to kExactInMerge rows by the merge; longer still by exact-row blocks
-//                 (streaming, about one round of them) dispatched after the packed blocks.
+//   packed split s of (b, h): a contiguous share of the tokens (equal, or weighted by the
+//                             block's dispatch class when the plan is one full round), one
+//                             contiguous quarter of it per wavefront; every wavefront streams
+//                             32-token chunks.
+//   exact window: with a one-round class plan, exact-row blocks of the same launch dispatched
+//                 after the packed blocks (they run on the slots the first class leaves free);
+//                 otherwise up to kFusedExact rows per packed split are attended by the packed
+//                 blocks themselves (fp32 VALU, staged in LDS with the query rows, after the
+//                 stream), longer windows of up to kExactInMerge rows by the merge, longer still
+//                 by exact-row blocks (streaming, about one round of them) of a launch of their
+//                 own after the packed blocks.
 // Each block writes one flash-decoding partial (m, l, acc) per row (base-2 logits); a second
 // kernel merges the partials exactly (log-sum-exp) and writes the output.
 //
@@ -66,6 +71,11 @@ namespace {
 #ifndef KVQ_LOAD_AUX
 #define KVQ_LOAD_AUX 2
 #endif
+//   KVQ_CLASSES     1: plans that are one full round of packed blocks map them class-major and
+//                   size the splits by dispatch class (see class_weight)
+#ifndef KVQ_CLASSES
+#define KVQ_CLASSES 1
+#endif
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kD = 128;            // head_dim supported by the matrix-core path
@@ -107,6 +117,8 @@ struct DecodeParams {
   int64_t spill_bh;
   float* ws_o;
   int n_exact_wg, n_split, split_tokens, S1;
+  int split_classes;                  // > 0: class-major split mapping and class-weighted splits
+  int exact_inline;                   // exact-row blocks dispatched after the packed blocks of the split
   int fused_per;                      // exact rows each packed split attends itself (0: none)
   int exact_rows;                     // rows of each exact-row block
   int BH;
@@ -311,6 +323,43 @@ constexpr int fused_lds_floats() {
   return 2 * kFusedExact * kD * esz / 4 + R * kFusedExact + R + 2 * R;   // keys, values, logits, masks, stats
 }
 
+// Dispatch classes.  A launch that is one full round of packed blocks fills every CU with
+// `classes` blocks (one wavefront of each per SIMD), and each SIMD's arbiter issues for its
+// oldest ready wavefront first: blocks dispatched in the first pass over the CUs progress
+// fastest, those of the last pass slowest, and with equal splits the last class would stream
+// alone at the end with too few loads in flight.  Such a plan maps blocks class-major (every
+// (b, h) has n_split / classes splits in each class) and sizes each split by its class's weight,
+// the rate the classes progress at when they share a CU (fitted on the 8B-shape layer from the
+// classes' measured stream times: 141 : 98 : 68; the youngest class still finishes last, since
+// it issues only when the older ones wait), so the classes finish close together.  Which tokens
+// each wavefront sums is fixed by the plan: results stay deterministic.
+constexpr int kCUsPerXcd = 32;
+__device__ __forceinline__ int class_weight(int c) { return c == 0 ? 141 : c == 1 ? 98 : 68; }
+// sum of the weights of splits [0, s) of a (b, h)
+__device__ __forceinline__ int64_t split_weight_before(const DecodeParams& p, int s) {
+  if (p.split_classes <= 0) return s;
+  const int q = p.n_split / p.split_classes;
+  const int c = s / q;
+  int64_t w = 0;
+  for (int k = 0; k < c; ++k) w += q * class_weight(k);
+  return w + static_cast<int64_t>(s % q) * class_weight(c);
+}
+// (b, h) and split of packed block `id`: round-robin over the 8 XCDs by linear id, so every split
+// of one (b, h) is on one XCD (its query rows and key metadata are read through one L2); within
+// an XCD class-major when the plan has classes
+__device__ __forceinline__ void packed_block_of(const DecodeParams& p, int id, int n_split, int* bh, int* sidx) {
+  const int k = id / 8;
+  if (p.split_classes > 0) {
+    const int q = n_split / p.split_classes;
+    const int cls = k / kCUsPerXcd, slot = k % kCUsPerXcd;
+    *bh = id % 8 + 8 * (slot / q);
+    *sidx = cls * q + slot % q;
+  } else {
+    *bh = id % 8 + 8 * (k / n_split);
+    *sidx = k % n_split;
+  }
+}
+
 template <int R, int GV, int DT, int MODE>
 __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* smem) {
   // fp32 output: p * sv enters the PV product as hi + lo fp16 parts (two column variants per
@@ -346,43 +395,6 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
       fne = min(p.fused_per, p.n_exact - fe0);
     }
   }
-  u32x4 ekr[kExU4], evr[kExU4];
-  if (fne > 0) {
-    const int64_t row0 = static_cast<int64_t>(bh) * p.cap_e + fe0;
-    const u32x4* gk = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.k_exact) + row0 * kD * kEsz);
-    const u32x4* gv = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.v_exact) + row0 * kD * kEsz);
-#pragma unroll
-    for (int u = 0; u < kExU4; ++u) {
-      const int w = threadIdx.x + kThreads * u;
-      if (w < fne * kRowU4) {
-        ekr[u] = gk[w];
-        evr[u] = gv[w];
-      }
-    }
-  }
-  load_q_rows<R, DT>(p, b, h, qs);
-  if (fne > 0) {
-#pragma unroll
-    for (int u = 0; u < kExU4; ++u) {
-      const int w = threadIdx.x + kThreads * u;
-      if (w < fne * kRowU4) {
-        ek4[w] = ekr[u];
-        ev4[w] = evr[u];
-      }
-    }
-    if (threadIdx.x < 64) {
-      const int i = threadIdx.x;
-      const bool masked = p.exact_pos != nullptr && p.q_pos != nullptr;
-      const int64_t ep = (masked && i < fne) ? p.exact_pos[fe0 + i] : 0;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const bool vis = i < fne && (!masked || ep <= p.q_pos[r % p.Tq]);
-        const uint64_t bal = __ballot(vis);
-        if (i == 0) emask[r] = static_cast<uint32_t>(bal);
-      }
-    }
-  }
-  __syncthreads();
 
   // wave index made explicitly uniform: every token offset derived from it lives in SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
@@ -403,14 +415,15 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
   uint32_t* bq = bq_all + wave * 2 * R * kBqStride;
   uint32_t* bv = bv_all + wave * R * 16;
 
-  // wavefront w = sidx * 4 + wave of this (b, h) takes chunks [w * NC / NW, (w + 1) * NC / NW) of
-  // the NC 32-token chunks (balanced to one chunk; a range may start inside a key group)
+  // wavefront `wave` of split sidx takes a quarter of the split's share of the NC 32-token chunks
+  // (a range may start inside a key group)
   const int G = p.group_k;
   const int NC = (p.n_q + 31) / 32;
-  const int NW = p.n_split * kWaves;
-  const int w_all = sidx * kWaves + wave;
-  const int t0 = 32 * static_cast<int>(static_cast<int64_t>(w_all) * NC / NW);
-  const int t1 = min(32 * static_cast<int>(static_cast<int64_t>(w_all + 1) * NC / NW), p.n_q);
+  const int64_t cwt = split_weight_before(p, p.n_split);
+  const int64_t sc0 = NC * split_weight_before(p, sidx) / cwt;       // the split's chunks [sc0, sc1)
+  const int64_t sc1 = NC * split_weight_before(p, sidx + 1) / cwt;
+  const int t0 = 32 * static_cast<int>(sc0 + (sc1 - sc0) * wave / kWaves);
+  const int t1 = min(32 * static_cast<int>(sc0 + (sc1 - sc0) * (wave + 1) / kWaves), p.n_q);
   // start of this wavefront's last chunk: loads past it are clamped onto it (they then hit in
   // cache), so every load of the pipeline is unconditional and the wait before each chunk's
   // compute counts exactly the loads issued after that chunk's
@@ -667,9 +680,72 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
 
   // ---- software pipeline over chunks: two register buffers used in turn; the load of the next
   // chunk is always issued (clamped) before the current chunk is computed ----
+  u32x4 ekr[kExU4], evr[kExU4];
+  if (fne > 0) {
+    const int64_t row0 = static_cast<int64_t>(bh) * p.cap_e + fe0;
+    const u32x4* gk = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.k_exact) + row0 * kD * kEsz);
+    const u32x4* gv = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.v_exact) + row0 * kD * kEsz);
+#pragma unroll
+    for (int u = 0; u < kExU4; ++u) {
+      const int w = threadIdx.x + kThreads * u;
+      if (w < fne * kRowU4) {
+        ekr[u] = gk[w];
+        evr[u] = gv[w];
+      }
+    }
+  }
+  // the query rows (scaled) into registers, then the first chunk's loads, then the LDS stores:
+  // the staging waits for the query and window rows only
+  constexpr int kQPer = (R * kD + kThreads - 1) / kThreads;
+  float qv[kQPer];
+#pragma unroll
+  for (int e = 0; e < kQPer; ++e) {
+    const int idx = threadIdx.x + kThreads * e;
+    const int r = idx / kD, c = idx % kD;
+    qv[e] = (idx < R * kD && r < p.R_real) ? load_as_f32<DT>(p.q, q_offset(p, b, h, r) + c) * p.qscale : 0.0f;
+  }
   Chunk ca, cb_;
   if (t0 < t1) load_chunk(t0, ca);
-  // ---- fused exact rows, while the first chunk is in flight: logits of rows 16u + 4*wave + g
+#pragma unroll
+  for (int e = 0; e < kQPer; ++e) {
+    const int idx = threadIdx.x + kThreads * e;
+    if (idx < R * kD) qs[idx / kD][idx % kD] = qv[e];
+  }
+  if (fne > 0) {
+#pragma unroll
+    for (int u = 0; u < kExU4; ++u) {
+      const int w = threadIdx.x + kThreads * u;
+      if (w < fne * kRowU4) {
+        ek4[w] = ekr[u];
+        ev4[w] = evr[u];
+      }
+    }
+    if (threadIdx.x < 64) {
+      const int i = threadIdx.x;
+      const bool masked = p.exact_pos != nullptr && p.q_pos != nullptr;
+      const int64_t ep = (masked && i < fne) ? p.exact_pos[fe0 + i] : 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const bool vis = i < fne && (!masked || ep <= p.q_pos[r % p.Tq]);
+        const uint64_t bal = __ballot(vis);
+        if (i == 0) emask[r] = static_cast<uint32_t>(bal);
+      }
+    }
+  }
+  block_lds_barrier();                             // the first chunk's loads stay in flight
+  if (t0 < t1) {
+    for (int cb = t0;; cb += 64) {
+      load_chunk(cb + 32, cb_);
+      step(cb, ca);
+      if (cb + 32 >= t1) break;
+      load_chunk(cb + 64, ca);
+      step(cb + 32, cb_);
+      if (cb + 64 >= t1) break;
+    }
+  }
+
+  // ---- fused exact rows, after the stream (a block dispatched early does this while later
+  // blocks stream; one in the last class with its CU to itself): logits of rows 16u + 4*wave + g
   // (16 lanes per row, 8 channels per lane; rows past fne are computed, not stored), then each
   // row's maximum, sum and value sums, left in LDS for the epilogue ----
   if (fne > 0) {
@@ -688,17 +764,29 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
         if (n == 0 && i < fne) esl[r * kFusedExact + i] = ((emask[r] >> i) & 1u) ? d : -INFINITY;
       }
     }
-    __syncthreads();                               // logits complete; key rows no longer read
+    block_lds_barrier();                           // logits complete; key rows no longer read
     const void* ev_lds = ev4;
     for (int idx = threadIdx.x; idx < p.R_real * kD; idx += kThreads) {
       const int r = idx / kD, c = idx % kD;
+      // every logit of the row and every value of channel c read before any use (rows past fne
+      // hold stale data: masked by selects)
+      float sl[kFusedExact], vv[kFusedExact];
+#pragma unroll
+      for (int i = 0; i < kFusedExact; i += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(&esl[r * kFusedExact + i]);
+        sl[i] = x.x; sl[i + 1] = x.y; sl[i + 2] = x.z; sl[i + 3] = x.w;
+      }
+#pragma unroll
+      for (int i = 0; i < kFusedExact; ++i) vv[i] = load_as_f32<DT>(ev_lds, static_cast<int64_t>(i) * kD + c);
       float me = -INFINITY, le = 0.0f, oe = 0.0f;
-      for (int i = 0; i < fne; ++i) me = fmaxf(me, esl[r * kFusedExact + i]);
+#pragma unroll
+      for (int i = 0; i < kFusedExact; ++i) me = fmaxf(me, i < fne ? sl[i] : -INFINITY);
       if (me != -INFINITY) {
-        for (int i = 0; i < fne; ++i) {
-          const float pr = __builtin_amdgcn_exp2f(esl[r * kFusedExact + i] - me);
+#pragma unroll
+        for (int i = 0; i < kFusedExact; ++i) {
+          const float pr = i < fne ? __builtin_amdgcn_exp2f(sl[i] - me) : 0.0f;
           le += pr;
-          oe = __builtin_fmaf(pr, load_as_f32<DT>(ev_lds, static_cast<int64_t>(i) * kD + c), oe);
+          oe = __builtin_fmaf(pr, i < fne ? vv[i] : 0.0f, oe);
         }
       }
       eo[idx] = oe;
@@ -708,17 +796,6 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
       }
     }
   }
-  if (t0 < t1) {
-    for (int cb = t0;; cb += 64) {
-      load_chunk(cb + 32, cb_);
-      step(cb, ca);
-      if (cb + 32 >= t1) break;
-      load_chunk(cb + 64, ca);
-      step(cb + 32, cb_);
-      if (cb + 64 >= t1) break;
-    }
-  }
-
   if constexpr (SCORE) return;
   // ---- wavefront epilogue: row sums over lane groups, hi+lo columns, offset and zero terms ----
   const float l_run = xsum32(xsum16(la + 16.0f * lb));
@@ -781,6 +858,15 @@ __device__ void packed_block(const DecodeParams& p, int bh, int sidx, float* sme
 }
 
 
+// Exact-row block e of a split launch (dispatched after the packed blocks, so the blocks of the
+// window run on CU slots the first packed blocks to finish leave free): same XCD-aware mapping.
+template <int R, int DT>
+__device__ __forceinline__ void exact_block_of(const DecodeParams& p, int e, float* smem) {
+  const int k = e / 8;
+  const int bh = e % 8 + 8 * (k / p.n_exact_wg);
+  if (bh < p.BH && k / p.n_exact_wg < (p.BH + 7) / 8) exact_block<R, DT>(p, bh, k % p.n_exact_wg, smem);
+}
+
 // One block per (b, h, split).  Blocks are dispatched round-robin over the 8 XCDs by linear id,
 // so id -> (xcd = id % 8, k = id / 8) -> bh = xcd + 8*(k / S1), split = k % S1 keeps every
 // split of one (b, h) on one XCD (its query rows and key metadata are read through one L2).
@@ -800,9 +886,11 @@ void kivi_decode_split(DecodeParams p) {
   const int n_packed = p.n_split * bh_pad;
   const int id = blockIdx.x;
   if (id < n_packed) {
-    const int k = id / 8;
-    const int bh = id % 8 + 8 * (k / p.n_split);
-    if (bh < p.BH) packed_block<R, GV, DT, 0>(p, bh, k % p.n_split, smem);
+    int bh, sidx;
+    packed_block_of(p, id, p.n_split, &bh, &sidx);
+    if (bh < p.BH) packed_block<R, GV, DT, 0>(p, bh, sidx, smem);
+  } else {
+    exact_block_of<R, DT>(p, id - n_packed, smem);
   }
 }
 
@@ -814,9 +902,11 @@ void kivi_decode_split_spill(DecodeParams p) {
   const int bh_pad = (p.BH + 7) / 8 * 8;
   const int id = blockIdx.x;
   if (id < p.n_split * bh_pad) {
-    const int k = id / 8;
-    const int bh = id % 8 + 8 * (k / p.n_split);
-    if (bh < p.BH) packed_block<R, GV, DT, 2>(p, bh, k % p.n_split, smem);
+    int bh, sidx;
+    packed_block_of(p, id, p.n_split, &bh, &sidx);
+    if (bh < p.BH) packed_block<R, GV, DT, 2>(p, bh, sidx, smem);
+  } else {
+    exact_block_of<R, DT>(p, id - p.n_split * bh_pad, smem);
   }
 }
 
@@ -900,9 +990,9 @@ template <int R, int GV, int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(split_waves<R, GV>())))
 void kivi_score_split(DecodeParams p) {
   extern __shared__ float smem[];
-  const int k = blockIdx.x / 8;
-  const int bh = blockIdx.x % 8 + 8 * (k / p.n_split);
-  if (bh < p.BH) packed_block<R, GV, DT, 1>(p, bh, k % p.n_split, smem);
+  int bh, sidx;
+  packed_block_of(p, blockIdx.x, p.n_split, &bh, &sidx);
+  if (bh < p.BH) packed_block<R, GV, DT, 1>(p, bh, sidx, smem);
 }
 
 template <int R, int GV, int DT>
@@ -912,15 +1002,15 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
   const size_t fused_smem = p.fused_per > 0 ? fused_lds_floats<R, DT>() * sizeof(float) : 0;
   const int bh_pad = (p.BH + 7) / 8 * 8;
   if ((phases & 1) && p.n_split > 0) {
+    const unsigned blocks = static_cast<unsigned>(p.n_split + (p.exact_inline ? p.n_exact_wg : 0)) * bh_pad;
+    const size_t smem = std::max(packed_smem + fused_smem, p.exact_inline ? exact_smem : 0);
     if (p.spill != nullptr)
-      hipLaunchKernelGGL((kivi_decode_split_spill<R, GV, DT>), dim3(static_cast<unsigned>(p.n_split) * bh_pad),
-                         dim3(kThreads), packed_smem + fused_smem, stream, p);
+      hipLaunchKernelGGL((kivi_decode_split_spill<R, GV, DT>), dim3(blocks), dim3(kThreads), smem, stream, p);
     else
-      hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), dim3(static_cast<unsigned>(p.n_split) * bh_pad),
-                         dim3(kThreads), packed_smem + fused_smem, stream, p);
+      hipLaunchKernelGGL((kivi_decode_split<R, GV, DT>), dim3(blocks), dim3(kThreads), smem, stream, p);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(split)");
   }
-  if ((phases & 1) && p.n_exact_wg > 0) {
+  if ((phases & 1) && p.n_exact_wg > 0 && !p.exact_inline) {
     hipLaunchKernelGGL((kivi_decode_exact<R, DT>), dim3(static_cast<unsigned>(p.n_exact_wg) * bh_pad),
                        dim3(kThreads), exact_smem, stream, p);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(exact)");
@@ -946,6 +1036,7 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
     DecodeParams ps = p;
     const int nc = (p.n_q + 31) / 32;
     ps.n_split = std::max(1, std::min(KVQ_SCORE_SPLITS * p.n_split, (nc + kWaves - 1) / kWaves));
+    ps.split_classes = 0;
     hipLaunchKernelGGL((kivi_score_split<R, GV, DT>), dim3(static_cast<unsigned>(ps.n_split) * bh_pad),
                        dim3(kThreads), packed_smem, stream, ps);
     KVQ_LAUNCH_CHECK("kvq_kivi_decode(score)");
@@ -954,7 +1045,7 @@ int launch(DecodeParams& p, int phases, hipStream_t stream) {
 }
 
 struct SplitPlan {
-  int n_exact_wg, n_split, split_tokens, S1, R, fused_per, exact_rows;
+  int n_exact_wg, n_split, split_tokens, S1, R, fused_per, exact_rows, classes, exact_inline;
 };
 
 constexpr int kCUs = 256;          // MI355X compute units
@@ -997,13 +1088,26 @@ inline SplitPlan plan_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int6
   ns = std::min<int64_t>(ns, (nc + kWaves - 1) / kWaves);
   sp.n_split = static_cast<int>(ns);
   sp.split_tokens = ns > 0 ? static_cast<int>((n_q + ns - 1) / ns) : 0;
+  // class-weighted splits: the packed blocks are exactly one round of 3 per CU, every (b, h)
+  // with the same number of splits in each class
+  const int64_t bhn = B * Hkv;
+  sp.classes = (KVQ_CLASSES != 0 && resident_blocks == 3 && bhn % 8 == 0 && ns % 3 == 0 && (bhn / 8) * (ns / 3) == kCUs / 8) ? 3 : 0;
   // exact window: in the packed splits (at most kFusedExact rows each), else in the merge (at
   // most kExactInMerge rows), else in exact-row blocks
   const int64_t per = ns > 0 ? (n_exact + ns - 1) / ns : 0;
   sp.fused_per = (n_exact > 0 && ns > 0 && per <= kFusedExact) ? static_cast<int>(per) : 0;
   sp.exact_rows = 0;
-  sp.n_exact_wg = (n_exact == 0 || sp.fused_per > 0 || exact_in_merge(n_exact))
-                      ? 0 : plan_exact_blocks(B * Hkv, n_exact, &sp.exact_rows);
+  sp.exact_inline = 0;
+  if (sp.classes > 0 && n_exact > 0) {
+    // one full round of packed blocks: the window in exact-row blocks of the same launch,
+    // which fill the slots of the first blocks to finish while the last class still streams
+    sp.fused_per = 0;
+    sp.exact_inline = 1;
+    sp.n_exact_wg = plan_exact_blocks(B * Hkv, n_exact, &sp.exact_rows);
+  } else {
+    sp.n_exact_wg = (n_exact == 0 || sp.fused_per > 0 || exact_in_merge(n_exact))
+                        ? 0 : plan_exact_blocks(B * Hkv, n_exact, &sp.exact_rows);
+  }
   sp.S1 = sp.n_exact_wg + sp.n_split;
   return sp;
 }
@@ -1154,6 +1258,8 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   p.n_exact_wg = sp.n_exact_wg; p.n_split = sp.n_split; p.split_tokens = sp.split_tokens; p.S1 = sp.S1;
   p.fused_per = sp.fused_per;
   p.exact_rows = sp.exact_rows;
+  p.split_classes = sp.classes;
+  p.exact_inline = sp.exact_inline;
   p.out = out;
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define KVQ_GV(R_, DT_)                                                             \

@@ -46,14 +46,17 @@ def test_argument_validation_without_gpu():
 
 def test_split_plan_fills_one_round():
     """Automatic split (16x8 (b, h), 32640 packed + 128 exact tokens, 3 resident blocks per CU on
-    256 CUs): 6 packed splits per (b, h) = 768 blocks, one round.  Exact windows of at most 1024
-    rows are attended by the merge (no exact-row blocks, no partials); longer ones are blocks of 64
-    rows dispatched after the packed blocks.  The workspace holds S1 * rows * (d + 2) + 2 * rows
-    floats per (b, h), S1 = exact-row blocks + packed splits (partials, then each row's max and sum)."""
+    256 CUs): 6 packed splits per (b, h) = 768 blocks, one round, so the plan is class-major and the
+    128 window rows go to 2 exact-row blocks of 64 rows per (b, h) in the same launch.  Off that
+    one-round shape, exact windows of at most 1024 rows are attended by the merge (no exact-row
+    blocks, no partials); longer ones are blocks of 64 rows dispatched after the packed blocks.  The
+    workspace holds S1 * rows * (d + 2) + 2 * rows floats per (b, h), S1 = exact-row blocks + packed
+    splits (partials, then each row's max and sum)."""
     from kvq import _lib
     lib = _lib.load()
     BH, R, d = 16 * 8, 4, 128
-    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 0) == BH * (6 * R * (d + 2) + 2 * R)
+    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 0) == BH * (8 * R * (d + 2) + 2 * R)
+    assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 0, 64, 64, 0) == BH * (6 * R * (d + 2) + 2 * R)
     # explicit split size: ceil(n_q / split_tokens) splits
     assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 64, 3000) == BH * (11 * R * (d + 2) + 2 * R)
     assert lib.kvq_kivi_decode_workspace(16, 32, 8, 1, 128, 32640, 128, 64, 48, 0) == -1
