@@ -323,41 +323,19 @@ constexpr int fused_lds_floats() {
   return 2 * kFusedExact * kD * esz / 4 + R * kFusedExact + R + 2 * R;   // keys, values, logits, masks, stats
 }
 
-// Dispatch classes.  A launch that is one full round of packed blocks fills every CU with
-// `classes` blocks (one wavefront of each per SIMD), and each SIMD's arbiter issues for its
-// oldest ready wavefront first: blocks dispatched in the first pass over the CUs progress
-// fastest, those of the last pass slowest, and with equal splits the last class would stream
-// alone at the end with too few loads in flight.  Such a plan maps blocks class-major (every
-// (b, h) has n_split / classes splits in each class) and sizes each split by its class's weight,
-// the rate the classes progress at when they share a CU (fitted on the 8B-shape layer from the
-// classes' measured stream times: 141 : 98 : 68; the youngest class still finishes last, since
-// it issues only when the older ones wait), so the classes finish close together.  Which tokens
-// each wavefront sums is fixed by the plan: results stay deterministic.
-constexpr int kCUsPerXcd = 32;
-__device__ __forceinline__ int class_weight(int c) { return c == 0 ? 141 : c == 1 ? 98 : 68; }
-// sum of the weights of splits [0, s) of a (b, h)
+// Dispatch-class weights of the packed split (see class_block_of): fitted on the 8B-shape layer
+// from the classes' measured stream times (the youngest class still finishes last, since it
+// issues only when the older ones wait)
+#ifndef KVQ_CLASS_W
+#define KVQ_CLASS_W 141, 98, 68
+#endif
+constexpr int kClassW[3] = {KVQ_CLASS_W};
+constexpr int kClassW0 = kClassW[0], kClassW1 = kClassW[1], kClassW2 = kClassW[2];
 __device__ __forceinline__ int64_t split_weight_before(const DecodeParams& p, int s) {
-  if (p.split_classes <= 0) return s;
-  const int q = p.n_split / p.split_classes;
-  const int c = s / q;
-  int64_t w = 0;
-  for (int k = 0; k < c; ++k) w += q * class_weight(k);
-  return w + static_cast<int64_t>(s % q) * class_weight(c);
+  return class_weight_before(s, p.n_split, p.split_classes, kClassW0, kClassW1, kClassW2);
 }
-// (b, h) and split of packed block `id`: round-robin over the 8 XCDs by linear id, so every split
-// of one (b, h) is on one XCD (its query rows and key metadata are read through one L2); within
-// an XCD class-major when the plan has classes
 __device__ __forceinline__ void packed_block_of(const DecodeParams& p, int id, int n_split, int* bh, int* sidx) {
-  const int k = id / 8;
-  if (p.split_classes > 0) {
-    const int q = n_split / p.split_classes;
-    const int cls = k / kCUsPerXcd, slot = k % kCUsPerXcd;
-    *bh = id % 8 + 8 * (slot / q);
-    *sidx = cls * q + slot % q;
-  } else {
-    *bh = id % 8 + 8 * (k / n_split);
-    *sidx = k % n_split;
-  }
+  class_block_of(id, n_split, p.split_classes, bh, sidx);
 }
 
 template <int R, int GV, int DT, int MODE>
@@ -1091,7 +1069,7 @@ inline SplitPlan plan_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int6
   // class-weighted splits: the packed blocks are exactly one round of 3 per CU, every (b, h)
   // with the same number of splits in each class
   const int64_t bhn = B * Hkv;
-  sp.classes = (KVQ_CLASSES != 0 && resident_blocks == 3 && bhn % 8 == 0 && ns % 3 == 0 && (bhn / 8) * (ns / 3) == kCUs / 8) ? 3 : 0;
+  sp.classes = KVQ_CLASSES != 0 ? split_classes(bhn, ns, resident_blocks) : 0;
   // exact window: in the packed splits (at most kFusedExact rows each), else in the merge (at
   // most kExactInMerge rows), else in exact-row blocks
   const int64_t per = ns > 0 ? (n_exact + ns - 1) / ns : 0;

@@ -24,6 +24,22 @@
 #include "partials.hpp"
 #include "widths.hpp"
 
+// Build-time switches: KVQ_MIXED_CLASSES 1 lets a plan that is exactly one round of blocks be
+// class-major with splits sized by dispatch class, weights KVQ_MIXED_W0 : W1 : W2 (see
+// class_block_of); 0 keeps the plain mapping and equal splits.
+#ifndef KVQ_MIXED_CLASSES
+#define KVQ_MIXED_CLASSES 1
+#endif
+#ifndef KVQ_MIXED_W0
+#define KVQ_MIXED_W0 165
+#endif
+#ifndef KVQ_MIXED_W1
+#define KVQ_MIXED_W1 95
+#endif
+#ifndef KVQ_MIXED_W2
+#define KVQ_MIXED_W2 55
+#endif
+
 namespace kvq {
 namespace {
 
@@ -131,6 +147,7 @@ struct MixedParams {
   const uint8_t* buf;
   const int64_t* seg;               // (BH, 4): base unit, n8, n4, n2
   int n_split;
+  int split_classes;                // > 0: class-major blocks, splits sized by dispatch class
   float* ws_o;
   float* ws_m;
   float* ws_l;
@@ -421,10 +438,13 @@ __device__ void mixed_block(const MixedParams& p, int bh, int sidx, float* smem)
   const int n4 = static_cast<int>(p.seg[bh * 4 + 2]);
   const int n2 = static_cast<int>(p.seg[bh * 4 + 3]);
   const int64_t C = 9LL * n8 + 5LL * n4 + 3LL * n2;
-  const int NW = p.n_split * kMWaves;
-  const int w_all = sidx * kMWaves + wave;
-  const int i0 = mixed_first_block(C * w_all / NW, n8, n4, n2);
-  const int i1 = mixed_first_block(C * (w_all + 1) / NW, n8, n4, n2);
+  // the split's share of the (b, h)'s cost units (by its dispatch class's weight when the plan has
+  // classes), a quarter of it per wavefront
+  const int64_t cwt = class_weight_before(p.n_split, p.n_split, p.split_classes, KVQ_MIXED_W0, KVQ_MIXED_W1, KVQ_MIXED_W2);
+  const int64_t sc0 = C * class_weight_before(sidx, p.n_split, p.split_classes, KVQ_MIXED_W0, KVQ_MIXED_W1, KVQ_MIXED_W2) / cwt;
+  const int64_t sc1 = C * class_weight_before(sidx + 1, p.n_split, p.split_classes, KVQ_MIXED_W0, KVQ_MIXED_W1, KVQ_MIXED_W2) / cwt;
+  const int i0 = mixed_first_block(sc0 + (sc1 - sc0) * wave / kMWaves, n8, n4, n2);
+  const int i1 = mixed_first_block(sc0 + (sc1 - sc0) * (wave + 1) / kMWaves, n8, n4, n2);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.buf + base * kUnit, static_cast<uint32_t>(C * kUnit));
 
   MixedState<R, LO> st;
@@ -509,9 +529,9 @@ template <int R, int DT>
 __global__ __launch_bounds__(kMThreads) __attribute__((amdgpu_waves_per_eu(mixed_waves<R, DT>())))
 void mixed_split(MixedParams p) {
   extern __shared__ float smem[];
-  const int k = blockIdx.x / 8;
-  const int bh = blockIdx.x % 8 + 8 * (k / p.n_split);
-  if (bh < p.BH) mixed_block<R, DT>(p, bh, k % p.n_split, smem);
+  int bh, sidx;
+  class_block_of(blockIdx.x, p.n_split, p.split_classes, &bh, &sidx);
+  if (bh < p.BH) mixed_block<R, DT>(p, bh, sidx, smem);
 }
 
 
@@ -551,9 +571,18 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
 namespace {
 int64_t mixed_ws_parts(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t nb, int64_t n_exact, int64_t* ex_floats,
                        int* S) {
-  // resident blocks per CU = waves per SIMD of the variant (one wavefront of each block per SIMD)
+  // resident blocks per CU = waves per SIMD of the variant (one wavefront of each block per SIMD);
+  // a plan as fast as the best that is exactly one round of class-major blocks is preferred
   const int64_t Rr = kvq::pow2_rows((Hq / Hkv) * Tq);
-  *S = nb > 0 ? kvq::plan_block_splits(B * Hkv, nb, (Rr <= 4) ? 3 : 2, 4) : 0;
+  const int res = (Rr <= 4) ? 3 : 2;
+  *S = nb > 0 ? kvq::plan_block_splits(B * Hkv, nb, res, 4) : 0;
+  if (*S > 0 && KVQ_MIXED_CLASSES != 0 && (B * Hkv) % 8 == 0) {
+    const int64_t s_cls = 3LL * kvq::kCUsPerXcd * 8 / (B * Hkv);
+    const int64_t slots = 256LL * res;
+    auto cost = [&](int64_t sv) { return ((B * Hkv * sv + slots - 1) / slots) * ((nb + 4 * sv - 1) / (4 * sv) + 4); };
+    if (s_cls >= 1 && s_cls <= (nb + 3) / 4 && kvq::split_classes(B * Hkv, s_cls, res) > 0 && cost(s_cls) <= cost(*S))
+      *S = static_cast<int>(s_cls);
+  }
   *ex_floats = (n_exact > 0 && !kvq::exact_in_merge(n_exact))
                    ? kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, 128, 0, n_exact, 32, 32, 0) : 0;
   const int64_t R = kvq::pow2_rows((Hq / Hkv) * Tq);
@@ -618,6 +647,7 @@ extern "C" int kvq_mixed_decode(const void* q, int q_dtype, int64_t q_sb, int64_
   p.BH = (int)(B * Hkv);
   p.qscale = scaling * 1.4426950408889634f;
   p.buf = buf; p.seg = seg; p.n_split = S;
+  p.split_classes = KVQ_MIXED_CLASSES != 0 ? split_classes(B * Hkv, S, (pow2_rows(R_real) <= 4 && q_dtype != KVQ_F32) ? 3 : 2) : 0;
   float* tw = workspace + ex_floats;
   const int64_t trow = B * Hkv * static_cast<int64_t>(S) * R;
   p.ws_o = tw;

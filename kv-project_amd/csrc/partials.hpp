@@ -266,6 +266,46 @@ inline int plan_block_splits(int64_t BH, int64_t nb, int resident_per_cu, int64_
   return static_cast<int>(best);
 }
 
+// ---- dispatch classes of a one-round launch -------------------------------------------------
+// A launch whose blocks are exactly one round with `resident` blocks per CU (one wavefront of each
+// per SIMD) fills every CU in `resident` passes over the CUs, and each SIMD's arbiter issues for
+// its oldest ready wavefront first: blocks of the first pass progress fastest, those of the last
+// slowest, and with equal splits the last class streams alone at the end with too few loads in
+// flight.  Such a plan maps blocks class-major (every (b, h) has n_split / classes splits in each
+// class) and sizes each split by its class's weight, the rate the classes progress at when they
+// share a CU, so the classes finish close together.  Which tokens each wavefront handles is fixed
+// by the plan: results stay deterministic.
+constexpr int kCUsPerXcd = 32;
+// classes of a plan (0: plain mapping, equal splits): blocks go round robin over the 8 XCDs by
+// linear id, BH / 8 (b, h) per XCD, each with n_split splits
+inline int split_classes(int64_t BH, int64_t n_split, int resident) {
+  return (resident == 3 && BH % 8 == 0 && n_split % 3 == 0 && (BH / 8) * (n_split / 3) == kCUsPerXcd) ? 3 : 0;
+}
+// (b, h) and split of block `id`: XCD-aware (every split of one (b, h) on one XCD, its query rows
+// and metadata read through one L2), class-major within the XCD when the plan has classes
+__device__ __forceinline__ void class_block_of(int id, int n_split, int classes, int* bh, int* sidx) {
+  const int k = id / 8;
+  if (classes > 0) {
+    const int q = n_split / classes;
+    const int cls = k / kCUsPerXcd, slot = k % kCUsPerXcd;
+    *bh = id % 8 + 8 * (slot / q);
+    *sidx = cls * q + slot % q;
+  } else {
+    *bh = id % 8 + 8 * (k / n_split);
+    *sidx = k % n_split;
+  }
+}
+// sum of the weights of splits [0, s) of a (b, h): w0 / w1 / w2 per class, 1 each without classes
+__device__ __forceinline__ int64_t class_weight_before(int s, int n_split, int classes, int w0, int w1, int w2) {
+  if (classes <= 0) return s;
+  const int q = n_split / classes;
+  const int c = s / q;
+  const int w[3] = {w0, w1, w2};
+  int64_t acc = 0;
+  for (int k = 0; k < c; ++k) acc += static_cast<int64_t>(q) * w[k];
+  return acc + static_cast<int64_t>(s % q) * w[c];
+}
+
 inline int pow2_rows(int64_t r) {
   int R = 1;
   while (R < r) R <<= 1;
