@@ -18,6 +18,14 @@ for the functions whose exact floats or draws nothing but the reference itself f
                        embedded_quantize codes of seeded coefficients (1172-1183)
   coverage_groups.npz  coverage_groups(H, cfg) (STRATA_KV.py:1206-1222) for several H under the
                        default Config and the reference's test config (1964)
+  quasar_state.npz     one seeded fp32 layer (Hq 8, Hkv 2, d 128, H 700; keep 0.5: 458 coded
+                       tokens over 23 levels, rank 128) compressed by the
+                       reference's own QuasarMethod.compress_layer (QUASAR_KV.py:1628-1710) under
+                       its default Config, its stored code QuasarMethod.pack (1786-1808: every step's
+                       side / band / stage / n and packed code bytes, rho, T, mu at fp16, the level
+                       histogram), the exact rows of native_state (1830-1843), and the output of
+                       QuasarState.attend (1952-1977, the reference's PyTorch path) for one query
+                       token after one appended token
 
 The tests load these files; nothing on the GPU box reads the reference.
 """
@@ -87,6 +95,45 @@ def quasar_codebooks(S, Q) -> dict:
     return out
 
 
+def quasar_state(Q) -> dict:
+    import types
+    import torch
+    rng = np.random.default_rng(20260103)
+    Hq, Hkv, d, H, hidden = 8, 2, 128, 700, 256
+    cfg = Q.Config()
+    q = rng.standard_normal((1, Hq, H, d)).astype(np.float32) * 1.5
+    k = rng.standard_normal((1, Hkv, H, d)).astype(np.float32) * (np.abs(rng.standard_t(3, (1, Hkv, 1, d))) + 0.3)
+    v = rng.standard_normal((1, Hkv, H, d)).astype(np.float32)
+    k[:, :, 0] += 2.0 * q[0, ::Hq // Hkv].mean(1)[None]                 # a sink the queries lean on
+    hot = rng.permutation(H - 64)[:16] + 16                             # a few heavily read tokens
+    k[:, :, hot] += 1.5 * q[0, ::Hq // Hkv, -32:].mean(1)[None, :, None]
+    Wo = (rng.standard_normal((hidden, Hq * d)) / np.sqrt(Hq * d)).astype(np.float32)
+    runner = types.SimpleNamespace(d=d, Hq=Hq, layers=[types.SimpleNamespace(
+        self_attn=types.SimpleNamespace(o_proj=types.SimpleNamespace(weight=torch.from_numpy(Wo))))])
+    qm = Q.QuasarMethod(cfg, 0.5, "quasar", runner)
+    qt, kt, vt = torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v)
+    al = qm.compress_layer(0, qt, kt, vt, d ** -0.5, H)
+    al["packed"] = qm.pack(al)
+    al.pop("sides")
+    qm.alloc[0] = al
+    st = qm.native_state(0, kt, vt, 2, torch.float32)
+    p = st.p
+    kn = torch.from_numpy(rng.standard_normal((1, Hkv, 1, d)).astype(np.float32))
+    vn = torch.from_numpy(rng.standard_normal((1, Hkv, 1, d)).astype(np.float32))
+    qn = torch.from_numpy((rng.standard_normal((1, Hq, 1, d)) * 1.5).astype(np.float32))
+    st.append(kn, vn, torch.tensor([H]))
+    out = st.attend(qn, d ** -0.5, torch.tensor([H]))
+    res = {"stages": np.array(qm.stages, np.int64), "H": np.array(H, np.int64), "n_c": np.array(p["n_c"], np.int64),
+           "counts": p["counts"].numpy(), "Ke": st.K[:, :, :st.n0].numpy(), "Ve": st.V[:, :, :st.n0].numpy(),
+           "kn": kn.numpy(), "vn": vn.numpy(), "qn": qn.numpy(), "out": out.numpy(),
+           "step_meta": np.array([[x["side"], x["a"], x["b"], x["stage"], x["n"]] for x in p["steps"]], np.int64)}
+    for i, x in enumerate(p["steps"]):
+        res[f"codes_{i}"] = x["codes"].numpy()
+    for nm in ("rho_k", "rho_v", "T_k", "T_v", "mu_k", "mu_v"):
+        res[nm] = p[nm].to(torch.float16).numpy()
+    return res
+
+
 def coverage_groups(S) -> dict:
     from dataclasses import replace
     out = {}
@@ -112,7 +159,7 @@ def main() -> int:
     S = _load(ref, "STRATA_KV")
     Q = _load(ref, "QUASAR_KV")
     for name, data in (("strata_codec", strata_codec(S)), ("quasar_codebooks", quasar_codebooks(S, Q)),
-                       ("coverage_groups", coverage_groups(S))):
+                       ("coverage_groups", coverage_groups(S)), ("quasar_state", quasar_state(Q))):
         np.savez_compressed(HERE / f"{name}.npz", **data)
         print(f"wrote {name}.npz ({(HERE / f'{name}.npz').stat().st_size} bytes, {len(data)} arrays)")
     return 0

@@ -9,7 +9,11 @@ These pin what only the reference fixes exactly:
     oracle's FWHT order); codes and fp16 scales at 2, 4 and 8 bits bit-equal both on the
     reference's own Y and end to end from X;
   * lloyd_max_gaussian levels, b = 1..4 (STRATA_KV.py:1082-1098), the QUASAR stage codebooks
-    (QUASAR_KV.py:1143-1169) and embedded_quantize codes (1172-1183): bit-equal.
+    (QUASAR_KV.py:1143-1169) and embedded_quantize codes (1172-1183): bit-equal;
+  * a layer compressed and packed by the reference's own QuasarMethod (1628-1710, 1786-1808) and
+    decoded by its QuasarState.attend (1952-1977): the oracle's attend on that stored code
+    within 1e-5 of the output's scale (the reference computes in float32, the oracle in
+    float64), and the stored code's structure (embedded prefix order, byte widths).
 """
 from pathlib import Path
 
@@ -72,3 +76,34 @@ def test_lloyd_max_and_stage_codebooks(books):
         codes = oq.embedded_quantize(books["u"], stages)
         for t, c in enumerate(codes):
             np.testing.assert_array_equal(np.asarray(c, np.uint8), books[f"codes_{tag}_{t}"])
+
+
+def reference_packed_layer():
+    """The reference-packed QUASAR layer of tests/golden/quasar_state.npz as the decoders take it:
+    (packed dict, stages, H, Ke, Ve, kn, vn, qn, the reference's attend output)."""
+    g = np.load(GOLD / "quasar_state.npz")
+    steps = [{"side": int(m[0]), "a": int(m[1]), "b": int(m[2]), "stage": int(m[3]), "n": int(m[4]),
+              "codes": g[f"codes_{i}"]} for i, m in enumerate(g["step_meta"])]
+    packed = {"steps": steps, "counts": g["counts"], "n_c": int(g["n_c"])}
+    for nm in ("rho_k", "rho_v", "T_k", "T_v", "mu_k", "mu_v"):
+        packed[nm] = g[nm]
+    return (packed, tuple(int(b) for b in g["stages"]), int(g["H"]), g["Ke"], g["Ve"], g["kn"], g["vn"], g["qn"],
+            g["out"])
+
+
+def test_quasar_reference_packed_layer_oracle():
+    packed, stages, H, Ke, Ve, kn, vn, qn, out = reference_packed_layer()
+    Hkv, n_c = Ke.shape[1], packed["n_c"]
+    assert n_c > 0 and Ke.shape[2] > 36
+    # the stored code's structure: a non-increasing prefix n per step, each step's rows
+    # (Hkv, n, w * bits / 8) bytes for its band width w
+    ns = [st["n"] for st in packed["steps"]]
+    assert ns[0] == n_c and all(a >= b for a, b in zip(ns, ns[1:]))
+    for st in packed["steps"]:
+        assert st["codes"].shape == (Hkv, st["n"], (st["b"] - st["a"]) * stages[st["stage"]] // 8)
+    K = np.concatenate([Ke, kn], 2)
+    V = np.concatenate([Ve, vn], 2)
+    got = oq.attend(qn, 128 ** -0.5, np.array([H]), K, V, Ke.shape[2], H, packed, stages)
+    err = float(np.abs(got - out).max() / np.abs(out).max())
+    print(f"oracle vs the reference's QuasarState.attend on its own packed layer: {err:.2e}")
+    assert err < 1e-5, err

@@ -82,3 +82,22 @@ def test_quasar_question_step_of_many_tokens():
     st.append(k.cuda(), v.cuda(), torch.arange(H, H + 6))
     q = torch.randn((1, 8, 6, 128), generator=g).to(dtype)
     _check(st, p, torch.cat([K, k], 2), torch.cat([V, v], 2), 120, H, q, list(range(H, H + 6)), (2, 2, 4), 2e-3)
+
+
+def test_quasar_reference_packed_layer():
+    """The stored code of a layer compressed and packed by the reference's own QuasarMethod
+    (tests/golden/quasar_state.npz: 456 coded tokens over 23 levels, rank 128, 76 exact rows)
+    decoded on the GPU after one appended token, against the reference's QuasarState.attend output
+    for the same query (fp32, bar 2e-3 of the output's scale, as the synthetic cases)."""
+    import kvq
+    from test_golden import reference_packed_layer
+    packed, stages, H, Ke, Ve, kn, vn, qn, out = reference_packed_layer()
+    to = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    p = dict(packed)
+    p["steps"] = [dict(st, codes=torch.from_numpy(np.ascontiguousarray(st["codes"]))) for st in packed["steps"]]
+    st = kvq.QuasarState(to(Ke), to(Ve), p, stages, 1, H)
+    st.append(to(kn), to(vn), torch.tensor([H]))
+    got = st.attend(to(qn), 128 ** -0.5, torch.tensor([H])).float().cpu().numpy()
+    err = float(np.abs(got - out).max() / np.abs(out).max())
+    print(f"GPU QUASAR decode vs the reference on its own packed layer: {err:.2e}", flush=True)
+    assert err < 2e-3, err
