@@ -26,6 +26,13 @@ for the functions whose exact floats or draws nothing but the reference itself f
                        histogram), the exact rows of native_state (1830-1843), and the output of
                        QuasarState.attend (1952-1977, the reference's PyTorch path) for one query
                        token after one appended token
+  strata_state.npz     the layer of layer_inputs.strata_layer (seeded; Hq 8, Hkv 2, d 128, H 700)
+                       compressed by the reference's own StrataMethod.compress_layer
+                       (STRATA_KV.py:1528-1581) at keep 0.25 under its default Config: the
+                       allocation (order, level histogram, bits, distortion ratio), its stored code
+                       StrataMethod.pack (1611-1627: per stratum planar codes and fp16 scales, fp16
+                       means) and the output of StrataState.attend (1762-1795, the reference's
+                       PyTorch path) after one appended token (native_state, 1673-1687)
 
 The tests load these files; nothing on the GPU box reads the reference.
 """
@@ -41,6 +48,7 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE))
 
 
 def _load(ref: Path, name: str):
@@ -134,6 +142,37 @@ def quasar_state(Q) -> dict:
     return res
 
 
+def strata_state(S) -> dict:
+    import types
+    import torch
+    from layer_inputs import strata_layer
+    q, k, v, Wo, kn, vn, qn = strata_layer()
+    Hq, Hkv, H, d = q.shape[1], k.shape[1], k.shape[2], k.shape[3]
+    runner = types.SimpleNamespace(d=d, Hq=Hq, layers=[types.SimpleNamespace(
+        self_attn=types.SimpleNamespace(o_proj=types.SimpleNamespace(weight=torch.from_numpy(Wo))))])
+    sm = S.StrataMethod(S.Config(), 0.25, "strata", runner)
+    kt, vt = torch.from_numpy(k), torch.from_numpy(v)
+    al = sm.compress_layer(0, torch.from_numpy(q), kt, vt, d ** -0.5, H)
+    al["packed"] = sm.pack(al)
+    sm.alloc[0] = al
+    st = sm.native_state(0, kt, vt, 2, torch.float32)
+    st.append(torch.from_numpy(kn), torch.from_numpy(vn), torch.tensor([H]))
+    out = st.attend(torch.from_numpy(qn), d ** -0.5, torch.tensor([H]))
+    p = al["packed"]
+    res = {"keep": np.array(0.25), "counts": np.array(al["counts"], np.int64), "n_ex": np.array(al["n_ex"], np.int64),
+           "n_c": np.array(al["n_c"], np.int64), "bits": np.array(al["bits"], np.float64),
+           "distortion": np.array(al["distortion"], np.float64), "order": al["order"].numpy().astype(np.int16),
+           "rs": np.array(al["rs"], np.int64), "re": np.array(al["re"], np.int64), "n0": np.array(st.n0, np.int64),
+           "tier_meta": np.array([[t["bits"], t["n"]] for t in p["tiers"]], np.int64), "out": out.numpy(),
+           "payload": np.array(sm.payload(0), np.int64)}
+    for i, t in enumerate(p["tiers"]):
+        for x in ("kc", "vc", "ks", "vs"):
+            res[f"{x}_{i}"] = t[x].numpy()
+    if al["n_c"]:
+        res["mu_k"], res["mu_v"] = p["mu_k"].numpy(), p["mu_v"].numpy()
+    return res
+
+
 def coverage_groups(S) -> dict:
     from dataclasses import replace
     out = {}
@@ -159,7 +198,8 @@ def main() -> int:
     S = _load(ref, "STRATA_KV")
     Q = _load(ref, "QUASAR_KV")
     for name, data in (("strata_codec", strata_codec(S)), ("quasar_codebooks", quasar_codebooks(S, Q)),
-                       ("coverage_groups", coverage_groups(S)), ("quasar_state", quasar_state(Q))):
+                       ("coverage_groups", coverage_groups(S)), ("quasar_state", quasar_state(Q)),
+                       ("strata_state", strata_state(S))):
         np.savez_compressed(HERE / f"{name}.npz", **data)
         print(f"wrote {name}.npz ({(HERE / f'{name}.npz').stat().st_size} bytes, {len(data)} arrays)")
     return 0

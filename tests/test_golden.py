@@ -13,8 +13,15 @@ These pin what only the reference fixes exactly:
   * a layer compressed and packed by the reference's own QuasarMethod (1628-1710, 1786-1808) and
     decoded by its QuasarState.attend (1952-1977): the oracle's attend on that stored code
     within 1e-5 of the output's scale (the reference computes in float32, the oracle in
-    float64), and the stored code's structure (embedded prefix order, byte widths).
+    float64), and the stored code's structure (embedded prefix order, byte widths);
+  * a layer compressed by the reference's own StrataMethod (STRATA_KV.py:1528-1581, inputs rebuilt
+    from tests/golden/layer_inputs.py) and decoded by its StrataState.attend (1762-1795): the
+    oracle's decode of that stored code within 1e-5 of the output's scale; the oracle's float64
+    allocation chain (coverage -> distortion table -> allocate) on the same inputs: every level
+    count within 1% of the coded range and the distortion ratio within 2% (tokens near a
+    decision boundary may move between float32 and float64 sums).
 """
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -24,6 +31,8 @@ import oracle.quasar as oq
 import oracle.strata as os_
 
 GOLD = Path(__file__).resolve().parent / "golden"
+if str(GOLD) not in sys.path:
+    sys.path.insert(0, str(GOLD))
 
 
 @pytest.fixture(scope="module")
@@ -107,3 +116,63 @@ def test_quasar_reference_packed_layer_oracle():
     err = float(np.abs(got - out).max() / np.abs(out).max())
     print(f"oracle vs the reference's QuasarState.attend on its own packed layer: {err:.2e}")
     assert err < 1e-5, err
+
+
+def strata_reference_layer():
+    """The reference-compressed STRATA layer: (fixture, q, k, v, M, kn, vn, qn, reference
+    allocation dict {rs, re, n_ex, order}, packed dict of the reference's stored code)."""
+    from layer_inputs import out_metric, strata_layer
+    g = np.load(GOLD / "strata_state.npz")
+    q, k, v, Wo, kn, vn, qn = strata_layer()
+    M = out_metric(Wo, q.shape[1], q.shape[-1])
+    al = {"rs": int(g["rs"]), "re": int(g["re"]), "n_ex": int(g["n_ex"]), "order": g["order"].astype(np.int64)}
+    tiers = [{"bits": int(b), "n": int(n), "kc": g[f"kc_{i}"], "vc": g[f"vc_{i}"], "ks": g[f"ks_{i}"],
+              "vs": g[f"vs_{i}"]} for i, (b, n) in enumerate(g["tier_meta"])]
+    packed = {"tiers": tiers, "counts": g["counts"].astype(np.int32), "n_c": int(g["n_c"])}
+    if int(g["n_c"]):
+        packed["mu_k"], packed["mu_v"] = g["mu_k"], g["mu_v"]
+    return g, q, k, v, M, kn, vn, qn, al, packed
+
+
+def _exact_rows(x, al, H):
+    """The exact rows native_state keeps (STRATA_KV.py:1679-1686): sinks, exact-level tokens, window."""
+    rs, re, n_ex = al["rs"], al["re"], al["n_ex"]
+    Hkv = x.shape[1]
+    ids = np.concatenate([np.broadcast_to(np.arange(rs), (Hkv, rs)), al["order"][:, :n_ex] + rs,
+                          np.broadcast_to(np.arange(re, H), (Hkv, H - re))], 1)
+    return np.take_along_axis(x[0], ids[..., None], 1)
+
+
+def test_strata_reference_layer_oracle():
+    import oracle.coverage as oc
+    import oracle.strata_alloc as oa
+    g, q, k, v, M, kn, vn, qn, al, packed = strata_reference_layer()
+    H, d = k.shape[2], k.shape[3]
+    assert int(g["payload"]) * 8 == float(g["bits"])            # the reference's own invariant
+    K = np.concatenate([_exact_rows(k, al, H), kn[0]], 1)
+    V = np.concatenate([_exact_rows(v, al, H), vn[0]], 1)
+    tiers = [(t["bits"], os_.unpack_planar(t["kc"], t["bits"]), t["ks"].astype(np.float32),
+              os_.unpack_planar(t["vc"], t["bits"]), t["vs"].astype(np.float32)) for t in packed["tiers"]]
+    got = os_.strata_attend(qn, d ** -0.5, K, V, tiers, packed["mu_k"].astype(np.float32),
+                            packed["mu_v"].astype(np.float32), os_.rotation_matrix(d))
+    out = g["out"]
+    err = float(np.abs(got - out).max() / np.abs(out).max())
+    print(f"oracle decode vs the reference's StrataState.attend on its own stored code: {err:.2e}")
+    assert err < 1e-5, err
+    # the allocation: the oracle's float64 chain on the same inputs
+    rs, re = al["rs"], al["re"]
+    bits = (2, 4, 8)
+    st = oc.coverage_stats(q[0].astype(np.float64), np.arange(H), k[0].astype(np.float64), v[0].astype(np.float64),
+                           d ** -0.5, H, rs, re, M.astype(np.float64), oc.CoverageParams())
+    signs = os_.rotation_signs(d)
+    _, Yk = os_.strata_center_rotate(k[0, :, rs:re], signs)
+    _, Yv = os_.strata_center_rotate(v[0, :, rs:re], signs)
+    Dt = oa.distortion_table(Yk, Yv, st["S"], st["Mbar"], st["A"], st["W"], st["DD"], bits)
+    cost, fixed, budget, hist_bits, _ = oa.layer_costs(bits, d, k.shape[1], H, float(g["keep"]), rs, re)
+    ref = oa.allocate(Dt, cost, fixed, budget, 4, search=budget >= hist_bits)
+    tol = max(2, int(0.01 * (re - rs)))
+    diff = np.abs(np.asarray(ref["counts"]) - g["counts"])
+    print(f"oracle counts {np.asarray(ref['counts']).tolist()} vs the reference's {g['counts'].tolist()}; "
+          f"distortion {ref['distortion']:.5f} vs {float(g['distortion']):.5f}")
+    assert diff.max() <= tol, diff
+    assert abs(ref["distortion"] - float(g["distortion"])) <= 0.02 * float(g["distortion"])

@@ -12,7 +12,12 @@ Checked, as the reference's own tests check its compression (STRATA_KV.py:1975-1
 * the allocation against the float64 oracle chain (oracle.coverage -> distortion_table ->
   allocate) on the same inputs: every level count within 1% of the coded range (the device's float32
   table is within 2e-3 of each column's scale, so tokens near a decision boundary may move), and the
-  distortion ratio within 2% relative.
+  distortion ratio within 2% relative;
+* and against the reference itself (tests/golden/strata_state.npz: a seeded layer compressed by its
+  own StrataMethod): the device's allocation of the same inputs (level counts within 1% of the coded
+  range, distortion ratio within 2%, payload bits == the reference's when the counts agree), and the
+  reference's own stored code decoded by the device's StrataState after one appended token against
+  its StrataState.attend (fp32: the STRATA decode's bar, 2e-3 of the output's scale; measured 1.4e-4).
 """
 import numpy as np
 import pytest
@@ -125,3 +130,36 @@ def test_compress_layer_uniform_and_nothing_to_code():
                                M.cuda()) is None
     st = comp.native_state(None, None, k.cuda(), v.cuda(), 2, torch.bfloat16)
     assert st.n0 == 700 and st.context_bytes() == 2 * 2 * 700 * D * 2
+
+
+def test_compress_and_decode_against_reference():
+    from kvq.strata_compress import StrataCompressor
+    from test_golden import strata_reference_layer
+    g, q, k, v, M, kn, vn, qn, ref_al, ref_packed = strata_reference_layer()
+    H, d = k.shape[2], k.shape[3]
+    cu = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    comp = StrataCompressor(float(g["keep"]))
+    al = comp.compress_layer(cu(q), cu(k), cu(v), d ** -0.5, H, cu(M))
+    rs, re = al["rs"], al["re"]
+    assert (rs, re) == (int(g["rs"]), int(g["re"]))
+    tol = max(2, int(0.01 * (re - rs)))
+    print(f"device counts {al['counts']} vs the reference's {g['counts'].tolist()}; "
+          f"distortion {al['distortion']:.5f} vs {float(g['distortion']):.5f}", flush=True)
+    assert np.abs(np.asarray(al["counts"]) - g["counts"]).max() <= tol
+    assert abs(al["distortion"] - float(g["distortion"])) <= 0.02 * float(g["distortion"])
+    packed = comp.pack(al)
+    if list(al["counts"]) == g["counts"].tolist():
+        assert comp.payload(packed) == int(g["payload"])
+    # the reference's own stored code, decoded on the device
+    p = dict(ref_packed)
+    p["tiers"] = [{"bits": t["bits"], "n": t["n"], "kc": cu(t["kc"]), "vc": cu(t["vc"]), "ks": cu(t["ks"]),
+                   "vs": cu(t["vs"])} for t in ref_packed["tiers"]]
+    p["counts"] = torch.from_numpy(ref_packed["counts"])
+    p["mu_k"], p["mu_v"] = cu(ref_packed["mu_k"]), cu(ref_packed["mu_v"])
+    ral = dict(ref_al, order=torch.from_numpy(ref_al["order"]).cuda())
+    st = comp.native_state(ral, p, cu(k), cu(v), 2, torch.float32)
+    st.append(cu(kn), cu(vn), torch.tensor([H]))
+    got = st.attend(cu(qn), d ** -0.5, torch.tensor([H])).float().cpu().numpy()
+    err = float(np.abs(got - g["out"]).max() / np.abs(g["out"]).max())
+    print(f"device decode vs the reference's StrataState.attend on its own stored code: {err:.2e}", flush=True)
+    assert err < 2e-3, err
