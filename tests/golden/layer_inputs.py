@@ -27,3 +27,28 @@ def out_metric(Wo: np.ndarray, Hq: int, d: int) -> np.ndarray:
     """M_a = W_O,a^T W_O,a per query head (Hq, d, d), float32 (STRATA_KV.py:1519-1526)."""
     Wa = Wo.reshape(Wo.shape[0], Hq, d).transpose(1, 0, 2)
     return np.einsum("ahi,ahj->aij", Wa, Wa).astype(np.float32)
+
+
+def kivi_inputs(seed: int = 20260105):
+    """Seeded inputs of the kivi_attention fixture: keys with heavy-tailed channel scales and values
+    (1, 2, 100, 128) (100 tokens: a partial group of 32 and of 64), the query and entries of one
+    chunked_attention call, SnapKV's layer (q (1, 8, 300, 128), k (1, 2, 300, 128)), and one
+    stratum's query / codes for tier_reference; all float32 / uint8."""
+    rng = np.random.default_rng(seed)
+    d = 128
+    K = (rng.standard_normal((1, 2, 100, d)) * (np.abs(rng.standard_t(3, (1, 2, 1, d))) + 0.2)).astype(np.float32)
+    V = rng.standard_normal((1, 2, 100, d)).astype(np.float32)
+    qa = rng.standard_normal((1, 8, 3, d)).astype(np.float32)
+    tk = rng.standard_normal((1, 2, 50, d)).astype(np.float32)
+    tv = rng.standard_normal((1, 2, 50, d)).astype(np.float32)
+    qs = (rng.standard_normal((1, 8, 300, d)) * 1.5).astype(np.float32)
+    ks = rng.standard_normal((1, 2, 300, d)).astype(np.float32)
+    ks[:, :, 7] += 2.0 * qs[0, ::4, -64:].mean(1)[None]
+    qr = rng.standard_normal((2, 5, d)).astype(np.float32)
+    qb = rng.standard_normal((2, 5)).astype(np.float32)
+    codes = {b: (rng.integers(0, 2 ** b, (2, 40, d)).astype(np.uint8), rng.integers(0, 2 ** b, (2, 40, d)).astype(np.uint8))
+             for b in (2, 4, 8)}
+    scales = {b: ((rng.random((2, 40)) * 0.1 + 0.01).astype(np.float32), (rng.random((2, 40)) * 0.1 + 0.01).astype(np.float32))
+              for b in (2, 4, 8)}
+    return {"K": K, "V": V, "qa": qa, "tk": tk, "tv": tv, "qs": qs, "ks": ks, "qr": qr, "qb": qb,
+            "codes": codes, "scales": scales}

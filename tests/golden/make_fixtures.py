@@ -33,6 +33,12 @@ for the functions whose exact floats or draws nothing but the reference itself f
                        StrataMethod.pack (1611-1627: per stratum planar codes and fp16 scales, fp16
                        means) and the output of StrataState.attend (1762-1795, the reference's
                        PyTorch path) after one appended token (native_state, 1673-1687)
+  kivi_attention.npz   on the seeded inputs of layer_inputs.kivi_inputs: kivi_quant (826-856) codes,
+                       fp16 zero points and scales of keys (per channel, groups 32 / 64, 2 and 4 bits,
+                       0 and 4 sink rows) and values (per token, groups 32 / 64 / 128); chunked_attention (641-675) over exact
+                       entries (causal positions, a per-head hide_at) and token entries (a -inf
+                       padding bias, tau) in chunks of 2; snapkv_scores (932-954) under the default
+                       Config; tier_reference (1751-1760) of one stratum at 2, 4 and 8 bits
 
 The tests load these files; nothing on the GPU box reads the reference.
 """
@@ -173,6 +179,45 @@ def strata_state(S) -> dict:
     return res
 
 
+def kivi_attention(S) -> dict:
+    import torch
+    from layer_inputs import kivi_inputs
+    x = kivi_inputs()
+    t = {k: torch.from_numpy(v) for k, v in x.items() if isinstance(v, np.ndarray)}
+    out = {}
+    for bits in (2, 4):
+        for group in (32, 64):
+            for sink in (0, 4):
+                r = S.kivi_quant(t["K"], bits, group, True, sink)
+                tag = f"k_{bits}_{group}_{sink}"
+                out[f"{tag}_codes"] = r["codes"].numpy()
+                out[f"{tag}_lo"], out[f"{tag}_scale"] = r["lo"].numpy(), r["scale"].numpy()
+        for group in (32, 64, 128):
+            r = S.kivi_quant(t["V"], bits, group, False, 0)
+            tag = f"v_{bits}_{group}"
+            out[f"{tag}_codes"] = r["codes"].numpy()
+            out[f"{tag}_lo"], out[f"{tag}_scale"] = r["lo"].numpy(), r["scale"].numpy()
+    q_pos = torch.tensor([97, 98, 99])
+    kv_pos = torch.arange(100)
+    hide = torch.full((1, 2, 100), 10 ** 9, dtype=torch.long)
+    hide[0, 0, 10:20] = 98                       # head 0: ten entries hidden from position 98 on
+    b = torch.zeros((1, 2, 50))
+    b[:, :, 45:] = float("-inf")                 # padding entries
+    tok = {"k": t["tk"], "v": t["tv"], "b": b, "tau": torch.arange(50) + 60}
+    out["attn"] = S.chunked_attention(t["qa"], 128 ** -0.5, q_pos, t["K"], t["V"], kv_pos, hide, tok, 2).numpy()
+    cfg = S.Config()
+    out["snap_params"] = np.array([cfg.SNAPKV_WINDOW, cfg.SNAPKV_KERNEL], np.int64)
+    out["snap"] = S.snapkv_scores(t["qs"], t["ks"], 300, 128 ** -0.5, cfg).numpy()
+    for bits in (2, 4, 8):
+        ck, cv = x["codes"][bits]
+        sk, sv = x["scales"][bits]
+        tier = {"bits": bits, "kc": S.pack_planar(torch.from_numpy(ck), bits), "vc": S.pack_planar(torch.from_numpy(cv), bits),
+                "ks": torch.from_numpy(sk).to(torch.float16), "vs": torch.from_numpy(sv).to(torch.float16)}
+        m, l_, acc, z = S.StrataState.tier_reference(t["qr"], t["qb"], tier)
+        out[f"tier_{bits}_m"], out[f"tier_{bits}_l"], out[f"tier_{bits}_acc"] = m.numpy(), l_.numpy(), acc.numpy()
+    return out
+
+
 def coverage_groups(S) -> dict:
     from dataclasses import replace
     out = {}
@@ -199,7 +244,7 @@ def main() -> int:
     Q = _load(ref, "QUASAR_KV")
     for name, data in (("strata_codec", strata_codec(S)), ("quasar_codebooks", quasar_codebooks(S, Q)),
                        ("coverage_groups", coverage_groups(S)), ("quasar_state", quasar_state(Q)),
-                       ("strata_state", strata_state(S))):
+                       ("strata_state", strata_state(S)), ("kivi_attention", kivi_attention(S))):
         np.savez_compressed(HERE / f"{name}.npz", **data)
         print(f"wrote {name}.npz ({(HERE / f'{name}.npz').stat().st_size} bytes, {len(data)} arrays)")
     return 0

@@ -19,7 +19,12 @@ These pin what only the reference fixes exactly:
     oracle's decode of that stored code within 1e-5 of the output's scale; the oracle's float64
     allocation chain (coverage -> distortion table -> allocate) on the same inputs: every level
     count within 1% of the coded range and the distortion ratio within 2% (tokens near a
-    decision boundary may move between float32 and float64 sums).
+    decision boundary may move between float32 and float64 sums);
+  * on the seeded inputs of tests/golden/layer_inputs.kivi_inputs, the reference's kivi_quant
+    (826-856) codes, fp16 zero points and scales of keys and values: bit-equal; its
+    chunked_attention (641-675, exact and token entries, causal positions, per-head hide_at,
+    -inf padding bias, chunks of 2), snapkv_scores (932-954) and tier_reference (1751-1760) at 2,
+    4 and 8 bits: within 2e-6 of each output's scale (the reference computes in float32).
 """
 import sys
 from pathlib import Path
@@ -176,3 +181,57 @@ def test_strata_reference_layer_oracle():
           f"distortion {ref['distortion']:.5f} vs {float(g['distortion']):.5f}")
     assert diff.max() <= tol, diff
     assert abs(ref["distortion"] - float(g["distortion"])) <= 0.02 * float(g["distortion"])
+
+
+@pytest.fixture(scope="module")
+def kiv():
+    from layer_inputs import kivi_inputs
+    return np.load(GOLD / "kivi_attention.npz"), kivi_inputs()
+
+
+def test_kivi_quant_reference(kiv):
+    import oracle.kivi as ok
+    g, x = kiv
+    for bits in (2, 4):
+        cases = [(f"k_{bits}_{gr}_{sk}", x["K"], gr, True, sk) for gr in (32, 64) for sk in (0, 4)]
+        cases += [(f"v_{bits}_{gr}", x["V"], gr, False, 0) for gr in (32, 64, 128)]
+        for tag, X, gr, along, sk in cases:
+            r = ok.kivi_quant(X, bits, gr, along, sk)
+            np.testing.assert_array_equal(r["codes"], g[f"{tag}_codes"], err_msg=tag)
+            np.testing.assert_array_equal(np.asarray(r["lo"], np.float32), g[f"{tag}_lo"], err_msg=tag)
+            np.testing.assert_array_equal(np.asarray(r["scale"], np.float32), g[f"{tag}_scale"], err_msg=tag)
+
+
+def _rel(got, want):
+    return float(np.abs(np.asarray(got, np.float64) - want).max() / np.abs(want).max())
+
+
+def test_chunked_attention_reference(kiv):
+    from oracle.attention import chunked_attention
+    g, x = kiv
+    hide = np.full((1, 2, 100), 10 ** 9, np.int64)
+    hide[0, 0, 10:20] = 98
+    b = np.zeros((1, 2, 50), np.float32)
+    b[:, :, 45:] = -np.inf
+    tok = {"k": x["tk"], "v": x["tv"], "b": b, "tau": np.arange(50) + 60}
+    got = chunked_attention(x["qa"], 128 ** -0.5, np.array([97, 98, 99]), x["K"], x["V"], np.arange(100), hide, tok, 2)
+    assert _rel(got, g["attn"]) < 2e-6
+
+
+def test_snapkv_scores_reference(kiv):
+    import oracle.evict as oe
+    g, x = kiv
+    w, kern = (int(v) for v in g["snap_params"])
+    got = oe.snapkv_scores(x["qs"], x["ks"], 300, 128 ** -0.5, w, kern)
+    assert _rel(got, g["snap"]) < 2e-6
+
+
+def test_tier_reference_partials(kiv):
+    g, x = kiv
+    for bits in (2, 4, 8):
+        ck, cv = x["codes"][bits]
+        sk, sv = (s_.astype(np.float16).astype(np.float32) for s_ in x["scales"][bits])
+        m, l_, acc = os_.tier_partials(x["qr"], x["qb"], ck, sk, cv, sv, bits)
+        assert _rel(m, g[f"tier_{bits}_m"][:, 0]) < 2e-6, bits
+        assert _rel(l_, g[f"tier_{bits}_l"][:, 0]) < 2e-6, bits
+        assert _rel(acc, g[f"tier_{bits}_acc"][:, 0]) < 2e-6, bits

@@ -75,3 +75,25 @@ def test_snapkv_qrows_and_topk_selection():
         diff = set(idx[0, h].tolist()) ^ set(ref[0, h].tolist())
         assert diff <= near, (h, sorted(diff - near)[:10])
     assert set(range(H - 64, H)) <= set(idx[0, 0].tolist())          # the window is always kept
+
+
+def test_snapkv_scores_reference_fixture():
+    """kvq.snapkv_scores against the reference's own snapkv_scores (tests/golden/kivi_attention.npz:
+    q (1, 8, 300, 128), k (1, 2, 300, 128) rebuilt from tests/golden/layer_inputs.py, its default
+    window 64 and kernel 5); fp32 input, bar 1e-5 of the scores' scale."""
+    import sys
+    from pathlib import Path
+    import kvq
+    gold = Path(__file__).resolve().parent / "golden"
+    if str(gold) not in sys.path:
+        sys.path.insert(0, str(gold))
+    from layer_inputs import kivi_inputs
+    g = np.load(gold / "kivi_attention.npz")
+    x = kivi_inputs()
+    w, kern = (int(v) for v in g["snap_params"])
+    cfg = type("Cfg", (), {"SNAPKV_WINDOW": w, "SNAPKV_KERNEL": kern})()
+    got = kvq.snapkv_scores(torch.from_numpy(x["qs"]).cuda(), torch.from_numpy(x["ks"]).cuda(), 300, 128 ** -0.5,
+                            cfg).cpu().numpy()
+    err = float(np.abs(got - g["snap"]).max() / np.abs(g["snap"]).max())
+    print(f"device snapkv_scores vs the reference's: {err:.2e}", flush=True)
+    assert err < 1e-5, err
