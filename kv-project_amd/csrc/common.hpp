@@ -104,6 +104,26 @@ __device__ __forceinline__ void load4(const void* base, int64_t i, float (&x)[4]
   }
 }
 
+// Correctly rounded float32 square root (IEEE round to nearest, what numpy and torch compute on the
+// host).  The hardware root (v_sqrt_f32) is accurate to about one ulp, not correctly rounded, so
+// its result y is moved to the nearest root by Tuckerman's test (Markstein, "IA-64 and Elementary
+// Functions", 2000, section 9.3): with y- and y+ the neighbours of y, RN(sqrt(x)) is y- when
+// x <= y y-, y+ when x > y y+, else y; the sign of x - y y± is exact through one fma.  Arguments
+// below 2^-96 are scaled by 2^32 first (the root by 2^-16 after: exact), so the neighbours stay
+// normal numbers.
+__device__ __forceinline__ float sqrt_rn(float x) {
+  const bool small = x < 0x1p-96f;
+  const float xs = small ? x * 0x1p32f : x;
+  float y = __builtin_amdgcn_sqrtf(xs);
+  if (xs > 0.0f && xs < INFINITY) {
+    const float yd = __uint_as_float(__float_as_uint(y) - 1u);
+    const float yu = __uint_as_float(__float_as_uint(y) + 1u);
+    if (__builtin_fmaf(-yd, y, xs) <= 0.0f) y = yd;
+    else if (__builtin_fmaf(-yu, y, xs) > 0.0f) y = yu;
+  }
+  return small ? y * 0x1p-16f : y;
+}
+
 inline bool valid_dtype(int dt) { return dt == KVQ_F32 || dt == KVQ_F16 || dt == KVQ_BF16; }
 
 }  // namespace kvq

@@ -9,7 +9,8 @@
 //   mu:   per channel, float64 sum over the n tokens, / n, rounded to float32, then to fp16;
 //   Y:    (x - mu) * s in float32, fast Walsh-Hadamard transform with butterfly stages
 //         h = 1, 2, ..., d/2 (pairs (a, b) -> (a + b, a - b)), then * float32(1 / sqrt(d));
-//   s:    rms = sqrt(float32(float64 sum of y^2 / d)); s = max(fp16(float32(step) * rms), 2^-24);
+//   s:    rms = sqrt(float32(float64 sum of y^2 / d)) (correctly rounded sqrt);
+//         s = max(fp16(float32(step) * rms), 2^-24);
 //   code: clamp(rint(y / s + (2^b - 1) / 2), 0, 2^b - 1) with IEEE float32 division and add.
 #include <algorithm>
 
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(256) void strata_quantize_kernel(const float* __res
   double ss = static_cast<double>(y0) * y0 + static_cast<double>(y1) * y1;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  const float rms = __fsqrt_rn(static_cast<float>(ss / kSD));
+  const float rms = sqrt_rn(static_cast<float>(ss / kSD));
   const float s = fmaxf(as_stored16(__fmul_rn(step, rms)), kMinScale);
   const float half = static_cast<float>((1 << bits) - 1) * 0.5f;
   const float qmax = static_cast<float>((1 << bits) - 1);
@@ -286,7 +287,7 @@ __global__ __launch_bounds__(256) void strata_err_kernel(const float* __restrict
       double ss = static_cast<double>(y0) * y0 + static_cast<double>(y1) * y1;
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      const float rms = __fsqrt_rn(static_cast<float>(ss / kSD));
+      const float rms = sqrt_rn(static_cast<float>(ss / kSD));
 #pragma unroll
       for (int b = 0; b < kSMaxBits; ++b) {
         e0[u][b] = e1[u][b] = m0[u][b] = m1[u][b] = 0.0f;

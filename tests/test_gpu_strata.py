@@ -54,6 +54,21 @@ def test_center_rotate_and_quantize_bit_exact(dtype):
 
 
 @pytest.mark.parametrize("bits", [2, 4, 8])
+def test_quantize_scales_at_fp16_ties(bits):
+    # every row's float32(step * rms) is an fp16 rounding midpoint: the stored scale is right only
+    # if rms is the correctly rounded square root (one ulp either way picks the other neighbour)
+    import kvq
+    from midpoint_rows import midpoint_rows
+    step = os_.uniform_step(bits)[0]
+    Y = midpoint_rows(bits, 4096, seed=100 + bits, step=step).reshape(2, 2, 1024, 128)
+    codes, sc = kvq.strata_quantize(torch.from_numpy(Y).cuda(), bits)
+    c_o, s_o, _ = os_.strata_quantize(Y.reshape(4, 1024, 128), bits, step)
+    got = sc.float().cpu().numpy().reshape(4, 1024)
+    assert np.array_equal(got, s_o), f"{int((got != s_o).sum())} of 4096 scales differ"
+    np.testing.assert_array_equal(codes.cpu().numpy().reshape(4, 1024, -1), os_.pack_planar(c_o, bits))
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
 def test_value_tiles_layout(bits):
     import kvq
     rng = np.random.default_rng(10 + bits)

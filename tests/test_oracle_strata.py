@@ -47,6 +47,27 @@ def test_strata_quantize_kat_and_nearest_level():
         assert rel <= 1.3 * uniform_step(b)[1]
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_midpoint_rows_land_on_fp16_ties(bits):
+    # the rows the GPU scale test uses: float32(step * rms) is exactly halfway between two fp16
+    # values, so the stored scale is the even neighbour (round half to even, torch's and numpy's
+    # fp16 rounding); one ulp less or more on rms gives the lower or upper neighbour
+    from midpoint_rows import midpoint_rows
+    step = uniform_step(bits)[0]
+    Y = midpoint_rows(bits, 200, seed=bits, step=step)
+    _, s, _ = strata_quantize(Y, bits, step)
+    rms = np.sqrt(np.float32((Y.astype(np.float64) ** 2).sum(-1) / Y.shape[-1]))
+    prod = (np.float32(step) * rms).astype(np.float32)
+    lo = prod.astype(np.float16)
+    nb = np.nextafter(lo, np.where(lo.astype(np.float32) < prod, np.float16(np.inf), np.float16(0)))
+    mid = (lo.astype(np.float64) + nb.astype(np.float64)) / 2
+    np.testing.assert_array_equal(prod.astype(np.float64), mid)             # exactly a tie
+    assert np.all(lo.view(np.uint16) % 2 == 0) and np.array_equal(s, lo.astype(np.float32))
+    for k in (-1, 1):
+        off = (np.float32(step) * np.nextafter(rms, np.float32(np.inf) * k)).astype(np.float32)
+        assert np.all(off != prod)                                        # a one-ulp root leaves the tie
+
+
 def test_planar_pack_kat_and_round_trip():
     c = np.array([[0, 1, 2, 3, 3, 2, 1, 0]], np.uint8)
     np.testing.assert_array_equal(pack_planar(c, 2), [[120, 45]])         # by hand
