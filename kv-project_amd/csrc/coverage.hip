@@ -13,19 +13,23 @@
 // the group table); padded rows have position -1 and contribute nothing.  Launches (one stream, no
 // host synchronisation, no atomics: every sum has a fixed order):
 //   cov_rowstats  per (group, 64-row block, h): logits of 16-key tiles on the matrix cores
-//                 (row_tiles.hpp), online max / sum per row -> row max (base 2) and 1 / sum.
-//   cov_output    same grid: the logits again, p = 2^(s - max) in registers as the A operand of the
-//                 PV product (hi + lo parts; the two 16-key tiles of a 32-key step give every lane 8
-//                 keys of its row, in an order the B operand follows), B = values of the step from an
-//                 LDS tile; o = PV / sum, fp32.
+//                 (row_tiles.hpp), online max / sum per row -> row max (base 2) and 1 / sum; every
+//                 key tile feeds all the block's rows a wavefront holds, the wavefronts split the keys.
+//   cov_output    per (group, 64-row block, h, key split): the logits again, p = 2^(s - max) / sum in
+//                 registers as the A operand of the PV product (hi + lo parts; the two 16-key tiles
+//                 of a 32-key step give every lane 8 keys of its row, in an order the B operand
+//                 follows), B = values of the step from an LDS tile; the split's part of o, fp32.
 //   cov_metric    x M and x M x for 32 vectors per workgroup with the query head's metric staged in
-//                 LDS: the row outputs (o M replaces o) and the coded values (v M v).
-//   cov_terms<A>  per (h, 256-token chunk): for every group reaching the chunk, logits and v.(oM) of
-//                 16-token tiles on the matrix cores, then the per-(row, token) terms: the group's
+//                 LDS: the row outputs (the key splits' parts summed in order; o M) and the coded
+//                 values (v M v).
+//   cov_terms<A>  per (h, 256-token chunk, group split): for every group of the split reaching the
+//                 chunk, logits and v.(oM) of 16-token tiles on the matrix cores (rows as the A side:
+//                 a lane holds four rows of one token), then the per-(row, token) terms: the group's
 //                 drop total and every row's key-term mass, as partials per chunk.
 //   cov_groups    N per group -> weight 1 / N (0 if N = 0), live count.
 //   cov_roww      per row: its group's weight x its key-term mass.
-//   cov_terms<B>  the same tiles with the weights: A, DD and the read mass per query head.
+//   cov_terms<B>  the same tiles with the weights: A, DD and the read mass per query head, one partial
+//                 per group split; cov_split_sums adds the splits in order.
 //   cov_smat      S = sum over rows of weight * alpha * (scaling q)(scaling q)^T.
 //   cov_final     live average, S / sum_j A_j, Mbar, floors (one workgroup for the sums, then all).
 #include <algorithm>
@@ -43,6 +47,8 @@ constexpr int kCWaves = 4;
 constexpr int kChunkTok = 256;          // tokens of a cov_terms workgroup
 constexpr int kGT = 8;                  // ints per group-table entry
 constexpr int kMetricRows = 32;         // vectors of a cov_metric workgroup
+constexpr int kOSplit = 4;              // key splits of cov_output (workgroups per 64-row item)
+constexpr int kTSplit = 4;              // group splits of cov_terms (workgroups per token chunk)
 constexpr float kCLog2e = 1.4426950408889634f;
 
 // group table entry (kGT ints): row_base, nq, nq_pad, mmax, te, local, 0, 0
@@ -60,7 +66,8 @@ struct CovParams {
   float scaling, eta;
   float* row_m;                          // (Hkv, NR) row max (base 2)
   float* row_il;                         // (Hkv, NR) 1 / row sum
-  float* o;                              // (Hkv, NR, d) fp32 outputs, then o M
+  float* o;                              // (Hkv, NR, d) o M (cov_metric over the summed outputs)
+  float* o_part;                         // (kOSplit, Hkv, NR, d) fp32 outputs of each key split
   float* oMo;                            // (Hkv, NR)
   float* vmv;                            // (Hkv, rep, n)
   float* ddpart;                         // (G, Hkv, n_chunks)
@@ -72,6 +79,9 @@ struct CovParams {
   float* W;                              // (Hkv, n)
   float* DD;                             // (Hkv, n)
   float* WVa;                            // (Hkv, rep, n)
+  float* A_part;                         // (kTSplit, Hkv, n) weighted pass: each group split's sums
+  float* DD_part;                        // (kTSplit, Hkv, n)
+  float* WVa_part;                       // (kTSplit, Hkv, rep, n)
   float* S;                              // (Hkv, d, d)
   float* Mbar;                           // (Hkv, d, d)
 };
@@ -117,48 +127,113 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rs, int64_t st,
     load_op_buf<DT>(rs, static_cast<int>((tok * st + 32 * ks + 8 * g) * TileOps<DT>::ESZ), op[ks]);
 }
 
+// Every key tile a wavefront loads feeds several of the item's 16-row blocks (16-bit data: all four,
+// the wavefronts splitting the keys in quarters; fp32 operands take twice the registers: two blocks,
+// halves), so the workgroup reads its keys once instead of once per row block.  The wavefronts'
+// states of a row meet in LDS, split by split in a fixed order.
 template <int DT>
 __global__ __launch_bounds__(kCThreads) void cov_rowstats(CovParams p) {
+  constexpr int NH = TileOps<DT>::NH;
+  constexpr int NRB = DT == KVQ_F32 ? 2 : 4;                 // row blocks per wavefront
+  constexpr int KS = kCWaves * NRB / 4;                      // key splits (wavefronts sharing blocks)
+  __shared__ float st[kCWaves][NRB][16][2];
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
   const int item = blockIdx.x % p.n_items, h = blockIdx.x / p.n_items;
   const int grp = p.items[2 * item], rb = p.items[2 * item + 1];
   const int32_t* gt = p.gtab + kGT * grp;
   const int rows_g = p.rep * gt[2];
-  const int row0 = gt[0] + 64 * rb + 16 * wave;
-  if (64 * rb + 16 * wave >= rows_g) return;                 // whole wavefront past the group's rows
-  u32x4 qop[4][TileOps<DT>::NH];
-  const int pos = load_rows<DT>(p, h, row0, g, n, qop);
   const int mmax = gt[3];
-  const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, TileOps<DT>::ESZ);
-  float m = -INFINITY, ls = 0.0f;
-  for (int t0 = 0; t0 < mmax; t0 += 16) {
-    u32x4 kop[4][TileOps<DT>::NH];
-    load_tile<DT>(rk, p.k_st, t0, g, n, kop);
-    const f32x4 d = tile_dots<DT, TileOps<DT>::NH, TileOps<DT>::NH>(kop, qop);
-    float sv[4], mt = -INFINITY;
+  const int ks = wave % KS, rgrp = wave / KS;
+  u32x4 qop[NRB][4][NH];
+  int pos[NRB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = t0 + 4 * g + i;
-      sv[i] = (j <= pos && j < mmax) ? d[i] * p.qscale : -INFINITY;
-      mt = fmaxf(mt, sv[i]);
-    }
-    if (mt > m) {
-      ls *= __builtin_amdgcn_exp2f(m - mt);
-      m = mt;
-    }
-    if (m != -INFINITY) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ls += __builtin_amdgcn_exp2f(sv[i] - m);
+  for (int b = 0; b < NRB; ++b) {
+    const int rl = 64 * rb + 16 * (rgrp * NRB + b);           // first row of the block in the group
+    if (rl < rows_g) {
+      pos[b] = load_rows<DT>(p, h, gt[0] + rl, g, n, qop[b]);
+    } else {
+      pos[b] = -1;
+      zero_ops<DT>(qop[b]);
     }
   }
-  // lanes (0..3, n) hold disjoint keys of row n
-  const float M = xmax32(xmax16(m));
-  const float part = (M == -INFINITY || m == -INFINITY) ? 0.0f : ls * __builtin_amdgcn_exp2f(m - M);
-  const float L = xsum32(xsum16(part));
-  if (g == 0 && row0 + n < p.NR) {
-    const int64_t o = static_cast<int64_t>(h) * p.NR + row0 + n;
-    p.row_m[o] = M == -INFINITY ? 0.0f : M;                  // padding rows: every p is masked to 0 below
-    p.row_il[o] = L > 0.0f ? 1.0f / L : 0.0f;
+  // this split's keys: whole 16-key tiles
+  const int ntile = (mmax + 15) / 16;
+  const int k0 = 16 * (ntile * ks / KS), k1 = min(mmax, 16 * (ntile * (ks + 1) / KS));
+  const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, TileOps<DT>::ESZ);
+  float m[NRB], ls[NRB];
+#pragma unroll
+  for (int b = 0; b < NRB; ++b) {
+    m[b] = -INFINITY;
+    ls[b] = 0.0f;
+  }
+  // three key tiles in rotation: two in flight behind the one computed (a tile past the split reads
+  // zeros through the buffer resource or in-range keys, masked or never computed)
+  u32x4 kt[3][4][NH];
+  load_tile<DT>(rk, p.k_st, k0, g, n, kt[0]);
+  load_tile<DT>(rk, p.k_st, k0 + 16, g, n, kt[1]);
+  auto tile = [&](int t0, const u32x4 (&kop)[4][NH]) {
+#pragma unroll
+    for (int b = 0; b < NRB; ++b) {
+      const f32x4 d = tile_dots<DT, NH, NH>(kop, qop[b]);
+      float sv[4], mt = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = t0 + 4 * g + i;
+        sv[i] = (j <= pos[b] && j < mmax) ? d[i] * p.qscale : -INFINITY;
+        mt = fmaxf(mt, sv[i]);
+      }
+      if (mt > m[b]) {
+        ls[b] *= __builtin_amdgcn_exp2f(m[b] - mt);
+        m[b] = mt;
+      }
+      if (m[b] != -INFINITY) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ls[b] += __builtin_amdgcn_exp2f(sv[i] - m[b]);
+      }
+    }
+  };
+  for (int t0 = k0; t0 < k1; t0 += 48) {
+    load_tile<DT>(rk, p.k_st, t0 + 32, g, n, kt[2]);
+    tile(t0, kt[0]);
+    if (t0 + 16 >= k1) break;
+    load_tile<DT>(rk, p.k_st, t0 + 48, g, n, kt[0]);
+    tile(t0 + 16, kt[1]);
+    if (t0 + 32 >= k1) break;
+    load_tile<DT>(rk, p.k_st, t0 + 64, g, n, kt[1]);
+    tile(t0 + 32, kt[2]);
+  }
+  // lanes (0..3, n) hold disjoint keys of row n: this split's state of the row
+#pragma unroll
+  for (int b = 0; b < NRB; ++b) {
+    const float M = xmax32(xmax16(m[b]));
+    const float part = (M == -INFINITY || m[b] == -INFINITY) ? 0.0f : ls[b] * __builtin_amdgcn_exp2f(m[b] - M);
+    const float L = xsum32(xsum16(part));
+    if (g == 0) {
+      st[wave][b][n][0] = M;
+      st[wave][b][n][1] = L;
+    }
+  }
+  __syncthreads();
+  // thread t < 64: row t % 16 of the item's block t / 16, its splits combined in order
+  if (threadIdx.x < 64) {
+    const int rbi = threadIdx.x / 16, row = threadIdx.x % 16;
+    const int rg = rbi / NRB, b = rbi % NRB;
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) M = fmaxf(M, st[rg * KS + s][b][row][0]);
+    float L = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const float ms = st[rg * KS + s][b][row][0];
+      if (ms != -INFINITY) L += st[rg * KS + s][b][row][1] * __builtin_amdgcn_exp2f(ms - M);
+    }
+    const int rl = 64 * rb + 16 * rbi;
+    const int r_abs = gt[0] + rl + row;
+    if (rl < rows_g && r_abs < p.NR) {
+      const int64_t o = static_cast<int64_t>(h) * p.NR + r_abs;
+      p.row_m[o] = M == -INFINITY ? 0.0f : M;                // padding rows: every p is masked to 0 below
+      p.row_il[o] = L > 0.0f ? 1.0f / L : 0.0f;
+    }
   }
 }
 
@@ -173,7 +248,8 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
   constexpr int U16 = kCD * ESZ / 16;                        // 16-byte units of a value row
   __shared__ uint32_t vt[32 * VRW];
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
-  const int item = blockIdx.x % p.n_items, h = blockIdx.x / p.n_items;
+  const int item = blockIdx.x % p.n_items, hs = blockIdx.x / p.n_items;
+  const int h = hs % p.Hkv, sp = hs / p.Hkv;                // head, key split
   const int grp = p.items[2 * item], rb = p.items[2 * item + 1];
   const int32_t* gt = p.gtab + kGT * grp;
   const int rows_g = p.rep * gt[2];
@@ -187,35 +263,61 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
     zero_ops<DT>(qop);
   const float rm = (active && row0 + n < p.NR) ? p.row_m[static_cast<int64_t>(h) * p.NR + row0 + n] : 0.0f;
   const int mmax = gt[3];
+  // this workgroup's keys: split sp of the item's 32-key steps (every split writes its partial,
+  // zeros when it holds no keys; the probabilities use the row's global maximum and sum, so the
+  // partials add up to o)
+  const int nstep = (mmax + 31) / 32;
+  const int k0 = 32 * (nstep * sp / kOSplit), k1 = min(mmax, 32 * (nstep * (sp + 1) / kOSplit));
   const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, ESZ);
   const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v, p.v_sh, p.v_st, h, p.T, ESZ);
   f32x4 acc[8];
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int t0 = 0; t0 < mmax; t0 += 32) {
-    // the step's 32 value rows (rows at or past mmax as zeros: p = 0 there must not meet a NaN)
-    __syncthreads();
-    for (int u = threadIdx.x; u < 32 * U16; u += kCThreads) {
+  // a step's loads: its 32 value rows (this thread's 16-byte units; rows at or past mmax as zeros:
+  // p = 0 there must not meet a NaN) and this wavefront's two key tiles.  The next step's loads go
+  // out as soon as the current key tiles have entered the logit products.
+  constexpr int KU = (32 * U16 + kCThreads - 1) / kCThreads;
+  u32x4 vr[KU];
+  u32x4 kr[2][4][TileOps<DT>::NH];
+  auto load_step = [&](int t0) {
+#pragma unroll
+    for (int k = 0; k < KU; ++k) {
+      const int u = threadIdx.x + kCThreads * k;
       const int key = u / U16, w16 = u % U16;
-      u32x4 x = u32x4{0u, 0u, 0u, 0u};
-      if (t0 + key < mmax)
-        x = __builtin_amdgcn_raw_buffer_load_b128(
+      vr[k] = u32x4{0u, 0u, 0u, 0u};
+      if (u < 32 * U16 && t0 + key < k1)
+        vr[k] = __builtin_amdgcn_raw_buffer_load_b128(
             rv, static_cast<int>((static_cast<int64_t>(t0 + key) * p.v_st) * ESZ + 16 * w16), 0, 0);
-      uint32_t* dst = vt + key * VRW + 4 * w16;
-      dst[0] = x[0];
-      dst[1] = x[1];
-      dst[2] = x[2];
-      dst[3] = x[3];
     }
-    __syncthreads();
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) load_tile<DT>(rk, p.k_st, t0 + 16 * tau, g, n, kr[tau]);
+  };
+  if (k0 < k1) load_step(k0);
+  for (int t0 = k0; t0 < k1; t0 += 32) {
+    // LDS-only barriers: the key tiles of the step stay in flight while its value rows are stored
+    block_lds_barrier();                                     // the previous step's value rows are read
+#pragma unroll
+    for (int k = 0; k < KU; ++k) {
+      const int u = threadIdx.x + kCThreads * k;
+      if (u < 32 * U16) {
+        uint32_t* dst = vt + (u / U16) * VRW + 4 * (u % U16);
+        dst[0] = vr[k][0];
+        dst[1] = vr[k][1];
+        dst[2] = vr[k][2];
+        dst[3] = vr[k][3];
+      }
+    }
+    block_lds_barrier();
     // probabilities of the two 16-key tiles: lane (g, n) holds keys t0 + 4g + i and t0 + 16 + 4g + i
     // of row n
+    f32x4 dd[2];
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) dd[tau] = tile_dots<DT, TileOps<DT>::NH, TileOps<DT>::NH>(kr[tau], qop);
+    if (t0 + 32 < k1) load_step(t0 + 32);
     float pr[8];
 #pragma unroll
     for (int tau = 0; tau < 2; ++tau) {
-      u32x4 kop[4][TileOps<DT>::NH];
-      load_tile<DT>(rk, p.k_st, t0 + 16 * tau, g, n, kop);
-      const f32x4 d = tile_dots<DT, TileOps<DT>::NH, TileOps<DT>::NH>(kop, qop);
+      const f32x4 d = dd[tau];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = t0 + 16 * tau + 4 * g + i;
@@ -263,7 +365,7 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
     const int row = row0 + 4 * g + i;
     if (row >= p.NR) continue;
     const float il = p.row_il[static_cast<int64_t>(h) * p.NR + row];
-    float* dst = p.o + (static_cast<int64_t>(h) * p.NR + row) * kCD + n;
+    float* dst = p.o_part + ((static_cast<int64_t>(sp) * p.Hkv + h) * p.NR + row) * kCD + n;
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) dst[16 * cb] = acc[cb][i] * il;
   }
@@ -290,7 +392,12 @@ __global__ __launch_bounds__(kCThreads) void cov_metric(CovParams p, const int32
     float x = 0.0f;
     if (idx < count) {
       if constexpr (ROWS) {
-        if (rl[idx] >= 0) x = p.o[(static_cast<int64_t>(h) * p.NR + rl[idx]) * kCD + c];
+        if (rl[idx] >= 0) {                            // the key splits' outputs, summed in order
+          const int64_t o = (static_cast<int64_t>(h) * p.NR + rl[idx]) * kCD + c;
+          const int64_t split = static_cast<int64_t>(p.Hkv) * p.NR * kCD;
+#pragma unroll
+          for (int sp = 0; sp < kOSplit; ++sp) x += p.o_part[sp * split + o];
+        }
       } else {
         x = load_as_f32<DT>(p.v, static_cast<int64_t>(h) * p.v_sh + static_cast<int64_t>(p.rs + idx) * p.v_st + c);
       }
@@ -346,6 +453,28 @@ __global__ __launch_bounds__(kCThreads) void cov_clear(float* x, int64_t count) 
   if (t < count) x[t] = 0.0f;
 }
 
+// the weighted pass's group splits summed in split order: A, DD (Hkv, n) and WVa (Hkv, rep, n)
+__global__ __launch_bounds__(kCThreads) void cov_split_sums(CovParams p) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kCThreads + threadIdx.x;
+  const int64_t nA = static_cast<int64_t>(p.Hkv) * p.n, nW = nA * p.rep;
+  if (t < nA) {
+    float a = 0.0f, dd = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kTSplit; ++s) {
+      a += p.A_part[s * nA + t];
+      dd += p.DD_part[s * nA + t];
+    }
+    p.A[t] = a;
+    p.DD[t] = dd;
+  }
+  if (t < nW) {
+    float w = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kTSplit; ++s) w += p.WVa_part[s * nW + t];
+    p.WVa[t] = w;
+  }
+}
+
 // per (h, 256-token chunk): every group reaching the chunk, its rows in 64-row blocks (one 16-row
 // block per wavefront, one query head per block since nq_pad is a multiple of 16), 16-token tiles.
 // WEIGHTED = false: drop totals and key-term masses; true: the weighted per-token sums.
@@ -356,8 +485,12 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
   __shared__ float accD[kCWaves][kChunkTok];
   __shared__ float accW[kCWaves][kChunkTok];             // read mass of the wavefront's current block
   __shared__ float red[kCWaves];
+  __shared__ float rsc[kCWaves][16];                     // o M scale of each row of a wavefront's block
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
-  const int h = blockIdx.x / p.n_chunks, chunk = blockIdx.x % p.n_chunks;
+  // groups ts, ts + kTSplit, ... of (h, chunk): the chunks near the start, which every group reaches,
+  // spread over kTSplit workgroups
+  const int ts = blockIdx.x % kTSplit;
+  const int h = blockIdx.x / kTSplit / p.n_chunks, chunk = blockIdx.x / kTSplit % p.n_chunks;
   const int c0 = p.rs + chunk * kChunkTok;               // first token of the chunk
   const int c1 = min(c0 + kChunkTok, p.re);
   const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, TileOps<DT>::ESZ);
@@ -368,7 +501,7 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
       (&accD[0][0])[u] = 0.0f;
     }
   }
-  for (int grp = 0; grp < p.G; ++grp) {
+  for (int grp = ts; grp < p.G; grp += kTSplit) {
     const int32_t* gt = p.gtab + kGT * grp;
     const int row_base = gt[0], nq = gt[1], nq_pad = gt[2], te = gt[4], local = gt[5];
     const int rows_g = p.rep * nq_pad;
@@ -389,16 +522,16 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
       const bool act = rbl < rows_g;
       const int r = act ? rbl / nq_pad : 0;
       const int row0 = row_base + rbl;
+      // operands (lane n: row n of the block, channels 8g + 32 ks ..) as the A side of the products,
+      // the token tiles as the B side: the results hold rows 4g + i of token n in lane (g, n), so a
+      // token's sums over the rows are three in-lane adds and two cross-group steps, and a row's sums
+      // over the tokens stay in the lane until the block's end
       u32x4 qop[4][NH], mop[4][2];
-      int pos = -1;
-      float rm = 0.0f, ril = 0.0f, omo = 0.0f, mscale = 1.0f;
+      float mscale_n = 1.0f;
       if (act) {
-        pos = load_rows<DT>(p, h, row0, g, n, qop);
+        (void)load_rows<DT>(p, h, row0, g, n, qop);
         const int64_t rid = static_cast<int64_t>(h) * p.NR + row0 + n;
-        rm = p.row_m[rid];
-        ril = p.row_il[rid];
-        omo = p.oMo[rid];
-        // B operand of v.(oM): the row's o M times a power of two that brings its largest entry to
+        // A operand of v.(oM): the row's o M times a power of two that brings its largest entry to
         // [128, 256) (inside the range of fp16 parts), in two parts of the operand type
         float x[4][8], mx = 0.0f;
 #pragma unroll
@@ -414,7 +547,7 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
         int ex = 0;
         if (mx > 0.0f) (void)frexpf(mx, &ex);
         const float up = ldexpf(1.0f, 8 - ex);
-        mscale = ldexpf(1.0f, ex - 8);
+        mscale_n = ldexpf(1.0f, ex - 8);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           float xs8[8];
@@ -427,25 +560,50 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) mop[ks][0] = mop[ks][1] = u32x4{0u, 0u, 0u, 0u};
       }
+      // the per-row values of this lane's rows 4g + i
+      if (g == 0) rsc[wave][n] = mscale_n;
+      wave_lds_fence();
+      int pos[4];
+      float rm[4], ril[4], omo[4], msc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = row0 + 4 * g + i;
+        const int64_t rid = static_cast<int64_t>(h) * p.NR + row;
+        pos[i] = act ? p.rowpos[row] : -1;
+        rm[i] = act ? p.row_m[rid] : 0.0f;
+        ril[i] = act ? p.row_il[rid] : 0.0f;
+        omo[i] = act ? p.oMo[rid] : 0.0f;
+        msc[i] = rsc[wave][4 * g + i];
+      }
       if constexpr (WEIGHTED) {
         for (int u = l; u < kChunkTok; u += 64) accW[wave][u] = 0.0f;
         wave_lds_fence();
       }
-      float alpha = 0.0f;                                 // key-term mass of this lane's row (pass A)
-      for (int t0 = c0; t0 < t_end; t0 += 16) {
-        u32x4 kop[4][NH], vop[4][NH];
+      float alpha[4] = {0.0f, 0.0f, 0.0f, 0.0f};          // key-term mass of rows 4g + i (pass A)
+      // a tile's loads (key and value tiles, v M v of this lane's token); the next tile's go out as
+      // soon as the current tiles have entered the matrix products
+      const int64_t vmv_base = (static_cast<int64_t>(h) * p.rep + r) * p.n - p.rs;   // + token j
+      u32x4 kop[4][NH], vop[4][NH];
+      float vmv1;
+      auto load_t = [&](int t0) {
         load_tile<DT>(rk, p.k_st, t0, g, n, kop);
         load_tile<DT>(rv, p.v_st, t0, g, n, vop);
-        const f32x4 s = tile_dots<DT, NH, NH>(kop, qop);
-        const f32x4 ov = tile_dots<DT, NH, 2>(vop, mop);
+        const int j = t0 + n;
+        vmv1 = (act && j < t_end) ? p.vmv[vmv_base + j] : 0.0f;
+      };
+      if (c0 < t_end) load_t(c0);
+      for (int t0 = c0; t0 < t_end; t0 += 16) {
+        const f32x4 s = tile_dots<DT, NH, NH>(qop, kop);
+        const f32x4 ov = tile_dots<DT, 2, NH>(mop, vop);
+        const float vmv = vmv1;
+        if (t0 + 16 < t_end) load_t(t0 + 16);
+        const int j = t0 + n;
         float ta[4], td[4], tw[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int j = t0 + 4 * g + i;
-          const bool far = act && j < t_end && j <= pos - local;
-          const float pr = far ? __builtin_amdgcn_exp2f(s[i] * p.qscale - rm) * ril : 0.0f;
-          const float vmv = far ? p.vmv[(static_cast<int64_t>(h) * p.rep + r) * p.n + (j - p.rs)] : 0.0f;
-          const float u2 = far ? fmaxf(vmv - 2.0f * (ov[i] * mscale) + omo, 0.0f) : 0.0f;
+          const bool far = act && j < t_end && j <= pos[i] - local;
+          const float pr = far ? __builtin_amdgcn_exp2f(s[i] * p.qscale - rm[i]) * ril[i] : 0.0f;
+          const float u2 = far ? fmaxf(vmv - 2.0f * (ov[i] * msc[i]) + omo[i], 0.0f) : 0.0f;
           const float qd = pr / fmaxf(1.0f - pr, 1e-6f);
           td[i] = qd * qd * u2;
           ta[i] = pr * pr * u2;
@@ -455,27 +613,32 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             dsum += td[i];
-            alpha += ta[i];
+            alpha[i] += ta[i];
           }
         } else {
-          // per token: the sums over the block's 16 rows; token 4g + i is owned by lane (g, n = i)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float sa = row_sum16(ta[i]), sd = row_sum16(td[i]), sw = row_sum16(tw[i]);
-            const int jj = t0 + 4 * g + i - c0;
-            if (n == i && act) {
-              accA[wave][jj] += sa * wq;
-              accD[wave][jj] += sd * wq;
-              accW[wave][jj] += sw * wq;
-            }
+          // token t0 + n: its sums over the block's 16 rows (the lane's four, then the lane groups')
+          float sa = (ta[0] + ta[1]) + (ta[2] + ta[3]);
+          float sd = (td[0] + td[1]) + (td[2] + td[3]);
+          float sw = (tw[0] + tw[1]) + (tw[2] + tw[3]);
+          sa = xsum32(xsum16(sa));
+          sd = xsum32(xsum16(sd));
+          sw = xsum32(xsum16(sw));
+          if (g == 0 && act && j < t_end) {
+            accA[wave][j - c0] += sa * wq;
+            accD[wave][j - c0] += sd * wq;
+            accW[wave][j - c0] += sw * wq;
           }
         }
       }
       if constexpr (!WEIGHTED) {
-        // the row's key-term mass over this chunk (its four lanes hold disjoint tokens)
-        const float a_row = xsum32(xsum16(alpha));
-        if (act && g == 0)
-          p.alpha_part[(static_cast<int64_t>(h) * p.n_chunks + chunk) * p.NR + row0 + n] = a_row / static_cast<float>(nq);
+        // rows 4g + i: their key-term mass over this chunk (the 16 lanes of group g hold its tokens)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a_row = row_sum16(alpha[i]);
+          if (act && n == 0)
+            p.alpha_part[(static_cast<int64_t>(h) * p.n_chunks + chunk) * p.NR + row0 + 4 * g + i] =
+                a_row / static_cast<float>(nq);
+        }
       } else {
         // the wavefronts' read masses into their query heads' rows of WVa, in wavefront order
         __syncthreads();
@@ -483,7 +646,8 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
           for (int w = 0; w < kCWaves; ++w) {
             const int rbw = rb0 + 16 * w;
             if (rbw >= rows_g) break;
-            p.WVa[(static_cast<int64_t>(h) * p.rep + rbw / nq_pad) * p.n + (c0 + u - p.rs)] += accW[w][u];
+            p.WVa_part[((static_cast<int64_t>(ts) * p.Hkv + h) * p.rep + rbw / nq_pad) * p.n + (c0 + u - p.rs)] +=
+                accW[w][u];
           }
         }
         __syncthreads();
@@ -502,9 +666,9 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
   if constexpr (WEIGHTED) {
     __syncthreads();
     for (int u = threadIdx.x; u < c1 - c0; u += kCThreads) {
-      const int64_t o = static_cast<int64_t>(h) * p.n + (c0 + u - p.rs);
-      p.A[o] = (accA[0][u] + accA[1][u]) + (accA[2][u] + accA[3][u]);
-      p.DD[o] = (accD[0][u] + accD[1][u]) + (accD[2][u] + accD[3][u]);
+      const int64_t o = (static_cast<int64_t>(ts) * p.Hkv + h) * p.n + (c0 + u - p.rs);
+      p.A_part[o] = (accA[0][u] + accA[1][u]) + (accA[2][u] + accA[3][u]);
+      p.DD_part[o] = (accD[0][u] + accD[1][u]) + (accD[2][u] + accD[3][u]);
     }
   }
 }
@@ -655,14 +819,14 @@ __global__ __launch_bounds__(kCThreads) void cov_final(CovParams p) {
 
 using namespace kvq;
 
-// workspace layout (floats): row_m, row_il, oMo, roww (Hkv NR each); o (Hkv NR d); vmv (Hkv rep n);
-// ddpart (G Hkv n_chunks); alpha_part (Hkv n_chunks NR); gw (G + 1); red (4 + Hkv rep + Hkv);
-// WVa (Hkv rep n)
+// workspace layout (floats): row_m, row_il, oMo, roww (Hkv NR each); o (Hkv NR d); o_part (kOSplit Hkv
+// NR d); vmv (Hkv rep n); ddpart (G Hkv n_chunks); alpha_part (Hkv n_chunks NR); gw (G + 1); red (4 +
+// Hkv rep + Hkv); WVa (Hkv rep n); A_part, DD_part (kTSplit Hkv n each); WVa_part (kTSplit Hkv rep n)
 extern "C" int64_t kvq_coverage_stats_workspace(int64_t Hkv, int64_t rep, int64_t n, int64_t NR, int64_t G) {
   if (Hkv <= 0 || rep <= 0 || n <= 0 || NR <= 0 || G <= 0) return -1;
   const int64_t nch = (n + kChunkTok - 1) / kChunkTok;
-  return 4 * Hkv * NR + Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch + Hkv * nch * NR + (G + 1) +
-         (4 + Hkv * rep + Hkv) + Hkv * rep * n;
+  return 4 * Hkv * NR + (1 + kOSplit) * Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch + Hkv * nch * NR + (G + 1) +
+         (4 + Hkv * rep + Hkv) + Hkv * rep * n + kTSplit * (2 * Hkv * n + Hkv * rep * n);
 }
 
 extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const int32_t* rowpos, const int32_t* rowgrp,
@@ -705,18 +869,22 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   p.oMo = w; w += Hkv * NR;
   p.roww = w; w += Hkv * NR;
   p.o = w; w += Hkv * NR * kCD;
+  p.o_part = w; w += kOSplit * Hkv * NR * kCD;
   p.vmv = w; w += Hkv * rep * n;
   p.ddpart = w; w += G * Hkv * p.n_chunks;
   p.alpha_part = w; w += Hkv * p.n_chunks * NR;
   p.gw = w; w += G + 1;
   p.red = w; w += 4 + Hkv * rep + Hkv;
-  p.WVa = w;
+  p.WVa = w; w += Hkv * rep * n;
+  p.A_part = w; w += kTSplit * Hkv * n;
+  p.DD_part = w; w += kTSplit * Hkv * n;
+  p.WVa_part = w;
   p.A = A; p.W = W; p.DD = DD; p.S = S; p.Mbar = Mbar;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 blk(kCThreads);
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowstats<DT_>), dim3(n_items * Hkv), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(rowstats)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_output<DT_>), dim3(n_items * Hkv), blk, 0, s, p));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_output<DT_>), dim3(n_items * Hkv * kOSplit), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(output)");
   hipLaunchKernelGGL((cov_metric<KVQ_F32, true>), dim3(Hkv * rep * ((n_rlist + kMetricRows - 1) / kMetricRows)), blk,
                      0, s, p, rlist, (int)n_rlist);
@@ -725,17 +893,20 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
                                                dim3(Hkv * rep * ((n + kMetricRows - 1) / kMetricRows)), blk, 0, s, p,
                                                rlist, (int)n_rlist));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(v M v)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, false>), dim3(Hkv * p.n_chunks), blk, 0, s, p));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, false>), dim3(Hkv * p.n_chunks * kTSplit), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(terms)");
   hipLaunchKernelGGL(cov_groups, dim3(1), blk, 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(groups)");
   hipLaunchKernelGGL(cov_roww, dim3((Hkv * NR + kCThreads - 1) / kCThreads), blk, 0, s, p, rowgrp);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(row weights)");
-  // WVa is accumulated by the weighted pass: cleared by a fill kernel (graph-capture safe)
-  hipLaunchKernelGGL(cov_clear, dim3((Hkv * rep * n + kCThreads - 1) / kCThreads), blk, 0, s, p.WVa, Hkv * rep * n);
+  // the read masses are accumulated by the weighted pass: cleared by a fill kernel (graph-capture safe)
+  const int64_t nwp = kTSplit * Hkv * rep * n;
+  hipLaunchKernelGGL(cov_clear, dim3((nwp + kCThreads - 1) / kCThreads), blk, 0, s, p.WVa_part, nwp);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(clear)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, true>), dim3(Hkv * p.n_chunks), blk, 0, s, p));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, true>), dim3(Hkv * p.n_chunks * kTSplit), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(weighted terms)");
+  hipLaunchKernelGGL(cov_split_sums, dim3((Hkv * rep * n + kCThreads - 1) / kCThreads), blk, 0, s, p);
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(split sums)");
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_smat<DT_>), dim3(Hkv * (kCD / 16)), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(S)");
   hipLaunchKernelGGL(cov_final_sums, dim3(1), dim3(1024), 0, s, p);

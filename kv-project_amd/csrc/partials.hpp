@@ -152,18 +152,21 @@ __device__ void exact_partial(const ExactArgs& e, int b, int hq, int t, int bh, 
 
 constexpr int kMergeThreads = 256;
 
+// barriers ordering LDS only: global loads issued before the reduction stay in flight across it
 __device__ __forceinline__ float block_reduce_256(float v, bool is_max, float* red) {
   v = is_max ? wave_max(v) : wave_sum(v);
-  __syncthreads();
+  block_lds_barrier();                              // earlier reads of red[] are done
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  block_lds_barrier();
   const float a = red[0], b = red[1], c = red[2], d = red[3];
   return is_max ? fmaxf(fmaxf(a, b), fmaxf(c, d)) : (a + b) + (c + d);
 }
 
 // grid = BH * R_real workgroups of kMergeThreads; thread t sums channels 4 (t % (D/4)) .. +3 of
-// the partials s = t / (D/4) (mod PARTS) with 16-byte loads, the PARTS slices meet in LDS.
-template <int R, int DT, int D>
+// the partials s = t / (D/4) (mod PARTS) with 16-byte loads, the PARTS slices meet in LDS.  The
+// first NPRE partials of every slice are loaded before anything else, so a merge of up to
+// NPRE x PARTS partials waits for one round of loads.
+template <int R, int DT, int D, int NPRE>
 __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(MergeArgs a) {
   static_assert(kMergeThreads % (D / 4) == 0, "channel quads must divide the workgroup");
   constexpr int PARTS = kMergeThreads / (D / 4);
@@ -190,11 +193,17 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(MergeArgs a) 
   const int c4 = tid % (D / 4), part = tid / (D / 4);
   const int b = bh / a.Hkv, h = bh % a.Hkv;
   const int hq = h * a.rep + r / a.Tq, t = r % a.Tq;
-  // the first coded partials are loaded before the exact pass so their latency overlaps it
+  // the first partials are loaded before the exact pass so their latency overlaps it
   const float m0 = tid < S_all ? m_of(tid) : -INFINITY;
   const float l0 = tid < S_all ? l_of(tid) : 0.0f;
-  const float mp0 = part < S_all ? m_of(part) : -INFINITY;
-  const float4 op0 = part < S_all ? o_of(part, c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  float mp[NPRE];
+  float4 op[NPRE];
+#pragma unroll
+  for (int k = 0; k < NPRE; ++k) {
+    const int s = part + PARTS * k;
+    mp[k] = s < S_all ? m_of(s) : -INFINITY;
+    op[k] = s < S_all ? o_of(s, c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   // exact rows attended here: their own partial (me, le, oe) joins the coded ones
   float me = -INFINITY, le = 0.0f;
   float4 oe = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -212,10 +221,17 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(MergeArgs a) 
   const float wc = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mx);
   const float we = me == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(me - Mx);
   const float L = wc * Lc + we * le;
-  const float w0 = mp0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp0 - M);
-  float4 o = make_float4(w0 * op0.x, w0 * op0.y, w0 * op0.z, w0 * op0.w);
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < NPRE; ++k) {
+    const float w = mp[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mp[k] - M);
+    o.x = __builtin_fmaf(w, op[k].x, o.x);
+    o.y = __builtin_fmaf(w, op[k].y, o.y);
+    o.z = __builtin_fmaf(w, op[k].z, o.z);
+    o.w = __builtin_fmaf(w, op[k].w, o.w);
+  }
 #pragma unroll 4
-  for (int s = part + PARTS; s < S_all; s += PARTS) {
+  for (int s = part + PARTS * NPRE; s < S_all; s += PARTS) {
     const float ms = m_of(s);
     const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
     const float4 v = o_of(s, c4);
@@ -315,7 +331,15 @@ inline int pow2_rows(int64_t r) {
 // launch merge_rows_kernel for a runtime row count R (power of two <= 8) and output dtype
 inline int launch_merge_rows(const MergeArgs& a, int R, int BH, int out_dtype, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(BH) * a.R_real);
-#define KVQ_MERGE_L(R_, DT_) hipLaunchKernelGGL((merge_rows_kernel<R_, DT_, 128>), grid, dim3(kMergeThreads), 0, s, a)
+  constexpr int kParts128 = kMergeThreads / 32;    // partial slices of the D = 128 merge
+  const int per = (a.S_ex + a.S + kParts128 - 1) / kParts128;
+#define KVQ_MERGE_N(R_, DT_, N_) hipLaunchKernelGGL((merge_rows_kernel<R_, DT_, 128, N_>), grid, dim3(kMergeThreads), 0, s, a)
+#define KVQ_MERGE_L(R_, DT_)                                   \
+  do {                                                         \
+    if (per <= 1) KVQ_MERGE_N(R_, DT_, 1);                     \
+    else if (per <= 4) KVQ_MERGE_N(R_, DT_, 4);                \
+    else KVQ_MERGE_N(R_, DT_, 16);                             \
+  } while (0)
 #define KVQ_MERGE_R(DT_)                           \
   switch (R) {                                     \
     case 1: KVQ_MERGE_L(1, DT_); break;            \
@@ -330,6 +354,7 @@ inline int launch_merge_rows(const MergeArgs& a, int R, int BH, int out_dtype, h
   }
 #undef KVQ_MERGE_R
 #undef KVQ_MERGE_L
+#undef KVQ_MERGE_N
   KVQ_LAUNCH_CHECK("merge_rows");
   return KVQ_OK;
 }
