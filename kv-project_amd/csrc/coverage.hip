@@ -69,6 +69,8 @@ struct CovParams {
   float* o;                              // (Hkv, NR, d) o M (cov_metric over the summed outputs)
   float* o_part;                         // (kOSplit, Hkv, NR, d) fp32 outputs of each key split
   float* oMo;                            // (Hkv, NR)
+  uint32_t* mop;                         // (Hkv, NR, 4 ks, 4 g, 2 parts) u32x4: o M operand parts
+  float* rowf;                           // (Hkv, NR) float4: row max, 1 / sum, o M o, o M scale
   float* vmv;                            // (Hkv, rep, n)
   float* ddpart;                         // (G, Hkv, n_chunks)
   float* alpha_part;                     // (Hkv, n_chunks, NR)
@@ -475,6 +477,38 @@ __global__ __launch_bounds__(kCThreads) void cov_split_sums(CovParams p) {
   }
 }
 
+// Once per row (after cov_metric): o M as the A operand of cov_terms' v.(oM) products -- times a
+// power of two that brings its largest entry to [128, 256) (inside the range of fp16 parts), in two
+// parts of the operand type -- and the row's values as one float4 (row max, 1 / sum, o M o, the
+// power of two back).  Thread (row, ks, g) converts channels 32 ks + 8 g .. + 7; a row's 16 threads
+// are one DPP row of a wavefront.
+template <int DT>
+__global__ __launch_bounds__(kCThreads) void cov_rowprep(CovParams p) {
+  const int64_t rid = static_cast<int64_t>(blockIdx.x) * (kCThreads / 16) + threadIdx.x / 16;
+  const int sl = threadIdx.x % 16, ks = sl / 4, g = sl % 4;
+  if (rid >= static_cast<int64_t>(p.Hkv) * p.NR) return;          // whole rows: 16 lanes alike
+  const float4* src = reinterpret_cast<const float4*>(p.o + rid * kCD + 32 * ks + 8 * g);
+  const float4 a = src[0], b = src[1];
+  float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(x[e]));
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  int ex = 0;
+  if (mx > 0.0f) (void)frexpf(mx, &ex);
+  const float up = ldexpf(1.0f, 8 - ex);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] *= up;
+  u32x4 hi, lo;
+  f32_parts<DT>(x, hi, lo);
+  u32x4* dst = reinterpret_cast<u32x4*>(p.mop) + rid * 32 + (ks * 4 + g) * 2;
+  dst[0] = hi;
+  dst[1] = lo;
+  if (sl == 0)
+    reinterpret_cast<float4*>(p.rowf)[rid] = make_float4(p.row_m[rid], p.row_il[rid], p.oMo[rid], ldexpf(1.0f, ex - 8));
+}
+
 // per (h, 256-token chunk): every group reaching the chunk, its rows in 64-row blocks (one 16-row
 // block per wavefront, one query head per block since nq_pad is a multiple of 16), 16-token tiles.
 // WEIGHTED = false: drop totals and key-term masses; true: the weighted per-token sums.
@@ -485,12 +519,16 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
   __shared__ float accD[kCWaves][kChunkTok];
   __shared__ float accW[kCWaves][kChunkTok];             // read mass of the wavefront's current block
   __shared__ float red[kCWaves];
-  __shared__ float rsc[kCWaves][16];                     // o M scale of each row of a wavefront's block
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
   // groups ts, ts + kTSplit, ... of (h, chunk): the chunks near the start, which every group reaches,
-  // spread over kTSplit workgroups
-  const int ts = blockIdx.x % kTSplit;
-  const int h = blockIdx.x / kTSplit / p.n_chunks, chunk = blockIdx.x / kTSplit % p.n_chunks;
+  // spread over kTSplit workgroups.  Work units u = (h, chunk, ts) in order; block b runs on XCD b % 8
+  // (round-robin dispatch), and each XCD takes a contiguous range of units, so the splits of a chunk
+  // share one L2 and its key and value tiles, which every group re-reads, stay there.
+  const int n_units = p.Hkv * p.n_chunks * kTSplit, per_xcd = (n_units + 7) / 8;
+  const int u = static_cast<int>(blockIdx.x % 8) * per_xcd + static_cast<int>(blockIdx.x / 8);
+  if (u >= n_units) return;
+  const int ts = u % kTSplit;
+  const int h = u / kTSplit / p.n_chunks, chunk = u / kTSplit % p.n_chunks;
   const int c0 = p.rs + chunk * kChunkTok;               // first token of the chunk
   const int c1 = min(c0 + kChunkTok, p.re);
   const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, TileOps<DT>::ESZ);
@@ -527,53 +565,38 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
       // token's sums over the rows are three in-lane adds and two cross-group steps, and a row's sums
       // over the tokens stay in the lane until the block's end
       u32x4 qop[4][NH], mop[4][2];
-      float mscale_n = 1.0f;
+      int pos[4];
+      float rm[4], ril[4], omo[4], msc[4];
       if (act) {
+        // row n's operands and rows 4g + i's values, prepared once per row by cov_rowprep: one
+        // round of independent loads
         (void)load_rows<DT>(p, h, row0, g, n, qop);
-        const int64_t rid = static_cast<int64_t>(h) * p.NR + row0 + n;
-        // A operand of v.(oM): the row's o M times a power of two that brings its largest entry to
-        // [128, 256) (inside the range of fp16 parts), in two parts of the operand type
-        float x[4][8], mx = 0.0f;
+        const u32x4* mp = reinterpret_cast<const u32x4*>(p.mop) + (static_cast<int64_t>(h) * p.NR + row0 + n) * 32;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const float4* src = reinterpret_cast<const float4*>(p.o + rid * kCD + 32 * ks + 8 * g);
-          const float4 a = src[0], b = src[1];
-          x[ks][0] = a.x; x[ks][1] = a.y; x[ks][2] = a.z; x[ks][3] = a.w;
-          x[ks][4] = b.x; x[ks][5] = b.y; x[ks][6] = b.z; x[ks][7] = b.w;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(x[ks][e]));
+          mop[ks][0] = mp[(ks * 4 + g) * 2];
+          mop[ks][1] = mp[(ks * 4 + g) * 2 + 1];
         }
-        mx = xmax32(xmax16(mx));                          // over the four lanes of row n
-        int ex = 0;
-        if (mx > 0.0f) (void)frexpf(mx, &ex);
-        const float up = ldexpf(1.0f, 8 - ex);
-        mscale_n = ldexpf(1.0f, ex - 8);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          float xs8[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) xs8[e] = x[ks][e] * up;
-          f32_parts<DT>(xs8, mop[ks][0], mop[ks][1]);
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + 4 * g + i;
+          const float4 f = reinterpret_cast<const float4*>(p.rowf)[static_cast<int64_t>(h) * p.NR + row];
+          pos[i] = p.rowpos[row];
+          rm[i] = f.x;
+          ril[i] = f.y;
+          omo[i] = f.z;
+          msc[i] = f.w;
         }
       } else {
         zero_ops<DT>(qop);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) mop[ks][0] = mop[ks][1] = u32x4{0u, 0u, 0u, 0u};
-      }
-      // the per-row values of this lane's rows 4g + i
-      if (g == 0) rsc[wave][n] = mscale_n;
-      wave_lds_fence();
-      int pos[4];
-      float rm[4], ril[4], omo[4], msc[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = row0 + 4 * g + i;
-        const int64_t rid = static_cast<int64_t>(h) * p.NR + row;
-        pos[i] = act ? p.rowpos[row] : -1;
-        rm[i] = act ? p.row_m[rid] : 0.0f;
-        ril[i] = act ? p.row_il[rid] : 0.0f;
-        omo[i] = act ? p.oMo[rid] : 0.0f;
-        msc[i] = rsc[wave][4 * g + i];
+        for (int i = 0; i < 4; ++i) {
+          pos[i] = -1;
+          rm[i] = ril[i] = omo[i] = 0.0f;
+          msc[i] = 1.0f;
+        }
       }
       if constexpr (WEIGHTED) {
         for (int u = l; u < kChunkTok; u += 64) accW[wave][u] = 0.0f;
@@ -821,12 +844,13 @@ using namespace kvq;
 
 // workspace layout (floats): row_m, row_il, oMo, roww (Hkv NR each); o (Hkv NR d); o_part (kOSplit Hkv
 // NR d); vmv (Hkv rep n); ddpart (G Hkv n_chunks); alpha_part (Hkv n_chunks NR); gw (G + 1); red (4 +
-// Hkv rep + Hkv); WVa (Hkv rep n); A_part, DD_part (kTSplit Hkv n each); WVa_part (kTSplit Hkv rep n)
+// Hkv rep + Hkv); WVa (Hkv rep n); A_part, DD_part (kTSplit Hkv n each); WVa_part (kTSplit Hkv rep n);
+// mop (Hkv NR 128), rowf (Hkv NR 4), 16-byte aligned
 extern "C" int64_t kvq_coverage_stats_workspace(int64_t Hkv, int64_t rep, int64_t n, int64_t NR, int64_t G) {
   if (Hkv <= 0 || rep <= 0 || n <= 0 || NR <= 0 || G <= 0) return -1;
   const int64_t nch = (n + kChunkTok - 1) / kChunkTok;
   return 4 * Hkv * NR + (1 + kOSplit) * Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch + Hkv * nch * NR + (G + 1) +
-         (4 + Hkv * rep + Hkv) + Hkv * rep * n + kTSplit * (2 * Hkv * n + Hkv * rep * n);
+         (4 + Hkv * rep + Hkv) + Hkv * rep * n + kTSplit * (2 * Hkv * n + Hkv * rep * n) + 132 * Hkv * NR + 4;
 }
 
 extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const int32_t* rowpos, const int32_t* rowgrp,
@@ -878,7 +902,10 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   p.WVa = w; w += Hkv * rep * n;
   p.A_part = w; w += kTSplit * Hkv * n;
   p.DD_part = w; w += kTSplit * Hkv * n;
-  p.WVa_part = w;
+  p.WVa_part = w; w += kTSplit * Hkv * rep * n;
+  w += (4 - (reinterpret_cast<uintptr_t>(w) / 4) % 4) % 4;       // 16-byte alignment of the next two
+  p.mop = reinterpret_cast<uint32_t*>(w); w += 128 * Hkv * NR;
+  p.rowf = w;
   p.A = A; p.W = W; p.DD = DD; p.S = S; p.Mbar = Mbar;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 blk(kCThreads);
@@ -893,7 +920,10 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
                                                dim3(Hkv * rep * ((n + kMetricRows - 1) / kMetricRows)), blk, 0, s, p,
                                                rlist, (int)n_rlist));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(v M v)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, false>), dim3(Hkv * p.n_chunks * kTSplit), blk, 0, s, p));
+  const unsigned terms_blocks = static_cast<unsigned>(8 * ((Hkv * p.n_chunks * kTSplit + 7) / 8));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowprep<DT_>), dim3((Hkv * NR + 15) / 16), blk, 0, s, p));
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(row operands)");
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, false>), dim3(terms_blocks), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(terms)");
   hipLaunchKernelGGL(cov_groups, dim3(1), blk, 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(groups)");
@@ -903,7 +933,7 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   const int64_t nwp = kTSplit * Hkv * rep * n;
   hipLaunchKernelGGL(cov_clear, dim3((nwp + kCThreads - 1) / kCThreads), blk, 0, s, p.WVa_part, nwp);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(clear)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, true>), dim3(Hkv * p.n_chunks * kTSplit), blk, 0, s, p));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, true>), dim3(terms_blocks), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(weighted terms)");
   hipLaunchKernelGGL(cov_split_sums, dim3((Hkv * rep * n + kCThreads - 1) / kCThreads), blk, 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(split sums)");
