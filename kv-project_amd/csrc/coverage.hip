@@ -95,6 +95,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void* base, in
   return make_rsrc(b, static_cast<uint32_t>((static_cast<int64_t>(T - 1) * st + kCD) * esz));
 }
 
+// Work unit of this block when each XCD (blocks b % 8, dispatched round-robin) takes a contiguous
+// range of the units, so neighbouring units, which read overlapping keys and values, share one L2;
+// -1 past the last unit (grids are rounded up to a multiple of 8)
+__device__ __forceinline__ int xcd_unit(int n_units) {
+  const int per = (n_units + 7) / 8;
+  const int u = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
+  return u < n_units ? u : -1;
+}
+inline unsigned xcd_grid(int64_t n_units) { return static_cast<unsigned>(8 * ((n_units + 7) / 8)); }
+
 template <int DT>
 __device__ __forceinline__ void zero_ops(u32x4 (&op)[4][TileOps<DT>::NH]) {
 #pragma unroll
@@ -140,7 +150,9 @@ __global__ __launch_bounds__(kCThreads) void cov_rowstats(CovParams p) {
   constexpr int KS = kCWaves * NRB / 4;                      // key splits (wavefronts sharing blocks)
   __shared__ float st[kCWaves][NRB][16][2];
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
-  const int item = blockIdx.x % p.n_items, h = blockIdx.x / p.n_items;
+  const int unit = xcd_unit(p.Hkv * p.n_items);                // (h, item), h outermost
+  if (unit < 0) return;
+  const int item = unit % p.n_items, h = unit / p.n_items;
   const int grp = p.items[2 * item], rb = p.items[2 * item + 1];
   const int32_t* gt = p.gtab + kGT * grp;
   const int rows_g = p.rep * gt[2];
@@ -250,8 +262,9 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
   constexpr int U16 = kCD * ESZ / 16;                        // 16-byte units of a value row
   __shared__ uint32_t vt[32 * VRW];
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
-  const int item = blockIdx.x % p.n_items, hs = blockIdx.x / p.n_items;
-  const int h = hs % p.Hkv, sp = hs / p.Hkv;                // head, key split
+  const int unit = xcd_unit(p.Hkv * kOSplit * p.n_items);      // (h, key split, item), h outermost
+  if (unit < 0) return;
+  const int item = unit % p.n_items, h = unit / p.n_items / kOSplit, sp = unit / p.n_items % kOSplit;
   const int grp = p.items[2 * item], rb = p.items[2 * item + 1];
   const int32_t* gt = p.gtab + kGT * grp;
   const int rows_g = p.rep * gt[2];
@@ -524,9 +537,8 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
   // spread over kTSplit workgroups.  Work units u = (h, chunk, ts) in order; block b runs on XCD b % 8
   // (round-robin dispatch), and each XCD takes a contiguous range of units, so the splits of a chunk
   // share one L2 and its key and value tiles, which every group re-reads, stay there.
-  const int n_units = p.Hkv * p.n_chunks * kTSplit, per_xcd = (n_units + 7) / 8;
-  const int u = static_cast<int>(blockIdx.x % 8) * per_xcd + static_cast<int>(blockIdx.x / 8);
-  if (u >= n_units) return;
+  const int u = xcd_unit(p.Hkv * p.n_chunks * kTSplit);
+  if (u < 0) return;
   const int ts = u % kTSplit;
   const int h = u / kTSplit / p.n_chunks, chunk = u / kTSplit % p.n_chunks;
   const int c0 = p.rs + chunk * kChunkTok;               // first token of the chunk
@@ -909,9 +921,9 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   p.A = A; p.W = W; p.DD = DD; p.S = S; p.Mbar = Mbar;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 blk(kCThreads);
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowstats<DT_>), dim3(n_items * Hkv), blk, 0, s, p));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowstats<DT_>), dim3(xcd_grid(n_items * Hkv)), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(rowstats)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_output<DT_>), dim3(n_items * Hkv * kOSplit), blk, 0, s, p));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_output<DT_>), dim3(xcd_grid(n_items * Hkv * kOSplit)), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(output)");
   hipLaunchKernelGGL((cov_metric<KVQ_F32, true>), dim3(Hkv * rep * ((n_rlist + kMetricRows - 1) / kMetricRows)), blk,
                      0, s, p, rlist, (int)n_rlist);
@@ -920,7 +932,7 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
                                                dim3(Hkv * rep * ((n + kMetricRows - 1) / kMetricRows)), blk, 0, s, p,
                                                rlist, (int)n_rlist));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(v M v)");
-  const unsigned terms_blocks = static_cast<unsigned>(8 * ((Hkv * p.n_chunks * kTSplit + 7) / 8));
+  const unsigned terms_blocks = xcd_grid(Hkv * p.n_chunks * kTSplit);
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowprep<DT_>), dim3((Hkv * NR + 15) / 16), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(row operands)");
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, false>), dim3(terms_blocks), blk, 0, s, p));
