@@ -49,6 +49,7 @@ constexpr int kGT = 8;                  // ints per group-table entry
 constexpr int kMetricRows = 32;         // vectors of a cov_metric workgroup
 constexpr int kOSplit = 4;              // key splits of cov_output (workgroups per 64-row item)
 constexpr int kTSplit = 4;              // group splits of cov_terms (workgroups per token chunk)
+constexpr int kSSplit = 16;             // row splits of cov_smat (workgroups per 16 rows of S)
 constexpr float kCLog2e = 1.4426950408889634f;
 
 // group table entry (kGT ints): row_base, nq, nq_pad, mmax, te, local, 0, 0
@@ -77,6 +78,7 @@ struct CovParams {
   float* gw;                             // (G): 1 / N or 0; [G]: live count
   float* roww;                           // (Hkv, NR): weight * alpha
   float* red;                            // finalisation sums
+  float* sums;                           // (Hkv, 2 + rep): per-head sums of A, DD, read masses
   float* A;                              // (Hkv, n)
   float* W;                              // (Hkv, n)
   float* DD;                             // (Hkv, n)
@@ -85,6 +87,7 @@ struct CovParams {
   float* DD_part;                        // (kTSplit, Hkv, n)
   float* WVa_part;                       // (kTSplit, Hkv, rep, n)
   float* S;                              // (Hkv, d, d)
+  float* S_part;                         // (kSSplit, Hkv, d, d): each row split's sum
   float* Mbar;                           // (Hkv, d, d)
 };
 
@@ -742,27 +745,48 @@ __global__ __launch_bounds__(kCThreads) void cov_roww(CovParams p, const int32_t
   p.roww[t] = a * p.gw[grp];
 }
 
-// S[h] = sum over rows of roww * (scaling q)(scaling q)^T: per (h, 16 output rows), 64 rows per stage
+// S[h] = sum over rows of roww * (scaling q)(scaling q)^T: per (h, 16 output rows, row split), 64
+// rows per stage staged with 16-byte loads; each split writes its partial sum, cov_smat_sum adds the
+// splits in order
 template <int DT>
 __global__ __launch_bounds__(kCThreads) void cov_smat(CovParams p) {
+  constexpr int ESZ = TileOps<DT>::ESZ;
+  constexpr int U = kCD * ESZ / 16;                     // 16-byte units of a row
   __shared__ float qs[64][kCD + 4];
   __shared__ float ws[64];
-  const int h = blockIdx.x / (kCD / 16), c1b = blockIdx.x % (kCD / 16);
+  const int sp = blockIdx.x % kSSplit, c1b = blockIdx.x / kSSplit % (kCD / 16);
+  const int h = blockIdx.x / kSSplit / (kCD / 16);
   const int c1 = 16 * c1b + threadIdx.x / 16, c2 = 8 * (threadIdx.x % 16);   // 8 output columns per thread
+  const int per = (p.NR + 64 * kSSplit - 1) / (64 * kSSplit) * 64;            // rows of a split, whole stages
+  const int rb = sp * per, re = min(p.NR, rb + per);
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  for (int r0 = 0; r0 < p.NR; r0 += 64) {
+  for (int r0 = rb; r0 < re; r0 += 64) {
     __syncthreads();
-    for (int u = threadIdx.x; u < 64 * kCD; u += kCThreads) {
-      const int k = u / kCD, c = u % kCD;
+    for (int u = threadIdx.x; u < 64 * U; u += kCThreads) {
+      const int k = u / U, w = u % U;
       const int row = r0 + k;
-      qs[k][c] = (row < p.NR && p.rowpos[row] >= 0)
-                     ? load_as_f32<DT>(p.qr, (static_cast<int64_t>(h) * p.NR + row) * kCD + c) * p.scaling
-                     : 0.0f;
+      float x[16 / ESZ];
+      const bool live = row < re && p.rowpos[row] >= 0;
+      if constexpr (DT == KVQ_F32) {
+        const float4 v = live ? *reinterpret_cast<const float4*>(static_cast<const float*>(p.qr) +
+                                                                 (static_cast<int64_t>(h) * p.NR + row) * kCD + 4 * w)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+      } else {
+        if (live) {
+          load8<DT>(p.qr, (static_cast<int64_t>(h) * p.NR + row) * kCD + 8 * w, x);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 16 / ESZ; ++e) qs[k][(16 / ESZ) * w + e] = x[e] * p.scaling;
     }
     if (threadIdx.x < 64)
-      ws[threadIdx.x] = r0 + threadIdx.x < p.NR ? p.roww[static_cast<int64_t>(h) * p.NR + r0 + threadIdx.x] : 0.0f;
+      ws[threadIdx.x] = r0 + threadIdx.x < re ? p.roww[static_cast<int64_t>(h) * p.NR + r0 + threadIdx.x] : 0.0f;
     __syncthreads();
     for (int k = 0; k < 64; ++k) {
       const float a = ws[k] * qs[k][c1];
@@ -770,54 +794,67 @@ __global__ __launch_bounds__(kCThreads) void cov_smat(CovParams p) {
       for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(a, qs[k][c2 + e], acc[e]);
     }
   }
+  float* dst = p.S_part + ((static_cast<int64_t>(sp) * p.Hkv + h) * kCD + c1) * kCD + c2;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) p.S[(static_cast<int64_t>(h) * kCD + c1) * kCD + c2 + e] = acc[e];
+  for (int e = 0; e < 8; ++e) dst[e] = acc[e];
 }
 
-// finalisation sums (one workgroup): red[0..2] the means of the live-averaged A, DD, W; red[3] the
-// live count; red[4 + h rep + r] omega (live-averaged read mass per query head); red[4 + Hkv rep + h]
-// sum_j A (live-averaged)
+__global__ __launch_bounds__(kCThreads) void cov_smat_sum(CovParams p) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kCThreads + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(p.Hkv) * kCD * kCD;
+  if (t >= total) return;
+  float a = 0.0f;
+#pragma unroll
+  for (int sp = 0; sp < kSSplit; ++sp) a += p.S_part[sp * total + t];
+  p.S[t] = a;
+}
+
+// finalisation sums: red[0..2] the means of the live-averaged A, DD, W; red[3] the live count;
+// red[4 + h rep + r] omega (live-averaged read mass per query head); red[4 + Hkv rep + h] sum_j A
+// (live-averaged).  First every per-head sum over the n tokens, one workgroup each (sums[h][0] A,
+// [1] DD, [2 + r] the read mass of query head r), then one thread combines them in a fixed order.
 __global__ __launch_bounds__(1024) void cov_final_sums(CovParams p) {
   __shared__ float part[16];
-  const float live = fmaxf(p.gw[p.G], 1.0f);
-  auto block_sum = [&](float v) -> float {
-    v = wave_sum(v);
-    if (threadIdx.x % 64 == 0) part[threadIdx.x / 64] = v;
-    __syncthreads();
+  const int nk = 2 + p.rep;
+  const int h = blockIdx.x / nk, kind = blockIdx.x % nk;
+  const float* src = kind == 0 ? p.A + static_cast<int64_t>(h) * p.n
+                   : kind == 1 ? p.DD + static_cast<int64_t>(h) * p.n
+                               : p.WVa + (static_cast<int64_t>(h) * p.rep + (kind - 2)) * p.n;
+  float v = 0.0f;
+  for (int j = threadIdx.x; j < p.n; j += 1024) v += src[j];
+  v = wave_sum(v);
+  if (threadIdx.x % 64 == 0) part[threadIdx.x / 64] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
     float t = 0.0f;
     for (int w = 0; w < 16; ++w) t += part[w];
-    __syncthreads();
-    return t;
-  };
+    p.sums[blockIdx.x] = t;
+  }
+}
+
+__global__ void cov_final_combine(CovParams p) {
+  if (threadIdx.x != 0) return;
+  const float live = fmaxf(p.gw[p.G], 1.0f);
+  const int nk = 2 + p.rep;
   float gA = 0.0f, gD = 0.0f, gW = 0.0f;
   for (int h = 0; h < p.Hkv; ++h) {
-    float sA = 0.0f, sD = 0.0f;
-    for (int j = threadIdx.x; j < p.n; j += 1024) {
-      sA += p.A[static_cast<int64_t>(h) * p.n + j];
-      sD += p.DD[static_cast<int64_t>(h) * p.n + j];
-    }
-    sA = block_sum(sA);
-    sD = block_sum(sD);
+    const float sA = p.sums[h * nk], sD = p.sums[h * nk + 1];
     float sW = 0.0f;
     for (int r = 0; r < p.rep; ++r) {
-      float om = 0.0f;
-      for (int j = threadIdx.x; j < p.n; j += 1024) om += p.WVa[(static_cast<int64_t>(h) * p.rep + r) * p.n + j];
-      om = block_sum(om);
-      if (threadIdx.x == 0) p.red[4 + h * p.rep + r] = om / live;
+      const float om = p.sums[h * nk + 2 + r];
+      p.red[4 + h * p.rep + r] = om / live;
       sW += om;
     }
-    if (threadIdx.x == 0) p.red[4 + p.Hkv * p.rep + h] = sA / live;
+    p.red[4 + p.Hkv * p.rep + h] = sA / live;
     gA += sA;
     gD += sD;
     gW += sW;
   }
-  if (threadIdx.x == 0) {
-    const float cnt = static_cast<float>(p.Hkv) * static_cast<float>(p.n);
-    p.red[0] = gA / live / cnt;
-    p.red[1] = gD / live / cnt;
-    p.red[2] = gW / live / cnt;
-    p.red[3] = live;
-  }
+  const float cnt = static_cast<float>(p.Hkv) * static_cast<float>(p.n);
+  p.red[0] = gA / live / cnt;
+  p.red[1] = gD / live / cnt;
+  p.red[2] = gW / live / cnt;
+  p.red[3] = live;
 }
 
 __global__ __launch_bounds__(kCThreads) void cov_final(CovParams p) {
@@ -857,12 +894,12 @@ using namespace kvq;
 // workspace layout (floats): row_m, row_il, oMo, roww (Hkv NR each); o (Hkv NR d); o_part (kOSplit Hkv
 // NR d); vmv (Hkv rep n); ddpart (G Hkv n_chunks); alpha_part (Hkv n_chunks NR); gw (G + 1); red (4 +
 // Hkv rep + Hkv); WVa (Hkv rep n); A_part, DD_part (kTSplit Hkv n each); WVa_part (kTSplit Hkv rep n);
-// mop (Hkv NR 128), rowf (Hkv NR 4), 16-byte aligned
+// mop (Hkv NR 128), rowf (Hkv NR 4), 16-byte aligned; S_part (kSSplit Hkv d d); sums (Hkv (2 + rep))
 extern "C" int64_t kvq_coverage_stats_workspace(int64_t Hkv, int64_t rep, int64_t n, int64_t NR, int64_t G) {
   if (Hkv <= 0 || rep <= 0 || n <= 0 || NR <= 0 || G <= 0) return -1;
   const int64_t nch = (n + kChunkTok - 1) / kChunkTok;
   return 4 * Hkv * NR + (1 + kOSplit) * Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch + Hkv * nch * NR + (G + 1) +
-         (4 + Hkv * rep + Hkv) + Hkv * rep * n + kTSplit * (2 * Hkv * n + Hkv * rep * n) + 132 * Hkv * NR + 4;
+         (4 + Hkv * rep + Hkv) + Hkv * rep * n + kTSplit * (2 * Hkv * n + Hkv * rep * n) + 132 * Hkv * NR + 4 + kSSplit * Hkv * kCD * kCD + Hkv * (2 + rep);
 }
 
 extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const int32_t* rowpos, const int32_t* rowgrp,
@@ -917,7 +954,9 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   p.WVa_part = w; w += kTSplit * Hkv * rep * n;
   w += (4 - (reinterpret_cast<uintptr_t>(w) / 4) % 4) % 4;       // 16-byte alignment of the next two
   p.mop = reinterpret_cast<uint32_t*>(w); w += 128 * Hkv * NR;
-  p.rowf = w;
+  p.rowf = w; w += 4 * Hkv * NR;
+  p.S_part = w; w += kSSplit * Hkv * kCD * kCD;
+  p.sums = w;
   p.A = A; p.W = W; p.DD = DD; p.S = S; p.Mbar = Mbar;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 blk(kCThreads);
@@ -949,10 +988,14 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(weighted terms)");
   hipLaunchKernelGGL(cov_split_sums, dim3((Hkv * rep * n + kCThreads - 1) / kCThreads), blk, 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(split sums)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_smat<DT_>), dim3(Hkv * (kCD / 16)), blk, 0, s, p));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_smat<DT_>), dim3(Hkv * (kCD / 16) * kSSplit), blk, 0, s, p));
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(S parts)");
+  hipLaunchKernelGGL(cov_smat_sum, dim3((Hkv * kCD * kCD + kCThreads - 1) / kCThreads), blk, 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(S)");
-  hipLaunchKernelGGL(cov_final_sums, dim3(1), dim3(1024), 0, s, p);
+  hipLaunchKernelGGL(cov_final_sums, dim3(static_cast<unsigned>(Hkv * (2 + rep))), dim3(1024), 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(sums)");
+  hipLaunchKernelGGL(cov_final_combine, dim3(1), dim3(64), 0, s, p);
+  KVQ_LAUNCH_CHECK("kvq_coverage_stats(combine)");
   const int64_t nmax = std::max<int64_t>(Hkv * n, Hkv * kCD * kCD);
   hipLaunchKernelGGL(cov_final, dim3((nmax + kCThreads - 1) / kCThreads), blk, 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(final)");
