@@ -27,9 +27,12 @@ events on the launch stream (device synchronisation on both sides).  C1/C2 also 
 timed from idle after only the W warm-ups (``cold_ms_per_step``).  The same step captured once in a HIP graph
 (the reference's _time_callable protocol, STRATA_KV.py:3424-3447) is timed too and reported as
 ``graph_us``: on this ROCm stack a replay of a one-step graph costs more than the eager launches.
-The dominant kernel is timed inside K more eager steps of the same sequence, with HIP events
-recorded on the launch stream right before and after each of its launches (``kernel_us``: the
-figure a rocprofv3 kernel-trace average gives; its summary is committed under profiles/).  The
+The dominant kernel's GPU time per launch (``roofline.kernel_us``, the figure a rocprofv3
+kernel-trace average gives; its summary is committed under profiles/) is, where it can run alone
+(C1/C2, C3, C5, QUASAR), K launches of it back to back between HIP events; HIP events recorded on the
+launch stream right before and after each of its launches inside K more eager steps are reported
+beside it (``kernel_us_events``), and for the other workloads they are the kernel figure.  Events
+around one launch also count its dispatch latency, a few µs that matter only for short kernels.  The
 CPU baseline is the oracle's restatement of the reference path on a bounded sample of the same
 workload, scaled to the whole workload, at the box's thread count and at 4 threads; for C1/C2 the
 oracle's outputs of the sampled (b, h) pairs are compared with the GPU step's (``parity``), and a
@@ -139,6 +142,16 @@ def kernel_in_step_ms(kern, steps: int, warmup: int, pre=None, post=None) -> flo
     return sum(a.elapsed_time(b) for a, b in evs) / steps
 
 
+def kernel_alone_ms(kern, steps: int, warmup: int) -> float:
+    """GPU time per launch of the dominant kernel launched alone, K times back to back on the launch
+    stream between HIP events, after a settle phase (each launch recomputes the same partials).  One
+    dispatch queues behind the other, so the figure is the kernel's duration plus the small gap
+    between dispatches: what a rocprofv3 kernel-trace average gives, where events recorded around a
+    single launch inside a step (kernel_in_step_ms) also count that launch's dispatch latency."""
+    settle(kern, SETTLE_MS)
+    return eager_ms(kern, steps, warmup)
+
+
 def eager_ms(fn, steps: int, warmup: int) -> float:
     """Back-to-back launches on the current stream between HIP events, after warm-up."""
     for _ in range(warmup):
@@ -195,11 +208,16 @@ def _result(args, *, metric, value, unit, ms_per_step, workload, config, dtype, 
     return res
 
 
-def _roof(bytes_alg: int, ms: float, kernel: str, traffic=None) -> dict:
+def _roof(bytes_alg: int, ms: float, kernel: str, traffic=None, events_ms=None) -> dict:
+    """``ms``: the kernel's GPU time per launch (kernel_by_difference_ms where the step has other
+    launches to leave out); ``events_ms``: the same kernel bracketed by events in the eager step."""
     achieved = bytes_alg / (ms * 1e-3) / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
-            "kernel_us": round(ms * 1e3, 3), "kernel_bytes_alg": int(bytes_alg)}
+    res = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
+           "kernel_us": round(ms * 1e3, 3), "kernel_bytes_alg": int(bytes_alg)}
+    if events_ms is not None:
+        res["kernel_us_events"] = round(events_ms * 1e3, 3)
+    return res
 
 
 def _traffic(name: str):
@@ -300,7 +318,8 @@ def run_kivi(args, shape_name: str) -> dict:
     # from idle: W warm-up steps, then K timed steps, before the clocks have settled
     cold_ms = eager_ms(step, args.steps, args.warmup)
     ms_per_step, g_ms = step_ms(step, args.steps, args.warmup)
-    split_ms = kernel_in_step_ms(split_only, args.steps, 0, post=merge_only)
+    split_ev_ms = kernel_in_step_ms(split_only, args.steps, 0, post=merge_only)
+    split_ms = kernel_alone_ms(split_only, args.steps, args.warmup)
     step_gpu_ms = graph_k_ms(step, args.steps, args.warmup)
     io_bytes = q.numel() * q.element_size() + out.numel() * out.element_size()
     bytes_alg = cache.payload_bytes() + io_bytes
@@ -322,7 +341,7 @@ def run_kivi(args, shape_name: str) -> dict:
                           "group_k": shape.group_k, "group_v": shape.group_v, "bits": shape.bits,
                           "split_tokens": args.split_tokens},
                   dtype="bf16" if shape.dtype == torch.bfloat16 else "fp32",
-                  roofline=_roof(split_bytes, split_ms, "kivi_decode_split", traffic),
+                  roofline=_roof(split_bytes, split_ms, "kivi_decode_split", traffic, events_ms=split_ev_ms),
                   us_per_layer=round(ms_per_step * 1e3, 3),
                   timer="back-to-back launches, HIP events over the timed steps",
                   settle_ms=SETTLE_MS, cold_ms_per_step=round(cold_ms, 5),
@@ -378,7 +397,8 @@ def run_c3(args) -> dict:
     split = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
     merge = lambda: kvq.mixed_decode(q, scaling, cache, out=out, workspace=ws, phases=2)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
-    split_ms = kernel_in_step_ms(split, args.steps, 0, post=merge)
+    split_ev_ms = kernel_in_step_ms(split, args.steps, 0, post=merge)
+    split_ms = kernel_alone_ms(split, args.steps, args.warmup)
     qb = q.numel() * q.element_size()
     bytes_alg = cache.coded_bytes() + qb + out.numel() * out.element_size()
     avg_bits = float(widths.float().mean())
@@ -388,7 +408,7 @@ def run_c3(args) -> dict:
                            "by LogNormal(0,1) block importance 10/30/60% (B=8, Hq=32, Hkv=8, d=128, T=16384)",
                   config={"global_batch": s.B, "seq_len": s.T, "parallelism": "single GPU", "group": 32,
                           "avg_bits": round(avg_bits, 4), "blocks_8_4_2": [int((widths == w).sum()) for w in (8, 4, 2)]},
-                  dtype="bf16", roofline=_roof(cache.coded_bytes() + qb, split_ms, "mixed_split"),
+                  dtype="bf16", roofline=_roof(cache.coded_bytes() + qb, split_ms, "mixed_split", events_ms=split_ev_ms),
                   us_per_layer=round(ms * 1e3, 3), graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg)
     log(f"C3 step {ms * 1e3:.1f} us, split {split_ms * 1e3:.1f} us")
     if not args.no_cpu_baseline:
@@ -497,7 +517,8 @@ def run_c5(args) -> dict:
     split = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws, phases=1)
     merge = lambda: kvq.dct_decode(q, scaling, cache, out=out, workspace=ws, phases=2)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
-    split_ms = kernel_in_step_ms(split, args.steps, 0, post=merge)
+    split_ev_ms = kernel_in_step_ms(split, args.steps, 0, post=merge)
+    split_ms = kernel_alone_ms(split, args.steps, args.warmup)
     # the encoder: keys and values of the whole context, one launch each
     kc, ks = torch.empty_like(cache.kc), torch.empty_like(cache.ks)
     ctab = kvq.dct_table()
@@ -517,7 +538,7 @@ def run_c5(args) -> dict:
                   workload="C5: one decode step over a blockwise-DCT-coded context (16 of 64 coefficients, 4-bit "
                            "absmax, fp16 scales; B=1, Hq=64, Hkv=8, d=128, T=131072, AR(1) rho=0.95 + N(0,0.1))",
                   config={"global_batch": s.B, "seq_len": s.T, "parallelism": "single GPU", "keep": 16, "block": 64},
-                  dtype="bf16", roofline=_roof(cache.coded_bytes() + qb, split_ms, "dct_split"),
+                  dtype="bf16", roofline=_roof(cache.coded_bytes() + qb, split_ms, "dct_split", events_ms=split_ev_ms),
                   us_per_layer=round(ms * 1e3, 3), graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg,
                   compression_vs_bf16=round(dense / cache.coded_bytes(), 3),
                   encoder={"us": round(enc_ms * 1e3, 3), "bytes": enc_bytes,
@@ -575,8 +596,9 @@ def run_quasar(args) -> dict:
     split = lambda: st.attend(q, scaling, qpos, out=out, phases=2)
     ms, g_ms = step_ms(step, args.steps, args.warmup)
     step_gpu_ms = graph_k_ms(step, args.steps, args.warmup)
-    split_ms = kernel_in_step_ms(split, args.steps, 0, pre=lambda: st.attend(q, scaling, qpos, out=out, phases=1),
-                                 post=lambda: st.attend(q, scaling, qpos, out=out, phases=4))
+    split_ev_ms = kernel_in_step_ms(split, args.steps, 0, pre=lambda: st.attend(q, scaling, qpos, out=out, phases=1),
+                                    post=lambda: st.attend(q, scaling, qpos, out=out, phases=4))
+    split_ms = kernel_alone_ms(split, args.steps, args.warmup)
     codes = sum(s_["flat"].numel() for s_ in st.sides)
     rho = 2 * 2 * Hkv * QUASAR_NC
     exact = 2 * K.numel() * K.element_size()
@@ -592,7 +614,7 @@ def run_quasar(args) -> dict:
                            "bf16 exact rows, synthetic N(0, 1) coefficients",
                   config={"global_batch": 1, "seq_len": QUASAR_CTX, "parallelism": "single GPU", "coded": QUASAR_NC,
                           "exact": QUASAR_N0, "stages": list(stages)},
-                  dtype="bf16", roofline=_roof(bytes_split, split_ms, "quasar_split"),
+                  dtype="bf16", roofline=_roof(bytes_split, split_ms, "quasar_split", events_ms=split_ev_ms),
                   eager_us=round(ms * 1e3, 3), graph_us=round(g_ms * 1e3, 3), bytes_alg=bytes_alg,
                   code_bytes=codes, context_bytes=st.context_bytes(),
                   reference_published_us_64k="4100-39000 (A100-class MIG slice, STRATA_KV.py:30-32)")
@@ -873,7 +895,7 @@ def run_append(args) -> dict:
     g = torch.Generator(device="cuda")
     g.manual_seed(7)
     newk = torch.randn((n_steps + 64, s.B, s.Hkv, 1, s.d), generator=g, device="cuda").to(s.dtype)
-    newv = torch.randn_like(newk)
+    newv = torch.randn(newk.shape, generator=g, device="cuda").to(s.dtype)
     for t in range(64):                                   # warm-up, not timed
         cache.append(newk[t], newv[t])
     torch.cuda.synchronize()
@@ -1094,7 +1116,8 @@ def run_compress(args) -> dict:
     log("generating one Llama-3-8B-shaped layer (queries at every position, keys, values, output metric)")
     g = torch.Generator(device="cuda").manual_seed(47)
     q = torch.randn((B, Hq, H, d), generator=g, device="cuda").to(torch.bfloat16)
-    t3 = torch.distributions.StudentT(3.0).sample((Hkv, 1, d)).abs().clamp(0.2, 8.0).cuda()
+    from kvq.synth import student_t3
+    t3 = student_t3((Hkv, 1, d), g, "cuda").abs().clamp(0.2, 8.0)   # seeded: the same layer every run
     k = (torch.randn((B, Hkv, H, d), generator=g, device="cuda") * t3).to(torch.bfloat16)
     v = torch.randn((B, Hkv, H, d), generator=g, device="cuda").to(torch.bfloat16)
     Wo = torch.randn((Hq, 64, d), generator=g, device="cuda") / 8
