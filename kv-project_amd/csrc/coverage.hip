@@ -389,6 +389,118 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
   }
 }
 
+// v M v of the coded values on the matrix cores (the row outputs' o M stays on cov_metric): per
+// (query head hr = (h, r), kVmvPer values) a workgroup stages that head's metric M transposed in LDS
+// as fp16 hi + lo parts of M x 2^(8 - em) (its largest entry brought to [128, 256)); each wavefront
+// then takes tiles of 16 values, every value row x scaled by its own power of two the same way and
+// split into parts, y = x M by the products hi*hi + hi*lo + lo*hi (fp32 accumulation, about 2^-22
+// relative), and x . y by a row sum with x exchanged through the wavefront's LDS into the layout
+// of the products' output.
+constexpr int kVmvPer = 512;             // values of a cov_vmv workgroup
+constexpr int kMtStride = kCD + 8;       // halves per LDS row of M^T (16-byte aligned rows)
+
+template <int DT>
+__global__ __launch_bounds__(kCThreads) void cov_vmv(CovParams p) {
+  __shared__ __align__(16) uint16_t mt[2][kCD * kMtStride];   // [part][col][k]
+  __shared__ __align__(16) float xs[kCWaves][16][kCD + 4];
+  __shared__ float red[kCWaves];
+  __shared__ int xex[kCWaves][16];
+  const int tiles = (p.n + kVmvPer - 1) / kVmvPer;
+  const int hr = blockIdx.x / tiles, tile = blockIdx.x % tiles;
+  const int h = hr / p.rep;
+  const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
+  // the metric's largest entry over the workgroup, then its transposed parts
+  const float* Mg = p.M + static_cast<int64_t>(hr) * kCD * kCD;
+  constexpr int kPer = kCD * kCD / kCThreads;
+  float mv[kPer];
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    mv[e] = Mg[threadIdx.x + kCThreads * e];
+    mx = fmaxf(mx, fabsf(mv[e]));
+  }
+  mx = wave_max(mx);
+  if (l == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int em = 0;
+  if (mx > 0.0f) (void)frexpf(mx, &em);
+  const float upm = ldexpf(1.0f, 8 - em);
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int idx = threadIdx.x + kCThreads * e, k = idx / kCD, c = idx % kCD;
+    const float x = mv[e] * upm;
+    const _Float16 hi = static_cast<_Float16>(x);
+    const _Float16 lo = static_cast<_Float16>(x - static_cast<float>(hi));
+    mt[0][c * kMtStride + k] = __builtin_bit_cast(uint16_t, hi);
+    mt[1][c * kMtStride + k] = __builtin_bit_cast(uint16_t, lo);
+  }
+  __syncthreads();
+  for (int t0 = 0; t0 < kVmvPer; t0 += 64) {
+    const int j0 = tile * kVmvPer + t0 + 16 * wave;         // this wavefront's 16 values
+    const int j = j0 + n;                                   // lane (g, n): value n, channels 32 ks + 8 g ..
+    float x[4][8];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (j < p.n) {
+        load8<DT>(p.v, static_cast<int64_t>(h) * p.v_sh + static_cast<int64_t>(p.rs + j) * p.v_st + 32 * ks + 8 * g,
+                  x[ks]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[ks][e] = 0.0f;
+      }
+    }
+    float mxv = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mxv = fmaxf(mxv, fabsf(x[ks][e]));
+    mxv = xmax32(xmax16(mxv));                               // over the four lanes of value n
+    int ex = 0;
+    if (mxv > 0.0f) (void)frexpf(mxv, &ex);
+    const float upx = ldexpf(1.0f, 8 - ex);
+    u32x4 xh[4], xl[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      float xs8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xs8[e] = x[ks][e] * upx;
+      f32_parts<KVQ_F16>(xs8, xh[ks], xl[ks]);
+      *reinterpret_cast<float4*>(&xs[wave][n][32 * ks + 8 * g]) = make_float4(xs8[0], xs8[1], xs8[2], xs8[3]);
+      *reinterpret_cast<float4*>(&xs[wave][n][32 * ks + 8 * g + 4]) = make_float4(xs8[4], xs8[5], xs8[6], xs8[7]);
+    }
+    if (g == 0) xex[wave][n] = ex;
+    wave_lds_fence();
+    float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int o = (16 * cb + n) * kMtStride + 32 * ks + 8 * g;
+        const u32x4 bh = *reinterpret_cast<const u32x4*>(&mt[0][o]);
+        const u32x4 bl = *reinterpret_cast<const u32x4*>(&mt[1][o]);
+        acc = mfma(as_half8(xh[ks]), as_half8(bh), acc);
+        acc = mfma(as_half8(xh[ks]), as_half8(bl), acc);
+        acc = mfma(as_half8(xl[ks]), as_half8(bh), acc);
+      }
+      // D lane (g, n) register i: value 4g + i, column 16 cb + n
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dot[i] = __builtin_fmaf(acc[i], xs[wave][4 * g + i][16 * cb + n], dot[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float q = row_sum16(dot[i]);                    // over the 16 columns a lane group holds
+      const int jj = j0 + 4 * g + i;
+      if (n == 0 && jj < p.n) {
+        // x M x = q x 2^(2 ex + em - 24): x and M entered as x 2^(8 - ex) and M 2^(8 - em)
+        p.vmv[static_cast<int64_t>(hr) * p.n + jj] = ldexpf(q, 2 * xex[wave][4 * g + i] + em - 24);
+      }
+    }
+    wave_lds_fence();                                       // xs, xex of this tile are read
+  }
+}
+
 // x M and x M x for 32 vectors per workgroup, M = the metric of query head (h, r) staged in LDS in
 // two halves of 64 rows.  ROWS: the row outputs of query head r (o M replaces o, o M o out);
 // otherwise the coded values (v M v out).  Grid: (h, r, tile of 32 vectors).
@@ -967,9 +1079,8 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   hipLaunchKernelGGL((cov_metric<KVQ_F32, true>), dim3(Hkv * rep * ((n_rlist + kMetricRows - 1) / kMetricRows)), blk,
                      0, s, p, rlist, (int)n_rlist);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(o M)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_metric<DT_, false>),
-                                               dim3(Hkv * rep * ((n + kMetricRows - 1) / kMetricRows)), blk, 0, s, p,
-                                               rlist, (int)n_rlist));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_vmv<DT_>),
+                                               dim3(Hkv * rep * ((n + kVmvPer - 1) / kVmvPer)), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(v M v)");
   const unsigned terms_blocks = xcd_grid(Hkv * p.n_chunks * kTSplit);
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowprep<DT_>), dim3((Hkv * NR + 15) / 16), blk, 0, s, p));
