@@ -254,9 +254,7 @@ __global__ __launch_bounds__(256) void strata_metric_kernel(const float* __restr
 }
 
 // err[bh][t][b] = e^T M e with e = y_hat - y of token t quantised at width bits[b] (the codes of
-// strata_quantize_kernel), M = Mt[bh] read as columns (M^T e gives the same form).  A block holds
-// one bh and kSErrTok tokens, two tokens per wavefront at a time; M staged in LDS once.
-constexpr int kSErrTok = 256;
+// strata_quantize_kernel), M = Mt[bh] read as columns (M^T e gives the same form).
 constexpr int kSMaxBits = 3;
 
 struct ErrWidths {
@@ -265,73 +263,148 @@ struct ErrWidths {
   float step[kSMaxBits];
 };
 
-__global__ __launch_bounds__(256) void strata_err_kernel(const float* __restrict__ y, int64_t n,
-                                                         const float* __restrict__ Mt, ErrWidths w,
-                                                         float* __restrict__ err) {
-  __shared__ float M[kSD * kSD];
-  __shared__ float e_l[4][2][kSMaxBits][kSD];
-  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+// Computed on the matrix cores: a workgroup per (bh, kSErrTok tokens) stages M
+// transposed in LDS as fp16 hi + lo parts of M x 2^(8 - em) (its largest entry brought to [128, 256));
+// each wavefront takes tiles of 16 tokens.  Lane (g, n) holds token n's coordinates 32 ks + 8 g ..;
+// per width it forms e with the codec's arithmetic (rms from the float64 sum of squares and the
+// correctly rounded root, the fp16 scale, IEEE quotient and rint), scales e by a power of two
+// (largest entry to [128, 256)), and y = e M comes from the products hi*hi + hi*lo + lo*hi in fp32
+// (about 2^-22 relative); e . y is a row sum, e exchanged through the wavefront's LDS into the
+// layout of the products' output.
+constexpr int kSErrTok = 512;
+constexpr int kSMtStride = kSD + 8;              // halves per LDS row of M^T (16-byte aligned rows)
+
+__global__ __launch_bounds__(256) void strata_err_mfma(const float* __restrict__ y, int64_t n,
+                                                       const float* __restrict__ Mt, ErrWidths w,
+                                                       float* __restrict__ err) {
+  __shared__ __align__(16) uint16_t mt[2][kSD * kSMtStride];  // [part][col][k]
+  __shared__ __align__(16) float es[4][16][kSD + 4];
+  __shared__ float red[4];
+  __shared__ int eex[4][16];
+  const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, nl = l & 15;
   const int64_t bh = blockIdx.y;
+  // M's largest entry over the workgroup, then its transposed parts
   const float* mg = Mt + bh * kSD * kSD;
-  for (int i = threadIdx.x; i < kSD * kSD; i += 256) M[i] = mg[i];
+  constexpr int kPer = kSD * kSD / 256;
+  float mv[kPer];
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    mv[e] = mg[threadIdx.x + 256 * e];
+    mx = fmaxf(mx, fabsf(mv[e]));
+  }
+  mx = wave_max(mx);
+  if (l == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int em = 0;
+  if (mx > 0.0f) (void)frexpf(mx, &em);
+  const float upm = ldexpf(1.0f, 8 - em);
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int idx = threadIdx.x + 256 * e, k = idx / kSD, c = idx % kSD;
+    const float x = mv[e] * upm;
+    const _Float16 hi = static_cast<_Float16>(x);
+    const _Float16 lo = static_cast<_Float16>(x - static_cast<float>(hi));
+    mt[0][c * kSMtStride + k] = __builtin_bit_cast(uint16_t, hi);
+    mt[1][c * kSMtStride + k] = __builtin_bit_cast(uint16_t, lo);
+  }
   __syncthreads();
   const int64_t t_end = min<int64_t>(n, static_cast<int64_t>(blockIdx.x + 1) * kSErrTok);
-  // two tokens (t, t + 4) per wavefront iteration share each metric read
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * kSErrTok + wave; t < t_end; t += 8) {
-    float e0[2][kSMaxBits], e1[2][kSMaxBits], m0[2][kSMaxBits], m1[2][kSMaxBits];
+  for (int64_t t0 = static_cast<int64_t>(blockIdx.x) * kSErrTok + 16 * wave; t0 < t_end; t0 += 64) {
+    const int64_t t = t0 + nl;                                  // this lane's token
+    float yv[32];
+    const bool ok = t < t_end;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const bool ok = t + 4 * u < t_end;                          // wave-uniform
-      const float* row = y + (bh * n + (ok ? t + 4 * u : t)) * kSD;
-      const float y0 = row[lane], y1 = row[lane + 64];
-      double ss = static_cast<double>(y0) * y0 + static_cast<double>(y1) * y1;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      const float rms = sqrt_rn(static_cast<float>(ss / kSD));
-#pragma unroll
-      for (int b = 0; b < kSMaxBits; ++b) {
-        e0[u][b] = e1[u][b] = m0[u][b] = m1[u][b] = 0.0f;
-        if (b < w.n) {
-          const int bits = w.bits[b];
-          const float sc = fmaxf(as_stored16(__fmul_rn(w.step[b], rms)), kMinScale);
-          const float half = static_cast<float>((1 << bits) - 1) * 0.5f;
-          const float qmax = static_cast<float>((1 << bits) - 1);
-          const float c0 = fminf(fmaxf(rintf(__fadd_rn(__fdiv_rn(y0, sc), half)), 0.0f), qmax);
-          const float c1 = fminf(fmaxf(rintf(__fadd_rn(__fdiv_rn(y1, sc), half)), 0.0f), qmax);
-          e0[u][b] = __fsub_rn(__fmul_rn(__fsub_rn(c0, half), sc), y0);
-          e1[u][b] = __fsub_rn(__fmul_rn(__fsub_rn(c1, half), sc), y1);
-        }
-        e_l[wave][u][b][lane] = e0[u][b];
-        e_l[wave][u][b][lane + 64] = e1[u][b];
-      }
+    for (int ks = 0; ks < 4; ++ks) {
+      const float* row = y + (bh * n + (ok ? t : t0)) * kSD + 32 * ks + 8 * g;
+      const float4 a = *reinterpret_cast<const float4*>(row), b = *reinterpret_cast<const float4*>(row + 4);
+      yv[8 * ks + 0] = a.x; yv[8 * ks + 1] = a.y; yv[8 * ks + 2] = a.z; yv[8 * ks + 3] = a.w;
+      yv[8 * ks + 4] = b.x; yv[8 * ks + 5] = b.y; yv[8 * ks + 6] = b.z; yv[8 * ks + 7] = b.w;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-#pragma unroll 4
-    for (int j = 0; j < kSD; ++j) {                               // (M^T e)_lane, (M^T e)_lane+64
-      const float a0 = M[j * kSD + lane], a1 = M[j * kSD + lane + 64];
+    // the sum of squares in the quantizer's order (leaf j = y[j]^2 + y[j + 64]^2, then pairs j, j ^ 32;
+    // j, j ^ 16; ...; j, j ^ 1), so rms and the fp16 scale are the quantizer's to the bit.  This lane
+    // holds leaves 8 g + e and 8 g + e + 32; leaves 16 apart sit in lanes 32 apart, 8 apart 16.
+    double ps[8];
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int b = 0; b < kSMaxBits; ++b) {
-          const float ej = e_l[wave][u][b][j];
-          m0[u][b] = __builtin_fmaf(a0, ej, m0[u][b]);
-          m1[u][b] = __builtin_fmaf(a1, ej, m1[u][b]);
-        }
+    for (int e = 0; e < 8; ++e) {
+      const double s0 = static_cast<double>(yv[e]) * yv[e] + static_cast<double>(yv[16 + e]) * yv[16 + e];
+      const double s1 = static_cast<double>(yv[8 + e]) * yv[8 + e] + static_cast<double>(yv[24 + e]) * yv[24 + e];
+      ps[e] = s0 + s1;
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int e = 0; e < 8; ++e) ps[e] += __shfl_xor(ps[e], 32, 64);
 #pragma unroll
-      for (int b = 0; b < kSMaxBits; ++b) {
-        float q = __builtin_fmaf(e0[u][b], m0[u][b], e1[u][b] * m1[u][b]);
+    for (int e = 0; e < 8; ++e) ps[e] += __shfl_xor(ps[e], 16, 64);
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
-        if (lane == 0 && b < w.n && t + 4 * u < t_end) err[(bh * n + t + 4 * u) * w.n + b] = q;
+    for (int e = 0; e < 4; ++e) ps[e] += ps[e + 4];
+    const double ss = (ps[0] + ps[2]) + (ps[1] + ps[3]);
+    const float rms = sqrt_rn(static_cast<float>(ss / kSD));
+    float q[kSMaxBits][4];
+#pragma unroll
+    for (int b = 0; b < kSMaxBits; ++b) {
+      if (b >= w.n) continue;                                   // uniform
+      const int bits = w.bits[b];
+      const float sc = fmaxf(as_stored16(__fmul_rn(w.step[b], rms)), kMinScale);
+      const float half = static_cast<float>((1 << bits) - 1) * 0.5f;
+      const float qmax = static_cast<float>((1 << bits) - 1);
+      float ev[32], emx = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        const float c = fminf(fmaxf(rintf(__fadd_rn(__fdiv_rn(yv[k], sc), half)), 0.0f), qmax);
+        ev[k] = __fsub_rn(__fmul_rn(__fsub_rn(c, half), sc), yv[k]);
+        emx = fmaxf(emx, fabsf(ev[k]));
       }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();                              // e_l of these tokens consumed
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      emx = xmax32(xmax16(emx));
+      int ex = 0;
+      if (emx > 0.0f) (void)frexpf(emx, &ex);
+      const float upe = ldexpf(1.0f, 8 - ex);
+      u32x4 eh[4], elo[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        float x8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x8[e] = ev[8 * ks + e] * upe;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const _Float16 h0 = static_cast<_Float16>(x8[2 * e]), h1 = static_cast<_Float16>(x8[2 * e + 1]);
+          eh[ks][e] = pack_h2(h0, h1);
+          elo[ks][e] = pack_h2(static_cast<_Float16>(x8[2 * e] - static_cast<float>(h0)),
+                               static_cast<_Float16>(x8[2 * e + 1] - static_cast<float>(h1)));
+        }
+        *reinterpret_cast<float4*>(&es[wave][nl][32 * ks + 8 * g]) = make_float4(x8[0], x8[1], x8[2], x8[3]);
+        *reinterpret_cast<float4*>(&es[wave][nl][32 * ks + 8 * g + 4]) = make_float4(x8[4], x8[5], x8[6], x8[7]);
+      }
+      if (g == 0) eex[wave][nl] = ex;
+      wave_lds_fence();
+      float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const int o = (16 * cb + nl) * kSMtStride + 32 * ks + 8 * g;
+          const u32x4 bhi = *reinterpret_cast<const u32x4*>(&mt[0][o]);
+          const u32x4 blo = *reinterpret_cast<const u32x4*>(&mt[1][o]);
+          acc = mfma(as_half8(eh[ks]), as_half8(bhi), acc);
+          acc = mfma(as_half8(eh[ks]), as_half8(blo), acc);
+          acc = mfma(as_half8(elo[ks]), as_half8(bhi), acc);
+        }
+        // D lane (g, nl) register i: token 4g + i of the tile, column 16 cb + nl
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dot[i] = __builtin_fmaf(acc[i], es[wave][4 * g + i][16 * cb + nl], dot[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) q[b][i] = ldexpf(row_sum16(dot[i]), 2 * eex[wave][4 * g + i] + em - 24);
+      wave_lds_fence();                                         // es, eex of this width are read
+    }
+    // e^T M e = q x 2^(2 ex + em - 24): e and M entered as e 2^(8 - ex) and M 2^(8 - em)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t tt = t0 + 4 * g + i;
+      if (nl == 0 && tt < t_end)
+        for (int b = 0; b < w.n; ++b) err[(bh * n + tt) * w.n + b] = q[b][i];
+    }
   }
 }
 
@@ -1156,8 +1229,8 @@ extern "C" int kvq_strata_distortion(const float* yk, const float* yv, int64_t H
   hipLaunchKernelGGL(strata_metric_kernel, dim3(static_cast<unsigned>(Hkv)), dim3(256), 0, st, S, signs, mk);
   hipLaunchKernelGGL(strata_metric_kernel, dim3(static_cast<unsigned>(Hkv)), dim3(256), 0, st, Mbar, signs, mv);
   const dim3 eg(static_cast<unsigned>((n + kSErrTok - 1) / kSErrTok), static_cast<unsigned>(Hkv));
-  hipLaunchKernelGGL(strata_err_kernel, eg, dim3(256), 0, st, yk, n, mk, w, ek);
-  hipLaunchKernelGGL(strata_err_kernel, eg, dim3(256), 0, st, yv, n, mv, w, ev);
+  hipLaunchKernelGGL(strata_err_mfma, eg, dim3(256), 0, st, yk, n, mk, w, ek);
+  hipLaunchKernelGGL(strata_err_mfma, eg, dim3(256), 0, st, yv, n, mv, w, ev);
   const int64_t total = Hkv * n;
   hipLaunchKernelGGL(strata_dtable_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 4096))),
                      dim3(256), 0, st, ek, ev, A, W, DD, nbits, total, D);
