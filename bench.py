@@ -812,11 +812,16 @@ def run_c4(args) -> dict:
     torch.cuda.synchronize()
     for t in range(C4_STEPS):
         kvq.kivi_decode(qs[t], scaling, cache, out=out, workspace=ws_s, scores=scores, score_weight=wgt)
-    topk = lambda: kvq.topk_retain(scores, C4_KEEP)
+    # top-k over several workgroups per row (a caller's workspace); one workgroup per row beside it
+    tk_ws = torch.empty(max(1, kvq.topk_workspace_words(s.B * s.Hkv, cache.n_q)), dtype=torch.int32, device="cuda")
+    topk = lambda: kvq.topk_retain(scores, C4_KEEP, workspace=tk_ws)
     topk_ms = eager_ms(topk, args.steps, args.warmup)
-    idx = kvq.topk_retain(scores, C4_KEEP)
+    idx = kvq.topk_retain(scores, C4_KEEP, workspace=tk_ws)
     idx_buf = torch.empty_like(idx)
-    topk_fixed = lambda: kvq.topk_retain(scores, C4_KEEP, out=idx_buf)
+    topk_fixed = lambda: kvq.topk_retain(scores, C4_KEEP, out=idx_buf, workspace=tk_ws)
+    topk_one = lambda: kvq.topk_retain(scores, C4_KEEP, out=idx_buf, split=False)
+    if not torch.equal(idx, kvq.topk_retain(scores, C4_KEEP, split=False)):
+        raise SystemExit("C4: the split top-k and the one-workgroup top-k disagree")
     kept = kvq.retained_cache(cache, idx)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -831,6 +836,7 @@ def run_c4(args) -> dict:
     kept_ms = eager_ms(kept_dec, args.steps, args.warmup)
     kept_gpu_ms = graph_k_ms(kept_dec, args.steps, args.warmup)
     topk_gpu_ms = graph_k_ms(topk_fixed, args.steps, args.warmup)
+    topk_one_gpu_ms = graph_k_ms(topk_one, args.steps, args.warmup)
     n_q, BH = cache.n_q, s.B * s.Hkv
     # the score kernel: the spilled logits (rep rows a token) and the scores row read and written
     score_bytes = BH * n_q * rep * 4 + 2 * BH * n_q * 4
@@ -847,7 +853,7 @@ def run_c4(args) -> dict:
                   scored_step_reread_us=round(reread_ms * 1e3, 3),
                   topk_us=round(topk_ms * 1e3, 3), gather_us_host_timed=round(gather_ms * 1e3, 3),
                   retained_decode_us=round(kept_ms * 1e3, 3), retained_decode_gpu_us=round(kept_gpu_ms * 1e3, 3),
-                  topk_gpu_us=round(topk_gpu_ms * 1e3, 3),
+                  topk_gpu_us=round(topk_gpu_ms * 1e3, 3), topk_one_wg_gpu_us=round(topk_one_gpu_ms * 1e3, 3),
                   episode_ms=round(ep_ms, 4),
                   decode_GBs=round((cache.payload_bytes() + 2 * q0.numel() * 2) / (plain_ms * 1e-3) / 1e9, 2))
     log(f"C4 scored step {scored_ms * 1e3:.1f} us (plain {plain_ms * 1e3:.1f}, score kernel {score_ms * 1e3:.1f}, "

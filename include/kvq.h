@@ -197,6 +197,18 @@ int kvq_kivi_decode_noalloc(const void* q, int q_dtype, int64_t q_sb, int64_t q_
 int kvq_topk_retain(const float* scores, int64_t BH, int64_t n, int64_t scores_bh, int64_t k,
                     int32_t* idx, int64_t idx_bh, void* stream);
 
+/* The same selection (same result, bit for bit) spread over several workgroups per row, for
+ * 4096 < n <= 2^24 and BH <= 65535: slices of 4096 scores, a row histogram, a candidate list and
+ * per-slice output offsets kept in a caller's workspace of kvq_topk_retain_workspace(BH, n) 32-bit
+ * words (256-byte aligned; contents need no clearing; calls sharing it must not overlap in time).
+ * kvq_topk_retain_workspace returns 0 outside that range, and kvq_topk_retain_ws then runs
+ * kvq_topk_retain (the workspace is not used).  Same replaced call as kvq_topk_retain
+ * (STRATA_KV.py:975, 1022-1023). */
+int64_t kvq_topk_retain_workspace(int64_t BH, int64_t n);
+int kvq_topk_retain_ws(const float* scores, int64_t BH, int64_t n, int64_t scores_bh, int64_t k,
+                       int32_t* idx, int64_t idx_bh, uint32_t* workspace, int64_t workspace_words,
+                       void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * A7  SnapKV scores of a prefilled context.  Replaces snapkv_scores (STRATA_KV.py:932-954), the
  * selection of SnapKVMethod.entries (969-981) and of MTLP (1010-1023).

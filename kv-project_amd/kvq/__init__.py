@@ -9,7 +9,7 @@ from .kivi import (kivi_quant, kivi_quant_stored, pack_codes, pack_rows, unpack_
                    v_untile, vmeta_tile)
 from .decode import PackedKIVICache, kivi_decode, score_workspace_floats, workspace_floats
 from .state import DecodeCtl, KIVIState, Router, payload_bytes, register, routed, router_attention
-from .evict import gather_dequant, retained_cache, snapkv_scores, topk_retain
+from .evict import gather_dequant, retained_cache, snapkv_scores, topk_retain, topk_workspace_words
 from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strata_center_rotate, strata_decode,
                      strata_quantize, strata_v_tile, strata_workspace_floats, uniform_step, unpack_planar)
 from .dct import DctCache, dct_decode, dct_encode, dct_table, dct_workspace_floats
@@ -24,7 +24,7 @@ __all__ = [
     "KVQError", "load_library", "kivi_quant", "kivi_quant_stored", "pack_codes", "unpack_codes", "pack_rows", "unpack_rows",
     "v_tile", "v_untile", "vmeta_tile", "PackedKIVICache", "kivi_decode", "workspace_floats", "score_workspace_floats",
     "DecodeCtl", "KIVIState", "Router", "register", "routed", "router_attention",
-    "gather_dequant", "retained_cache", "snapkv_scores", "topk_retain", "pack_planar", "unpack_planar", "rotation_signs",
+    "gather_dequant", "retained_cache", "snapkv_scores", "topk_retain", "topk_workspace_words", "pack_planar", "unpack_planar", "rotation_signs",
     "uniform_step", "strata_center_rotate", "strata_quantize", "strata_v_tile", "StrataCache", "StrataTier",
     "strata_decode", "strata_workspace_floats", "DctCache", "dct_decode", "dct_encode", "dct_table",
     "dct_workspace_floats", "MixedKIVICache", "c3_widths", "mixed_decode", "mixed_workspace_floats", "offset_table",

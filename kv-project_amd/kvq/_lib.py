@@ -49,6 +49,8 @@ SIGNATURES = {
     "kvq_snapkv_scores": (i32, [vp, i32, i64, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64, f32, i32,
                                 vp, vp, i64, vp]),
     "kvq_topk_retain": (i32, [vp, i64, i64, i64, i64, vp, i64, vp]),
+    "kvq_topk_retain_workspace": (i64, [i64, i64]),
+    "kvq_topk_retain_ws": (i32, [vp, i64, i64, i64, i64, vp, i64, vp, i64, vp]),
     "kvq_kivi_gather_dequant": (i32, [vp, vp, vp, vp, vp, i64, i64, i32, i32, i64, i64, vp, i64, i64, vp,
                                       vp, i32, i64, vp]),
     "kvq_pack_planar": (i32, [vp, i64, i64, i32, vp, vp]),

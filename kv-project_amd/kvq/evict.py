@@ -71,10 +71,20 @@ def snapkv_scores(q, k: torch.Tensor, H: int, scaling: float, cfg=None, out: tor
 
 
 @torch.no_grad()
-def topk_retain(scores: torch.Tensor, k: int, out: torch.Tensor | None = None) -> torch.Tensor:
+def topk_workspace_words(rows: int, n: int) -> int:
+    """32-bit words of workspace the split selection needs for ``rows`` rows of n scores (0 when
+    such rows take the one-workgroup kernels: n <= 4096, n > 2^24 or more than 65535 rows)."""
+    return int(_lib.load().kvq_topk_retain_workspace(rows, n))
+
+
+def topk_retain(scores: torch.Tensor, k: int, out: torch.Tensor | None = None, *,
+                workspace: torch.Tensor | None = None, split: bool = True) -> torch.Tensor:
     """scores (..., n) float32 on the GPU -> int32 (..., k): the positions of the k largest scores of
     each row in increasing order (lowest positions kept among scores tied at the k-th).  ``out``: a
-    contiguous int32 (..., k) tensor to write them into."""
+    contiguous int32 (..., k) tensor to write them into.  ``split`` (default) spreads each row over
+    several workgroups (kvq_topk_retain_ws) where topk_workspace_words > 0, with ``workspace`` (a
+    contiguous 32-bit tensor of at least that many elements, 256-byte aligned) or one from torch's
+    allocator; False keeps one workgroup per row (kvq_topk_retain).  Both give the same result."""
     _lib.require_gpu(scores)
     if scores.dtype != torch.float32:
         raise TypeError("scores must be float32")
@@ -90,8 +100,18 @@ def topk_retain(scores: torch.Tensor, k: int, out: torch.Tensor | None = None) -
         if out.dtype != torch.int32 or out.shape != scores.shape[:-1] + (k,) or not out.is_contiguous():
             raise ValueError("out must be a contiguous int32 (..., k) tensor")
         idx = out.view(rows.shape[0], k)
-    _lib.call("kvq_topk_retain", rows.data_ptr(), rows.shape[0], n, rows.stride(0), k, idx.data_ptr(), k,
-              _lib.stream_of(scores))
+    words = topk_workspace_words(rows.shape[0], n) if split else 0
+    if words > 0:
+        if workspace is None:
+            workspace = torch.empty(words, dtype=torch.int32, device=scores.device)
+        elif (workspace.element_size() != 4 or not workspace.is_contiguous() or workspace.numel() < words
+              or workspace.device != scores.device):
+            raise ValueError(f"workspace must be a contiguous 32-bit tensor of >= {words} elements on the scores' device")
+        _lib.call("kvq_topk_retain_ws", rows.data_ptr(), rows.shape[0], n, rows.stride(0), k, idx.data_ptr(), k,
+                  workspace.data_ptr(), workspace.numel(), _lib.stream_of(scores))
+    else:
+        _lib.call("kvq_topk_retain", rows.data_ptr(), rows.shape[0], n, rows.stride(0), k, idx.data_ptr(), k,
+                  _lib.stream_of(scores))
     return idx.reshape(scores.shape[:-1] + (k,))
 
 

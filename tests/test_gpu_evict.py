@@ -24,8 +24,9 @@ from oracle.evict import accumulate_decode_scores, decode_step_probs, topk_retai
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("split", [True, False], ids=["split", "one_wg"])
 @pytest.mark.parametrize("n,k", [(1, 1), (100, 7), (1023, 1023), (1024, 300), (5000, 2048), (65280, 2048)])
-def test_topk_retain_bit_exact(n, k):
+def test_topk_retain_bit_exact(n, k, split):
     import kvq
     rng = np.random.default_rng(n + k)
     rows = np.stack([
@@ -37,13 +38,14 @@ def test_topk_retain_bit_exact(n, k):
         (1.0 + rng.integers(0, 1 << 13, n) * 2.0 ** -23).astype(np.float32),  # span 13 bits
         rng.choice(np.array([-np.inf, np.inf, -3.4e38, 3.4e38, 0.0, 1e-45, -1e-45, 1.0], np.float32), n),
     ])
-    got = kvq.topk_retain(torch.from_numpy(rows).cuda(), k).cpu().numpy()
+    got = kvq.topk_retain(torch.from_numpy(rows).cuda(), k, split=split).cpu().numpy()
     want = topk_retain(rows, k)
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("split", [True, False], ids=["split", "one_wg"])
 @pytest.mark.parametrize("n,k", [(65537, 2048), (131072, 2048)])
-def test_topk_retain_long_rows(n, k):
+def test_topk_retain_long_rows(n, k, split):
     """Rows beyond 65536 scores take the general kernel: distinct, tied-at-the-k-th (planted) and
     equal rows, bit-exact against the full-sort oracle."""
     import kvq
@@ -55,9 +57,33 @@ def test_topk_retain_long_rows(n, k):
     tied[hot[k // 2:]] = 0.75                                           # 2.5k ties straddle the k-th
     c4_like = (rng.lognormal(-11.0, 1.0, n)).astype(np.float32)          # probability-sized scores
     rows = np.stack([distinct, tied, np.full(n, 0.5, np.float32), c4_like])
-    got = kvq.topk_retain(torch.from_numpy(rows).cuda(), k).cpu().numpy()
+    got = kvq.topk_retain(torch.from_numpy(rows).cuda(), k, split=split).cpu().numpy()
     want = topk_retain(rows, k)
     np.testing.assert_array_equal(got, want)
+
+
+def test_topk_retain_split_workspace_reuse_and_strided_rows():
+    """The split selection with one caller workspace over several calls (no clearing between them)
+    on rows read through a stride wider than n, k from 1 to n: bit-exact against the oracle; a
+    workspace one word short is refused."""
+    import kvq
+    rng = np.random.default_rng(7)
+    n, rows_n = 20000, 6
+    wide = np.zeros((rows_n, n + 37), np.float32)
+    wide[:, :n] = rng.lognormal(-9.0, 2.0, (rows_n, n)).astype(np.float32)
+    wide[1, :n] = np.round(wide[1, :n] * 1e4).astype(np.float32)                 # many ties
+    wide[2, rng.choice(n, 50, replace=False)] = np.inf
+    dev = torch.from_numpy(wide).cuda()[:, :n]
+    assert dev.stride(0) == n + 37
+    words = kvq.topk_workspace_words(rows_n, n)
+    assert words > 0
+    ws = torch.empty(words, dtype=torch.int32, device="cuda")
+    for k in (1, 50, 2048, 19999, n):
+        got = kvq.topk_retain(dev, k, workspace=ws).cpu().numpy()
+        np.testing.assert_array_equal(got, topk_retain(wide[:, :n], k))
+    with pytest.raises(ValueError):
+        kvq.topk_retain(dev, 10, workspace=ws[:words - 1])
+    assert kvq.topk_workspace_words(rows_n, 4096) == 0                     # one-workgroup rows
 
 
 def _packed(B, Hkv, T, W, gk, gv, seed, dtype=torch.float32, shift_frac=0.0):
