@@ -95,6 +95,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t key_rsrc(const SnapParams& p, 
   return make_rsrc(base, static_cast<uint32_t>((static_cast<int64_t>(p.H - 1) * p.k_st + 128) * esz));
 }
 
+// the A/B operand registers of key kj (channels 32 ks + 8 g .. + 7 of each k-step); keys past the
+// resource's range read as zeros
+template <int DT>
+__device__ __forceinline__ void load_keys(const __amdgpu_buffer_rsrc_t& rk, const SnapParams& p, int kj, int g,
+                                          u32x4 (&kop)[4][SnapTraits<DT>::NH]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    load_op_buf<DT>(rk, static_cast<int>((static_cast<int64_t>(kj) * p.k_st + 32 * ks + 8 * g) * SnapTraits<DT>::ESZ),
+                    kop[ks]);
+}
+
 template <int DT>
 __global__ __launch_bounds__(kSnapThreads) void snap_stats(SnapParams p) {
   using T = SnapTraits<DT>;
@@ -115,12 +126,7 @@ __global__ __launch_bounds__(kSnapThreads) void snap_stats(SnapParams p) {
   }
   const __amdgpu_buffer_rsrc_t rk = key_rsrc(p, b, h, T::ESZ);
   const int k0 = s * p.split_keys, k1 = min(k0 + p.split_keys, p.H);
-  for (int t0 = k0; t0 < k1; t0 += 16) {
-    u32x4 kop[4][T::NH];
-    const int kj = t0 + n;                                   // this lane's key of the A operand
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      load_op_buf<DT>(rk, static_cast<int>((static_cast<int64_t>(kj) * p.k_st + 32 * ks + 8 * g) * T::ESZ), kop[ks]);
+  auto stat_tile = [&](int t0, const u32x4 (&kop)[4][T::NH]) {
 #pragma unroll
     for (int bw = 0; bw < T::NBW; ++bw) {
       const f32x4 acc = tile_dots<DT, SnapTraits<DT>::NH, SnapTraits<DT>::NH>(kop, qop[bw]);
@@ -140,6 +146,20 @@ __global__ __launch_bounds__(kSnapThreads) void snap_stats(SnapParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) ls[bw] += __builtin_amdgcn_exp2f(sv[i] - m[bw]);
       }
+    }
+  };
+  // two key tiles in registers used in turn: the next tile's loads are issued before the current
+  // one is computed (tiles past the split are loaded -- keys past H read as zeros -- never used)
+  if (k0 < k1) {
+    u32x4 ka[4][T::NH], kb[4][T::NH];
+    load_keys<DT>(rk, p, k0 + n, g, ka);
+    for (int t0 = k0;; t0 += 32) {
+      load_keys<DT>(rk, p, t0 + 16 + n, g, kb);
+      stat_tile(t0, ka);
+      if (t0 + 16 >= k1) break;
+      load_keys<DT>(rk, p, t0 + 32 + n, g, ka);
+      stat_tile(t0 + 16, kb);
+      if (t0 + 32 >= k1) break;
     }
   }
   // the four lanes of a row (xor 16, xor 32) hold disjoint keys of it
@@ -184,38 +204,48 @@ __global__ __launch_bounds__(kSnapThreads) void snap_cols(SnapParams p) {
   u32x4 qop[T::NBW][4][T::NH];
   int rowpos[T::NBW], row[T::NBW];
   load_queries<DT>(p, b, h, rg, wave, g, n, qop, rowpos, row);
-  float rm[T::NBW], ril[T::NBW];
+  // operand roles swapped against snap_stats (A = query rows, B = keys): D lane (g, n) register i
+  // is the logit of row 16 (wave NBW + bw) + 4 g + i against key t0 + n, so a column sum over the
+  // wavefront's rows is a register sum and two cross-lane steps per tile.  Row statistics per
+  // register: the rows of lane group g.
+  float rm[T::NBW][4], ril[T::NBW][4];
 #pragma unroll
   for (int bw = 0; bw < T::NBW; ++bw) {
-    const bool ok = row[bw] < p.rows;
-    rm[bw] = ok ? p.row_m[static_cast<int64_t>(bh) * p.rows + row[bw]] : 0.0f;
-    ril[bw] = ok ? p.row_il[static_cast<int64_t>(bh) * p.rows + row[bw]] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rg * T::RG + (wave * T::NBW + bw) * 16 + 4 * g + i;
+      const bool ok = r < p.rows;
+      rm[bw][i] = ok ? p.row_m[static_cast<int64_t>(bh) * p.rows + r] : 0.0f;
+      ril[bw][i] = ok ? p.row_il[static_cast<int64_t>(bh) * p.rows + r] : 0.0f;
+    }
   }
   const __amdgpu_buffer_rsrc_t rk = key_rsrc(p, b, h, T::ESZ);
   const int nc = p.H - p.w;                 // scored keys: every window row sees all of them
   const int c0 = c * kSnapChunk;
-  for (int tt = 0; tt < kSnapChunk / 16; ++tt) {
+  auto col_tile = [&](int tt, const u32x4 (&kop)[4][T::NH]) {
     const int t0 = c0 + 16 * tt;
-    float colv[4] = {0.f, 0.f, 0.f, 0.f};
+    float colv = 0.0f;
     if (t0 < nc) {
-      u32x4 kop[4][T::NH];
-      const int kj = t0 + n;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        load_op_buf<DT>(rk, static_cast<int>((static_cast<int64_t>(kj) * p.k_st + 32 * ks + 8 * g) * T::ESZ),
-                        kop[ks]);
 #pragma unroll
       for (int bw = 0; bw < T::NBW; ++bw) {
-        const f32x4 acc = tile_dots<DT, SnapTraits<DT>::NH, SnapTraits<DT>::NH>(kop, qop[bw]);
+        const f32x4 acc = tile_dots<DT, SnapTraits<DT>::NH, SnapTraits<DT>::NH>(qop[bw], kop);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) colv[i] += __builtin_amdgcn_exp2f(acc[i] * p.qscale - rm[bw]) * ril[bw];
+        for (int i = 0; i < 4; ++i) colv += __builtin_amdgcn_exp2f(acc[i] * p.qscale - rm[bw][i]) * ril[bw][i];
       }
     }
-    // sum over the 16 rows of the lane group (one per lane of the row of 16)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = row_sum16(colv[i]);
-      if (n == 0) cols[wave][16 * tt + 4 * g + i] = v;
+    // the four lane groups hold disjoint rows of key t0 + n
+    colv = xsum32(xsum16(colv));
+    if (g == 0) cols[wave][16 * tt + n] = colv;
+  };
+  // two key tiles in registers used in turn, the next one's loads issued first
+  {
+    u32x4 ka[4][T::NH], kb[4][T::NH];
+    load_keys<DT>(rk, p, c0 + n, g, ka);
+    for (int tt = 0; tt < kSnapChunk / 16; tt += 2) {
+      load_keys<DT>(rk, p, c0 + 16 * (tt + 1) + n, g, kb);
+      col_tile(tt, ka);
+      if (tt + 2 < kSnapChunk / 16) load_keys<DT>(rk, p, c0 + 16 * (tt + 2) + n, g, ka);
+      col_tile(tt + 1, kb);
     }
   }
   __syncthreads();
