@@ -533,6 +533,18 @@ constexpr int kSWaves = 4;
 constexpr int kMaxTiers = 16;
 
 // One stratum of the launch: its codes, scales and split range [s_base, s_base + n_split).
+// Dispatch-class weights of the strata's splits (see class_block_of): the mixed-width decode's
+// (measured at the C3 shape: 29.6 us per step, against 30.0 with the KIVI decode's 141 : 98 : 68,
+// 30.0 without classes and 30.2 with 125 : 100 : 80)
+#ifndef KVQ_STRATA_CLASS_W
+#define KVQ_STRATA_CLASS_W 165, 95, 55
+#endif
+#ifndef KVQ_STRATA_CLASSES
+#define KVQ_STRATA_CLASSES 1
+#endif
+constexpr int kStrataClassW[3] = {KVQ_STRATA_CLASS_W};
+constexpr int kStrataClassWSum = kStrataClassW[0] + kStrataClassW[1] + kStrataClassW[2];
+
 struct StrataTierArg {
   const uint8_t* kc;            // (BH, n_t, d*bits/8) planar rows
   const uint16_t* ks;           // (BH, cap_t) fp16, zero past n_t
@@ -556,6 +568,7 @@ struct StrataParams {
   float* ws_m;
   float* ws_l;
   int S_all;
+  int split_classes;            // 3: class-major blocks (split sa = 3 j + class), splits sized by class
   ExactArgs ex;                 // exact rows attended in the merge (ex.n > 0)
   const float* ex_o;            // exact-row partials (BH * S_ex partials)
   const float* ex_m;
@@ -657,12 +670,25 @@ __device__ void strata_block(const StrataParams& p, const StrataTierArg& ta, int
   const float qbr = qbias[r_n];
   constexpr float kDotScale = static_cast<float>(1 << (24 - smax_shift<BITS>()));   // dot = D * this
 
-  // ---- this wavefront's chunk range (balanced over the split's 4 wavefronts and all splits) ----
+  // ---- this wavefront's chunk range: the stratum's chunks over its splits' 4 wavefronts each, in
+  // proportion to the splits' dispatch-class weights when the plan has classes (a stratum's splits
+  // then cycle through the classes: split i is of class i % 3), else equally ----
   const int NC = static_cast<int>((ta.n_t + 31) / 32);
-  const int NW = ta.n_split * kSWaves;
-  const int w_all = sidx * kSWaves + wave;
-  const int t0 = 32 * static_cast<int>(static_cast<int64_t>(w_all) * NC / NW);
-  const int t1 = min(32 * static_cast<int>(static_cast<int64_t>(w_all + 1) * NC / NW), static_cast<int>(ta.n_t));
+  int64_t wb0, wb1, wtot;
+  if (p.split_classes > 0) {
+    const int c = sidx % 3;
+    const int64_t before = static_cast<int64_t>(sidx / 3) * kStrataClassWSum + (c > 0 ? kStrataClassW[0] : 0) +
+                           (c > 1 ? kStrataClassW[1] : 0);
+    wb0 = kSWaves * before + static_cast<int64_t>(wave) * kStrataClassW[c];
+    wb1 = wb0 + kStrataClassW[c];
+    wtot = static_cast<int64_t>(kSWaves) * (ta.n_split / 3) * kStrataClassWSum;
+  } else {
+    wb0 = sidx * kSWaves + wave;
+    wb1 = wb0 + 1;
+    wtot = static_cast<int64_t>(ta.n_split) * kSWaves;
+  }
+  const int t0 = 32 * static_cast<int>(wb0 * NC / wtot);
+  const int t1 = min(32 * static_cast<int>(wb1 * NC / wtot), static_cast<int>(ta.n_t));
   const int t_last = t0 < t1 ? t0 + ((t1 - 1 - t0) & ~31) : t0;
 
   const __amdgpu_buffer_rsrc_t rk =
@@ -871,10 +897,19 @@ template <int R, int DT, int W>
 __global__ __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(W)))
 void strata_split_all(StrataParams p) {
   extern __shared__ float smem[];
-  const int k = blockIdx.x / 8;
-  const int bh = blockIdx.x % 8 + 8 * (k / p.S_all);
+  int bh, sa;
+  if (p.split_classes > 0) {
+    // class-major (class_block_of), and the class's j-th split of a (b, h) is split 3 j + class
+    int scm;
+    class_block_of(blockIdx.x, p.S_all, 3, &bh, &scm);
+    const int q = p.S_all / 3;
+    sa = 3 * (scm % q) + scm / q;
+  } else {
+    const int k = blockIdx.x / 8;
+    bh = blockIdx.x % 8 + 8 * (k / p.S_all);
+    sa = k % p.S_all;
+  }
   if (bh >= p.BH) return;
-  const int sa = k % p.S_all;
   int t = 0;
   while (t + 1 < p.n_tiers && sa >= p.tiers[t + 1].s_base) ++t;
   const StrataTierArg& ta = p.tiers[t];
@@ -975,8 +1010,11 @@ inline int strata_pow2(int64_t r) {
 }
 
 // Splits per stratum: about one round of resident blocks (resident_per_cu x 256 CUs) shared in
-// proportion to each stratum's bytes (tokens x (32 bits + 8) B: K and V codes and scales).
-inline void strata_plan(int64_t BH, int n_tiers, const int* tier_bits, const int64_t* tier_n, int* ns) {
+// proportion to each stratum's bytes (tokens x (32 bits + 8) B: K and V codes and scales).  When a
+// round of 3 blocks per CU holds 768 / BH splits per (b, h), a multiple of 3 of them per stratum
+// (each stratum with enough chunks for its splits' wavefronts), the plan has dispatch classes:
+// returns 3 (0 otherwise), with every stratum's split count a multiple of 3.
+inline int strata_plan(int64_t BH, int n_tiers, const int* tier_bits, const int64_t* tier_n, int* ns) {
   double total = 0.0;
   for (int t = 0; t < n_tiers; ++t) total += static_cast<double>(tier_n[t]) * (32 * tier_bits[t] + 8);
   const double target = 256.0 * 3 / static_cast<double>(BH);             // splits per (b, h)
@@ -987,6 +1025,34 @@ inline void strata_plan(int64_t BH, int n_tiers, const int* tier_bits, const int
     s = std::max<int64_t>(1, std::min<int64_t>(s, (nc + kSWaves - 1) / kSWaves));
     ns[t] = tier_n[t] > 0 ? static_cast<int>(s) : 0;
   }
+  if (KVQ_STRATA_CLASSES == 0 || BH <= 0 || BH % 8 != 0 || 768 % BH != 0 || (768 / BH) % 3 != 0 || total <= 0) return 0;
+  // units of 3 splits (one per class): one per stratum with tokens, the rest by largest deficit
+  const int units = static_cast<int>(768 / BH / 3);
+  int alloc[16] = {0}, cap[16] = {0}, used = 0;
+  for (int t = 0; t < n_tiers; ++t) {
+    if (tier_n[t] <= 0) continue;
+    cap[t] = static_cast<int>(((tier_n[t] + 31) / 32 + kSWaves - 1) / kSWaves / 3);   // splits <= ceil(chunks / 4)
+    if (cap[t] < 1) return 0;
+    alloc[t] = 1;
+    ++used;
+  }
+  if (used == 0 || used > units) return 0;
+  for (; used < units; ++used) {
+    int best = -1;
+    double best_d = -1e300;
+    for (int t = 0; t < n_tiers; ++t) {
+      if (alloc[t] == 0 || alloc[t] >= cap[t]) continue;
+      const double d = units * static_cast<double>(tier_n[t]) * (32 * tier_bits[t] + 8) / total - alloc[t];
+      if (d > best_d) {
+        best_d = d;
+        best = t;
+      }
+    }
+    if (best < 0) return 0;
+    ++alloc[best];
+  }
+  for (int t = 0; t < n_tiers; ++t) ns[t] = 3 * alloc[t];
+  return 3;
 }
 
 }  // namespace
@@ -1096,7 +1162,7 @@ extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64
   p.ws_l = p.ws_m + trow;
   p.S_all = S_all;
   int ns[16];
-  strata_plan(B * Hkv, n_tiers, tier_bits, tier_n, ns);
+  p.split_classes = strata_plan(B * Hkv, n_tiers, tier_bits, tier_n, ns);
   // strata with tokens, widest first (their blocks carry the most bytes: dispatched first)
   int base = 0;
   for (int pass_bits : {8, 4, 2}) {
