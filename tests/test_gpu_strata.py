@@ -171,3 +171,23 @@ def test_strata_decode_many_query_tokens():
     ref = _oracle_out(cache, q, K, V, W, d ** -0.5)
     assert out.shape == (B, Tq, Hq, d)
     assert float(np.abs(out - ref).max()) <= 2e-3
+
+
+@pytest.mark.parametrize("B,T,fracs", [(4, 4096, (0.1, 0.3, 0.5)), (4, 2048, (0.01, 0.3, 0.5))])
+def test_strata_decode_class_plan(B, T, fracs):
+    """B 4 x Hkv 8 = 32 (b, h): one round of 3 blocks per CU holds 768 / 32 = 24 splits per (b, h).
+    At T 4096 every stratum has chunks for at least one split per dispatch class (8-bit 403 tokens,
+    4-bit 1210, 2-bit 2016), so the splits are mapped class-major and sized by class weight; at
+    T 2048 with 1% 8-bit tokens (20 tokens, one chunk) the plan falls back to byte-sized splits.
+    Both against the oracle."""
+    import kvq
+    g = torch.Generator().manual_seed(81 + T)
+    Hq, Hkv, W, d = 32, 8, 64, 128
+    K = (torch.randn((B, Hkv, T, d), generator=g) * 1.5 + 0.3).to(torch.bfloat16)
+    V = torch.randn((B, Hkv, T, d), generator=g).to(torch.bfloat16)
+    q = torch.randn((B, Hq, 1, d), generator=g).to(torch.bfloat16)
+    assign = _assign(B, Hkv, T - W, fracs, g)
+    cache = kvq.StrataCache.from_context(K.cuda(), V.cuda(), window=W, assign=assign)
+    out = kvq.strata_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
+    ref = _oracle_out(cache, q, K, V, W, d ** -0.5)
+    assert float(np.abs(out - ref).max()) <= 1e-2
