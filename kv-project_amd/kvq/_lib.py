@@ -146,3 +146,26 @@ def require_gpu(*tensors: torch.Tensor) -> None:
     for t in tensors:
         if t is not None and not t.is_cuda:
             raise KVQError("kvq kernels take GPU tensors only (got a CPU tensor); there is no CPU path")
+
+
+def check_q_cache(q: torch.Tensor, B: int, Hkv: int, d: int, what: str) -> None:
+    """q (B, Hq, Tq, d) must match the cache it attends over: the same batch and head_dim, and a
+    query head count that is a multiple of the cache's KV heads.  The kernels index the cache by
+    q's batch and heads, so a mismatch is refused here rather than read past the cache."""
+    if q.dim() != 4:
+        raise ValueError(f"{what}: q must be (B, Hq, Tq, d), got {tuple(q.shape)}")
+    qb, hq, _, qd = q.shape
+    if qb != B or qd != d or Hkv <= 0 or hq % Hkv != 0:
+        raise ValueError(f"{what}: q {tuple(q.shape)} does not match the cache (batch {B}, {Hkv} KV heads, "
+                         f"head_dim {d})")
+
+
+def out_or_new(out, shape, dtype, device, what: str) -> torch.Tensor:
+    """The caller's output tensor after checking that the kernels can write ``shape`` into it
+    (contiguous, that dtype, that device), or a new one.  The kernels write a dense (B, Tq, Hq, d)
+    block at out's address, so any other tensor is refused."""
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype or not out.is_contiguous() or out.device != device:
+        raise ValueError(f"{what}: out must be a contiguous {tuple(shape)} tensor of {dtype} on {device}")
+    return out

@@ -162,8 +162,12 @@ def coverage_stats(q, k: torch.Tensor, v: torch.Tensor, scaling: float, H: int, 
     need = _lib.load().kvq_coverage_stats_workspace(Hkv, rep, n, plan.NR, G)
     if need < 0:
         raise _lib.KVQError("kvq_coverage_stats_workspace rejected the shape")
-    if workspace is None or workspace.numel() < need:
+    if workspace is None:
         workspace = torch.empty((need,), dtype=torch.float32, device=dev)
+    elif (workspace.numel() < need or workspace.dtype != torch.float32 or not workspace.is_contiguous()
+          or workspace.device != dev):
+        # a caller who preallocated (e.g. for graph capture) gets an error, never a silent allocation
+        raise ValueError(f"workspace must be a contiguous float32 tensor of >= {need} elements on {dev}")
     _lib.call("kvq_coverage_stats", qr.data_ptr(), _lib.DTYPE_CODE[k.dtype], plan.NR, plan.rowpos.data_ptr(),
               plan.rowgrp.data_ptr(), plan.rlist.data_ptr(), plan.n_rlist, plan.gtab.data_ptr(), G,
               plan.items.data_ptr(), plan.items.shape[0], k0.data_ptr(), k0.stride(0), k0.stride(1), v0.data_ptr(),

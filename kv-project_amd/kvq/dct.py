@@ -122,11 +122,12 @@ def dct_decode(q: torch.Tensor, scaling: float, cache: DctCache, *, q_pos: Optio
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.k_exact.shape[1]
+    _lib.check_q_cache(q, cache.k_exact.shape[0], Hkv, cache.k_exact.shape[3], "dct_decode")
     pieces = query_pieces(Hq // Hkv, Tq, chunk)
     if len(pieces) > 1:
         if phases != 3:
             raise ValueError("a chunked query step runs whole steps (phases 3)")
-        return decode_in_pieces(lambda qs, qp: dct_decode(qs, scaling, cache, q_pos=qp, workspace=workspace),
+        return decode_in_pieces(lambda qs, qp, o: dct_decode(qs, scaling, cache, q_pos=qp, out=o, workspace=workspace),
                                 q, q_pos, out, pieces)
     if q.stride(-1) != 1:
         q = q.contiguous()
@@ -134,8 +135,7 @@ def dct_decode(q: torch.Tensor, scaling: float, cache: DctCache, *, q_pos: Optio
         raise TypeError("q and the exact rows must share a dtype")
     if workspace is None:                      # a caller's workspace is size-checked by the library
         workspace = torch.zeros((dct_workspace_floats(B, Hq, Hkv, Tq, d, cache.T, cache.n_exact),), dtype=torch.float32, device=q.device)
-    if out is None:
-        out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
+    out = _lib.out_or_new(out, (B, Tq, Hq, d), q.dtype, q.device, "dct_decode")
     ep = cache.exact_pos if q_pos is not None else None
     qp = q_pos if ep is not None else None
     _lib.call("kvq_dct_decode", q.data_ptr(), _lib.DTYPE_CODE[q.dtype], q.stride(0), q.stride(1), q.stride(2),

@@ -223,26 +223,27 @@ def kivi_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, *,
 
     ``static_scratch``: run through kvq_kivi_decode_noalloc, which keeps the split partials in the
     library's static per-GPU scratch instead of a workspace (no device allocation in the call;
-    pass ``out`` too for a step that allocates nothing).  Steps on one GPU that use it must not
-    overlap in time."""
+    pass ``out`` too for a step that allocates nothing -- a step split into query-token pieces
+    allocates nothing at batch 1, and one staging tensor of a piece's output at a larger batch).
+    Steps on one GPU that use it must not overlap in time."""
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.kc.shape[1]
+    _lib.check_q_cache(q, cache.kc.shape[0], Hkv, cache.kc.shape[3] * 2, "kivi_decode")
     pieces = query_pieces(Hq // Hkv, Tq, chunk)
     if len(pieces) > 1:
         if phases not in (None, 3, 7):
             raise ValueError("a chunked query step runs whole steps (phases 3 or 7)")
         return decode_in_pieces(
-            lambda qs, qp: kivi_decode(qs, scaling, cache, q_pos=qp, workspace=workspace, split_tokens=split_tokens,
-                                       phases=phases, scores=scores, score_weight=score_weight,
-                                       static_scratch=static_scratch),
+            lambda qs, qp, o: kivi_decode(qs, scaling, cache, q_pos=qp, out=o, workspace=workspace,
+                                          split_tokens=split_tokens, phases=phases, scores=scores,
+                                          score_weight=score_weight, static_scratch=static_scratch),
             q, q_pos, out, pieces)
     if q.stride(-1) != 1:
         q = q.contiguous()
     if cache.k_exact.dtype != q.dtype:
         raise TypeError("q and the exact rows must share a dtype")
-    if out is None:
-        out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
+    out = _lib.out_or_new(out, (B, Tq, Hq, d), q.dtype, q.device, "kivi_decode")
     if static_scratch and workspace is not None:
         raise ValueError("static_scratch takes no workspace")
     if workspace is None and not static_scratch:   # a caller's workspace is size-checked by the library

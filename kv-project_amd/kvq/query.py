@@ -34,18 +34,28 @@ def query_pieces(rep: int, Tq: int, chunk: Optional[int] = None) -> List[Tuple[i
     return [(s, min(Tq, s + per)) for s in range(0, Tq, per)]
 
 
-def decode_in_pieces(fn: Callable[[torch.Tensor, Optional[torch.Tensor]], torch.Tensor], q: torch.Tensor,
-                     q_pos: Optional[torch.Tensor], out: Optional[torch.Tensor],
+def decode_in_pieces(fn: Callable[[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor]], torch.Tensor],
+                     q: torch.Tensor, q_pos: Optional[torch.Tensor], out: Optional[torch.Tensor],
                      pieces: List[Tuple[int, int]]) -> torch.Tensor:
-    """Run ``fn(q_piece, q_pos_piece) -> (B, t, Hq, d)`` over the pieces of q (B, Hq, Tq, d) and
-    gather the results into ``out`` (B, Tq, Hq, d), allocated when None.  Launches stay on the
-    current stream in piece order."""
+    """Run ``fn(q_piece, q_pos_piece, out_piece) -> (B, t, Hq, d)`` over the pieces of q (B, Hq, Tq, d)
+    into ``out`` (B, Tq, Hq, d), allocated when None.  With batch 1 a piece's rows of ``out`` are one
+    dense block, so each piece is decoded straight into them and the step allocates nothing beyond
+    what ``fn`` does; with a larger batch they are strided, so the pieces go through one staging
+    tensor of the largest piece's shape (allocated once per call) and are copied over.  Launches
+    stay on the current stream in piece order."""
     B, Hq, Tq, d = q.shape
     if out is None:
         out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
-    elif tuple(out.shape) != (B, Tq, Hq, d):
-        raise ValueError("out must be (B, Tq, Hq, d)")
+    elif tuple(out.shape) != (B, Tq, Hq, d) or not out.is_contiguous() or out.dtype != q.dtype:
+        raise ValueError("out must be a contiguous (B, Tq, Hq, d) tensor of q's dtype")
+    staging = None
+    if B > 1:
+        staging = torch.empty((B * max(e - s for s, e in pieces) * Hq * d,), dtype=q.dtype, device=q.device)
     for s, e in pieces:
-        part = fn(q[:, :, s:e], None if q_pos is None else q_pos[s:e])
-        out[:, s:e].copy_(part)
+        qp = None if q_pos is None else q_pos[s:e]
+        if staging is None:
+            fn(q[:, :, s:e], qp, out[:, s:e])
+        else:
+            part = staging[:B * (e - s) * Hq * d].view(B, e - s, Hq, d)
+            out[:, s:e].copy_(fn(q[:, :, s:e], qp, part))
     return out

@@ -2,7 +2,8 @@
 kvq_kivi_decode with a caller's workspace, through the C ABI: two calls in a row, the second on a
 smaller step (fewer (b, h), a shorter context, a different split plan), each bit-identical to the
 workspace entry point (same kernels, same plan, no atomics).  Then a scored step (phases 7) whose
-accumulated scores are bit-identical too, and a step beyond the scratch, rejected."""
+accumulated scores are bit-identical too, and a query that does not match the cache, rejected on
+the host."""
 import numpy as np
 import pytest
 import torch
@@ -46,8 +47,9 @@ def test_noalloc_scored_step_and_limit():
         got = kvq.kivi_decode(q, 128 ** -0.5, cache, scores=s_got, score_weight=0.25, static_scratch=True)
         assert torch.equal(got, ref)
     assert torch.equal(s_got, s_ref)
-    # a step whose partials exceed the scratch (4096 sequences over this cache's 2 KV heads) is
-    # refused before any launch: the cache is never read
+    # a query whose batch does not match the cache is refused on the host before any launch (the
+    # kernels would index the cache by q's batch); the scratch limit itself is checked on the CPU
+    # with null pointers (test_abi.py::test_noalloc_rejects_steps_beyond_the_static_scratch)
     q = torch.zeros((4096, Hq, 1, 128), device="cuda")
-    with pytest.raises(kvq.KVQError, match="static scratch"):
+    with pytest.raises(ValueError, match="does not match the cache"):
         kvq.kivi_decode(q, 128 ** -0.5, cache, static_scratch=True)
