@@ -11,7 +11,8 @@ from .decode import PackedKIVICache, kivi_decode, score_workspace_floats, worksp
 from .state import DecodeCtl, KIVIState, Router, payload_bytes, register, routed, router_attention
 from .evict import gather_dequant, retained_cache, snapkv_scores, topk_retain, topk_workspace_words
 from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strata_center_rotate, strata_decode,
-                     strata_quantize, strata_v_tile, strata_workspace_floats, uniform_step, unpack_planar)
+                     strata_quantize, strata_quantize_planar, strata_v_tile, strata_workspace_floats, uniform_step,
+                     unpack_planar, unpack_planar_u8)
 from .dct import DctCache, dct_decode, dct_encode, dct_table, dct_workspace_floats
 from .mixed import MixedKIVICache, c3_widths, mixed_decode, mixed_workspace_floats, offset_table
 from .strata_state import StrataState, strata_pack, strata_tier_kernel
@@ -25,7 +26,8 @@ __all__ = [
     "v_tile", "v_untile", "vmeta_tile", "PackedKIVICache", "kivi_decode", "workspace_floats", "score_workspace_floats",
     "DecodeCtl", "KIVIState", "Router", "register", "routed", "router_attention",
     "gather_dequant", "retained_cache", "snapkv_scores", "topk_retain", "topk_workspace_words", "pack_planar", "unpack_planar", "rotation_signs",
-    "uniform_step", "strata_center_rotate", "strata_quantize", "strata_v_tile", "StrataCache", "StrataTier",
+    "uniform_step", "strata_center_rotate", "strata_quantize", "strata_quantize_planar", "unpack_planar_u8",
+    "strata_v_tile", "StrataCache", "StrataTier",
     "strata_decode", "strata_workspace_floats", "DctCache", "dct_decode", "dct_encode", "dct_table",
     "dct_workspace_floats", "MixedKIVICache", "c3_widths", "mixed_decode", "mixed_workspace_floats", "offset_table",
     "StrataState", "strata_pack", "strata_tier_kernel", "QuasarState", "stage_codebooks", "payload_bytes", "AllocWorkspace", "allocate_layer", "layer_costs",

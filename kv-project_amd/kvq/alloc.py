@@ -83,7 +83,7 @@ def strata_distortion(K: torch.Tensor, V: torch.Tensor, A: torch.Tensor, W: torc
     K, V (Hkv, n, 128) the coded rows [rs, re) of one layer (any float dtype); A, W, DD (Hkv, n) and
     S, Mbar (Hkv, 128, 128) float32 as ``coverage_stats`` returns them.  Returns D (Hkv, n,
     len(bits) + 2) float32 [drop | widths | exact] and the centred, rotated rows (mu_k, y_k, mu_v,
-    y_v) the code is then cut from (``kvq.strata_quantize`` with the allocation's order)."""
+    y_v) the code is then cut from (``kvq.strata_quantize_planar`` with the allocation's order)."""
     from .strata import rotation_signs, strata_center_rotate, uniform_step
     _lib.require_gpu(K, V, A, W, DD, S, Mbar)
     Hkv, n, d = K.shape
@@ -101,7 +101,7 @@ def strata_distortion(K: torch.Tensor, V: torch.Tensor, A: torch.Tensor, W: torc
     ws = torch.empty(int(_lib.load().kvq_strata_distortion_workspace(Hkv, n, nb)) // 4 + 1, dtype=torch.float32,
                      device=K.device)
     b_arr = (C.c_int * nb)(*bits)
-    s_arr = (C.c_float * nb)(*[uniform_step(b) for b in bits])
+    s_arr = (C.c_float * nb)(*[uniform_step(b)[0] for b in bits])
     c = lambda t: t.contiguous()
     S_, M_, A_, W_, DD_ = c(S), c(Mbar), c(A), c(W), c(DD)
     _lib.call("kvq_strata_distortion", yk.data_ptr(), yv.data_ptr(), Hkv, n, d, S_.data_ptr(), M_.data_ptr(),

@@ -9,7 +9,7 @@ from __future__ import annotations
 import math
 import zlib
 from functools import lru_cache
-from typing import Optional
+from typing import Optional, Tuple
 
 import numpy as np
 import torch
@@ -32,9 +32,10 @@ def rotation_signs(d: int, key: str = "strata", device="cuda") -> torch.Tensor:
 
 
 @lru_cache(maxsize=None)
-def uniform_step(bits: int) -> float:
-    """Step (in RMS units) of the MSE-optimal mid-rise uniform quantiser of N(0, 1) with 2^bits
-    levels: the reference's golden-section search on a 360001-point grid (STRATA_KV.py:1132-1155)."""
+def uniform_step(bits: int) -> Tuple[float, float]:
+    """(step, mse): the step (in RMS units) of the MSE-optimal mid-rise uniform quantiser of N(0, 1)
+    with 2^bits levels and its mean squared error -- the reference's golden-section search on a
+    360001-point grid (STRATA_KV.py:1132-1155), same return shape."""
     x = np.linspace(-9.0, 9.0, 360001)
     w = np.exp(-0.5 * x * x)
     w /= w.sum()
@@ -48,7 +49,8 @@ def uniform_step(bits: int) -> float:
     for _ in range(200):
         a, b = hi - g * (hi - lo), lo + g * (hi - lo)
         lo, hi = (lo, b) if mse(a) < mse(b) else (a, hi)
-    return 0.5 * (lo + hi)
+    step = 0.5 * (lo + hi)
+    return step, mse(step)
 
 
 @torch.no_grad()
@@ -64,7 +66,14 @@ def pack_planar(codes: torch.Tensor, bits: int) -> torch.Tensor:
 
 @torch.no_grad()
 def unpack_planar(packed: torch.Tensor, bits: int) -> torch.Tensor:
-    """Inverse of pack_planar (STRATA_KV.py:1185-1189), uint8 codes."""
+    """Inverse of pack_planar (STRATA_KV.py:1185-1189): (..., d*bits/8) uint8 -> (..., d) int32 codes,
+    the reference's return type."""
+    return unpack_planar_u8(packed, bits).to(torch.int32)
+
+
+@torch.no_grad()
+def unpack_planar_u8(packed: torch.Tensor, bits: int) -> torch.Tensor:
+    """unpack_planar with the codes left as uint8 (the library's output, one byte per code)."""
     _lib.require_gpu(packed)
     d = packed.shape[-1] * 8 // bits
     p = packed.reshape(-1, packed.shape[-1]).contiguous()
@@ -88,9 +97,27 @@ def strata_center_rotate(x: torch.Tensor, signs: Optional[torch.Tensor] = None):
 
 
 @torch.no_grad()
-def strata_quantize(y: torch.Tensor, bits: int, idx: Optional[torch.Tensor] = None):
+def strata_quantize(Y: torch.Tensor, bits: int):
+    """Drop-in for strata_quantize (STRATA_KV.py:1158-1168): rotated, centred vectors Y (..., 128) on
+    the GPU -> (codes uint8 (..., 128), s (...), y_hat (..., 128)), s the fp16-stored scale and
+    y_hat = s (c - (2^bits - 1) / 2), both in float32 (the library quantises float32 rows; Y of
+    another dtype is converted first).  The codes and scales come from kvq_strata_quantize, the
+    kernel the compressor uses (planar form: ``strata_quantize_planar``)."""
+    _lib.require_gpu(Y)
+    d = Y.shape[-1]
+    y = Y.reshape(1, 1, -1, d).to(torch.float32)
+    planar, s16 = strata_quantize_planar(y, bits)
+    codes = unpack_planar_u8(planar, bits).reshape(Y.shape)
+    s = s16.float().reshape(Y.shape[:-1])
+    y_hat = (codes.float() - (2 ** bits - 1) / 2.0) * s[..., None]
+    return codes, s, y_hat
+
+
+@torch.no_grad()
+def strata_quantize_planar(y: torch.Tensor, bits: int, idx: Optional[torch.Tensor] = None):
     """Rotated rows y (B, Hkv, n, d) float32 (rows idx (B, Hkv, m) int32 if given) -> (planar codes
-    (B, Hkv, m, d*bits/8) uint8, scales (B, Hkv, m) fp16), STRATA_KV.py:1158-1168."""
+    (B, Hkv, m, d*bits/8) uint8, scales (B, Hkv, m) fp16): strata_quantize (STRATA_KV.py:1158-1168)
+    followed by pack_planar (1171-1182), the stored form of a stratum, in one launch."""
     _lib.require_gpu(y)
     B, H, n, d = y.shape
     y = y.contiguous()
@@ -101,7 +128,7 @@ def strata_quantize(y: torch.Tensor, bits: int, idx: Optional[torch.Tensor] = No
     m = n if idx is None else idx.shape[2]
     codes = torch.empty((B, H, m, d * bits // 8), dtype=torch.uint8, device=y.device)
     scales = torch.empty((B, H, m), dtype=torch.float16, device=y.device)
-    _lib.call("kvq_strata_quantize", y.data_ptr(), B * H, n, d, _lib.ptr(idx), m, bits, uniform_step(bits),
+    _lib.call("kvq_strata_quantize", y.data_ptr(), B * H, n, d, _lib.ptr(idx), m, bits, uniform_step(bits)[0],
               codes.data_ptr(), scales.data_ptr(), _lib.stream_of(y))
     return codes, scales
 
@@ -172,8 +199,8 @@ class StrataCache:
         for bits, idx in assign:
             idx = idx.to(device=K.device, dtype=torch.int32)
             m = idx.shape[2]
-            kc, ks = strata_quantize(yk, bits, idx)
-            vc, vs = strata_quantize(yv, bits, idx)
+            kc, ks = strata_quantize_planar(yk, bits, idx)
+            vc, vs = strata_quantize_planar(yv, bits, idx)
             cap = max(32, -(-m // 32) * 32)
             vt, vsl = strata_v_tile(vc, vs, bits, cap)
             ksp = torch.zeros((B, H, cap), dtype=torch.float16, device=K.device)
@@ -218,9 +245,10 @@ def strata_decode(q: torch.Tensor, scaling: float, cache: StrataCache, *, q_pos:
     _lib.require_gpu(q)
     B, Hq, Tq, d = q.shape
     Hkv = cache.k_exact.shape[1]
+    _lib.check_q_cache(q, cache.k_exact.shape[0], Hkv, cache.k_exact.shape[3], "strata_decode")
     pieces = query_pieces(Hq // Hkv, Tq, chunk)
     if len(pieces) > 1:
-        return decode_in_pieces(lambda qs, qp: strata_decode(qs, scaling, cache, q_pos=qp, workspace=workspace),
+        return decode_in_pieces(lambda qs, qp, o: strata_decode(qs, scaling, cache, q_pos=qp, out=o, workspace=workspace),
                                 q, q_pos, out, pieces)
     if q.stride(-1) != 1:
         q = q.contiguous()
@@ -231,8 +259,7 @@ def strata_decode(q: torch.Tensor, scaling: float, cache: StrataCache, *, q_pos:
     if workspace is None:                      # a caller's workspace is size-checked by the library
         need = strata_workspace_floats(B, Hq, Hkv, Tq, d, cache.n_exact, [t.n for t in tiers], [t.bits for t in tiers])
         workspace = torch.zeros((need,), dtype=torch.float32, device=q.device)
-    if out is None:
-        out = torch.empty((B, Tq, Hq, d), dtype=q.dtype, device=q.device)
+    out = _lib.out_or_new(out, (B, Tq, Hq, d), q.dtype, q.device, "strata_decode")
     P = ctypes.c_void_p
     bits = (ctypes.c_int * max(1, nt))(*[t.bits for t in tiers])
     tn = (ctypes.c_int64 * max(1, nt))(*[t.n for t in tiers])

@@ -14,7 +14,7 @@ Reference (STRATA_KV.py, StrataMethod):
 Every step with arithmetic runs on the GPU: ``kvq.coverage_stats`` (kvq_coverage_stats),
 ``kvq.strata_distortion`` (centring, rotation, metrics, per-width errors, D), ``kvq.allocate_layer``
 (kvq_strata_allocate: order, head sum, Lagrangian search, lev, histogram, distortion ratio) and
-``kvq.strata_quantize`` + planar packing of each stratum's rows (the order's rows of that width).
+``kvq.strata_quantize_planar`` (quantise + planar packing) of each stratum's rows (the order's rows of that width).
 The one host synchronisation is the histogram's, as in the reference (1571).  Batch 1, as the
 reference's compression (1533).
 """
@@ -26,7 +26,7 @@ import torch
 
 from .alloc import AllocWorkspace, allocate_layer, strata_distortion
 from .coverage import coverage_stats
-from .strata import rotation_signs, strata_quantize
+from .strata import rotation_signs, strata_quantize_planar
 from .strata_state import StrataState, _tensor_bytes
 
 # the Config fields compress_layer reads beyond coverage_stats', with the reference's defaults
@@ -118,7 +118,7 @@ class StrataCompressor:
             b = self.bits[o - 1]
             t = {"bits": b, "n": m}
             for s, nm in ((0, "k"), (1, "v")):
-                codes, scales = strata_quantize(al["y"][s][None], b, idx)
+                codes, scales = strata_quantize_planar(al["y"][s][None], b, idx)
                 t[f"{nm}c"], t[f"{nm}s"] = codes[0], scales[0]
             tiers.append(t)
         out = {"tiers": tiers, "counts": torch.tensor(al["counts"], dtype=torch.int32), "n_c": al["n_c"]}

@@ -29,7 +29,10 @@ def test_strata_codec_against_reference_vectors():
     assert np.abs(Yg - Y).max() <= 1e-6 * np.abs(Y).max()
     for b in (2, 4, 8):
         for y in (torch.from_numpy(Y)[None].cuda(), Y_g):
-            codes, scales = kvq.strata_quantize(y, b)
+            codes, scales = kvq.strata_quantize_planar(y, b)
             got = kvq.unpack_planar(codes, b)[0].cpu().numpy()
             np.testing.assert_array_equal(got, z[f"codes_{b}"])
             np.testing.assert_array_equal(scales[0].float().cpu().numpy(), z[f"scales_{b}"])
+            c_r, s_r, _ = kvq.strata_quantize(y[0], b)                     # the reference's call shape
+            np.testing.assert_array_equal(c_r.cpu().numpy(), z[f"codes_{b}"])
+            np.testing.assert_array_equal(s_r.cpu().numpy(), z[f"scales_{b}"])

@@ -24,8 +24,9 @@ def test_planar_pack_unpack(bits):
     codes = rng.integers(0, 2 ** bits, (3, 37, 128)).astype(np.uint8)
     packed = kvq.pack_planar(torch.from_numpy(codes).cuda(), bits).cpu().numpy()
     np.testing.assert_array_equal(packed, os_.pack_planar(codes, bits))
-    back = kvq.unpack_planar(torch.from_numpy(packed).cuda(), bits).cpu().numpy()
-    np.testing.assert_array_equal(back, codes)
+    back = kvq.unpack_planar(torch.from_numpy(packed).cuda(), bits)
+    assert back.dtype == torch.int32                         # the reference's return type
+    np.testing.assert_array_equal(back.cpu().numpy(), codes)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -40,13 +41,19 @@ def test_center_rotate_and_quantize_bit_exact(dtype):
     np.testing.assert_array_equal(mu.float().cpu().numpy().reshape(B * H, d), mu_o)
     np.testing.assert_array_equal(y.cpu().numpy().reshape(B * H, n, d), y_o)
     for bits in (2, 4, 8):
-        assert kvq.uniform_step(bits) == os_.uniform_step(bits)[0]
-        codes, sc = kvq.strata_quantize(y, bits)
-        c_o, s_o, _ = os_.strata_quantize(y_o, bits, os_.uniform_step(bits)[0])
+        assert kvq.uniform_step(bits) == os_.uniform_step(bits)            # (step, mse)
+        codes, sc = kvq.strata_quantize_planar(y, bits)
+        c_o, s_o, yh_o = os_.strata_quantize(y_o, bits, os_.uniform_step(bits)[0])
         np.testing.assert_array_equal(codes.cpu().numpy().reshape(B * H, n, -1), os_.pack_planar(c_o, bits))
         np.testing.assert_array_equal(sc.float().cpu().numpy().reshape(B * H, n), s_o)
+        # the reference's call shape: (codes uint8 (..., d), s (...), y_hat (..., d)) of any leading shape
+        c_r, s_r, yh_r = kvq.strata_quantize(y[1], bits)
+        assert c_r.dtype == torch.uint8 and tuple(c_r.shape) == (H, n, d) and tuple(s_r.shape) == (H, n)
+        np.testing.assert_array_equal(c_r.cpu().numpy(), c_o.reshape(B, H, n, d)[1])
+        np.testing.assert_array_equal(s_r.cpu().numpy(), s_o.reshape(B, H, n)[1])
+        np.testing.assert_array_equal(yh_r.cpu().numpy(), yh_o.reshape(B, H, n, d)[1])
         idx = torch.stack([torch.randperm(n, generator=g)[:50] for _ in range(B * H)]).reshape(B, H, 50)
-        cg, sg = kvq.strata_quantize(y, bits, idx.cuda())
+        cg, sg = kvq.strata_quantize_planar(y, bits, idx.cuda())
         ii = idx.numpy().reshape(B * H, 50)
         want = os_.pack_planar(np.take_along_axis(c_o, ii[..., None], 1), bits)
         np.testing.assert_array_equal(cg.cpu().numpy().reshape(B * H, 50, -1), want)
@@ -61,7 +68,7 @@ def test_quantize_scales_at_fp16_ties(bits):
     from midpoint_rows import midpoint_rows
     step = os_.uniform_step(bits)[0]
     Y = midpoint_rows(bits, 4096, seed=100 + bits, step=step).reshape(2, 2, 1024, 128)
-    codes, sc = kvq.strata_quantize(torch.from_numpy(Y).cuda(), bits)
+    codes, sc = kvq.strata_quantize_planar(torch.from_numpy(Y).cuda(), bits)
     c_o, s_o, _ = os_.strata_quantize(Y.reshape(4, 1024, 128), bits, step)
     got = sc.float().cpu().numpy().reshape(4, 1024)
     assert np.array_equal(got, s_o), f"{int((got != s_o).sum())} of 4096 scales differ"
