@@ -8,7 +8,8 @@ bits, level offset] (1883-1898).  ``attend`` reads only those bytes: the query i
 head's coefficient space once (q T_K), every K step adds q~[band] . level[code] for the tokens
 owning it, one softmax covers exact rows and coded tokens, and the coded tokens' weighted levels
 are lifted back once (acc T_V^T + P mu_V).  The kernel path is the only path; ``reference_attend``
-(the reference's per-step torch formulation on the same GPU tensors) exists for ``check_kernel``.
+(dense attention over the stored code decoded back to rows, ``reconstruct``) exists for
+``check_kernel``.
 """
 from __future__ import annotations
 
@@ -246,7 +247,7 @@ class QuasarState:
             qp_all = torch.as_tensor(qpos, dtype=torch.int64).reshape(-1)
             if qp_all.numel() != Tq:
                 raise ValueError("qpos needs one position per query row")
-            return decode_in_pieces(lambda qs, qp: self.attend(qs, scaling, qp), q, qp_all, out, pieces)
+            return decode_in_pieces(lambda qs, qp, o: self.attend(qs, scaling, qp, out=o), q, qp_all, out, pieces)
         if q.dtype != self.dtype:
             q = q.to(self.dtype)
         if q.stride(-1) != 1:
@@ -256,8 +257,7 @@ class QuasarState:
         if qp.numel() != Tq:
             raise ValueError("qpos needs one position per query row")
         ws = self._workspace(Hq, Tq)
-        if out is None:
-            out = torch.empty((1, Tq, Hq, d), dtype=q.dtype, device=q.device)
+        out = _lib.out_or_new(out, (1, Tq, Hq, d), q.dtype, q.device, "QuasarState.attend")
         coded = self.n_c > 0
         k_s, v_s = (self.sides[0], self.sides[1]) if coded else ({}, {})
         P = _lib.ptr
@@ -277,49 +277,48 @@ class QuasarState:
         return out
 
     @torch.no_grad()
+    def reconstruct(self):
+        """The coded tokens decoded back to key and value rows, float32 (Hkv, n_c, d): each side's
+        coefficients summed over the steps that own a token (every step's pack_rows bytes read through
+        its stage's level table, kvq.unpack_rows), then lifted out of the coefficient basis, x = rho c T^T
+        + mu -- the rows whose attention the compressed-domain decode computes (QUASAR_KV.py:1952-1966)."""
+        from .kivi import unpack_rows
+        Hkv, d = self.K.shape[1], self.K.shape[-1]
+        dev = self.K.device
+        if self.n_c == 0:
+            z = torch.zeros((Hkv, 0, d), device=dev)
+            return z, z.clone()
+        books = [torch.from_numpy(x).to(dev) for x in stage_codebooks(self.stages)]
+        rows = []
+        for side, T, rho, mu in ((0, self.T_k, self.rho_k, self.mu_k), (1, self.T_v, self.rho_v, self.mu_v)):
+            coef = torch.zeros((Hkv, self.n_c, T.shape[-1]), device=dev)
+            for st in self.p["steps"]:
+                if st["side"] != side or int(st["n"]) == 0:
+                    continue
+                b = self.stages[st["stage"]]
+                lv = unpack_rows(torch.as_tensor(st["codes"]).to(dev), b, books[st["stage"]])   # (Hkv, n_s, w)
+                coef[:, :int(st["n"]), st["a"]:st["b"]] += lv
+            rows.append(rho.float()[..., None] * torch.matmul(coef, T.transpose(-1, -2)) + mu[:, None, :])
+        return rows[0], rows[1]
+
+    @torch.no_grad()
     def reference_attend(self, q: torch.Tensor, scaling: float, qpos) -> torch.Tensor:
-        """The reference's torch formulation (QUASAR_KV.py:1920-1968, use_kernel False) on the
-        same GPU tensors, in float32: one byte-table gather and one matmul per step."""
+        """The gate check_kernel holds the kernel to: one dense float32 softmax over the exact rows
+        (appended ones causal) and the coded tokens' reconstructed rows (``reconstruct``) -- the
+        attention the compressed-domain decode must reproduce."""
         B, Hq, Tq, d = q.shape
         Hkv = self.K.shape[1]
         rep = Hq // Hkv
-        qg = q.reshape(B, Hkv, rep * Tq, d).float()
-        n = self.n
-        s_ex = (qg @ self.K[:, :, :n].float().transpose(-1, -2)) * scaling
-        if n > self.n0:
-            row_pos = self.H + torch.arange(n - self.n0, device=q.device)
-            bad = row_pos[None, :] > torch.as_tensor(qpos, device=q.device).reshape(-1)[:, None]
-            s_ex[..., self.n0:] = s_ex[..., self.n0:].masked_fill(bad.repeat(rep, 1), float("-inf"))
-        if self.n_c == 0:
-            att = s_ex.softmax(-1)
-            o = att @ self.V[:, :, :n].float()
-            return o.reshape(B, Hq, Tq, d).transpose(1, 2).to(q.dtype).contiguous()
-        books = stage_codebooks(self.stages)
-        luts = []
-        for t, b in enumerate(self.stages):
-            per = 8 // b
-            byte = torch.arange(256)[:, None]
-            sh = (per - 1 - torch.arange(per))[None, :] * b
-            luts.append(torch.from_numpy(books[t])[(byte >> sh) & ((1 << b) - 1)].to(q.device))
-        def deq(st):
-            x = luts[st["stage"]][torch.as_tensor(st["codes"]).to(q.device).long()]
-            return x.reshape(x.shape[0], x.shape[1], st["b"] - st["a"])
-        qt = qg @ self.T_k
-        sc = torch.zeros((B, Hkv, rep * Tq, self.n_c), device=q.device)
-        for st in self.p["steps"]:
-            if st["side"] == 0:
-                sc[..., :st["n"]] += qt[..., st["a"]:st["b"]] @ deq(st).transpose(-1, -2)
-        sc = (sc * self.rho_k.float()[:, None, :] + (qg @ self.mu_k[..., None])) * scaling
-        att = torch.cat([s_ex, sc], -1).softmax(-1)
-        o = att[..., :n] @ self.V[:, :, :n].float()
-        pc = att[..., n:]
-        pv = pc * self.rho_v.float()[:, None, :]
-        acc = torch.zeros((B, Hkv, rep * Tq, self.T_v.shape[-1]), device=q.device)
-        for st in self.p["steps"]:
-            if st["side"] == 1:
-                acc[..., st["a"]:st["b"]] += pv[..., :st["n"]] @ deq(st)
-        o = o + acc @ self.T_v.transpose(-1, -2) + pc.sum(-1, keepdim=True) * self.mu_v[:, None, :]
-        return o.reshape(B, Hq, Tq, d).transpose(1, 2).to(q.dtype).contiguous()
+        qp = torch.as_tensor(qpos, device=q.device).reshape(-1)
+        kr, vr = self.reconstruct()
+        keys = torch.cat([self.K[0, :, :self.n].float(), kr], 1)          # (Hkv, n + n_c, d)
+        vals = torch.cat([self.V[0, :, :self.n].float(), vr], 1)
+        vis = torch.cat([self.exact_pos[None, :self.n] <= qp[:, None],
+                         torch.ones((Tq, kr.shape[1]), dtype=torch.bool, device=q.device)], 1)
+        qg = q[0].float().reshape(Hkv, rep, Tq, d)
+        s = torch.matmul(qg, keys[:, None].transpose(-1, -2)) * scaling
+        o = torch.matmul(s.masked_fill(~vis, float("-inf")).softmax(-1), vals[:, None])
+        return o.reshape(Hq, Tq, d).transpose(0, 1)[None].to(q.dtype).contiguous()
 
     @torch.no_grad()
     def check_kernel(self, tol: float = 2e-2) -> Dict:

@@ -209,51 +209,55 @@ class StrataState:
         return strata_decode(q.to(self.dtype), scaling, self.cache, q_pos=qp, chunk=chunk).to(q.dtype)
 
     @torch.no_grad()
+    def reconstruct(self, b: int = 0):
+        """The coded tokens of sequence b decoded back to key and value rows, float32 (Hkv, n_c, d):
+        every stratum's stored code read through unpack_planar and its per-vector scales, then taken
+        out of the rotated basis and re-centred, x = s (c - (2^bits - 1) / 2) R + mu (the inverse of
+        compress_layer's Y = (X - mu) R^T, STRATA_KV.py:1546-1548).  Strata in storage order."""
+        p, d = self.p, self.K.shape[-1]
+        Hkv = self.K.shape[1]
+        if p is None or not p["n_c"]:
+            z = torch.zeros((Hkv, 0, d), device=self.K.device)
+            return z, z.clone()
+        one = lambda x: x if x.dim() == (3 if x.dtype == torch.uint8 else 2) else x[b]
+        Rf = self.R.float().to(self.K.device)
+        mu_k = (p["mu_k"] if p["mu_k"].dim() == 2 else p["mu_k"][b]).float().to(self.K.device)
+        mu_v = (p["mu_v"] if p["mu_v"].dim() == 2 else p["mu_v"][b]).float().to(self.K.device)
+        ks_rows, vs_rows = [], []
+        for t in p["tiers"]:
+            n, bits = int(t["n"]), int(t["bits"])
+            if n == 0:
+                continue
+            mid = (2 ** bits - 1) / 2.0
+            for src, scale, mu, acc in ((t["kc"], t["ks"], mu_k, ks_rows), (t["vc"], t["vs"], mu_v, vs_rows)):
+                codes = unpack_planar(one(src).to(self.K.device), bits).float()            # (Hkv, n, d)
+                y = (codes - mid) * one(torch.as_tensor(scale)).to(self.K.device).float()[..., None]
+                acc.append(y @ Rf + mu[:, None, :])
+        return torch.cat(ks_rows, 1), torch.cat(vs_rows, 1)
+
+    @torch.no_grad()
     def reference_attend(self, q: torch.Tensor, scaling: float, qpos) -> torch.Tensor:
-        """The reference's torch path (tier_reference + merge, STRATA_KV.py:1751-1795) in float32 on
-        the same GPU tensors, batch by batch (for check_kernel)."""
+        """The gate check_kernel holds the kernel to: one dense float32 softmax, per sequence, over the
+        exact rows (appended ones causal) and the coded tokens' reconstructed rows (``reconstruct``).
+        The reference's decode identity (STRATA_KV.py:1983-1985) states that its compressed-domain
+        decode equals attention over the reconstruction; this computes the right-hand side."""
         B, Hq, Tq, d = q.shape
         Hkv = self.K.shape[1]
         rep = Hq // Hkv
-        outs = []
         qp = torch.as_tensor(qpos, device=q.device).reshape(-1)
-        Rf = self.R.float().to(q.device)
+        pos = self.exact_pos[:self.n]                                   # (n,) -2^62 for the first n0
+        outs = []
         for b in range(B):
-            qg = q[b].reshape(Hkv, rep * Tq, d).float()
-            n = self.n
-            s_ex = (qg @ self.K[b, :, :n].float().transpose(-1, -2)) * scaling
-            if n > self.n0:
-                row_pos = self.H + torch.arange(n - self.n0, device=q.device)
-                bad = row_pos[None, :] > qp[:, None]
-                s_ex[..., self.n0:] = s_ex[..., self.n0:].masked_fill(bad.repeat(rep, 1), float("-inf"))
-            m_e = s_ex.amax(-1)
-            e_ex = (s_ex - m_e[..., None]).exp()
-            l_e = e_ex.sum(-1)
-            o = e_ex @ self.V[b, :, :n].float()
-            p = self.p
-            if p is not None and p["n_c"]:
-                mu_k = (p["mu_k"] if p["mu_k"].dim() == 2 else p["mu_k"][b]).float().to(q.device)
-                mu_v = (p["mu_v"] if p["mu_v"].dim() == 2 else p["mu_v"][b]).float().to(q.device)
-                qr = (qg @ Rf.T) * scaling
-                qb = (qg @ mu_k[..., None])[..., 0] * scaling
-                parts = []
-                for t in p["tiers"]:
-                    half = (2 ** t["bits"] - 1) / 2.0
-                    sel = (lambda x: x if x.dim() == 2 + (x.dtype == torch.uint8) else x[b])
-                    kc, vc, ks, vs = sel(t["kc"]), sel(t["vc"]), sel(t["ks"]), sel(t["vs"])
-                    kh = (unpack_planar(kc, t["bits"]).float() - half) * ks.float()[..., None]
-                    vh = (unpack_planar(vc, t["bits"]).float() - half) * vs.float()[..., None]
-                    s = qr @ kh.transpose(-1, -2) + qb[..., None]
-                    mt = s.amax(-1)
-                    e = (s - mt[..., None]).exp()
-                    parts.append((mt, e.sum(-1), e @ vh))
-                M = torch.maximum(m_e, torch.stack([x[0] for x in parts]).amax(0))
-                we = (m_e - M).exp()
-                accr = sum((x[0] - M).exp()[..., None] * x[2] for x in parts)
-                wl = sum((x[0] - M).exp() * x[1] for x in parts)
-                o = (we[..., None] * o + accr @ Rf + wl[..., None] * mu_v[:, None, :]) / (we * l_e + wl)[..., None]
-            else:
-                o = o / l_e[..., None]
+            kr, vr = self.reconstruct(b)
+            keys = torch.cat([self.K[b, :, :self.n].float(), kr], 1)   # (Hkv, n + n_c, d)
+            vals = torch.cat([self.V[b, :, :self.n].float(), vr], 1)
+            # visibility per query token: exact row i iff pos[i] <= qpos[t]; every coded token
+            vis = torch.cat([pos[None, :] <= qp[:, None],
+                             torch.ones((Tq, kr.shape[1]), dtype=torch.bool, device=q.device)], 1)
+            qg = q[b].float().reshape(Hkv, rep, Tq, d)
+            s = torch.matmul(qg, keys[:, None].transpose(-1, -2)) * scaling              # (Hkv, rep, Tq, N)
+            s = s.masked_fill(~vis, float("-inf"))
+            o = torch.matmul(s.softmax(-1), vals[:, None])                               # (Hkv, rep, Tq, d)
             outs.append(o.reshape(Hq, Tq, d).transpose(0, 1))
         return torch.stack(outs).to(q.dtype).contiguous()
 
