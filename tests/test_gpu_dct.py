@@ -105,9 +105,9 @@ def test_decode_matches_oracle(dtype, Hq, Hkv, Tq, T, W):
 
 @pytest.mark.parametrize("T,W", [(4096, 0), (4096 + 64, 64), (8192 + 37, 37)])
 def test_decode_c5_shape_bf16(T, W):
-    """The C5 instantiation itself: bf16, Hq 64 over Hkv 8 (R = 8, the dct_split<8, bf16> kernel the
-    c5 workload times) on the C5 generator's AR(1) + noise rows at a reduced context, with and
-    without an exact tail.  bf16 bar (1e-2) against the float64 oracle."""
+    """The C5 instantiation itself: bf16, Hq 64 over Hkv 8 (R = 8, the dct_pair_split<bf16> kernel
+    the c5 workload times: blocks two at a time) on the C5 generator's AR(1) + noise rows at a
+    reduced context, with and without an exact tail.  bf16 bar (1e-2) against the float64 oracle."""
     import kvq
     from kvq.synth import C5, c5_inputs
     q, K, V = c5_inputs("cpu", T=T)

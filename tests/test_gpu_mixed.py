@@ -158,3 +158,29 @@ def test_decode_many_query_tokens():
     out = kvq.mixed_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
     ref = _oracle(cache, K, V, widths.to(torch.int64), q, d ** -0.5)
     assert float(np.abs(out - ref).max()) <= 2e-3
+
+
+def test_decode_c3_class_plan_every_pair():
+    """The plan the c3 workload times, at a shorter context: B 8 x Hkv 8 = 64 (b, h) with 64 blocks
+    each takes the class-major plan (3 dispatch classes x 4 splits = 12 splits per (b, h), one full
+    round of 768 blocks, splits sized by the class weights), asserted through the workspace size;
+    every (b, h) against the oracle at the bf16 bar, and two runs bit-equal."""
+    import kvq
+    from kvq.synth import C3, c3_inputs
+    s = C3
+    T = 4096
+    q, K, V, imp = c3_inputs("cpu", T=T)
+    widths = kvq.c3_widths(imp)
+    cache = kvq.MixedKIVICache.from_context(K.cuda(), V.cuda(), widths.cuda(), window=0)
+    assert cache.nb == 64 and cache.n_exact == 0
+    BH, R = s.B * s.Hkv, s.Hq // s.Hkv
+    ws = kvq.mixed_workspace_floats(s.B, s.Hq, s.Hkv, 1, s.d, cache.nb, 0)
+    assert ws == BH * 12 * R * (s.d + 2), ws                    # 12 class-weighted splits per (b, h)
+    qc = q.cuda()
+    got = kvq.mixed_decode(qc, s.d ** -0.5, cache)
+    assert torch.equal(got, kvq.mixed_decode(qc, s.d ** -0.5, cache))
+    out = got.float().cpu().numpy()
+    ref = _oracle(cache, K, V, widths.to(torch.int64), q, s.d ** -0.5)
+    err = float(np.abs(out - ref).max())
+    print(f"C3 class plan (12 splits per (b, h)), every pair: max-abs-err {err:.3e}", flush=True)
+    assert err <= 1e-2, err
