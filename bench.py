@@ -227,6 +227,26 @@ def _traffic(name: str):
     return None
 
 
+def _spread_pairs(B: int, H: int) -> list:
+    """Every (b, h) pair, ordered so that any prefix is spread over the batch and the heads (and so
+    over the split slots and XCDs the plan maps them to): first and last pairs, then the rest in a
+    stride that visits every batch row and head early."""
+    allp = [(b, h) for b in range(B) for h in range(H)]
+    n = len(allp)
+    stride = next(st for st in (H + 1, H + 3, H + 5, 7, 11, 13, 1) if math.gcd(st, n) == 1)
+    order = [0, n - 1] + [(i * stride) % n for i in range(1, n)]
+    seen, res = set(), []
+    for i in order:
+        if i not in seen:
+            seen.add(i)
+            res.append(allp[i])
+    return res
+
+
+def _parity_block(errs, bar: float, oracle: str) -> dict:
+    return {"pairs": len(errs), "max_abs_err": max(errs), "bar": bar, "ok": max(errs) <= bar, "oracle": oracle}
+
+
 # ---------------------------------------------------------------------------------------------
 # C2 (default) and C1: packed 4-bit KIVI decode
 
@@ -413,8 +433,10 @@ def run_c3(args) -> dict:
     log(f"C3 step {ms * 1e3:.1f} us, split {split_ms * 1e3:.1f} us")
     if not args.no_cpu_baseline:
         from oracle.mixed import dequant_blocks, mixed_decode, mixed_quant
-        pairs = [(b, h) for b in range(s.B) for h in range(s.Hkv)]
-        times = []
+        step()
+        gpu_out = out.float().cpu().numpy()                                           # (B, 1, Hq, d)
+        pairs = _spread_pairs(s.B, s.Hkv)
+        times, errs = [], []
         rep = s.Hq // s.Hkv
         for b, h in pairs:
             Kb = K[b:b + 1, h:h + 1].float().cpu().numpy()
@@ -423,15 +445,19 @@ def run_c3(args) -> dict:
             qb_ = q[b:b + 1, h * rep:(h + 1) * rep].float().cpu().numpy()
             t0 = time.perf_counter()
             xk, xv = dequant_blocks(m["kc"], m["k_lo"], m["k_sc"], m["vc"], m["v_lo"], m["v_sc"])
-            mixed_decode(qb_, scaling, xk, xv)
+            o = mixed_decode(qb_, scaling, xk, xv)                                     # (1, 1, rep, d)
             times.append(time.perf_counter() - t0)
-            if sum(times) >= args.cpu_seconds and len(times) >= 2:
+            errs.append(float(np.abs(gpu_out[b, 0, h * rep:(h + 1) * rep] - o[0, 0]).max()))
+            if sum(times) >= args.cpu_seconds and len(times) >= 4:
                 break
-        t = float(np.median(times)) * len(pairs)
+        t = float(np.median(times)) * s.B * s.Hkv
         res["cpu_baseline"] = {"value": bytes_alg / t / 1e9, "unit": "GB/s", "cores": _threads(), "kind": "port",
                                "us_per_layer": t * 1e6,
-                               "sample": f"{len(times)} of {len(pairs)} (batch, KV-head) pairs; median per pair x "
-                                         f"{len(pairs)}; numpy per-block dequantise + chunked_attention"}
+                               "sample": f"{len(times)} of {s.B * s.Hkv} (batch, KV-head) pairs; median per pair x "
+                                         f"{s.B * s.Hkv}; numpy per-block dequantise + chunked_attention"}
+        res["parity"] = _parity_block(errs, 1e-2, "oracle.mixed mixed_quant + dequant_blocks + mixed_decode "
+                                                  "(chunked_attention, float64) of the same pairs, same inputs; the "
+                                                  "timed plan (class-major splits)")
     return res
 
 
@@ -548,24 +574,29 @@ def run_c5(args) -> dict:
     log(f"C5 step {ms * 1e3:.1f} us, split {split_ms * 1e3:.1f} us, encode {enc_ms * 1e3:.1f} us")
     if not args.no_cpu_baseline:
         from oracle.dct import dct_decode, dct_encode
-        times = []
+        step()
+        gpu_out = out.float().cpu().numpy()                                           # (1, 1, Hq, d)
+        times, errs = [], []
         rep = s.Hq // s.Hkv
-        for h in range(s.Hkv):
+        for h in (0, s.Hkv - 1) + tuple(range(1, s.Hkv - 1)):
             Kh = K[:, h:h + 1].float().cpu().numpy().reshape(1, s.T, s.d)
             Vh = V[:, h:h + 1].float().cpu().numpy().reshape(1, s.T, s.d)
             kc_, ks_, _ = dct_encode(Kh)                                            # compression: not timed
             vc_, vs_, _ = dct_encode(Vh)
             qh = q[:, h * rep:(h + 1) * rep].float().cpu().numpy()
             t0 = time.perf_counter()
-            dct_decode(qh, scaling, kc_, ks_, vc_, vs_)
+            o = dct_decode(qh, scaling, kc_, ks_, vc_, vs_)                         # (1, 1, rep, d)
             times.append(time.perf_counter() - t0)
-            if sum(times) >= args.cpu_seconds and len(times) >= 1:
+            errs.append(float(np.abs(gpu_out[0, 0, h * rep:(h + 1) * rep] - o[0, 0]).max()))
+            if sum(times) >= args.cpu_seconds and len(times) >= 2:
                 break
         t = float(np.median(times)) * s.Hkv
         res["cpu_baseline"] = {"value": bytes_alg / t / 1e9, "unit": "GB/s", "cores": _threads(), "kind": "port",
                                "us_per_layer": t * 1e6,
                                "sample": f"{len(times)} of {s.Hkv} KV heads; median per head x {s.Hkv}; numpy IDCT "
                                          f"reconstruction + chunked_attention (float64)"}
+        res["parity"] = _parity_block(errs, 1e-2, "oracle.dct dct_encode + dct_decode (IDCT reconstruction + "
+                                                  "chunked_attention, float64) of the same KV heads at full context")
     return res
 
 
@@ -882,7 +913,63 @@ def run_c4(args) -> dict:
                                "sample": f"{len(times)} of {len(pairs)} (batch, KV-head) pairs; one scored step "
                                          f"(dequantise keys, softmax probabilities, accumulate) + top-k per pair, "
                                          f"median x {len(pairs)}"}
+        res["parity"] = c4_parity(args, qs, K, V, scores, idx, out_k, n_q, scaling, wgt)
     return res
+
+
+def c4_parity(args, qs, K, V, scores, idx, out_k, n_q: int, scaling: float, wgt: float) -> dict:
+    """The eviction episode the C4 line times, against the oracle on sampled (b, h) pairs at full size:
+    the scores after all C4_STEPS scored steps (relative to the row's largest score), the retained set
+    (equal to the oracle's top-k of its own scores except where both sides' candidates tie with the
+    oracle's k-th score within 1e-4 of it, torch.topk leaving tie order unspecified), and the decode over
+    the retained rows plus the exact window (q of step 0; oracle: chunked_attention over the oracle's
+    dequantised rows at the GPU's retained positions)."""
+    import numpy as np
+    from kvq.synth import C4, C4_GROUP, C4_KEEP
+    from oracle.attention import chunked_attention
+    from oracle.evict import accumulate_decode_scores, decode_step_probs, topk_retain
+    from oracle.kivi import kivi_dequant, kivi_quant
+    s = C4
+    rep = s.Hq // s.Hkv
+    sc_gpu = scores.cpu().numpy()
+    idx_gpu = idx.cpu().numpy().astype(np.int64)
+    o_gpu = out_k.float().cpu().numpy()                                   # (B, 1, Hq, d)
+    q_all = qs.float().cpu().numpy()                                      # (steps, B, Hq, 1, d)
+    n_steps = q_all.shape[0]
+    sc_err, out_err, set_diff, tie_gap = [], [], 0, 0.0
+    t0 = time.perf_counter()
+    for b, h in _spread_pairs(s.B, s.Hkv):
+        Kb = K[b:b + 1, h:h + 1].float().cpu().numpy()
+        Vb = V[b:b + 1, h:h + 1].float().cpu().numpy()
+        kq, vq = kivi_quant(Kb, 4, C4_GROUP, True, 0), kivi_quant(Vb, 4, C4_GROUP, False, 0)
+        kh = kivi_dequant(kq["codes"], kq["lo"], kq["scale"], C4_GROUP, True)[:, :, :n_q]
+        vh = kivi_dequant(vq["codes"][:, :, :n_q], vq["lo"][:, :, :n_q], vq["scale"][:, :, :n_q], C4_GROUP, False)
+        # every step's query rows at once: each row is its own softmax over the packed + exact keys
+        qb = q_all[:, b, h * rep:(h + 1) * rep, 0].transpose(1, 0, 2)[None]   # (1, rep, steps, d)
+        p = decode_step_probs(qb, scaling, kh, Kb[:, :, n_q:])
+        sc = accumulate_decode_scores(np.zeros((1, 1, n_q)), p, wgt)[0, 0]
+        sc_err.append(float(np.abs(sc_gpu[b, h] - sc).max() / sc.max()))
+        ref = topk_retain(sc[None], C4_KEEP)[0]
+        kth = float(np.sort(sc)[::-1][C4_KEEP - 1])
+        diff = np.setxor1d(ref, idx_gpu[b, h])
+        set_diff += int(diff.size)
+        if diff.size:
+            tie_gap = max(tie_gap, float(np.abs(sc[diff] - kth).max() / kth))
+        keep = idx_gpu[b, h]
+        tok = {"k": kh[:, :, keep], "v": vh[:, :, keep], "b": np.zeros((1, 1, keep.size)),
+               "tau": np.full(keep.size, -1)}
+        W = Kb.shape[2] - n_q
+        o = chunked_attention(q_all[0, b:b + 1, h * rep:(h + 1) * rep], scaling, np.array([Kb.shape[2]]),
+                              Kb[:, :, n_q:], Vb[:, :, n_q:], np.arange(W), np.full(W, 1 << 40), tok)
+        out_err.append(float(np.abs(o_gpu[b, 0, h * rep:(h + 1) * rep] - o[0, 0]).max()))
+        if time.perf_counter() - t0 >= args.cpu_seconds and len(sc_err) >= 3:
+            break
+    ok = max(sc_err) <= 1e-4 and tie_gap <= 1e-4 and max(out_err) <= 1e-2
+    return {"pairs": len(sc_err), "steps": n_steps, "scores_max_rel_err": max(sc_err),
+            "retained_set_differences": set_diff, "differences_max_rel_gap_to_kth": tie_gap,
+            "retained_decode_max_abs_err": max(out_err), "max_abs_err": max(out_err), "bar": 1e-2, "ok": ok,
+            "oracle": "oracle.kivi kivi_quant + oracle.evict decode_step_probs / accumulate_decode_scores / "
+                      "topk_retain + chunked_attention (float64), same inputs, full context"}
 
 
 # ---------------------------------------------------------------------------------------------
