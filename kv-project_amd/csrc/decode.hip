@@ -159,8 +159,6 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
   float (*qs)[kD] = reinterpret_cast<float (*)[kD]>(smem);
   float* red_o = smem + R * kD;                     // [wave][R][kD]
   float* red_ml = red_o + kWaves * R * kD;          // [wave][2][R]
-  load_q_rows<R, DT>(p, b, h, qs);
-  __syncthreads();
   const int e0 = sidx * p.exact_rows;
   const int e1 = min(e0 + p.exact_rows, p.n_exact);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
@@ -168,14 +166,8 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
   const int w0 = e0 + (e1 - e0) * wave / kWaves, w1 = e0 + (e1 - e0) * (wave + 1) / kWaves;
   const int64_t kbase = static_cast<int64_t>(bh) * p.cap_e * kD;
   const bool masked = p.exact_pos != nullptr && p.q_pos != nullptr;
-  float qv[R][8];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int k = 0; k < 8; ++k) qv[r][k] = qs[r][8 * part + k];
+  float qv[R][8];                                   // scaled query rows (set once they are staged)
   int64_t qp[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) qp[r] = masked ? p.q_pos[r % p.Tq] : 0;
   float m[R], l[R], o[R][8];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -239,13 +231,26 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
       for (int k = 0; k < 8; ++k) o[r][k] = __builtin_fmaf(pr, vx[k], o[r][k]);
     }
   };
+  // the first four row quads of the wavefront go out before the query rows are staged, so the
+  // block waits for one round of loads, not two
+  Rows x0, x1, x2, x3;
   if (w0 < w1) {
-    Rows x0, x1, x2, x3;
     load_rows(w0 + j, x0);
     load_rows(w0 + 4 + j, x1);
     load_rows(w0 + 8 + j, x2);
+    load_rows(w0 + 12 + j, x3);
+  }
+  load_q_rows<R, DT>(p, b, h, qs);
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) qv[r][k] = qs[r][8 * part + k];
+#pragma unroll
+  for (int r = 0; r < R; ++r) qp[r] = masked ? p.q_pos[r % p.Tq] : 0;
+  if (w0 < w1) {
     for (int i0 = w0;; i0 += 16) {
-      load_rows(i0 + 12 + j, x3);
+      if (i0 != w0) load_rows(i0 + 12 + j, x3);
       attend(i0 + j, x0);
       if (i0 + 4 >= w1) break;
       load_rows(i0 + 16 + j, x0);
