@@ -526,6 +526,35 @@ int kvq_strata_allocate(const float* D, int64_t Hkv, int64_t n, int nlev, const 
                         void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * A7  Eviction families that keep exact rows, and chunk-local selection.
+ *
+ * kvq_gather_rows: rows idx[bh][0..count) of one or two (b, h)-sliced row arrays (k, and v when
+ * non-null; rows of row_bytes bytes, (b, h) stride x_bh bytes) into k_out / v_out (rows in idx
+ * order, (b, h) stride out_bh bytes); an index outside [0, n_valid) writes a zero row.  It replaces
+ * the torch.gather of the kept rows in SnapKVQuantMethod.entries (STRATA_KV.py:1024-1025) and the
+ * column selection of LayerState.__init__ over a SnapKV / StreamingLLM keep set (682-694, hide
+ * masks of 969-981 and 1048-1059).  row_bytes, strides and pointers multiples of 16 bytes.
+ *
+ * kvq_chunk_share: finalize_chunk's within-chunk attention share (STRATA_KV.py:581-583) --
+ * share[bh][c] = (1/nq) sum_q softmax_c(qref[bh][q] . k[bh][c]) for qref (BH, nq, d) the scaled
+ * observed queries and k (BH, C, d), both float32 and 16-byte aligned; C <= 2048, d % 4 == 0.
+ * workspace >= kvq_chunk_share_workspace(BH, nq, C) floats (the logits).  The top-k of the share
+ * (kvq_topk_retain) and the gather of the kept rows complete finalize_chunk's selection.
+ *
+ * kvq_absmax_fake_quant: fake_quant_tokens (STRATA_KV.py:556-563) for 2 <= bits <= 15 -- per row
+ * of d float32, s = max(fp16(max|x| / qmax), 2^-24) with qmax = 2^(bits-1) - 1 and the value
+ * saturated to the fp16 range, out = clamp(round_half_even(x / s), -qmax, qmax) * s (absmax_quant,
+ * 549-554), bit-exact; out may alias x.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_gather_rows(const void* k, const void* v, int64_t BH, int64_t n_valid, int64_t x_bh, int64_t row_bytes,
+                    const int32_t* idx, int64_t count, int64_t idx_bh, void* k_out, void* v_out, int64_t out_bh,
+                    void* stream);
+int64_t kvq_chunk_share_workspace(int64_t BH, int64_t nq, int64_t C);
+int kvq_chunk_share(const float* qref, const float* k, int64_t BH, int64_t nq, int64_t C, int64_t d, float* share,
+                    float* workspace, int64_t workspace_floats, void* stream);
+int kvq_absmax_fake_quant(const float* x, int64_t rows, int64_t d, int bits, float* out, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Self-test of the matrix-core operand layout the decode kernel is written against
  * (v_mfma_f32_16x16x32_f16 on gfx950): writes, for A = I-pattern inputs, the 16x16 product
  * as each lane sees it, followed by the lane each lane reads under row_shr:4 and row_ror:4 and

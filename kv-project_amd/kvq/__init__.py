@@ -7,9 +7,11 @@ op requires GPU tensors and raises ``KVQError`` when the library is missing.
 from ._lib import KVQError, load as load_library
 from .kivi import (kivi_quant, kivi_quant_stored, pack_codes, pack_rows, unpack_codes, unpack_rows, v_tile,
                    v_untile, vmeta_tile)
-from .decode import PackedKIVICache, kivi_decode, score_workspace_floats, workspace_floats
-from .state import DecodeCtl, KIVIState, Router, payload_bytes, register, routed, router_attention
-from .evict import gather_dequant, retained_cache, snapkv_scores, topk_retain, topk_workspace_words
+from .decode import PackedKIVICache, exact_rows_cache, kivi_decode, score_workspace_floats, workspace_floats
+from .state import DecodeCtl, KIVIState, PackedState, Router, payload_bytes, register, routed, router_attention
+from .evict import (chunk_share, fake_quant_tokens, finalize_chunk, gather_dequant, gather_rows, retained_cache,
+                    snapkv_scores, topk_retain, topk_workspace_words)
+from .evict_state import EvictedState, MTLPState, mtlp_budget, mtlp_select, snapkv_keep, streaming_keep
 from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strata_center_rotate, strata_decode,
                      strata_quantize, strata_quantize_planar, strata_v_tile, strata_workspace_floats, uniform_step,
                      unpack_planar, unpack_planar_u8)
@@ -32,5 +34,7 @@ __all__ = [
     "dct_workspace_floats", "MixedKIVICache", "c3_widths", "mixed_decode", "mixed_workspace_floats", "offset_table",
     "StrataState", "strata_pack", "strata_tier_kernel", "QuasarState", "stage_codebooks", "payload_bytes", "AllocWorkspace", "allocate_layer", "layer_costs",
     "strata_allocate", "strata_distortion", "coverage_groups", "coverage_plan", "coverage_stats",
-    "StrataCompressor", "rotation_matrix",
+    "StrataCompressor", "rotation_matrix", "chunk_share", "fake_quant_tokens", "finalize_chunk", "gather_rows",
+    "EvictedState", "MTLPState", "mtlp_budget", "mtlp_select", "snapkv_keep", "streaming_keep", "PackedState",
+    "exact_rows_cache",
 ]

@@ -179,6 +179,19 @@ class PackedKIVICache:
         return out[:nbytes]
 
 
+def exact_rows_cache(k_exact: torch.Tensor, v_exact: torch.Tensor, n_exact: int,
+                     exact_pos: Optional[torch.Tensor] = None) -> PackedKIVICache:
+    """A cache of exact rows only (n_q = 0): k_exact, v_exact (B, Hkv, cap_e, d) of which the first
+    ``n_exact`` rows are held, visible per ``exact_pos`` (all visible when None).  The packed fields
+    are minimal placeholders the decode never reads (it reads no packed row when n_q = 0)."""
+    B, H, _, d = k_exact.shape
+    dev = k_exact.device
+    z8 = lambda *s: torch.zeros(s, dtype=torch.uint8, device=dev)
+    z16 = lambda *s: torch.zeros(s, dtype=torch.float16, device=dev)
+    return PackedKIVICache(z8(B, H, 64, d // 2), z16(B, H, 1, d), z16(B, H, 1, d), z8(B, H, 2, 16 * d),
+                           z16(B, H, 2, d // 64, 32, 2), 0, 64, 64, k_exact, v_exact, n_exact, exact_pos)
+
+
 def workspace_floats(B: int, Hq: int, Hkv: int, Tq: int, d: int, n_q: int, n_exact: int,
                      group_k: int, group_v: int, split_tokens: int = 0) -> int:
     n = _lib.load().kvq_kivi_decode_workspace(B, Hq, Hkv, Tq, d, n_q, n_exact, group_k, group_v,

@@ -157,3 +157,96 @@ def retained_cache(cache: PackedKIVICache, idx: torch.Tensor) -> PackedKIVICache
         ke[:, :, k:].copy_(cache.k_exact[:, :, :ne])
         ve[:, :, k:].copy_(cache.v_exact[:, :, :ne])
     return replace(cache, n_q=0, k_exact=ke, v_exact=ve, n_exact=k + ne, exact_pos=None, ring=False)
+
+
+@torch.no_grad()
+def gather_rows(k: torch.Tensor, v: torch.Tensor | None, idx: torch.Tensor, out=None):
+    """Rows of k (and v) (B, Hkv, T, d) at positions idx (B, Hkv, m) int32, in idx order ->
+    (B, Hkv, m, d) of k's dtype (libkvq kvq_gather_rows; an index outside [0, T) gives a zero row).
+    ``out`` = (ko, vo): rows [0, m) of two (B, Hkv, >= m, d) tensors receive them instead."""
+    _lib.require_gpu(k, idx)
+    B, H, T, d = k.shape
+    if idx.dim() != 3 or idx.shape[:2] != (B, H) or idx.dtype != torch.int32:
+        raise ValueError("idx must be int32 (B, Hkv, m)")
+    k = k.contiguous()
+    if v is not None:
+        _lib.require_gpu(v)
+        if v.shape != k.shape or v.dtype != k.dtype:
+            raise ValueError("k and v must have one shape and dtype")
+        v = v.contiguous()
+    idx = idx.contiguous()
+    m = idx.shape[2]
+    if out is None:
+        ko = torch.empty((B, H, m, d), dtype=k.dtype, device=k.device)
+        vo = torch.empty_like(ko) if v is not None else None
+    else:
+        ko, vo = out
+        for o in (ko, vo):
+            if o is None:
+                continue
+            if (o.shape[:2] != (B, H) or o.shape[2] < m or o.shape[3] != d or o.dtype != k.dtype
+                    or not o.is_contiguous()):
+                raise ValueError("out must be contiguous (B, Hkv, >= m, d) tensors of k's dtype")
+        if (vo is None) != (v is None):
+            raise ValueError("out must hold a value buffer exactly when v is given")
+    row = d * k.element_size()
+    _lib.call("kvq_gather_rows", k.data_ptr(), _lib.ptr(v), B * H, T, T * row, row, idx.data_ptr(), m, m,
+              ko.data_ptr(), _lib.ptr(vo), ko.shape[2] * row, _lib.stream_of(k))
+    return ko, vo
+
+
+@torch.no_grad()
+def chunk_share(qref: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
+    """finalize_chunk's within-chunk attention share (STRATA_KV.py:581-583): qref (B, Hkv, nq, d) the
+    scaled observed queries, k (B, Hkv, C, d) -> (B, Hkv, C) float32, the softmax over the chunk's
+    keys of each query averaged over the queries (libkvq kvq_chunk_share)."""
+    _lib.require_gpu(qref, k)
+    B, H, nq, d = qref.shape
+    C = k.shape[2]
+    if k.shape[:2] != (B, H) or k.shape[3] != d:
+        raise ValueError("qref (B, Hkv, nq, d) and k (B, Hkv, C, d) must agree")
+    q32, k32 = qref.float().contiguous(), k.float().contiguous()
+    share = torch.empty((B, H, C), dtype=torch.float32, device=k.device)
+    ws = torch.empty((_lib.load().kvq_chunk_share_workspace(B * H, nq, C),), dtype=torch.float32, device=k.device)
+    _lib.call("kvq_chunk_share", q32.data_ptr(), k32.data_ptr(), B * H, nq, C, d, share.data_ptr(), ws.data_ptr(),
+              ws.numel(), _lib.stream_of(k))
+    return share
+
+
+@torch.no_grad()
+def fake_quant_tokens(x: torch.Tensor, bits: int) -> torch.Tensor:
+    """What a reader of a token stored at ``bits`` sees (fake_quant_tokens, STRATA_KV.py:556-563):
+    bits >= 16 keeps x; otherwise absmax_quant's codes times its fp16 scale per vector (549-554), in
+    float32 (libkvq kvq_absmax_fake_quant)."""
+    if bits >= 16:
+        return x
+    _lib.require_gpu(x)
+    xf = x.float().contiguous()
+    out = torch.empty_like(xf)
+    d = xf.shape[-1]
+    _lib.call("kvq_absmax_fake_quant", xf.data_ptr(), xf.numel() // d, d, int(bits), out.data_ptr(),
+              _lib.stream_of(xf))
+    return out
+
+
+@torch.no_grad()
+def finalize_chunk(k: torch.Tensor, v: torch.Tensor, qref: torch.Tensor, method, plan, keep_bits: int, cfg=None):
+    """Drop-in for finalize_chunk (STRATA_KV.py:573-592) of the top-k families: k, v (B, Hkv, C, d),
+    qref (B, Hkv, nq, d) scaled observed queries; keeps plan["tokens"] tokens per (b, KV head) by
+    their within-chunk attention share (``chunk_share``), in position order (``topk_retain``; among
+    shares tied at the m-th the lowest positions), gathers them (``gather_rows``) and stores them at
+    ``keep_bits`` (``fake_quant_tokens``).  Returns {k, v, b (zeros), idx (int64)}.  ``method``: an
+    object with ``family`` (or the family name); attention matching ("am", a least-squares fit
+    outside this path) is refused."""
+    family = getattr(method, "family", method)
+    if family == "am":
+        raise NotImplementedError("attention matching (family 'am') is not part of the device path")
+    m = int(plan["tokens"] if isinstance(plan, dict) else plan)
+    B, H, C, d = k.shape
+    if not 1 <= m <= C:
+        raise ValueError("plan['tokens'] must be in [1, C]")
+    share = chunk_share(qref, k)
+    idx = topk_retain(share, m)                                          # (B, Hkv, m) int32, position order
+    gk, gv = gather_rows(k.float(), v.float(), idx)
+    return {"k": fake_quant_tokens(gk, keep_bits), "v": fake_quant_tokens(gv, keep_bits),
+            "b": torch.zeros((B, H, m), device=k.device), "idx": idx.to(torch.int64)}

@@ -100,7 +100,89 @@ class DecodeCtl:
         return src.attend(q, scaling, self.pos, self.chunk), None
 
 
-class KIVIState:
+class PackedState:
+    """The decode-state protocol (LayerState / StrataState, STRATA_KV.py:682-719, 1710-1818) over one
+    ``PackedKIVICache`` ``self.cache`` whose exact rows carry positions (``cache.exact_pos``): append,
+    attend, reference_attend and check_kernel.  Subclasses build the cache (KIVIState: KIVIMethod's
+    cache; kvq.evict_state: the eviction families') and count their stored bytes."""
+
+    cache: PackedKIVICache
+    n: int
+    n0: int
+    shared: Optional[int] = None
+    use_kernel: bool = True
+
+    def append(self, k: torch.Tensor, v: torch.Tensor, pos) -> None:
+        """Append t tokens (B, Hkv, t, d) at positions ``pos`` exactly (STRATA_KV.py:707-714)."""
+        c = self.cache
+        t = k.shape[2]
+        if c.n_exact + t > c.cap_e:
+            raise RuntimeError("decode buffer exhausted")
+        c.k_exact[:, :, c.n_exact:c.n_exact + t] = k.to(c.k_exact.dtype)
+        c.v_exact[:, :, c.n_exact:c.n_exact + t] = v.to(c.v_exact.dtype)
+        p = torch.as_tensor(pos, dtype=torch.int64).reshape(-1).to(c.k_exact.device)
+        c.exact_pos[c.n_exact:c.n_exact + t] = p
+        c.n_exact += t
+        self.n += t
+
+    def attend(self, q: torch.Tensor, scaling: float, qpos, chunk=None) -> torch.Tensor:
+        """q (B, Hq, Tq, d) at positions ``qpos`` (Tq,) -> (B, Tq, Hq, d) in q's dtype.  Query t
+        reads every quantised row, the window rows and the appended rows at positions <= qpos[t]
+        (chunked_attention's visibility, STRATA_KV.py:641-675).  Any Tq: the step runs in
+        query-token pieces of at most 8 // rep tokens, and at most ``chunk`` when it is given
+        (the reference's ATTN_CHUNK query chunks)."""
+        if not self.use_kernel:
+            raise RuntimeError(f"{type(self).__name__}: the HIP decode kernel is disabled (check_kernel failed)")
+        c = self.cache
+        qp = torch.as_tensor(qpos, dtype=torch.int64).reshape(-1).to(q.device)
+        if qp.numel() != q.shape[2]:
+            raise ValueError("qpos must hold one position per query token")
+        return kivi_decode(q.to(c.k_exact.dtype), scaling, c, q_pos=qp, chunk=chunk).to(q.dtype)
+
+    @torch.no_grad()
+    def reference_attend(self, q: torch.Tensor, scaling: float, qpos) -> torch.Tensor:
+        """The same attention in float32 torch ops from the dequantised cache (for check_kernel):
+        one softmax over the dequantised rows and the visible exact rows."""
+        c = self.cache
+        B, Hkv, _, d = c.k_exact.shape
+        from .decode import _dequant_keys, _dequant_values
+        if c.n_q > 0:
+            kh = _dequant_keys(c)                                 # (B, Hkv, n_q, d) fp32
+            vh = _dequant_values(c)
+        else:
+            kh = vh = torch.zeros((B, Hkv, 0, d), device=c.k_exact.device)
+        ke = c.k_exact[:, :, :c.n_exact].float()
+        ve = c.v_exact[:, :, :c.n_exact].float()
+        rep = q.shape[1] // Hkv
+        K = torch.cat([kh, ke], 2).repeat_interleave(rep, 1)
+        V = torch.cat([vh, ve], 2).repeat_interleave(rep, 1)
+        qp = torch.as_tensor(qpos, dtype=torch.int64).reshape(-1).to(q.device)
+        s = (q.float() * scaling) @ K.transpose(-1, -2)             # (B, Hq, Tq, n)
+        vis_e = c.exact_pos[:c.n_exact][None, :] <= qp[:, None]     # (Tq, n_exact)
+        mask = torch.cat([torch.ones((qp.numel(), c.n_q), dtype=torch.bool, device=q.device), vis_e], 1)
+        s = s.masked_fill(~mask, float("-inf"))
+        o = s.softmax(-1) @ V
+        return o.transpose(1, 2).to(q.dtype).contiguous()
+
+    @torch.no_grad()
+    def check_kernel(self, tol: float = 2e-2) -> Dict:
+        """Relative max error of the kernel against reference_attend on seeded random queries
+        (STRATA_KV.py:1797-1817).  Raises when it exceeds ``tol``: there is no other path."""
+        c = self.cache
+        g = torch.Generator(device="cpu").manual_seed(42)
+        Hkv, d = c.k_exact.shape[1], c.k_exact.shape[3]
+        q = torch.randn(c.k_exact.shape[0], Hkv * 4, 2, d, generator=g).to(c.k_exact.device, c.k_exact.dtype)
+        qpos = torch.tensor([self.n, self.n + 1])
+        ref = self.reference_attend(q, d ** -0.5, qpos).float()
+        out = self.attend(q, d ** -0.5, qpos).float()
+        err = float((out - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+        self.use_kernel = err <= tol
+        if not self.use_kernel:
+            raise RuntimeError(f"{type(self).__name__}.check_kernel: relative error {err:.3e} > {tol}")
+        return {"kernel": True, "kernel_rel_err": err}
+
+
+class KIVIState(PackedState):
     """One layer's KIVI cache as the decoder holds it (LayerState protocol).
 
     ``K, V`` (B, Hkv, H, d): the prefilled context (post-RoPE, model dtype, on the GPU).
@@ -141,69 +223,3 @@ class KIVIState:
         """MEASURED bytes of the stored context: the length of ``payload()``."""
         c = self.cache
         return c.wire_bytes(n_exact=self.n0 - c.n_q)
-
-    def append(self, k: torch.Tensor, v: torch.Tensor, pos) -> None:
-        """Append t tokens (B, Hkv, t, d) at positions ``pos`` exactly (STRATA_KV.py:707-714)."""
-        c = self.cache
-        t = k.shape[2]
-        if c.n_exact + t > c.cap_e:
-            raise RuntimeError("decode buffer exhausted")
-        c.k_exact[:, :, c.n_exact:c.n_exact + t] = k.to(c.k_exact.dtype)
-        c.v_exact[:, :, c.n_exact:c.n_exact + t] = v.to(c.v_exact.dtype)
-        p = torch.as_tensor(pos, dtype=torch.int64).reshape(-1).to(c.k_exact.device)
-        c.exact_pos[c.n_exact:c.n_exact + t] = p
-        c.n_exact += t
-        self.n += t
-
-    def attend(self, q: torch.Tensor, scaling: float, qpos, chunk=None) -> torch.Tensor:
-        """q (B, Hq, Tq, d) at positions ``qpos`` (Tq,) -> (B, Tq, Hq, d) in q's dtype.  Query t
-        reads every quantised row, the window rows and the appended rows at positions <= qpos[t]
-        (chunked_attention's visibility, STRATA_KV.py:641-675).  Any Tq: the step runs in
-        query-token pieces of at most 8 // rep tokens, and at most ``chunk`` when it is given
-        (the reference's ATTN_CHUNK query chunks)."""
-        if not self.use_kernel:
-            raise RuntimeError("KIVIState: the HIP decode kernel is disabled (check_kernel failed)")
-        c = self.cache
-        qp = torch.as_tensor(qpos, dtype=torch.int64).reshape(-1).to(q.device)
-        if qp.numel() != q.shape[2]:
-            raise ValueError("qpos must hold one position per query token")
-        return kivi_decode(q.to(c.k_exact.dtype), scaling, c, q_pos=qp, chunk=chunk).to(q.dtype)
-
-    @torch.no_grad()
-    def reference_attend(self, q: torch.Tensor, scaling: float, qpos) -> torch.Tensor:
-        """The same attention in float32 torch ops from the dequantised cache (for check_kernel):
-        one softmax over the dequantised rows and the visible exact rows."""
-        c = self.cache
-        B, Hkv, _, d = c.k_exact.shape
-        from .decode import _dequant_keys, _dequant_values
-        kh = _dequant_keys(c)                                     # (B, Hkv, n_q, d) fp32
-        vh = _dequant_values(c)
-        ke = c.k_exact[:, :, :c.n_exact].float()
-        ve = c.v_exact[:, :, :c.n_exact].float()
-        rep = q.shape[1] // Hkv
-        K = torch.cat([kh, ke], 2).repeat_interleave(rep, 1)
-        V = torch.cat([vh, ve], 2).repeat_interleave(rep, 1)
-        qp = torch.as_tensor(qpos, dtype=torch.int64).reshape(-1).to(q.device)
-        s = (q.float() * scaling) @ K.transpose(-1, -2)             # (B, Hq, Tq, n)
-        vis_e = c.exact_pos[:c.n_exact][None, :] <= qp[:, None]     # (Tq, n_exact)
-        mask = torch.cat([torch.ones((qp.numel(), c.n_q), dtype=torch.bool, device=q.device), vis_e], 1)
-        s = s.masked_fill(~mask, float("-inf"))
-        o = s.softmax(-1) @ V
-        return o.transpose(1, 2).to(q.dtype).contiguous()
-
-    @torch.no_grad()
-    def check_kernel(self, tol: float = 2e-2) -> Dict:
-        """Relative max error of the kernel against reference_attend on seeded random queries
-        (STRATA_KV.py:1797-1817).  Raises when it exceeds ``tol``: there is no other path."""
-        c = self.cache
-        g = torch.Generator(device="cpu").manual_seed(42)
-        Hkv, d = c.k_exact.shape[1], c.k_exact.shape[3]
-        q = torch.randn(c.k_exact.shape[0], Hkv * 4, 2, d, generator=g).to(c.k_exact.device, c.k_exact.dtype)
-        qpos = torch.tensor([self.n, self.n + 1])
-        ref = self.reference_attend(q, d ** -0.5, qpos).float()
-        out = self.attend(q, d ** -0.5, qpos).float()
-        err = float((out - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
-        self.use_kernel = err <= tol
-        if not self.use_kernel:
-            raise RuntimeError(f"KIVIState.check_kernel: relative error {err:.3e} > {tol}")
-        return {"kernel": True, "kernel_rel_err": err}

@@ -92,3 +92,64 @@ def topk_retain(scores: np.ndarray, k: int) -> np.ndarray:
         order = np.lexsort((np.arange(n), -row.astype(np.float64)))     # score desc, position asc
         out[i] = np.sort(order[:k])
     return out.reshape(scores.shape[:-1] + (k,))
+
+
+# ---- chunk-local selection (finalize_chunk, STRATA_KV.py:573-592) -----------------------------
+
+def chunk_share(qref: np.ndarray, k: np.ndarray) -> np.ndarray:
+    """qref (B, H, nq, d) scaled observed queries, k (B, H, C, d) -> (B, H, C) float64: each query's
+    softmax over the chunk's keys, averaged over the queries (STRATA_KV.py:581-582)."""
+    s = np.einsum("bhqd,bhcd->bhqc", qref.astype(np.float64), k.astype(np.float64))
+    s = np.exp(s - s.max(-1, keepdims=True))
+    return (s / s.sum(-1, keepdims=True)).mean(2)
+
+
+def absmax_fake_quant(x: np.ndarray, bits: int) -> np.ndarray:
+    """fake_quant_tokens (STRATA_KV.py:556-563) in float32 as the reference computes it:
+    absmax_quant's s = max(fp16(clamp(max|x| / qmax)), 2^-24) per vector (549-554), codes
+    clamp(round_half_even(x / s), -qmax, qmax), returned codes * s; bits >= 16 keeps x."""
+    if bits >= 16:
+        return x
+    x = x.astype(np.float32)
+    qmax = np.float32(2 ** (bits - 1) - 1)
+    ratio = (np.abs(x).max(-1, keepdims=True) / qmax).astype(np.float32)
+    s = np.maximum(np.clip(ratio, -65504, 65504).astype(np.float16).astype(np.float32), np.float32(2.0 ** -24))
+    c = np.clip(np.rint(x / s), -qmax, qmax).astype(np.float32)
+    return (c * s).astype(np.float32)
+
+
+def finalize_chunk(k: np.ndarray, v: np.ndarray, qref: np.ndarray, m: int, keep_bits: int) -> dict:
+    """The top-k families' finalize_chunk (STRATA_KV.py:573-592): the m tokens of largest chunk
+    share per (b, h) in position order (ties at the m-th: lowest positions, as topk_retain), their
+    rows gathered and stored at keep_bits.  {k, v, idx, share}."""
+    share = chunk_share(qref, k)
+    idx = topk_retain(share, m)
+    d = k.shape[-1]
+    gk = np.take_along_axis(k.astype(np.float32), idx[..., None].repeat(d, -1), 2)
+    gv = np.take_along_axis(v.astype(np.float32), idx[..., None].repeat(d, -1), 2)
+    return {"k": absmax_fake_quant(gk, keep_bits), "v": absmax_fake_quant(gv, keep_bits), "idx": idx,
+            "share": share}
+
+
+# ---- keep sets of the exact-row eviction families ------------------------------------------
+
+BIG = 1 << 40
+
+
+def streaming_hide(H: int, keep: int, n_sink: int = 4) -> np.ndarray:
+    """hide of a frozen StreamingLLMMethod (STRATA_KV.py:1055-1059) over the context positions
+    [0, H): H for dropped positions (n_sink <= p < H - recent), BIG for kept ones,
+    recent = max(1, keep - n_sink)."""
+    pc = np.arange(H)
+    recent = max(1, keep - n_sink)
+    drop = (pc >= n_sink) & (pc < H - recent)
+    return np.where(drop, H, BIG)
+
+
+def keep_hide(keep: np.ndarray, H: int) -> np.ndarray:
+    """Per-KV-head hide of SnapKVMethod (STRATA_KV.py:976-980): keep (B, Hkv, m) kept positions ->
+    (B, Hkv, H) BIG where kept, H elsewhere."""
+    B, Hkv, _ = keep.shape
+    hide = np.full((B, Hkv, H), H, np.int64)
+    np.put_along_axis(hide, keep.astype(np.int64), BIG, -1)
+    return hide

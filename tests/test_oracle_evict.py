@@ -8,6 +8,8 @@
 * topk_retain: a brute-force sort with explicit (score desc, position asc) keys, on data with
   many ties.
 """
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -78,3 +80,66 @@ def test_topk_retain_brute_force_with_ties(k):
     for r, row in enumerate(rows):
         order = sorted(range(64), key=lambda i: (-float(row[i]), i))
         assert list(got[r]) == sorted(order[:k])
+
+
+def test_chunk_share_by_per_query_loop():
+    """finalize_chunk's share against an explicit loop: each query's softmax over the keys (float64
+    exp / sum), summed over queries, divided by nq."""
+    from oracle.evict import chunk_share
+    rng = np.random.default_rng(5)
+    B, H, nq, C, d = 2, 3, 5, 7, 4
+    q, k = rng.standard_normal((B, H, nq, d)), rng.standard_normal((B, H, C, d))
+    want = np.zeros((B, H, C))
+    for b in range(B):
+        for h in range(H):
+            for i in range(nq):
+                logits = [sum(q[b, h, i, e] * k[b, h, c, e] for e in range(d)) for c in range(C)]
+                mx = max(logits)
+                ex = [math.exp(x - mx) for x in logits]
+                for c in range(C):
+                    want[b, h, c] += ex[c] / sum(ex) / nq
+    np.testing.assert_allclose(chunk_share(q, k), want, rtol=1e-12, atol=0)
+    assert np.allclose(chunk_share(q, k).sum(-1), 1.0)
+
+
+def test_absmax_fake_quant_known_answers():
+    """absmax_quant at 8 and 4 bits on hand-checked rows: the scale is the fp16 value of
+    max|x| / qmax (float32 quotient), codes round half to even, and the scale floor 2^-24."""
+    from oracle.evict import absmax_fake_quant
+    x = np.array([[1.0, -0.5, 0.25, 0.0]], np.float32)
+    s8 = np.float32(np.float16(np.float32(1.0) / np.float32(127)))       # 0.007873535...
+    assert s8 == np.float32(0.007873535)
+    got = absmax_fake_quant(x, 8)
+    np.testing.assert_array_equal(got, (np.rint(x / s8) * s8).astype(np.float32))
+    assert got[0, 0] == np.float32(127) * s8 and got[0, 1] == np.float32(-64) * s8   # -63.5 -> -64 (half even)
+    # 4 bits: qmax 7, s = fp16(2/7) = 0.28564453 (below 2/7), so 1.0 / s = 3.5009 -> 4; with the
+    # float32 scale 2/7 unrounded the quotient would be 3.4999999 -> 3 (a dropped fp16 rounding fails)
+    x4 = np.array([[2.0, 1.0, -2.0, 0.7]], np.float32)
+    s4 = np.float32(np.float16(np.float32(2.0) / np.float32(7)))
+    np.testing.assert_array_equal(absmax_fake_quant(x4, 4), (np.clip(np.rint(x4 / s4), -7, 7) * s4).astype(np.float32))
+    assert s4 == np.float32(0.28564453) and absmax_fake_quant(x4, 4)[0, 1] == 4 * s4
+    # an all-zero row keeps the 2^-24 floor and zero codes; bits >= 16 returns the input
+    np.testing.assert_array_equal(absmax_fake_quant(np.zeros((1, 4), np.float32), 8), np.zeros((1, 4)))
+    assert absmax_fake_quant(x, 16) is x
+
+
+def test_finalize_chunk_keeps_largest_share_in_position_order():
+    from oracle.evict import finalize_chunk
+    rng = np.random.default_rng(9)
+    B, H, nq, C, d = 1, 2, 6, 32, 8
+    q, k, v = (rng.standard_normal((B, H, n, d)).astype(np.float32) for n in (nq, C, C))
+    out = finalize_chunk(k, v, q, 5, 16)
+    for h in range(H):
+        order = np.argsort(-out["share"][0, h], kind="stable")[:5]
+        assert out["idx"][0, h].tolist() == sorted(order.tolist())
+        np.testing.assert_array_equal(out["k"][0, h], k[0, h, out["idx"][0, h]])
+
+
+def test_streaming_and_keep_hides():
+    from oracle.evict import BIG, keep_hide, streaming_hide
+    hide = streaming_hide(100, 20)                 # sinks 0..3 and the last 16 kept
+    kept = np.nonzero(hide == BIG)[0]
+    assert kept.tolist() == [0, 1, 2, 3] + list(range(84, 100)) and (hide[4:84] == 100).all()
+    assert (np.nonzero(streaming_hide(10, 3)[4:] == BIG)[0] + 4).tolist() == [9]   # recent = max(1, keep - 4)
+    kh = keep_hide(np.array([[[1, 4], [0, 2]]]), 5)
+    assert kh.tolist() == [[[5, BIG, 5, 5, BIG], [BIG, 5, BIG, 5, 5]]]
