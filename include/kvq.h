@@ -555,6 +555,28 @@ int kvq_chunk_share(const float* qref, const float* k, int64_t BH, int64_t nq, i
 int kvq_absmax_fake_quant(const float* x, int64_t rows, int64_t d, int bits, float* out, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * F2  QUASAR coded-domain products of one side, with the reference's kernel-wrapper call shapes
+ * quasar_scores(qt, side, n_c) and quasar_values(pv, side, R) (QUASAR_KV.py:1556-1577).  A side
+ * is QuasarState's stored code (1883-1898): the flat uint8 buffer (flat_bytes) of every step's
+ * (Hkv, n_s, nb) pack_rows block, the step table -- n_steps <= 64 int32 rows [offset, n_s, nb, a,
+ * w, bits, level offset], in HOST memory, checked against the buffers before any launch -- and the
+ * concatenated stage codebooks levels (n_levels float32).
+ *   kvq_quasar_scores: qt (Hkv, rows, R) float32 -> out (Hkv, rows, n_c) float32, out[h][r][j] =
+ *     sum over the steps owning token j of qt[h][r][band] . levels[codes of j]   (n_c <= 65535 * 64)
+ *   kvq_quasar_values: pv (Hkv, rows, n_c) float32 -> out (Hkv, rows, R) float32, out[h][r][c] =
+ *     sum over the steps covering coefficient c and their tokens j of pv[h][r][j] levels[code];
+ *     workspace >= kvq_quasar_values_workspace(...) floats.
+ * Fixed summation order (steps, then band positions or tokens): reproducible bit for bit.
+ * ---------------------------------------------------------------------------------------- */
+int kvq_quasar_scores(const float* qt, int64_t Hkv, int64_t rows, int64_t R, const uint8_t* flat, int64_t flat_bytes,
+                      const int32_t* table, int n_steps, const float* levels, int64_t n_levels, int64_t n_c,
+                      float* out, void* stream);
+int64_t kvq_quasar_values_workspace(int64_t Hkv, int64_t rows, int64_t R, int64_t n_c);
+int kvq_quasar_values(const float* pv, int64_t Hkv, int64_t rows, int64_t n_c, const uint8_t* flat, int64_t flat_bytes,
+                      const int32_t* table, int n_steps, const float* levels, int64_t n_levels, int64_t R,
+                      float* out, float* workspace, int64_t workspace_floats, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Self-test of the matrix-core operand layout the decode kernel is written against
  * (v_mfma_f32_16x16x32_f16 on gfx950): writes, for A = I-pattern inputs, the 16x16 product
  * as each lane sees it, followed by the lane each lane reads under row_shr:4 and row_ror:4 and

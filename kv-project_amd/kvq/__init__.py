@@ -18,7 +18,7 @@ from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strat
 from .dct import DctCache, dct_decode, dct_encode, dct_table, dct_workspace_floats
 from .mixed import MixedKIVICache, c3_widths, mixed_decode, mixed_workspace_floats, offset_table
 from .strata_state import StrataState, strata_pack, strata_tier_kernel
-from .quasar import QuasarState, stage_codebooks
+from .quasar import QuasarState, quasar_scores, quasar_values, stage_codebooks
 from .alloc import AllocWorkspace, allocate_layer, layer_costs, strata_allocate, strata_distortion
 from .coverage import coverage_groups, coverage_plan, coverage_stats
 from .strata_compress import StrataCompressor, rotation_matrix
@@ -36,5 +36,5 @@ __all__ = [
     "strata_allocate", "strata_distortion", "coverage_groups", "coverage_plan", "coverage_stats",
     "StrataCompressor", "rotation_matrix", "chunk_share", "fake_quant_tokens", "finalize_chunk", "gather_rows",
     "EvictedState", "MTLPState", "mtlp_budget", "mtlp_select", "snapkv_keep", "streaming_keep", "PackedState",
-    "exact_rows_cache",
+    "exact_rows_cache", "quasar_scores", "quasar_values",
 ]

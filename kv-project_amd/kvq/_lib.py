@@ -77,6 +77,9 @@ SIGNATURES = {
     "kvq_chunk_share_workspace": (i64, [i64, i64, i64]),
     "kvq_chunk_share": (i32, [vp, vp, i64, i64, i64, i64, vp, vp, i64, vp]),
     "kvq_absmax_fake_quant": (i32, [vp, i64, i64, i32, vp, vp]),
+    "kvq_quasar_scores": (i32, [vp, i64, i64, i64, vp, i64, vp, i32, vp, i64, i64, vp, vp]),
+    "kvq_quasar_values_workspace": (i64, [i64, i64, i64, i64]),
+    "kvq_quasar_values": (i32, [vp, i64, i64, i64, vp, i64, vp, i32, vp, i64, i64, vp, vp, i64, vp]),
     "kvq_kivi_payload_bytes": (i64, [i64, i64, i64, i32, i32, i64, i32]),
     "kvq_kivi_export": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i32, i32, vp, vp, i32, i64, i64, i64, vp, i64, vp]),
     "kvq_quasar_plan": (i32, [vp, i32, vp, i32, i64, i64, i32, vp, vp, vp, vp]),

@@ -156,6 +156,8 @@ class QuasarState:
             books = stage_codebooks(self.stages)
             self.levels = torch.from_numpy(np.concatenate(books).astype(np.float32)).to(dev)
             self.sides = [_side_buffers(packed, s, self.stages, dev) for s in (0, 1)]
+            for sd in self.sides:                  # a side dict as the reference's kernel wrappers take it
+                sd["levels"] = self.levels
             if self.sides[0]["flat"] is None or self.sides[1]["flat"] is None:
                 raise ValueError("a coded layer needs steps on both sides")
             f16 = lambda x: torch.as_tensor(x).to(dev, torch.float16).contiguous()
@@ -334,6 +336,60 @@ class QuasarState:
         if err > tol:
             raise RuntimeError(f"QuasarState.check_kernel: relative error {err:.3e} > {tol}")
         return {"kernel": True, "kernel_rel_err": err}
+
+
+# ---- the reference's kernel-wrapper call shapes (QUASAR_KV.py:1556-1577) --------------------
+
+def _host_table(side: Dict) -> np.ndarray:
+    t = side.get("table_np")
+    if t is None:                                  # the reference keeps its table on the device
+        t = torch.as_tensor(side["table"]).detach().cpu().numpy()
+    return np.ascontiguousarray(np.asarray(t, dtype=np.int32).reshape(-1, 7))
+
+
+def _side_parts(side: Dict, device):
+    flat = side["flat"]
+    levels = torch.as_tensor(side["levels"]).to(device, torch.float32).contiguous()
+    if flat is not None:
+        _lib.require_gpu(flat)
+    return flat, levels
+
+
+@torch.no_grad()
+def quasar_scores(qt: torch.Tensor, side: Dict, n_c: int) -> torch.Tensor:
+    """Drop-in for quasar_scores (QUASAR_KV.py:1556-1564): qt (Hkv, rows, R) the query's coefficients
+    -> (Hkv, rows, n_c) float32, the sum over the key side's steps owning each coded token of
+    qt[band] . levels[codes] (libkvq kvq_quasar_scores).  ``side``: a QuasarState side ({flat, table
+    (or table_np), levels}), the reference's or this package's."""
+    _lib.require_gpu(qt)
+    Hkv, rows, R = qt.shape
+    tab = _host_table(side)
+    flat, levels = _side_parts(side, qt.device)
+    q32 = qt.float().contiguous()
+    out = torch.empty((Hkv, rows, int(n_c)), dtype=torch.float32, device=qt.device)
+    _lib.call("kvq_quasar_scores", q32.data_ptr(), Hkv, rows, R, _lib.ptr(flat), 0 if flat is None else flat.numel(),
+              tab.ctypes.data, tab.shape[0], levels.data_ptr(), levels.numel(), int(n_c), out.data_ptr(),
+              _lib.stream_of(qt))
+    return out
+
+
+@torch.no_grad()
+def quasar_values(pv: torch.Tensor, side: Dict, R: int) -> torch.Tensor:
+    """Drop-in for quasar_values (QUASAR_KV.py:1567-1577): pv (Hkv, rows, n_c) weighted probabilities
+    of the coded tokens -> (Hkv, rows, R) float32, per coefficient the sum over the value side's
+    steps covering it of pv . levels[codes] (libkvq kvq_quasar_values)."""
+    _lib.require_gpu(pv)
+    Hkv, rows, n_c = pv.shape
+    tab = _host_table(side)
+    flat, levels = _side_parts(side, pv.device)
+    p32 = pv.float().contiguous()
+    out = torch.empty((Hkv, rows, int(R)), dtype=torch.float32, device=pv.device)
+    ws = torch.empty((_lib.load().kvq_quasar_values_workspace(Hkv, rows, int(R), n_c),), dtype=torch.float32,
+                     device=pv.device)
+    _lib.call("kvq_quasar_values", p32.data_ptr(), Hkv, rows, n_c, _lib.ptr(flat), 0 if flat is None else flat.numel(),
+              tab.ctypes.data, tab.shape[0], levels.data_ptr(), levels.numel(), int(R), out.data_ptr(), ws.data_ptr(),
+              ws.numel(), _lib.stream_of(pv))
+    return out
 
 
 # ---- synthetic stored codes (tests and the benchmark) -------------------------------------

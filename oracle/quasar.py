@@ -119,6 +119,27 @@ def _deq(step: Dict, stage_bits: Sequence[int]) -> np.ndarray:
     return unpack_rows_lut(np.asarray(step["codes"]), b, levels).astype(np.float64)
 
 
+def coded_scores(qt: np.ndarray, packed: Dict, stage_bits: Sequence[int]) -> np.ndarray:
+    """QuasarState.coded_scores' torch path (QUASAR_KV.py:1920-1929) in float64: qt (..., Hkv, rows, R)
+    -> (..., Hkv, rows, n_c), per key-side step the band of qt dotted with the levels of the tokens
+    owning the step."""
+    sc = np.zeros(qt.shape[:-1] + (int(packed["n_c"]),))
+    for st in packed["steps"]:
+        if st["side"] == 0:
+            sc[..., :st["n"]] += np.einsum("...hrw,hjw->...hrj", qt[..., st["a"]:st["b"]], _deq(st, stage_bits))
+    return sc
+
+
+def coded_values(pv: np.ndarray, packed: Dict, stage_bits: Sequence[int], R: int) -> np.ndarray:
+    """QuasarState.coded_values' torch path (QUASAR_KV.py:1931-1941) in float64: pv (..., Hkv, rows, n_c)
+    -> (..., Hkv, rows, R), per value-side step the tokens' weights times their levels, into the band."""
+    acc = np.zeros(pv.shape[:-1] + (R,))
+    for st in packed["steps"]:
+        if st["side"] == 1:
+            acc[..., st["a"]:st["b"]] += np.einsum("...hrj,hjw->...hrw", pv[..., :st["n"]], _deq(st, stage_bits))
+    return acc
+
+
 def attend(q: np.ndarray, scaling: float, qpos: np.ndarray, K: np.ndarray, V: np.ndarray, n0: int, H: int,
            packed: Dict, stage_bits: Sequence[int]) -> np.ndarray:
     """QuasarState.attend (QUASAR_KV.py:1945-1968) in float64 for B = 1.
@@ -141,10 +162,7 @@ def attend(q: np.ndarray, scaling: float, qpos: np.ndarray, K: np.ndarray, V: np
     if n_c > 0:
         Tk = np.asarray(packed["T_k"], dtype=np.float64)
         qt = np.einsum("bhrd,hdk->bhrk", qg, Tk)
-        sc = np.zeros((B, Hkv, rep * Tq, n_c))
-        for st in packed["steps"]:
-            if st["side"] == 0:
-                sc[..., :st["n"]] += np.einsum("bhrw,hjw->bhrj", qt[..., st["a"]:st["b"]], _deq(st, stage_bits))
+        sc = coded_scores(qt, packed, stage_bits)
         rho_k = np.asarray(packed["rho_k"], dtype=np.float64)
         mu_k = np.asarray(packed["mu_k"], dtype=np.float64)
         sc = (sc * rho_k[None, :, None, :] + np.einsum("bhrd,hd->bhr", qg, mu_k)[..., None]) * scaling
@@ -161,22 +179,16 @@ def attend(q: np.ndarray, scaling: float, qpos: np.ndarray, K: np.ndarray, V: np
         Tv = np.asarray(packed["T_v"], dtype=np.float64)
         mu_v = np.asarray(packed["mu_v"], dtype=np.float64)
         pv = pc * rho_v[None, :, None, :]
-        acc = np.zeros((B, Hkv, rep * Tq, Tv.shape[-1]))
-        for st in packed["steps"]:
-            if st["side"] == 1:
-                acc[..., st["a"]:st["b"]] += np.einsum("bhrj,hjw->bhrw", pv[..., :st["n"]], _deq(st, stage_bits))
+        acc = coded_values(pv, packed, stage_bits, Tv.shape[-1])
         o = o + np.einsum("bhrk,hdk->bhrd", acc, Tv) + pc.sum(-1, keepdims=True) * mu_v[None, :, None, :]
     return o.reshape(B, Hq, Tq, d).transpose(0, 2, 1, 3)
 
 
-def reconstruct(packed: Dict, side: int, stage_bits: Sequence[int]) -> np.ndarray:
-    """The coded tokens of a side as a reader of the code sees them (QuasarMethod.reconstruct,
-    1715-1733): mu + (rho u_hat) T^T, u_hat_j the sum of the levels of every step token j owns.
-    Decoded code by code (shift and mask), not through the byte table."""
-    nm = "k" if side == 0 else "v"
-    T = np.asarray(packed[f"T_{nm}"], dtype=np.float64)
-    Hkv, d, R = T.shape
+def coefficients(packed: Dict, side: int, stage_bits: Sequence[int], R: int) -> np.ndarray:
+    """u_hat (Hkv, n_c, R) of a side: per token, the sum of the levels of every step it owns, decoded
+    code by code (shift and mask), not through the byte table."""
     n_c = int(packed["n_c"])
+    Hkv = np.asarray(packed["steps"][0]["codes"]).shape[0]
     u = np.zeros((Hkv, n_c, R))
     books = stage_codebooks(tuple(stage_bits))
     for st in packed["steps"]:
@@ -188,6 +200,15 @@ def reconstruct(packed: Dict, side: int, stage_bits: Sequence[int]) -> np.ndarra
         shifts = (per - 1 - np.arange(per)) * b
         codes = ((raw[..., None] >> shifts) & ((1 << b) - 1)).reshape(Hkv, st["n"], -1)
         u[:, :st["n"], st["a"]:st["b"]] += books[st["stage"]].astype(np.float64)[codes]
+    return u
+
+
+def reconstruct(packed: Dict, side: int, stage_bits: Sequence[int]) -> np.ndarray:
+    """The coded tokens of a side as a reader of the code sees them (QuasarMethod.reconstruct,
+    1715-1733): mu + (rho u_hat) T^T, u_hat (``coefficients``) decoded code by code."""
+    nm = "k" if side == 0 else "v"
+    T = np.asarray(packed[f"T_{nm}"], dtype=np.float64)
+    u = coefficients(packed, side, stage_bits, T.shape[-1])
     rho = np.asarray(packed[f"rho_{nm}"], dtype=np.float64)
     mu = np.asarray(packed[f"mu_{nm}"], dtype=np.float64)
     return mu[:, None, :] + np.einsum("hjk,hdk->hjd", rho[..., None] * u, T)

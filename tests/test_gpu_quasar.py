@@ -101,3 +101,37 @@ def test_quasar_reference_packed_layer():
     err = float(np.abs(got - out).max() / np.abs(out).max())
     print(f"GPU QUASAR decode vs the reference on its own packed layer: {err:.2e}", flush=True)
     assert err < 2e-3, err
+
+
+@pytest.mark.parametrize("stages", [(2, 2, 4), (4, 4), (8,)])
+def test_quasar_scores_and_values_wrappers(stages):
+    """kvq.quasar_scores / quasar_values with the reference's call shapes (QUASAR_KV.py:1556-1577):
+    on a QuasarState's own sides and on a side laid out as the reference's QuasarState holds it (step
+    table on the device, concatenated levels), against the oracle's per-step products (float64) at
+    rtol 1e-5 of the largest entry; n_c crosses a 1024-token chunk of the values partials."""
+    import kvq
+    from kvq.quasar import synthetic_packed
+    Hkv, n_c, rows = 2, 2500, 6
+    p = synthetic_packed(Hkv, 128, n_c, stages=stages, seed=9)
+    K = torch.zeros((1, Hkv, 4, 128), device="cuda")
+    st = kvq.QuasarState(K, K, p, stages, 2, 100)
+    R = st.T_k.shape[-1]
+    g = torch.Generator().manual_seed(3)
+    qt = torch.randn((Hkv, rows, R), generator=g)
+    pv = torch.rand((Hkv, rows, n_c), generator=g)
+    want_s = oq.coded_scores(qt.double().numpy(), p, stages)
+    want_v = oq.coded_values(pv.double().numpy(), p, stages, R)
+    ref_side = lambda s_: {"flat": st.sides[s_]["flat"], "table": st.sides[s_]["table"],      # device table
+                           "levels": torch.cat([torch.from_numpy(b) for b in kvq.stage_codebooks(stages)]).cuda(),
+                           "W": 128}
+    for side0, side1 in ((st.sides[0], st.sides[1]), (ref_side(0), ref_side(1))):
+        got_s = kvq.quasar_scores(qt.cuda(), side0, n_c).cpu().numpy()
+        got_v = kvq.quasar_values(pv.cuda(), side1, R).cpu().numpy()
+        assert got_s.shape == (Hkv, rows, n_c) and got_v.shape == (Hkv, rows, R)
+        assert np.abs(got_s - want_s).max() <= 1e-5 * np.abs(want_s).max()
+        assert np.abs(got_v - want_v).max() <= 1e-5 * np.abs(want_v).max()
+    # a step table that points past the code buffer is refused before any launch
+    bad = dict(st.sides[0], table_np=st.sides[0]["table_np"].copy())
+    bad["table_np"][0, 0] = st.sides[0]["flat"].numel()
+    with pytest.raises(kvq.KVQError, match="leave the buffer"):
+        kvq.quasar_scores(qt.cuda(), bad, n_c)

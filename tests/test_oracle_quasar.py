@@ -85,3 +85,24 @@ def test_step_checks():
     p["steps"][2]["n"], p["steps"][4]["n"] = 10, 90         # K side: n_s grows again
     with pytest.raises(ValueError):
         kq._side_buffers(p, 0, (2, 2, 4), "cpu")
+
+
+@pytest.mark.parametrize("stages", [(2, 2, 4), (4, 4), (8,)])
+def test_coded_products_equal_products_with_the_decoded_coefficients(stages):
+    """coded_scores / coded_values (the per-step byte-table path of QUASAR_KV.py:1920-1941) equal the
+    plain products with the coefficients decoded code by code (shift and mask): qt u^T and pv u.
+    A step whose band is shifted by one coefficient fails both."""
+    from kvq.quasar import synthetic_packed
+    p = synthetic_packed(2, 128, 257, stages=stages, seed=4)
+    rng = np.random.default_rng(2)
+    R = np.asarray(p["T_k"]).shape[-1]
+    qt = rng.standard_normal((2, 5, R))
+    pv = rng.random((2, 5, 257))
+    uk, uv = oq.coefficients(p, 0, stages, R), oq.coefficients(p, 1, stages, R)
+    np.testing.assert_allclose(oq.coded_scores(qt, p, stages), np.einsum("hrk,hjk->hrj", qt, uk), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(oq.coded_values(pv, p, stages, R), np.einsum("hrj,hjk->hrk", pv, uv), rtol=1e-12,
+                               atol=1e-12)
+    bad = dict(p, steps=[dict(st, a=st["a"] + 1, b=st["b"] + 1) if i == 0 else st for i, st in enumerate(p["steps"])])
+    bad_k = dict(bad, steps=[st for st in bad["steps"] if st["side"] == 0] + [st for st in p["steps"] if st["side"] == 1])
+    assert np.abs(oq.coded_scores(np.pad(qt, [(0, 0), (0, 0), (0, 1)]), bad_k, stages)[..., :]
+                  - np.einsum("hrk,hjk->hrj", qt, uk)).max() > 1e-3
