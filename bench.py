@@ -502,7 +502,9 @@ def run_strata(args) -> dict:
     if not args.no_cpu_baseline:
         import oracle.strata as os_
         Rm = os_.rotation_matrix(s.d)
-        times = []
+        step()
+        gpu_out = out.float().cpu().numpy()                                           # (B, 1, Hq, d)
+        times, errs = [], []
         for b in range(s.B):
             tiers = []
             for t in cache.tiers:
@@ -511,16 +513,19 @@ def run_strata(args) -> dict:
             qb_ = q[b:b + 1].float().cpu().numpy()
             empty = np.zeros((s.Hkv, 0, s.d))
             t0 = time.perf_counter()
-            os_.strata_attend(qb_, scaling, empty, empty, tiers, cache.mu_k[b].float().cpu().numpy(),
-                              cache.mu_v[b].float().cpu().numpy(), Rm)
+            o = os_.strata_attend(qb_, scaling, empty, empty, tiers, cache.mu_k[b].float().cpu().numpy(),
+                                  cache.mu_v[b].float().cpu().numpy(), Rm)
             times.append(time.perf_counter() - t0)
-            if sum(times) >= args.cpu_seconds and len(times) >= 1:
+            errs.append(float(np.abs(gpu_out[b] - o[0]).max()))
+            if sum(times) >= args.cpu_seconds and len(times) >= 2:
                 break
         t = float(np.median(times)) * s.B
         res["cpu_baseline"] = {"value": bytes_alg / t / 1e9, "unit": "GB/s", "cores": _threads(), "kind": "port",
                                "us_per_layer": t * 1e6,
                                "sample": f"{len(times)} of {s.B} sequences (all 8 KV heads each); median x {s.B}; "
                                          f"numpy tier_reference per stratum + merge (float64)"}
+        res["parity"] = _parity_block(errs, 1e-2, "oracle.strata strata_attend (tier_reference per stratum + merge, "
+                                                  "float64) over the device's stored strata, whole sequences")
     return res
 
 
@@ -655,15 +660,19 @@ def run_quasar(args) -> dict:
         import oracle.quasar as oq
         qn = q.float().cpu().numpy()
         Kn, Vn = K.float().cpu().numpy(), V.float().cpu().numpy()
+        step()
+        gpu_out = out.float().cpu().numpy()
         times = []
         while sum(times) < args.cpu_seconds or len(times) < 2:
             t0 = time.perf_counter()
-            oq.attend(qn, scaling, np.array([H]), Kn, Vn, QUASAR_N0, H, packed, stages)
+            ref = oq.attend(qn, scaling, np.array([H]), Kn, Vn, QUASAR_N0, H, packed, stages)
             times.append(time.perf_counter() - t0)
         t = float(np.median(times))
         res["cpu_baseline"] = {"value": t * 1e6, "unit": "us", "cores": _threads(), "kind": "port",
                                "sample": f"the whole step, {len(times)} runs, median; numpy float64 restatement of "
                                          "QuasarState.attend (byte-table gather + matmul per step)"}
+        res["parity"] = _parity_block([float(np.abs(gpu_out - ref).max())], 1e-2,
+                                      "oracle.quasar attend (QuasarState.attend restated in float64), the whole step")
     return res
 
 
