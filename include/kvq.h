@@ -265,6 +265,24 @@ int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const int32_t* row
  * k_out, v_out, k_lo and k_sc 16-byte aligned; out_bh a multiple of 8 (so a caller can write
  * the rows straight into a larger buffer that also holds the window).
  * ---------------------------------------------------------------------------------------- */
+/* Decode over the retained set straight from the packed cache (the gather and the exact-row decode
+ * fused): attention of q over the packed positions idx[bh][0..n_ret) (idx_bh stride; each row read
+ * and dequantised in registers, code * scale + lo in fp32 as kivi_quant's xhat, STRATA_KV.py:855;
+ * a position outside [0, n_q) counts as a masked row) and the n_exact exact rows (the window, with
+ * the exact_pos / q_pos rule of kvq_kivi_decode) -- the LayerState.attend over an MTLP / SnapKV
+ * selection of a KIVI cache (STRATA_KV.py:682-719, 1010-1033) without writing the kept rows out.
+ * Cache fields as kvq_kivi_decode; key metadata 16-byte aligned.  workspace >=
+ * kvq_kivi_retained_workspace(...) floats; one retained/exact-row launch plus the merge. */
+int64_t kvq_kivi_retained_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, int64_t n_ret,
+                                    int64_t n_exact);
+int kvq_kivi_decode_retained(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int64_t B,
+                             int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling, const uint8_t* kc,
+                             const uint16_t* k_lo, const uint16_t* k_sc, const uint8_t* vc, const uint16_t* vmeta,
+                             int64_t cap_t, int64_t n_q, int group_k, int group_v, const int32_t* idx, int64_t n_ret,
+                             int64_t idx_bh, const void* k_exact, const void* v_exact, int exact_dtype,
+                             int64_t cap_e, int64_t n_exact, const int64_t* exact_pos, const int64_t* q_pos,
+                             void* out, int out_dtype, float* workspace, int64_t workspace_floats, void* stream);
+
 int kvq_kivi_gather_dequant(const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_sc,
                             const uint8_t* vc, const uint16_t* vmeta, int64_t cap_t, int64_t n_valid,
                             int group_k, int group_v, int64_t BH, int64_t d, const int32_t* idx,

@@ -123,6 +123,11 @@ struct DecodeParams {
   int exact_rows;                     // rows of each exact-row block
   int BH;
   void* out;
+  int ex_po0;                         // partial index of exact-row block 0 (after the retained-row blocks)
+  const int32_t* ret_idx;             // retained decode: (BH, ret_bh) positions into the packed rows
+  int64_t ret_bh;
+  int n_ret;                          // retained positions per (b, h)
+  int ret_wg;                         // retained-row blocks per (b, h)
 };
 
 // Row r of KV head h is (query head h*rep + r/Tq, position t = r%Tq).
@@ -146,15 +151,89 @@ __device__ void load_q_rows(const DecodeParams& p, int b, int h, float (*qs)[kD]
 // ---------------------------------------------------------------------------------------------
 // exact rows: fp32 attention over rows [e0, e1) of the residual buffer (e0 = sidx * exact_rows)
 
+constexpr float kRowLazy = 4.0f;
+
+// One row of a lane group (16 lanes, 8 channels each) into the group's base-2 online softmax of
+// every query row r whose bit is set in `vis`: the logit's 16-lane sum, a lazy maximum (rescaled
+// only when a logit exceeds it by more than kRowLazy), the probability-weighted values.
+template <int R>
+__device__ __forceinline__ void attend_row(const float (&qv)[R][8], const float (&kx)[8], const float (&vx)[8],
+                                           uint32_t vis, float (&m)[R], float (&l)[R], float (&o)[R][8]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s = __builtin_fmaf(qv[r][k], kx[k], s);
+    s = row_sum16(s);
+    if (!((vis >> r) & 1u)) s = -INFINITY;
+    if (s > m[r] + kRowLazy) {                       // m[r] = -inf: first visible row
+      const float a = __builtin_amdgcn_exp2f(m[r] - s);
+      l[r] *= a;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[r][k] *= a;
+      m[r] = s;
+    }
+    const float pr = s == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s - m[r]);
+    l[r] += pr;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[r][k] = __builtin_fmaf(pr, vx[k], o[r][k]);
+  }
+}
+
+// The 16 lane-group states of a block meet (shuffles within a wavefront, then the wavefronts in
+// LDS) and the block's partial (m, l, o) of each real query row is written at partial index po.
+template <int R>
+__device__ __forceinline__ void rows_epilogue(const DecodeParams& p, int64_t po, float (&m)[R], float (&l)[R],
+                                              float (&o)[R][8], float* red_o, float* red_ml, int wave, int lane,
+                                              int j, int part) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float M = m[r];
+    M = xmax32(xmax16(M));
+    const float w = m[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[r] - M);
+    float L = l[r] * w;
+    L = xsum32(xsum16(L));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float t = o[r][k] * w;
+      t = xsum32(xsum16(t));
+      if (j == 0) red_o[(wave * R + r) * kD + 8 * part + k] = t;
+    }
+    if (lane == 0) {
+      red_ml[(wave * 2) * R + r] = M;
+      red_ml[(wave * 2 + 1) * R + r] = L;
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < p.R_real * kD; idx += kThreads) {
+    const int r = idx / kD, c = idx % kD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_ml[(w * 2) * R + r]);
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw_ = red_ml[(w * 2) * R + r];
+      const float wgt = (mw_ == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw_ - M);
+      O += wgt * red_o[(w * R + r) * kD + c];
+      L += wgt * red_ml[(w * 2 + 1) * R + r];
+    }
+    p.ws_o[(po * R + r) * kD + c] = O;
+    if (c == 0) {
+      p.ws_m[po * R + r] = M;
+      p.ws_l[po * R + r] = L;
+    }
+  }
+}
+
 // Partial (m, l, o) of exact-row block `sidx`.  Each wavefront streams a contiguous quarter of the
 // block's rows, four at a time: lane group j = lane / 16 takes one row, 8 channels per lane
 // (coalesced 16-byte loads, kept raw until used), the loads of the next three row quads in flight
-// while one is computed.  Every
-// lane group keeps its own base-2 online softmax per query row (lazy maximum: rescaled only when a
-// logit exceeds it by more than kLazy); the 16 states of the block are merged at the end.
+// while one is computed.  Every lane group keeps its own base-2 online softmax per query row; the
+// 16 states of the block are merged at the end.  The partial goes to index ex_po0 + sidx of the
+// (b, h)'s S1 partials.
 template <int R, int DT>
 __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem) {
-  constexpr float kLazy = 4.0f;
   const int b = bh / p.Hkv, h = bh % p.Hkv;
   float (*qs)[kD] = reinterpret_cast<float (*)[kD]>(smem);
   float* red_o = smem + R * kD;                     // [wave][R][kD]
@@ -211,25 +290,10 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
     float kx[8], vx[8];
     to_f32(x.kw, kx);
     to_f32(x.vw, vx);
+    uint32_t vis = 0u;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float s = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) s = __builtin_fmaf(qv[r][k], kx[k], s);
-      s = row_sum16(s);
-      if (i >= w1 || (masked && x.pos > qp[r])) s = -INFINITY;
-      if (s > m[r] + kLazy) {                        // m[r] = -inf: first visible row
-        const float a = __builtin_amdgcn_exp2f(m[r] - s);
-        l[r] *= a;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) o[r][k] *= a;
-        m[r] = s;
-      }
-      const float pr = s == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s - m[r]);
-      l[r] += pr;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) o[r][k] = __builtin_fmaf(pr, vx[k], o[r][k]);
-    }
+    for (int r = 0; r < R; ++r) vis |= (i < w1 && !(masked && x.pos > qp[r])) ? (1u << r) : 0u;
+    attend_row<R>(qv, kx, vx, vis, m, l, o);
   };
   // the first four row quads of the wavefront go out before the query rows are staged, so the
   // block waits for one round of loads, not two
@@ -264,46 +328,121 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
       if (i0 + 16 >= w1) break;
     }
   }
-  // the four lane groups' states of each row meet by shuffles, then the wavefronts' in LDS
+  rows_epilogue<R>(p, static_cast<int64_t>(bh) * p.S1 + p.ex_po0 + sidx, m, l, o, red_o, red_ml, wave, lane, j,
+                   part);
+}
+
+// Partial of retained-row block `sidx`: rows [sidx * exact_rows, ...) of the (b, h)'s retained
+// positions ret_idx, read straight from the packed cache and dequantised in registers exactly as
+// kivi_quant's xhat (code * scale + lo in fp32: two roundings, STRATA_KV.py:855) -- the eviction
+// path's decode over the kept tokens without writing them out first.  Lane group j takes a token,
+// lane `part` its channels 8 part .. 8 part + 7: the key codes' 4 bytes of the token's pack_codes
+// row, the 16 bytes of key scale and zero of those channels in the token's key group, the token's
+// 8 words of the value tile (one per channel: 8 tokens of a channel each) and its (scale, lo) word
+// of the channel group.  A position outside [0, n_q) counts as a masked row (its loads read
+// position 0).  The wavefront's indices are loaded first; each row quad's loads depend on them
+// only.
+__device__ __constant__ int kNibbleOfSlotD[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+
+template <int R, int DT>
+__device__ void retained_block(const DecodeParams& p, int bh, int sidx, float* smem) {
+  const int b = bh / p.Hkv, h = bh % p.Hkv;
+  float (*qs)[kD] = reinterpret_cast<float (*)[kD]>(smem);
+  float* red_o = smem + R * kD;
+  float* red_ml = red_o + kWaves * R * kD;
+  const int e0 = sidx * p.exact_rows;
+  const int e1 = min(e0 + p.exact_rows, p.n_ret);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+  const int j = lane >> 4, part = lane & 15;
+  const int w0 = e0 + (e1 - e0) * wave / kWaves, w1 = e0 + (e1 - e0) * (wave + 1) / kWaves;
+  const int G = p.group_k;
+  const int ngv = kD / p.group_v;
+  const int32_t* ridx = p.ret_idx + static_cast<int64_t>(bh) * p.ret_bh;
+  const uint8_t* kc = p.kc + static_cast<int64_t>(bh) * p.cap_t * (kD / 2);
+  const uint16_t* ksc = p.k_sc + static_cast<int64_t>(bh) * (p.cap_t / G) * kD;
+  const uint16_t* klo = p.k_lo + static_cast<int64_t>(bh) * (p.cap_t / G) * kD;
+  const uint8_t* vc = p.vc + static_cast<int64_t>(bh) * p.cap_t * (kD / 2);
+  const uint16_t* vm = p.vmeta + static_cast<int64_t>(bh) * (p.cap_t / 32) * ngv * 64;
+  float qv[R][8];
+  float m[R], l[R], o[R][8];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float M = m[r];
-    M = xmax32(xmax16(M));
-    const float w = m[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[r] - M);
-    float L = l[r] * w;
-    L = xsum32(xsum16(L));
+    m[r] = -INFINITY;
+    l[r] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[r][k] = 0.0f;
+  }
+  struct Tok {
+    uint32_t kw, vw[8], vmw;
+    uint4 sc4, lo4;
+    int t;                                       // the position, or -1 for a masked row
+  };
+  // the positions of this wavefront's rows, lane group j holding rows w0 + j + 4 u
+  constexpr int kMaxU = 16;                      // rows per lane group held in registers (64 per wavefront)
+  auto pos_of = [&](int i) -> int {
+    if (i >= w1) return -1;
+    const int t = ridx[i];
+    return (t >= 0 && t < p.n_q) ? t : -1;
+  };
+  auto load_tok = [&](int t, Tok& x) {
+    x.t = t;
+    const int tt = t < 0 ? 0 : t;
+    x.kw = *reinterpret_cast<const uint32_t*>(kc + static_cast<int64_t>(tt) * (kD / 2) + 4 * part);
+    const int64_t km = static_cast<int64_t>(tt / G) * kD + 8 * part;
+    x.sc4 = *reinterpret_cast<const uint4*>(ksc + km);
+    x.lo4 = *reinterpret_cast<const uint4*>(klo + km);
+    const int chunk = tt / 32, u = tt % 32;
+    const int g = (u % 16) / 4, jj = 4 * (u / 16) + (u % 4);
+    const int blk = part / 2;
+    const uint32_t* tile = reinterpret_cast<const uint32_t*>(vc + static_cast<int64_t>(chunk) * 16 * kD) +
+                           (blk / 4) * 256 + (16 * g + 8 * (part % 2)) * 4 + (blk % 4);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x.vw[e] = tile[4 * e];
+    x.vmw = *reinterpret_cast<const uint32_t*>(vm + ((static_cast<int64_t>(chunk) * ngv + (8 * part) / p.group_v) * 64 +
+                                                      (8 * g + jj) * 2));
+  };
+  auto attend = [&](const Tok& x) {
+    float kx[8], vx[8];
+    const uint32_t scw[4] = {x.sc4.x, x.sc4.y, x.sc4.z, x.sc4.w}, low[4] = {x.lo4.x, x.lo4.y, x.lo4.z, x.lo4.w};
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      float t = o[r][k] * w;
-      t = xsum32(xsum16(t));
-      if (j == 0) red_o[(wave * R + r) * kD + 8 * part + k] = t;
+      const uint32_t byte = (x.kw >> (8 * (k / 2))) & 0xffu;
+      const int code = (k & 1) ? static_cast<int>(byte & 15u) : static_cast<int>(byte >> 4);
+      const float sc = f16_to_f32(static_cast<uint16_t>(scw[k / 2] >> (16 * (k & 1))));
+      const float lo = f16_to_f32(static_cast<uint16_t>(low[k / 2] >> (16 * (k & 1))));
+      kx[k] = __fadd_rn(__fmul_rn(static_cast<float>(code), sc), lo);
     }
-    if (lane == 0) {
-      red_ml[(wave * 2) * R + r] = M;
-      red_ml[(wave * 2 + 1) * R + r] = L;
-    }
-  }
+    const int u = (x.t < 0 ? 0 : x.t) % 32;
+    const int jj = 4 * (u / 16) + (u % 4);
+    const int shift = 4 * kNibbleOfSlotD[jj];
+    const float sv = f16_to_f32(static_cast<uint16_t>(x.vmw & 0xffffu));
+    const float lv = f16_to_f32(static_cast<uint16_t>(x.vmw >> 16));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vx[e] = __fadd_rn(__fmul_rn(static_cast<float>((x.vw[e] >> shift) & 15u), sv), lv);
+    attend_row<R>(qv, kx, vx, x.t >= 0 ? 0xffffffffu : 0u, m, l, o);
+  };
+  const int n_u = w0 < w1 ? (w1 - w0 + 3) / 4 : 0;     // row quads of the wavefront
+  int tpos[kMaxU];
+#pragma unroll
+  for (int u = 0; u < kMaxU; ++u) tpos[u] = u < n_u ? pos_of(w0 + 4 * u + j) : -1;
+  Tok x0, x1;
+  if (n_u > 0) load_tok(tpos[0], x0);
+  load_q_rows<R, DT>(p, b, h, qs);
   __syncthreads();
-  const int64_t po = static_cast<int64_t>(bh) * p.S1 + sidx;
-  for (int idx = threadIdx.x; idx < p.R_real * kD; idx += kThreads) {
-    const int r = idx / kD, c = idx % kD;
-    float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_ml[(w * 2) * R + r]);
-    float O = 0.0f, L = 0.0f;
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float mw_ = red_ml[(w * 2) * R + r];
-      const float wgt = (mw_ == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw_ - M);
-      O += wgt * red_o[(w * R + r) * kD + c];
-      L += wgt * red_ml[(w * 2 + 1) * R + r];
-    }
-    p.ws_o[(po * R + r) * kD + c] = O;
-    if (c == 0) {
-      p.ws_m[po * R + r] = M;
-      p.ws_l[po * R + r] = L;
-    }
+    for (int k = 0; k < 8; ++k) qv[r][k] = qs[r][8 * part + k];
+#pragma unroll
+  for (int u = 0; u < kMaxU; u += 2) {
+    if (u >= n_u) break;
+    if (u + 1 < n_u) load_tok(tpos[u + 1], x1);
+    attend(x0);
+    if (u + 1 >= n_u) break;
+    if (u + 2 < n_u) load_tok(tpos[u + 2], x0);
+    attend(x1);
   }
+  rows_epilogue<R>(p, static_cast<int64_t>(bh) * p.S1 + sidx, m, l, o, red_o, red_ml, wave, lane, j, part);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -968,6 +1107,19 @@ __global__ __launch_bounds__(kThreads) void kivi_decode_exact(DecodeParams p) {
   if (bh < p.BH) exact_block<R, DT>(p, bh, k % p.n_exact_wg, smem);
 }
 
+// Retained decode of the eviction path: the retained-row blocks of every (b, h), then its exact-row
+// blocks (the window), S1 = ret_wg + n_exact_wg partials per (b, h); XCD-aware as the exact launch.
+template <int R, int DT>
+__global__ __launch_bounds__(kThreads) void kivi_decode_retained(DecodeParams p) {
+  extern __shared__ float smem[];
+  const int k = blockIdx.x / 8;
+  const int bh = blockIdx.x % 8 + 8 * (k / p.S1);
+  const int s = k % p.S1;
+  if (bh >= p.BH) return;
+  if (s < p.ret_wg) retained_block<R, DT>(p, bh, s, smem);
+  else exact_block<R, DT>(p, bh, s - p.ret_wg, smem);
+}
+
 // Score pass of the eviction path: packed blocks only, same split grid and mapping.
 template <int R, int GV, int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(split_waves<R, GV>())))
@@ -1265,6 +1417,119 @@ extern "C" int kvq_kivi_decode(const void* q, int q_dtype, int64_t q_sb, int64_t
   }
 #undef KVQ_R
 #undef KVQ_GV
+}
+
+namespace kvq {
+namespace {
+// Rows per block of a retained decode (one plan for the retained rows and the window: about one
+// round of workgroups over the (b, h), at most 64 rows a wavefront) and the blocks of each part.
+struct RetainedPlan {
+  int rows, ret_wg, ex_wg, R;
+};
+inline RetainedPlan plan_retained(int64_t BH, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t n_ret, int64_t n_exact) {
+  RetainedPlan rp;
+  rp.R = pow2_rows((Hq / Hkv) * Tq);
+  int rows = 0;
+  plan_exact_blocks(BH, n_ret + n_exact, &rows);
+  rows = std::max(16, std::min(rows, 256));
+  rp.rows = rows;
+  rp.ret_wg = static_cast<int>((n_ret + rows - 1) / rows);
+  rp.ex_wg = static_cast<int>((n_exact + rows - 1) / rows);
+  return rp;
+}
+}  // namespace
+}  // namespace kvq
+
+extern "C" int64_t kvq_kivi_retained_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d,
+                                               int64_t n_ret, int64_t n_exact) {
+  if (d != kD || B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Tq <= 0 || n_ret < 0 || n_exact < 0 || n_ret + n_exact == 0)
+    return -1;
+  const RetainedPlan rp = plan_retained(B * Hkv, Hq, Hkv, Tq, n_ret, n_exact);
+  return B * Hkv * (static_cast<int64_t>(rp.ret_wg + rp.ex_wg) * rp.R * (kD + 2) + 2 * rp.R);
+}
+
+extern "C" int kvq_kivi_decode_retained(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                                        int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t d, float scaling,
+                                        const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_sc,
+                                        const uint8_t* vc, const uint16_t* vmeta, int64_t cap_t, int64_t n_q,
+                                        int group_k, int group_v, const int32_t* idx, int64_t n_ret, int64_t idx_bh,
+                                        const void* k_exact, const void* v_exact, int exact_dtype, int64_t cap_e,
+                                        int64_t n_exact, const int64_t* exact_pos, const int64_t* q_pos, void* out,
+                                        int out_dtype, float* workspace, int64_t workspace_floats, void* stream) {
+  KVQ_REQUIRE(d == kD, "kvq_kivi_decode_retained: head_dim must be 128 (got %lld)", (long long)d);
+  KVQ_REQUIRE(valid_dtype(q_dtype) && q_dtype == exact_dtype && q_dtype == out_dtype,
+              "kvq_kivi_decode_retained: q, exact rows and output must share one dtype");
+  KVQ_REQUIRE(B > 0 && Hkv > 0 && Hq % Hkv == 0 && Tq > 0, "kvq_kivi_decode_retained: bad head counts");
+  const int64_t R_real = (Hq / Hkv) * Tq;
+  KVQ_REQUIRE(R_real <= 8, "kvq_kivi_decode_retained: rep*Tq must be <= 8 (got %lld)", (long long)R_real);
+  KVQ_REQUIRE(group_k % 32 == 0 && group_k > 0, "kvq_kivi_decode_retained: group_k must be a multiple of 32");
+  KVQ_REQUIRE(group_v == 32 || group_v == 64 || group_v == 128, "kvq_kivi_decode_retained: group_v in {32,64,128}");
+  KVQ_REQUIRE(cap_t % group_k == 0 && cap_t % 32 == 0 && n_q >= 0 && n_q <= cap_t && n_q < (1LL << 31),
+              "kvq_kivi_decode_retained: cap_t must be a multiple of group_k and 32, 0 <= n_q <= cap_t");
+  KVQ_REQUIRE(n_ret >= 0 && n_ret < (1LL << 31) && idx_bh >= n_ret, "kvq_kivi_decode_retained: bad retained count");
+  KVQ_REQUIRE(n_exact >= 0 && n_exact <= cap_e && n_exact <= 65536, "kvq_kivi_decode_retained: bad n_exact");
+  KVQ_REQUIRE(n_ret + n_exact > 0, "kvq_kivi_decode_retained: empty cache");
+  KVQ_REQUIRE(n_ret == 0 || (kc && k_lo && k_sc && vc && vmeta && idx), "kvq_kivi_decode_retained: null packed cache");
+  // a masked retained row still loads position 0, so a retained set needs a non-empty cache
+  KVQ_REQUIRE(n_ret == 0 || cap_t >= 32, "kvq_kivi_decode_retained: retained rows over an empty packed cache");
+  KVQ_REQUIRE(n_ret == 0 || (reinterpret_cast<uintptr_t>(k_lo) % 16 == 0 && reinterpret_cast<uintptr_t>(k_sc) % 16 == 0),
+              "kvq_kivi_decode_retained: key metadata must be 16-byte aligned");
+  KVQ_REQUIRE(n_exact == 0 || (k_exact && v_exact), "kvq_kivi_decode_retained: null exact rows");
+  KVQ_REQUIRE(n_exact == 0 || (reinterpret_cast<uintptr_t>(k_exact) % 16 == 0 &&
+                               reinterpret_cast<uintptr_t>(v_exact) % 16 == 0),
+              "kvq_kivi_decode_retained: exact rows must be 16-byte aligned");
+  KVQ_REQUIRE(q && out && workspace, "kvq_kivi_decode_retained: null q/out/workspace");
+  KVQ_REQUIRE((exact_pos == nullptr) == (q_pos == nullptr), "kvq_kivi_decode_retained: exact_pos and q_pos go together");
+  KVQ_REQUIRE(B * Hkv < 65536, "kvq_kivi_decode_retained: sizes out of range");
+  const RetainedPlan rp = plan_retained(B * Hkv, Hq, Hkv, Tq, n_ret, n_exact);
+  const int S1 = rp.ret_wg + rp.ex_wg;
+  const int64_t need = B * Hkv * (static_cast<int64_t>(S1) * rp.R * (kD + 2) + 2 * rp.R);
+  KVQ_REQUIRE(workspace_floats >= need, "kvq_kivi_decode_retained: workspace too small (%lld < %lld floats)",
+              (long long)workspace_floats, (long long)need);
+  DecodeParams p{};
+  p.q = q; p.q_sb = q_sb; p.q_sh = q_sh; p.q_st = q_st;
+  p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.Tq = (int)Tq; p.rep = (int)(Hq / Hkv); p.R_real = (int)R_real;
+  p.qscale = scaling * kLog2e;
+  p.kc = kc; p.k_lo = k_lo; p.k_sc = k_sc; p.vc = vc; p.vmeta = vmeta;
+  p.cap_t = cap_t; p.n_q = (int)n_q; p.group_k = group_k; p.group_v = group_v; p.ngv = (int)(kD / group_v);
+  p.k_exact = k_exact; p.v_exact = v_exact; p.cap_e = cap_e; p.n_exact = (int)n_exact;
+  p.exact_pos = exact_pos; p.q_pos = q_pos;
+  const int64_t nrow = B * Hkv * static_cast<int64_t>(S1) * rp.R;
+  p.ws_o = workspace;
+  p.ws_m = workspace + nrow * kD;
+  p.ws_l = p.ws_m + nrow;
+  p.row_ml = p.ws_l + nrow;
+  p.BH = static_cast<int>(B * Hkv);
+  p.S1 = S1;
+  p.exact_rows = rp.rows;
+  p.ex_po0 = rp.ret_wg;
+  p.ret_idx = idx; p.ret_bh = idx_bh; p.n_ret = (int)n_ret; p.ret_wg = rp.ret_wg;
+  p.out = out;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int bh_pad = (p.BH + 7) / 8 * 8;
+  const size_t smem = (rp.R * kD + kWaves * rp.R * kD + kWaves * 2 * rp.R) * sizeof(float);
+  const dim3 grid(static_cast<unsigned>(S1) * bh_pad);
+#define KVQ_RT(R_, DT_) hipLaunchKernelGGL((kivi_decode_retained<R_, DT_>), grid, dim3(kThreads), smem, s, p)
+#define KVQ_RT_R(DT_)                       \
+  switch (rp.R) {                           \
+    case 1: KVQ_RT(1, DT_); break;          \
+    case 2: KVQ_RT(2, DT_); break;          \
+    case 4: KVQ_RT(4, DT_); break;          \
+    default: KVQ_RT(8, DT_); break;         \
+  }
+  switch (q_dtype) {
+    case KVQ_F32: KVQ_RT_R(KVQ_F32) break;
+    case KVQ_F16: KVQ_RT_R(KVQ_F16) break;
+    default: KVQ_RT_R(KVQ_BF16) break;
+  }
+#undef KVQ_RT_R
+#undef KVQ_RT
+  KVQ_LAUNCH_CHECK("kvq_kivi_decode_retained");
+  MergeArgs ma{};
+  ma.ws_o = p.ws_o; ma.ws_m = p.ws_m; ma.ws_l = p.ws_l; ma.S = S1;
+  ma.Hq = p.Hq; ma.Hkv = p.Hkv; ma.Tq = p.Tq; ma.rep = p.rep; ma.R_real = p.R_real;
+  ma.out = out; ma.row_ml = p.row_ml;
+  return launch_merge_rows(ma, rp.R, p.BH, q_dtype, s);
 }
 
 extern "C" int kvq_kivi_decode_noalloc(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,

@@ -10,7 +10,7 @@ from .kivi import (kivi_quant, kivi_quant_stored, pack_codes, pack_rows, unpack_
 from .decode import PackedKIVICache, exact_rows_cache, kivi_decode, score_workspace_floats, workspace_floats
 from .state import DecodeCtl, KIVIState, PackedState, Router, payload_bytes, register, routed, router_attention
 from .evict import (chunk_share, fake_quant_tokens, finalize_chunk, gather_dequant, gather_rows, retained_cache,
-                    snapkv_scores, topk_retain, topk_workspace_words)
+                    retained_decode, retained_workspace_floats, snapkv_scores, topk_retain, topk_workspace_words)
 from .evict_state import EvictedState, MTLPState, mtlp_budget, mtlp_select, snapkv_keep, streaming_keep
 from .strata import (StrataCache, StrataTier, pack_planar, rotation_signs, strata_center_rotate, strata_decode,
                      strata_quantize, strata_quantize_planar, strata_v_tile, strata_workspace_floats, uniform_step,
@@ -36,5 +36,6 @@ __all__ = [
     "strata_allocate", "strata_distortion", "coverage_groups", "coverage_plan", "coverage_stats",
     "StrataCompressor", "rotation_matrix", "chunk_share", "fake_quant_tokens", "finalize_chunk", "gather_rows",
     "EvictedState", "MTLPState", "mtlp_budget", "mtlp_select", "snapkv_keep", "streaming_keep", "PackedState",
-    "exact_rows_cache", "quasar_scores", "quasar_values",
+    "exact_rows_cache", "quasar_scores", "quasar_values", "retained_decode",
+    "retained_workspace_floats",
 ]

@@ -73,6 +73,10 @@ SIGNATURES = {
     "kvq_kivi_append": (i32, [vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp, vp, i64,
                               vp, vp, vp, vp, vp, i64, i32, i32, vp]),
     "kvq_selftest_mfma_layout": (i32, [vp, vp, vp, vp]),
+    "kvq_kivi_retained_workspace": (i64, [i64, i64, i64, i64, i64, i64, i64]),
+    "kvq_kivi_decode_retained": (i32, [vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32, vp, vp, vp, vp, vp,
+                                       i64, i64, i32, i32, vp, i64, i64, vp, vp, i32, i64, i64, vp, vp, vp, i32,
+                                       vp, i64, vp]),
     "kvq_gather_rows": (i32, [vp, vp, i64, i64, i64, i64, vp, i64, i64, vp, vp, i64, vp]),
     "kvq_chunk_share_workspace": (i64, [i64, i64, i64]),
     "kvq_chunk_share": (i32, [vp, vp, i64, i64, i64, i64, vp, vp, i64, vp]),

@@ -250,3 +250,54 @@ def finalize_chunk(k: torch.Tensor, v: torch.Tensor, qref: torch.Tensor, method,
     gk, gv = gather_rows(k.float(), v.float(), idx)
     return {"k": fake_quant_tokens(gk, keep_bits), "v": fake_quant_tokens(gv, keep_bits),
             "b": torch.zeros((B, H, m), device=k.device), "idx": idx.to(torch.int64)}
+
+
+def retained_workspace_floats(q: torch.Tensor, cache: PackedKIVICache, idx: torch.Tensor) -> int:
+    """Floats of workspace one retained_decode launch of q (B, Hq, Tq, d) over idx (B, Hkv, k) needs
+    (Tq within one query-token piece)."""
+    B, Hq, Tq, d = q.shape
+    need = _lib.load().kvq_kivi_retained_workspace(B, Hq, cache.kc.shape[1], Tq, d, idx.shape[2], cache.n_exact)
+    if need < 0:
+        raise _lib.KVQError("kvq_kivi_retained_workspace rejected the shape")
+    return int(need)
+
+
+@torch.no_grad()
+def retained_decode(q: torch.Tensor, scaling: float, cache: PackedKIVICache, idx: torch.Tensor, *,
+                    q_pos: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                    workspace: torch.Tensor | None = None, chunk: int | None = None) -> torch.Tensor:
+    """Attention of q (B, Hq, Tq, d) over the retained packed positions idx (B, Hkv, k) int32 of the
+    cache and its exact rows (the recent window), read straight from the packed cache (libkvq
+    kvq_kivi_decode_retained: each kept token dequantised in registers, no gathered copy) ->
+    (B, Tq, Hq, d) in q's dtype.  The same attention as kivi_decode over retained_cache(cache, idx),
+    with the kept rows in fp32 rather than rounded to the model dtype.  Exact rows are visible per
+    q_pos / cache.exact_pos as in kivi_decode; any Tq (query-token pieces, kvq.query)."""
+    from .query import decode_in_pieces, query_pieces
+    _lib.require_gpu(q, idx)
+    B, Hq, Tq, d = q.shape
+    Hkv = cache.kc.shape[1]
+    _lib.check_q_cache(q, cache.kc.shape[0], Hkv, cache.kc.shape[3] * 2, "retained_decode")
+    if idx.dim() != 3 or idx.shape[:2] != (B, Hkv) or idx.dtype != torch.int32:
+        raise ValueError("idx must be int32 (B, Hkv, k)")
+    pieces = query_pieces(Hq // Hkv, Tq, chunk)
+    if len(pieces) > 1:
+        return decode_in_pieces(lambda qs, qp, o: retained_decode(qs, scaling, cache, idx, q_pos=qp, out=o,
+                                                                  workspace=workspace), q, q_pos, out, pieces)
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if cache.k_exact.dtype != q.dtype:
+        raise TypeError("q and the exact rows must share a dtype")
+    idx = idx.contiguous()
+    k = idx.shape[2]
+    if workspace is None:
+        workspace = torch.empty((retained_workspace_floats(q, cache, idx),), dtype=torch.float32, device=q.device)
+    out = _lib.out_or_new(out, (B, Tq, Hq, d), q.dtype, q.device, "retained_decode")
+    ep = cache.exact_pos if q_pos is not None else None
+    qp = q_pos if ep is not None else None
+    dt = _lib.DTYPE_CODE[q.dtype]
+    _lib.call("kvq_kivi_decode_retained", q.data_ptr(), dt, q.stride(0), q.stride(1), q.stride(2), B, Hq, Hkv, Tq, d,
+              float(scaling), cache.kc.data_ptr(), cache.k_lo.data_ptr(), cache.k_sc.data_ptr(), cache.vc.data_ptr(),
+              cache.vmeta.data_ptr(), cache.cap_t, cache.n_q, cache.group_k, cache.group_v, idx.data_ptr(), k, k,
+              cache.k_exact.data_ptr(), cache.v_exact.data_ptr(), dt, cache.cap_e, cache.n_exact, _lib.ptr(ep),
+              _lib.ptr(qp), out.data_ptr(), dt, workspace.data_ptr(), workspace.numel(), _lib.stream_of(q))
+    return out

@@ -223,3 +223,63 @@ def test_c4_reduced_eviction_end_to_end(dtype):
     ref_out = chunked_attention(q.float().numpy(), d ** -0.5, np.array([T]), kk, vv, np.zeros(kk.shape[2], int),
                                 np.full(kk.shape[2], 1 << 40), None)
     assert float(np.abs(out - ref_out).max()) <= tol_out
+
+
+@pytest.mark.parametrize("Hq,Hkv,Tq,dtype,k", [(16, 4, 1, torch.bfloat16, 512), (8, 2, 2, torch.float32, 300),
+                                               (8, 8, 1, torch.float32, 77), (32, 4, 3, torch.bfloat16, 1000),
+                                               (8, 2, 1, torch.float32, 0), (8, 1, 1, torch.float32, 2900)])
+def test_retained_decode_against_oracle(Hq, Hkv, Tq, dtype, k):
+    """The fused retained decode (kvq.retained_decode): the kept rows read from the packed cache as
+    kivi_quant's xhat in fp32, the window exact; positions outside [0, n_q) are masked rows.
+    Against chunked_attention over exactly those rows (2e-3 fp32, 1e-2 bf16), and against the
+    gathered path retained_cache + kivi_decode (bf16 rows there, so the same bars)."""
+    import kvq
+    B, T, W, gk, gv, d = 2, 3000, 128, 64, 32, 128
+    cache, K, V, kh, vh, g = _packed(B, Hkv, T, W, gk, gv, seed=Hq + Tq + k, dtype=dtype)
+    n_q = T - W
+    k = min(k, n_q)
+    idx = torch.stack([torch.sort(torch.randperm(n_q, generator=g)[:k]).values for _ in range(B * Hkv)])
+    idx = idx.reshape(B, Hkv, k).to(torch.int32)
+    if k:
+        idx[0, 0, -1] = n_q                                             # masked rows
+        idx[B - 1, Hkv - 1, 0] = -1
+    q = torch.randn((B, Hq, Tq, d), generator=g).to(dtype)
+    qpos = torch.arange(T, T + Tq)
+    out = kvq.retained_decode(q.cuda(), d ** -0.5, cache, idx.cuda(), q_pos=qpos.cuda())
+    assert out.shape == (B, Tq, Hq, d) and out.dtype == dtype
+    got = out.float().cpu().numpy()
+    ii = idx.long().numpy()
+    bad = (ii < 0) | (ii >= n_q)
+    jj = np.where(bad, 0, ii)
+    kk = np.concatenate([np.take_along_axis(kh, jj[..., None], 2), K[:, :, n_q:].float().numpy()], 2)
+    vv = np.concatenate([np.take_along_axis(vh, jj[..., None], 2), V[:, :, n_q:].float().numpy()], 2)
+    hide = np.full((B, Hkv, k + W), 1 << 40)
+    hide[:, :, :k][bad] = 0                                             # never readable
+    ref = chunked_attention(q.float().numpy(), d ** -0.5, qpos.numpy(), kk, vv, np.zeros(k + W, int), hide, None)
+    tol = 2e-3 if dtype == torch.float32 else 1e-2
+    err = float(np.abs(got - ref).max())
+    print(f"retained Hq {Hq} Hkv {Hkv} Tq {Tq} {dtype} k {k}: max-abs-err {err:.3e}", flush=True)
+    assert err <= tol, err
+    if not bad.any():
+        via = kvq.kivi_decode(q.cuda(), d ** -0.5, kvq.retained_cache(cache, idx.cuda())).float().cpu().numpy()
+        assert float(np.abs(via - got).max()) <= tol
+    # a caller-owned output and workspace; a second call with the same workspace gives the same bits
+    ws = torch.empty((kvq.retained_workspace_floats(q, cache, idx),), dtype=torch.float32, device="cuda")
+    o2 = torch.empty_like(out)
+    kvq.retained_decode(q.cuda(), d ** -0.5, cache, idx.cuda(), q_pos=qpos.cuda(), out=o2, workspace=ws)
+    assert torch.equal(o2, out)
+
+
+def test_retained_decode_rejects_bad_inputs():
+    import kvq
+    cache, K, V, kh, vh, g = _packed(1, 2, 600, 64, 32, 32, seed=3)
+    q = torch.randn((1, 8, 1, 128), generator=g).cuda()
+    with pytest.raises(ValueError):
+        kvq.retained_decode(q, 0.1, cache, torch.zeros((1, 2, 5), dtype=torch.int64, device="cuda"))
+    with pytest.raises(ValueError):
+        kvq.retained_decode(q, 0.1, cache, torch.zeros((1, 3, 5), dtype=torch.int32, device="cuda"))
+    with pytest.raises(TypeError):
+        kvq.retained_decode(q.bfloat16(), 0.1, cache, torch.zeros((1, 2, 5), dtype=torch.int32, device="cuda"))
+    idx = torch.zeros((1, 2, 5), dtype=torch.int32, device="cuda")
+    with pytest.raises(kvq.KVQError):
+        kvq.retained_decode(q, 0.1, cache, idx, workspace=torch.empty((4,), dtype=torch.float32, device="cuda"))
