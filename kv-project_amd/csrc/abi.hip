@@ -57,7 +57,7 @@ __global__ void mfma_layout_probe(const uint16_t* __restrict__ a, const uint16_t
 
 extern "C" const char* kvq_last_error(void) { return kvq::g_last_error; }
 
-extern "C" int kvq_abi_version(void) { return 17; }
+extern "C" int kvq_abi_version(void) { return 18; }
 
 extern "C" int kvq_selftest_mfma_layout(const uint16_t* a, const uint16_t* b, float* out, void* stream) {
   KVQ_REQUIRE(a && b && out, "kvq_selftest_mfma_layout: null pointer");

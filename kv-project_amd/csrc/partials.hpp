@@ -318,8 +318,9 @@ __device__ __forceinline__ int64_t class_weight_before(int s, int n_split, int c
   const int c = s / q;
   const int w[3] = {w0, w1, w2};
   int64_t acc = 0;
-  for (int k = 0; k < c; ++k) acc += static_cast<int64_t>(q) * w[k];
-  return acc + static_cast<int64_t>(s % q) * w[c];
+  for (int k = 0; k < c && k < 3; ++k) acc += static_cast<int64_t>(q) * w[k];
+  // s == n_split (the total) ends on a class boundary: no partial class to add
+  return c < 3 ? acc + static_cast<int64_t>(s % q) * w[c] : acc;
 }
 
 inline int pow2_rows(int64_t r) {

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/kvq.h but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert lib.kvq_abi_version() == 17
+    assert lib.kvq_abi_version() == 18
     assert lib.kvq_last_error() == b""
 
 
