@@ -267,9 +267,9 @@ __device__ void exact_block(const DecodeParams& p, int bh, int sidx, float* smem
     const u32x4* kp = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.k_exact) + off);
     const u32x4* vp = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(p.v_exact) + off);
 #pragma unroll
-    for (int w = 0; w < kW; ++w) {
-      x.kw[w] = kp[w];
-      x.vw[w] = vp[w];
+    for (int w = 0; w < kW; ++w) {            // streamed once: non-temporal
+      x.kw[w] = __builtin_nontemporal_load(kp + w);
+      x.vw[w] = __builtin_nontemporal_load(vp + w);
     }
     x.pos = masked ? p.exact_pos[i] : 0;
   };
@@ -387,7 +387,7 @@ __device__ void retained_block(const DecodeParams& p, int bh, int sidx, float* s
   auto load_tok = [&](int t, Tok& x) {
     x.t = t;
     const int tt = t < 0 ? 0 : t;
-    x.kw = *reinterpret_cast<const uint32_t*>(kc + static_cast<int64_t>(tt) * (kD / 2) + 4 * part);
+    x.kw = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(kc + static_cast<int64_t>(tt) * (kD / 2) + 4 * part));
     const int64_t km = static_cast<int64_t>(tt / G) * kD + 8 * part;
     x.sc4 = *reinterpret_cast<const uint4*>(ksc + km);
     x.lo4 = *reinterpret_cast<const uint4*>(klo + km);

@@ -67,7 +67,9 @@ struct QuasarParams {
   float* ex_o;                            // [Hkv][S_ex][R][128]
 };
 
-// qt[h][r][k] = qscale sum_c q[c] T_K[h][c][k]; qmu[h][r] = qscale q . mu_K[h]
+// qt[h][k][r] = qscale sum_c q[c] T_K[h][c][k] (coefficient-major: the R rows of a coefficient
+// side by side, so the split reads four coefficients of every row as one scalar load);
+// qmu[h][r] = qscale q . mu_K[h]; padded rows r >= R_real are zero
 template <int DT>
 __global__ __launch_bounds__(256) void quasar_prologue(const void* __restrict__ q, int64_t q_sh, int64_t q_st, int rep,
                                                        int Tq, int R, int R_real, int d, const float* __restrict__ Tk,
@@ -75,9 +77,14 @@ __global__ __launch_bounds__(256) void quasar_prologue(const void* __restrict__ 
                                                        float* __restrict__ qt, float* __restrict__ qmu) {
   __shared__ float qs[256];
   __shared__ float red[4];
-  const int h = blockIdx.x / R_real, r = blockIdx.x % R_real;     // rows r >= R_real stay unwritten
-  const int hq = h * rep + r / Tq, t = r % Tq;
+  const int h = blockIdx.x / R, r = blockIdx.x % R;
   const int tid = threadIdx.x;
+  if (r >= R_real) {
+    if (tid < Rk) qt[(static_cast<int64_t>(h) * Rk + tid) * R + r] = 0.0f;
+    if (tid == 0) qmu[static_cast<int64_t>(h) * R + r] = 0.0f;
+    return;
+  }
+  const int hq = h * rep + r / Tq, t = r % Tq;
   float pm = 0.0f;
   if (tid < d) {
     const float qc = load_as_f32<DT>(q, static_cast<int64_t>(hq) * q_sh + static_cast<int64_t>(t) * q_st + tid);
@@ -92,7 +99,7 @@ __global__ __launch_bounds__(256) void quasar_prologue(const void* __restrict__ 
     float acc = 0.0f;
 #pragma unroll 16
     for (int c = 0; c < d; ++c) acc = __builtin_fmaf(qs[c], col[static_cast<int64_t>(c) * Rk], acc);
-    qt[(static_cast<int64_t>(h) * R + r) * Rk + tid] = acc * qscale;
+    qt[(static_cast<int64_t>(h) * Rk + tid) * R + r] = acc * qscale;
   }
   if (tid == 0) qmu[static_cast<int64_t>(h) * R + r] = ((red[0] + red[1]) + (red[2] + red[3])) * qscale;
 }
@@ -138,10 +145,16 @@ __device__ __forceinline__ void dma_step(const uint8_t* codes, int off, int ns, 
   }
 }
 
+// wave-uniform tables read through the constant address space: scalar loads into SGPRs, which
+// the FMAs take as operands directly
+typedef __attribute__((address_space(4))) const float qcfloat;
+typedef __attribute__((address_space(4))) const int32_t qcint;
+
 // Scores of one K dword for this lane's token: its 32 / B codes (coefficients c0 ..), each code's
-// level times qt[r][c]; qt read four coefficients at a time (broadcast LDS reads).
+// level times qt[c][r]; qt (this head's, coefficient-major) read four coefficients of every row at
+// a time by scalar loads.
 template <int R, int B>
-__device__ __forceinline__ void score_word(uint32_t word, int c0, int lo, const float* lv, const float* qtl,
+__device__ __forceinline__ void score_word(uint32_t word, int c0, int lo, const float* lv, qcfloat* qtc,
                                            float (&sc)[R]) {
   constexpr int per = 8 / B, mask = (1 << B) - 1, cpw = 32 / B;
 #pragma unroll
@@ -152,31 +165,28 @@ __device__ __forceinline__ void score_word(uint32_t word, int c0, int lo, const 
       const int m = 4 * g + i, by = m / per, k = m % per;
       l[i] = lv[lo + static_cast<int>((word >> (8 * by + (per - 1 - k) * B)) & mask)];
     }
+    qcfloat* qg = qtc + (c0 + 4 * g) * R;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float4 qv = *reinterpret_cast<const float4*>(qtl + r * kQRowCoef + c0 + 4 * g);
-      sc[r] = __builtin_fmaf(qv.x, l[0], sc[r]);
-      sc[r] = __builtin_fmaf(qv.y, l[1], sc[r]);
-      sc[r] = __builtin_fmaf(qv.z, l[2], sc[r]);
-      sc[r] = __builtin_fmaf(qv.w, l[3], sc[r]);
-    }
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < R; ++r) sc[r] = __builtin_fmaf(qg[i * R + r], l[i], sc[r]);
   }
 }
 
 // Scores of one staged K step for this lane's token.
 template <int R, int B>
 __device__ __forceinline__ void score_step(const uint8_t* st, int nb, int a, int lo, int lane, const float* lv,
-                                           const float* qtl, float (&sc)[R]) {
+                                           qcfloat* qtc, float (&sc)[R]) {
   constexpr int cpw = 32 / B;
   if (nb >= 16) {
     for (int q = 0; q < nb / 16; ++q) {
       const u32x4 w = *reinterpret_cast<const u32x4*>(st + q * 1024 + lane * 16);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) score_word<R, B>(w[i], a + (4 * q + i) * cpw, lo, lv, qtl, sc);
+      for (int i = 0; i < 4; ++i) score_word<R, B>(w[i], a + (4 * q + i) * cpw, lo, lv, qtc, sc);
     }
   } else {
     for (int d = 0; d < nb / 4; ++d)
-      score_word<R, B>(*reinterpret_cast<const uint32_t*>(st + d * 256 + lane * 4), a + d * cpw, lo, lv, qtl, sc);
+      score_word<R, B>(*reinterpret_cast<const uint32_t*>(st + d * 256 + lane * 4), a + d * cpw, lo, lv, qtc, sc);
   }
 }
 
@@ -195,19 +205,30 @@ __device__ __forceinline__ void value_step(const uint8_t* st, int nb, int a, int
   for (int k = 0; k < per; ++k)
 #pragma unroll
     for (int r = 0; r < R; ++r) v[k][r] = 0.0f;
-#pragma unroll 4
-  for (int t = 0; t < nb; ++t) {
-    const int jj = u + G * t;
-    const bool own = j0 + jj < ns;
-    const uint32_t byte = col[jj * ts];
-    float pr[R];
+  // four tokens per turn (nb is a multiple of 4): their bytes and probabilities are read first,
+  // then their codes' levels, then the products, in token order
+  for (int t0 = 0; t0 < nb; t0 += 4) {
+    uint32_t byte[4];
+    float pr[4][R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) pr[r] = own ? pch[jj * R + r] : 0.0f;
+    for (int e = 0; e < 4; ++e) {
+      const int jj = u + G * (t0 + e);              // < 64: read unconditionally, selected below
+      byte[e] = col[jj * ts];
 #pragma unroll
-    for (int k = 0; k < per; ++k) {
-      const float l = lv[lo + static_cast<int>((byte >> ((per - 1 - k) * B)) & mask)];
+      for (int r = 0; r < R; ++r) pr[e][r] = pch[jj * R + r];
+    }
+    float lvl[4][per];
 #pragma unroll
-      for (int r = 0; r < R; ++r) v[k][r] = __builtin_fmaf(pr[r], l, v[k][r]);
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int k = 0; k < per; ++k) lvl[e][k] = lv[lo + static_cast<int>((byte[e] >> ((per - 1 - k) * B)) & mask)];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool own = j0 + u + G * (t0 + e) < ns;
+#pragma unroll
+      for (int k = 0; k < per; ++k)
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[k][r] = __builtin_fmaf(own ? pr[e][r] : 0.0f, lvl[e][k], v[k][r]);
     }
   }
 #pragma unroll
@@ -227,7 +248,6 @@ __device__ __forceinline__ void value_step(const uint8_t* st, int nb, int a, int
 template <int R, int DT>
 __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) void quasar_split(QuasarParams p) {
   __shared__ __align__(16) uint8_t stage_all[kQWaves][1][kQSideBytes];
-  __shared__ __align__(16) float qtl[R * kQRowCoef];
   __shared__ float lv[kQMaxLevels];
   __shared__ __align__(16) float pch_all[kQWaves][kQChunk * R];
   __shared__ float acc_all[kQWaves][R * kQRowCoef];
@@ -280,16 +300,13 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   uint8_t* stV = stK;
   float* pch = pch_all[wave];
   float* accw = acc_all[wave];
-  for (int i = tid; i < R * kQRowCoef; i += kQThreads) {
-    const int r = i / kQRowCoef, c = i % kQRowCoef;
-    qtl[i] = r < p.R_real && c < p.Rk ? p.qt[(static_cast<int64_t>(h) * R + r) * p.Rk + c] : 0.0f;
-  }
+  qcfloat* qtc = (qcfloat*)(p.qt + static_cast<int64_t>(h) * p.Rk * R);
   for (int i = tid; i < p.n_levels; i += kQThreads) lv[i] = p.levels[i];
   for (int i = lane; i < R * kQRowCoef; i += 64) accw[i] = 0.0f;
   if (tid == 0) next_chunk = p.bounds[sidx];
   __syncthreads();
-  const int32_t* __restrict__ ks = p.slots;                       // scalar loads: wave-uniform indices
-  const int32_t* __restrict__ vs = p.slots + kQSlots * kQSlotInts;
+  qcint* ks = (qcint*)p.slots;                                    // scalar loads: wave-uniform indices
+  qcint* vs = ks + kQSlots * kQSlotInts;
   const int nks = p.nslots_k, nvs = p.nslots_v;
   float qmu[R];
 #pragma unroll
@@ -315,7 +332,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     const bool valid = tok < p.n_c;
     // ---- every key row of the chunk's owned steps into LDS at once ----
     for (int j = 0; j < nks;) {
-      const int32_t* sl = ks + j * kQSlotInts;
+      qcint* sl = ks + j * kQSlotInts;
       if (sl[1] <= j0) break;                                     // steps own prefixes: n_s never grows
       dma_step(p.kcodes, sl[0], sl[1], sl[2], h, tok, stK + j * 256);
       j += sl[2] / 4;
@@ -328,15 +345,15 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
 #pragma unroll
     for (int r = 0; r < R; ++r) sc[r] = 0.0f;
     for (int j = 0; j < nks;) {
-      const int32_t* sl = ks + j * kQSlotInts;
+      qcint* sl = ks + j * kQSlotInts;
       const int ns = sl[1], nb = sl[2];
       if (ns <= j0) break;
       if (tok < ns) {                                             // code 0 is a level, not nothing
         switch (sl[4]) {
-          case 1: score_step<R, 1>(stK + j * 256, nb, sl[3], sl[5], lane, lv, qtl, sc); break;
-          case 2: score_step<R, 2>(stK + j * 256, nb, sl[3], sl[5], lane, lv, qtl, sc); break;
-          case 4: score_step<R, 4>(stK + j * 256, nb, sl[3], sl[5], lane, lv, qtl, sc); break;
-          default: score_step<R, 8>(stK + j * 256, nb, sl[3], sl[5], lane, lv, qtl, sc); break;
+          case 1: score_step<R, 1>(stK + j * 256, nb, sl[3], sl[5], lane, lv, qtc, sc); break;
+          case 2: score_step<R, 2>(stK + j * 256, nb, sl[3], sl[5], lane, lv, qtc, sc); break;
+          case 4: score_step<R, 4>(stK + j * 256, nb, sl[3], sl[5], lane, lv, qtc, sc); break;
+          default: score_step<R, 8>(stK + j * 256, nb, sl[3], sl[5], lane, lv, qtc, sc); break;
         }
       }
       j += nb / 4;
@@ -363,7 +380,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     // ---- the value rows into the same staging area (key rows consumed) ----
     wave_lds_fence();
     for (int j = 0; j < nvs;) {
-      const int32_t* sl = vs + j * kQSlotInts;
+      qcint* sl = vs + j * kQSlotInts;
       if (sl[1] <= j0) break;
       dma_step(p.vcodes, sl[0], sl[1], sl[2], h, tok, stV + j * 256);
       j += sl[2] / 4;
@@ -371,7 +388,7 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
     __builtin_amdgcn_s_waitcnt(0);
     // ---- values ----
     for (int j = 0; j < nvs;) {
-      const int32_t* sl = vs + j * kQSlotInts;
+      qcint* sl = vs + j * kQSlotInts;
       const int ns = sl[1], nb = sl[2];
       if (ns <= j0) break;
       switch (sl[4]) {
@@ -605,7 +622,7 @@ extern "C" int kvq_quasar_decode(const void* q, int q_dtype, int64_t q_sh, int64
   float* ex_l = ex_m + Hkv * S_ex * R;
   float* ex_o = ex_l + Hkv * S_ex * R;
   if (n_c > 0 && (phases & 1)) {
-    KVQ_DISPATCH_DTYPE(q_dtype, hipLaunchKernelGGL((quasar_prologue<DT_>), dim3(static_cast<unsigned>(Hkv * R_real)), dim3(256), 0,
+    KVQ_DISPATCH_DTYPE(q_dtype, hipLaunchKernelGGL((quasar_prologue<DT_>), dim3(static_cast<unsigned>(Hkv * R)), dim3(256), 0,
                                                    st, q, q_sh, q_st, static_cast<int>(Hq / Hkv), static_cast<int>(Tq), R,
                                                    static_cast<int>(R_real), static_cast<int>(d), T_k, mu_k,
                                                    static_cast<int>(R_k), qscale, qt, qmu));
