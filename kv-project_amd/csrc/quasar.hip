@@ -104,19 +104,6 @@ __global__ __launch_bounds__(256) void quasar_prologue(const void* __restrict__ 
   if (tid == 0) qmu[static_cast<int64_t>(h) * R + r] = ((red[0] + red[1]) + (red[2] + red[3])) * qscale;
 }
 
-// sum over the lanes ib + nb u (u = 0 .. 64 / nb - 1) of x, every lane receiving its class's sum
-__device__ __forceinline__ float class_sum(float x, int nb) {
-  if (nb < 16) {
-    if (nb <= 1) x += dpp<kRowRor + 1>(x);
-    if (nb <= 2) x += dpp<kRowRor + 2>(x);
-    if (nb <= 4) x += dpp<kRowRor + 4>(x);
-    x += dpp<kRowRor + 8>(x);
-  }
-  if (nb < 32) x = xsum16(x);
-  if (nb < 64) x = xsum32(x);
-  return x;
-}
-
 // Code slots: the dwords of a token's rows over every step of a side, in step order (step s holds
 // nb_s / 4 consecutive slots).  A side holds at most kQSlots of them (128 bytes per token: d = 128
 // coefficients at 8 bits over all stages).  kvq_quasar_plan writes the slot table, int32
@@ -151,23 +138,27 @@ typedef __attribute__((address_space(4))) const float qcfloat;
 typedef __attribute__((address_space(4))) const int32_t qcint;
 
 // Scores of one K dword for this lane's token: its 32 / B codes (coefficients c0 ..), each code's
-// level times qt[c][r]; qt (this head's, coefficient-major) read four coefficients of every row at
-// a time by scalar loads.
+// level times qt[c][r]; qt (this head's, coefficient-major) read by scalar loads, kQG coefficients
+// of every row at a time.  A scalar load's data is waited for together with the LDS lookups in
+// flight (one counter), so each group of kQG codes costs one exposed wait: groups of eight halve
+// them against groups of four.
+constexpr int kQG = 8;
 template <int R, int B>
 __device__ __forceinline__ void score_word(uint32_t word, int c0, int lo, const float* lv, qcfloat* qtc,
                                            float (&sc)[R]) {
   constexpr int per = 8 / B, mask = (1 << B) - 1, cpw = 32 / B;
+  constexpr int QG = cpw < kQG ? cpw : kQG;
 #pragma unroll
-  for (int g = 0; g < cpw / 4; ++g) {
-    float l[4];
+  for (int g = 0; g < cpw / QG; ++g) {
+    float l[QG];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = 4 * g + i, by = m / per, k = m % per;
+    for (int i = 0; i < QG; ++i) {
+      const int m = QG * g + i, by = m / per, k = m % per;
       l[i] = lv[lo + static_cast<int>((word >> (8 * by + (per - 1 - k) * B)) & mask)];
     }
-    qcfloat* qg = qtc + (c0 + 4 * g) * R;
+    qcfloat* qg = qtc + (c0 + QG * g) * R;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < QG; ++i)
 #pragma unroll
       for (int r = 0; r < R; ++r) sc[r] = __builtin_fmaf(qg[i * R + r], l[i], sc[r]);
   }
@@ -190,57 +181,66 @@ __device__ __forceinline__ void score_step(const uint8_t* st, int nb, int a, int
   }
 }
 
-// Values of one staged V step over the chunk's tokens: lane (u, ib) takes byte ib of tokens u,
-// u + 64/nb, ...; the per-lane sums meet by class_sum and land in the wavefront's accumulator.
+// Values of one staged V step on the matrix cores: acc[r][a + c] += sum_t pv[t][r] level(code(t, c))
+// as D = A B per 16-coefficient tile and 32-token k-block, A = the chunk's probabilities (rows r,
+// fp16 hi + lo parts), B = the levels of column c's codes (fp16 hi + lo parts from lvp), three
+// products (hi hi, hi lo, lo hi).  Lane l supplies column n = l % 16 (coefficient 16 j + n: byte
+// (16 j + n) / per, code position (16 j + n) % per) for the k-slots of lane group g = l / 16, which
+// stand for tokens 32 kb + g + 4 i (neighbouring lane groups read neighbouring tokens: distinct
+// LDS banks).  The products reduce over the tokens inside the matrix core; each tile then joins
+// the wavefront's accumulator once (lanes of rows r < R, the tile's coefficients below w).
 template <int R, int B>
-__device__ __forceinline__ void value_step(const uint8_t* st, int nb, int a, int lo, int ns, int j0, const float* lv,
-                                           const float* pch, float* accw, int lane) {
+__device__ __forceinline__ void value_step_mfma(const uint8_t* st, int nb, int a, int lo, int ns, int j0,
+                                                const uint32_t* lvp, const half8 (&Ah)[2], const half8 (&Al)[2],
+                                                float* accw, int lane) {
   constexpr int per = 8 / B, mask = (1 << B) - 1;
-  const int ib = lane % nb, u = lane / nb, G = 64 / nb;
-  // byte ib of token jj: 16-byte pieces [q][token][16] or dwords [d][token][4]
-  const uint8_t* col = nb >= 16 ? st + (ib >> 4) * 1024 + (ib & 15) : st + (ib >> 2) * 256 + (ib & 3);
-  const int ts = nb >= 16 ? 16 : 4;
-  float v[per][R];
+  const int w = nb * per;                                         // coefficients of the step
+  const int n = lane & 15, g = lane >> 4;
+  // tokens j0 + t with t >= ns - j0 own no code of this step: their probabilities drop out
+  half8 Ahm[2] = {Ah[0], Ah[1]}, Alm[2] = {Al[0], Al[1]};
+  const int n_own = ns - j0;
+  if (n_own < kQChunk) {                                          // wave-uniform
 #pragma unroll
-  for (int k = 0; k < per; ++k)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int r = 0; r < R; ++r) v[k][r] = 0.0f;
-  // four tokens per turn (nb is a multiple of 4): their bytes and probabilities are read first,
-  // then their codes' levels, then the products, in token order
-  for (int t0 = 0; t0 < nb; t0 += 4) {
-    uint32_t byte[4];
-    float pr[4][R];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int jj = u + G * (t0 + e);              // < 64: read unconditionally, selected below
-      byte[e] = col[jj * ts];
-#pragma unroll
-      for (int r = 0; r < R; ++r) pr[e][r] = pch[jj * R + r];
-    }
-    float lvl[4][per];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int k = 0; k < per; ++k) lvl[e][k] = lv[lo + static_cast<int>((byte[e] >> ((per - 1 - k) * B)) & mask)];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool own = j0 + u + G * (t0 + e) < ns;
-#pragma unroll
-      for (int k = 0; k < per; ++k)
-#pragma unroll
-        for (int r = 0; r < R; ++r) v[k][r] = __builtin_fmaf(own ? pr[e][r] : 0.0f, lvl[e][k], v[k][r]);
-    }
+      for (int i = 0; i < 8; ++i) {
+        const bool own = 32 * kb + g + 4 * i < n_own;
+        Ahm[kb][i] = own ? Ahm[kb][i] : static_cast<_Float16>(0.0f);
+        Alm[kb][i] = own ? Alm[kb][i] : static_cast<_Float16>(0.0f);
+      }
   }
+  const int ts = nb >= 16 ? 16 : 4;                               // staged bytes per token
+  for (int j = 0; j < (w + 15) / 16; ++j) {
+    const int c = 16 * j + n;
+    const int cc = c < w ? c : w - 1;                             // columns past w read a real byte
+    const int byte = cc / per;
+    const int shift = (per - 1 - cc % per) * B;
+    const uint8_t* col = nb >= 16 ? st + (byte >> 4) * 1024 + (byte & 15) : st + (byte >> 2) * 256 + (byte & 3);
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < per; ++k)
+    for (int kb = 0; kb < 2; ++kb) {
+      uint32_t pr[8];
 #pragma unroll
-    for (int r = 0; r < R; ++r) v[k][r] = class_sum(v[k][r], nb);
-  if (u == 0) {
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t v = col[(32 * kb + g + 4 * i) * ts];
+        pr[i] = lvp[lo + static_cast<int>((v >> shift) & static_cast<uint32_t>(mask))];
+      }
+      u32x4 bh, bl;
 #pragma unroll
-    for (int k = 0; k < per; ++k) {
-      const int c = a + ib * per + k;
+      for (int m = 0; m < 4; ++m) {
+        bh[m] = __builtin_amdgcn_perm(pr[2 * m + 1], pr[2 * m], 0x05040100u);   // hi parts
+        bl[m] = __builtin_amdgcn_perm(pr[2 * m + 1], pr[2 * m], 0x07060302u);   // lo parts
+      }
+      d = mfma(Ahm[kb], as_half8(bh), d);
+      d = mfma(Ahm[kb], as_half8(bl), d);
+      d = mfma(Alm[kb], as_half8(bh), d);
+    }
+    if (c < w) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) accw[r * kQRowCoef + c] += v[k][r];
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * g + i;
+        if (r < R) accw[r * kQRowCoef + a + c] += d[i];
+      }
     }
   }
 }
@@ -249,6 +249,7 @@ template <int R, int DT>
 __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) void quasar_split(QuasarParams p) {
   __shared__ __align__(16) uint8_t stage_all[kQWaves][1][kQSideBytes];
   __shared__ float lv[kQMaxLevels];
+  __shared__ uint32_t lvp[kQMaxLevels];                           // levels as fp16 (hi, lo) pairs
   __shared__ __align__(16) float pch_all[kQWaves][kQChunk * R];
   __shared__ float acc_all[kQWaves][R * kQRowCoef];
   __shared__ int next_chunk;                                      // the split's next unclaimed chunk
@@ -301,7 +302,14 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   float* pch = pch_all[wave];
   float* accw = acc_all[wave];
   qcfloat* qtc = (qcfloat*)(p.qt + static_cast<int64_t>(h) * p.Rk * R);
-  for (int i = tid; i < p.n_levels; i += kQThreads) lv[i] = p.levels[i];
+  for (int i = tid; i < p.n_levels; i += kQThreads) {
+    const float x = p.levels[i];
+    const _Float16 hi = static_cast<_Float16>(x);
+    const _Float16 lo = static_cast<_Float16>(x - static_cast<float>(hi));
+    lv[i] = x;
+    lvp[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) << 16);
+  }
   for (int i = lane; i < R * kQRowCoef; i += 64) accw[i] = 0.0f;
   if (tid == 0) next_chunk = p.bounds[sidx];
   __syncthreads();
@@ -386,16 +394,28 @@ __global__ __launch_bounds__(kQThreads) __attribute__((amdgpu_waves_per_eu(3))) 
       j += sl[2] / 4;
     }
     __builtin_amdgcn_s_waitcnt(0);
-    // ---- values ----
+    // ---- values: the chunk's probabilities as the A operand (rows r = lane % 16, fp16 hi + lo),
+    // then every owned step on the matrix cores ----
+    half8 Ah[2], Al[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = lane & 15;
+        const float x = r < R ? pch[(32 * kb + (lane >> 4) + 4 * i) * R + (r < R ? r : 0)] : 0.0f;
+        const _Float16 hi = static_cast<_Float16>(x);
+        Ah[kb][i] = hi;
+        Al[kb][i] = static_cast<_Float16>(x - static_cast<float>(hi));
+      }
     for (int j = 0; j < nvs;) {
       qcint* sl = vs + j * kQSlotInts;
       const int ns = sl[1], nb = sl[2];
       if (ns <= j0) break;
       switch (sl[4]) {
-        case 1: value_step<R, 1>(stV + j * 256, nb, sl[3], sl[5], ns, j0, lv, pch, accw, lane); break;
-        case 2: value_step<R, 2>(stV + j * 256, nb, sl[3], sl[5], ns, j0, lv, pch, accw, lane); break;
-        case 4: value_step<R, 4>(stV + j * 256, nb, sl[3], sl[5], ns, j0, lv, pch, accw, lane); break;
-        default: value_step<R, 8>(stV + j * 256, nb, sl[3], sl[5], ns, j0, lv, pch, accw, lane); break;
+        case 1: value_step_mfma<R, 1>(stV + j * 256, nb, sl[3], sl[5], ns, j0, lvp, Ah, Al, accw, lane); break;
+        case 2: value_step_mfma<R, 2>(stV + j * 256, nb, sl[3], sl[5], ns, j0, lvp, Ah, Al, accw, lane); break;
+        case 4: value_step_mfma<R, 4>(stV + j * 256, nb, sl[3], sl[5], ns, j0, lvp, Ah, Al, accw, lane); break;
+        default: value_step_mfma<R, 8>(stV + j * 256, nb, sl[3], sl[5], ns, j0, lvp, Ah, Al, accw, lane); break;
       }
       j += nb / 4;
     }
