@@ -225,16 +225,21 @@ def test_c4_reduced_eviction_end_to_end(dtype):
     assert float(np.abs(out - ref_out).max()) <= tol_out
 
 
-@pytest.mark.parametrize("Hq,Hkv,Tq,dtype,k", [(16, 4, 1, torch.bfloat16, 512), (8, 2, 2, torch.float32, 300),
-                                               (8, 8, 1, torch.float32, 77), (32, 4, 3, torch.bfloat16, 1000),
-                                               (8, 2, 1, torch.float32, 0), (8, 1, 1, torch.float32, 2900)])
-def test_retained_decode_against_oracle(Hq, Hkv, Tq, dtype, k):
+@pytest.mark.parametrize("Hq,Hkv,Tq,dtype,k,gk,gv", [(16, 4, 1, torch.bfloat16, 512, 64, 32),
+                                                     (8, 2, 2, torch.float32, 300, 64, 32),
+                                                     (8, 8, 1, torch.float32, 77, 64, 32),
+                                                     (32, 4, 3, torch.bfloat16, 1000, 64, 32),
+                                                     (8, 2, 1, torch.float32, 0, 64, 32),
+                                                     (8, 1, 1, torch.float32, 2900, 64, 32),
+                                                     (16, 2, 1, torch.float16, 700, 32, 128),
+                                                     (8, 4, 1, torch.float16, 257, 128, 64)])
+def test_retained_decode_against_oracle(Hq, Hkv, Tq, dtype, k, gk, gv):
     """The fused retained decode (kvq.retained_decode): the kept rows read from the packed cache as
     kivi_quant's xhat in fp32, the window exact; positions outside [0, n_q) are masked rows.
     Against chunked_attention over exactly those rows (2e-3 fp32, 1e-2 bf16), and against the
     gathered path retained_cache + kivi_decode (bf16 rows there, so the same bars)."""
     import kvq
-    B, T, W, gk, gv, d = 2, 3000, 128, 64, 32, 128
+    B, T, W, d = 2, 3000, 128, 128
     cache, K, V, kh, vh, g = _packed(B, Hkv, T, W, gk, gv, seed=Hq + Tq + k, dtype=dtype)
     n_q = T - W
     k = min(k, n_q)
@@ -258,7 +263,7 @@ def test_retained_decode_against_oracle(Hq, Hkv, Tq, dtype, k):
     ref = chunked_attention(q.float().numpy(), d ** -0.5, qpos.numpy(), kk, vv, np.zeros(k + W, int), hide, None)
     tol = 2e-3 if dtype == torch.float32 else 1e-2
     err = float(np.abs(got - ref).max())
-    print(f"retained Hq {Hq} Hkv {Hkv} Tq {Tq} {dtype} k {k}: max-abs-err {err:.3e}", flush=True)
+    print(f"retained Hq {Hq} Hkv {Hkv} Tq {Tq} {dtype} k {k} groups {gk}/{gv}: max-abs-err {err:.3e}", flush=True)
     assert err <= tol, err
     if not bad.any():
         via = kvq.kivi_decode(q.cuda(), d ** -0.5, kvq.retained_cache(cache, idx.cuda())).float().cpu().numpy()

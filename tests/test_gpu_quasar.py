@@ -2,7 +2,8 @@
 (oracle/quasar.py: QuasarState.attend, QUASAR_KV.py:1945-1968, in float64).
 
 Tolerances (relative to the output's max magnitude): float32 2e-3, bfloat16 1e-2.  Cases: GQA 4
-with one and two query rows, codes at (2, 2, 4), (4, 4) and (8,) bits, coded-token counts around
+with one and two query rows, one and two rows per KV head (GQA 1 and 2), codes at (2, 2, 4),
+(4, 4), (8,) and (1, 2, 4) bits, coded-token counts around
 the 64-token chunk (1, 63, 64, 65) and long ones, exact rows in the merge (up to 128) and in 128-row blocks of the split launch (129 .. 1500), appended
 causal rows, no coded tokens, and the state's own kernel check.
 """
@@ -15,11 +16,12 @@ import oracle.quasar as oq
 pytestmark = pytest.mark.gpu
 
 
-def _state(Hkv, n_c, n0, extra, stages, dtype, seed):
+def _state(Hkv, n_c, n0, extra, stages, dtype, seed, bands=None):
     import kvq
     from kvq.quasar import synthetic_packed
     g = torch.Generator().manual_seed(seed)
-    p = synthetic_packed(Hkv, 128, n_c, stages=stages, seed=seed) if n_c > 0 else {"steps": [], "n_c": 0}
+    kw = {} if bands is None else {"bands": bands}
+    p = synthetic_packed(Hkv, 128, n_c, stages=stages, seed=seed, **kw) if n_c > 0 else {"steps": [], "n_c": 0}
     K = torch.randn((1, Hkv, n0, 128), generator=g).to(dtype)
     V = torch.randn((1, Hkv, n0, 128), generator=g).to(dtype)
     H = 5000
@@ -53,6 +55,20 @@ def test_quasar_decode_stages_two_rows_and_appends(stages):
     q = torch.randn((1, 16, 2, 128), generator=g).to(dtype)
     qpos = [H + 1, H + 2]                                   # row H+2 visible to the second query only
     _check(st, p, torch.cat([K, k], 2), torch.cat([V, v], 2), 200, H, q, qpos, stages, 1e-2)
+
+
+@pytest.mark.parametrize("rep,Tq,stages,bands,dtype", [(1, 1, (1, 2, 4), (0.25, 0.25, 0.5), torch.float32),
+                                                      (2, 1, (2, 2, 4), None, torch.bfloat16),
+                                                      (1, 2, (4, 4), None, torch.float32),
+                                                      (2, 2, (1, 2, 4), (0.25, 0.25, 0.5), torch.bfloat16)])
+def test_quasar_decode_one_and_two_rows_one_bit(rep, Tq, stages, bands, dtype):
+    """One and two query rows per KV head (the split's R = 1, 2 instantiations) and 1-bit stage codes
+    (bands of at least 32 coefficients, so every step's rows fill whole 4-byte slots)."""
+    Hkv = 4
+    st, p, K, V, H, g = _state(Hkv, 1300, 150, 0, stages, dtype, 50 + rep + Tq, bands)
+    q = torch.randn((1, Hkv * rep, Tq, 128), generator=g).to(dtype)
+    qpos = [H] * Tq
+    _check(st, p, K, V, 150, H, q, qpos, stages, 2e-3 if dtype == torch.float32 else 1e-2)
 
 
 def test_quasar_exact_only_and_kernel_check():
