@@ -7,7 +7,8 @@
 //
 // One workgroup per (b, h, row): the partials are spread over all 256 threads (max and sum by
 // block reduction; the output columns by 32 channel quads x 8 partial slices), so the merge
-// costs a few dependent loads whatever the split count.
+// costs a few dependent loads whatever the split count.  Rows with at most 32 partials and no
+// exact rows to attend take one wavefront each instead (merge_rows_wave_kernel).
 #pragma once
 #include <algorithm>
 
@@ -262,6 +263,55 @@ __global__ __launch_bounds__(kMergeThreads) void merge_rows_kernel(MergeArgs a) 
   }
 }
 
+// The merge of a step whose rows have at most NS (<= 32) partials and no exact rows left to attend:
+// one wavefront per query row (four rows a workgroup, rows in the order of merge_rows_kernel's
+// grid), lane s holding partial s's (m, l) and lane l channels 2 l, 2 l + 1 of every partial's o.
+// Every load goes out at once; the row's maximum and sum are wavefront reductions, the weights
+// reach every lane by readlane; no LDS and no barrier.  Same partial order and formulas as
+// merge_rows_kernel (exact-row partials first).
+template <int R, int DT, int NS>
+__global__ __launch_bounds__(256) void merge_rows_wave_kernel(MergeArgs a, int n_rows) {
+  constexpr int D = 128;
+  const int row = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x >> 6);
+  if (row >= n_rows) return;
+  const int lane = threadIdx.x & 63;
+  const int bh = row / a.R_real, r = row % a.R_real;
+  const int S_all = a.S_ex + a.S;
+  auto o_ptr = [&](int s) -> const float* {
+    return s < a.S_ex ? a.ex_o + ((static_cast<int64_t>(bh) * a.S_ex + s) * R + r) * D
+                      : a.ws_o + ((static_cast<int64_t>(bh) * a.S + (s - a.S_ex)) * R + r) * D;
+  };
+  float ms = -INFINITY, ls = 0.0f;
+  if (lane < S_all) {
+    ms = lane < a.S_ex ? a.ex_m[(static_cast<int64_t>(bh) * a.S_ex + lane) * R + r]
+                       : a.ws_m[(static_cast<int64_t>(bh) * a.S + (lane - a.S_ex)) * R + r];
+    ls = lane < a.S_ex ? a.ex_l[(static_cast<int64_t>(bh) * a.S_ex + lane) * R + r]
+                       : a.ws_l[(static_cast<int64_t>(bh) * a.S + (lane - a.S_ex)) * R + r];
+  }
+  float2 ov[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) ov[s] = reinterpret_cast<const float2*>(o_ptr(s < S_all ? s : S_all - 1))[lane];
+  const float M = wave_max(ms);
+  const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+  const float L = wave_sum(w * ls);
+  float ox = 0.0f, oy = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s));   // 0 past S_all
+    ox = __builtin_fmaf(ws, ov[s].x, ox);
+    oy = __builtin_fmaf(ws, ov[s].y, oy);
+  }
+  const int b = bh / a.Hkv, h = bh % a.Hkv;
+  const int hq = h * a.rep + r / a.Tq, t = r % a.Tq;
+  const int64_t o0 = ((static_cast<int64_t>(b) * a.Tq + t) * a.Hq + hq) * D + 2 * lane;
+  store_from_f32<DT>(a.out, o0, ox / L);
+  store_from_f32<DT>(a.out, o0 + 1, oy / L);
+  if (lane == 0 && a.row_ml != nullptr) {
+    a.row_ml[(static_cast<int64_t>(bh) * R + r) * 2] = M;
+    a.row_ml[(static_cast<int64_t>(bh) * R + r) * 2 + 1] = L;
+  }
+}
+
 // Splits per (b, h) of a block-streaming decode launch: BH * S workgroups of 4 wavefronts, each
 // wavefront taking about nb / (4 S) blocks.  Workgroups run in rounds of `slots` resident ones
 // (256 CUs x resident_per_cu); the count minimises rounds x (blocks of one wavefront + a fixed
@@ -331,6 +381,35 @@ inline int pow2_rows(int64_t r) {
 
 // launch merge_rows_kernel for a runtime row count R (power of two <= 8) and output dtype
 inline int launch_merge_rows(const MergeArgs& a, int R, int BH, int out_dtype, hipStream_t s) {
+  const int S_all = a.S_ex + a.S;
+  if (a.ex.n == 0 && S_all >= 1 && S_all <= 32) {                // one wavefront per row
+    const int n_rows = BH * a.R_real;
+    const dim3 wgrid(static_cast<unsigned>((n_rows + 3) / 4));
+#define KVQ_MW_N(R_, DT_, N_) hipLaunchKernelGGL((merge_rows_wave_kernel<R_, DT_, N_>), wgrid, dim3(256), 0, s, a, n_rows)
+#define KVQ_MW_L(R_, DT_)                                      \
+  do {                                                         \
+    if (S_all <= 8) KVQ_MW_N(R_, DT_, 8);                      \
+    else if (S_all <= 16) KVQ_MW_N(R_, DT_, 16);               \
+    else KVQ_MW_N(R_, DT_, 32);                                \
+  } while (0)
+#define KVQ_MW_R(DT_)                              \
+  switch (R) {                                     \
+    case 1: KVQ_MW_L(1, DT_); break;               \
+    case 2: KVQ_MW_L(2, DT_); break;               \
+    case 4: KVQ_MW_L(4, DT_); break;               \
+    default: KVQ_MW_L(8, DT_); break;              \
+  }
+    switch (out_dtype) {
+      case KVQ_F32: KVQ_MW_R(KVQ_F32) break;
+      case KVQ_F16: KVQ_MW_R(KVQ_F16) break;
+      default: KVQ_MW_R(KVQ_BF16) break;
+    }
+#undef KVQ_MW_R
+#undef KVQ_MW_L
+#undef KVQ_MW_N
+    KVQ_LAUNCH_CHECK("merge_rows");
+    return KVQ_OK;
+  }
   const dim3 grid(static_cast<unsigned>(BH) * a.R_real);
   constexpr int kParts128 = kMergeThreads / 32;    // partial slices of the D = 128 merge
   const int per = (a.S_ex + a.S + kParts128 - 1) / kParts128;
