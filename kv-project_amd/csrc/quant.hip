@@ -549,9 +549,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
                         static_cast<int64_t>(n_sink + t0) * st;
   const uint32_t rstride = static_cast<uint32_t>(st * 2);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, static_cast<uint32_t>(rv) * rstride);
-  u32x4 raw[RPL];
+  u32x4 raw[RPL];                                   // rows read once: non-temporal loads
 #pragma unroll
-  for (int j = 0; j < RPL; ++j) raw[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (rq + 4 * j) * rstride + s * 16, 0, 0);
+  for (int j = 0; j < RPL; ++j) raw[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (rq + 4 * j) * rstride + s * 16, 0, 2);
   float mn[8], mx[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -632,9 +632,9 @@ __global__ __launch_bounds__(256) void kivi_quant_values_p4(
                         static_cast<int64_t>(n_sink + t0) * st;
   const uint32_t rstride = static_cast<uint32_t>(st * 2);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, static_cast<uint32_t>(rv) * rstride);
-  u32x4 raw[RPL];
+  u32x4 raw[RPL];                                   // rows read once: non-temporal loads
 #pragma unroll
-  for (int j = 0; j < RPL; ++j) raw[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (rq + 4 * j) * rstride + s * 16, 0, 0);
+  for (int j = 0; j < RPL; ++j) raw[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (rq + 4 * j) * rstride + s * 16, 0, 2);
   uint32_t* dst = reinterpret_cast<uint32_t*>(packed + static_cast<int64_t>(bh) * packed_bh + static_cast<int64_t>(t0) * (D / 2)) + s;
   const int64_t mrow = static_cast<int64_t>(bh) * meta_bh + static_cast<int64_t>(t0) * NG + s / L;
 #pragma unroll
