@@ -49,6 +49,7 @@ constexpr int kGT = 8;                  // ints per group-table entry
 constexpr int kMetricRows = 32;         // vectors of a cov_metric workgroup
 constexpr int kOSplit = 4;              // key splits of cov_output (workgroups per 64-row item)
 constexpr int kTSplit = 4;              // group splits of cov_terms (workgroups per token chunk)
+constexpr int kTermsLdsRep = 16;        // most query heads per KV head of cov_terms' LDS form
 constexpr int kSSplit = 16;             // row splits of cov_smat (workgroups per 16 rows of S)
 constexpr float kCLog2e = 1.4426950408889634f;
 
@@ -73,7 +74,7 @@ struct CovParams {
   uint32_t* mop;                         // (Hkv, NR, 4 ks, 4 g, 2 parts) u32x4: o M operand parts
   float* rowf;                           // (Hkv, NR) float4: row max, 1 / sum, o M o, o M scale
   float* vmv;                            // (Hkv, rep, n)
-  float* ddpart;                         // (G, Hkv, n_chunks)
+  float* ddpart;                         // (G, Hkv, n_chunks, 4): drop totals per wavefront
   float* alpha_part;                     // (Hkv, n_chunks, NR)
   float* gw;                             // (G): 1 / N or 0; [G]: live count
   float* roww;                           // (Hkv, NR): weight * alpha
@@ -637,21 +638,36 @@ __global__ __launch_bounds__(kCThreads) void cov_rowprep(CovParams p) {
     reinterpret_cast<float4*>(p.rowf)[rid] = make_float4(p.row_m[rid], p.row_il[rid], p.oMo[rid], ldexpf(1.0f, ex - 8));
 }
 
-// per (h, 256-token chunk): every group reaching the chunk, its rows in 64-row blocks (one 16-row
-// block per wavefront, one query head per block since nq_pad is a multiple of 16), 16-token tiles.
-// WEIGHTED = false: drop totals and key-term masses; true: the weighted per-token sums.
-template <int DT, bool WEIGHTED>
-__global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
+// per (h, 256-token chunk, group split): every group reaching the chunk, its rows in 64-row blocks
+// (one 16-row block per wavefront, one query head per block since nq_pad is a multiple of 16),
+// 16-token tiles.  WEIGHTED = false: drop totals (one partial per wavefront, combined in order by
+// cov_groups) and key-term masses; true: the weighted per-token sums.
+// LDS (16-bit keys and values, rep <= kTermsLdsRep): the chunk's 256 key and value rows (128 KiB)
+// and its v M v of every query head are staged in LDS once, and every group and wavefront reads its
+// tiles there (a tile used to come from L2 once per group and wavefront).  Row t of a tensor holds
+// its 16-byte column c at c ^ (t & 15), so the 16 tokens of a tile read in one instruction fall on
+// distinct banks.  The workgroup is two quads of wavefronts (two per SIMD, so one's products overlap
+// the other's terms): for the drop totals the quads take alternate groups with work; for the weighted
+// sums every group, quad q the tokens [c0 + 128 q, c0 + 128 q + 128).  Each sum keeps the order of
+// the one-quad form (a row's terms over the chunk in one wavefront, a token's over the groups in one
+// LDS cell), so the results are the same bit for bit.  LDS = false: tiles and v M v from memory, one
+// tile ahead, one quad.
+template <int DT, bool WEIGHTED, bool LDS>
+__global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(CovParams p) {
   constexpr int NH = TileOps<DT>::NH;
+  static_assert(!LDS || NH == 1, "LDS tiles hold 16-bit rows");
+  constexpr int NT = LDS ? 2 * kCThreads : kCThreads;
+  __shared__ u32x4 kv_lds[LDS ? 2 * kChunkTok * 16 : 1];         // [K, V][token][16-byte column]
+  __shared__ float vmv_lds[LDS ? kTermsLdsRep * kChunkTok : 1];  // [query head][token]
   __shared__ float accA[kCWaves][kChunkTok];
   __shared__ float accD[kCWaves][kChunkTok];
   __shared__ float accW[kCWaves][kChunkTok];             // read mass of the wavefront's current block
-  __shared__ float red[kCWaves];
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
+  const int quad = wave / kCWaves, wq = wave % kCWaves;
   // groups ts, ts + kTSplit, ... of (h, chunk): the chunks near the start, which every group reaches,
   // spread over kTSplit workgroups.  Work units u = (h, chunk, ts) in order; block b runs on XCD b % 8
   // (round-robin dispatch), and each XCD takes a contiguous range of units, so the splits of a chunk
-  // share one L2 and its key and value tiles, which every group re-reads, stay there.
+  // share one L2 and its key and value tiles stay there.
   const int u = xcd_unit(p.Hkv * p.n_chunks * kTSplit);
   if (u < 0) return;
   const int ts = u % kTSplit;
@@ -661,29 +677,69 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
   const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, TileOps<DT>::ESZ);
   const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v, p.v_sh, p.v_st, h, p.T, TileOps<DT>::ESZ);
   if constexpr (WEIGHTED) {
-    for (int u = threadIdx.x; u < kCWaves * kChunkTok; u += kCThreads) {
+    for (int u = threadIdx.x; u < kCWaves * kChunkTok; u += NT) {
       (&accA[0][0])[u] = 0.0f;
       (&accD[0][0])[u] = 0.0f;
     }
   }
+  // a group has work in this chunk if it reaches it (and, weighted, has a nonzero weight)
+  auto has_work = [&](int grp) { return p.gtab[kGT * grp + 4] > c0 && (!WEIGHTED || p.gw[grp] != 0.0f); };
+  if constexpr (LDS) {
+    bool used = false;                                   // some group of this split reaches the chunk
+    for (int grp = ts; grp < p.G; grp += kTSplit) used = used || has_work(grp);
+    if (used) {
+      // 16-byte unit u = (tensor, token, column): all of a thread's loads issued before its stores
+      constexpr int kPer = 2 * kChunkTok * 16 / NT;
+      u32x4 x[kPer];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int u = i * NT + static_cast<int>(threadIdx.x);
+        const int tok = (u >> 4) & (kChunkTok - 1), col = u & 15;
+        const bool key = u < kChunkTok * 16;
+        const int64_t off = (static_cast<int64_t>(c0 + tok) * (key ? p.k_st : p.v_st) + 8 * col) * 2;
+        x[i] = __builtin_amdgcn_raw_buffer_load_b128(key ? rk : rv, static_cast<int>(off), 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int u = i * NT + static_cast<int>(threadIdx.x);
+        const int tok = (u >> 4) & (kChunkTok - 1), col = u & 15;
+        kv_lds[((u < kChunkTok * 16 ? 0 : kChunkTok) + tok) * 16 + (col ^ (tok & 15))] = x[i];
+      }
+      for (int u = threadIdx.x; u < p.rep * kChunkTok; u += NT) {
+        const int r = u / kChunkTok, j = c0 + u % kChunkTok;
+        vmv_lds[u] = j < c1 ? p.vmv[(static_cast<int64_t>(h) * p.rep + r) * p.n + (j - p.rs)] : 0.0f;
+      }
+    }
+    __syncthreads();
+  }
+  int n_work = 0;                                        // groups with work so far (drop totals, LDS)
   for (int grp = ts; grp < p.G; grp += kTSplit) {
     const int32_t* gt = p.gtab + kGT * grp;
     const int row_base = gt[0], nq = gt[1], nq_pad = gt[2], te = gt[4], local = gt[5];
     const int rows_g = p.rep * nq_pad;
+    const int64_t dd_at = ((static_cast<int64_t>(grp) * p.Hkv + h) * p.n_chunks + chunk) * kCWaves;
     if (te <= c0) {                                      // the group does not reach this chunk
       if constexpr (!WEIGHTED) {
-        for (int u = threadIdx.x; u < rows_g; u += kCThreads)
-          p.alpha_part[(static_cast<int64_t>(h) * p.n_chunks + chunk) * p.NR + row_base + u] = 0.0f;
-        if (threadIdx.x == 0) p.ddpart[(static_cast<int64_t>(grp) * p.Hkv + h) * p.n_chunks + chunk] = 0.0f;
+        if (quad == 0) {
+          for (int u = threadIdx.x; u < rows_g; u += kCThreads)
+            p.alpha_part[(static_cast<int64_t>(h) * p.n_chunks + chunk) * p.NR + row_base + u] = 0.0f;
+          if (threadIdx.x < kCWaves) p.ddpart[dd_at + threadIdx.x] = 0.0f;
+        }
       }
       continue;
     }
     if (WEIGHTED && p.gw[grp] == 0.0f) continue;        // N = 0: every term of the group is zero
+    if constexpr (LDS && !WEIGHTED) {
+      if ((n_work++ & 1) != quad) continue;              // the other quad's group
+    }
     const int t_end = min(c1, te);
-    const float wq = (WEIGHTED ? p.gw[grp] : 1.0f) / static_cast<float>(nq);
+    // the tiles of this quad: weighted LDS form, its half of the chunk
+    const int ta0 = LDS && WEIGHTED ? c0 + (kChunkTok / 2) * quad : c0;
+    const int ta1 = LDS && WEIGHTED ? min(t_end, ta0 + kChunkTok / 2) : t_end;
+    const float wq_w = (WEIGHTED ? p.gw[grp] : 1.0f) / static_cast<float>(nq);
     float dsum = 0.0f;                                   // drop terms of this wavefront (pass A)
     for (int rb0 = 0; rb0 < rows_g; rb0 += 64) {
-      const int rbl = rb0 + 16 * wave;                    // this wavefront's first row in the group
+      const int rbl = rb0 + 16 * wq;                      // this wavefront's first row in the group
       const bool act = rbl < rows_g;
       const int r = act ? rbl / nq_pad : 0;
       const int row0 = row_base + rbl;
@@ -726,27 +782,37 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
         }
       }
       if constexpr (WEIGHTED) {
-        for (int u = l; u < kChunkTok; u += 64) accW[wave][u] = 0.0f;
+        for (int u = ta0 - c0 + l; u < ta0 - c0 + (LDS ? kChunkTok / 2 : kChunkTok); u += 64) accW[wq][u] = 0.0f;
         wave_lds_fence();
       }
       float alpha[4] = {0.0f, 0.0f, 0.0f, 0.0f};          // key-term mass of rows 4g + i (pass A)
-      // a tile's loads (key and value tiles, v M v of this lane's token); the next tile's go out as
-      // soon as the current tiles have entered the matrix products
+      // a tile's operands (key and value tiles, v M v of this lane's token); the next tile's are
+      // fetched as soon as the current tiles have entered the matrix products
       const int64_t vmv_base = (static_cast<int64_t>(h) * p.rep + r) * p.n - p.rs;   // + token j
       u32x4 kop[4][NH], vop[4][NH];
       float vmv1;
       auto load_t = [&](int t0) {
-        load_tile<DT>(rk, p.k_st, t0, g, n, kop);
-        load_tile<DT>(rv, p.v_st, t0, g, n, vop);
         const int j = t0 + n;
-        vmv1 = (act && j < t_end) ? p.vmv[vmv_base + j] : 0.0f;
+        if constexpr (LDS) {
+          const int row = t0 - c0 + n;                     // (t0 - c0) % 16 == 0: row & 15 == n
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            kop[ks][0] = kv_lds[row * 16 + ((4 * ks + g) ^ n)];
+            vop[ks][0] = kv_lds[(kChunkTok + row) * 16 + ((4 * ks + g) ^ n)];
+          }
+          vmv1 = (act && j < t_end) ? vmv_lds[r * kChunkTok + row] : 0.0f;
+        } else {
+          load_tile<DT>(rk, p.k_st, t0, g, n, kop);
+          load_tile<DT>(rv, p.v_st, t0, g, n, vop);
+          vmv1 = (act && j < t_end) ? p.vmv[vmv_base + j] : 0.0f;
+        }
       };
-      if (c0 < t_end) load_t(c0);
-      for (int t0 = c0; t0 < t_end; t0 += 16) {
+      if (ta0 < ta1) load_t(ta0);
+      for (int t0 = ta0; t0 < ta1; t0 += 16) {
         const f32x4 s = tile_dots<DT, NH, NH>(qop, kop);
         const f32x4 ov = tile_dots<DT, 2, NH>(mop, vop);
         const float vmv = vmv1;
-        if (t0 + 16 < t_end) load_t(t0 + 16);
+        if (t0 + 16 < ta1) load_t(t0 + 16);
         const int j = t0 + n;
         float ta[4], td[4], tw[4];
 #pragma unroll
@@ -774,9 +840,9 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
           sd = xsum32(xsum16(sd));
           sw = xsum32(xsum16(sw));
           if (g == 0 && act && j < t_end) {
-            accA[wave][j - c0] += sa * wq;
-            accD[wave][j - c0] += sd * wq;
-            accW[wave][j - c0] += sw * wq;
+            accA[wq][j - c0] += sa * wq_w;
+            accD[wq][j - c0] += sd * wq_w;
+            accW[wq][j - c0] += sw * wq_w;
           }
         }
       }
@@ -792,7 +858,7 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
       } else {
         // the wavefronts' read masses into their query heads' rows of WVa, in wavefront order
         __syncthreads();
-        for (int u = threadIdx.x; u < t_end - c0; u += kCThreads) {
+        for (int u = threadIdx.x; u < t_end - c0; u += NT) {
           for (int w = 0; w < kCWaves; ++w) {
             const int rbw = rb0 + 16 * w;
             if (rbw >= rows_g) break;
@@ -804,18 +870,13 @@ __global__ __launch_bounds__(kCThreads) void cov_terms(CovParams p) {
       }
     }
     if constexpr (!WEIGHTED) {
-      dsum = wave_sum(dsum);
-      if (l == 0) red[wave] = dsum;
-      __syncthreads();
-      if (threadIdx.x == 0)
-        p.ddpart[(static_cast<int64_t>(grp) * p.Hkv + h) * p.n_chunks + chunk] =
-            ((red[0] + red[1]) + (red[2] + red[3])) / static_cast<float>(nq);
-      __syncthreads();
+      dsum = wave_sum(dsum);                             // cov_groups adds the four in order
+      if (l == 0) p.ddpart[dd_at + wq] = dsum;
     }
   }
   if constexpr (WEIGHTED) {
     __syncthreads();
-    for (int u = threadIdx.x; u < c1 - c0; u += kCThreads) {
+    for (int u = threadIdx.x; u < c1 - c0; u += NT) {
       const int64_t o = (static_cast<int64_t>(ts) * p.Hkv + h) * p.n + (c0 + u - p.rs);
       p.A_part[o] = (accA[0][u] + accA[1][u]) + (accA[2][u] + accA[3][u]);
       p.DD_part[o] = (accD[0][u] + accD[1][u]) + (accD[2][u] + accD[3][u]);
@@ -829,8 +890,13 @@ __global__ __launch_bounds__(kCThreads) void cov_groups(CovParams p) {
   float live = 0.0f;
   const int per = p.Hkv * p.n_chunks;
   for (int grp = 0; grp < p.G; ++grp) {
+    // the drop total of (group, h, chunk): cov_terms' four wavefront partials, in order, over nq
+    const float nq = static_cast<float>(p.gtab[kGT * grp + 1]);
     float s = 0.0f;
-    for (int u = threadIdx.x; u < per; u += kCThreads) s += p.ddpart[static_cast<int64_t>(grp) * per + u];
+    for (int u = threadIdx.x; u < per; u += kCThreads) {
+      const float* d = p.ddpart + (static_cast<int64_t>(grp) * per + u) * kCWaves;
+      s += ((d[0] + d[1]) + (d[2] + d[3])) / nq;
+    }
     s = wave_sum(s);
     if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = s;
     __syncthreads();
@@ -1004,13 +1070,13 @@ __global__ __launch_bounds__(kCThreads) void cov_final(CovParams p) {
 using namespace kvq;
 
 // workspace layout (floats): row_m, row_il, oMo, roww (Hkv NR each); o (Hkv NR d); o_part (kOSplit Hkv
-// NR d); vmv (Hkv rep n); ddpart (G Hkv n_chunks); alpha_part (Hkv n_chunks NR); gw (G + 1); red (4 +
+// NR d); vmv (Hkv rep n); ddpart (G Hkv n_chunks 4); alpha_part (Hkv n_chunks NR); gw (G + 1); red (4 +
 // Hkv rep + Hkv); WVa (Hkv rep n); A_part, DD_part (kTSplit Hkv n each); WVa_part (kTSplit Hkv rep n);
 // mop (Hkv NR 128), rowf (Hkv NR 4), 16-byte aligned; S_part (kSSplit Hkv d d); sums (Hkv (2 + rep))
 extern "C" int64_t kvq_coverage_stats_workspace(int64_t Hkv, int64_t rep, int64_t n, int64_t NR, int64_t G) {
   if (Hkv <= 0 || rep <= 0 || n <= 0 || NR <= 0 || G <= 0) return -1;
   const int64_t nch = (n + kChunkTok - 1) / kChunkTok;
-  return 4 * Hkv * NR + (1 + kOSplit) * Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch + Hkv * nch * NR + (G + 1) +
+  return 4 * Hkv * NR + (1 + kOSplit) * Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch * kCWaves + Hkv * nch * NR + (G + 1) +
          (4 + Hkv * rep + Hkv) + Hkv * rep * n + kTSplit * (2 * Hkv * n + Hkv * rep * n) + 132 * Hkv * NR + 4 + kSSplit * Hkv * kCD * kCD + Hkv * (2 + rep);
 }
 
@@ -1056,7 +1122,7 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   p.o = w; w += Hkv * NR * kCD;
   p.o_part = w; w += kOSplit * Hkv * NR * kCD;
   p.vmv = w; w += Hkv * rep * n;
-  p.ddpart = w; w += G * Hkv * p.n_chunks;
+  p.ddpart = w; w += G * Hkv * p.n_chunks * kCWaves;
   p.alpha_part = w; w += Hkv * p.n_chunks * NR;
   p.gw = w; w += G + 1;
   p.red = w; w += 4 + Hkv * rep + Hkv;
@@ -1085,7 +1151,16 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   const unsigned terms_blocks = xcd_grid(Hkv * p.n_chunks * kTSplit);
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowprep<DT_>), dim3((Hkv * NR + 15) / 16), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(row operands)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, false>), dim3(terms_blocks), blk, 0, s, p));
+  // 16-bit rows and up to kTermsLdsRep query heads per KV head: the chunk's rows staged in LDS, two
+  // quads of wavefronts
+  const bool terms_lds = dtype != KVQ_F32 && rep <= kTermsLdsRep;
+  const dim3 blk2(2 * kCThreads);
+  if (terms_lds) {
+    if (dtype == KVQ_BF16) hipLaunchKernelGGL((cov_terms<KVQ_BF16, false, true>), dim3(terms_blocks), blk2, 0, s, p);
+    else hipLaunchKernelGGL((cov_terms<KVQ_F16, false, true>), dim3(terms_blocks), blk2, 0, s, p);
+  } else {
+    KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, false, false>), dim3(terms_blocks), blk, 0, s, p));
+  }
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(terms)");
   hipLaunchKernelGGL(cov_groups, dim3(1), blk, 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(groups)");
@@ -1095,7 +1170,12 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   const int64_t nwp = kTSplit * Hkv * rep * n;
   hipLaunchKernelGGL(cov_clear, dim3((nwp + kCThreads - 1) / kCThreads), blk, 0, s, p.WVa_part, nwp);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(clear)");
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, true>), dim3(terms_blocks), blk, 0, s, p));
+  if (terms_lds) {
+    if (dtype == KVQ_BF16) hipLaunchKernelGGL((cov_terms<KVQ_BF16, true, true>), dim3(terms_blocks), blk2, 0, s, p);
+    else hipLaunchKernelGGL((cov_terms<KVQ_F16, true, true>), dim3(terms_blocks), blk2, 0, s, p);
+  } else {
+    KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, true, false>), dim3(terms_blocks), blk, 0, s, p));
+  }
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(weighted terms)");
   hipLaunchKernelGGL(cov_split_sums, dim3((Hkv * rep * n + kCThreads - 1) / kCThreads), blk, 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(split sums)");
