@@ -49,7 +49,7 @@ constexpr int kGT = 8;                  // ints per group-table entry
 constexpr int kMetricRows = 32;         // vectors of a cov_metric workgroup
 constexpr int kOSplit = 4;              // key splits of cov_output (workgroups per 64-row item)
 constexpr int kTSplit = 4;              // group splits of cov_terms (workgroups per token chunk)
-constexpr int kTermsLdsRep = 16;        // most query heads per KV head of cov_terms' LDS form
+constexpr int kTermsLdsRep = 8;         // most query heads per KV head of cov_terms' LDS form
 constexpr int kSSplit = 16;             // row splits of cov_smat (workgroups per 16 rows of S)
 constexpr float kCLog2e = 1.4426950408889634f;
 
@@ -643,7 +643,8 @@ __global__ __launch_bounds__(kCThreads) void cov_rowprep(CovParams p) {
 // 16-token tiles.  WEIGHTED = false: drop totals (one partial per wavefront, combined in order by
 // cov_groups) and key-term masses; true: the weighted per-token sums.
 // LDS (16-bit keys and values, rep <= kTermsLdsRep): the chunk's 256 key and value rows (128 KiB)
-// and its v M v of every query head are staged in LDS once, and every group and wavefront reads its
+// and its v M v of every query head are staged in LDS once (the weighted pass also keeps its read
+// masses there until the end), and every group and wavefront reads its
 // tiles there (a tile used to come from L2 once per group and wavefront).  Row t of a tensor holds
 // its 16-byte column c at c ^ (t & 15), so the 16 tokens of a tile read in one instruction fall on
 // distinct banks.  The workgroup is two quads of wavefronts (two per SIMD, so one's products overlap
@@ -659,6 +660,7 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
   constexpr int NT = LDS ? 2 * kCThreads : kCThreads;
   __shared__ u32x4 kv_lds[LDS ? 2 * kChunkTok * 16 : 1];         // [K, V][token][16-byte column]
   __shared__ float vmv_lds[LDS ? kTermsLdsRep * kChunkTok : 1];  // [query head][token]
+  __shared__ float wva_lds[LDS && WEIGHTED ? kTermsLdsRep * kChunkTok : 1];   // read masses [head][token]
   __shared__ float accA[kCWaves][kChunkTok];
   __shared__ float accD[kCWaves][kChunkTok];
   __shared__ float accW[kCWaves][kChunkTok];             // read mass of the wavefront's current block
@@ -681,6 +683,8 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
       (&accA[0][0])[u] = 0.0f;
       (&accD[0][0])[u] = 0.0f;
     }
+    if constexpr (LDS)
+      for (int u = threadIdx.x; u < kTermsLdsRep * kChunkTok; u += NT) wva_lds[u] = 0.0f;
   }
   // a group has work in this chunk if it reaches it (and, weighted, has a nonzero weight)
   auto has_work = [&](int grp) { return p.gtab[kGT * grp + 4] > c0 && (!WEIGHTED || p.gw[grp] != 0.0f); };
@@ -713,6 +717,10 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
     __syncthreads();
   }
   int n_work = 0;                                        // groups with work so far (drop totals, LDS)
+  // weighted LDS form: this lane's token sums over the groups, tile by tile of the quad's half
+  float rA[kChunkTok / 32], rD[kChunkTok / 32];
+#pragma unroll
+  for (int it = 0; it < kChunkTok / 32; ++it) rA[it] = rD[it] = 0.0f;
   for (int grp = ts; grp < p.G; grp += kTSplit) {
     const int32_t* gt = p.gtab + kGT * grp;
     const int row_base = gt[0], nq = gt[1], nq_pad = gt[2], te = gt[4], local = gt[5];
@@ -781,8 +789,8 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
           msc[i] = 1.0f;
         }
       }
-      if constexpr (WEIGHTED) {
-        for (int u = ta0 - c0 + l; u < ta0 - c0 + (LDS ? kChunkTok / 2 : kChunkTok); u += 64) accW[wq][u] = 0.0f;
+      if constexpr (WEIGHTED && !LDS) {
+        for (int u = l; u < kChunkTok; u += 64) accW[wq][u] = 0.0f;
         wave_lds_fence();
       }
       float alpha[4] = {0.0f, 0.0f, 0.0f, 0.0f};          // key-term mass of rows 4g + i (pass A)
@@ -807,14 +815,10 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
           vmv1 = (act && j < t_end) ? p.vmv[vmv_base + j] : 0.0f;
         }
       };
-      if (ta0 < ta1) load_t(ta0);
-      for (int t0 = ta0; t0 < ta1; t0 += 16) {
-        const f32x4 s = tile_dots<DT, NH, NH>(qop, kop);
-        const f32x4 ov = tile_dots<DT, 2, NH>(mop, vop);
-        const float vmv = vmv1;
-        if (t0 + 16 < ta1) load_t(t0 + 16);
+      // the terms of (row 4g + i, token t0 + n) from the tile's products
+      auto terms = [&](int t0, const f32x4& s, const f32x4& ov, float vmv, float (&ta)[4], float (&td)[4],
+                       float (&tw)[4]) {
         const int j = t0 + n;
-        float ta[4], td[4], tw[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const bool far = act && j < t_end && j <= pos[i] - local;
@@ -825,24 +829,67 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
           ta[i] = pr * pr * u2;
           tw[i] = pr * pr;
         }
-        if constexpr (!WEIGHTED) {
+      };
+      if constexpr (LDS && WEIGHTED) {
+        // the quad's eight tiles unrolled: token t0 + n's sums over the groups stay in registers (a
+        // masked token adds +0, which leaves a sum of nonnegative terms unchanged)
+        float wr[kChunkTok / 32];
+        if (ta0 < ta1) load_t(ta0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            dsum += td[i];
-            alpha[i] += ta[i];
+        for (int it = 0; it < kChunkTok / 32; ++it) {
+          const int t0 = ta0 + 16 * it;
+          wr[it] = 0.0f;
+          if (t0 < ta1) {
+            const f32x4 s = tile_dots<DT, NH, NH>(qop, kop);
+            const f32x4 ov = tile_dots<DT, 2, NH>(mop, vop);
+            const float vmv = vmv1;
+            if (t0 + 16 < ta1) load_t(t0 + 16);
+            float ta[4], td[4], tw[4];
+            terms(t0, s, ov, vmv, ta, td, tw);
+            float sa = (ta[0] + ta[1]) + (ta[2] + ta[3]);
+            float sd = (td[0] + td[1]) + (td[2] + td[3]);
+            float sw = (tw[0] + tw[1]) + (tw[2] + tw[3]);
+            sa = xsum32(xsum16(sa));
+            sd = xsum32(xsum16(sd));
+            sw = xsum32(xsum16(sw));
+            rA[it] += sa * wq_w;
+            rD[it] += sd * wq_w;
+            wr[it] = sw * wq_w;
           }
-        } else {
-          // token t0 + n: its sums over the block's 16 rows (the lane's four, then the lane groups')
-          float sa = (ta[0] + ta[1]) + (ta[2] + ta[3]);
-          float sd = (td[0] + td[1]) + (td[2] + td[3]);
-          float sw = (tw[0] + tw[1]) + (tw[2] + tw[3]);
-          sa = xsum32(xsum16(sa));
-          sd = xsum32(xsum16(sd));
-          sw = xsum32(xsum16(sw));
-          if (g == 0 && act && j < t_end) {
-            accA[wq][j - c0] += sa * wq_w;
-            accD[wq][j - c0] += sd * wq_w;
-            accW[wq][j - c0] += sw * wq_w;
+        }
+        if (g == 0) {
+#pragma unroll
+          for (int it = 0; it < kChunkTok / 32; ++it) accW[wq][ta0 - c0 + 16 * it + n] = wr[it];
+        }
+      } else {
+        if (ta0 < ta1) load_t(ta0);
+        for (int t0 = ta0; t0 < ta1; t0 += 16) {
+          const f32x4 s = tile_dots<DT, NH, NH>(qop, kop);
+          const f32x4 ov = tile_dots<DT, 2, NH>(mop, vop);
+          const float vmv = vmv1;
+          if (t0 + 16 < ta1) load_t(t0 + 16);
+          const int j = t0 + n;
+          float ta[4], td[4], tw[4];
+          terms(t0, s, ov, vmv, ta, td, tw);
+          if constexpr (!WEIGHTED) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              dsum += td[i];
+              alpha[i] += ta[i];
+            }
+          } else {
+            // token t0 + n: its sums over the block's 16 rows (the lane's four, then the lane groups')
+            float sa = (ta[0] + ta[1]) + (ta[2] + ta[3]);
+            float sd = (td[0] + td[1]) + (td[2] + td[3]);
+            float sw = (tw[0] + tw[1]) + (tw[2] + tw[3]);
+            sa = xsum32(xsum16(sa));
+            sd = xsum32(xsum16(sd));
+            sw = xsum32(xsum16(sw));
+            if (g == 0 && act && j < t_end) {
+              accA[wq][j - c0] += sa * wq_w;
+              accD[wq][j - c0] += sd * wq_w;
+              accW[wq][j - c0] += sw * wq_w;
+            }
           }
         }
       }
@@ -856,14 +903,18 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
                 a_row / static_cast<float>(nq);
         }
       } else {
-        // the wavefronts' read masses into their query heads' rows of WVa, in wavefront order
+        // the wavefronts' read masses into their query heads' rows of WVa, in wavefront order (LDS:
+        // kept in LDS until the workgroup ends, then stored once)
         __syncthreads();
         for (int u = threadIdx.x; u < t_end - c0; u += NT) {
           for (int w = 0; w < kCWaves; ++w) {
             const int rbw = rb0 + 16 * w;
             if (rbw >= rows_g) break;
-            p.WVa_part[((static_cast<int64_t>(ts) * p.Hkv + h) * p.rep + rbw / nq_pad) * p.n + (c0 + u - p.rs)] +=
-                accW[w][u];
+            if constexpr (LDS)
+              wva_lds[(rbw / nq_pad) * kChunkTok + u] += accW[w][u];
+            else
+              p.WVa_part[((static_cast<int64_t>(ts) * p.Hkv + h) * p.rep + rbw / nq_pad) * p.n + (c0 + u - p.rs)] +=
+                  accW[w][u];
           }
         }
         __syncthreads();
@@ -875,7 +926,24 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
     }
   }
   if constexpr (WEIGHTED) {
+    if constexpr (LDS) {
+      if (g == 0) {
+        const int tb = (kChunkTok / 2) * quad;
+#pragma unroll
+        for (int it = 0; it < kChunkTok / 32; ++it) {
+          accA[wq][tb + 16 * it + n] = rA[it];
+          accD[wq][tb + 16 * it + n] = rD[it];
+        }
+      }
+    }
     __syncthreads();
+    if constexpr (LDS) {
+      // this workgroup is the only writer of its (split, h, heads, chunk) read masses
+      for (int u = threadIdx.x; u < p.rep * kChunkTok; u += NT) {
+        const int r = u / kChunkTok, t = u % kChunkTok;
+        if (c0 + t < c1) p.WVa_part[((static_cast<int64_t>(ts) * p.Hkv + h) * p.rep + r) * p.n + (c0 + t - p.rs)] = wva_lds[u];
+      }
+    }
     for (int u = threadIdx.x; u < c1 - c0; u += NT) {
       const int64_t o = (static_cast<int64_t>(ts) * p.Hkv + h) * p.n + (c0 + u - p.rs);
       p.A_part[o] = (accA[0][u] + accA[1][u]) + (accA[2][u] + accA[3][u]);
