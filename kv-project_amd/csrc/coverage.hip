@@ -26,7 +26,7 @@
 //                 chunk, logits and v.(oM) of 16-token tiles on the matrix cores (rows as the A side:
 //                 a lane holds four rows of one token), then the per-(row, token) terms: the group's
 //                 drop total and every row's key-term mass, as partials per chunk.
-//   cov_groups    N per group -> weight 1 / N (0 if N = 0), live count.
+//   cov_groups    N per group -> weight 1 / N (0 if N = 0), live flag.
 //   cov_roww      per row: its group's weight x its key-term mass.
 //   cov_terms<B>  the same tiles with the weights: A, DD and the read mass per query head, one partial
 //                 per group split; cov_split_sums adds the splits in order.
@@ -76,7 +76,7 @@ struct CovParams {
   float* vmv;                            // (Hkv, rep, n)
   float* ddpart;                         // (G, Hkv, n_chunks, 4): drop totals per wavefront
   float* alpha_part;                     // (Hkv, n_chunks, NR)
-  float* gw;                             // (G): 1 / N or 0; [G]: live count
+  float* gw;                             // (2 G + 1): 1 / N or 0 per group; [G + 1 + group]: 1 if live
   float* roww;                           // (Hkv, NR): weight * alpha
   float* red;                            // finalisation sums
   float* sums;                           // (Hkv, 2 + rep): per-head sums of A, DD, read masses
@@ -686,11 +686,18 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
     if constexpr (LDS)
       for (int u = threadIdx.x; u < kTermsLdsRep * kChunkTok; u += NT) wva_lds[u] = 0.0f;
   }
+  // weighted LDS form: every group with work has 16 padded queries, so a wavefront's 16 rows are one
+  // query head and a head's read masses only ever come from one wavefront (no barrier between blocks)
+  bool solo = LDS && WEIGHTED;
   // a group has work in this chunk if it reaches it (and, weighted, has a nonzero weight)
   auto has_work = [&](int grp) { return p.gtab[kGT * grp + 4] > c0 && (!WEIGHTED || p.gw[grp] != 0.0f); };
   if constexpr (LDS) {
     bool used = false;                                   // some group of this split reaches the chunk
-    for (int grp = ts; grp < p.G; grp += kTSplit) used = used || has_work(grp);
+    for (int grp = ts; grp < p.G; grp += kTSplit) {
+      const bool w = has_work(grp);
+      used = used || w;
+      solo = solo && (!w || p.gtab[kGT * grp + 2] == 16);
+    }
     if (used) {
       // 16-byte unit u = (tensor, token, column): all of a thread's loads issued before its stores
       constexpr int kPer = 2 * kChunkTok * 16 / NT;
@@ -857,7 +864,12 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
             wr[it] = sw * wq_w;
           }
         }
-        if (g == 0) {
+        if (solo) {
+          if (g == 0 && act) {
+#pragma unroll
+            for (int it = 0; it < kChunkTok / 32; ++it) wva_lds[r * kChunkTok + ta0 - c0 + 16 * it + n] += wr[it];
+          }
+        } else if (g == 0) {
 #pragma unroll
           for (int it = 0; it < kChunkTok / 32; ++it) accW[wq][ta0 - c0 + 16 * it + n] = wr[it];
         }
@@ -902,7 +914,7 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
             p.alpha_part[(static_cast<int64_t>(h) * p.n_chunks + chunk) * p.NR + row0 + 4 * g + i] =
                 a_row / static_cast<float>(nq);
         }
-      } else {
+      } else if (!solo) {
         // the wavefronts' read masses into their query heads' rows of WVa, in wavefront order (LDS:
         // kept in LDS until the workgroup ends, then stored once)
         __syncthreads();
@@ -952,28 +964,27 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
   }
 }
 
-// N per group (over heads and chunks) -> weights; live count in gw[G]
+// N per group (over heads and chunks) -> weight 1 / N (0 if N = 0) in gw[group], and whether the
+// group is live (N > 0) in gw[G + 1 + group]; one workgroup per group
 __global__ __launch_bounds__(kCThreads) void cov_groups(CovParams p) {
   __shared__ float red[kCWaves];
-  float live = 0.0f;
+  const int grp = blockIdx.x;
   const int per = p.Hkv * p.n_chunks;
-  for (int grp = 0; grp < p.G; ++grp) {
-    // the drop total of (group, h, chunk): cov_terms' four wavefront partials, in order, over nq
-    const float nq = static_cast<float>(p.gtab[kGT * grp + 1]);
-    float s = 0.0f;
-    for (int u = threadIdx.x; u < per; u += kCThreads) {
-      const float* d = p.ddpart + (static_cast<int64_t>(grp) * per + u) * kCWaves;
-      s += ((d[0] + d[1]) + (d[2] + d[3])) / nq;
-    }
-    s = wave_sum(s);
-    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = s;
-    __syncthreads();
-    const float N = (red[0] + red[1]) + (red[2] + red[3]);
-    if (threadIdx.x == 0) p.gw[grp] = N > 0.0f ? 1.0f / N : 0.0f;
-    live += N > 0.0f ? 1.0f : 0.0f;
-    __syncthreads();
+  // the drop total of (group, h, chunk): cov_terms' four wavefront partials, in order, over nq
+  const float nq = static_cast<float>(p.gtab[kGT * grp + 1]);
+  float s = 0.0f;
+  for (int u = threadIdx.x; u < per; u += kCThreads) {
+    const float* d = p.ddpart + (static_cast<int64_t>(grp) * per + u) * kCWaves;
+    s += ((d[0] + d[1]) + (d[2] + d[3])) / nq;
   }
-  if (threadIdx.x == 0) p.gw[p.G] = live;
+  s = wave_sum(s);
+  if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float N = (red[0] + red[1]) + (red[2] + red[3]);
+    p.gw[grp] = N > 0.0f ? 1.0f / N : 0.0f;
+    p.gw[p.G + 1 + grp] = N > 0.0f ? 1.0f : 0.0f;
+  }
 }
 
 // per row: its group's weight x its key-term mass (summed over the chunks)
@@ -1080,7 +1091,9 @@ __global__ __launch_bounds__(1024) void cov_final_sums(CovParams p) {
 
 __global__ void cov_final_combine(CovParams p) {
   if (threadIdx.x != 0) return;
-  const float live = fmaxf(p.gw[p.G], 1.0f);
+  float live = 0.0f;                                      // live groups, counted in group order
+  for (int g = 0; g < p.G; ++g) live += p.gw[p.G + 1 + g];
+  live = fmaxf(live, 1.0f);
   const int nk = 2 + p.rep;
   float gA = 0.0f, gD = 0.0f, gW = 0.0f;
   for (int h = 0; h < p.Hkv; ++h) {
@@ -1138,13 +1151,13 @@ __global__ __launch_bounds__(kCThreads) void cov_final(CovParams p) {
 using namespace kvq;
 
 // workspace layout (floats): row_m, row_il, oMo, roww (Hkv NR each); o (Hkv NR d); o_part (kOSplit Hkv
-// NR d); vmv (Hkv rep n); ddpart (G Hkv n_chunks 4); alpha_part (Hkv n_chunks NR); gw (G + 1); red (4 +
+// NR d); vmv (Hkv rep n); ddpart (G Hkv n_chunks 4); alpha_part (Hkv n_chunks NR); gw (2 G + 1); red (4 +
 // Hkv rep + Hkv); WVa (Hkv rep n); A_part, DD_part (kTSplit Hkv n each); WVa_part (kTSplit Hkv rep n);
 // mop (Hkv NR 128), rowf (Hkv NR 4), 16-byte aligned; S_part (kSSplit Hkv d d); sums (Hkv (2 + rep))
 extern "C" int64_t kvq_coverage_stats_workspace(int64_t Hkv, int64_t rep, int64_t n, int64_t NR, int64_t G) {
   if (Hkv <= 0 || rep <= 0 || n <= 0 || NR <= 0 || G <= 0) return -1;
   const int64_t nch = (n + kChunkTok - 1) / kChunkTok;
-  return 4 * Hkv * NR + (1 + kOSplit) * Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch * kCWaves + Hkv * nch * NR + (G + 1) +
+  return 4 * Hkv * NR + (1 + kOSplit) * Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch * kCWaves + Hkv * nch * NR + (2 * G + 1) +
          (4 + Hkv * rep + Hkv) + Hkv * rep * n + kTSplit * (2 * Hkv * n + Hkv * rep * n) + 132 * Hkv * NR + 4 + kSSplit * Hkv * kCD * kCD + Hkv * (2 + rep);
 }
 
@@ -1192,7 +1205,7 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   p.vmv = w; w += Hkv * rep * n;
   p.ddpart = w; w += G * Hkv * p.n_chunks * kCWaves;
   p.alpha_part = w; w += Hkv * p.n_chunks * NR;
-  p.gw = w; w += G + 1;
+  p.gw = w; w += 2 * G + 1;
   p.red = w; w += 4 + Hkv * rep + Hkv;
   p.WVa = w; w += Hkv * rep * n;
   p.A_part = w; w += kTSplit * Hkv * n;
@@ -1230,7 +1243,7 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
     KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_terms<DT_, false, false>), dim3(terms_blocks), blk, 0, s, p));
   }
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(terms)");
-  hipLaunchKernelGGL(cov_groups, dim3(1), blk, 0, s, p);
+  hipLaunchKernelGGL(cov_groups, dim3(static_cast<unsigned>(G)), blk, 0, s, p);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(groups)");
   hipLaunchKernelGGL(cov_roww, dim3((Hkv * NR + kCThreads - 1) / kCThreads), blk, 0, s, p, rowgrp);
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(row weights)");
