@@ -266,9 +266,12 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
   constexpr int U16 = kCD * ESZ / 16;                        // 16-byte units of a value row
   __shared__ uint32_t vt[32 * VRW];
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
-  const int unit = xcd_unit(p.Hkv * kOSplit * p.n_items);      // (h, key split, item), h outermost
+  // work units (h, item, key split), h outermost; the items in reverse plan order, so the groups at
+  // the end of the context, whose keys reach furthest, start first and the short ones fill the tail
+  const int unit = xcd_unit(p.Hkv * kOSplit * p.n_items);
   if (unit < 0) return;
-  const int item = unit % p.n_items, h = unit / p.n_items / kOSplit, sp = unit / p.n_items % kOSplit;
+  const int h = unit / (p.n_items * kOSplit), w = unit % (p.n_items * kOSplit);
+  const int item = p.n_items - 1 - w / kOSplit, sp = w % kOSplit;
   const int grp = p.items[2 * item], rb = p.items[2 * item + 1];
   const int32_t* gt = p.gtab + kGT * grp;
   const int rows_g = p.rep * gt[2];
