@@ -144,19 +144,22 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rs, int64_t st,
 }
 
 // Every key tile a wavefront loads feeds several of the item's 16-row blocks (16-bit data: all four,
-// the wavefronts splitting the keys in quarters; fp32 operands take twice the registers: two blocks,
-// halves), so the workgroup reads its keys once instead of once per row block.  The wavefronts'
-// states of a row meet in LDS, split by split in a fixed order.
+// eight wavefronts (two per SIMD) splitting the keys in eighths; fp32 operands take twice the
+// registers: two blocks, four wavefronts in halves), so the workgroup reads its keys once instead of
+// once per row block.  The wavefronts' states of a row meet in LDS, split by split in a fixed order.
+// The items go in reverse plan order: the groups at the end of the context, whose keys reach
+// furthest, start first.
 template <int DT>
-__global__ __launch_bounds__(kCThreads) void cov_rowstats(CovParams p) {
+__global__ __launch_bounds__(DT == KVQ_F32 ? kCThreads : 2 * kCThreads) void cov_rowstats(CovParams p) {
   constexpr int NH = TileOps<DT>::NH;
+  constexpr int NW = DT == KVQ_F32 ? kCWaves : 2 * kCWaves;  // wavefronts (16-bit: two per SIMD)
   constexpr int NRB = DT == KVQ_F32 ? 2 : 4;                 // row blocks per wavefront
-  constexpr int KS = kCWaves * NRB / 4;                      // key splits (wavefronts sharing blocks)
-  __shared__ float st[kCWaves][NRB][16][2];
+  constexpr int KS = NW * NRB / 4;                           // key splits (wavefronts sharing blocks)
+  __shared__ float st[NW][NRB][16][2];
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
   const int unit = xcd_unit(p.Hkv * p.n_items);                // (h, item), h outermost
   if (unit < 0) return;
-  const int item = unit % p.n_items, h = unit / p.n_items;
+  const int item = p.n_items - 1 - unit % p.n_items, h = unit / p.n_items;
   const int grp = p.items[2 * item], rb = p.items[2 * item + 1];
   const int32_t* gt = p.gtab + kGT * grp;
   const int rows_g = p.rep * gt[2];
@@ -1222,7 +1225,8 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   p.A = A; p.W = W; p.DD = DD; p.S = S; p.Mbar = Mbar;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 blk(kCThreads);
-  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowstats<DT_>), dim3(xcd_grid(n_items * Hkv)), blk, 0, s, p));
+  KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowstats<DT_>), dim3(xcd_grid(n_items * Hkv)),
+                                               dim3(DT_ == KVQ_F32 ? kCThreads : 2 * kCThreads), 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(rowstats)");
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_output<DT_>), dim3(xcd_grid(n_items * Hkv * kOSplit)), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(output)");
