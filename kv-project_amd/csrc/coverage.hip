@@ -655,10 +655,9 @@ __global__ __launch_bounds__(kCThreads) void cov_rowprep(CovParams p) {
 // its 16-byte column c at c ^ (t & 15), so the 16 tokens of a tile read in one instruction fall on
 // distinct banks.  The workgroup is two quads of wavefronts (two per SIMD, so one's products overlap
 // the other's terms): for the drop totals the quads take alternate groups with work; for the weighted
-// sums every group, quad q the tokens [c0 + 128 q, c0 + 128 q + 128).  Each sum keeps the order of
-// the one-quad form (a row's terms over the chunk in one wavefront, a token's over the groups in one
-// LDS cell), so the results are the same bit for bit.  LDS = false: tiles and v M v from memory, one
-// tile ahead, one quad.
+// sums every group, quad q the tokens [c0 + 128 q, c0 + 128 q + 128), a lane's sums over the groups
+// kept in registers and added across the lane groups once at the end.  LDS = false: tiles and v M v
+// from memory, one tile ahead, one quad, a token's sums over the groups in LDS.
 template <int DT, bool WEIGHTED, bool LDS>
 __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(CovParams p) {
   constexpr int NH = TileOps<DT>::NH;
@@ -844,8 +843,9 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
         }
       };
       if constexpr (LDS && WEIGHTED) {
-        // the quad's eight tiles unrolled: token t0 + n's sums over the groups stay in registers (a
-        // masked token adds +0, which leaves a sum of nonnegative terms unchanged)
+        // the quad's eight tiles unrolled: token t0 + n's sums over the groups stay in registers, each
+        // lane's four rows apart from the other lane groups' until the workgroup ends (a masked token
+        // adds +0)
         float wr[kChunkTok / 32];
         if (ta0 < ta1) load_t(ta0);
 #pragma unroll
@@ -859,17 +859,14 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
             if (t0 + 16 < ta1) load_t(t0 + 16);
             float ta[4], td[4], tw[4];
             terms(t0, s, ov, vmv, ta, td, tw);
-            float sa = (ta[0] + ta[1]) + (ta[2] + ta[3]);
-            float sd = (td[0] + td[1]) + (td[2] + td[3]);
-            float sw = (tw[0] + tw[1]) + (tw[2] + tw[3]);
-            sa = xsum32(xsum16(sa));
-            sd = xsum32(xsum16(sd));
-            sw = xsum32(xsum16(sw));
-            rA[it] += sa * wq_w;
-            rD[it] += sd * wq_w;
-            wr[it] = sw * wq_w;
+            rA[it] += ((ta[0] + ta[1]) + (ta[2] + ta[3])) * wq_w;
+            rD[it] += ((td[0] + td[1]) + (td[2] + td[3])) * wq_w;
+            wr[it] = ((tw[0] + tw[1]) + (tw[2] + tw[3])) * wq_w;
           }
         }
+        // the block's read mass of token t0 + n: the four lane groups' rows added
+#pragma unroll
+        for (int it = 0; it < kChunkTok / 32; ++it) wr[it] = xsum32(xsum16(wr[it]));
         if (solo) {
           if (g == 0 && act) {
 #pragma unroll
@@ -945,6 +942,11 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
   }
   if constexpr (WEIGHTED) {
     if constexpr (LDS) {
+#pragma unroll
+      for (int it = 0; it < kChunkTok / 32; ++it) {
+        rA[it] = xsum32(xsum16(rA[it]));
+        rD[it] = xsum32(xsum16(rD[it]));
+      }
       if (g == 0) {
         const int tb = (kChunkTok / 2) * quad;
 #pragma unroll
