@@ -1003,6 +1003,62 @@ __global__ __launch_bounds__(kSThreads) void strata_merge(StrataParams p) {
   }
 }
 
+// The merge of one (b, h, row) when no exact rows are attended here and the row has at most NS
+// (<= 32) partials: one wavefront per row (four rows a workgroup, rows in strata_merge's grid order),
+// lane s holding partial s's (m, l) (exact-row partials first, then the strata's) and lane l channels
+// l and l + 64 of every partial's o, the FWHT's two coordinates; every load at once, wavefront
+// reductions, the coded sum rotated back in registers; no LDS and no barrier.  Same formula as
+// strata_merge: o = [sum_e w o_e + (sum_t w o_t) R + (sum_t w l_t) mu_V] / sum_all w l.
+template <int R, int DT, int NS>
+__global__ __launch_bounds__(kSThreads) void strata_merge_wave(StrataParams p, int n_rows) {
+  const int row = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x >> 6);
+  if (row >= n_rows) return;
+  const int lane = threadIdx.x & 63;
+  const int bh = row / p.R_real, r = row % p.R_real;
+  const int S_ex = p.S_ex, S_all = p.S_ex + p.S_all;
+  auto o_ptr = [&](int s) -> const float* {
+    return s < S_ex ? p.ex_o + ((static_cast<int64_t>(bh) * S_ex + s) * R + r) * kSD
+                    : p.ws_o + ((static_cast<int64_t>(bh) * p.S_all + (s - S_ex)) * R + r) * kSD;
+  };
+  float ms = -INFINITY, ls = 0.0f;
+  if (lane < S_all) {
+    ms = lane < S_ex ? p.ex_m[(static_cast<int64_t>(bh) * S_ex + lane) * R + r]
+                     : p.ws_m[(static_cast<int64_t>(bh) * p.S_all + (lane - S_ex)) * R + r];
+    ls = lane < S_ex ? p.ex_l[(static_cast<int64_t>(bh) * S_ex + lane) * R + r]
+                     : p.ws_l[(static_cast<int64_t>(bh) * p.S_all + (lane - S_ex)) * R + r];
+  }
+  float2 ov[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float* o = o_ptr(s < S_all ? s : S_all - 1);
+    ov[s] = float2{o[lane], o[lane + 64]};
+  }
+  const float M = wave_max(ms);
+  const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);   // 0 past S_all
+  const float Le = wave_sum(lane < S_ex ? w * ls : 0.0f);
+  const float Lc = wave_sum(lane >= S_ex ? w * ls : 0.0f);
+  float c0 = 0.0f, c1 = 0.0f, e0 = 0.0f, e1 = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s));
+    const bool ex = s < S_ex;
+    e0 = __builtin_fmaf(ex ? ws : 0.0f, ov[s].x, e0);
+    e1 = __builtin_fmaf(ex ? ws : 0.0f, ov[s].y, e1);
+    c0 = __builtin_fmaf(ex ? 0.0f : ws, ov[s].x, c0);
+    c1 = __builtin_fmaf(ex ? 0.0f : ws, ov[s].y, c1);
+  }
+  fwht128(c0, c1, lane);                                   // coded sum back to the channel basis: x R
+  c0 *= 0.08838834764831845f * p.signs[lane];
+  c1 *= 0.08838834764831845f * p.signs[lane + 64];
+  const int b = bh / p.Hkv, h = bh % p.Hkv;
+  const int hq = h * p.rep + r / p.Tq, tq = r % p.Tq;
+  const float L = Le + Lc;
+  const int64_t o0 = ((static_cast<int64_t>(b) * p.Tq + tq) * p.Hq + hq) * kSD + lane;
+  store_from_f32<DT>(p.out, o0, (c0 + Lc * f16_to_f32(p.mu_v[static_cast<int64_t>(bh) * kSD + lane]) + e0) / L);
+  store_from_f32<DT>(p.out, o0 + 64,
+                     (c1 + Lc * f16_to_f32(p.mu_v[static_cast<int64_t>(bh) * kSD + lane + 64]) + e1) / L);
+}
+
 inline int strata_pow2(int64_t r) {
   int R = 1;
   while (R < r) R <<= 1;
@@ -1198,7 +1254,36 @@ extern "C" int kvq_strata_decode(const void* q, int q_dtype, int64_t q_sb, int64
 #undef KVQ_STRATA_LAUNCH
     KVQ_LAUNCH_CHECK("kvq_strata_decode(tiers)");
   }
-  const dim3 mgrid(static_cast<unsigned>(p.BH) * p.R_real);
+  const int n_rows = p.BH * p.R_real;
+  const int S_merge = p.S_ex + p.S_all;
+  if (p.ex.n == 0 && S_merge >= 1 && S_merge <= 32) {            // one wavefront per row
+    const dim3 wgrid(static_cast<unsigned>((n_rows + 3) / 4));
+#define KVQ_SMW_N(R_, DT_, N_) hipLaunchKernelGGL((strata_merge_wave<R_, DT_, N_>), wgrid, dim3(kSThreads), 0, s, p, n_rows)
+#define KVQ_SMW_L(R_, DT_)                                        \
+    do {                                                          \
+      if (S_merge <= 8) KVQ_SMW_N(R_, DT_, 8);                    \
+      else if (S_merge <= 16) KVQ_SMW_N(R_, DT_, 16);             \
+      else KVQ_SMW_N(R_, DT_, 32);                                \
+    } while (0)
+#define KVQ_SMW_R(DT_)                                            \
+    switch (R) {                                                  \
+      case 1: KVQ_SMW_L(1, DT_); break;                           \
+      case 2: KVQ_SMW_L(2, DT_); break;                           \
+      case 4: KVQ_SMW_L(4, DT_); break;                           \
+      default: KVQ_SMW_L(8, DT_); break;                          \
+    }
+    switch (q_dtype) {
+      case KVQ_F32: KVQ_SMW_R(KVQ_F32) break;
+      case KVQ_F16: KVQ_SMW_R(KVQ_F16) break;
+      default: KVQ_SMW_R(KVQ_BF16) break;
+    }
+#undef KVQ_SMW_R
+#undef KVQ_SMW_L
+#undef KVQ_SMW_N
+    KVQ_LAUNCH_CHECK("kvq_strata_decode(merge)");
+    return KVQ_OK;
+  }
+  const dim3 mgrid(static_cast<unsigned>(n_rows));
 #define KVQ_STRATA_MERGE(R_, DT_) hipLaunchKernelGGL((strata_merge<R_, DT_>), mgrid, dim3(kSThreads), 0, s, p)
 #define KVQ_STRATA_MR(DT_)                                               \
   switch (R) {                                                           \

@@ -163,6 +163,27 @@ def test_strata_decode_single_width_no_exact_rows(bits):
     assert float(np.abs(out - ref).max()) <= 2e-3
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_strata_decode_long_window(dtype):
+    """A window of 1100 exact rows, past what the merge attends itself: exact-row blocks write
+    partials, and the one-wavefront-per-row merge (at most 32 partials, none attended in the merge)
+    combines them, unrotated, with the strata's rotated partials."""
+    import kvq
+    g = torch.Generator().manual_seed(61)
+    B, Hq, Hkv, T, W, d = 1, 8, 2, 2300, 1100, 128
+    K = (torch.randn((B, Hkv, T, d), generator=g) * 1.5 + 0.3).to(dtype)
+    V = torch.randn((B, Hkv, T, d), generator=g).to(dtype)
+    q = torch.randn((B, Hq, 1, d), generator=g).to(dtype)
+    assign = _assign(B, Hkv, T - W, (0.1, 0.3, 0.5), g)
+    cache = kvq.StrataCache.from_context(K.cuda(), V.cuda(), window=W, assign=assign)
+    assert cache.n_exact == W
+    print(f"strata long window: {dtype} T {T} W {W}", flush=True)
+    out = kvq.strata_decode(q.cuda(), d ** -0.5, cache).float().cpu().numpy()
+    ref = _oracle_out(cache, q, K, V, W, d ** -0.5)
+    err = float(np.abs(out - ref).max())
+    assert err <= (2e-3 if dtype == torch.float32 else 1e-2), err
+
+
 def test_strata_decode_many_query_tokens():
     """Tq 5 at rep 4 (20 rows per KV head): query-token pieces of 2, 2 and 1 tokens, each a full
     decode launch, against the oracle over the whole block of queries."""
