@@ -649,11 +649,10 @@ __global__ __launch_bounds__(kCThreads) void cov_rowprep(CovParams p) {
 // 16-token tiles.  WEIGHTED = false: drop totals (one partial per wavefront, combined in order by
 // cov_groups) and key-term masses; true: the weighted per-token sums.
 // LDS (16-bit keys and values, rep <= kTermsLdsRep): the chunk's 256 key and value rows (128 KiB)
-// and its v M v of every query head are staged in LDS once (the weighted pass also keeps its read
-// masses there until the end), and every group and wavefront reads its
-// tiles there (a tile used to come from L2 once per group and wavefront).  Row t of a tensor holds
-// its 16-byte column c at c ^ (t & 15), so the 16 tokens of a tile read in one instruction fall on
-// distinct banks.  The workgroup is two quads of wavefronts (two per SIMD, so one's products overlap
+// and its v M v of every query head are staged in LDS once, and every group and wavefront reads its
+// tiles there (a tile used to come from L2 once per group and wavefront); the weighted pass also
+// keeps its read masses there until the end.  Row t of a tensor holds its 16-byte column c at
+// c ^ (t & 15), so the 16 tokens of a tile read in one instruction fall on distinct banks.  The workgroup is two quads of wavefronts (two per SIMD, so one's products overlap
 // the other's terms): for the drop totals the quads take alternate groups with work; for the weighted
 // sums every group, quad q the tokens [c0 + 128 q, c0 + 128 q + 128), a lane's sums over the groups
 // kept in registers and added across the lane groups once at the end.  LDS = false: tiles and v M v
