@@ -90,7 +90,16 @@ struct CovParams {
   float* S;                              // (Hkv, d, d)
   float* S_part;                         // (kSSplit, Hkv, d, d): each row split's sum
   float* Mbar;                           // (Hkv, d, d)
+  // fp32 rows: the powers of two of qr, k and v (rows_scale_kernel, row_tiles.hpp); null otherwise
+  const float* xs;
 };
+
+// the power of two of fp32 view i (0: qr, 1: k, 2: v); 16-bit rows are exact operands: 1
+template <int DT>
+__device__ __forceinline__ float cov_xs(const CovParams& p, int i) {
+  if constexpr (DT == KVQ_F32) return p.xs[i];
+  else return 1.0f;
+}
 
 // the rows of head h as a buffer resource covering T token rows (reads past it return zero)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void* base, int64_t sh, int64_t st, int h, int T,
@@ -126,7 +135,7 @@ __device__ __forceinline__ int load_rows(const CovParams& p, int h, int row0, in
   if (pos >= 0) {
     const int64_t base = (static_cast<int64_t>(h) * p.NR + row) * kCD;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) load_op<DT>(p.qr, base + 32 * ks + 8 * g, qop[ks]);
+    for (int ks = 0; ks < 4; ++ks) load_op<DT>(p.qr, base + 32 * ks + 8 * g, qop[ks], cov_xs<DT>(p, 0));
   } else {
     zero_ops<DT>(qop);
   }
@@ -136,11 +145,11 @@ __device__ __forceinline__ int load_rows(const CovParams& p, int h, int row0, in
 // A operand (tokens) of the 16-token tile at t0: this lane's token t0 + n
 template <int DT>
 __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rs, int64_t st, int t0, int g, int n,
-                                          u32x4 (&op)[4][TileOps<DT>::NH]) {
+                                          u32x4 (&op)[4][TileOps<DT>::NH], float sc) {
   const int64_t tok = t0 + n;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
-    load_op_buf<DT>(rs, static_cast<int>((tok * st + 32 * ks + 8 * g) * TileOps<DT>::ESZ), op[ks]);
+    load_op_buf<DT>(rs, static_cast<int>((tok * st + 32 * ks + 8 * g) * TileOps<DT>::ESZ), op[ks], sc);
 }
 
 // Every key tile a wavefront loads feeds several of the item's 16-row blocks (16-bit data: all four,
@@ -181,6 +190,7 @@ __global__ __launch_bounds__(DT == KVQ_F32 ? kCThreads : 2 * kCThreads) void cov
   const int ntile = (mmax + 15) / 16;
   const int k0 = 16 * (ntile * ks / KS), k1 = min(mmax, 16 * (ntile * (ks + 1) / KS));
   const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, TileOps<DT>::ESZ);
+  const float qsc = p.qscale / (cov_xs<DT>(p, 0) * cov_xs<DT>(p, 1));   // logit scale of the scaled rows
   float m[NRB], ls[NRB];
 #pragma unroll
   for (int b = 0; b < NRB; ++b) {
@@ -190,8 +200,8 @@ __global__ __launch_bounds__(DT == KVQ_F32 ? kCThreads : 2 * kCThreads) void cov
   // three key tiles in rotation: two in flight behind the one computed (a tile past the split reads
   // zeros through the buffer resource or in-range keys, masked or never computed)
   u32x4 kt[3][4][NH];
-  load_tile<DT>(rk, p.k_st, k0, g, n, kt[0]);
-  load_tile<DT>(rk, p.k_st, k0 + 16, g, n, kt[1]);
+  load_tile<DT>(rk, p.k_st, k0, g, n, kt[0], cov_xs<DT>(p, 1));
+  load_tile<DT>(rk, p.k_st, k0 + 16, g, n, kt[1], cov_xs<DT>(p, 1));
   auto tile = [&](int t0, const u32x4 (&kop)[4][NH]) {
 #pragma unroll
     for (int b = 0; b < NRB; ++b) {
@@ -200,7 +210,7 @@ __global__ __launch_bounds__(DT == KVQ_F32 ? kCThreads : 2 * kCThreads) void cov
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = t0 + 4 * g + i;
-        sv[i] = (j <= pos[b] && j < mmax) ? d[i] * p.qscale : -INFINITY;
+        sv[i] = (j <= pos[b] && j < mmax) ? d[i] * qsc : -INFINITY;
         mt = fmaxf(mt, sv[i]);
       }
       if (mt > m[b]) {
@@ -214,13 +224,13 @@ __global__ __launch_bounds__(DT == KVQ_F32 ? kCThreads : 2 * kCThreads) void cov
     }
   };
   for (int t0 = k0; t0 < k1; t0 += 48) {
-    load_tile<DT>(rk, p.k_st, t0 + 32, g, n, kt[2]);
+    load_tile<DT>(rk, p.k_st, t0 + 32, g, n, kt[2], cov_xs<DT>(p, 1));
     tile(t0, kt[0]);
     if (t0 + 16 >= k1) break;
-    load_tile<DT>(rk, p.k_st, t0 + 48, g, n, kt[0]);
+    load_tile<DT>(rk, p.k_st, t0 + 48, g, n, kt[0], cov_xs<DT>(p, 1));
     tile(t0 + 16, kt[1]);
     if (t0 + 32 >= k1) break;
-    load_tile<DT>(rk, p.k_st, t0 + 64, g, n, kt[1]);
+    load_tile<DT>(rk, p.k_st, t0 + 64, g, n, kt[1], cov_xs<DT>(p, 1));
     tile(t0 + 32, kt[2]);
   }
   // lanes (0..3, n) hold disjoint keys of row n: this split's state of the row
@@ -295,6 +305,8 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
   const int k0 = 32 * (nstep * sp / kOSplit), k1 = min(mmax, 32 * (nstep * (sp + 1) / kOSplit));
   const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, ESZ);
   const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v, p.v_sh, p.v_st, h, p.T, ESZ);
+  const float qsc = p.qscale / (cov_xs<DT>(p, 0) * cov_xs<DT>(p, 1));   // logit scale of the scaled rows
+  const float vsc = cov_xs<DT>(p, 2);
   f32x4 acc[8];
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -315,7 +327,7 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
             rv, static_cast<int>((static_cast<int64_t>(t0 + key) * p.v_st) * ESZ + 16 * w16), 0, 0);
     }
 #pragma unroll
-    for (int tau = 0; tau < 2; ++tau) load_tile<DT>(rk, p.k_st, t0 + 16 * tau, g, n, kr[tau]);
+    for (int tau = 0; tau < 2; ++tau) load_tile<DT>(rk, p.k_st, t0 + 16 * tau, g, n, kr[tau], cov_xs<DT>(p, 1));
   };
   if (k0 < k1) load_step(k0);
   for (int t0 = k0; t0 < k1; t0 += 32) {
@@ -346,7 +358,7 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = t0 + 16 * tau + 4 * g + i;
-        pr[4 * tau + i] = (j <= pos && j < mmax) ? __builtin_amdgcn_exp2f(d[i] * p.qscale - rm) : 0.0f;
+        pr[4 * tau + i] = (j <= pos && j < mmax) ? __builtin_amdgcn_exp2f(d[i] * qsc - rm) : 0.0f;
       }
     }
     // A operand: row n, k-index 8g + kk <-> key kk < 4 ? 4g + kk : 16 + 4g + kk - 4 (hi and lo parts)
@@ -361,7 +373,7 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
           const int key = kk < 4 ? 4 * g + kk : 16 + 4 * g + kk - 4;
-          x[kk] = __uint_as_float(vt[key * VRW + c]);
+          x[kk] = __uint_as_float(vt[key * VRW + c]) * vsc;
         }
         u32x4 vh, vl;
         f32_parts<DT>(x, vh, vl);
@@ -389,7 +401,7 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
   for (int i = 0; i < 4; ++i) {
     const int row = row0 + 4 * g + i;
     if (row >= p.NR) continue;
-    const float il = p.row_il[static_cast<int64_t>(h) * p.NR + row];
+    const float il = p.row_il[static_cast<int64_t>(h) * p.NR + row] / vsc;   // exact: vsc a power of two
     float* dst = p.o_part + ((static_cast<int64_t>(sp) * p.Hkv + h) * p.NR + row) * kCD + n;
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) dst[16 * cb] = acc[cb][i] * il;
@@ -682,6 +694,7 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
   const int c1 = min(c0 + kChunkTok, p.re);
   const __amdgpu_buffer_rsrc_t rk = head_rsrc(p.k, p.k_sh, p.k_st, h, p.T, TileOps<DT>::ESZ);
   const __amdgpu_buffer_rsrc_t rv = head_rsrc(p.v, p.v_sh, p.v_st, h, p.T, TileOps<DT>::ESZ);
+  const float qsc = p.qscale / (cov_xs<DT>(p, 0) * cov_xs<DT>(p, 1));   // logit scale of the scaled rows
   if constexpr (WEIGHTED) {
     for (int u = threadIdx.x; u < kCWaves * kChunkTok; u += NT) {
       (&accA[0][0])[u] = 0.0f;
@@ -787,7 +800,7 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
           rm[i] = f.x;
           ril[i] = f.y;
           omo[i] = f.z;
-          msc[i] = f.w;
+          msc[i] = f.w / cov_xs<DT>(p, 2);                  // v M o of the scaled values: exact
         }
       } else {
         zero_ops<DT>(qop);
@@ -821,8 +834,8 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
           }
           vmv1 = (act && j < t_end) ? vmv_lds[r * kChunkTok + row] : 0.0f;
         } else {
-          load_tile<DT>(rk, p.k_st, t0, g, n, kop);
-          load_tile<DT>(rv, p.v_st, t0, g, n, vop);
+          load_tile<DT>(rk, p.k_st, t0, g, n, kop, cov_xs<DT>(p, 1));
+          load_tile<DT>(rv, p.v_st, t0, g, n, vop, cov_xs<DT>(p, 2));
           vmv1 = (act && j < t_end) ? p.vmv[vmv_base + j] : 0.0f;
         }
       };
@@ -833,7 +846,7 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const bool far = act && j < t_end && j <= pos[i] - local;
-          const float pr = far ? __builtin_amdgcn_exp2f(s[i] * p.qscale - rm[i]) * ril[i] : 0.0f;
+          const float pr = far ? __builtin_amdgcn_exp2f(s[i] * qsc - rm[i]) * ril[i] : 0.0f;
           const float u2 = far ? fmaxf(vmv - 2.0f * (ov[i] * msc[i]) + omo[i], 0.0f) : 0.0f;
           const float qd = pr / fmaxf(1.0f - pr, 1e-6f);
           td[i] = qd * qd * u2;
@@ -1160,12 +1173,14 @@ using namespace kvq;
 // workspace layout (floats): row_m, row_il, oMo, roww (Hkv NR each); o (Hkv NR d); o_part (kOSplit Hkv
 // NR d); vmv (Hkv rep n); ddpart (G Hkv n_chunks 4); alpha_part (Hkv n_chunks NR); gw (2 G + 1); red (4 +
 // Hkv rep + Hkv); WVa (Hkv rep n); A_part, DD_part (kTSplit Hkv n each); WVa_part (kTSplit Hkv rep n);
-// mop (Hkv NR 128), rowf (Hkv NR 4), 16-byte aligned; S_part (kSSplit Hkv d d); sums (Hkv (2 + rep))
+// mop (Hkv NR 128), rowf (Hkv NR 4), 16-byte aligned; S_part (kSSplit Hkv d d); sums (Hkv (2 + rep));
+// fp32 rows: partial maxima and scales (kAmaxFloats)
 extern "C" int64_t kvq_coverage_stats_workspace(int64_t Hkv, int64_t rep, int64_t n, int64_t NR, int64_t G) {
   if (Hkv <= 0 || rep <= 0 || n <= 0 || NR <= 0 || G <= 0) return -1;
   const int64_t nch = (n + kChunkTok - 1) / kChunkTok;
   return 4 * Hkv * NR + (1 + kOSplit) * Hkv * NR * kCD + Hkv * rep * n + G * Hkv * nch * kCWaves + Hkv * nch * NR + (2 * G + 1) +
-         (4 + Hkv * rep + Hkv) + Hkv * rep * n + kTSplit * (2 * Hkv * n + Hkv * rep * n) + 132 * Hkv * NR + 4 + kSSplit * Hkv * kCD * kCD + Hkv * (2 + rep);
+         (4 + Hkv * rep + Hkv) + Hkv * rep * n + kTSplit * (2 * Hkv * n + Hkv * rep * n) + 132 * Hkv * NR + 4 + kSSplit * Hkv * kCD * kCD + Hkv * (2 + rep) +
+         kAmaxFloats;
 }
 
 extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const int32_t* rowpos, const int32_t* rowgrp,
@@ -1222,10 +1237,21 @@ extern "C" int kvq_coverage_stats(const void* qr, int dtype, int64_t NR, const i
   p.mop = reinterpret_cast<uint32_t*>(w); w += 128 * Hkv * NR;
   p.rowf = w; w += 4 * Hkv * NR;
   p.S_part = w; w += kSSplit * Hkv * kCD * kCD;
-  p.sums = w;
+  p.sums = w; w += Hkv * (2 + rep);
+  float* amax_part = w;                                       // fp32 rows: partial maxima, then scales
+  p.xs = dtype == KVQ_F32 ? w + kAmaxViews * kAmaxBlocks : nullptr;
   p.A = A; p.W = W; p.DD = DD; p.S = S; p.Mbar = Mbar;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 blk(kCThreads);
+  if (dtype == KVQ_F32) {
+    // the powers of two that bring the query rows, keys and values into the fp16 parts' range
+    const RowView views[3] = {
+        RowView{static_cast<const float*>(qr), static_cast<int>(Hkv), static_cast<int>(NR), 1, NR * kCD, kCD, 0},
+        RowView{static_cast<const float*>(k), static_cast<int>(Hkv), static_cast<int>(T), 1, k_sh, k_st, 0},
+        RowView{static_cast<const float*>(v), static_cast<int>(Hkv), static_cast<int>(T), 1, v_sh, v_st, 0}};
+    launch_rows_scales(views, 3, amax_part, const_cast<float*>(p.xs), s);
+    KVQ_LAUNCH_CHECK("kvq_coverage_stats(fp32 scales)");
+  }
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((cov_rowstats<DT_>), dim3(xcd_grid(n_items * Hkv)),
                                                dim3(DT_ == KVQ_F32 ? kCThreads : 2 * kCThreads), 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_coverage_stats(rowstats)");

@@ -60,7 +60,16 @@ struct SnapParams {
   float* colsum;                        // (BH, n_rg, H - w)
   float* blockmax;                      // (BH, n_pool)
   float* out;                           // (BH, H)
+  // fp32 rows: the powers of two of the query rows and the keys (rows_scale_kernel, row_tiles.hpp)
+  const float* xs;
 };
+
+// the power of two of fp32 view i (0: query rows, 1: keys); 16-bit rows are exact operands: 1
+template <int DT>
+__device__ __forceinline__ float snap_xs(const SnapParams& p, int i) {
+  if constexpr (DT == KVQ_F32) return p.xs[i];
+  else return 1.0f;
+}
 
 // query operands of this wavefront's row blocks and the position of each lane's row (-1: no row)
 template <int DT>
@@ -77,7 +86,7 @@ __device__ __forceinline__ void load_queries(const SnapParams& p, int b, int h, 
       const int64_t base = static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq) * p.q_sh +
                            static_cast<int64_t>(i) * p.q_st;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) load_op<DT>(p.q, base + 32 * ks + 8 * g, qop[bw][ks]);
+      for (int ks = 0; ks < 4; ++ks) load_op<DT>(p.q, base + 32 * ks + 8 * g, qop[bw][ks], snap_xs<DT>(p, 0));
       rowpos[bw] = p.H - p.w + i;
     } else {
 #pragma unroll
@@ -103,7 +112,7 @@ __device__ __forceinline__ void load_keys(const __amdgpu_buffer_rsrc_t& rk, cons
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
     load_op_buf<DT>(rk, static_cast<int>((static_cast<int64_t>(kj) * p.k_st + 32 * ks + 8 * g) * SnapTraits<DT>::ESZ),
-                    kop[ks]);
+                    kop[ks], snap_xs<DT>(p, 1));
 }
 
 template <int DT>
@@ -126,6 +135,7 @@ __global__ __launch_bounds__(kSnapThreads) void snap_stats(SnapParams p) {
   }
   const __amdgpu_buffer_rsrc_t rk = key_rsrc(p, b, h, T::ESZ);
   const int k0 = s * p.split_keys, k1 = min(k0 + p.split_keys, p.H);
+  const float qsc = p.qscale / (snap_xs<DT>(p, 0) * snap_xs<DT>(p, 1));   // logit scale of the scaled rows
   auto stat_tile = [&](int t0, const u32x4 (&kop)[4][T::NH]) {
 #pragma unroll
     for (int bw = 0; bw < T::NBW; ++bw) {
@@ -135,7 +145,7 @@ __global__ __launch_bounds__(kSnapThreads) void snap_stats(SnapParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = t0 + 4 * g + i;
-        sv[i] = (j < k1 && j <= rowpos[bw]) ? acc[i] * p.qscale : -INFINITY;
+        sv[i] = (j < k1 && j <= rowpos[bw]) ? acc[i] * qsc : -INFINITY;
         mt = fmaxf(mt, sv[i]);
       }
       if (mt > m[bw]) {
@@ -222,6 +232,7 @@ __global__ __launch_bounds__(kSnapThreads) void snap_cols(SnapParams p) {
   const __amdgpu_buffer_rsrc_t rk = key_rsrc(p, b, h, T::ESZ);
   const int nc = p.H - p.w;                 // scored keys: every window row sees all of them
   const int c0 = c * kSnapChunk;
+  const float qsc = p.qscale / (snap_xs<DT>(p, 0) * snap_xs<DT>(p, 1));   // logit scale of the scaled rows
   auto col_tile = [&](int tt, const u32x4 (&kop)[4][T::NH]) {
     const int t0 = c0 + 16 * tt;
     float colv = 0.0f;
@@ -230,7 +241,7 @@ __global__ __launch_bounds__(kSnapThreads) void snap_cols(SnapParams p) {
       for (int bw = 0; bw < T::NBW; ++bw) {
         const f32x4 acc = tile_dots<DT, SnapTraits<DT>::NH, SnapTraits<DT>::NH>(qop[bw], kop);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) colv += __builtin_amdgcn_exp2f(acc[i] * p.qscale - rm[bw][i]) * ril[bw][i];
+        for (int i = 0; i < 4; ++i) colv += __builtin_amdgcn_exp2f(acc[i] * qsc - rm[bw][i]) * ril[bw][i];
       }
     }
     // the four lane groups hold disjoint rows of key t0 + n
@@ -325,8 +336,9 @@ SnapPlan snap_plan(int64_t BH, int64_t rows, int64_t w, int64_t H, int dtype) {
   return sp;
 }
 
-int64_t snap_ws(int64_t BH, int64_t rows, int64_t w, int64_t H, const SnapPlan& sp) {
-  return 2 * BH * sp.n_split * rows + 2 * BH * rows + BH * sp.n_rg * (H - w) + BH * sp.n_pool;
+int64_t snap_ws(int64_t BH, int64_t rows, int64_t w, int64_t H, const SnapPlan& sp, int dtype) {
+  return 2 * BH * sp.n_split * rows + 2 * BH * rows + BH * sp.n_rg * (H - w) + BH * sp.n_pool +
+         (dtype == KVQ_F32 ? kAmaxFloats : 0);
 }
 
 }  // namespace
@@ -339,7 +351,7 @@ extern "C" int64_t kvq_snapkv_scores_workspace(int64_t B, int64_t Hq, int64_t Hk
   if (B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || window <= 0 || H <= window || !valid_dtype(dtype)) return -1;
   const int64_t rows = (Hq / Hkv) * window;
   const SnapPlan sp = snap_plan(B * Hkv, rows, window, H, dtype);
-  return snap_ws(B * Hkv, rows, window, H, sp);
+  return snap_ws(B * Hkv, rows, window, H, sp, dtype);
 }
 
 extern "C" int kvq_snapkv_scores(const void* q, int dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k,
@@ -364,7 +376,7 @@ extern "C" int kvq_snapkv_scores(const void* q, int dtype, int64_t q_sb, int64_t
   KVQ_REQUIRE((H + 16) * k_st * esz < (1LL << 31), "kvq_snapkv_scores: one head's keys must span < 2 GiB");
   const int64_t BH = B * Hkv, rows = (Hq / Hkv) * window;
   const SnapPlan sp = snap_plan(BH, rows, window, H, dtype);
-  const int64_t need = snap_ws(BH, rows, window, H, sp);
+  const int64_t need = snap_ws(BH, rows, window, H, sp, dtype);
   KVQ_REQUIRE(workspace_floats >= need, "kvq_snapkv_scores: workspace too small (%lld < %lld floats)",
               (long long)workspace_floats, (long long)need);
   SnapParams p{};
@@ -382,10 +394,21 @@ extern "C" int kvq_snapkv_scores(const void* q, int dtype, int64_t q_sb, int64_t
   p.row_m = ws; ws += BH * rows;
   p.row_il = ws; ws += BH * rows;
   p.colsum = ws; ws += BH * sp.n_rg * (H - window);
-  p.blockmax = ws;
+  p.blockmax = ws; ws += BH * sp.n_pool;
   p.out = out;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 blk(kSnapThreads);
+  if (dtype == KVQ_F32) {
+    // the powers of two that bring the window's query rows and the keys into the fp16 parts' range
+    p.xs = ws + kAmaxViews * kAmaxBlocks;
+    const RowView views[2] = {
+        RowView{static_cast<const float*>(q), static_cast<int>(B), static_cast<int>(Hq), static_cast<int>(window),
+                q_sb, q_sh, q_st},
+        RowView{static_cast<const float*>(k), static_cast<int>(B), static_cast<int>(Hkv), static_cast<int>(H), k_sb,
+                k_sh, k_st}};
+    launch_rows_scales(views, 2, ws, const_cast<float*>(p.xs), s);
+    KVQ_LAUNCH_CHECK("kvq_snapkv_scores(fp32 scales)");
+  }
   KVQ_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((snap_stats<DT_>), dim3(BH * sp.n_rg * sp.n_split), blk, 0, s, p));
   KVQ_LAUNCH_CHECK("kvq_snapkv_scores(stats)");
   hipLaunchKernelGGL(snap_rows, dim3((BH * rows + kSnapThreads - 1) / kSnapThreads), blk, 0, s, p, BH * rows);

@@ -88,6 +88,18 @@ def test_coverage_stats_matches_oracle(case):
     _compare(st, _oracle(q, k, v, M, H, rs, re))
 
 
+@pytest.mark.parametrize("qs,ks,vs", [(2.0 ** -17, 2.0 ** 17, 2.0 ** 17), (2.0 ** 20, 2.0 ** -20, 2.0 ** -20)])
+def test_coverage_stats_fp32_extreme_magnitudes(qs, ks, vs):
+    """fp32 rows far outside fp16's range (keys and values up to ~6e5, past 65504) and far below it
+    (~4e-6): each tensor is brought into the fp16 parts' range by a power of two before the products
+    and the results scaled back, so the statistics match the oracle at the usual bar."""
+    q, k, v, M = _inputs(13, 8, 2, 640, 640, torch.float32)
+    q, k, v = q * qs, k * ks, v * vs
+    print(f"coverage fp32 magnitudes: |k| max {float(k.abs().max()):.3e}, |v| max {float(v.abs().max()):.3e}", flush=True)
+    st = _run(q, k, v, M, 640, 4, 608)
+    _compare(st, _oracle(q, k, v, M, 640, 4, 608))
+
+
 def test_coverage_window_only_and_deterministic():
     q, k, v, M = _inputs(11, 8, 2, 1200, 1200, torch.bfloat16)
     print("coverage window_only: Hq 8 Hkv 2 H 1200", flush=True)

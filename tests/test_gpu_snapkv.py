@@ -48,6 +48,23 @@ def test_snapkv_scores_match_oracle(B, Hq, Hkv, H, w, kern, dtype):
     np.testing.assert_allclose(got[..., H - w:], want[..., H - w:], rtol=1e-6)
 
 
+@pytest.mark.parametrize("qs,ks", [(2.0 ** -17, 2.0 ** 17), (2.0 ** 20, 2.0 ** -20)])
+def test_snapkv_scores_fp32_extreme_magnitudes(qs, ks):
+    """fp32 keys past fp16's range (~5e5) or far below it (~4e-6), queries scaled the other way so
+    the logits keep their size: the rows are brought into the fp16 parts' range by a power of two
+    per tensor and the logits scaled back, so the scores match the oracle as for ordinary rows."""
+    import kvq
+    B, Hq, Hkv, H, w, kern, d = 1, 8, 2, 700, 64, 5, 128
+    q, k = _case(B, Hq, Hkv, H, d, torch.float32, seed=77)
+    q, k = q * qs, k * ks
+    print(f"snapkv fp32 magnitudes: |k| max {float(k.abs().max()):.3e}", flush=True)
+    cfg = SimpleNamespace(SNAPKV_WINDOW=w, SNAPKV_KERNEL=kern)
+    got = kvq.snapkv_scores(q.cuda(), k.cuda(), H, d ** -0.5, cfg).cpu().numpy()
+    want = oracle_snapkv(q.double().numpy(), k.double().numpy(), H, d ** -0.5, w, kern)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got[..., :H - w], want[..., :H - w], rtol=1e-4, atol=1e-7 * want[..., :H - w].max())
+
+
 def test_snapkv_qrows_and_topk_selection():
     """Queries as the reference's QRows (only the kept positions), then the top-k of the scores as
     SnapKVMethod keeps them; against the oracle's sets modulo ties within 1e-4 of the k-th score."""
