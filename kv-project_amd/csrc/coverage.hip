@@ -848,7 +848,11 @@ __global__ __launch_bounds__(LDS ? 2 * kCThreads : kCThreads) void cov_terms(Cov
           const bool far = act && j < t_end && j <= pos[i] - local;
           const float pr = far ? __builtin_amdgcn_exp2f(s[i] * qsc - rm[i]) * ril[i] : 0.0f;
           const float u2 = far ? fmaxf(vmv - 2.0f * (ov[i] * msc[i]) + omo[i], 0.0f) : 0.0f;
-          const float qd = pr / fmaxf(1.0f - pr, 1e-6f);
+          // pr / b for b = max(1 - pr, 1e-6) in [1e-6, 1]: the reciprocal's quotient and one
+          // residual correction (no subnormal, infinite or zero operand can occur)
+          const float qb = fmaxf(1.0f - pr, 1e-6f), rb = __builtin_amdgcn_rcpf(qb);
+          const float q0 = pr * rb;
+          const float qd = __builtin_fmaf(__builtin_fmaf(-qb, q0, pr), rb, q0);
           td[i] = qd * qd * u2;
           ta[i] = pr * pr * u2;
           tw[i] = pr * pr;
