@@ -268,16 +268,21 @@ __global__ __launch_bounds__(DT == KVQ_F32 ? kCThreads : 2 * kCThreads) void cov
   }
 }
 
-// values of one 32-key step in LDS: [key][channel], rows padded by 8 bytes against bank conflicts
+// values of one 32-key step in LDS: [key][channel].  fp32 rows are padded by 8 bytes against bank
+// conflicts; 16-bit rows take 288 bytes (72 words), so that the transposed reads of a channel block
+// (16 lanes reading 8 bytes each of 4 keys x 4 channel quads) fall on distinct banks
 template <int DT>
-constexpr int vrow_words() { return (kCD * TileOps<DT>::ESZ + 8) / 4; }
+constexpr int vrow_words() { return DT == KVQ_F32 ? (kCD * 4 + 8) / 4 : 72; }
+
+typedef short tr16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) tr16x4 lds_tr16x4;
 
 template <int DT>
 __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
   constexpr int ESZ = TileOps<DT>::ESZ;
   constexpr int VRW = vrow_words<DT>();
   constexpr int U16 = kCD * ESZ / 16;                        // 16-byte units of a value row
-  __shared__ uint32_t vt[32 * VRW];
+  __shared__ __align__(16) uint32_t vt[32 * VRW];
   const int wave = threadIdx.x / 64, l = threadIdx.x % 64, g = l >> 4, n = l & 15;
   // work units (h, item, key split), h outermost; the items in reverse plan order, so the groups at
   // the end of the context, whose keys reach furthest, start first and the short ones fill the tail
@@ -338,10 +343,14 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
       const int u = threadIdx.x + kCThreads * k;
       if (u < 32 * U16) {
         uint32_t* dst = vt + (u / U16) * VRW + 4 * (u % U16);
-        dst[0] = vr[k][0];
-        dst[1] = vr[k][1];
-        dst[2] = vr[k][2];
-        dst[3] = vr[k][3];
+        if constexpr (DT == KVQ_F32) {
+          dst[0] = vr[k][0];
+          dst[1] = vr[k][1];
+          dst[2] = vr[k][2];
+          dst[3] = vr[k][3];
+        } else {
+          *reinterpret_cast<u32x4*>(dst) = vr[k];                // 288-byte rows: 16-byte aligned
+        }
       }
     }
     block_lds_barrier();
@@ -381,15 +390,16 @@ __global__ __launch_bounds__(kCThreads) void cov_output(CovParams p) {
         acc[cb] = tile_mfma<DT>(pl, vh, acc[cb]);
         acc[cb] = tile_mfma<DT>(ph, vl, acc[cb]);
       } else {
-        const uint16_t* v16 = reinterpret_cast<const uint16_t*>(vt);
-        uint32_t wv[4];
-#pragma unroll
-        for (int kk = 0; kk < 8; kk += 2) {
-          const int k0 = kk < 4 ? 4 * g + kk : 16 + 4 * g + kk - 4;
-          wv[kk / 2] = static_cast<uint32_t>(v16[k0 * 2 * VRW + c]) |
-                       (static_cast<uint32_t>(v16[(k0 + 1) * 2 * VRW + c]) << 16);
-        }
-        const u32x4 vb = u32x4{wv[0], wv[1], wv[2], wv[3]};
+        // LDS transpose reads (ds_read_b64_tr_b16): within each 16-lane group, lane n receives
+        // element n & 3 of the 8-byte loads of lanes (n >> 2) + 4 j, j = 0..3.  Lane (g, q + 4 j)
+        // therefore points at key 4g + j (then 16 + 4g + j), channels 16 cb + 4q .. + 3, and lane
+        // (g, n) receives keys 4g .. 4g + 3 (16 + 4g ..) of channel 16 cb + n: the B operand
+        const int src_key = 4 * g + (n >> 2), src_ch = 16 * cb + 4 * (n & 3);
+        const uint32_t* a0 = vt + src_key * VRW + src_ch / 2;
+        const tr16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_tr16x4*)(a0));
+        const tr16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_tr16x4*)(a0 + 16 * VRW));
+        const uint2 lw = __builtin_bit_cast(uint2, lo), hw = __builtin_bit_cast(uint2, hi);
+        const u32x4 vb = u32x4{lw.x, lw.y, hw.x, hw.y};
         acc[cb] = tile_mfma<DT>(ph, vb, acc[cb]);
         acc[cb] = tile_mfma<DT>(pl, vb, acc[cb]);
       }
