@@ -1077,7 +1077,7 @@ __global__ __launch_bounds__(kCThreads) void cov_smat(CovParams p) {
       for (int e = 0; e < 16 / ESZ; ++e) qs[k][(16 / ESZ) * w + e] = x[e] * p.scaling;
     }
     if (threadIdx.x < 64)
-      ws[threadIdx.x] = r0 + threadIdx.x < re ? p.roww[static_cast<int64_t>(h) * p.NR + r0 + threadIdx.x] : 0.0f;
+      ws[threadIdx.x] = r0 + static_cast<int>(threadIdx.x) < re ? p.roww[static_cast<int64_t>(h) * p.NR + r0 + threadIdx.x] : 0.0f;
     __syncthreads();
     for (int k = 0; k < 64; ++k) {
       const float a = ws[k] * qs[k][c1];

@@ -1187,7 +1187,7 @@ constexpr int kCUs = 256;          // MI355X compute units
 constexpr int64_t kBlockCost = 1024;
 
 inline SplitPlan plan_split(int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t n_q,
-                            int64_t n_exact, int64_t split_tokens, int group_k, int group_v) {
+                            int64_t n_exact, int64_t split_tokens, int /*group_k*/, int group_v) {
   SplitPlan sp;
   sp.R = pow2_rows((Hq / Hkv) * Tq);
   // blocks resident per CU = waves per SIMD of the variant (one wavefront of each block per SIMD)

@@ -131,7 +131,7 @@ __global__ void kivi_quant_values(const void* __restrict__ x, int H, int64_t sb,
   const int t = blockIdx.x * tok_per_block + threadIdx.x / slabs;
   const int s = threadIdx.x % slabs;
   const int lanes = width / 8;
-  const bool valid = t < n && threadIdx.x < tok_per_block * slabs;
+  const bool valid = t < n && static_cast<int>(threadIdx.x) < tok_per_block * slabs;
   const int qmax = (1 << bits) - 1;
   float v[8];
   float mn = INFINITY, mx = -INFINITY;
