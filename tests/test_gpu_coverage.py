@@ -70,7 +70,8 @@ def _compare(st, ref):
     assert [len(g) for g in st["groups"]] == [len(g) for g in ref["groups"]]
 
 
-@pytest.mark.parametrize("case", ["bf16_rep4", "f32_rep1_nan_tail", "f16_rep8_skip", "bf16_rep16"])
+@pytest.mark.parametrize("case", ["bf16_rep4", "f32_rep1_nan_tail", "f16_rep8_skip", "bf16_rep16", "bf16_rep1",
+                                  "f16_rep2_ragged"])
 def test_coverage_stats_matches_oracle(case):
     # 16-bit rows with up to 8 query heads per KV head take the LDS form of the token terms; fp32
     # rows and rep 16 the form that reads its tiles from memory
@@ -78,6 +79,10 @@ def test_coverage_stats_matches_oracle(case):
         Hq, Hkv, T, H, dt, rs, re, nan = 8, 2, 1200, 1200, torch.bfloat16, 4, 1168, False
     elif case == "bf16_rep16":
         Hq, Hkv, T, H, dt, rs, re, nan = 16, 1, 700, 700, torch.bfloat16, 4, 668, False
+    elif case == "bf16_rep1":
+        Hq, Hkv, T, H, dt, rs, re, nan = 3, 3, 900, 900, torch.bfloat16, 4, 868, False
+    elif case == "f16_rep2_ragged":      # coded range and context not multiples of 16 or 256
+        Hq, Hkv, T, H, dt, rs, re, nan = 4, 2, 1011, 1003, torch.float16, 7, 971, False
     elif case == "f32_rep1_nan_tail":
         Hq, Hkv, T, H, dt, rs, re, nan = 4, 4, 336, 300, torch.float32, 4, 268, True
     else:
