@@ -484,11 +484,12 @@ void dct_split(DctParams p) {
 //
 // Memory: per pair 6 loads of distinct bytes (key words of A and B, 1 KiB each; value words, two
 // 1 KiB loads; key and value scales of both blocks, 8 bytes per lane each, handed out through the
-// wavefront's LDS).  Two pairs are in flight behind the one computed; every load is unconditional
-// (exact compiler wait counts), and a prefetch past the wavefront's range goes through a resource
+// wavefront's LDS).  A step computes two pairs while the next two are in flight (deeper prefetch
+// measured slower); every load is unconditional (exact compiler wait counts), and a prefetch past the wavefront's range goes through a resource
 // of zero size, which returns zeros without touching memory.  No workgroup barrier before the
 // loop: the query operand and the DCT constants load straight into registers.
-constexpr int kPWaveLds = 424;     // dwords per wavefront: scales 256, w' 128, zero 4, alpha 16, m 16, pad
+// dwords per wavefront: scales 2 x 256, w' 2 x 128, zero 4, alpha 16, m 16, pad (two pairs a step)
+constexpr int kPWaveLds = 808;
 
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 
@@ -520,10 +521,12 @@ __device__ void dct_pair_block(const DctParams& p, int bh, int sidx, float* smem
   float* red_o = smem;
   float* red_ml = smem + kDWaves * R * kDD;
   uint32_t* wl = reinterpret_cast<uint32_t*>(red_ml + kDWaves * R * 2) + wave * kPWaveLds;
-  uint32_t* sc_l = wl;                 // [0, 128) key scales of A | B, [128, 256) value scales of A | B
-  uint32_t* wt = wl + 256;             // w' [16 columns][8 words], then 4 zero words
-  float* al = reinterpret_cast<float*>(wl + 388);       // 16 alphas
-  float* mlw = reinterpret_cast<float*>(wl + 404);      // 16 column maxima (epilogue)
+  // per pair of the step (+256 for the second): [0, 128) key scales of A | B, [128, 256) value scales
+  uint32_t* sc_l = wl;
+  uint32_t* wt = wl + 512;             // w' [16 columns][8 words] per pair (+128 for the second)
+  constexpr int kZero = 256;           // 4 zero words after both w' buffers (offset from wt)
+  float* al = reinterpret_cast<float*>(wl + 772);       // 16 alphas
+  float* mlw = reinterpret_cast<float*>(wl + 788);      // 16 column maxima (epilogue)
 
   // ---- this wavefront's pairs ----
   const int64_t np = (p.nb + 1) / 2;
@@ -596,10 +599,10 @@ __device__ void dct_pair_block(const DctParams& p, int bh, int sidx, float* smem
 #pragma unroll
   for (int k = 0; k < 4; ++k) cwl[k] = c4[(n * kDB + 32 * (k >> 1) + 16 * (k & 1) + 4 * g) / 4];  // C[n][..]
   __builtin_amdgcn_sched_barrier(0);
-  Pair buf[kDepth + 1];
+  Pair buf[kDepth + 2];
 #pragma unroll
   for (int j = 0; j < kDepth; ++j) load_pair(p0 + j, buf[j]);
-  if (l < 4) wt[128 + l] = 0u;
+  if (l < 4) wt[kZero + l] = 0u;
 
   const float qsc = rq < p.R_real ? p.qscale : 0.0f;
   uint32_t qh[4][4];
@@ -647,16 +650,11 @@ __device__ void dct_pair_block(const DctParams& p, int bh, int sidx, float* smem
   for (int k = 0; k < 8; ++k) acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.0f;
   float m_run = -INFINITY, la = 0.0f;              // column n
 
-  auto step = [&](const Pair& c, bool hasB) {
-    // ---- scales through the wavefront's LDS ----
-    *reinterpret_cast<uint2*>(sc_l + 2 * l) = c.ks;
-    *reinterpret_cast<uint2*>(sc_l + 128 + 2 * l) = c.vs;
-    wave_lds_fence();
-    u32x4 sk[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sk[i] = *reinterpret_cast<const u32x4*>(sc_l + (colB ? 64 : 0) + 16 * g + 4 * i);
-    const u32x4 sv4 = *reinterpret_cast<const u32x4*>(sc_l + 128 + (rowB ? 64 : 0) + 4 * n);
-    // ---- key stage ----
+  // Two pairs per step: their key, logit, coefficient and value stages are independent chains the
+  // scheduler interleaves (one wavefront per SIMD has no other wavefront to hide a chain behind),
+  // and one softmax update and one LDS hand-off of each kind serve both.  Pair 1 of a step may be
+  // dead (past the wavefront's range): its loads read zeros and its logits are masked.
+  auto key_stage = [&](const Pair& c, const u32x4 (&sk)[4], uint32_t& ub0, uint32_t& ub1) {
     u32x4 qt[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -671,28 +669,60 @@ __device__ void dct_pair_block(const DctParams& p, int bh, int sidx, float* smem
       db = mfma(unpack(c.kb[i]), as_half8(qt[i]), db);
     }
     const f32x4 du = (colB ? db : da) + dc;
-    const uint32_t ub0 = pack_h2(static_cast<_Float16>(du[0] * kTwo20), static_cast<_Float16>(du[1] * kTwo20));
-    const uint32_t ub1 = pack_h2(static_cast<_Float16>(du[2] * kTwo20), static_cast<_Float16>(du[3] * kTwo20));
-    // ---- logits: token 16t + 4g + i of column n ----
-    float s[4][4];
+    ub0 = pack_h2(static_cast<_Float16>(du[0] * kTwo20), static_cast<_Float16>(du[1] * kTwo20));
+    ub1 = pack_h2(static_cast<_Float16>(du[2] * kTwo20), static_cast<_Float16>(du[3] * kTwo20));
+  };
+  // logits: token 16t + 4g + i of column n
+  auto logit_stage = [&](uint32_t ub0, uint32_t ub1, bool dead, float (&s)[4][4]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const f32x4 e = mfma16(cl[t][0], cl[t][1], ub0, ub1, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[t][i] = e[i];
+      for (int i = 0; i < 4; ++i) s[t][i] = dead ? -INFINITY : e[i];
     }
-    if (!hasB && colB) {
+  };
+  // coefficient stage: w'[coefficient 4g + i] of column n
+  auto coef_stage = [&](const float (&pr)[4][4]) -> f32x4 {
+    f32x4 dw = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[t][i] = -INFINITY;
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x4 pb = u32x4{pack_h2(static_cast<_Float16>(pr[2 * ks][0]), static_cast<_Float16>(pr[2 * ks][1])),
+                             pack_h2(static_cast<_Float16>(pr[2 * ks][2]), static_cast<_Float16>(pr[2 * ks][3])),
+                             pack_h2(static_cast<_Float16>(pr[2 * ks + 1][0]), static_cast<_Float16>(pr[2 * ks + 1][1])),
+                             pack_h2(static_cast<_Float16>(pr[2 * ks + 1][2]), static_cast<_Float16>(pr[2 * ks + 1][3]))};
+      dw = mfma(as_half8(u32x4{cw[ks][0], cw[ks][1], cw[ks][2], cw[ks][3]}), as_half8(pb), dw);
     }
-    // ---- online softmax, lazy maximum ----
-    float lm = s[0][0];
+    return dw;
+  };
+
+  auto step2 = [&](const Pair& c0, const Pair& c1, bool hasB0, bool live1, bool hasB1) {
+    // ---- scales of both pairs through the wavefront's LDS ----
+    *reinterpret_cast<uint2*>(sc_l + 2 * l) = c0.ks;
+    *reinterpret_cast<uint2*>(sc_l + 128 + 2 * l) = c0.vs;
+    *reinterpret_cast<uint2*>(sc_l + 256 + 2 * l) = c1.ks;
+    *reinterpret_cast<uint2*>(sc_l + 384 + 2 * l) = c1.vs;
+    wave_lds_fence();
+    u32x4 sk0[4], sk1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sk0[i] = *reinterpret_cast<const u32x4*>(sc_l + (colB ? 64 : 0) + 16 * g + 4 * i);
+      sk1[i] = *reinterpret_cast<const u32x4*>(sc_l + 256 + (colB ? 64 : 0) + 16 * g + 4 * i);
+    }
+    const u32x4 sv0 = *reinterpret_cast<const u32x4*>(sc_l + 128 + (rowB ? 64 : 0) + 4 * n);
+    const u32x4 sv1 = *reinterpret_cast<const u32x4*>(sc_l + 384 + (rowB ? 64 : 0) + 4 * n);
+    // ---- key and logit stages ----
+    uint32_t u00, u01, u10, u11;
+    key_stage(c0, sk0, u00, u01);
+    key_stage(c1, sk1, u10, u11);
+    float s0[4][4], s1[4][4];
+    logit_stage(u00, u01, !hasB0 && colB, s0);
+    logit_stage(u10, u11, !live1 || (!hasB1 && colB), s1);
+    // ---- online softmax over both pairs, lazy maximum ----
+    float lm = s0[0][0];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lm = fmaxf(lm, s[t][i]);
+      for (int i = 0; i < 4; ++i) lm = fmaxf(lm, fmaxf(s0[t][i], s1[t][i]));
     if (__any(lm > m_run + kLazy)) {
       const float m_new = fmaxf(m_run, xmax32(xmax16(lm)));
       const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -710,48 +740,60 @@ __device__ void dct_pair_block(const DctParams& p, int bh, int sidx, float* smem
       }
     }
     const float mo = (m_run == -INFINITY ? 0.0f : m_run) - kPOff;
-    float pr[4][4];
+    float pr0[4][4], pr1[4][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        pr[t][i] = __builtin_amdgcn_exp2f(s[t][i] - mo);
-        la += pr[t][i];
+        pr0[t][i] = __builtin_amdgcn_exp2f(s0[t][i] - mo);
+        pr1[t][i] = __builtin_amdgcn_exp2f(s1[t][i] - mo);
       }
-    // ---- coefficient stage: w'[coefficient 4g + i] of column n ----
-    f32x4 dw = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const u32x4 pb = u32x4{pack_h2(static_cast<_Float16>(pr[2 * ks][0]), static_cast<_Float16>(pr[2 * ks][1])),
-                             pack_h2(static_cast<_Float16>(pr[2 * ks][2]), static_cast<_Float16>(pr[2 * ks][3])),
-                             pack_h2(static_cast<_Float16>(pr[2 * ks + 1][0]), static_cast<_Float16>(pr[2 * ks + 1][1])),
-                             pack_h2(static_cast<_Float16>(pr[2 * ks + 1][2]), static_cast<_Float16>(pr[2 * ks + 1][3]))};
-      dw = mfma(as_half8(u32x4{cw[ks][0], cw[ks][1], cw[ks][2], cw[ks][3]}), as_half8(pb), dw);
-    }
-    // ---- w' transposed through LDS into the block-diagonal A operand of the value stage ----
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) la += pr0[t][i];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) la += pr1[t][i];
+    const f32x4 dw0 = coef_stage(pr0), dw1 = coef_stage(pr1);
+    // ---- w' of both pairs transposed through LDS into the block-diagonal A operands ----
     *reinterpret_cast<uint2*>(wt + n * 8 + 2 * g) =
-        make_uint2(pack_h2(static_cast<_Float16>(dw[0]), static_cast<_Float16>(dw[1])),
-                   pack_h2(static_cast<_Float16>(dw[2]), static_cast<_Float16>(dw[3])));
+        make_uint2(pack_h2(static_cast<_Float16>(dw0[0]), static_cast<_Float16>(dw0[1])),
+                   pack_h2(static_cast<_Float16>(dw0[2]), static_cast<_Float16>(dw0[3])));
+    *reinterpret_cast<uint2*>(wt + 128 + n * 8 + 2 * g) =
+        make_uint2(pack_h2(static_cast<_Float16>(dw1[0]), static_cast<_Float16>(dw1[1])),
+                   pack_h2(static_cast<_Float16>(dw1[2]), static_cast<_Float16>(dw1[3])));
     wave_lds_fence();
-    const u32x4 aw = *reinterpret_cast<const u32x4*>(wt + (colB == rowB ? n * 8 + 4 * (g & 1) : 128));
-    const f32x4 dv = mfma(as_half8(aw), as_half8(k7), f32x4{0.f, 0.f, 0.f, 0.f});
+    const bool diag = colB == rowB;
+    const u32x4 aw0 = *reinterpret_cast<const u32x4*>(wt + (diag ? n * 8 + 4 * (g & 1) : kZero));
+    const u32x4 aw1 = *reinterpret_cast<const u32x4*>(wt + (diag ? 128 + n * 8 + 4 * (g & 1) : kZero));
+    // ---- value stage ----
+    const f32x4 dv0 = mfma(as_half8(aw0), as_half8(k7), f32x4{0.f, 0.f, 0.f, 0.f});
+    const f32x4 dv1 = mfma(as_half8(aw1), as_half8(k7), f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
-      const f32x4 d5 = mfma(as_half8(aw), unpack(c.vw[blk >> 2][blk & 3]), dv);
-      const float sv = h2f(sv4[blk >> 1], blk & 1);
+      const f32x4 d0 = mfma(as_half8(aw0), unpack(c0.vw[blk >> 2][blk & 3]), dv0);
+      const f32x4 d1 = mfma(as_half8(aw1), unpack(c1.vw[blk >> 2][blk & 3]), dv1);
+      const float v0 = h2f(sv0[blk >> 1], blk & 1), v1 = h2f(sv1[blk >> 1], blk & 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[blk][i] = __builtin_fmaf(sv, d5[i], acc[blk][i]);
+      for (int i = 0; i < 4; ++i) acc[blk][i] = __builtin_fmaf(v1, d1[i], __builtin_fmaf(v0, d0[i], acc[blk][i]));
     }
   };
 
   {
     const int last_full = (p.nb & 1) ? p_last : static_cast<int>(np);   // pairs below it have a block B
-    // kDepth pairs in flight behind the one being computed; loads unconditional, steps guarded
-    for (int pi = p0; pi < p1; pi += kDepth + 1) {
+    // kDepth pairs in flight behind the two being computed; loads unconditional (a pair past the
+    // range reads zeros and no memory), steps guarded
+    constexpr int NBUF = kDepth + 2;
+    static_assert(kDepth % 2 == 0, "pairs go two a step");
+    for (int pi = p0; pi < p1; pi += NBUF) {
 #pragma unroll
-      for (int j = 0; j <= kDepth; ++j) {
-        load_pair(pi + j + kDepth, buf[(j + kDepth) % (kDepth + 1)]);
-        if (j == 0 || pi + j < p1) step(buf[j], pi + j < last_full);
+      for (int j = 0; j < NBUF / 2; ++j) {
+        const int q = pi + 2 * j;
+        load_pair(q + kDepth, buf[(2 * j + kDepth) % NBUF]);
+        load_pair(q + kDepth + 1, buf[(2 * j + kDepth + 1) % NBUF]);
+        if (j == 0 || q < p1) step2(buf[2 * j], buf[2 * j + 1], q < last_full, q + 1 < p1, q + 1 < last_full);
       }
     }
   }
@@ -824,7 +866,7 @@ __device__ void dct_pair_block(const DctParams& p, int bh, int sidx, float* smem
 
 // one workgroup per CU (one wavefront per SIMD) with kPairDepth pairs in flight per wavefront: a
 // wavefront's prologue and epilogue are paid over more pairs, and the registers a single
-// wavefront may hold carry the deep prefetch
+// wavefront may hold carry the prefetch and the two pairs of a step
 constexpr int kPairDepth = 2;
 
 template <int DT>
