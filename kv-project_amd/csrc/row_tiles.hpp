@@ -90,7 +90,10 @@ __device__ __forceinline__ void load_op_buf(__amdgpu_buffer_rsrc_t rs, int byte_
 // fp32 rows enter the products as fp16 hi + lo parts, whose range ends at 65504 (and whose lo part
 // turns subnormal for values below about 2^-2), so each fp32 tensor is first multiplied by a power of
 // two (exact) that brings its largest finite |x| to [2^12, 2^13); the products are scaled back by the
-// inverse powers.  A view of rows of 128 floats: row (i0, i1, i2) at base + i0 s0 + i1 s1 + i2 s2.
+// inverse powers.  The power is at most 2^63, so that the product of two of them stays finite: a
+// tensor whose largest |x| is below 2^-50 comes out smaller than 2^13 (full precision down to a
+// largest |x| of about 2^-66; below that its products lose relative precision, and they are zero
+// below about 2^-87, never NaN).  A view of rows of 128 floats: row (i0, i1, i2) at base + i0 s0 + i1 s1 + i2 s2.
 struct RowView {
   const float* base;
   int n0, n1, n2;
@@ -124,8 +127,8 @@ __global__ __launch_bounds__(256) void rows_absmax_kernel(RowView v0, RowView v1
   if (threadIdx.x == 0) part[blockIdx.y * gridDim.x + blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// one wavefront per view: scale[v] = 2^(13 - e) for a largest |x| of f 2^e (f in [0.5, 1)), 1 when
-// the view is all zeros
+// one wavefront per view: scale[v] = 2^min(13 - e, 63) for a largest |x| of f 2^e (f in [0.5, 1)),
+// 1 when the view is all zeros
 __global__ __launch_bounds__(64 * kAmaxViews) void rows_scale_kernel(const float* part, int n_part, float* scale) {
   const int vi = threadIdx.x / 64, lane = threadIdx.x % 64;
   float m = 0.0f;
@@ -134,7 +137,7 @@ __global__ __launch_bounds__(64 * kAmaxViews) void rows_scale_kernel(const float
   if (lane == 0) {
     int e = 0;
     if (m > 0.0f) (void)frexpf(m, &e);
-    scale[vi] = m > 0.0f ? ldexpf(1.0f, 13 - e) : 1.0f;
+    scale[vi] = m > 0.0f ? ldexpf(1.0f, min(13 - e, 63)) : 1.0f;
   }
 }
 

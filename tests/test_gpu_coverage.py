@@ -53,7 +53,8 @@ def _check(got, ref, name, rel):
     err = float(np.abs(g - r).max())
     print(f"  {name}: max-abs-err {err:.3e} (scale {scale:.3e})", flush=True)
     assert np.isfinite(g).all(), name
-    assert err <= rel * scale, (name, err, scale)
+    # plus fp32's smallest normal: statistics whose true size is below it are zero in any fp32 sum
+    assert err <= rel * scale + np.finfo(np.float32).tiny, (name, err, scale)
 
 
 def _run(q, k, v, M, H, rs, re, window_only=False):
@@ -93,11 +94,14 @@ def test_coverage_stats_matches_oracle(case):
     _compare(st, _oracle(q, k, v, M, H, rs, re))
 
 
-@pytest.mark.parametrize("qs,ks,vs", [(2.0 ** -17, 2.0 ** 17, 2.0 ** 17), (2.0 ** 20, 2.0 ** -20, 2.0 ** -20)])
+@pytest.mark.parametrize("qs,ks,vs", [(2.0 ** -17, 2.0 ** 17, 2.0 ** 17), (2.0 ** 20, 2.0 ** -20, 2.0 ** -20),
+                                      (2.0 ** -122, 1.0, 1.0)])
 def test_coverage_stats_fp32_extreme_magnitudes(qs, ks, vs):
     """fp32 rows far outside fp16's range (keys and values up to ~6e5, past 65504) and far below it
     (~4e-6): each tensor is brought into the fp16 parts' range by a power of two before the products
-    and the results scaled back, so the statistics match the oracle at the usual bar."""
+    and the results scaled back, so the statistics match the oracle at the usual bar.  Queries near
+    fp32's smallest normal (~2^-120, logits ~0): the power stays finite (at most 2^63), so the
+    statistics are those of uniform attention, as the oracle's, not NaN."""
     q, k, v, M = _inputs(13, 8, 2, 640, 640, torch.float32)
     q, k, v = q * qs, k * ks, v * vs
     print(f"coverage fp32 magnitudes: |k| max {float(k.abs().max()):.3e}, |v| max {float(v.abs().max()):.3e}", flush=True)

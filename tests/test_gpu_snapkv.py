@@ -48,11 +48,13 @@ def test_snapkv_scores_match_oracle(B, Hq, Hkv, H, w, kern, dtype):
     np.testing.assert_allclose(got[..., H - w:], want[..., H - w:], rtol=1e-6)
 
 
-@pytest.mark.parametrize("qs,ks", [(2.0 ** -17, 2.0 ** 17), (2.0 ** 20, 2.0 ** -20)])
+@pytest.mark.parametrize("qs,ks", [(2.0 ** -17, 2.0 ** 17), (2.0 ** 20, 2.0 ** -20), (2.0 ** -122, 1.0)])
 def test_snapkv_scores_fp32_extreme_magnitudes(qs, ks):
     """fp32 keys past fp16's range (~5e5) or far below it (~4e-6), queries scaled the other way so
     the logits keep their size: the rows are brought into the fp16 parts' range by a power of two
-    per tensor and the logits scaled back, so the scores match the oracle as for ordinary rows."""
+    per tensor and the logits scaled back, so the scores match the oracle as for ordinary rows.
+    Queries near fp32's smallest normal (~2^-120): the power stays finite (at most 2^63) and the
+    scores are those of uniform attention, as the oracle's, not NaN."""
     import kvq
     B, Hq, Hkv, H, w, kern, d = 1, 8, 2, 700, 64, 5, 128
     q, k = _case(B, Hq, Hkv, H, d, torch.float32, seed=77)
