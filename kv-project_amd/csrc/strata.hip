@@ -535,7 +535,8 @@ constexpr int kMaxTiers = 16;
 // One stratum of the launch: its codes, scales and split range [s_base, s_base + n_split).
 // Dispatch-class weights of the strata's splits (see class_block_of): the mixed-width decode's
 // (measured at the C3 shape: 29.6 us per step, against 30.0 with the KIVI decode's 141 : 98 : 68,
-// 30.0 without classes and 30.2 with 125 : 100 : 80)
+// 30.0 without classes and 30.2 with 125 : 100 : 80; steeper weights, 180 : 92 : 50 and
+// 200 : 85 : 42, 0.6 and 1.2 us slower)
 #ifndef KVQ_STRATA_CLASS_W
 #define KVQ_STRATA_CLASS_W 165, 95, 55
 #endif
