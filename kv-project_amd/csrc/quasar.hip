@@ -551,8 +551,10 @@ extern "C" int kvq_quasar_plan(const int32_t* k_table, int k_steps, const int32_
     return KVQ_OK;
   }
   // cost of chunk c: coefficients the chunk's tokens own over both sides (FMAs per query row)
-  // plus a fixed per-chunk part (softmax, row loads)
-  std::vector<double> cost(static_cast<size_t>(n_chunks), 64.0 * 16.0);
+  // plus a fixed per-chunk part (softmax, the row staging and its waits), measured best at 96
+  // coefficients per token (6144 per chunk; 2048 / 3072 / 4096 / 8192: 74.2 / 65.7 / 64.7 / 68.3 us
+  // of the split at the F2 workload against 64.5)
+  std::vector<double> cost(static_cast<size_t>(n_chunks), 6144.0);
   auto add = [&](const int32_t* tab, int steps) {
     for (int s = 0; s < steps; ++s) {
       const int64_t ns = tab[7 * s + 1], w = tab[7 * s + 4];
@@ -562,22 +564,50 @@ extern "C" int kvq_quasar_plan(const int32_t* k_table, int k_steps, const int32_
   };
   add(k_table, k_steps);
   add(v_table, v_steps);
-  double total = 0.0;
-  for (double c : cost) total += c;
-  // one resident round of workgroups over the heads (3 per CU), each split at least 4 chunks
-  int64_t S = std::max<int64_t>(1, std::min<int64_t>({static_cast<int64_t>(max_splits), (768 + Hkv - 1) / Hkv,
-                                                       (n_chunks + 3) / 4}));
-  int64_t s = 0;
-  double run = 0.0;
-  bounds[0] = 0;
-  for (int64_t c = 0; c < n_chunks && s + 1 < S; ++c) {
-    run += cost[static_cast<size_t>(c)];
-    if (run >= total * static_cast<double>(s + 1) / static_cast<double>(S)) bounds[++s] = static_cast<int32_t>(c + 1);
+  double total = 0.0, c_max = 0.0;
+  for (double c : cost) {
+    total += c;
+    c_max = std::max(c_max, c);
   }
-  bounds[++s] = static_cast<int32_t>(n_chunks);
-  for (int64_t i = 1; i <= s; ++i)
-    if (bounds[i] < bounds[i - 1]) bounds[i] = bounds[i - 1];
-  *n_splits = static_cast<int32_t>(s);
+  // one resident round of workgroups over the heads (3 per CU), splits of 4 chunks on average at least
+  const int64_t S = std::max<int64_t>(1, std::min<int64_t>({static_cast<int64_t>(max_splits), (768 + Hkv - 1) / Hkv,
+                                                             (n_chunks + 3) / 4}));
+  // The wavefronts of a split claim its chunks in order, each taking the next when it is free, so a
+  // split's time is the makespan of that list schedule, and one full early chunk costs several
+  // times a split's average share per wavefront: splits of equal cost would hand some wavefronts
+  // two heavy chunks.  Contiguous splits are cut greedily under a makespan bound B (a split closes
+  // before the chunk that would push its schedule past B), and B is the least bound (bisection)
+  // that needs at most S splits.
+  auto cut = [&](double B, int32_t* out) -> int64_t {
+    int64_t ns = 0;
+    int64_t c = 0;
+    if (out != nullptr) out[0] = 0;
+    while (c < n_chunks) {
+      double fin[kQWaves] = {};
+      double span = 0.0;
+      int64_t e = c;
+      for (; e < n_chunks; ++e) {
+        int w = 0;
+        for (int i = 1; i < kQWaves; ++i)
+          if (fin[i] < fin[w]) w = i;
+        const double f = fin[w] + cost[static_cast<size_t>(e)];
+        if (e > c && std::max(span, f) > B) break;
+        fin[w] = f;
+        span = std::max(span, f);
+      }
+      ++ns;
+      c = e;
+      if (out != nullptr) out[ns] = static_cast<int32_t>(c);
+    }
+    return ns;
+  };
+  double lo = c_max, hi = total;
+  for (int it = 0; it < 60 && hi - lo > 1e-6 * total; ++it) {
+    const double mid = 0.5 * (lo + hi);
+    if (cut(mid, nullptr) <= S) hi = mid;
+    else lo = mid;
+  }
+  *n_splits = static_cast<int32_t>(cut(hi, bounds));
   return KVQ_OK;
 }
 
