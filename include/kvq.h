@@ -484,8 +484,10 @@ int kvq_kivi_export(const uint8_t* kc, const uint16_t* k_lo, const uint16_t* k_s
  *   query's coefficients), 2 (the split launch), 4 (the row merge, where up to 128 exact rows are
  *   attended); 7 for a decode step (the others are timing hooks that reuse the workspace of an
  *   earlier call).
- * kvq_quasar_plan: host-memory step tables in (checked); out, in host memory: cost-balanced chunk
- * boundaries (bounds needs max_splits + 1 entries; *n_splits receives the split count) and the
+ * kvq_quasar_plan: host-memory step tables in (checked); out, in host memory: chunk boundaries of
+ * the splits, cut so that the longest split (its wavefronts claiming its chunks in order, chunk
+ * costs from the coefficients the tokens own) is shortest within one resident round of workgroups
+ * (bounds needs max_splits + 1 entries; *n_splits receives the split count) and the
  * slot table (2 x 32 x 8 int32: per 4-byte slot of a token's rows, the step offset + 4 dw, n_s, nb,
  * first coefficient, bits, level offset, step) with n_slots[2].  No reference counterpart (the
  * reference launches one program per 64-token block).

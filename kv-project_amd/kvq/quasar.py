@@ -186,7 +186,7 @@ class QuasarState:
         self._ws = None
 
     def _plan(self, Hkv: int):
-        """Cost-balanced token splits and the slot table (kvq_quasar_plan, host memory), uploaded."""
+        """Makespan-balanced token splits and the slot table (kvq_quasar_plan, host memory), uploaded."""
         kt, vt = self.sides[0]["table_np"], self.sides[1]["table_np"]
         bounds = np.zeros(MAX_SPLITS + 1, dtype=np.int32)
         slots = np.zeros((2, 32, 8), dtype=np.int32)
