@@ -15,7 +15,7 @@
 // with qt = q T_K; the value coefficients are lifted once per query row: o += acc T_V^T + P mu_V.
 //
 // Launches: quasar_prologue (qt and q . mu_K, log2 units), quasar_split (coded workgroups over
-// cost-balanced token ranges, each lifting its coefficient sums by T_V into an output partial, then
+// makespan-balanced token ranges, each lifting its coefficient sums by T_V into an output partial, then
 // exact-row workgroups when the exact part is long), merge_rows_kernel (the shared row merge; a short
 // exact part is attended there).
 #include <algorithm>
