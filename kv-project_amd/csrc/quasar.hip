@@ -28,6 +28,7 @@
 namespace kvq {
 namespace {
 
+constexpr int kQD = 128;                  // head_dim (the decode entry point requires it)
 constexpr int kQChunk = 64;               // coded tokens per wavefront iteration (lane = token)
 constexpr int kQWaves = 4;
 constexpr int kQThreads = 256;
@@ -95,10 +96,15 @@ __global__ __launch_bounds__(256) void quasar_prologue(const void* __restrict__ 
   if ((tid & 63) == 0) red[tid >> 6] = pm;
   __syncthreads();
   if (tid < Rk) {
+    // the column's d = 128 values loaded at once (one memory round trip), then the dot product in
+    // channel order
     const float* col = Tk + static_cast<int64_t>(h) * d * Rk + tid;
+    float cv[kQD];
+#pragma unroll
+    for (int c = 0; c < kQD; ++c) cv[c] = col[static_cast<int64_t>(c) * Rk];
     float acc = 0.0f;
-#pragma unroll 16
-    for (int c = 0; c < d; ++c) acc = __builtin_fmaf(qs[c], col[static_cast<int64_t>(c) * Rk], acc);
+#pragma unroll
+    for (int c = 0; c < kQD; ++c) acc = __builtin_fmaf(qs[c], cv[c], acc);
     qt[(static_cast<int64_t>(h) * Rk + tid) * R + r] = acc * qscale;
   }
   if (tid == 0) qmu[static_cast<int64_t>(h) * R + r] = ((red[0] + red[1]) + (red[2] + red[3])) * qscale;
