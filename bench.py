@@ -1358,8 +1358,8 @@ def main() -> int:
                     help="only run a plain 1 GiB device-to-device copy (profiler counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this path is single-GPU by design (multi-GPU sharding is "
-              "described in DESIGN.md, not launched); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this path is single-GPU by design (sharding over (batch, KV "
+              "head) is a design, not launched); run with --gpus 1", file=sys.stderr)
         return 2
     import torch
     torch.cuda.set_device(0)

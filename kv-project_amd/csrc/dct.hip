@@ -1,6 +1,6 @@
 // Blockwise token-axis DCT coding of K/V (A9) and the decode over it.
 //
-// The reference has no DCT; the contract follows its conventions: per (KV head,
+// The reference has no DCT; this contract follows the reference's own conventions: per (KV head,
 // channel, 64-token block) an orthonormal DCT-II along tokens, coefficients 0..15 kept, each
 // (block, channel) quantised with symmetric absmax at 4 bits (absmax_quant, STRATA_KV.py:549-554:
 // s = max(fp16(max|X| / 7), 2^-24), codes clamp(round(X / s), -7, 7)), stored offset-binary (+7) as

@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
-The reference has no DCT (SURVEY: grep finds none); the build defines the contract, following the
+The reference has no DCT (no DCT transform appears in its sources); the build defines the contract, following the
 reference's own conventions where it has them:
   * per (KV head, channel, 64-token block): orthonormal DCT-II along tokens,
     C[k, n] = a_k cos(pi (2n + 1) k / 128), a_0 = sqrt(1/64), a_k = sqrt(2/64); keep k = 0..15;
