@@ -32,8 +32,11 @@ __device__ __forceinline__ f32x4 tile_mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                   0, 0);
 }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two fp32 values rounded to nearest even as one packed bf16 pair (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
-  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+  return __builtin_bit_cast(uint32_t, bf16x2{static_cast<__bf16>(a), static_cast<__bf16>(b)});
 }
 
 // fp32 x[8] -> hi and lo parts in DT's operand type (bf16 parts for bf16, fp16 parts otherwise)
