@@ -599,7 +599,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     float v[8];
     cvt_slab<DT>(raw[j], v);
     const uint32_t w = code_word4(v, lo, sc, rc);
-    if (rq + 4 * j < rv) dst[(rq + 4 * j) * (D / 8)] = w;
+    if (rq + 4 * j < rv) __builtin_nontemporal_store(w, &dst[(rq + 4 * j) * (D / 8)]);   // written once
   }
 }
 
@@ -656,7 +656,7 @@ __global__ __launch_bounds__(256) void kivi_quant_values_p4(
     const float rc[8] = {r1, r1, r1, r1, r1, r1, r1, r1};
     const uint32_t w = code_word4(v, lo, sc, rc);
     if (r < rv) {
-      dst[r * (D / 8)] = w;
+      __builtin_nontemporal_store(w, &dst[r * (D / 8)]);                                 // written once
       if (s % L == 0) {
         lo_out[mrow + static_cast<int64_t>(r) * NG] = f32_to_f16(l1);
         sc_out[mrow + static_cast<int64_t>(r) * NG] = f32_to_f16(s1);
